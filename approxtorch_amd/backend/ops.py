@@ -1,0 +1,469 @@
+"""Tensor-level wrappers over the C ABI, named after the reference's ops.
+
+Each wrapper mirrors one op of approxtorch/backend/ops.py (and the schema it
+binds in csrc/), checks arguments the way the reference's TORCH_CHECKs do
+(RuntimeError), allocates outputs with torch on the input's device and
+launches the HIP kernels on the current stream.  The GEMM operands are
+re-laid out for the gfx950 kernels (row-offset activations, transposed
+weights) inside these wrappers; callers see the reference's shapes.
+"""
+import threading
+from collections import OrderedDict
+
+import torch
+from torch import Tensor
+from torch.nn.modules.utils import _pair
+
+from . import _lib as L
+
+__all__ = [
+    "lut_image", "bgemm_fake_int8_claude", "bgemm_fake_int8_claude_save",
+    "bgemm_fake_uint8_claude", "bgemm_fake_uint8_claude_save", "bgemm_fake_int8_claude_cfg",
+    "bgemm_fake_uint8_claude_cfg", "lut_gemm_i32", "im2col_u8", "lut_map", "lut_map_pad",
+    "bgemm_lre_backward_claude", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
+    "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "fakequant_per_tensor",
+    "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
+    "conv_backward_data", "conv_backward_weight", "col2im",
+]
+
+# --------------------------------------------------------------------- LUTs
+_LUT_CACHE = OrderedDict()
+_LUT_LOCK = threading.Lock()
+_LUT_CACHE_MAX = 32
+
+
+def _check_lut(lut, name="lut"):
+    if not lut.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if lut.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32")
+    if lut.numel() != 256 * 256:
+        raise RuntimeError(f"{name} must have 65536 elements")
+
+
+def lut_image(lut: Tensor):
+    """(lut16t, lutf32t, class) for an fp32 [65536] LUT, cached per tensor.
+
+    The 16-bit transposed image and its class (int16 / uint16 / fp32
+    fallback) are computed once per (storage, version) -- the reference
+    rebuilds them inside every forward (csrc/claude/bgemm_float_claude.cu:161-192).
+    """
+    _check_lut(lut)
+    key = (lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset())
+    with _LUT_LOCK:
+        hit = _LUT_CACHE.get(key)
+        if hit is not None:
+            _LUT_CACHE.move_to_end(key)
+            return hit
+    lc = lut.contiguous()
+    dev = lut.device
+    img16 = torch.empty(65536, dtype=torch.int16, device=dev)
+    imgf = torch.empty(65536, dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    L.call("atx_lut_prepare", L.ptr(lc), L.ptr(img16), L.ptr(imgf), L.ptr(flags),
+           L.stream_of(lc))
+    f = flags.tolist()          # one host sync per new LUT
+    cls = L.ATX_LUT_I16 if f[0] == 0 else (L.ATX_LUT_U16 if f[1] == 0 else L.ATX_LUT_F32)
+    val = (img16, imgf, cls, lc)   # keep the source alive: its pointer is the key
+    with _LUT_LOCK:
+        _LUT_CACHE[key] = val
+        while len(_LUT_CACHE) > _LUT_CACHE_MAX:
+            _LUT_CACHE.popitem(last=False)
+    return val
+
+
+# -------------------------------------------------------------- LUT GEMM
+def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None):
+    img16, imgf, cls, _ = lut_image(lut)
+    dev = y.device
+    wsb = L.query("atx_lut_gemm_workspace_bytes", N, K, Lc, O) if cls != L.ATX_LUT_F32 else 0
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
+    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
+    L.call("atx_lut_gemm", L.ptr(xt), Rpad, L.ptr(wt), Opad, N, K, Lc, O, L.ptr(img16),
+           L.ptr(imgf), cls, ep, L.ptr(y), L.ptr(ws), L.stream_of(y))
+    return y
+
+
+def _pack_w(w, offset, want_wq=True):
+    """w fp32 [O,K] (quantized values) or uint8 [O,K] indices -> (wq, wt, Opad)."""
+    O, K = w.shape
+    Opad = L.round_up(max(O, 1), L.COL_TILE)
+    wt = torch.empty((K, Opad), dtype=torch.uint8, device=w.device)
+    s = L.stream_of(w)
+    if w.dtype == torch.uint8:
+        L.call("atx_pack_w_u8", L.ptr(w), O, K, L.ptr(wt), Opad, s)
+        return w, wt, Opad
+    wq = torch.empty((O, K), dtype=torch.uint8, device=w.device) if want_wq else None
+    L.call("atx_pack_w_f32", L.ptr(w), O, K, offset, L.ptr(wq), L.ptr(wt), Opad, s)
+    return wq, wt, Opad
+
+
+def _bgemm_save(x, w, lut, offset, name):
+    # checks of csrc/claude/bgemm_float_claude.cu:80-91
+    if not (x.is_cuda and w.is_cuda and lut.is_cuda):
+        raise RuntimeError(f"{name}: x, w and lut must be CUDA tensors")
+    if x.dtype not in (torch.float32, torch.uint8):
+        raise RuntimeError("x must be float32 or uint8 (LUT indices)")
+    if w.dtype != torch.float32:
+        raise RuntimeError("w must be float32")
+    _check_lut(lut)
+    if x.dim() != 3:
+        raise RuntimeError("x must have shape [N, CKK, L]")
+    if w.dim() != 2:
+        raise RuntimeError("w must have shape [O, CKK]")
+    if x.size(1) != w.size(1):
+        raise RuntimeError("x.size(1) must equal w.size(1)")
+    xc, wc = x.contiguous(), w.contiguous()
+    N, K, Lc = xc.shape
+    O = wc.size(0)
+    dev, s = xc.device, L.stream_of(xc)
+    R = N * Lc
+    Rpad = L.round_up(max(R, 1), L.ROW_TILE)
+    xt = torch.empty((K, Rpad), dtype=torch.int16, device=dev)
+    if xc.dtype == torch.uint8:
+        xq = xc
+        L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, s)
+    else:
+        xq = torch.empty((N, K, Lc), dtype=torch.uint8, device=dev)
+        L.call("atx_pack_x_f32", L.ptr(xc), N, K, Lc, offset, L.ptr(xq), L.ptr(xt), Rpad, s)
+    wq, wt, Opad = _pack_w(wc, offset)
+    y = torch.empty((N, O, Lc), dtype=torch.float32, device=dev)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_F32, y)
+    return y, xq, wq
+
+
+def bgemm_fake_int8_claude_save(X: Tensor, W: Tensor, lut: Tensor):
+    """(y, xq, wq): y[n,o,l] = sum_k lut[(x+128)*256 + (w+128)], plus the uint8
+    index images (xq aliases X when X is uint8).  csrc/claude/bgemm_float_claude.cu:209-241."""
+    return _bgemm_save(X, W, lut, 128, "bgemm_fake_int8_claude_save")
+
+
+def bgemm_fake_int8_claude(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
+    return bgemm_fake_int8_claude_save(X, W, lut)[0]
+
+
+def bgemm_fake_int8_claude_cfg(X: Tensor, W: Tensor, lut: Tensor, cfg: int) -> Tensor:
+    """`cfg` selected one of the reference's CUDA tile configurations; the gfx950
+    kernel has a single tiling, so it is accepted and ignored."""
+    return bgemm_fake_int8_claude(X, W, lut)
+
+
+def bgemm_fake_uint8_claude_save(X: Tensor, W: Tensor, lut: Tensor):
+    """uint8 x uint8 variant: lut[x*256 + w] with raw values as indices.
+    csrc/claude/bgemm_float_claude.cu:245-277."""
+    return _bgemm_save(X, W, lut, 0, "bgemm_fake_uint8_claude_save")
+
+
+def bgemm_fake_uint8_claude(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
+    return bgemm_fake_uint8_claude_save(X, W, lut)[0]
+
+
+def bgemm_fake_uint8_claude_cfg(X: Tensor, W: Tensor, lut: Tensor, cfg: int) -> Tensor:
+    return bgemm_fake_uint8_claude(X, W, lut)
+
+
+def lut_gemm_i32(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
+    """Exact int32 LUT sums for uint8 index operands X [N,K,L], W [O,K]
+    (integer LUT classes only)."""
+    if X.dtype != torch.uint8 or W.dtype != torch.uint8:
+        raise RuntimeError("lut_gemm_i32 takes uint8 index operands")
+    xc, wc = X.contiguous(), W.contiguous()
+    N, K, Lc = xc.shape
+    O = wc.size(0)
+    Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
+    xt = torch.empty((K, Rpad), dtype=torch.int16, device=xc.device)
+    L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, L.stream_of(xc))
+    _, wt, Opad = _pack_w(wc, 0)
+    y = torch.empty((N, O, Lc), dtype=torch.int32, device=xc.device)
+    return _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_I32, y)
+
+
+# ------------------------------------------------------------- conv path
+_DTYPE_CODE = {torch.int8: 0, torch.uint8: 1, torch.float32: 2}
+
+
+def _dtype_code(t, unsigned=False):
+    """Kernel dtype code; fp32 images hold signed (index v+128) or, with
+    unsigned=True, unsigned (index v) quantized values."""
+    code = _DTYPE_CODE.get(t.dtype)
+    if code is None:
+        raise RuntimeError(f"unsupported dtype {t.dtype} (int8, uint8 or float32)")
+    return 3 if (code == 2 and unsigned) else code
+
+
+def conv_geom(x_shape, kernel_size, stride, padding, dilation):
+    N, C, H, W = x_shape
+    kh, kw = _pair(kernel_size)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    return L.geom(N, C, H, W, kh, kw, sh, sw, ph, pw, dh, dw)
+
+
+def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
+                 pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
+                 pad_dev=None):
+    """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
+
+    img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
+    offset 128 = signed operands, 0 = unsigned); w: [O, C*KH*KW] fp32
+    quantized values or uint8 indices.  Out-of-image taps use pad_index, or
+    the device scalar pad_dev when given.  Returns (y, wq), wq the uint8
+    weight index image."""
+    imgc = img.contiguous()
+    N, K = g.N, g.C * g.KH * g.KW
+    Lc = g.OH * g.OW
+    O = w_idx_or_val.size(0)
+    if w_idx_or_val.size(1) != K:
+        raise RuntimeError(f"weight has {w_idx_or_val.size(1)} taps, geometry needs {K}")
+    dev = imgc.device
+    Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
+    xt = torch.empty((K, Rpad), dtype=torch.int16, device=dev)
+    L.call("atx_im2col_rows", L.ptr(imgc), _dtype_code(imgc, offset == 0), g, pad_index,
+           L.ptr(pad_dev), L.ptr(xt), Rpad, L.stream_of(imgc))
+    wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)
+    y = torch.empty((N, O, Lc), dtype=torch.float32, device=dev)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
+    return y, wq
+
+
+def conv_backward_data(go: Tensor, wq: Tensor, table: Tensor, g, mask=None, scale=None):
+    """grad wrt the quantized image: fold(sum_o go * table[wq]) (+ fused STE mask/s)."""
+    goc = go.contiguous()
+    N, K, Lc = g.N, g.C * g.KH * g.KW, g.OH * g.OW
+    O = wq.size(0)
+    col = torch.empty((N, K, Lc), dtype=torch.float32, device=goc.device)
+    s = L.stream_of(goc)
+    L.call("atx_conv_bwd_data_col", L.ptr(goc), L.ptr(wq.contiguous()), L.ptr(table), N, O, K,
+           Lc, L.ptr(col), s)
+    img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
+    L.call("atx_col2im", L.ptr(col), g, L.ptr(mask), L.ptr(scale), L.ptr(img), s)
+    return img
+
+
+def conv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, O: int, pad_index: int,
+                         mask_w=None, scale_w=None, pad_dev=None, unsigned=False):
+    """grad wrt the weights: sum_{n,l} go * table[xi] with implicit im2col."""
+    goc, imgc = go.contiguous(), img.contiguous()
+    K = g.C * g.KH * g.KW
+    P = g.N * g.OH * g.OW
+    gw = torch.empty((O, K), dtype=torch.float32, device=goc.device)
+    wsb = L.query("atx_conv_bwd_weight_workspace_bytes", O, K, P)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
+    L.call("atx_conv_bwd_weight", L.ptr(goc), L.ptr(imgc), _dtype_code(imgc, unsigned), g, O,
+           pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(mask_w), L.ptr(scale_w), L.ptr(gw),
+           L.ptr(ws), L.stream_of(goc))
+    return gw
+
+
+def tap_sum(img: Tensor, g, pad_dev=None) -> Tensor:
+    """[N, L] column sums of the unfolded fp32 image (padding = pad_dev)."""
+    ic = img.contiguous()
+    out = torch.empty((g.N, g.OH * g.OW), dtype=torch.float32, device=ic.device)
+    L.call("atx_tap_sum", L.ptr(ic), g, L.ptr(pad_dev), L.ptr(out), L.stream_of(ic))
+    return out
+
+
+def tap_sum_backward(go: Tensor, g) -> Tensor:
+    goc = go.contiguous()
+    img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
+    L.call("atx_tap_sum_bwd", L.ptr(goc), g, L.ptr(img), L.stream_of(goc))
+    return img
+
+
+def col2im(col: Tensor, g) -> Tensor:
+    colc = col.contiguous()
+    img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=colc.device)
+    L.call("atx_col2im", L.ptr(colc), g, None, None, L.ptr(img), L.stream_of(colc))
+    return img
+
+
+# ------------------------------------------------------------ index maps
+def im2col_u8(feature: Tensor, kernel_size, stride=1, padding=0, dilation=1) -> Tensor:
+    """[N,C,H,W] int8/uint8/fp32 -> uint8 LUT indices [N, C*kh*kw, L], padding -> 128.
+    csrc/claude/bgemm_lre_backward_claude.cu:737-791."""
+    if not feature.is_cuda:
+        raise RuntimeError("im2col_u8: feature must be a CUDA tensor")
+    if feature.dim() != 4:
+        raise RuntimeError("im2col_u8: feature must be [N, C, H, W]")
+    fc = feature.contiguous()
+    g = conv_geom(fc.shape, kernel_size, stride, padding, dilation)
+    if g.OH <= 0 or g.OW <= 0:
+        raise RuntimeError("im2col_u8: empty output")
+    out = torch.empty((g.N, g.C * g.KH * g.KW, g.OH * g.OW), dtype=torch.uint8,
+                      device=fc.device)
+    L.call("atx_im2col_u8", L.ptr(fc), _dtype_code(fc), g, L.ptr(out), L.stream_of(fc))
+    return out
+
+
+def lut_map(x: Tensor, lut: Tensor) -> Tensor:
+    """out[i] = lut[idx(x[i])] for a [256] table (int8: v+128, uint8: v,
+    fp32: clamp(rint(v))+128).  csrc/claude/bgemm_lre_backward_claude.cu:793-807."""
+    if not (x.is_cuda and lut.is_cuda):
+        raise RuntimeError("lut_map: tensors must be CUDA tensors")
+    if lut.dtype != torch.float32 or lut.numel() != 256:
+        raise RuntimeError("lut_map: lut must be float32 with 256 elements")
+    xc = x.contiguous()
+    out = torch.empty(xc.shape, dtype=torch.float32, device=xc.device)
+    L.call("atx_lut_map", L.ptr(xc), _dtype_code(xc), xc.numel(), L.ptr(lut.contiguous()),
+           L.ptr(out), L.stream_of(xc))
+    return out
+
+
+def lut_map_pad(x: Tensor, lut: Tensor, padding) -> Tensor:
+    """lut_map of an image [N,C,H,W] with a constant border lut[128].
+    csrc/claude/bgemm_lre_backward_claude.cu:809-848."""
+    ph, pw = _pair(padding)
+    if x.dim() != 4:
+        raise RuntimeError("lut_map_pad: x must be [N, C, H, W]")
+    if lut.dtype != torch.float32 or lut.numel() != 256:
+        raise RuntimeError("lut_map_pad: lut must be float32 with 256 elements")
+    xc = x.contiguous()
+    N, C, H, W = xc.shape
+    out = torch.empty((N, C, H + 2 * ph, W + 2 * pw), dtype=torch.float32, device=xc.device)
+    L.call("atx_lut_map_pad", L.ptr(xc), _dtype_code(xc), N, C, H, W, ph, pw,
+           L.ptr(lut.contiguous()), L.ptr(out), L.stream_of(xc))
+    return out
+
+
+# ------------------------------------------------------------ LRE backward
+def _weight_index(w: Tensor) -> Tensor:
+    """Any reference weight operand (uint8 index, int8 value, fp32 value) ->
+    uint8 index image of the same shape."""
+    if w.dtype == torch.uint8:
+        return w.contiguous()
+    if w.dtype == torch.int8:
+        return (w.to(torch.int16) + 128).to(torch.uint8).contiguous()
+    if w.dtype == torch.float32:
+        O, K = w.shape
+        wq, _, _ = _pack_w(w.contiguous(), 128)
+        return wq
+    raise RuntimeError(f"unsupported weight dtype {w.dtype}")
+
+
+def bgemm_lre_backward_claude(grad_output: Tensor, x: Tensor, w: Tensor, dx: Tensor,
+                              dw: Tensor):
+    """LRE backward of the LUT BGEMM (csrc/claude/bgemm_lre_backward_claude.cu:539-647):
+      grad_x[n,k,l] = sum_o go[n,o,l] * dx[idx(w[k,o])]
+      grad_w[k,o]   = sum_{n,l} go[n,o,l] * dw[idx(x[n,k,l])]
+    x [N,K,L] and w [K,O] are uint8 indices, int8 values or fp32 values."""
+    for t, nm in ((grad_output, "grad_output"), (x, "x"), (w, "w"), (dx, "dx"), (dw, "dw")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{nm} must be a CUDA tensor")
+    if dx.numel() != 256 or dw.numel() != 256 or dx.dtype != torch.float32 or \
+            dw.dtype != torch.float32:
+        raise RuntimeError("dx and dw must be float32 tables with 256 elements")
+    if x.dim() != 3 or w.dim() != 2 or grad_output.dim() != 3:
+        raise RuntimeError("expected grad_output [N,O,L], x [N,K,L], w [K,O]")
+    N, K, Lc = x.shape
+    O = w.size(1)
+    if w.size(0) != K or tuple(grad_output.shape) != (N, O, Lc):
+        raise RuntimeError("shape mismatch between grad_output, x and w")
+    wq = _weight_index(w.t().contiguous())                 # [O, K]
+    go = grad_output.contiguous().float()
+    col = torch.empty((N, K, Lc), dtype=torch.float32, device=go.device)
+    L.call("atx_conv_bwd_data_col", L.ptr(go), L.ptr(wq), L.ptr(dx.contiguous()), N, O, K, Lc,
+           L.ptr(col), L.stream_of(go))
+    g = L.geom(N, K, 1, Lc, 1, 1, 1, 1, 0, 0, 1, 1)
+    gw = conv_backward_weight(go, x.contiguous().view(N, K, 1, Lc), dw.contiguous(), g, O, 128)
+    return col, gw.t().contiguous()
+
+
+# --------------------------------------------------------- custom backward
+def _custom(kind, X, W, dY, lut, signed):
+    want = torch.int8 if signed else torch.uint8
+    if X.dtype != want or W.dtype != want:
+        raise RuntimeError(f"X and W must be {want}")
+    if dY.dtype != torch.float32 or lut.dtype != torch.float32 or lut.numel() != 65536:
+        raise RuntimeError("dY must be float32 and lut a float32 [65536] table")
+    if X.dim() != 3 or W.dim() != 2 or dY.dim() != 3:
+        raise RuntimeError("expected X [N,K,L], W [O,K], dY [N,O,L]")
+    N, K, Lc = X.shape
+    O = W.size(0)
+    if W.size(1) != K or tuple(dY.shape) != (N, O, Lc):
+        raise RuntimeError("shape mismatch between X, W and dY")
+    Xc, Wc, dYc, lc = X.contiguous(), W.contiguous(), dY.contiguous(), lut.contiguous()
+    s = L.stream_of(Xc)
+    if kind == "dx":
+        gx = torch.empty((N, K, Lc), dtype=torch.float32, device=Xc.device)
+        L.call("atx_custom_grad_dx", L.ptr(Xc), L.ptr(Wc), int(signed), L.ptr(dYc), L.ptr(lc),
+               N, K, Lc, O, L.ptr(gx), s)
+        return gx
+    gw = torch.empty((O, K), dtype=torch.float32, device=Xc.device)
+    wsb = L.query("atx_custom_grad_dw_workspace_bytes", N, K, Lc, O)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=Xc.device)
+    L.call("atx_custom_grad_dw", L.ptr(Xc), L.ptr(Wc), int(signed), L.ptr(dYc), L.ptr(lc), N, K,
+           Lc, O, L.ptr(gw), L.ptr(ws), s)
+    return gw
+
+
+def bgemm_custom_grad_uint8_dx(X, W, dY, dx_lut):
+    """csrc/cuda/bgemm_custom_grad_optimize.cu:212-256 (uint8 LUT indices)."""
+    return _custom("dx", X, W, dY, dx_lut, False)
+
+
+def bgemm_custom_grad_uint8_dw(X, W, dY, dW_lut):
+    """csrc/cuda/bgemm_custom_grad_optimize.cu:259-301."""
+    return _custom("dw", X, W, dY, dW_lut, False)
+
+
+def bgemm_custom_grad_int8_dx(X, W, dY, dx_lut):
+    """csrc/cuda/bgemm_custom_grad_optimize.cu:497-541 (int8 values, index v+128)."""
+    return _custom("dx", X, W, dY, dx_lut, True)
+
+
+def bgemm_custom_grad_int8_dw(X, W, dY, dW_lut):
+    """csrc/cuda/bgemm_custom_grad_optimize.cu:544-585."""
+    return _custom("dw", X, W, dY, dW_lut, True)
+
+
+# ------------------------------------------------------------- fake-quant
+def _reduce_ws(dev):
+    return torch.empty(L.query("atx_reduce_workspace_bytes") // 4, dtype=torch.float32,
+                       device=dev)
+
+
+def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
+                         want_q=True, q8_dtype=None):
+    """(q fp32, mask bool[, q8]) of the fused per-tensor fake-quant
+    (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric)."""
+    if qmin >= qmax:
+        raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
+    xc = x.contiguous()
+    q = torch.empty_like(xc) if want_q else None
+    mask = torch.empty(xc.shape, dtype=torch.bool, device=xc.device)
+    q8 = torch.empty(xc.shape, dtype=q8_dtype, device=xc.device) if q8_dtype else None
+    L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale), L.ptr(zero_point), qmin,
+           qmax, L.ptr(q), L.ptr(mask), L.ptr(q8), L.stream_of(xc))
+    return q, mask, q8
+
+
+def fakequant_per_tensor_backward(grad_output: Tensor, mask: Tensor, scale: Tensor,
+                                  channels: int = 1, inner: int = 1) -> Tensor:
+    """gx = (mask ? go : 0) / max(scale, 1e-12) (csrc/claude/quantization.cu:223-258)."""
+    go = grad_output.contiguous()
+    gx = torch.empty_like(go)
+    L.call("atx_fakequant_bwd", L.ptr(go), L.ptr(mask.contiguous()), go.numel(), L.ptr(scale),
+           channels, inner, L.ptr(gx), L.stream_of(go))
+    return gx
+
+
+def fakequant_per_channel(w: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
+                          offset=None, want_wt=False):
+    """Per-channel (axis 0) fake-quant of a weight: (q, mask, wq index image,
+    wt GEMM operand or None, Opad)."""
+    if qmin >= qmax:
+        raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
+    wc = w.contiguous()
+    O = wc.size(0)
+    inner = wc.numel() // max(O, 1)
+    q = torch.empty_like(wc)
+    mask = torch.empty(wc.shape, dtype=torch.bool, device=wc.device)
+    wq = torch.empty((O, inner), dtype=torch.uint8, device=wc.device) if offset is not None \
+        else None
+    Opad = L.round_up(max(O, 1), L.COL_TILE)
+    wt = torch.empty((inner, Opad), dtype=torch.uint8, device=wc.device) if want_wt else None
+    L.call("atx_fakequant_channel_fwd", L.ptr(wc), O, inner, L.ptr(scale), L.ptr(zero_point),
+           qmin, qmax, offset if offset is not None else 0, L.ptr(q), L.ptr(mask), L.ptr(wq),
+           L.ptr(wt), Opad, L.stream_of(wc))
+    return q, mask, wq, wt, Opad

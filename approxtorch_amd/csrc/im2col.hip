@@ -1,0 +1,371 @@
+// Image -> LUT-index operands (implicit im2col), LUT maps and col2im (fold).
+// All HBM-bound index arithmetic; k order is (c, kh, kw), l = oh*OW + ow.
+
+#include "atx_internal.h"
+
+#include <algorithm>
+
+namespace atx {
+
+constexpr int TB = 256;
+
+// Index of one image element: int8 values index as v + 128, uint8 values as
+// v, fp32 quantized values as clamp(rint(v), -128, 127) + 128 (the fp32
+// convention of csrc/claude/bgemm_lre_backward_claude.cu:64-78).
+template <typename T> __device__ __forceinline__ unsigned elem_index(T v, int offset);
+template <> __device__ __forceinline__ unsigned elem_index<int8_t>(int8_t v, int) {
+  return (unsigned)((int)v + 128);
+}
+template <> __device__ __forceinline__ unsigned elem_index<uint8_t>(uint8_t v, int) {
+  return (unsigned)v;
+}
+template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int offset) {
+  return quant_index(v, offset);
+}
+
+// xt[k][r] = row_offset(index of tap k at output position r); r >= N*L -> 0.
+template <typename T>
+__global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset,
+                                   int pad_index, const float* __restrict__ pad_dev,
+                                   uint16_t* __restrict__ xt, int Rpad) {
+  if (pad_dev) pad_index = (int)quant_index(pad_dev[0], 0);
+  const int L = g.OH * g.OW;
+  const int R = g.N * L;
+  const int KK = g.KH * g.KW;
+  const int K = g.C * KK;
+  for (int k = blockIdx.y; k < K; k += gridDim.y) {
+    const int c = k / KK;
+    const int t = k - c * KK;
+    const int kh = t / g.KW;
+    const int kw = t - kh * g.KW;
+    const int ih0 = kh * g.DH - g.PH;
+    const int iw0 = kw * g.DW - g.PW;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < Rpad;
+         r += gridDim.x * blockDim.x) {
+      unsigned off = 0;
+      if (r < R) {
+        const int n = r / L;
+        const int l = r - n * L;
+        const int oh = l / g.OW;
+        const int ow = l - oh * g.OW;
+        const int ih = oh * g.SH + ih0;
+        const int iw = ow * g.SW + iw0;
+        unsigned v = (unsigned)pad_index;
+        if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+          v = elem_index<T>(img[(((long long)n * g.C + c) * g.H + ih) * g.W + iw], offset);
+        off = row_offset(v);
+      }
+      xt[(long long)k * Rpad + r] = (uint16_t)off;
+    }
+  }
+}
+
+// The reference's im2col_u8 op: out[n][k][l] = index, padding -> 128.
+template <typename T>
+__global__ void im2col_u8_kernel(const T* __restrict__ img, atx_conv_geom g,
+                                 uint8_t* __restrict__ out) {
+  const int L = g.OH * g.OW;
+  const int KK = g.KH * g.KW;
+  const int K = g.C * KK;
+  for (int k = blockIdx.y; k < K; k += gridDim.y) {
+    const int c = k / KK;
+    const int t = k - c * KK;
+    const int kh = t / g.KW;
+    const int kw = t - kh * g.KW;
+    const int ih0 = kh * g.DH - g.PH;
+    const int iw0 = kw * g.DW - g.PW;
+    for (int n = blockIdx.z; n < g.N; n += gridDim.z) {
+      uint8_t* o = out + ((long long)n * K + k) * L;
+      for (int l = blockIdx.x * blockDim.x + threadIdx.x; l < L;
+           l += gridDim.x * blockDim.x) {
+        const int oh = l / g.OW;
+        const int ow = l - oh * g.OW;
+        const int ih = oh * g.SH + ih0;
+        const int iw = ow * g.SW + iw0;
+        unsigned v = 128u;
+        if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+          v = elem_index<T>(img[(((long long)n * g.C + c) * g.H + ih) * g.W + iw], 128);
+        o[l] = (uint8_t)v;
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ void lut_map_kernel(const T* __restrict__ in, long long n,
+                               const float* __restrict__ lut, float* __restrict__ out) {
+  __shared__ float sl[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) sl[i] = lut[i];
+  __syncthreads();
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = sl[elem_index<T>(in[i], 128)];
+}
+
+template <typename T>
+__global__ void lut_map_pad_kernel(const T* __restrict__ in, int N, int C, int H, int W,
+                                   int PH, int PW, const float* __restrict__ lut,
+                                   float* __restrict__ out) {
+  __shared__ float sl[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) sl[i] = lut[i];
+  __syncthreads();
+  const int HP = H + 2 * PH, WP = W + 2 * PW;
+  const long long n = (long long)N * C * HP * WP;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int wp = (int)(i % WP);
+    const long long t = i / WP;
+    const int hp = (int)(t % HP);
+    const long long nc = t / HP;
+    const int h = hp - PH, w = wp - PW;
+    float v = sl[128];
+    if ((unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
+      v = sl[elem_index<T>(in[(nc * H + h) * W + w], 128)];
+    out[i] = v;
+  }
+}
+
+// col2im: img[n,c,h,w] = sum over taps (kh,kw) hitting (h,w) of
+// col[n, (c,kh,kw), (oh,ow)], taps in ascending (kh, kw) order (F.fold).
+// Optional fused STE: img = mask ? img / s : 0 (s = max(scale[0], 1e-12)).
+__global__ void col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
+                              const uint8_t* __restrict__ mask,
+                              const float* __restrict__ scale, float* __restrict__ img) {
+  const int L = g.OH * g.OW;
+  const int KK = g.KH * g.KW;
+  const long long total = (long long)g.N * g.C * g.H * g.W;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += stride) {
+    const int w = (int)(i % g.W);
+    long long t = i / g.W;
+    const int h = (int)(t % g.H);
+    t /= g.H;
+    const int c = (int)(t % g.C);
+    const int n = (int)(t / g.C);
+    const float* cn = col + ((long long)n * g.C * KK + (long long)c * KK) * L;
+    float a = 0.0f;
+    for (int kh = 0; kh < g.KH; ++kh) {
+      const int y = h + g.PH - kh * g.DH;
+      if (y < 0 || y % g.SH) continue;
+      const int oh = y / g.SH;
+      if (oh >= g.OH) continue;
+      for (int kw = 0; kw < g.KW; ++kw) {
+        const int x = w + g.PW - kw * g.DW;
+        if (x < 0 || x % g.SW) continue;
+        const int ow = x / g.SW;
+        if (ow >= g.OW) continue;
+        a += cn[(long long)(kh * g.KW + kw) * L + oh * g.OW + ow];
+      }
+    }
+    if (mask) {
+      const float s = fmaxf(scale[0], 1e-12f);
+      a = (mask[i] ? a : 0.0f) / s;
+    }
+    img[i] = a;
+  }
+}
+
+// Sum over the K taps of each output position (out-of-image taps count as
+// pad_dev[0]): the column sums of the unfolded image, used by the uint8
+// zero-point correction (nn/Conv2d_uint8.py:311).
+__global__ void tap_sum_kernel(const float* __restrict__ img, atx_conv_geom g,
+                               const float* __restrict__ pad_dev, float* __restrict__ out) {
+  const int L = g.OH * g.OW;
+  const long long total = (long long)g.N * L;
+  const float pad = pad_dev ? pad_dev[0] : 0.0f;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int n = (int)(i / L), l = (int)(i - (i / L) * L);
+    const int oh = l / g.OW, ow = l - (l / g.OW) * g.OW;
+    float a = 0.0f;
+    for (int c = 0; c < g.C; ++c) {
+      const float* ic = img + ((long long)n * g.C + c) * g.H * g.W;
+      for (int kh = 0; kh < g.KH; ++kh) {
+        const int ih = oh * g.SH + kh * g.DH - g.PH;
+        for (int kw = 0; kw < g.KW; ++kw) {
+          const int iw = ow * g.SW + kw * g.DW - g.PW;
+          a += ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+                   ? ic[(long long)ih * g.W + iw] : pad;
+        }
+      }
+    }
+    out[i] = a;
+  }
+}
+
+// Backward of tap_sum: img_grad[n,c,h,w] = sum of go[n,l] over the taps
+// (kh, kw) that read (h, w) (independent of c).
+__global__ void tap_sum_bwd_kernel(const float* __restrict__ go, atx_conv_geom g,
+                                   float* __restrict__ img) {
+  const int L = g.OH * g.OW;
+  const long long total = (long long)g.N * g.C * g.H * g.W;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int w = (int)(i % g.W);
+    long long t = i / g.W;
+    const int h = (int)(t % g.H);
+    const int n = (int)(t / g.H / g.C);
+    const float* gn = go + (long long)n * L;
+    float a = 0.0f;
+    for (int kh = 0; kh < g.KH; ++kh) {
+      const int y = h + g.PH - kh * g.DH;
+      if (y < 0 || y % g.SH) continue;
+      const int oh = y / g.SH;
+      if (oh >= g.OH) continue;
+      for (int kw = 0; kw < g.KW; ++kw) {
+        const int x = w + g.PW - kw * g.DW;
+        if (x < 0 || x % g.SW) continue;
+        const int ow = x / g.SW;
+        if (ow >= g.OW) continue;
+        a += gn[oh * g.OW + ow];
+      }
+    }
+    img[i] = a;
+  }
+}
+
+}  // namespace atx
+
+using namespace atx;
+
+static int check_geom(const atx_conv_geom& g) {
+  ATX_REQUIRE(g.N >= 0 && g.C >= 0 && g.H >= 0 && g.W >= 0, "conv geometry: negative size");
+  ATX_REQUIRE(g.KH > 0 && g.KW > 0 && g.SH > 0 && g.SW > 0 && g.DH > 0 && g.DW > 0 &&
+                  g.PH >= 0 && g.PW >= 0,
+              "conv geometry: kernel/stride/dilation must be positive, padding >= 0");
+  ATX_REQUIRE(g.OH == (g.H + 2 * g.PH - g.DH * (g.KH - 1) - 1) / g.SH + 1 &&
+                  g.OW == (g.W + 2 * g.PW - g.DW * (g.KW - 1) - 1) / g.SW + 1,
+              "conv geometry: OH/OW do not match the input geometry");
+  ATX_REQUIRE(g.OH > 0 && g.OW > 0, "conv geometry: empty output");
+  return ATX_OK;
+}
+
+extern "C" {
+
+int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
+                    const float* pad_dev, uint16_t* xt, int Rpad, hipStream_t stream) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  ATX_REQUIRE(dtype >= 0 && dtype <= 3, "atx_im2col_rows: bad dtype %d", dtype);
+  // dtype 2: fp32 signed quantized values (index v+128); 3: fp32 unsigned
+  // quantized values (index v).
+  const int offset = dtype == 3 ? 0 : 128;
+  if (dtype == 3) dtype = 2;
+  ATX_REQUIRE(pad_index >= 0 && pad_index <= 255, "atx_im2col_rows: bad pad_index");
+  const long long R = (long long)g.N * g.OH * g.OW;
+  ATX_REQUIRE(Rpad >= R && Rpad % ATX_ROW_TILE == 0, "atx_im2col_rows: bad Rpad %d", Rpad);
+  const int K = g.C * g.KH * g.KW;
+  if ((long long)K * Rpad == 0) return ATX_OK;
+  ATX_REQUIRE(xt && (R == 0 || img), "atx_im2col_rows: null pointer");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, TB), 1024), (unsigned)std::min(K, 65535));
+  if (dtype == 0)
+    hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,
+                       (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(im2col_rows_kernel<uint8_t>, grid, dim3(TB), 0, stream,
+                       (const uint8_t*)img, g, 0, pad_index, pad_dev, xt, Rpad);
+  else
+    hipLaunchKernelGGL(im2col_rows_kernel<float>, grid, dim3(TB), 0, stream,
+                       (const float*)img, g, offset, pad_index, pad_dev, xt, Rpad);
+  return check_launch("im2col_rows_kernel");
+}
+
+int atx_im2col_u8(const void* img, int dtype, atx_conv_geom g, uint8_t* out,
+                  hipStream_t stream) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  ATX_REQUIRE(dtype >= 0 && dtype <= 2, "atx_im2col_u8: bad dtype %d", dtype);
+  const int K = g.C * g.KH * g.KW;
+  const int L = g.OH * g.OW;
+  if ((long long)g.N * K * L == 0) return ATX_OK;
+  ATX_REQUIRE(img && out, "atx_im2col_u8: null pointer");
+  dim3 grid((unsigned)std::min<long long>(cdiv(L, TB), 64), (unsigned)std::min(K, 65535),
+            (unsigned)std::min(g.N, 64));
+  if (dtype == 0)
+    hipLaunchKernelGGL(im2col_u8_kernel<int8_t>, grid, dim3(TB), 0, stream,
+                       (const int8_t*)img, g, out);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(im2col_u8_kernel<uint8_t>, grid, dim3(TB), 0, stream,
+                       (const uint8_t*)img, g, out);
+  else
+    hipLaunchKernelGGL(im2col_u8_kernel<float>, grid, dim3(TB), 0, stream,
+                       (const float*)img, g, out);
+  return check_launch("im2col_u8_kernel");
+}
+
+int atx_lut_map(const void* in, int dtype, long long n, const float* lut256, float* out,
+                hipStream_t stream) {
+  ATX_REQUIRE(n >= 0 && dtype >= 0 && dtype <= 2, "atx_lut_map: bad arguments");
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(in && lut256 && out, "atx_lut_map: null pointer");
+  const int grid = elem_grid(n, TB);
+  if (dtype == 0)
+    hipLaunchKernelGGL(lut_map_kernel<int8_t>, dim3(grid), dim3(TB), 0, stream,
+                       (const int8_t*)in, n, lut256, out);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(lut_map_kernel<uint8_t>, dim3(grid), dim3(TB), 0, stream,
+                       (const uint8_t*)in, n, lut256, out);
+  else
+    hipLaunchKernelGGL(lut_map_kernel<float>, dim3(grid), dim3(TB), 0, stream,
+                       (const float*)in, n, lut256, out);
+  return check_launch("lut_map_kernel");
+}
+
+int atx_lut_map_pad(const void* in, int dtype, int N, int C, int H, int W, int PH, int PW,
+                    const float* lut256, float* out, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && C >= 0 && H >= 0 && W >= 0 && PH >= 0 && PW >= 0 && dtype >= 0 &&
+                  dtype <= 2,
+              "atx_lut_map_pad: bad arguments");
+  const long long n = (long long)N * C * (H + 2 * PH) * (W + 2 * PW);
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(lut256 && out && ((long long)N * C * H * W == 0 || in), "atx_lut_map_pad: null");
+  const int grid = elem_grid(n, TB);
+  if (dtype == 0)
+    hipLaunchKernelGGL(lut_map_pad_kernel<int8_t>, dim3(grid), dim3(TB), 0, stream,
+                       (const int8_t*)in, N, C, H, W, PH, PW, lut256, out);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(lut_map_pad_kernel<uint8_t>, dim3(grid), dim3(TB), 0, stream,
+                       (const uint8_t*)in, N, C, H, W, PH, PW, lut256, out);
+  else
+    hipLaunchKernelGGL(lut_map_pad_kernel<float>, dim3(grid), dim3(TB), 0, stream,
+                       (const float*)in, N, C, H, W, PH, PW, lut256, out);
+  return check_launch("lut_map_pad_kernel");
+}
+
+int atx_tap_sum(const float* img, atx_conv_geom g, const float* pad_dev, float* out,
+                hipStream_t stream) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  const long long total = (long long)g.N * g.OH * g.OW;
+  if (total == 0) return ATX_OK;
+  ATX_REQUIRE(out && ((long long)g.C * g.H * g.W == 0 || img), "atx_tap_sum: null pointer");
+  hipLaunchKernelGGL(tap_sum_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, img, g,
+                     pad_dev, out);
+  return check_launch("tap_sum_kernel");
+}
+
+int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img, hipStream_t stream) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  const long long total = (long long)g.N * g.C * g.H * g.W;
+  if (total == 0) return ATX_OK;
+  ATX_REQUIRE(go && img, "atx_tap_sum_bwd: null pointer");
+  hipLaunchKernelGGL(tap_sum_bwd_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, go, g,
+                     img);
+  return check_launch("tap_sum_bwd_kernel");
+}
+
+int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const float* scale,
+               float* img, hipStream_t stream) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  const long long total = (long long)g.N * g.C * g.H * g.W;
+  if (total == 0) return ATX_OK;
+  ATX_REQUIRE(col && img && (!mask || scale), "atx_col2im: null pointer");
+  hipLaunchKernelGGL(col2im_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, col, g,
+                     mask, scale, img);
+  return check_launch("col2im_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,572 @@
+// LUT GEMM forward for gfx950: y[n,o,l] = sum_k LUT[xi(n,k,l)][wi(o,k)].
+//
+// Kernel structure ("expanded tables"):
+//   A workgroup owns a tile of ATX_ROW_TILE (1024) rows r = n*L + l and
+//   ATX_COL_TILE (64) output channels.  For every k it builds, in LDS, the
+//   table E_k[v][o] = LUT16[v][wi(o,k)] (256 rows x 64 channels x 16 bit =
+//   32 KiB) from the transposed 16-bit LUT image (L2-resident, 128 KiB), then
+//   every lane looks up E_k[xi(r,k)][o..o+7] for its rows with one
+//   conflict-free 16-byte LDS read and adds the eight 16-bit entries into
+//   int32 accumulators (exact).  E is double-buffered, so one barrier per k.
+//
+//   LDS bank layout: an E row is 128 bytes (all 32 banks).  Its 16-byte
+//   chunk for channels 8g..8g+7 is stored at chunk position g ^ ((v>>3)&7).
+//   The activation operand is pre-encoded as the byte offset
+//   v*128 + ((v>>3)&7)*16 ("row offset"), so the lane's address is
+//   row_offset ^ (g*16): no arithmetic on the index itself.  The swizzle
+//   makes the table build's 4-byte LDS writes conflict-free.
+//
+//   Threads: 512 (8 waves).  Lane = (row group rg 0..7, channel group g);
+//   each lane owns RPL = 16 consecutive rows x 8 channels = 128 int32
+//   accumulators (256-VGPR budget at 2 waves per SIMD).
+//
+// Reference: bgemm_lut_u8_kernel / bgemm_mainloop
+// (csrc/claude/bgemm_lut_kernels.cuh:183-387) computes the same sum with a
+// 16-bit LUT gathered through L1 and fp32 accumulation.
+
+#include "atx_internal.h"
+
+#include <algorithm>
+
+namespace atx {
+
+constexpr int RT = ATX_ROW_TILE;   // rows per workgroup
+constexpr int OT = ATX_COL_TILE;   // channels per workgroup
+constexpr int RPL = 16;            // rows per lane
+constexpr int RPW = 8 * RPL;       // rows per wave (8 row groups)
+constexpr int NWAVE = RT / RPW;    // waves per workgroup
+constexpr int NT = 64 * NWAVE;     // threads per workgroup
+constexpr int IPT = 1024 / NT;     // table-build items per thread
+constexpr int ETAB = 256 * OT * 2; // bytes of one E_k table (32 KiB)
+constexpr int STAGE_S = RPW + 1;   // epilogue staging stride (dwords per channel)
+constexpr int STAGE_WAVE = OT * STAGE_S * 4;  // bytes per wave
+constexpr int SMEM_BYTES = 2 * ETAB;          // static LDS: two E tables
+static_assert(STAGE_WAVE <= SMEM_BYTES, "epilogue stages one wave at a time");
+static_assert(1024 % NT == 0, "table build needs an integral item count");
+
+// K limits for exact int32 partial sums (entries up to 32767 / 65535).
+constexpr int KMAX_I16 = 65536;
+constexpr int KMAX_U16 = 32768;
+
+struct GemmParams {
+  const uint16_t* xt; int Rpad;
+  const uint8_t* wt; int Opad;
+  const uint16_t* lut16t;
+  const float* lutf32t;
+  int K, R, L, O;
+  int k_chunk, splits, tiles_r, tiles_o;
+  int out_kind;                 // ATX_OUT_*; splits > 1 => raw int32 partials
+  void* y;
+  long long split_stride;       // elements per partial slice
+  const float* sx; const float* sw; const float* bias;
+};
+
+// ------------------------------------------------------------------ prepare
+__global__ void lut_prepare_kernel(const float* __restrict__ lut,
+                                   uint16_t* __restrict__ out16t,
+                                   float* __restrict__ outf32t,
+                                   int* __restrict__ flags) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 65536 entries
+  const float v = lut[i];
+  const float r = __builtin_rintf(v);
+  const bool is_int = (v == r);
+  const bool ok16 = is_int && fabsf(v) <= 32767.0f;
+  const bool oku16 = is_int && v >= 0.0f && v <= 65535.0f;
+  if (!ok16) flags[0] = 1;     // benign race: every writer stores 1
+  if (!oku16) flags[1] = 1;
+  const unsigned short v16 =
+      (ok16 || oku16) ? (unsigned short)(unsigned)(int)r : (unsigned short)0;
+  const int t = ((i & 255) << 8) | (i >> 8);             // [x][w] -> [w][x]
+  out16t[t] = v16;
+  outf32t[t] = v;
+}
+
+// ------------------------------------------------------------- operand pack
+// xt[k][r] for r < R from x[n][k][l] (r = n*L + l); zero offsets for r >= R.
+template <typename T>
+__global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
+                              int offset, uint8_t* __restrict__ xq,
+                              uint16_t* __restrict__ xt, int Rpad) {
+  const int R = N * L;
+  for (int k = blockIdx.y; k < K; k += gridDim.y) {
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < Rpad;
+         r += gridDim.x * blockDim.x) {
+      unsigned off = 0;
+      if (r < R) {
+        const int n = r / L;
+        const int l = r - n * L;
+        const long long src = ((long long)n * K + k) * L + l;
+        unsigned v;
+        if constexpr (sizeof(T) == 4) {
+          v = quant_index((float)x[src], offset);
+          if (xq) xq[src] = (uint8_t)v;
+        } else {
+          v = (unsigned)x[src];
+        }
+        off = row_offset(v);
+      }
+      xt[(long long)k * Rpad + r] = (uint16_t)off;
+    }
+  }
+}
+
+template <typename T>
+__global__ void pack_w_kernel(const T* __restrict__ w, int O, int K, int offset,
+                              uint8_t* __restrict__ wq, uint8_t* __restrict__ wt,
+                              int Opad) {
+  const long long total = (long long)K * Opad;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int k = (int)(i / Opad);
+    const int o = (int)(i - (long long)k * Opad);
+    unsigned v = 0;
+    if (o < O) {
+      const long long src = (long long)o * K + k;
+      if constexpr (sizeof(T) == 4) {
+        v = quant_index((float)w[src], offset);
+        if (wq) wq[src] = (uint8_t)v;
+      } else {
+        v = (unsigned)w[src];
+      }
+    }
+    wt[i] = (uint8_t)v;
+  }
+}
+
+// ------------------------------------------------------------- main kernel
+__device__ __forceinline__ int logical_block() {
+  // Blocks are dispatched round-robin over the 8 XCDs (bid % 8).  Give each
+  // XCD a contiguous range of logical tiles so tiles sharing an activation
+  // row tile (consecutive logical ids) share that XCD's L2.
+  const int bid = blockIdx.x, nb = gridDim.x;
+  const int q = nb >> 3, rem = nb & 7;
+  const int xcd = bid & 7, slot = bid >> 3;
+  return xcd < rem ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
+}
+
+template <bool SIGNED>
+__device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
+  const unsigned d[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (SIGNED) {
+      a[2 * i] += (int)(short)(unsigned short)(d[i] & 0xffffu);
+      a[2 * i + 1] += ((int)d[i]) >> 16;
+    } else {
+      a[2 * i] += (int)(d[i] & 0xffffu);
+      a[2 * i + 1] += (int)(d[i] >> 16);
+    }
+  }
+}
+
+struct Rows { uint4 a[IPT], b[IPT]; };
+struct XRows { uint4 v[RPL / 8]; };
+
+__device__ __forceinline__ unsigned load_w(const uint8_t* __restrict__ wt, int Opad,
+                                           int k, int pair_col) {
+  return *(const unsigned short*)(wt + (long long)k * Opad + pair_col);
+}
+
+// LUT16T rows of the two weight indices packed in w (lo byte: channel 2pp,
+// hi byte: channel 2pp+1), v-chunk c[i] (8 entries each) per build item.
+__device__ __forceinline__ void load_rows(Rows& r, const uint16_t* __restrict__ lut,
+                                          const unsigned (&w)[IPT], const int (&c)[IPT]) {
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    r.a[i] = *(const uint4*)(lut + (w[i] & 255u) * 256u + c[i] * 8);
+    r.b[i] = *(const uint4*)(lut + ((w[i] >> 8) & 255u) * 256u + c[i] * 8);
+  }
+}
+
+__device__ __forceinline__ void load_x(XRows& x, const uint16_t* __restrict__ xt,
+                                       int Rpad, int k, int r0) {
+  const uint4* xp = (const uint4*)(xt + (long long)k * Rpad + r0);
+#pragma unroll
+  for (int i = 0; i < RPL / 8; ++i) x.v[i] = xp[i];
+}
+
+// Writes this lane's dwords of one table (wbase includes the LDS buffer):
+// entry pairs (channel 2pp, 2pp+1) for v = 8c .. 8c+7 of each build item.
+__device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
+                                            const int (&wbase)[IPT]) {
+#pragma unroll
+  for (int it = 0; it < IPT; ++it) {
+    unsigned char* base = smem + wbase[it];
+    const unsigned av[4] = {r.a[it].x, r.a[it].y, r.a[it].z, r.a[it].w};
+    const unsigned bv[4] = {r.b[it].x, r.b[it].y, r.b[it].z, r.b[it].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // dword i holds entries v = 8c + 2i (low half) and 8c + 2i + 1 (high)
+      *(unsigned*)(base + (2 * i) * 128) = __builtin_amdgcn_perm(bv[i], av[i], 0x05040100u);
+      *(unsigned*)(base + (2 * i + 1) * 128) = __builtin_amdgcn_perm(bv[i], av[i], 0x07060302u);
+    }
+  }
+}
+
+// Accumulates one table for this lane's RPL rows.  x holds the rows'
+// offsets (two per dword); gx XORs in the lane's channel chunk (bits 4-6) and
+// the LDS buffer (bit 15; offsets are below 32768).
+template <bool SIGNED>
+__device__ __forceinline__ void use_table(int (&acc)[RPL][8], const unsigned char* smem,
+                                          const XRows& x, unsigned gx) {
+#pragma unroll
+  for (int h = 0; h < RPL / 8; ++h) {
+    const unsigned xd[4] = {x.v[h].x, x.v[h].y, x.v[h].z, x.v[h].w};
+    uint4 e[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e[2 * j] = *(const uint4*)(smem + ((xd[j] & 0xffffu) ^ gx));
+      e[2 * j + 1] = *(const uint4*)(smem + ((xd[j] >> 16) ^ gx));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) add8<SIGNED>(acc[8 * h + j], e[j]);
+  }
+}
+
+template <bool SIGNED>
+__global__ void __launch_bounds__(NT, 1)
+lut_gemm_kernel(const GemmParams p) {
+  __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane >> 3, g = lane & 7;
+
+  int lb = logical_block();
+  const int to = lb % p.tiles_o; lb /= p.tiles_o;
+  const int tr = lb % p.tiles_r;
+  const int s = lb / p.tiles_r;
+
+  const int o0 = to * OT;
+  const int rtile0 = tr * RT;
+  const int r0 = rtile0 + (wave * 8 + rg) * RPL;         // this lane's rows
+  const int kb = s * p.k_chunk;
+  const int ke = min(p.K, kb + p.k_chunk);
+
+  // Table-build mapping: build item q = wave*IPT + i (16 items) covers
+  // channel group og = q & 7 and v-chunk c = (q >> 3) * 16 + cc; lane
+  // (cc, pp) handles channel pair o0 + 8*og + 2*pp (+1).  Within a wave the
+  // 4-byte LDS writes hit every bank exactly twice (the minimum for 64 lanes).
+  const int cc = lane >> 2, pp = lane & 3;
+  int c[IPT], pair_col[IPT], wbase[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int q = wave * IPT + i;
+    const int og = q & 7;
+    c[i] = (q >> 3) * 16 + cc;
+    pair_col[i] = o0 + og * 8 + 2 * pp;
+    wbase[i] = c[i] * 1024 + ((og ^ (cc & 7)) << 4) + pp * 4;
+  }
+
+  const uint16_t* __restrict__ xt = p.xt;
+  const uint8_t* __restrict__ wt = p.wt;
+  const uint16_t* __restrict__ lut = p.lut16t;
+
+  int acc[RPL][8];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0;
+
+  if (kb < ke) {
+    // At step k the wave issues the loads for row offsets k+1, LUT rows of
+    // table k+1 and weight indices of k+2 (indices clamped to the range, so
+    // every load is unconditional), accumulates from table k, writes table
+    // k+1 into the other LDS buffer and meets the other waves at one barrier.
+    // The scheduling fence keeps the table write (which waits for the LUT
+    // rows) behind the accumulation, so the loads overlap a whole step.
+    const int klast = ke - 1;
+    constexpr unsigned BUFX = (unsigned)ETAB;               // bit 15
+    XRows xc;
+    unsigned wnext[IPT];
+    {
+      unsigned w0[IPT];
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        w0[i] = load_w(wt, p.Opad, kb, pair_col[i]);
+        wnext[i] = load_w(wt, p.Opad, min(kb + 1, klast), pair_col[i]);
+      }
+      Rows rows;
+      load_rows(rows, lut, w0, c);
+      load_x(xc, xt, p.Rpad, kb, r0);
+      write_table(smem, rows, wbase);
+    }
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) wbase[i] += ETAB;   // table kb+1 -> buffer 1
+    unsigned gx = (unsigned)(g << 4);                   // table kb in buffer 0
+    __syncthreads();
+
+    for (int k = kb; k < ke; ++k) {
+      XRows xn;
+      Rows rows;
+      unsigned wn2[IPT];
+      load_x(xn, xt, p.Rpad, min(k + 1, klast), r0);
+      load_rows(rows, lut, wnext, c);
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        wn2[i] = load_w(wt, p.Opad, min(k + 2, klast), pair_col[i]);
+      use_table<SIGNED>(acc, smem, xc, gx);
+      __builtin_amdgcn_sched_barrier(0);
+      write_table(smem, rows, wbase);
+      xc = xn;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        wnext[i] = wn2[i];
+        wbase[i] ^= ETAB;
+      }
+      gx ^= BUFX;
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: stage through LDS (channel-major), write rows coalesced.
+  __syncthreads();
+  const bool partial = p.splits > 1;
+  for (int round = 0; round < NWAVE; ++round) {
+    const bool mine = wave == round;
+    if (mine) {
+      // row j of row group rg is staged at position rg + 8*j (bank-spread)
+      int* stage = (int*)smem;
+#pragma unroll
+      for (int j = 0; j < RPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          stage[(g * 8 + e) * STAGE_S + rg + 8 * j] = acc[j][e];
+    }
+    __syncthreads();
+    if (mine) {
+      const int* stage = (const int*)smem;
+      const int rw0 = rtile0 + wave * RPW;   // first row of this wave
+#pragma unroll
+      for (int h = 0; h < RPW / 64; ++h) {
+        const int a = lane + 64 * h;             // row within the wave tile
+        const int r = rw0 + a;
+        const int n = r / p.L;
+        const int l = r - n * p.L;
+        const int q = (a / RPL) + 8 * (a % RPL); // staged position of row a
+        const long long ybase = (long long)n * p.O * p.L + l;
+        for (int oo = 0; oo < OT && r < p.R; ++oo) {
+          const int o = o0 + oo;
+          if (o >= p.O) break;
+          const int v = stage[oo * STAGE_S + q];
+          const long long yi = ybase + (long long)o * p.L;
+          if (partial) {
+            ((int*)p.y)[(long long)s * p.split_stride + yi] = v;
+          } else if (p.out_kind == ATX_OUT_I32) {
+            ((int*)p.y)[yi] = v;
+          } else if (p.out_kind == ATX_OUT_F32) {
+            ((float*)p.y)[yi] = (float)v;
+          } else {
+            const float sc = p.sx[0] * p.sw[o];
+            const float t = (float)v * sc;
+            ((float*)p.y)[yi] = p.bias ? p.bias[o] + t : t;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Split-K reduction: exact int64 sum of int32 partials, then the epilogue.
+__global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
+                                    long long numel, int O, int L, int out_kind,
+                                    void* __restrict__ y, const float* sx,
+                                    const float* sw, const float* bias) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
+       i += (long long)gridDim.x * blockDim.x) {
+    long long a = 0;
+    for (int s = 0; s < S; ++s) a += ws[(long long)s * numel + i];
+    if (out_kind == ATX_OUT_I32) {
+      ((int*)y)[i] = (int)a;
+    } else if (out_kind == ATX_OUT_F32) {
+      ((float*)y)[i] = (float)a;
+    } else {
+      const int o = (int)((i / L) % O);
+      const float sc = sx[0] * sw[o];
+      const float t = (float)a * sc;
+      ((float*)y)[i] = bias ? bias[o] + t : t;
+    }
+  }
+}
+
+// fp32-LUT fallback: one thread per output, fp32 sum in ascending k (the
+// reference's non-split order, csrc/claude/bgemm_lut_kernels.cuh:276-284).
+__global__ void lut_gemm_f32_kernel(const GemmParams p) {
+  const long long numel = (long long)p.R * p.O;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int o = (int)(i / p.R);
+    const int r = (int)(i - (long long)o * p.R);
+    float a = 0.0f;
+    for (int k = 0; k < p.K; ++k) {
+      const unsigned xi = (unsigned)p.xt[(long long)k * p.Rpad + r] >> 7;
+      const unsigned wi = p.wt[(long long)k * p.Opad + o];
+      a += p.lutf32t[wi * 256u + xi];
+    }
+    const int n = r / p.L, l = r - (r / p.L) * p.L;
+    const long long yi = ((long long)n * p.O + o) * p.L + l;
+    if (p.out_kind == ATX_OUT_DEQUANT) {
+      const float t = a * (p.sx[0] * p.sw[o]);
+      ((float*)p.y)[yi] = p.bias ? p.bias[o] + t : t;
+    } else {
+      ((float*)p.y)[yi] = a;
+    }
+  }
+}
+
+// Split plan shared by the workspace query and the launch.
+struct Plan { int tiles_r, tiles_o, splits, k_chunk; };
+
+static Plan make_plan(int N, int K, int L, int O, int kmax) {
+  Plan pl;
+  const long long R = (long long)N * L;
+  pl.tiles_r = (int)cdiv(R, RT);
+  pl.tiles_o = (int)cdiv(O, OT);
+  const long long tiles = (long long)pl.tiles_r * pl.tiles_o;
+  // Aim for >= 2 workgroups per CU (256 CUs) when K is long enough that each
+  // split still runs >= 64 k-steps; always split when K exceeds the exact
+  // int32 bound of one pass.
+  int splits = 1;
+  while (tiles * splits < 512 && K / (splits * 2) >= 64) splits *= 2;
+  while (cdiv(K, splits) > kmax) splits *= 2;
+  pl.k_chunk = K > 0 ? (int)cdiv(K, splits) : 1;
+  pl.splits = K > 0 ? (int)cdiv(K, pl.k_chunk) : 1;
+  return pl;
+}
+
+}  // namespace atx
+
+using namespace atx;
+
+extern "C" {
+
+int atx_lut_prepare(const float* lut, uint16_t* out16t, float* outf32t,
+                    int* flags, hipStream_t stream) {
+  ATX_REQUIRE(lut && out16t && outf32t && flags, "atx_lut_prepare: null pointer");
+  hipLaunchKernelGGL(lut_prepare_kernel, dim3(256), dim3(256), 0, stream, lut,
+                     out16t, outf32t, flags);
+  return check_launch("lut_prepare_kernel");
+}
+
+int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
+                   uint16_t* xt, int Rpad, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_pack_x_f32: negative size");
+  ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
+              "atx_pack_x_f32: Rpad must be a multiple of %d covering N*L", RT);
+  if ((long long)K * Rpad == 0) return ATX_OK;
+  ATX_REQUIRE(x && xt, "atx_pack_x_f32: null pointer");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
+  hipLaunchKernelGGL(pack_x_kernel<float>, grid, dim3(256), 0, stream, x, N, K, L,
+                     offset, xq, xt, Rpad);
+  return check_launch("pack_x_kernel<float>");
+}
+
+int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad,
+                  hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_pack_x_u8: negative size");
+  ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
+              "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
+  if ((long long)K * Rpad == 0) return ATX_OK;
+  ATX_REQUIRE(xq && xt, "atx_pack_x_u8: null pointer");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
+  hipLaunchKernelGGL(pack_x_kernel<uint8_t>, grid, dim3(256), 0, stream, xq, N, K,
+                     L, 0, (uint8_t*)nullptr, xt, Rpad);
+  return check_launch("pack_x_kernel<u8>");
+}
+
+int atx_pack_w_f32(const float* w, int O, int K, int offset, uint8_t* wq,
+                   uint8_t* wt, int Opad, hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && K >= 0, "atx_pack_w_f32: negative size");
+  ATX_REQUIRE(Opad >= O && Opad % OT == 0,
+              "atx_pack_w_f32: Opad must be a multiple of %d covering O", OT);
+  if ((long long)K * Opad == 0) return ATX_OK;
+  ATX_REQUIRE(w && wt, "atx_pack_w_f32: null pointer");
+  hipLaunchKernelGGL(pack_w_kernel<float>, dim3(elem_grid((long long)K * Opad, 256)),
+                     dim3(256), 0, stream, w, O, K, offset, wq, wt, Opad);
+  return check_launch("pack_w_kernel<float>");
+}
+
+int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
+                  hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && K >= 0, "atx_pack_w_u8: negative size");
+  ATX_REQUIRE(Opad >= O && Opad % OT == 0,
+              "atx_pack_w_u8: Opad must be a multiple of %d covering O", OT);
+  if ((long long)K * Opad == 0) return ATX_OK;
+  ATX_REQUIRE(wq && wt, "atx_pack_w_u8: null pointer");
+  hipLaunchKernelGGL(pack_w_kernel<uint8_t>, dim3(elem_grid((long long)K * Opad, 256)),
+                     dim3(256), 0, stream, wq, O, K, 0, (uint8_t*)nullptr, wt, Opad);
+  return check_launch("pack_w_kernel<u8>");
+}
+
+long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O) {
+  if (N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
+  const Plan pl = make_plan(N, K, L, O, KMAX_U16);
+  if (pl.splits <= 1) return 0;
+  return (long long)pl.splits * N * O * L * 4;
+}
+
+int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                 int N, int K, int L, int O, const uint16_t* lut16t,
+                 const float* lutf32t, int lut_class, atx_gemm_epilogue ep,
+                 void* y, void* workspace, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_lut_gemm: negative size");
+  const long long R = (long long)N * L;
+  ATX_REQUIRE(R <= 0x7fffffffLL - RT, "atx_lut_gemm: N*L too large");
+  ATX_REQUIRE(Rpad >= R && Rpad % RT == 0, "atx_lut_gemm: bad Rpad %d", Rpad);
+  ATX_REQUIRE(Opad >= O && Opad % OT == 0, "atx_lut_gemm: bad Opad %d", Opad);
+  ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,
+              "atx_lut_gemm: bad out_kind");
+  ATX_REQUIRE(lut_class >= ATX_LUT_I16 && lut_class <= ATX_LUT_F32,
+              "atx_lut_gemm: bad lut_class");
+  ATX_REQUIRE(!(lut_class == ATX_LUT_F32 && ep.out_kind == ATX_OUT_I32),
+              "atx_lut_gemm: int32 output needs an integer LUT");
+  ATX_REQUIRE(ep.out_kind != ATX_OUT_DEQUANT || (ep.scale_x && ep.scale_w),
+              "atx_lut_gemm: dequant epilogue needs scale_x and scale_w");
+  if (R * O == 0) return ATX_OK;
+  ATX_REQUIRE(y, "atx_lut_gemm: null output");
+  // K == 0 is an empty contraction: every sum is 0 and only the epilogue runs.
+  ATX_REQUIRE(K == 0 || (xt && wt), "atx_lut_gemm: null operand");
+
+  GemmParams p{};
+  p.xt = xt; p.Rpad = Rpad; p.wt = wt; p.Opad = Opad;
+  p.lut16t = lut16t; p.lutf32t = lutf32t;
+  p.K = K; p.R = (int)R; p.L = L; p.O = O;
+  p.out_kind = ep.out_kind; p.y = y;
+  p.sx = ep.scale_x; p.sw = ep.scale_w; p.bias = ep.bias;
+
+  if (lut_class == ATX_LUT_F32) {
+    ATX_REQUIRE(lutf32t, "atx_lut_gemm: fp32 class needs the fp32 image");
+    p.tiles_r = p.tiles_o = p.splits = 1;
+    hipLaunchKernelGGL(lut_gemm_f32_kernel, dim3(elem_grid(R * O, 256)), dim3(256),
+                       0, stream, p);
+    return check_launch("lut_gemm_f32_kernel");
+  }
+  ATX_REQUIRE(lut16t, "atx_lut_gemm: integer class needs the 16-bit image");
+  const Plan pl = make_plan(N, K, L, O, KMAX_U16);
+  p.tiles_r = pl.tiles_r; p.tiles_o = pl.tiles_o;
+  p.splits = pl.splits; p.k_chunk = pl.k_chunk;
+  const long long numel = R * O;
+  if (pl.splits > 1) {
+    ATX_REQUIRE(workspace, "atx_lut_gemm: split-K plan needs a workspace of %lld bytes",
+                (long long)pl.splits * numel * 4);
+    p.y = workspace;
+    p.split_stride = numel;
+  }
+  const long long blocks = (long long)pl.tiles_r * pl.tiles_o * pl.splits;
+  ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_lut_gemm: grid too large");
+  if (lut_class == ATX_LUT_I16)
+    hipLaunchKernelGGL(lut_gemm_kernel<true>, dim3((unsigned)blocks), dim3(NT), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL(lut_gemm_kernel<false>, dim3((unsigned)blocks), dim3(NT), 0,
+                       stream, p);
+  int rc = check_launch("lut_gemm_kernel");
+  if (rc != ATX_OK || pl.splits == 1) return rc;
+  hipLaunchKernelGGL(split_reduce_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
+                     stream, (const int*)workspace, pl.splits, numel, O, L,
+                     ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
+  return check_launch("split_reduce_kernel");
+}
+
+}  // extern "C"

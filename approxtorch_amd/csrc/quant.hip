@@ -1,0 +1,335 @@
+// Fake-quant, EMA statistics and quantization-parameter kernels (HBM-bound).
+//
+// Bit-exactness with the reference's torch formulas matters here: a scale
+// that differs by one ulp can flip the rounding of x/s and change LUT sums.
+// The library is compiled with -ffp-contract=off, so every a*b+c below is two
+// rounded operations, exactly like the separate torch ops it mirrors, and
+// x/s is the correctly rounded fp32 division.
+
+#include "atx_internal.h"
+
+#include <algorithm>
+
+namespace atx {
+
+constexpr int EW = 256;   // threads per elementwise block
+
+// torch.clamp semantics: NaN propagates (comparisons with NaN are false).
+__device__ __forceinline__ float clamp_lo(float v, float lo) { return v < lo ? lo : v; }
+__device__ __forceinline__ float clamp_hi(float v, float hi) { return v > hi ? hi : v; }
+
+// nn/quantization.py:48-52 (symmetric) and :76-80 (asymmetric);
+// csrc/claude/quantization.cu:54-75.
+__device__ __forceinline__ float fake_quant(float x, float s, float z, bool asym,
+                                            float qmin, float qmax, bool& m) {
+  float v = x / s;
+  if (asym) v = v + z;
+  m = (v >= qmin) && (v <= qmax);
+  float r = __builtin_rintf(v);          // round half to even == torch.round
+  r = clamp_lo(r, qmin);
+  r = clamp_hi(r, qmax);
+  return r;
+}
+
+// Byte image of a quantized value; NaN maps to 0.
+__device__ __forceinline__ int to_int(float r) { return (r == r) ? (int)r : 0; }
+
+__global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
+                                     const float* __restrict__ scale,
+                                     const float* __restrict__ zero, float qmin,
+                                     float qmax, float* __restrict__ q,
+                                     uint8_t* __restrict__ mask, uint8_t* __restrict__ q8) {
+  const float s = fmaxf(scale[0], 1e-12f);
+  const bool asym = zero != nullptr;
+  const float z = asym ? zero[0] : 0.0f;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    bool m;
+    const float r = fake_quant(x[i], s, z, asym, qmin, qmax, m);
+    if (q) q[i] = r;
+    if (mask) mask[i] = m;
+    if (q8) q8[i] = (uint8_t)to_int(r);
+  }
+}
+
+// gx = (mask ? go : 0) / s[c], c = (i / inner) % C.
+__global__ void fakequant_bwd_kernel(const float* __restrict__ go,
+                                     const uint8_t* __restrict__ mask, long long n,
+                                     const float* __restrict__ scale, int C,
+                                     long long inner, float* __restrict__ gx) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int c = C == 1 ? 0 : (int)((i / inner) % C);
+    const float s = fmaxf(scale[c], 1e-12f);
+    gx[i] = (mask[i] ? go[i] : 0.0f) / s;
+  }
+}
+
+// Weight [O, inner] per-channel fake-quant; wt is the LUT GEMM's transposed
+// weight operand [inner][Opad] (columns >= O hold index 0).
+__global__ void fakequant_channel_kernel(const float* __restrict__ w, int O,
+                                         long long inner, const float* __restrict__ scale,
+                                         const float* __restrict__ zero, float qmin,
+                                         float qmax, int offset, float* __restrict__ q,
+                                         uint8_t* __restrict__ mask, uint8_t* __restrict__ wq,
+                                         uint8_t* __restrict__ wt, int Opad) {
+  const long long total = inner * Opad;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
+       t += stride) {
+    // t enumerates the transposed operand so its stores are coalesced.
+    const long long k = t / Opad;
+    const int o = (int)(t - k * Opad);
+    unsigned idx = 0;
+    if (o < O) {
+      const float s = fmaxf(scale[o], 1e-12f);
+      const bool asym = zero != nullptr;
+      bool m;
+      const long long i = (long long)o * inner + k;
+      const float r = fake_quant(w[i], s, asym ? zero[o] : 0.0f, asym, qmin, qmax, m);
+      if (q) q[i] = r;
+      if (mask) mask[i] = m;
+      int v = to_int(r) + offset;
+      v = v < 0 ? 0 : (v > 255 ? 255 : v);
+      idx = (unsigned)v;
+      if (wq) wq[i] = (uint8_t)idx;
+    }
+    if (wt) wt[t] = (uint8_t)idx;
+  }
+}
+
+// ------------------------------------------------------------ reductions
+// NaN-propagating max/min (torch.max / torch.amin semantics).
+__device__ __forceinline__ float nmax(float a, float b) {
+  return (a != a) ? a : ((b > a || b != b) ? b : a);
+}
+__device__ __forceinline__ float nmin(float a, float b) {
+  return (a != a) ? a : ((b < a || b != b) ? b : a);
+}
+
+template <bool ABS>
+__device__ __forceinline__ void block_minmax(float& mn, float& mx) {
+  __shared__ float smn[EW / 64], smx[EW / 64];
+  for (int off = 32; off > 0; off >>= 1) {
+    mn = nmin(mn, __shfl_xor(mn, off));
+    mx = nmax(mx, __shfl_xor(mx, off));
+  }
+  const int wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { smn[wv] = mn; smx[wv] = mx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < EW / 64; ++i) { mn = nmin(mn, smn[i]); mx = nmax(mx, smx[i]); }
+  }
+}
+
+// Pass 1: per-block min / max (or |x| max) into part[2*block].
+template <bool ABS>
+__global__ void minmax_partial_kernel(const float* __restrict__ x, long long n,
+                                      float* __restrict__ part) {
+  float mn = __builtin_inff(), mx = ABS ? 0.0f : -__builtin_inff();
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = ABS ? fabsf(x[i]) : x[i];
+    mn = nmin(mn, v);
+    mx = nmax(mx, v);
+  }
+  block_minmax<ABS>(mn, mx);
+  if (threadIdx.x == 0) { part[2 * blockIdx.x] = mn; part[2 * blockIdx.x + 1] = mx; }
+}
+
+// Pass 2: one block folds the partials.
+template <bool ABS>
+__global__ void minmax_final_kernel(const float* __restrict__ part, int nb,
+                                    float* mn_out, float* mx_out) {
+  float mn = __builtin_inff(), mx = ABS ? 0.0f : -__builtin_inff();
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+    mn = nmin(mn, part[2 * i]);
+    mx = nmax(mx, part[2 * i + 1]);
+  }
+  block_minmax<ABS>(mn, mx);
+  if (threadIdx.x == 0) {
+    if (mn_out) *mn_out = mn;
+    if (mx_out) *mx_out = mx;
+  }
+}
+
+constexpr int RED_BLOCKS = 1024;   // partial-result slots (2 floats each)
+
+// nn/Conv2d_int8.py:144-146 — cur = stat / denom; new = m*cur + (1-m)*old.
+__global__ void ema_absmax_kernel(const float* stat, float denom, float m32, float om32,
+                                  float* scale) {
+  const float cur = stat[0] / denom;
+  const float a = m32 * cur;
+  const float b = om32 * scale[0];
+  scale[0] = a + b;
+}
+
+// nn/Conv2d_uint8.py:11-23 (uint8_qparams) for one (min, max) pair.
+__device__ __forceinline__ void uint8_qparams(float mn, float mx, float qmax,
+                                              float& scale, float& zero) {
+  mn = clamp_hi(mn, 0.0f);
+  mx = clamp_lo(mx, 0.0f);
+  scale = clamp_lo((mx - mn) / qmax, 1e-12f);
+  const float z = __builtin_rintf(-mn / scale);
+  zero = clamp_hi(clamp_lo(z, 0.0f), qmax);
+}
+
+// nn/Conv2d_uint8.py:234-240.
+__global__ void ema_minmax_kernel(const float* mn, const float* mx, float m32, float om32,
+                                  float qmax, float* x_min, float* x_max, float* scale,
+                                  float* zero) {
+  x_min[0] = m32 * mn[0] + om32 * x_min[0];
+  x_max[0] = m32 * mx[0] + om32 * x_max[0];
+  uint8_qparams(x_min[0], x_max[0], qmax, scale[0], zero[0]);
+}
+
+// Per-channel reductions of a weight [O, inner]: one block per channel.
+// mode 0: int8 absmax EMA (nn/Conv2d_int8.py:148-158)
+// mode 1: int8 absmax reset (nn/Conv2d_int8.py:160-167)
+// mode 2: uint8 min/max EMA + qparams (nn/Conv2d_uint8.py:242-255)
+__global__ void weight_stats_kernel(const float* __restrict__ w, long long inner, int mode,
+                                    float qmax, float m32, float om32, float* scale_w,
+                                    float* zero_w, float* w_min, float* w_max) {
+  const int o = blockIdx.x;
+  const float* row = w + (long long)o * inner;
+  const bool absmode = mode != 2;
+  float mn = __builtin_inff(), mx = absmode ? 0.0f : -__builtin_inff();
+  for (long long i = threadIdx.x; i < inner; i += blockDim.x) {
+    const float v = absmode ? fabsf(row[i]) : row[i];
+    mn = nmin(mn, v);
+    mx = nmax(mx, v);
+  }
+  block_minmax<false>(mn, mx);
+  if (threadIdx.x != 0) return;
+  if (mode == 0) {
+    const float cur = (mx > 0.0f) ? mx / qmax : scale_w[o];
+    scale_w[o] = m32 * cur + om32 * scale_w[o];
+  } else if (mode == 1) {
+    scale_w[o] = (mx > 0.0f) ? mx / qmax : 1.0f;
+  } else {
+    w_min[o] = m32 * mn + om32 * w_min[o];
+    w_max[o] = m32 * mx + om32 * w_max[o];
+    uint8_qparams(w_min[o], w_max[o], qmax, scale_w[o], zero_w[o]);
+  }
+}
+
+}  // namespace atx
+
+using namespace atx;
+
+extern "C" {
+
+int atx_fakequant_fwd(const float* x, long long n, const float* scale, const float* zero,
+                      int qmin, int qmax, float* q, uint8_t* mask, void* q8,
+                      hipStream_t stream) {
+  ATX_REQUIRE(n >= 0, "atx_fakequant_fwd: negative size");
+  ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(x && scale, "atx_fakequant_fwd: null pointer");
+  hipLaunchKernelGGL(fakequant_fwd_kernel, dim3(elem_grid(n, EW)), dim3(EW), 0, stream,
+                     x, n, scale, zero, (float)qmin, (float)qmax, q, mask, (uint8_t*)q8);
+  return check_launch("fakequant_fwd_kernel");
+}
+
+int atx_fakequant_bwd(const float* go, const uint8_t* mask, long long n, const float* scale,
+                      int C, long long inner, float* gx, hipStream_t stream) {
+  ATX_REQUIRE(n >= 0 && C >= 1 && inner >= 1, "atx_fakequant_bwd: bad size");
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(go && mask && scale && gx, "atx_fakequant_bwd: null pointer");
+  hipLaunchKernelGGL(fakequant_bwd_kernel, dim3(elem_grid(n, EW)), dim3(EW), 0, stream, go,
+                     mask, n, scale, C, inner, gx);
+  return check_launch("fakequant_bwd_kernel");
+}
+
+int atx_fakequant_channel_fwd(const float* w, int O, long long inner, const float* scale,
+                              const float* zero, int qmin, int qmax, int offset, float* q,
+                              uint8_t* mask, uint8_t* wq, uint8_t* wt, int Opad,
+                              hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && inner >= 0, "atx_fakequant_channel_fwd: negative size");
+  ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
+  ATX_REQUIRE(!wt || (Opad >= O && Opad % ATX_COL_TILE == 0),
+              "atx_fakequant_channel_fwd: bad Opad %d", Opad);
+  const long long cols = wt ? Opad : O;
+  if (inner * cols == 0) return ATX_OK;
+  ATX_REQUIRE(w && scale, "atx_fakequant_channel_fwd: null pointer");
+  hipLaunchKernelGGL(fakequant_channel_kernel, dim3(elem_grid(inner * cols, EW)), dim3(EW),
+                     0, stream, w, O, inner, scale, zero, (float)qmin, (float)qmax, offset, q,
+                     mask, wq, wt, (int)cols);
+  return check_launch("fakequant_channel_kernel");
+}
+
+static int minmax_impl(const float* x, long long n, unsigned int* ws, float* mn_out,
+                       float* mx_out, bool absmode, hipStream_t stream) {
+  ATX_REQUIRE(n > 0, "min/max of an empty tensor is undefined");
+  ATX_REQUIRE(x && ws, "minmax: null pointer");
+  const int nb = elem_grid(n, EW, RED_BLOCKS);
+  float* part = (float*)ws;
+  if (absmode)
+    hipLaunchKernelGGL(minmax_partial_kernel<true>, dim3(nb), dim3(EW), 0, stream, x, n, part);
+  else
+    hipLaunchKernelGGL(minmax_partial_kernel<false>, dim3(nb), dim3(EW), 0, stream, x, n, part);
+  int rc = check_launch("minmax_partial_kernel");
+  if (rc) return rc;
+  if (absmode)
+    hipLaunchKernelGGL(minmax_final_kernel<true>, dim3(1), dim3(EW), 0, stream, part, nb,
+                       mn_out, mx_out);
+  else
+    hipLaunchKernelGGL(minmax_final_kernel<false>, dim3(1), dim3(EW), 0, stream, part, nb,
+                       mn_out, mx_out);
+  return check_launch("minmax_final_kernel");
+}
+
+long long atx_reduce_workspace_bytes(void) { return (long long)RED_BLOCKS * 2 * 4; }
+
+int atx_absmax(const float* x, long long n, unsigned int* ws, float* stat_out,
+               hipStream_t stream) {
+  ATX_REQUIRE(stat_out, "atx_absmax: null output");
+  return minmax_impl(x, n, ws, nullptr, stat_out, true, stream);
+}
+
+int atx_minmax(const float* x, long long n, unsigned int* ws, float* mn_out, float* mx_out,
+               hipStream_t stream) {
+  ATX_REQUIRE(mn_out && mx_out, "atx_minmax: null output");
+  return minmax_impl(x, n, ws, mn_out, mx_out, false, stream);
+}
+
+int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32, float* scale,
+                         hipStream_t stream) {
+  ATX_REQUIRE(stat && scale, "atx_ema_absmax_apply: null pointer");
+  hipLaunchKernelGGL(ema_absmax_kernel, dim3(1), dim3(1), 0, stream, stat, denom, m32, om32,
+                     scale);
+  return check_launch("ema_absmax_kernel");
+}
+
+int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32, int qmax,
+                         float* x_min, float* x_max, float* scale, float* zero,
+                         hipStream_t stream) {
+  ATX_REQUIRE(mn && mx && x_min && x_max && scale && zero, "atx_ema_minmax_apply: null");
+  hipLaunchKernelGGL(ema_minmax_kernel, dim3(1), dim3(1), 0, stream, mn, mx, m32, om32,
+                     (float)qmax, x_min, x_max, scale, zero);
+  return check_launch("ema_minmax_kernel");
+}
+
+int atx_weight_scale_ema(const float* w, int O, long long inner, float qmax_w, float m32,
+                         float om32, int reset, float* scale_w, hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && inner > 0, "atx_weight_scale_ema: bad size");
+  if (O == 0) return ATX_OK;
+  ATX_REQUIRE(w && scale_w, "atx_weight_scale_ema: null pointer");
+  hipLaunchKernelGGL(weight_stats_kernel, dim3(O), dim3(EW), 0, stream, w, inner,
+                     reset ? 1 : 0, qmax_w, m32, om32, scale_w, (float*)nullptr,
+                     (float*)nullptr, (float*)nullptr);
+  return check_launch("weight_stats_kernel");
+}
+
+int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32, float om32,
+                          int qmax, float* w_min, float* w_max, float* scale_w, float* zero_w,
+                          hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && inner > 0, "atx_weight_minmax_ema: bad size");
+  if (O == 0) return ATX_OK;
+  ATX_REQUIRE(w && w_min && w_max && scale_w && zero_w, "atx_weight_minmax_ema: null");
+  hipLaunchKernelGGL(weight_stats_kernel, dim3(O), dim3(EW), 0, stream, w, inner, 2,
+                     (float)qmax, m32, om32, scale_w, zero_w, w_min, w_max);
+  return check_launch("weight_stats_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,213 @@
+"""Conv2d_int8: int8 approximate-multiplier convolution (decoupled: integer
+LUT conv + dequant at the end).  Mirrors approxtorch/nn/Conv2d_int8.py:9-220:
+same constructor, buffers (lut, scale_x, scale_w, dx, dw), EMA rules and
+forward composition; the per-step statistics, fake-quant and LUT conv run as
+HIP kernels.
+"""
+import math
+
+import torch
+import torch.distributed as dist
+import torch.nn as nn
+from torch.nn.modules.utils import _pair
+
+from . import bgemm_int8, quantization
+from ..backend import _lib as L
+from ..backend import ops
+
+
+def _ema_coeffs(m):
+    # torch evaluates `m * cur + (1 - m) * old` with both python scalars cast
+    # to fp32: reproduce those two constants exactly.
+    return float(torch.tensor(m, dtype=torch.float32)), \
+        float(torch.tensor(1 - m, dtype=torch.float32))
+
+
+class Conv2d_int8(nn.Module):
+
+    def __init__(self,
+                 in_channels: int,
+                 out_channels: int,
+                 kernel_size,
+                 lut: torch.Tensor,
+                 grad: str = 'ste',
+                 dx: torch.Tensor | None = None,
+                 dw: torch.Tensor | None = None,
+                 bias=None,
+                 stride=1,
+                 padding=0,
+                 dilation=1,
+                 groups: int = 1,
+                 update_scale: bool = True,
+                 scale_momentum: float = 0.05,
+                 weight_bits: int = 8):
+        super().__init__()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = _pair(kernel_size)
+        self.stride = _pair(stride)
+        self.padding = _pair(padding)
+        self.dilation = _pair(dilation)
+        if groups != 1 and not (groups == in_channels and out_channels == in_channels):
+            raise NotImplementedError(
+                "Conv2d_int8 supports groups=1 or depthwise "
+                f"(groups == in_channels == out_channels), got groups={groups}, "
+                f"in={in_channels}, out={out_channels}")
+        if groups != 1:
+            raise NotImplementedError(
+                "depthwise Conv2d_int8 (groups == in_channels) is not built for gfx950 yet")
+        self.groups = groups
+        if grad not in ('ste', 'lre', 'custom'):
+            raise ValueError(f"grad must be 'ste', 'lre' or 'custom', got {grad}")
+        if grad == 'custom' and groups != 1:
+            raise NotImplementedError("custom gradient currently supports only groups=1")
+        self.grad = grad
+        self.qmin = -127
+        self.qmax = 127
+        self.weight_bits = weight_bits
+        if not 3 <= weight_bits <= 8:
+            raise ValueError(f"weight_bits must be between 3 and 8, got {weight_bits}")
+        if not 0.0 <= scale_momentum <= 1.0:
+            raise ValueError(f"scale_momentum must be between 0 and 1, got {scale_momentum}")
+        self.scale_momentum = scale_momentum
+        self.update_scale = update_scale
+
+        self.register_buffer('lut', lut)
+        self.weight = nn.Parameter(torch.empty(self.out_channels,
+                                               self.in_channels // self.groups,
+                                               self.kernel_size[0], self.kernel_size[1]))
+        self.register_buffer('scale_x', torch.tensor(1.0))
+        self.register_buffer('scale_w', torch.ones(self.out_channels))
+
+        if isinstance(bias, torch.Tensor) or bias is True:
+            self.bias = nn.Parameter(torch.empty(self.out_channels))
+        elif bias is False or bias is None:
+            self.bias = None
+        else:
+            raise ValueError("Invalid bias type")
+
+        self.reset_parameters()
+        self._reset_scale_w_from_weight()
+
+        if isinstance(bias, torch.Tensor):
+            if bias.shape != (self.out_channels,):
+                raise ValueError(
+                    f"bias must have shape ({self.out_channels},), got {tuple(bias.shape)}")
+            with torch.no_grad():
+                self.bias.copy_(bias)
+
+        if grad == 'lre':
+            if dx is None or dw is None:
+                raise ValueError("dx and dw are required when grad='lre'")
+            self.register_buffer('dx', dx)
+            self.register_buffer('dw', dw)
+        elif grad == 'custom':
+            if dx is None or dw is None:
+                raise ValueError("dx and dw are required when grad='custom'")
+            if not isinstance(dx, torch.Tensor) or not isinstance(dw, torch.Tensor):
+                raise TypeError("custom dx and dw must be torch.Tensor objects")
+            if dx.numel() != 256 * 256 or dw.numel() != 256 * 256:
+                raise ValueError("custom dx and dw must each have 65536 elements "
+                                 "for grad_lut[x + 128][w + 128]")
+            if dx.dtype != torch.float32 or dw.dtype != torch.float32:
+                raise TypeError("custom dx and dw must have dtype torch.float32")
+            self.register_buffer('dx', dx.contiguous().view(-1))
+            self.register_buffer('dw', dw.contiguous().view(-1))
+
+    def reset_parameters(self):
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            fan_in = (self.in_channels // self.groups) * self.kernel_size[0] * self.kernel_size[1]
+            bound = 1 / math.sqrt(fan_in) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def __repr__(self):
+        return (f"Conv2d_int8(in_channels={self.in_channels}, out_channels={self.out_channels}, "
+                f"kernel_size={self.kernel_size}, stride={self.stride}, padding={self.padding}, "
+                f"dilation={self.dilation}, groups={self.groups}, grad={self.grad}, "
+                f"weight_bits={self.weight_bits})")
+
+    def unfreeze_scale(self):
+        self.update_scale = True
+
+    def freeze_scale(self):
+        self.update_scale = False
+
+    def _update_scale(self, x):
+        """scale_x <- m * absmax(x)/127 + (1-m) * scale_x (nn/Conv2d_int8.py:137-146).
+        The absmax reduction and the EMA run on the device; under DDP the
+        statistic is MAX-all-reduced in between so every rank's scale agrees."""
+        with torch.no_grad():
+            xc = x.contiguous()
+            stat = torch.empty((), dtype=torch.float32, device=x.device)
+            ws = ops._reduce_ws(x.device)
+            s = L.stream_of(xc)
+            L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
+            if dist.is_available() and dist.is_initialized():
+                dist.all_reduce(stat, op=dist.ReduceOp.MAX)
+            m32, om32 = _ema_coeffs(self.scale_momentum)
+            L.call("atx_ema_absmax_apply", L.ptr(stat),
+                   float((self.qmax - self.qmin) / 2), m32, om32, L.ptr(self.scale_x), s)
+
+    def _update_scale_w(self):
+        """Per-channel EMA of absmax(W)/qmax_w; zero channels keep their scale
+        (nn/Conv2d_int8.py:148-158)."""
+        with torch.no_grad():
+            w = self.weight.detach().contiguous()
+            O = w.size(0)
+            m32, om32 = _ema_coeffs(self.scale_momentum)
+            L.call("atx_weight_scale_ema", L.ptr(w), O, w.numel() // max(O, 1),
+                   float(2 ** (self.weight_bits - 1) - 1), m32, om32, 0,
+                   L.ptr(self.scale_w), L.stream_of(w))
+
+    def _reset_scale_w_from_weight(self):
+        """scale_w = absmax(W)/qmax_w per channel (1 for zero channels); runs at
+        construction / conversion time, possibly on the CPU
+        (nn/Conv2d_int8.py:160-167)."""
+        with torch.no_grad():
+            qmax_w = 2 ** (self.weight_bits - 1) - 1
+            w = self.weight.detach()
+            if w.is_cuda:
+                wc = w.contiguous()
+                O = wc.size(0)
+                L.call("atx_weight_scale_ema", L.ptr(wc), O, wc.numel() // max(O, 1),
+                       float(qmax_w), 1.0, 0.0, 1, L.ptr(self.scale_w), L.stream_of(wc))
+                return
+            absmax = w.abs().amax(dim=tuple(range(1, w.dim())))
+            self.scale_w.copy_(torch.where(absmax > 0, absmax / qmax_w, torch.ones_like(absmax)))
+
+    def forward(self, x: torch.Tensor):
+        B, _, H, W = x.shape
+        O, _, kH, kW = self.weight.shape
+        sH, sW = self.stride
+        pH, pW = self.padding
+        dH, dW = self.dilation
+        OH = (H + 2 * pH - dH * (kH - 1) - 1) // sH + 1
+        OW = (W + 2 * pW - dW * (kW - 1) - 1) // sW + 1
+
+        if self.training and self.update_scale:
+            self._update_scale(x)
+            self._update_scale_w()
+
+        x = quantization.static_quantize_int8(x, self.scale_x, self.qmin, self.qmax)
+        qmax_w = 2 ** (self.weight_bits - 1) - 1
+        w = quantization.static_quantize_int8(self.weight, self.scale_w, -qmax_w, qmax_w,
+                                              ch_axis=0)
+        s_w = self.scale_w
+
+        geom = ((kH, kW), self.stride, self.padding, self.dilation, self.groups)
+        if self.grad == 'lre':
+            y = bgemm_int8.conv2d_int8_lre(x, w.view(O, -1), self.lut, self.dx, self.dw, geom)
+        elif self.grad == 'custom':
+            y = bgemm_int8.conv2d_int8_custom(x, w.view(O, -1), self.lut, self.dx, self.dw,
+                                              geom)
+        else:
+            y = bgemm_int8.conv2d_int8_ste(x, w.view(O, -1), self.lut, geom)
+
+        y = y.view(B, O, OH, OW)
+        s = (self.scale_x * s_w).view(1, -1, 1, 1)
+        if self.bias is not None:
+            y = torch.addcmul(self.bias.view(1, -1, 1, 1), y, s)
+        else:
+            y = y * s
+        return y

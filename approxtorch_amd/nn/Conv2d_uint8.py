@@ -1,0 +1,257 @@
+"""Conv2d_uint8: uint8 x uint8 approximate-multiplier convolution with static
+asymmetric quantization (per-tensor activations, per-channel weights).
+Mirrors approxtorch/nn/Conv2d_uint8.py:11-325: same buffers (x_min, x_max,
+w_min, w_max, scale_x, zero_x, scale_w, zero_w, lut, dx, dw), legacy
+checkpoint loading and the differentiable zero-point correction
+
+  sum_k (q_x - z_x)(q_w - z_w) = LUTSUM - z_w*sum_k q_x - z_x*sum_k q_w + K*z_x*z_w.
+
+Extension: `weight_bits` (default 8, the reference's only setting) quantizes
+weights to [0, 2**weight_bits - 1] with per-channel EMA qparams.
+"""
+import math
+
+import torch
+import torch.distributed as dist
+import torch.nn as nn
+from torch.nn.modules.utils import _pair
+
+from . import bgemm_uint8, quantization
+from ..backend import _lib as L
+from ..backend import ops
+from .Conv2d_int8 import _ema_coeffs
+
+
+def uint8_qparams(mn, mx, qmax=255):
+    """(scale, zero_point) from min/max statistics, range clamped to include 0
+    (nn/Conv2d_uint8.py:11-23)."""
+    mn = torch.clamp(mn, max=0.0)
+    mx = torch.clamp(mx, min=0.0)
+    scale = torch.clamp((mx - mn) / qmax, min=1e-12)
+    zero = torch.round(-mn / scale).clamp(0.0, float(qmax))
+    return scale, zero
+
+
+class Conv2d_uint8(nn.Module):
+
+    def __init__(self,
+                 in_channels: int,
+                 out_channels: int,
+                 kernel_size,
+                 lut: torch.Tensor,
+                 grad: str = 'ste',
+                 dx: torch.Tensor | None = None,
+                 dw: torch.Tensor | None = None,
+                 bias=None,
+                 stride=1,
+                 padding=0,
+                 dilation=1,
+                 groups: int = 1,
+                 update_scale: bool = True,
+                 scale_momentum: float = 0.05,
+                 weight_bits: int = 8):
+        super().__init__()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = _pair(kernel_size)
+        self.stride = _pair(stride)
+        self.padding = _pair(padding)
+        self.dilation = _pair(dilation)
+        if groups != 1:
+            raise NotImplementedError(
+                f"Conv2d_uint8 only supports groups=1 for now, got groups={groups}")
+        self.groups = groups
+        if grad not in ('ste', 'lre', 'custom'):
+            raise ValueError(f"grad must be 'ste', 'lre' or 'custom', got {grad}")
+        self.grad = grad
+        self.qmin = 0
+        self.qmax = 255
+        if not 1 <= weight_bits <= 8:
+            raise ValueError(f"weight_bits must be between 1 and 8, got {weight_bits}")
+        self.weight_bits = weight_bits
+        self.qmax_w = 2 ** weight_bits - 1
+        if not 0.0 <= scale_momentum <= 1.0:
+            raise ValueError(f"scale_momentum must be between 0 and 1, got {scale_momentum}")
+        self.scale_momentum = scale_momentum
+        self.update_scale = update_scale
+
+        self.register_buffer('lut', lut)
+        self.weight = nn.Parameter(torch.empty(self.out_channels, self.in_channels,
+                                               self.kernel_size[0], self.kernel_size[1]))
+        self.register_buffer('x_min', torch.tensor(0.0))
+        self.register_buffer('x_max', torch.tensor(1.0))
+        self.register_buffer('w_min', torch.zeros(self.out_channels))
+        self.register_buffer('w_max', torch.ones(self.out_channels))
+        self.register_buffer('scale_x', torch.tensor(1.0 / self.qmax))
+        self.register_buffer('zero_x', torch.tensor(0.0))
+        self.register_buffer('scale_w', torch.ones(self.out_channels))
+        self.register_buffer('zero_w', torch.zeros(self.out_channels))
+
+        if isinstance(bias, torch.Tensor) or bias is True:
+            self.bias = nn.Parameter(torch.empty(self.out_channels))
+        elif bias is False or bias is None:
+            self.bias = None
+        else:
+            raise ValueError("Invalid bias type")
+
+        self.reset_parameters()
+        with torch.no_grad():
+            reduce_dims = tuple(range(1, self.weight.dim()))
+            self.w_min.copy_(self.weight.detach().amin(dim=reduce_dims))
+            self.w_max.copy_(self.weight.detach().amax(dim=reduce_dims))
+        self._reset_qparams_from_stats()
+
+        if isinstance(bias, torch.Tensor):
+            if bias.shape != (self.out_channels,):
+                raise ValueError(
+                    f"bias must have shape ({self.out_channels},), got {tuple(bias.shape)}")
+            with torch.no_grad():
+                self.bias.copy_(bias)
+
+        if grad == 'lre':
+            if dx is None or dw is None:
+                raise ValueError("dx and dw are required when grad='lre'")
+            if not isinstance(dx, torch.Tensor) or not isinstance(dw, torch.Tensor):
+                raise TypeError("lre dx and dw must be torch.Tensor objects")
+            if dx.numel() != 256 or dw.numel() != 256:
+                raise ValueError("lre dx and dw must each have 256 elements, indexed by "
+                                 "the raw uint8 operand value")
+            if dx.dtype != torch.float32 or dw.dtype != torch.float32:
+                raise TypeError("lre dx and dw must have dtype torch.float32")
+            self.register_buffer('dx', dx.contiguous().view(-1))
+            self.register_buffer('dw', dw.contiguous().view(-1))
+        elif grad == 'custom':
+            if dx is None or dw is None:
+                raise ValueError("dx and dw are required when grad='custom'")
+            if not isinstance(dx, torch.Tensor) or not isinstance(dw, torch.Tensor):
+                raise TypeError("custom dx and dw must be torch.Tensor objects")
+            if dx.numel() != 256 * 256 or dw.numel() != 256 * 256:
+                raise ValueError("custom dx and dw must each have 65536 elements for "
+                                 "grad_lut[x][w]")
+            if dx.dtype != torch.float32 or dw.dtype != torch.float32:
+                raise TypeError("custom dx and dw must have dtype torch.float32")
+            self.register_buffer('dx', dx.contiguous().view(-1))
+            self.register_buffer('dw', dw.contiguous().view(-1))
+
+    def reset_parameters(self):
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            fan_in = self.in_channels * self.kernel_size[0] * self.kernel_size[1]
+            bound = 1 / math.sqrt(fan_in) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def __repr__(self):
+        extra = f", weight_bits={self.weight_bits}" if self.weight_bits != 8 else ""
+        return (f"Conv2d_uint8(in_channels={self.in_channels}, out_channels={self.out_channels}, "
+                f"kernel_size={self.kernel_size}, stride={self.stride}, padding={self.padding}, "
+                f"dilation={self.dilation}, groups={self.groups}, grad={self.grad}{extra})")
+
+    def unfreeze_scale(self):
+        self.update_scale = True
+
+    def freeze_scale(self):
+        self.update_scale = False
+
+    def _reset_qparams_from_stats(self):
+        with torch.no_grad():
+            scale_x, zero_x = uint8_qparams(self.x_min, self.x_max, self.qmax)
+            scale_w, zero_w = uint8_qparams(self.w_min, self.w_max, self.qmax_w)
+            self.scale_x.copy_(scale_x)
+            self.zero_x.copy_(zero_x)
+            self.scale_w.copy_(scale_w)
+            self.zero_w.copy_(zero_w)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict,
+                              missing_keys, unexpected_keys, error_msgs):
+        # checkpoints with only min/max statistics (nn/Conv2d_uint8.py:195-223)
+        qparam_names = ('scale_x', 'zero_x', 'scale_w', 'zero_w')
+        legacy_stats_only = all(prefix + name not in state_dict for name in qparam_names)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict,
+                                      missing_keys, unexpected_keys, error_msgs)
+        if legacy_stats_only:
+            self._reset_qparams_from_stats()
+            for name in qparam_names:
+                key = prefix + name
+                if key in missing_keys:
+                    missing_keys.remove(key)
+        for name, hi in (('zero_x', self.qmax), ('zero_w', self.qmax_w)):
+            zero = getattr(self, name)
+            valid = (torch.isfinite(zero).all() and (zero >= self.qmin).all()
+                     and (zero <= hi).all() and torch.equal(zero, torch.round(zero)))
+            if not valid:
+                error_msgs.append(f"{prefix}{name} must contain integer-valued "
+                                  f"values in [{self.qmin}, {hi}]")
+
+    def _update_scale(self, x):
+        """min/max EMA of the activations, then qparams, on the device; MIN/MAX
+        all-reduce under DDP (nn/Conv2d_uint8.py:225-240)."""
+        with torch.no_grad():
+            xc = x.contiguous()
+            mn = torch.empty((), dtype=torch.float32, device=x.device)
+            mx = torch.empty((), dtype=torch.float32, device=x.device)
+            ws = ops._reduce_ws(x.device)
+            s = L.stream_of(xc)
+            L.call("atx_minmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn), L.ptr(mx), s)
+            if dist.is_available() and dist.is_initialized():
+                dist.all_reduce(mn, op=dist.ReduceOp.MIN)
+                dist.all_reduce(mx, op=dist.ReduceOp.MAX)
+            m32, om32 = _ema_coeffs(self.scale_momentum)
+            L.call("atx_ema_minmax_apply", L.ptr(mn), L.ptr(mx), m32, om32, self.qmax,
+                   L.ptr(self.x_min), L.ptr(self.x_max), L.ptr(self.scale_x),
+                   L.ptr(self.zero_x), s)
+
+    def _update_scale_w(self):
+        """Per-channel min/max EMA of the weights + qparams (nn/Conv2d_uint8.py:242-255)."""
+        with torch.no_grad():
+            w = self.weight.detach().contiguous()
+            O = w.size(0)
+            m32, om32 = _ema_coeffs(self.scale_momentum)
+            L.call("atx_weight_minmax_ema", L.ptr(w), O, w.numel() // max(O, 1), m32, om32,
+                   self.qmax_w, L.ptr(self.w_min), L.ptr(self.w_max), L.ptr(self.scale_w),
+                   L.ptr(self.zero_w), L.stream_of(w))
+
+    def forward(self, x: torch.Tensor):
+        B, C, H, W = x.shape
+        O, _, kH, kW = self.weight.shape
+        sH, sW = self.stride
+        pH, pW = self.padding
+        dH, dW = self.dilation
+        OH = (H + 2 * pH - dH * (kH - 1) - 1) // sH + 1
+        OW = (W + 2 * pW - dW * (kW - 1) - 1) // sW + 1
+
+        if self.training and self.update_scale:
+            self._update_scale(x)
+            self._update_scale_w()
+
+        scale_x, zero_x = self.scale_x, self.zero_x
+        scale_w, zero_w = self.scale_w, self.zero_w
+
+        xq = quantization.static_quantize_uint8(x, scale_x, zero_x, self.qmin, self.qmax)
+        wq = quantization.static_quantize_uint8(self.weight, scale_w, zero_w, self.qmin,
+                                                self.qmax_w, ch_axis=0)
+        wu = wq.view(O, -1)
+        geom = ((kH, kW), self.stride, self.padding, self.dilation, self.groups)
+
+        # LUT sum of the raw uint8 values; padded taps read z_x.
+        if self.grad == 'lre':
+            y = bgemm_uint8.conv2d_uint8_lre(xq, wu, self.lut, self.dx, self.dw, zero_x, geom)
+        elif self.grad == 'custom':
+            y = bgemm_uint8.conv2d_uint8_custom(xq, wu, self.lut, self.dx, self.dw, zero_x,
+                                                geom)
+        else:
+            y = bgemm_uint8.conv2d_uint8_ste(xq, wu, self.lut, zero_x, geom)
+
+        # zero-point correction (differentiable through xsum / wsum)
+        Kdim = wu.shape[1]
+        xsum = bgemm_uint8.tap_sum(xq, zero_x, geom)             # (B, L)
+        wsum = wu.sum(dim=1)                                     # (O,)
+        zw = zero_w.view(1, -1, 1)
+        y = y - zw * xsum.unsqueeze(1) - (zero_x * wsum).view(1, -1, 1) + Kdim * zero_x * zw
+
+        y = y.view(B, O, OH, OW)
+        s = (scale_x * scale_w).view(1, -1, 1, 1)
+        if self.bias is not None:
+            y = torch.addcmul(self.bias.view(1, -1, 1, 1), y, s)
+        else:
+            y = y * s
+        return y

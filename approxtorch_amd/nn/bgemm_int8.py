@@ -1,0 +1,216 @@
+"""int8 LUT BGEMM / LUT conv autograd Functions (STE, LRE, custom).
+
+Forward: y[n,o,l] = sum_k lut[(x+128)*256 + (w+128)] on the gfx950 LUT GEMM.
+Backward (all HIP):
+  STE     the multiply is treated as exact on the quantized values;
+  LRE     grad_x uses dx[idx(w)], grad_w uses dw[idx(x)] (256-entry tables);
+  custom  grad_x uses dx_lut[idx(x)][idx(w)], grad_w dw_lut[idx(x)][idx(w)].
+Mirrors approxtorch/nn/bgemm_int8.py (GEMM level 5-84, conv level 87-298).
+Saved tensors are the uint8 index images (or the int8 image for the conv
+level), never the fp32 operands.
+"""
+import torch
+from torch.autograd import Function
+
+from ..backend import ops
+
+_TABLES = {}
+
+
+def decode_table(device, signed=True):
+    """[256] fp32 table idx -> quantized value (idx - 128 signed, idx unsigned)."""
+    key = (str(device), signed)
+    t = _TABLES.get(key)
+    if t is None:
+        t = torch.arange(256, device=device, dtype=torch.float32)
+        if signed:
+            t = t - 128
+        _TABLES[key] = t
+    return t
+
+
+def _gemm_geom(N, K, L):
+    # a [N, K, L] operand is the 1x1 im2col of an image [N, K, 1, L]
+    return ops.L.geom(N, K, 1, L, 1, 1, 1, 1, 0, 0, 1, 1)
+
+
+def _gemm_grads(go, xq, wq, tx, tw):
+    """grad_x [N,K,L], grad_w [O,K] of sum_k f(x,w) with per-operand tables."""
+    N, K, L = xq.shape
+    O = wq.size(0)
+    g = _gemm_geom(N, K, L)
+    go = go.contiguous()
+    col = torch.empty((N, K, L), dtype=torch.float32, device=go.device)
+    ops.L.call("atx_conv_bwd_data_col", go.data_ptr(), wq.data_ptr(), tx.data_ptr(), N, O, K,
+               L, col.data_ptr(), ops.L.stream_of(go))
+    gw = ops.conv_backward_weight(go, xq.view(N, K, 1, L), tw, g, O, 128)
+    return col, gw
+
+
+class _bgemm_int8_base(Function):
+
+    @staticmethod
+    def forward(ctx, x, w, lut):
+        y, xq, wq = ops.bgemm_fake_int8_claude_save(x, w, lut)
+        ctx.save_for_backward(xq, wq)
+        return y
+
+
+class _bgemm_int8_ste(_bgemm_int8_base):
+    """STE at GEMM level (nn/bgemm_int8.py:15-25): grad_x = W^T go, grad_w = go X^T
+    on the quantized values (decoded from the saved index images)."""
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xq, wq = ctx.saved_tensors
+        dec = decode_table(xq.device)
+        gx, gw = _gemm_grads(grad_output, xq, wq, dec, dec)
+        return gx, gw, None
+
+
+def bgemm_int8_ste(x, w, lut):
+    return _bgemm_int8_ste.apply(x, w, lut)
+
+
+class _bgemm_int8_lre(Function):
+    """LRE at GEMM level (nn/bgemm_int8.py:29-52)."""
+
+    @staticmethod
+    def forward(ctx, x, w, lut, dx, dw):
+        y, xq, wq = ops.bgemm_fake_int8_claude_save(x, w, lut)
+        ctx.save_for_backward(xq, wq)
+        ctx.dx, ctx.dw = dx, dw
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_outputs):
+        xq, wq = ctx.saved_tensors
+        gx, gw = _gemm_grads(grad_outputs, xq, wq, ctx.dx.contiguous(), ctx.dw.contiguous())
+        return gx, gw, None, None, None
+
+
+def bgemm_int8_lre(x, w, lut, dx, dw):
+    return _bgemm_int8_lre.apply(x, w, lut, dx, dw)
+
+
+class _bgemm_int8_custom(Function):
+    """BGEMM with one custom derivative per quantized (x, w) pair
+    (nn/bgemm_int8.py:55-84).  dx_lut / dw_lut are 256 x 256 row-major tables
+    indexed [x + 128][w + 128]."""
+
+    @staticmethod
+    def forward(ctx, x, w, lut, dx_lut, dw_lut):
+        y, xq, wq = ops.bgemm_fake_int8_claude_save(x, w, lut)
+        ctx.save_for_backward(xq, wq, dx_lut, dw_lut)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xq, wq, dx_lut, dw_lut = ctx.saved_tensors
+        grad_x = ops.bgemm_custom_grad_uint8_dx(xq, wq, grad_output, dx_lut)
+        grad_w = ops.bgemm_custom_grad_uint8_dw(xq, wq, grad_output, dw_lut)
+        return grad_x, grad_w, None, None, None
+
+
+def bgemm_int8_custom(x, w, lut, dx_lut, dw_lut):
+    return _bgemm_int8_custom.apply(x, w, lut, dx_lut, dw_lut)
+
+
+# ------------------------------------------------------------- conv level
+def _check_groups(groups):
+    if groups != 1:
+        raise NotImplementedError(
+            "the gfx950 LUT conv supports groups=1; depthwise LUT conv is not built yet")
+
+
+def _conv_setup(x, w, geom):
+    kernel_size, stride, padding, dilation, groups = geom
+    _check_groups(groups)
+    g = ops.conv_geom(tuple(x.shape), kernel_size, stride, padding, dilation)
+    return g
+
+
+class _conv2d_int8_ste(Function):
+    """Conv-level STE (nn/bgemm_int8.py:229-297).  Forward: implicit-im2col LUT
+    conv of the quantized image; saves the int8 image and uint8 weight
+    indices.  Backward: fp32-MFMA backward-data (+ fold) and backward-weight
+    on the decoded quantized values (zero padding decodes to 0)."""
+
+    @staticmethod
+    def forward(ctx, x, w, lut, geom):
+        g = _conv_setup(x, w, geom)
+        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
+        ctx.save_for_backward(x.detach().to(torch.int8), wq)
+        ctx.g = g
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_outputs):
+        xq8, wq = ctx.saved_tensors
+        g = ctx.g
+        dec = decode_table(xq8.device)
+        go = grad_outputs.contiguous()
+        grad_x = ops.conv_backward_data(go, wq, dec, g)
+        grad_w = ops.conv_backward_weight(go, xq8, dec, g, wq.size(0), 128)
+        return grad_x, grad_w, None, None
+
+
+def conv2d_int8_ste(x, w, lut, geom):
+    return _conv2d_int8_ste.apply(x, w, lut, geom)
+
+
+class _conv2d_int8_lre(Function):
+    """Conv-level LRE (nn/bgemm_int8.py:126-214): grad_x = fold(W'^T go) with
+    W' = dx[idx(w)], grad_w = go X'^T with X' = dw[idx(x)] and padded taps
+    taking dw[128]."""
+
+    @staticmethod
+    def forward(ctx, x, w, lut, dx, dw, geom):
+        g = _conv_setup(x, w, geom)
+        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
+        ctx.save_for_backward(x.detach().to(torch.int8), wq)
+        ctx.g, ctx.dx, ctx.dw = g, dx, dw
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_outputs):
+        xq8, wq = ctx.saved_tensors
+        g = ctx.g
+        go = grad_outputs.contiguous()
+        grad_x = ops.conv_backward_data(go, wq, ctx.dx.contiguous(), g)
+        grad_w = ops.conv_backward_weight(go, xq8, ctx.dw.contiguous(), g, wq.size(0), 128)
+        return grad_x, grad_w, None, None, None, None
+
+
+def conv2d_int8_lre(x, w, lut, dx, dw, geom):
+    return _conv2d_int8_lre.apply(x, w, lut, dx, dw, geom)
+
+
+class _conv2d_int8_custom(Function):
+    """Conv wrapper of the pair-wise custom-gradient kernels
+    (nn/bgemm_int8.py:87-123): saves the unfolded uint8 index image."""
+
+    @staticmethod
+    def forward(ctx, x, w, lut, dx_lut, dw_lut, geom):
+        kernel_size, stride, padding, dilation, groups = geom
+        if groups != 1:
+            raise NotImplementedError("custom gradient currently supports only groups=1")
+        g = _conv_setup(x, w, geom)
+        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
+        xu8 = ops.im2col_u8(x.detach(), kernel_size, stride, padding, dilation)
+        ctx.save_for_backward(xu8, wq, dx_lut, dw_lut)
+        ctx.g = g
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xq, wq, dx_lut, dw_lut = ctx.saved_tensors
+        go = grad_output.contiguous()
+        grad_x_col = ops.bgemm_custom_grad_uint8_dx(xq, wq, go, dx_lut)
+        grad_w = ops.bgemm_custom_grad_uint8_dw(xq, wq, go, dw_lut)
+        grad_x = ops.col2im(grad_x_col, ctx.g)
+        return grad_x, grad_w, None, None, None, None
+
+
+def conv2d_int8_custom(x, w, lut, dx_lut, dw_lut, geom):
+    return _conv2d_int8_custom.apply(x, w, lut, dx_lut, dw_lut, geom)

@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Benchmark of the LUT approximate-multiplier training path on one MI355X.
+
+Default workload (BASELINE.json metric "ResNet-50 224^2 approx-QAT img/s",
+config 4): ResNet-50, batch 64 x [3,224,224] ~ N(0,1), 1000 classes, every conv
+but the first converted to Conv2d_int8 (weight_bits 8) with the perturbed
+int16 LUT and LRE gradient tables; one step = forward, cross-entropy, LRE
+backward, SGD update.  `value` is img/s of the whole job (1 GPU).
+
+Also reported:
+  roofline      the dominant kernel, the LUT GEMM (lut_gemm_kernel): LUT-MACs
+                of every launch inside the timed region / their summed
+                durations (HIP events on the launch stream); bound = LDS, one
+                LUT-MAC = one 2-byte table read from LDS, peak = 256 CUs x
+                128 B/clk x 2.4 GHz.
+  lut_gemm      the standalone BGEMM microbench (config 3: B=32, 4096x2304 by
+                2304x256, perturbed LUT) in G LUT-MAC/s.
+  cpu_baseline  the torch-CPU restatement of the same training step
+                (oracle/torch_cpu.py) on a bounded sample (batch 1), scaled to img/s.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+LDS_PEAK_GBS = 256 * 128 * 2.4      # GB/s: 256 CUs x 128 B/clk x 2.4 GHz
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c4", choices=["c2", "c4", "c5", "c3"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-microbench", action="store_true")
+    ap.add_argument("--cpu-sample-batch", type=int, default=1)
+    return ap.parse_args()
+
+
+class GemmTimer:
+    """Brackets every atx_lut_gemm launch with events on its stream."""
+
+    def __init__(self):
+        self.events = []
+        self.macs = 0
+        self.active = False
+
+    def install(self):
+        import torch
+        from approxtorch_amd.backend import ops
+        orig = ops._gemm
+        timer = self
+
+        def timed(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw):
+            if not timer.active:
+                return orig(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            r = orig(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw)
+            e.record()
+            timer.events.append((s, e))
+            timer.macs += N * K * Lc * O
+            return r
+        ops._gemm = timed
+
+    def summary(self):
+        ms = sum(s.elapsed_time(e) for s, e in self.events)
+        return ms, self.macs, len(self.events)
+
+
+def lut_gemm_microbench(torch, reps=5):
+    """Config 3: B=32 x [4096 x K] int8 times [K x 256] int8 via the LUT GEMM."""
+    import numpy as np
+    from approxtorch_amd import workloads
+    from approxtorch_amd.backend import ops
+    out = {}
+    lut = torch.from_numpy(workloads.lut_perturbed(3)).cuda()
+    g = torch.Generator().manual_seed(3)
+    for K in (576, 1152, 2304, 4608):
+        x = torch.randint(0, 256, (32, K, 4096), generator=g, dtype=torch.uint8).cuda()
+        w = torch.randint(-128, 128, (256, K), generator=g).float().cuda()
+        ops.bgemm_fake_int8_claude(x, w, lut)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            ops.bgemm_fake_int8_claude(x, w, lut)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        out[str(K)] = round(32 * 4096 * K * 256 / (ms * 1e-3) / 1e9, 1)
+        del x, w
+    return out
+
+
+def cpu_baseline(model, cfg, sample_batch):
+    import torch
+    from approxtorch_amd import workloads
+    from oracle import torch_cpu
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cpu_model = torch_cpu.to_cpu_reference(model).train()
+    opt = torch.optim.SGD(cpu_model.parameters(), lr=0.01, momentum=0.9)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(sample_batch, 3, cfg["hw"], cfg["hw"], generator=g)
+    y = torch.randint(0, cfg["classes"], (sample_batch,), generator=g)
+    t0 = time.perf_counter()
+    workloads.training_step(cpu_model, opt, x, y)
+    dt = time.perf_counter() - t0
+    return {"value": round(sample_batch / dt, 4), "unit": "img/s", "cores": threads,
+            "kind": "port",
+            "sample": f"1 training step of the same model at batch {sample_batch} "
+                      f"(torch-CPU restatement, oracle/torch_cpu.py), {dt:.1f} s, "
+                      f"scaled as img/s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU runs are not part of this build)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import approxtorch_amd  # noqa: F401  (loads libatx.so, fails loudly if missing)
+    from approxtorch_amd import workloads
+    torch.backends.cudnn.benchmark = False
+    dev = torch.device("cuda:0")
+    name = args.workload if args.workload != "c3" else "c4"
+    model, opt, x, y, cfg = workloads.build_training_workload(name, dev)
+    macs_fwd = workloads.conv_lut_macs(model, tuple(x.shape))
+    timer = GemmTimer()
+    timer.install()
+    for _ in range(args.warmup):
+        workloads.training_step(model, opt, x, y)
+    torch.cuda.synchronize()
+    timer.active = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        workloads.training_step(model, opt, x, y)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timer.active = False
+    gemm_ms, gemm_macs, launches = timer.summary()
+    achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
+    result = {
+        "metric": "ResNet-50 224^2 approx-QAT img/s (LUT-MAC/s + % LDS roofline)"
+        if name == "c4" else f"{name} approx-QAT img/s",
+        "value": round(cfg["batch"] * args.steps / dt, 2),
+        "unit": "img/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32 LUT sums (int8 operands), fp32 backward",
+        "data": "synthetic (seeded N(0,1) images, uniform labels, random-init weights)",
+        "config": {"workload": f"{name}: {cfg['model']} batch {cfg['batch']} "
+                               f"{cfg['hw']}x{cfg['hw']} {cfg['qtype']} grad={cfg['grad']} "
+                               f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
+                   "global_batch": cfg["batch"], "parallelism": "single GPU",
+                   "forward_lut_macs": macs_fwd},
+        "roofline": {
+            "kernel": "lut_gemm_kernel (+ split-K reduce)",
+            "bound": "lds",
+            "achieved": round(2 * achieved_glut, 1),
+            "peak": LDS_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(2 * achieved_glut / LDS_PEAK_GBS, 4),
+            "traffic": None,
+            "lut_mac_per_s_G": round(achieved_glut, 1),
+            "launches": launches,
+            "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
+            "share_of_step": round(gemm_ms / (dt * 1e3), 4),
+        },
+    }
+    if not args.no_microbench:
+        result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_sample_batch)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,271 @@
+/*
+ * atx.h — C ABI of the MI355X (gfx950) LUT approximate-multiplier library.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t,
+ * launches HIP kernels on that stream, never allocates device memory itself
+ * (workspaces are passed in by the caller) and never throws.  Return value:
+ * ATX_OK (0) or a negative ATX_E* code; atx_last_error() returns a message for
+ * the last failure on the calling thread.  Reference citations below are
+ * relative to the ApproxTorch tree (approxtorch/backend/csrc = csrc/).
+ *
+ * Index conventions (shared with the reference, csrc/naive_cuda/README.md:17-35):
+ *   LUT is a flat fp32 [65536] table, entry [xi * 256 + wi]; the activation
+ *   operand selects the row.  int8 operands index as v + 128, uint8 as v.
+ */
+#ifndef ATX_H
+#define ATX_H
+
+#include <stdint.h>
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ATX_OK = 0,
+  ATX_EINVAL = -1,   /* bad argument (shape, size, null pointer) */
+  ATX_ELAUNCH = -2,  /* a kernel launch or HIP runtime call failed */
+  ATX_ERANGE = -3,   /* problem larger than the kernel's documented limits */
+};
+
+/* LUT image classes returned by atx_lut_prepare (flags on the device). */
+enum {
+  ATX_LUT_I16 = 0,   /* every entry is an integer in [-32767, 32767]   */
+  ATX_LUT_U16 = 1,   /* every entry is an integer in [0, 65535]        */
+  ATX_LUT_F32 = 2,   /* anything else: fp32 accumulation fallback      */
+};
+
+/* Convolution geometry (NCHW input, OIHW weight). */
+typedef struct atx_conv_geom {
+  int N, C, H, W;          /* input image                       */
+  int KH, KW;              /* kernel                            */
+  int SH, SW, PH, PW, DH, DW;
+  int OH, OW;              /* output spatial size               */
+} atx_conv_geom;
+
+const char* atx_last_error(void);
+int atx_version(void);
+
+/* ---------------------------------------------------------------- LUT image
+ * Re-encodes an fp32 LUT into the 16-bit transposed image used by the
+ * LUT GEMM: out16t[wi * 256 + xi] = low 16 bits of lut[xi * 256 + wi]; also
+ * writes the fp32 transposed copy outf32t (same layout) and flags[2]:
+ * flags[0] = 1 if some entry is not an exact int16, flags[1] = 1 if some entry
+ * is not an exact uint16.  flags must be zeroed by the caller beforehand.
+ * Replaces prepare_lut_kernel (csrc/claude/bgemm_lut_kernels.cuh:116-142),
+ * which the reference re-runs inside every forward call
+ * (csrc/claude/bgemm_float_claude.cu:161-192). */
+int atx_lut_prepare(const float* lut, uint16_t* out16t, float* outf32t,
+                    int* flags, hipStream_t stream);
+
+/* --------------------------------------------------------- operand packing
+ * The LUT GEMM reads its activation operand as "row offsets": a [K][Rpad]
+ * uint16 array (R = N*L rows, Rpad = R rounded up to ATX_ROW_TILE) whose
+ * entry for index value v is atx_row_offset(v).  Padding rows hold offset 0.
+ */
+#define ATX_ROW_TILE 1024
+#define ATX_COL_TILE 64
+
+/* x fp32 [N,K,L] holding quantized integer values -> xq uint8 [N,K,L]
+ * (LUT index clamp(rint(v) + offset, 0, 255), nullable) and the row-offset
+ * operand xt [K][Rpad].  Replaces quantize_to_u8_kernel
+ * (csrc/claude/bgemm_lut_kernels.cuh:62-97) for the x operand. */
+int atx_pack_x_f32(const float* x, int N, int K, int L, int offset,
+                   uint8_t* xq, uint16_t* xt, int Rpad, hipStream_t stream);
+
+/* x uint8 [N,K,L] (already LUT indices) -> row-offset operand xt. */
+int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L,
+                  uint16_t* xt, int Rpad, hipStream_t stream);
+
+/* w fp32 [O,K] quantized values -> wq uint8 [O,K] (LUT index, nullable) and
+ * the transposed, column-padded operand wt uint8 [K][Opad] (Opad = O rounded
+ * up to ATX_COL_TILE; padding columns hold index 0).  Replaces the weight
+ * prepass of csrc/claude/bgemm_float_claude.cu:108-130. */
+int atx_pack_w_f32(const float* w, int O, int K, int offset,
+                   uint8_t* wq, uint8_t* wt, int Opad, hipStream_t stream);
+
+/* w uint8 [O,K] LUT indices -> wt uint8 [K][Opad]. */
+int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
+                  hipStream_t stream);
+
+/* Quantized image -> row-offset operand xt [K = C*KH*KW][Rpad] of the
+ * implicit im2col, k order (c, kh, kw), r = n*OH*OW + oh*OW + ow.  dtype:
+ * 0 = int8 values (index v+128), 1 = uint8 (index v), 2 = fp32 signed
+ * quantized values (index clamp(rint(v),-128,127)+128), 3 = fp32 unsigned
+ * quantized values (index clamp(rint(v),0,255)).  Out-of-image taps take LUT
+ * index pad_index (128 = quantized zero for int8), or rint(pad_dev[0]) when
+ * pad_dev is non-null (the device-resident uint8 zero point).
+ * Replaces im2col_u8_kernel (csrc/claude/bgemm_lre_backward_claude.cu:215-269)
+ * feeding the forward (nn/bgemm_int8.py:152-153). */
+int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g,
+                    int pad_index, const float* pad_dev, uint16_t* xt, int Rpad,
+                    hipStream_t stream);
+
+/* The reference op im2col_u8 itself: image (int8 values, uint8 indices or
+ * fp32 values; dtype 0 = int8, 1 = uint8, 2 = fp32) -> uint8 LUT indices
+ * [N, C*KH*KW, OH*OW], padding -> index 128.
+ * csrc/claude/bgemm_lre_backward_claude.cu:215-269 (kernel), 737-791 (host). */
+int atx_im2col_u8(const void* img, int dtype, atx_conv_geom g, uint8_t* out,
+                  hipStream_t stream);
+
+/* ------------------------------------------------------------- LUT GEMM
+ * y[n, o, l] = sum_k LUT[xi(n,k,l)][wi(o,k)], exact int32 accumulation,
+ * for the operands produced by the pack / im2col entry points above.
+ * lut16t / lutf32t come from atx_lut_prepare; lut_class selects the path
+ * (ATX_LUT_I16 / ATX_LUT_U16: LDS-resident 16-bit tables, int32 sums;
+ * ATX_LUT_F32: fp32 sums in ascending k, the reference's own order).
+ * Epilogue (out_kind):
+ *   ATX_OUT_F32     y fp32 [N,O,L] = (float) sum
+ *   ATX_OUT_I32     y int32 [N,O,L] = sum  (integer classes only)
+ *   ATX_OUT_DEQUANT y fp32 [N,O,L] = bias[o] + (float) sum * (sx[0]*sw[o])
+ *                   (bias nullable)  — nn/Conv2d_int8.py:213-218 fused.
+ * workspace: int32 scratch of atx_lut_gemm_workspace_bytes() bytes (split-K
+ * partial sums); may be null when that function returns 0.
+ * Replaces bgemm_lut_u8_kernel + reduce_splits_kernel + launch/dispatch
+ * (csrc/claude/bgemm_lut_kernels.cuh:148-163,183-506). */
+enum { ATX_OUT_F32 = 0, ATX_OUT_I32 = 1, ATX_OUT_DEQUANT = 2 };
+
+typedef struct atx_gemm_epilogue {
+  int out_kind;
+  const float* scale_x;   /* [1]  (DEQUANT) */
+  const float* scale_w;   /* [O]  (DEQUANT) */
+  const float* bias;      /* [O] or null    */
+} atx_gemm_epilogue;
+
+long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O);
+
+int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                 int N, int K, int L, int O,
+                 const uint16_t* lut16t, const float* lutf32t, int lut_class,
+                 atx_gemm_epilogue ep, void* y, void* workspace,
+                 hipStream_t stream);
+
+/* ------------------------------------------------------------ fake-quant
+ * Per-tensor fake-quant, fused: q = clamp(rint(x / max(s,1e-12) [+ z]),
+ * qmin, qmax) (NaN passes through), mask = qmin <= v <= qmax on the
+ * pre-round v.  zero may be null (symmetric).  q and mask may each be null.
+ * q8 (nullable): the same value as a signed/unsigned byte image.
+ * csrc/claude/quantization.cu:54-75,77-110,148-183 (kernels), 187-311 (host). */
+int atx_fakequant_fwd(const float* x, long long n, const float* scale,
+                      const float* zero, int qmin, int qmax, float* q,
+                      uint8_t* mask, void* q8, hipStream_t stream);
+
+/* gx = (mask ? go : 0) / max(scale, 1e-12); scale has 1 (per-tensor) or
+ * C (per-channel, channel = (i / inner) % C) elements.
+ * csrc/claude/quantization.cu:112-143; nn/quantization.py:110-113. */
+int atx_fakequant_bwd(const float* go, const uint8_t* mask, long long n,
+                      const float* scale, int C, long long inner, float* gx,
+                      hipStream_t stream);
+
+/* Per-channel fake-quant of a weight [O, inner]: q, mask, and the LUT index
+ * image wq = q + offset (nullable), the transposed operand wt [inner][Opad]
+ * (nullable).  nn/quantization.py:98-133. */
+int atx_fakequant_channel_fwd(const float* w, int O, long long inner,
+                              const float* scale, const float* zero,
+                              int qmin, int qmax, int offset, float* q,
+                              uint8_t* mask, uint8_t* wq, uint8_t* wt,
+                              int Opad, hipStream_t stream);
+
+/* col2im (F.fold): img[n,c,h,w] = sum of col[n,(c,kh,kw),(oh,ow)] over the
+ * taps that read (h,w).  If mask is non-null the per-tensor fake-quant
+ * backward is fused: img = mask ? img / max(scale[0],1e-12) : 0.
+ * nn/bgemm_int8.py:116-118 (F.fold) + csrc/claude/quantization.cu:112-143. */
+int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask,
+               const float* scale, float* img, hipStream_t stream);
+
+/* Column sums of the unfolded fp32 image, out[n,l] = sum over the K taps
+ * (out-of-image taps count as pad_dev[0], 0 if null), and its backward
+ * img[n,c,h,w] = sum of go[n,l] over the taps reading (h,w).  The uint8
+ * zero-point correction term sum_k q_x of nn/Conv2d_uint8.py:308-315. */
+int atx_tap_sum(const float* img, atx_conv_geom g, const float* pad_dev,
+                float* out, hipStream_t stream);
+int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img,
+                    hipStream_t stream);
+
+/* --------------------------------------------------------------- EMA stats
+ * absmax EMA (nn/Conv2d_int8.py:137-146):
+ *   stat = max|x|; scale <- m*(stat/denom) + (1-m)*scale, in fp32 with
+ *   torch's operation order.  ws: 2 uint32 of scratch.  If stat_out is
+ *   non-null the raw statistic is also written there (for an all-reduce by
+ *   the caller between atx_absmax and atx_ema_apply). */
+long long atx_reduce_workspace_bytes(void);
+int atx_absmax(const float* x, long long n, unsigned int* ws, float* stat_out,
+               hipStream_t stream);
+int atx_minmax(const float* x, long long n, unsigned int* ws, float* mn_out,
+               float* mx_out, hipStream_t stream);
+/* scale[0] <- m32 * (stat[0] / denom) + om32 * scale[0] */
+int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32,
+                         float* scale, hipStream_t stream);
+/* uint8 activation qparams (nn/Conv2d_uint8.py:11-23,225-240): EMA of
+ * min/max then scale = max((mx'-mn')/qmax, 1e-12), zero = clamp(rint(-mn'/scale)). */
+int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32,
+                         int qmax, float* x_min, float* x_max, float* scale,
+                         float* zero, hipStream_t stream);
+/* Per-channel weight absmax EMA (nn/Conv2d_int8.py:148-158); a zero channel
+ * keeps its old scale.  mode 1 = reset (nn/Conv2d_int8.py:160-167). */
+int atx_weight_scale_ema(const float* w, int O, long long inner, float qmax_w,
+                         float m32, float om32, int reset, float* scale_w,
+                         hipStream_t stream);
+/* Per-channel weight min/max EMA + uint8 qparams (nn/Conv2d_uint8.py:242-255). */
+int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32,
+                          float om32, int qmax, float* w_min, float* w_max,
+                          float* scale_w, float* zero_w, hipStream_t stream);
+
+/* ------------------------------------------------------------ LUT maps
+ * out[i] = lut256[idx(in[i])], in dtype 0 int8 (v+128), 1 uint8 (v), 2 fp32
+ * (clamp(rint(v),-128,127)+128).  csrc/claude/bgemm_lre_backward_claude.cu:95-127. */
+int atx_lut_map(const void* in, int dtype, long long n, const float* lut256,
+                float* out, hipStream_t stream);
+/* image [N,C,H,W] -> [N,C,H+2PH,W+2PW], border = lut256[128].
+ * csrc/claude/bgemm_lre_backward_claude.cu:276-307. */
+int atx_lut_map_pad(const void* in, int dtype, int N, int C, int H, int W,
+                    int PH, int PW, const float* lut256, float* out,
+                    hipStream_t stream);
+
+/* ------------------------------------------- STE / LRE backward (fp32 MFMA)
+ * Backward of the LUT GEMM under an estimator that treats each product as
+ * Tx[wi] * (something in go) and Tw[xi] * (...):
+ *   col[n,k,l] = sum_o go[n,o,l] * tx[wq[o,k]]       (then atx_col2im)
+ *   gw[o,k]    = sum_{n,l} go[n,o,l] * tw[xi(n,k,l)]
+ * STE: tx/tw decode indices to quantized values; LRE: the dx / dw slope
+ * tables.  xi is read from the saved image (dtype as atx_im2col_rows,
+ * out-of-image taps -> tw[pad_index]).  mask_w/scale_w (nullable) fuse the
+ * per-channel weight fake-quant backward.  Replace the cuBLAS / cuDNN calls
+ * of csrc/claude/bgemm_lre_backward_claude.cu:443-524 and
+ * nn/bgemm_int8.py:184-207,277-290. */
+int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx,
+                          int N, int O, int K, int L, float* col,
+                          hipStream_t stream);
+long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P);
+int atx_conv_bwd_weight(const float* go, const void* img, int dtype,
+                        atx_conv_geom g, int O, int pad_index,
+                        const float* pad_dev, const float* tw,
+                        const uint8_t* mask_w, const float* scale_w, float* gw,
+                        float* workspace, hipStream_t stream);
+
+/* ------------------------------------------------------- custom gradients
+ * grad_x[n,k,l] = sum_o dy[n,o,l] * dx_lut[xi(n,k,l)*256 + wi(o,k)] (ascending o)
+ * grad_w[o,k]   = sum_{n,l} dy[n,o,l] * dw_lut[xi(n,k,l)*256 + wi(o,k)]
+ * x, w: LUT indices (is_signed = 0) or int8 values (is_signed = 1, idx = v+128).
+ * csrc/cuda/bgemm_custom_grad_optimize.cu:30-116,136-205 (uint8),
+ * 315-404,419-490 (int8), hosts 212-301,497-585. */
+int atx_custom_grad_dx(const void* x, const void* w, int is_signed,
+                       const float* dy, const float* dx_lut, int N, int K,
+                       int L, int O, float* grad_x, hipStream_t stream);
+long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O);
+int atx_custom_grad_dw(const void* x, const void* w, int is_signed,
+                       const float* dy, const float* dw_lut, int N, int K,
+                       int L, int O, float* grad_w, float* workspace,
+                       hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+/* Row-offset encoding of LUT index v used by the LUT GEMM's LDS tables. */
+static inline unsigned atx_row_offset(unsigned v) {
+  return v * 128u + (((v >> 3) & 7u) << 4);
+}
+
+#endif /* ATX_H */

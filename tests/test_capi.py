@@ -1,0 +1,57 @@
+"""libatx.so loads on the CPU, exports every symbol include/atx.h declares, and
+its host-side argument validation returns error codes without touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from approxtorch_amd.backend import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "atx.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^(?:int|long long|const char\*)\s+(atx_\w+)\(", text, flags=re.M)
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = L.load()
+    names = header_functions()
+    assert len(names) >= 30
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(names) == L.exported_symbols()
+    assert lib.atx_version() == 1
+
+
+def test_invalid_arguments_return_einval_without_gpu():
+    lib = L.load()
+    ep = L.GemmEpilogue(0, None, None, None)
+    rc = lib.atx_lut_gemm(None, 1024, None, 64, -1, 4, 4, 4, None, None, 0, ep, None, None, None)
+    assert rc == -1
+    assert b"negative size" in lib.atx_last_error()
+    rc = lib.atx_lut_gemm(None, 100, None, 64, 1, 4, 4, 4, None, None, 0, ep, None, None, None)
+    assert rc == -1 and b"Rpad" in lib.atx_last_error()
+    rc = lib.atx_fakequant_fwd(None, 10, None, None, 5, 5, None, None, None, None)
+    assert rc == -1 and b"qmin" in lib.atx_last_error()
+    g = L.geom(1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1)
+    g.OH = 7
+    rc = lib.atx_im2col_u8(None, 0, g, None, None)
+    assert rc == -1 and b"OH/OW" in lib.atx_last_error()
+
+
+def test_workspace_queries_are_host_only():
+    assert L.query("atx_lut_gemm_workspace_bytes", 32, 2304, 4096, 256) == 0      # 512 tiles
+    assert L.query("atx_lut_gemm_workspace_bytes", 8, 576, 1024, 64) > 0          # split-K
+    assert L.query("atx_lut_gemm_workspace_bytes", 1, 40000, 49, 64) > 0          # K > int32 bound
+    assert L.query("atx_reduce_workspace_bytes") == 1024 * 8
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        L.load()

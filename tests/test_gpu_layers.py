@@ -1,0 +1,164 @@
+"""Layer-level GPU parity: Conv2d_int8 / Conv2d_uint8 forward and backward
+(STE, LRE, custom) against the CPU oracle's restatement of the reference
+layers; outputs and gradients within rel 1e-5 / abs 1e-4 (relative to the
+largest magnitude where values cancel)."""
+import numpy as np
+import pytest
+import torch
+
+import approxtorch_amd as at
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-5, 1e-4
+
+
+def close(got, want):
+    got = got.detach().double().cpu().numpy()
+    want = np.asarray(want, dtype=np.float64)
+    scale = max(1.0, float(np.abs(want).max()))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL * scale)
+
+
+def perturbed_lut(seed=0):
+    r = np.random.default_rng(seed)
+    a = np.arange(256) - 128
+    p = a[:, None] * a[None, :]
+    e = np.rint(r.normal(0, 1, p.shape) * (0.02 * np.abs(p) + 1))
+    return np.clip(p + e, -32768, 32767).astype(np.float32).reshape(-1)
+
+
+def tables(kind, lut, qtype="int8"):
+    if kind == "ste":
+        return None, None
+    if kind == "lre":
+        ga, gb = O.lre_tables(lut, qtype)
+        return ga, gb
+    ga, gb = O.date_tables(lut.reshape(256, 256), 2)
+    return ga.reshape(-1), gb.reshape(-1)
+
+
+GEOMS = [dict(k=3, s=1, p=1, d=1), dict(k=3, s=2, p=1, d=1), dict(k=1, s=1, p=0, d=1),
+         dict(k=1, s=2, p=0, d=1), dict(k=7, s=2, p=3, d=1), dict(k=3, s=1, p=2, d=2)]
+
+
+@pytest.mark.parametrize("kind", ["ste", "lre", "custom"])
+@pytest.mark.parametrize("gi", range(len(GEOMS)))
+def test_conv2d_int8_forward_backward(kind, gi):
+    gm = GEOMS[gi]
+    torch.manual_seed(gi)
+    lut = perturbed_lut(gi)
+    dx, dw = tables(kind, lut)
+    layer = at.nn.Conv2d_int8(6, 70, gm["k"], torch.from_numpy(lut).to(DEV), grad=kind,
+                              dx=None if dx is None else torch.from_numpy(dx).to(DEV),
+                              dw=None if dw is None else torch.from_numpy(dw).to(DEV),
+                              bias=True, stride=gm["s"], padding=gm["p"], dilation=gm["d"],
+                              weight_bits=6).to(DEV)
+    layer.eval()
+    x = torch.randn(3, 6, 13, 12, device=DEV)
+    with torch.no_grad():
+        layer.scale_x.fill_(float(x.abs().max()) / 110.0)     # some activations clip
+    xr = x.clone().requires_grad_()
+    y = layer(xr)
+    k2, s2, p2, d2 = (gm["k"],) * 2, (gm["s"],) * 2, (gm["p"],) * 2, (gm["d"],) * 2
+    sx = np.float32(layer.scale_x.item())
+    sw = layer.scale_w.cpu().numpy()
+    want, ctx = O.conv_int8_forward(x.cpu().numpy(), layer.weight.detach().cpu().numpy(),
+                                    layer.bias.detach().cpu().numpy(), lut, sx, sw,
+                                    k2, s2, p2, d2, weight_bits=6)
+    close(y, want)
+    go = torch.randn_like(y)
+    y.backward(go)
+    tb = None if kind == "ste" else (dx, dw)
+    gx, gw, gb = O.conv_int8_backward(go.cpu().numpy(), ctx, sx, sw, kind, tb, k2, s2, p2, d2)
+    close(xr.grad, gx)
+    close(layer.weight.grad, gw)
+    close(layer.bias.grad, gb)
+
+
+@pytest.mark.parametrize("kind", ["ste", "lre", "custom"])
+@pytest.mark.parametrize("gi", [0, 1, 2, 5])
+def test_conv2d_uint8_forward_backward(kind, gi):
+    gm = GEOMS[gi]
+    torch.manual_seed(10 + gi)
+    v = np.arange(256)
+    lut = ((v[:, None] * v[None, :]) & ~63).astype(np.float32).reshape(-1)   # config 5 table
+    dx, dw = tables(kind, lut, "uint8")
+    wb = 4 if kind == "custom" else 8
+    layer = at.nn.Conv2d_uint8(5, 66, gm["k"], torch.from_numpy(lut).to(DEV), grad=kind,
+                               dx=None if dx is None else torch.from_numpy(dx).to(DEV),
+                               dw=None if dw is None else torch.from_numpy(dw).to(DEV),
+                               bias=True, stride=gm["s"], padding=gm["p"], dilation=gm["d"],
+                               weight_bits=wb).to(DEV)
+    x = torch.randn(2, 5, 11, 13, device=DEV) + 0.4
+    layer.train()
+    with torch.no_grad():
+        layer(x)                                      # one EMA step sets non-trivial qparams
+    layer.eval()
+    xr = x.clone().requires_grad_()
+    y = layer(xr)
+    k2, s2, p2, d2 = (gm["k"],) * 2, (gm["s"],) * 2, (gm["p"],) * 2, (gm["d"],) * 2
+    want, ctx = O.conv_uint8_forward(
+        x.cpu().numpy(), layer.weight.detach().cpu().numpy(), layer.bias.detach().cpu().numpy(),
+        lut, np.float32(layer.scale_x.item()), np.float32(layer.zero_x.item()),
+        layer.scale_w.cpu().numpy(), layer.zero_w.cpu().numpy(), k2, s2, p2, d2,
+        qmax_w=2 ** wb - 1)
+    close(y, want)
+    go = torch.randn_like(y)
+    y.backward(go)
+    tb = None if kind == "ste" else (dx, dw)
+    gx, gw, gb = O.conv_uint8_backward(go.cpu().numpy(), ctx, np.float32(layer.scale_x.item()),
+                                       layer.scale_w.cpu().numpy(), kind, tb, k2, s2, p2, d2)
+    close(xr.grad, gx)
+    close(layer.weight.grad, gw)
+    close(layer.bias.grad, gb)
+
+
+def test_train_mode_ema_matches_reference_rules():
+    torch.manual_seed(3)
+    lut = torch.from_numpy(perturbed_lut(3)).to(DEV)
+    layer = at.nn.Conv2d_int8(4, 8, 3, lut, padding=1, scale_momentum=0.1, weight_bits=5).to(DEV)
+    layer.train()
+    sx = np.float32(layer.scale_x.item())
+    sw = layer.scale_w.cpu().numpy()
+    with torch.no_grad():
+        layer.weight[2].zero_()
+    for step in range(3):
+        x = torch.randn(2, 4, 9, 9, device=DEV) * (step + 1)
+        w = layer.weight.detach().cpu().numpy()
+        layer(x)
+        sx = O.ema_absmax(x.cpu().numpy(), sx, 0.1)
+        sw = O.weight_scale_ema(w, sw, 0.1, 15)
+        assert layer.scale_x.item() == sx
+        assert np.array_equal(layer.scale_w.cpu().numpy(), sw)
+    layer.freeze_scale()
+    before = layer.scale_x.item()
+    layer(torch.randn(2, 4, 9, 9, device=DEV) * 50)
+    assert layer.scale_x.item() == before
+
+
+def test_convert_model_training_step_runs_and_learns():
+    torch.manual_seed(0)
+    net = torch.nn.Sequential(
+        torch.nn.Conv2d(3, 16, 3, padding=1), torch.nn.ReLU(),
+        torch.nn.Conv2d(16, 32, 3, padding=1, stride=2), torch.nn.ReLU(),
+        torch.nn.Conv2d(32, 32, 3, padding=1), torch.nn.ReLU(),
+        torch.nn.AdaptiveAvgPool2d(1), torch.nn.Flatten(), torch.nn.Linear(32, 10)).to(DEV)
+    a = np.arange(256) - 128
+    lut = torch.tensor(((a[:, None] * a[None, :]) >> 4 << 4).reshape(-1),
+                       dtype=torch.float32, device=DEV)
+    net = at.convert_model(net, lut, qtype="int8", grad="ste", scale_momentum=0.1)
+    assert isinstance(net[0], torch.nn.Conv2d) and isinstance(net[2], at.nn.Conv2d_int8)
+    opt = torch.optim.SGD(net.parameters(), lr=0.05, momentum=0.9)
+    x = torch.randn(16, 3, 16, 16, device=DEV)
+    y = torch.randint(0, 10, (16,), device=DEV)
+    losses = []
+    for _ in range(15):
+        opt.zero_grad()
+        loss = torch.nn.functional.cross_entropy(net(x), y)
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    assert np.isfinite(losses).all()
+    assert losses[-1] < losses[0]

@@ -1,0 +1,334 @@
+"""GPU parity of every HIP entry point against the CPU oracle (seeded inputs).
+
+Bar: integer / index results bit-exact (int64 oracle); fp32 results of the
+fake-quant, EMA and qparam kernels bit-exact (they restate torch's op
+sequence); gradients within rel 1e-5 / abs 1e-4 (fp32 accumulation order).
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from approxtorch_amd.backend import ops
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-5, 1e-4
+
+
+def gen(seed):
+    return np.random.default_rng(seed)
+
+
+def t(a, dtype=None):
+    return torch.as_tensor(np.ascontiguousarray(a), device=DEV, dtype=dtype)
+
+
+def luts(seed):
+    r = gen(seed)
+    v = np.arange(256)
+    a = v - 128
+    return {
+        "asym": (37 * v[:, None] - 19 * v[None, :] + 11).reshape(-1),       # int16
+        "exact_int8": (a[:, None] * a[None, :]).reshape(-1),                 # int16
+        "trunc4": (((a[:, None] * a[None, :]) >> 4) << 4).reshape(-1),       # config 2
+        "u16_c5": ((v[:, None] * v[None, :]) & ~63).reshape(-1),            # config 5 (uint16)
+        "i16_edge": np.clip(r.integers(-40000, 40000, 65536), -32767, 32767),
+        "perturbed": np.clip((a[:, None] * a[None, :]) +
+                             np.rint(r.normal(0, 1, (256, 256)) *
+                                     (0.02 * np.abs(a[:, None] * a[None, :]) + 1)),
+                             -32768, 32767).reshape(-1),
+    }
+
+
+SHAPES = [(1, 1, 1, 1), (2, 5, 7, 3), (3, 33, 9, 17), (2, 576, 64, 64), (1, 300, 1100, 65),
+          (4, 64, 49, 130), (1, 4608, 49, 64), (2, 3, 1024, 64), (8, 576, 1024, 64)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("lut_name", ["asym", "perturbed"])
+def test_bgemm_int8_u8_input_bit_exact(shape, lut_name):
+    N, K, L, Oc = shape
+    r = gen(zlib.crc32(repr((shape, lut_name)).encode()))
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wv = r.integers(-128, 128, (Oc, K)).astype(np.float32)
+    lut = luts(7)[lut_name]
+    xg = t(xi)
+    y, xq, wq = ops.bgemm_fake_int8_claude_save(xg, t(wv), t(lut, torch.float32))
+    assert xq.data_ptr() == xg.data_ptr()          # _save aliases a uint8 x
+    want = O.lut_gemm_i64(xi, (wv + 128).astype(np.uint8), lut)
+    assert np.array_equal(wq.cpu().numpy(), (wv + 128).astype(np.uint8))
+    assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("lut_name", ["asym", "exact_int8", "trunc4", "u16_c5", "i16_edge"])
+def test_lut_gemm_int32_exact_all_integer_classes(lut_name):
+    r = gen(11)
+    N, K, L, Oc = 3, 700, 333, 70
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(3)[lut_name]
+    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32))
+    assert np.array_equal(y.cpu().numpy().astype(np.int64), O.lut_gemm_i64(xi, wi, lut))
+
+
+def test_bgemm_float_inputs_quantize_like_reference():
+    # fp32 x, w holding quantized values (plus half-integers and out-of-range
+    # values: index = clamp(rint(v) + 128, 0, 255))
+    r = gen(5)
+    x = r.integers(-140, 140, (2, 50, 40)).astype(np.float32)
+    x[0, 0, :6] = [0.5, 1.5, -0.5, -2.5, 127.5, np.nan]
+    w = r.integers(-128, 128, (9, 50)).astype(np.float32)
+    lut = luts(1)["asym"]
+    y, xq, wq = ops.bgemm_fake_int8_claude_save(t(x), t(w), t(lut, torch.float32))
+    xi = O.quant_index(x, 128)
+    assert np.array_equal(xq.cpu().numpy(), xi)
+    assert np.array_equal(y.cpu().numpy(),
+                          O.lut_gemm_i64(xi, O.quant_index(w, 128), lut).astype(np.float32))
+
+
+def test_int8_equals_uint8_shifted():
+    r = gen(9)
+    x = r.integers(-128, 128, (3, 64, 50)).astype(np.float32)
+    w = r.integers(-128, 128, (20, 64)).astype(np.float32)
+    lut = t(luts(2)["perturbed"], torch.float32)
+    a = ops.bgemm_fake_int8_claude(t(x), t(w), lut)
+    b = ops.bgemm_fake_uint8_claude(t(x + 128), t(w + 128), lut)
+    assert torch.equal(a, b)
+
+
+def test_fp32_lut_fallback_matches_sequential_fp32():
+    r = gen(4)
+    xi = r.integers(0, 256, (2, 100, 37), dtype=np.uint8)
+    w = r.integers(-128, 128, (11, 100)).astype(np.float32)
+    lut = (r.integers(-4000, 4000, 65536) / 2 + 0.25).astype(np.float32)   # non-integer
+    y = ops.bgemm_fake_int8_claude(t(xi), t(w), t(lut))
+    want = O.lut_gemm_f32(xi, (w + 128).astype(np.uint8), lut)
+    assert np.array_equal(y.cpu().numpy(), want)          # same ascending-k fp32 order
+
+
+def test_lut_cache_tracks_in_place_updates():
+    r = gen(6)
+    xi = t(r.integers(0, 256, (1, 8, 8), dtype=np.uint8))
+    w = t(r.integers(-128, 128, (4, 8)).astype(np.float32))
+    lut = t(luts(0)["asym"], torch.float32)
+    y0 = ops.bgemm_fake_int8_claude(xi, w, lut)
+    lut.mul_(2)                                            # bumps the version counter
+    y1 = ops.bgemm_fake_int8_claude(xi, w, lut)
+    assert torch.equal(y1, 2 * y0)
+
+
+def test_empty_and_degenerate_shapes():
+    lut = t(luts(0)["asym"], torch.float32)
+    y = ops.bgemm_fake_int8_claude(torch.zeros(2, 0, 5, device=DEV),
+                                   torch.zeros(3, 0, device=DEV), lut)
+    assert y.shape == (2, 3, 5) and torch.count_nonzero(y) == 0
+    y = ops.bgemm_fake_int8_claude(torch.zeros(0, 4, 5, device=DEV),
+                                   torch.zeros(3, 4, device=DEV), lut)
+    assert y.shape == (0, 3, 5)
+    with pytest.raises(RuntimeError, match="x.size"):
+        ops.bgemm_fake_int8_claude(torch.zeros(1, 4, 5, device=DEV),
+                                   torch.zeros(3, 5, device=DEV), lut)
+    with pytest.raises(RuntimeError, match="float32"):
+        ops.bgemm_fake_int8_claude(torch.zeros(1, 4, 5, device=DEV),
+                                   torch.zeros(3, 4, device=DEV), lut.int())
+
+
+GEOMS = [((3, 3), (1, 1), (1, 1), (1, 1)), ((7, 7), (2, 2), (3, 3), (1, 1)),
+         ((1, 1), (2, 2), (0, 0), (1, 1)), ((3, 3), (1, 2), (2, 0), (2, 1)),
+         ((3, 3), (2, 2), (1, 1), (1, 1))]
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+@pytest.mark.parametrize("dtype", ["int8", "uint8", "float32"])
+def test_im2col_u8(geom, dtype):
+    k, s, p, d = geom
+    r = gen(8)
+    if dtype == "int8":
+        img = r.integers(-128, 128, (2, 3, 13, 11)).astype(np.int8)
+    elif dtype == "uint8":
+        img = r.integers(0, 256, (2, 3, 13, 11)).astype(np.uint8)
+    else:
+        img = r.integers(-130, 130, (2, 3, 13, 11)).astype(np.float32)
+    got = ops.im2col_u8(t(img), k, s, p, d).cpu().numpy()
+    assert np.array_equal(got, O.im2col_index(O.image_index(img, 128), k, s, p, d, 128))
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_lut_conv_forward_matches_oracle(geom):
+    k, s, p, d = geom
+    r = gen(12)
+    img = r.integers(-127, 128, (3, 8, 15, 14)).astype(np.float32)
+    w = r.integers(-127, 128, (70, 8 * k[0] * k[1])).astype(np.float32)
+    lut = luts(4)["perturbed"]
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    y, wq = ops.conv_forward(t(img), t(w), t(lut, torch.float32), g, 128, 128)
+    xi = O.im2col_index(O.image_index(img, 128), k, s, p, d, 128)
+    want = O.lut_gemm_i64(xi, (w + 128).astype(np.uint8), lut)
+    assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
+
+
+def test_lut_map_and_pad():
+    r = gen(13)
+    table = r.standard_normal(256).astype(np.float32)
+    for arr in (r.integers(-128, 128, (2, 3, 5, 4)).astype(np.int8),
+                r.integers(0, 256, (2, 3, 5, 4)).astype(np.uint8),
+                r.integers(-130, 130, (2, 3, 5, 4)).astype(np.float32)):
+        idx = O.image_index(arr, 128)
+        assert np.array_equal(ops.lut_map(t(arr), t(table)).cpu().numpy(), O.lut_map(idx, table))
+        assert np.array_equal(ops.lut_map_pad(t(arr), t(table), (2, 1)).cpu().numpy(),
+                              O.lut_map_pad(idx, table, (2, 1)))
+
+
+# ---------------------------------------------------------------- fake-quant
+def special_x(seed, n=20000):
+    r = gen(seed)
+    x = (r.standard_normal(n) * 3).astype(np.float32)
+    x[:12] = [0.5, 1.5, 2.5, -0.5, -1.5, 126.5, 127.5, -127.5, 300, -300, np.nan, -0.0]
+    return x
+
+
+@pytest.mark.parametrize("scale", [0.023, 1.0, 0.0, 1e-30])
+def test_fakequant_symmetric_bitwise(scale):
+    x = special_x(1)
+    s = np.float32(scale)
+    q, m, _ = ops.fakequant_per_tensor(t(x), t(np.array([s])), -127, 127)
+    qo, mo = O.fakequant(x, s, -127, 127)
+    assert np.array_equal(q.cpu().numpy(), qo, equal_nan=True)
+    assert np.array_equal(m.cpu().numpy(), mo)
+    go = gen(2).standard_normal(x.size).astype(np.float32)
+    gx = ops.fakequant_per_tensor_backward(t(go), m, t(np.array([s])))
+    assert np.array_equal(gx.cpu().numpy(), O.fakequant_backward(go, mo, s))
+
+
+def test_fakequant_asymmetric_and_per_channel_bitwise():
+    x = special_x(3).reshape(20, 1000)
+    s, z = np.float32(0.031), np.float32(113)
+    q, m, _ = ops.fakequant_per_tensor(t(x), t(np.array([s])), 0, 255, zero_point=t(np.array([z])))
+    qo, mo = O.fakequant(x, s, 0, 255, zero=z)
+    assert np.array_equal(q.cpu().numpy(), qo, equal_nan=True)
+    assert np.array_equal(m.cpu().numpy(), mo)
+    sc = gen(4).random(20).astype(np.float32) * 0.05
+    sc[3] = 0
+    q, m, wq, wt, Opad = ops.fakequant_per_channel(t(x), t(sc), -15, 15, offset=128, want_wt=True)
+    qo, mo = O.fakequant(x, sc.reshape(20, 1), -15, 15)
+    assert np.array_equal(q.cpu().numpy(), qo, equal_nan=True)
+    assert np.array_equal(m.cpu().numpy(), mo)
+    idx = O.quant_index(qo, 128)
+    assert np.array_equal(wq.cpu().numpy(), idx)
+    assert np.array_equal(wt.cpu().numpy()[:, :20], idx.T)
+
+
+@pytest.mark.parametrize("m", [0.05, 0.1])
+def test_ema_kernels_bitwise(m):
+    from approxtorch_amd.backend import _lib as L
+    from approxtorch_amd.nn.Conv2d_int8 import _ema_coeffs
+    r = gen(21)
+    x = (r.standard_normal(300001) * 2.5).astype(np.float32)
+    xg = t(x)
+    scale = t(np.array([0.0371], dtype=np.float32))
+    stat = torch.empty((), device=DEV)
+    ws = ops._reduce_ws(xg.device)
+    st = L.stream_of(xg)
+    m32, om32 = _ema_coeffs(m)
+    L.call("atx_absmax", xg.data_ptr(), x.size, ws.data_ptr(), stat.data_ptr(), st)
+    L.call("atx_ema_absmax_apply", stat.data_ptr(), 127.0, m32, om32, scale.data_ptr(), st)
+    assert scale.item() == O.ema_absmax(x, np.float32(0.0371), m)
+    w = (r.standard_normal((33, 3, 3, 3)) * 0.1).astype(np.float32)
+    w[5] = 0
+    sw = (r.random(33) * 0.01).astype(np.float32)
+    swg = t(sw.copy())
+    wg = t(w)
+    L.call("atx_weight_scale_ema", wg.data_ptr(), 33, 27, 7.0, m32, om32, 0, swg.data_ptr(), st)
+    assert np.array_equal(swg.cpu().numpy(), O.weight_scale_ema(w, sw, m, 7))
+    L.call("atx_weight_scale_ema", wg.data_ptr(), 33, 27, 7.0, 1.0, 0.0, 1, swg.data_ptr(), st)
+    assert np.array_equal(swg.cpu().numpy(), O.weight_scale_reset(w, 7))
+    # uint8 activation min/max EMA + qparams
+    mn, mx = torch.empty((), device=DEV), torch.empty((), device=DEV)
+    bufs = [t(np.array([v], dtype=np.float32)) for v in (-0.2, 1.7, 0.0, 0.0)]
+    L.call("atx_minmax", xg.data_ptr(), x.size, ws.data_ptr(), mn.data_ptr(), mx.data_ptr(), st)
+    L.call("atx_ema_minmax_apply", mn.data_ptr(), mx.data_ptr(), m32, om32, 255,
+           *[b.data_ptr() for b in bufs], st)
+    want = O.ema_minmax(x, np.float32(-0.2), np.float32(1.7), m)
+    assert [b.item() for b in bufs] == [float(v) for v in want]
+    # uint8 weights
+    wmin, wmax = (r.standard_normal(33) * 0.1).astype(np.float32), \
+        (r.random(33) * 0.1).astype(np.float32)
+    g4 = [t(wmin.copy()), t(wmax.copy()), torch.empty(33, device=DEV), torch.empty(33, device=DEV)]
+    L.call("atx_weight_minmax_ema", wg.data_ptr(), 33, 27, m32, om32, 15,
+           *[b.data_ptr() for b in g4], st)
+    want = O.weight_minmax_ema(w, wmin, wmax, m, 15)
+    for got, exp in zip(g4, want):
+        assert np.array_equal(got.cpu().numpy(), exp)
+
+
+# ------------------------------------------------------------ backward ops
+def close(a, b):
+    np.testing.assert_allclose(np.asarray(a, dtype=np.float64), b, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("xdtype", ["uint8", "int8", "float32"])
+def test_bgemm_lre_backward(xdtype):
+    r = gen(31)
+    N, K, L, Oc = 3, 90, 77, 40
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    q = np.arange(256, dtype=np.float32) - 128
+    dx = (0.0003 * q * q - 0.07 * q + 1.25).astype(np.float32)      # test_bgemm_lre_naive.py:55-57
+    dw = (2.5 * np.sin(0.031 * q) + 0.004 * q).astype(np.float32)
+    go = r.standard_normal((N, Oc, L)).astype(np.float32)
+    if xdtype == "uint8":
+        xa, wa = xi, wi
+    elif xdtype == "int8":
+        xa, wa = (xi.astype(np.int16) - 128).astype(np.int8), (wi.astype(np.int16) - 128).astype(np.int8)
+    else:
+        xa, wa = xi.astype(np.float32) - 128, wi.astype(np.float32) - 128
+    gx, gw = ops.bgemm_lre_backward_claude(t(go), t(xa), t(np.ascontiguousarray(wa.T)), t(dx), t(dw))
+    ex, ew = O.gemm_grads(go, xi, wi, "lre", (dx, dw))
+    close(gx.cpu().numpy(), ex)
+    close(gw.cpu().numpy(), ew.T)
+
+
+@pytest.mark.parametrize("signed", [False, True])
+def test_custom_grad_kernels(signed):
+    r = gen(41)
+    N, K, L, Oc = 2, 45, 130, 70
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    rr, cc = np.meshgrid(np.arange(256), np.arange(256), indexing="ij")
+    dxl = (rr * 1009 + cc * 7 + (rr * cc) % 31).astype(np.float32) / 1000.0   # test_conv_custom_grad.py:41-44
+    dwl = dxl.T.copy()
+    go = r.standard_normal((N, Oc, L)).astype(np.float32)
+    if signed:
+        X, W = (xi.astype(np.int16) - 128).astype(np.int8), (wi.astype(np.int16) - 128).astype(np.int8)
+        fdx, fdw = ops.bgemm_custom_grad_int8_dx, ops.bgemm_custom_grad_int8_dw
+    else:
+        X, W = xi, wi
+        fdx, fdw = ops.bgemm_custom_grad_uint8_dx, ops.bgemm_custom_grad_uint8_dw
+    gx = fdx(t(X), t(W), t(go), t(dxl.reshape(-1)))
+    gw = fdw(t(X), t(W), t(go), t(dwl.reshape(-1)))
+    ex, ew = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl))
+    close(gx.cpu().numpy(), ex)
+    close(gw.cpu().numpy(), ew)
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_conv_backward_kernels(geom):
+    k, s, p, d = geom
+    r = gen(51)
+    img = r.integers(-127, 128, (2, 6, 12, 13)).astype(np.int8)
+    Oc = 20
+    K = 6 * k[0] * k[1]
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    go = r.standard_normal((2, Oc, g.OH * g.OW)).astype(np.float32)
+    tx = r.standard_normal(256).astype(np.float32)
+    tw = r.standard_normal(256).astype(np.float32)
+    gi = ops.conv_backward_data(t(go), t(wi), t(tx), g)
+    gwk = ops.conv_backward_weight(t(go), t(img), t(tw), g, Oc, 128)
+    xi = O.im2col_index(O.image_index(img), k, s, p, d, 128)
+    ex, ew = O.gemm_grads(go, xi, wi, "lre", (tx, tw))
+    close(gi.cpu().numpy(), O.fold(ex, img.shape, k, s, p, d))
+    close(gwk.cpu().numpy(), ew)

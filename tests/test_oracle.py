@@ -1,0 +1,293 @@
+"""Pins the CPU oracle (oracle/oracle.py, oracle/lut_oracle.c) with checks that
+do not restate its formulas: brute-force loops, closed forms, invariants and
+library routines (torch on the CPU, scipy.stats.linregress)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+
+rng = np.random.default_rng(1234)
+
+
+def asym_lut():
+    # test_naive_lut_ops.py:57-59 recipe: distinguishes lut[x][w] from lut[w][x]
+    r = np.arange(256)[:, None]
+    c = np.arange(256)[None, :]
+    return (37 * r - 19 * c + 11).reshape(-1)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (2, 5, 7, 3), (3, 33, 9, 17)])
+def test_lut_gemm_matches_bruteforce_asymmetric_lut(shape):
+    N, K, L, Oc = shape
+    xi = rng.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = rng.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = asym_lut()
+    y = O.lut_gemm_i64(xi, wi, lut)
+    assert np.array_equal(y, O.lut_gemm_bruteforce(xi, wi, lut).astype(np.int64))
+    # swapping the operand roles must change the result for this LUT
+    lut_t = lut.reshape(256, 256).T.reshape(-1)
+    if K > 1:
+        assert not np.array_equal(y, O.lut_gemm_i64(xi, wi, lut_t))
+
+
+def test_exact_product_lut_is_integer_gemm():
+    a = np.arange(256) - 128
+    lut = (a[:, None] * a[None, :]).reshape(-1)
+    xi = rng.integers(0, 256, (4, 37, 21), dtype=np.uint8)
+    wi = rng.integers(0, 256, (11, 37), dtype=np.uint8)
+    want = np.einsum("nkl,ok->nol", xi.astype(np.int64) - 128, wi.astype(np.int64) - 128)
+    assert np.array_equal(O.lut_gemm_i64(xi, wi, lut), want)
+
+
+def test_linearity_in_the_lut():
+    xi = rng.integers(0, 256, (2, 19, 13), dtype=np.uint8)
+    wi = rng.integers(0, 256, (5, 19), dtype=np.uint8)
+    p = rng.integers(-300, 300, 65536)
+    q = rng.integers(-300, 300, 65536)
+    lhs = O.lut_gemm_i64(xi, wi, 3 * p - 7 * q)
+    rhs = 3 * O.lut_gemm_i64(xi, wi, p) - 7 * O.lut_gemm_i64(xi, wi, q)
+    assert np.array_equal(lhs, rhs)
+
+
+def test_f32_sum_exact_for_small_integers_and_sequential_for_halves():
+    xi = rng.integers(0, 256, (2, 40, 9), dtype=np.uint8)
+    wi = rng.integers(0, 256, (3, 40), dtype=np.uint8)
+    lut = rng.integers(-1000, 1000, 65536)
+    assert np.array_equal(O.lut_gemm_f32(xi, wi, lut.astype(np.float32)),
+                          O.lut_gemm_i64(xi, wi, lut).astype(np.float32))
+    half = (rng.integers(-2000, 2000, 65536) / 2 + 1e-3).astype(np.float32)
+    got = O.lut_gemm_f32(xi[:1, :, :2], wi[:1], half)
+    for l in range(2):
+        acc = np.float32(0)
+        for k in range(40):
+            acc = np.float32(acc + half[int(xi[0, k, l]) * 256 + int(wi[0, k])])
+        assert got[0, 0, l] == acc
+
+
+def test_lut_class_boundaries():
+    base = np.zeros(65536, dtype=np.float32)
+    t = base.copy(); t[5] = 32767; t[6] = -32767
+    assert O.lut_class(t) == 0
+    t = base.copy(); t[5] = 32768
+    assert O.lut_class(t) == 1
+    t = base.copy(); t[5] = 65535
+    assert O.lut_class(t) == 1
+    t = base.copy(); t[5] = 65536
+    assert O.lut_class(t) == 2
+    t = base.copy(); t[5] = 32768; t[6] = -1
+    assert O.lut_class(t) == 2
+    t = base.copy(); t[5] = 0.5
+    assert O.lut_class(t) == 2
+
+
+@pytest.mark.parametrize("geom", [((3, 3), (1, 1), (1, 1), (1, 1)), ((7, 7), (2, 2), (3, 3), (1, 1)),
+                                  ((3, 3), (2, 1), (0, 2), (2, 1)), ((1, 1), (2, 2), (0, 0), (1, 1))])
+def test_unfold_and_fold_match_torch(geom):
+    k, s, p, d = geom
+    x = rng.standard_normal((2, 3, 11, 9))
+    ref = F.unfold(torch.from_numpy(x), k, dilation=d, padding=p, stride=s).numpy()
+    assert np.allclose(O.unfold_values(x, k, s, p, d, 0.0), ref)
+    OH, OW = O.out_size(11, 9, k, s, p, d)
+    col = rng.standard_normal((2, 3 * k[0] * k[1], OH * OW))
+    ref_f = F.fold(torch.from_numpy(col), (11, 9), k, dilation=d, padding=p, stride=s).numpy()
+    assert np.allclose(O.fold(col, (2, 3, 11, 9), k, s, p, d), ref_f)
+
+
+def test_im2col_index_padding_and_order():
+    img = rng.integers(-128, 128, (2, 3, 5, 6)).astype(np.int8)
+    k, s, p, d = (3, 2), (2, 1), (1, 2), (1, 2)
+    got = O.im2col_index(O.image_index(img), k, s, p, d, 128)
+    vals = O.unfold_values(img.astype(np.float64) + 128, k, s, p, d, 128.0)
+    assert np.array_equal(got.astype(np.float64), vals)
+
+
+def test_fakequant_matches_reference_formula_in_torch():
+    # nn/quantization.py:48-52, evaluated with torch on the CPU
+    x = np.concatenate([rng.standard_normal(5000).astype(np.float32) * 3,
+                        np.array([0.5, 1.5, 2.5, -0.5, -1.5, 126.5, 127.4, 127.6, -127.5, -200,
+                                  np.nan, 0.0, -0.0], dtype=np.float32)])
+    for scale in (np.float32(0.023), np.float32(1.0), np.float32(0.0)):
+        q, m = O.fakequant(x, scale, -127, 127)
+        xt = torch.from_numpy(x)
+        s = torch.clamp(torch.tensor(scale), min=1e-12)
+        v = xt / s
+        assert np.array_equal(m, ((v >= -127) & (v <= 127)).numpy())
+        qt = torch.clamp(torch.round(v), -127, 127).numpy()
+        assert np.array_equal(q, qt, equal_nan=True)
+    # asymmetric: v = x/s + z
+    z = np.float32(17)
+    q, m = O.fakequant(x, np.float32(0.05), 0, 255, zero=z)
+    v = torch.from_numpy(x) / torch.tensor(np.float32(0.05)) + torch.tensor(z)
+    assert np.array_equal(q, torch.clamp(torch.round(v), 0, 255).numpy(), equal_nan=True)
+    assert np.array_equal(m, ((v >= 0) & (v <= 255)).numpy())
+
+
+def test_fakequant_hand_cases():
+    q, m = O.fakequant(np.array([0.5, 1.5, 2.5, 130.0, -130.0], dtype=np.float32),
+                       np.float32(1.0), -127, 127)
+    assert q.tolist() == [0.0, 2.0, 2.0, 127.0, -127.0]
+    assert m.tolist() == [True, True, True, False, False]
+    g = O.fakequant_backward(np.array([1, 1, 1, 1, 1], dtype=np.float32), m, np.float32(0.5))
+    assert g.tolist() == [2.0, 2.0, 2.0, 0.0, 0.0]
+
+
+def test_ema_and_qparams_match_torch_bitwise():
+    for m in (0.05, 0.1, 0.3333):
+        x = rng.standard_normal(777).astype(np.float32) * 4
+        old = np.float32(0.0371)
+        xt = torch.from_numpy(x)
+        cur = xt.abs().max() / ((127 - -127) / 2)
+        want = (m * cur + (1 - m) * torch.tensor(old)).item()
+        assert O.ema_absmax(x, old, m) == np.float32(want)
+        w = rng.standard_normal((6, 3, 3, 3)).astype(np.float32)
+        w[2] = 0
+        sw = rng.random(6).astype(np.float32)
+        wt = torch.from_numpy(w)
+        absmax = wt.abs().amax(dim=(1, 2, 3))
+        cur_w = torch.where(absmax > 0, absmax / 7, torch.from_numpy(sw))
+        want_w = (m * cur_w + (1 - m) * torch.from_numpy(sw)).numpy()
+        assert np.array_equal(O.weight_scale_ema(w, sw, m, 7), want_w)
+    mn = torch.tensor([-1.3, 0.4, -0.0, -5.0])
+    mx = torch.tensor([2.2, 3.0, 0.0, -1.0])
+    mnc, mxc = torch.clamp(mn, max=0.0), torch.clamp(mx, min=0.0)
+    sc = torch.clamp((mxc - mnc) / 255, min=1e-12)
+    zr = torch.round(-mnc / sc).clamp(0.0, 255.0)
+    s, z = O.uint8_qparams(mn.numpy(), mx.numpy())
+    assert np.array_equal(s, sc.numpy()) and np.array_equal(z, zr.numpy())
+
+
+def test_lre_tables_closed_form_and_linregress():
+    a = np.arange(256) - 128
+    ga, gb = O.lre_tables((a[:, None] * a[None, :]).astype(np.float32))
+    assert np.allclose(ga, a) and np.allclose(gb, a)
+    from scipy.stats import linregress
+    lut = rng.integers(-2000, 2000, (256, 256)).astype(np.float32)
+    ga, gb = O.lre_tables(lut)
+    for y in (0, 77, 255):
+        assert abs(ga[y] - linregress(a, lut[:, y]).slope) < 1e-5
+        assert abs(gb[y] - linregress(a, lut[y, :]).slope) < 1e-5
+
+
+def test_date_closed_forms():
+    i = np.arange(256, dtype=np.float64)
+    lin = (3 * i[:, None] + 5 * i[None, :]).astype(np.float32)
+    ga, gb = O.date_tables(lin, 2)
+    assert np.allclose(ga, 3) and np.allclose(gb, 5)
+    quad = np.repeat((i * i)[:, None], 256, axis=1).astype(np.float32)
+    ga, _ = O.date_tables(quad, 2)
+    inner = np.arange(3, 253)
+    assert np.allclose(ga[inner, 0], 2 * inner)           # d/da of a^2 = 2a
+    assert np.allclose(ga[0, 0], (quad[255, 0] - quad[0, 0]) / 255)
+
+
+def test_gemm_grads_estimators_agree_on_exact_tables():
+    xi = rng.integers(0, 256, (2, 7, 5), dtype=np.uint8)
+    wi = rng.integers(0, 256, (3, 7), dtype=np.uint8)
+    go = rng.standard_normal((2, 3, 5))
+    gx, gw = O.gemm_grads(go, xi, wi, "ste")
+    want_x = np.einsum("nol,ok->nkl", go, wi.astype(np.float64) - 128)
+    want_w = np.einsum("nol,nkl->ok", go, xi.astype(np.float64) - 128)
+    assert np.allclose(gx, want_x) and np.allclose(gw, want_w)
+    dec = np.arange(256, dtype=np.float32) - 128
+    lx, lw = O.gemm_grads(go, xi, wi, "lre", (dec, dec))
+    assert np.allclose(lx, gx) and np.allclose(lw, gw)
+    a = np.arange(256) - 128.0
+    dxl = np.repeat(a[None, :], 256, axis=0)       # d(x*w)/dx = w
+    dwl = np.repeat(a[:, None], 256, axis=1)       # d(x*w)/dw = x
+    cx, cw = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl))
+    assert np.allclose(cx, gx) and np.allclose(cw, gw)
+
+
+def _geoms():
+    return [((3, 3), (1, 1), (1, 1), (1, 1)), ((3, 3), (2, 2), (1, 1), (1, 1)),
+            ((1, 1), (1, 1), (0, 0), (1, 1)), ((3, 1), (1, 2), (2, 0), (2, 1))]
+
+
+@pytest.mark.parametrize("geom", _geoms())
+def test_int8_layer_exact_lut_equals_float_conv(geom):
+    k, s, p, d = geom
+    x = rng.standard_normal((2, 4, 9, 8)).astype(np.float32)
+    w = rng.standard_normal((5, 4, *k)).astype(np.float32) * 0.3
+    b = rng.standard_normal(5).astype(np.float32)
+    sx = np.float32(np.abs(x).max() / 127)
+    sw = (np.abs(w).reshape(5, -1).max(axis=1) / 127).astype(np.float32)
+    a = np.arange(256) - 128
+    lut = (a[:, None] * a[None, :]).reshape(-1)
+    y, _ = O.conv_int8_forward(x, w, b, lut, sx, sw, k, s, p, d)
+    qx, _ = O.fakequant(x, sx, -127, 127)
+    qw, _ = O.fakequant(w, sw.reshape(5, 1, 1, 1), -127, 127)
+    ref = F.conv2d(torch.from_numpy(qx).double(), torch.from_numpy(qw).double(), None, s, p, d)
+    sc = (sx * sw).astype(np.float32).astype(np.float64)
+    ref = ref.numpy() * sc[None, :, None, None] + b[None, :, None, None]
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-9)
+
+
+@pytest.mark.parametrize("geom", _geoms())
+def test_int8_layer_ste_grads_match_torch_autograd(geom):
+    k, s, p, d = geom
+    x = rng.standard_normal((2, 3, 8, 7)).astype(np.float32)
+    w = rng.standard_normal((4, 3, *k)).astype(np.float32) * 0.3
+    sx = np.float32(np.abs(x).max() / 100)     # some values clip
+    sw = (np.abs(w).reshape(4, -1).max(axis=1) / 100).astype(np.float32)
+    a = np.arange(256) - 128
+    lut = ((a[:, None] * a[None, :]) >> 3).reshape(-1)
+    go = rng.standard_normal((2, 4, *O.out_size(8, 7, k, s, p, d)))
+    _, ctx = O.conv_int8_forward(x, w, None, lut, sx, sw, k, s, p, d)
+    gx, gw, _ = O.conv_int8_backward(go, ctx, sx, sw, "ste", None, k, s, p, d)
+    # the reference composition with torch autograd (STE = exact product)
+    xt = torch.from_numpy(x).double().requires_grad_()
+    wt = torch.from_numpy(w).double().requires_grad_()
+    vx = xt / float(sx)
+    mx = ((vx >= -127) & (vx <= 127)).double()
+    qx = torch.clamp(torch.round(vx), -127, 127).detach() + (vx - vx.detach()) * mx
+    vw = wt / torch.from_numpy(sw).double().view(-1, 1, 1, 1)
+    mw = ((vw >= -127) & (vw <= 127)).double()
+    qw = torch.clamp(torch.round(vw), -127, 127).detach() + (vw - vw.detach()) * mw
+    y = F.conv2d(qx, qw, None, s, p, d)
+    sc = torch.from_numpy((sx * sw).astype(np.float32)).double().view(1, -1, 1, 1)
+    (y * sc * torch.from_numpy(go)).sum().backward()
+    assert np.allclose(gx, xt.grad.numpy(), rtol=1e-9, atol=1e-9)
+    assert np.allclose(gw, wt.grad.numpy(), rtol=1e-9, atol=1e-9)
+
+
+def test_uint8_layer_exact_lut_is_centred_conv_and_grads_match_autograd():
+    k, s, p, d = (3, 3), (1, 1), (1, 1), (1, 1)
+    x = rng.standard_normal((2, 3, 7, 6)).astype(np.float32) + 0.3
+    w = rng.standard_normal((4, 3, 3, 3)).astype(np.float32) * 0.2
+    sx, zx = O.uint8_qparams(x.min(), x.max())
+    sw, zw = O.uint8_qparams(w.reshape(4, -1).min(1), w.reshape(4, -1).max(1))
+    v = np.arange(256)
+    lut = (v[:, None] * v[None, :]).reshape(-1)
+    y, ctx = O.conv_uint8_forward(x, w, None, lut, sx, zx, sw, zw, k, s, p, d)
+    qx, _ = O.fakequant(x, sx, 0, 255, zero=zx)
+    qw, _ = O.fakequant(w, sw.reshape(4, 1, 1, 1), 0, 255, zero=zw.reshape(4, 1, 1, 1))
+    cx = torch.from_numpy(qx).double() - float(zx)
+    cw = torch.from_numpy(qw).double() - torch.from_numpy(zw).double().view(-1, 1, 1, 1)
+    sc = (sx * sw).astype(np.float32).astype(np.float64)
+    ref = F.conv2d(cx, cw, None, s, p, d).numpy() * sc[None, :, None, None]
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-9)
+    # STE gradients vs torch autograd of the reference's unfold formulation
+    go = rng.standard_normal(y.shape)
+    gx, gw, _ = O.conv_uint8_backward(go, ctx, sx, sw, "ste", None, k, s, p, d)
+    xt = torch.from_numpy(x).double().requires_grad_()
+    wt = torch.from_numpy(w).double().requires_grad_()
+    vx = xt / float(sx) + float(zx)
+    mx = ((vx >= 0) & (vx <= 255)).double()
+    q_x = torch.clamp(torch.round(vx), 0, 255).detach() + (vx - vx.detach()) * mx
+    vw = wt / torch.from_numpy(sw).double().view(-1, 1, 1, 1) + \
+        torch.from_numpy(zw).double().view(-1, 1, 1, 1)
+    mw = ((vw >= 0) & (vw <= 255)).double()
+    q_w = torch.clamp(torch.round(vw), 0, 255).detach() + (vw - vw.detach()) * mw
+    xp = F.pad(q_x - float(zx), (1, 1, 1, 1)) + float(zx)
+    xu = F.unfold(xp, k, dilation=d, padding=0, stride=s)
+    wu = q_w.view(4, -1)
+    lutsum = torch.einsum("nkl,ok->nol", xu, wu)
+    corr = lutsum - torch.from_numpy(zw).double().view(1, -1, 1) * xu.sum(1, keepdim=True) \
+        - (float(zx) * wu.sum(1)).view(1, -1, 1) + 27 * float(zx) * \
+        torch.from_numpy(zw).double().view(1, -1, 1)
+    yy = corr.view(go.shape) * torch.from_numpy(sc).view(1, -1, 1, 1)
+    (yy * torch.from_numpy(go)).sum().backward()
+    assert np.allclose(gx, xt.grad.numpy(), rtol=1e-9, atol=1e-8)
+    assert np.allclose(gw, wt.grad.numpy(), rtol=1e-9, atol=1e-8)
