@@ -53,7 +53,8 @@ custom_dx_kernel(const void* __restrict__ x, const void* __restrict__ w,
     __syncthreads();
     if (valid) {
       const int oe = min(DX_O, O - ob);
-      for (int oo = 0; oo < oe; ++oo) acc += sdy[oo][tl] * lut[row + sw[oo][tk]];
+      // fused multiply-add, as the reference's contracted acc += dy * lut
+      for (int oo = 0; oo < oe; ++oo) acc = fmaf(sdy[oo][tl], lut[row + sw[oo][tk]], acc);
     }
     __syncthreads();
   }
@@ -100,7 +101,8 @@ custom_dw_kernel(const void* __restrict__ x, const void* __restrict__ w,
     __syncthreads();
     if (valid) {
       const int pn = (int)std::min<long long>(DW_P, pe - p0);
-      for (int pp = 0; pp < pn; ++pp) acc += sdy[pp][to] * lut[sx[pp][tk] * 256u + col];
+      for (int pp = 0; pp < pn; ++pp)
+        acc = fmaf(sdy[pp][to], lut[sx[pp][tk] * 256u + col], acc);
     }
     __syncthreads();
   }

@@ -455,7 +455,8 @@ int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
   ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
               "atx_pack_x_f32: Rpad must be a multiple of %d covering N*L", RT);
   if ((long long)K * Rpad == 0) return ATX_OK;
-  ATX_REQUIRE(x && xt, "atx_pack_x_f32: null pointer");
+  // an empty x (N*L == 0) only writes the zero padding rows
+  ATX_REQUIRE(xt && ((long long)N * L == 0 || x), "atx_pack_x_f32: null pointer");
   dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
   hipLaunchKernelGGL(pack_x_kernel<float>, grid, dim3(256), 0, stream, x, N, K, L,
                      offset, xq, xt, Rpad);
@@ -468,7 +469,7 @@ int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad
   ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
               "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
   if ((long long)K * Rpad == 0) return ATX_OK;
-  ATX_REQUIRE(xq && xt, "atx_pack_x_u8: null pointer");
+  ATX_REQUIRE(xt && ((long long)N * L == 0 || xq), "atx_pack_x_u8: null pointer");
   dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
   hipLaunchKernelGGL(pack_x_kernel<uint8_t>, grid, dim3(256), 0, stream, xq, N, K,
                      L, 0, (uint8_t*)nullptr, xt, Rpad);
@@ -481,7 +482,8 @@ int atx_pack_w_f32(const float* w, int O, int K, int offset, uint8_t* wq,
   ATX_REQUIRE(Opad >= O && Opad % OT == 0,
               "atx_pack_w_f32: Opad must be a multiple of %d covering O", OT);
   if ((long long)K * Opad == 0) return ATX_OK;
-  ATX_REQUIRE(w && wt, "atx_pack_w_f32: null pointer");
+  // an empty w (O == 0) only writes the padding columns
+  ATX_REQUIRE(wt && (O == 0 || w), "atx_pack_w_f32: null pointer");
   hipLaunchKernelGGL(pack_w_kernel<float>, dim3(elem_grid((long long)K * Opad, 256)),
                      dim3(256), 0, stream, w, O, K, offset, wq, wt, Opad);
   return check_launch("pack_w_kernel<float>");
@@ -493,7 +495,7 @@ int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
   ATX_REQUIRE(Opad >= O && Opad % OT == 0,
               "atx_pack_w_u8: Opad must be a multiple of %d covering O", OT);
   if ((long long)K * Opad == 0) return ATX_OK;
-  ATX_REQUIRE(wq && wt, "atx_pack_w_u8: null pointer");
+  ATX_REQUIRE(wt && (O == 0 || wq), "atx_pack_w_u8: null pointer");
   hipLaunchKernelGGL(pack_w_kernel<uint8_t>, dim3(elem_grid((long long)K * Opad, 256)),
                      dim3(256), 0, stream, wq, O, K, 0, (uint8_t*)nullptr, wt, Opad);
   return check_launch("pack_w_kernel<u8>");

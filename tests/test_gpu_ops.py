@@ -265,8 +265,16 @@ def test_ema_kernels_bitwise(m):
 
 
 # ------------------------------------------------------------ backward ops
-def close(a, b):
-    np.testing.assert_allclose(np.asarray(a, dtype=np.float64), b, rtol=RTOL, atol=ATOL)
+def close(a, b, absref=None):
+    """rel 1e-5 / abs 1e-4.  With absref (the sum of |terms| of each output),
+    the relative part is taken against it: an fp32 sum of n terms in any order
+    is within n * 6e-8 * sum|terms| of the exact value, so this is the bound
+    the reference's own fp32 accumulation order meets (cancelling sums make a
+    relative bound on the result itself meaningless)."""
+    a = np.asarray(a, dtype=np.float64)
+    ref = np.abs(b) if absref is None else absref
+    excess = np.abs(a - b) - (ATOL + RTOL * ref)
+    assert excess.max() <= 0, f"max excess {excess.max():.3g} at {np.unravel_index(excess.argmax(), a.shape)}"
 
 
 @pytest.mark.parametrize("xdtype", ["uint8", "int8", "float32"])
@@ -310,8 +318,9 @@ def test_custom_grad_kernels(signed):
     gx = fdx(t(X), t(W), t(go), t(dxl.reshape(-1)))
     gw = fdw(t(X), t(W), t(go), t(dwl.reshape(-1)))
     ex, ew = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl))
-    close(gx.cpu().numpy(), ex)
-    close(gw.cpu().numpy(), ew)
+    ax, aw = O.gemm_grads(np.abs(go), xi, wi, "custom", (np.abs(dxl), np.abs(dwl)))
+    close(gx.cpu().numpy(), ex, ax)
+    close(gw.cpu().numpy(), ew, aw)
 
 
 @pytest.mark.parametrize("geom", GEOMS)
