@@ -26,8 +26,10 @@ inline int elem_grid(long long n, int threads, int cap = 8192) {
   return (int)(b < cap ? b : cap);
 }
 
+// Byte offset of row v of a LUT GEMM table (128-byte rows of 8 16-byte
+// channel chunks; chunk g of row v sits at position g ^ ((v >> 1) & 7)).
 __device__ __forceinline__ unsigned row_offset(unsigned v) {
-  return v * 128u + (((v >> 3) & 7u) << 4);
+  return v * 128u + (((v >> 1) & 7u) << 4);
 }
 
 // clamp(rint(v) + offset, 0, 255) with round-half-even; NaN maps to `offset`

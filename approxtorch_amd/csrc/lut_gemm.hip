@@ -10,11 +10,19 @@
 //   int32 accumulators (exact).  E is double-buffered, so one barrier per k.
 //
 //   LDS bank layout: an E row is 128 bytes (all 32 banks).  Its 16-byte
-//   chunk for channels 8g..8g+7 is stored at chunk position g ^ ((v>>3)&7).
+//   chunk for channels 8g..8g+7 is stored at chunk position g ^ ((v>>1)&7).
 //   The activation operand is pre-encoded as the byte offset
-//   v*128 + ((v>>3)&7)*16 ("row offset"), so the lane's address is
-//   row_offset ^ (g*16): no arithmetic on the index itself.  The swizzle
-//   makes the table build's 4-byte LDS writes conflict-free.
+//   v*128 + ((v>>1)&7)*16 ("row offset"), so the lane's address is
+//   row_offset ^ (g*16): no arithmetic on the index itself.
+//
+//   Table build: wave w builds channel group w.  Its eight weight indices at
+//   k are wave-uniform (one scalar load); lane t loads the dwords
+//   LUT16T[w_j][2t, 2t+1] of the eight channels j (scalar base + lane
+//   offset, 256 contiguous bytes per instruction), interleaves them with
+//   v_perm into the 16-byte chunks of rows 2t and 2t+1 and stores each with
+//   one ds_write_b128.  The swizzle gives the eight lanes of every write
+//   group distinct chunk positions, so the writes are conflict-free (4-byte
+//   LDS writes reach only about a third of the 16-byte write bandwidth).
 //
 //   Threads: 512 (8 waves).  Lane = (row group rg 0..7, channel group g);
 //   each lane owns RPL = 16 consecutive rows x 8 channels = 128 int32
@@ -159,22 +167,26 @@ __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
   }
 }
 
-struct Rows { uint4 a[IPT], b[IPT]; };
+// Table-build registers: for each build item, the LUT16T dwords
+// (entries v0, v0+1) of the wave's eight channels.
+struct Rows { unsigned d[IPT][8]; };
 struct XRows { uint4 v[RPL / 8]; };
 
-__device__ __forceinline__ unsigned load_w(const uint8_t* __restrict__ wt, int Opad,
-                                           int k, int pair_col) {
-  return *(const unsigned short*)(wt + (long long)k * Opad + pair_col);
+// Eight weight indices (channels o0 + 8*og .. +7) at k: wave-uniform.
+__device__ __forceinline__ uint2 load_w8(const uint8_t* __restrict__ wrow, int Opad, int k) {
+  return *(const uint2*)(wrow + (long long)k * Opad);
 }
 
-// LUT16T rows of the two weight indices packed in w (lo byte: channel 2pp,
-// hi byte: channel 2pp+1), v-chunk c[i] (8 entries each) per build item.
+// Dword at entries (v0, v0+1) of LUT16T row w_j for every channel j of the
+// group; item i covers v0 = 2*lane + 128*i.  Row bases are wave-uniform.
 __device__ __forceinline__ void load_rows(Rows& r, const uint16_t* __restrict__ lut,
-                                          const unsigned (&w)[IPT], const int (&c)[IPT]) {
+                                          uint2 w8, int lane) {
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    r.a[i] = *(const uint4*)(lut + (w[i] & 255u) * 256u + c[i] * 8);
-    r.b[i] = *(const uint4*)(lut + ((w[i] >> 8) & 255u) * 256u + c[i] * 8);
+  for (int j = 0; j < 8; ++j) {
+    const unsigned wj = ((j < 4 ? w8.x : w8.y) >> (8 * (j & 3))) & 255u;
+    const unsigned* row = (const unsigned*)(lut + wj * 256u);
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) r.d[i][j] = row[lane + 64 * i];
   }
 }
 
@@ -185,21 +197,25 @@ __device__ __forceinline__ void load_x(XRows& x, const uint16_t* __restrict__ xt
   for (int i = 0; i < RPL / 8; ++i) x.v[i] = xp[i];
 }
 
-// Writes this lane's dwords of one table (wbase includes the LDS buffer):
-// entry pairs (channel 2pp, 2pp+1) for v = 8c .. 8c+7 of each build item.
+// Writes this lane's two 16-byte chunks per build item (rows v0 and v0+1,
+// channels 8*og .. 8*og+7); wbase holds the chunk address of row v0
+// including the LDS buffer.
 __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
                                             const int (&wbase)[IPT]) {
 #pragma unroll
   for (int it = 0; it < IPT; ++it) {
-    unsigned char* base = smem + wbase[it];
-    const unsigned av[4] = {r.a[it].x, r.a[it].y, r.a[it].z, r.a[it].w};
-    const unsigned bv[4] = {r.b[it].x, r.b[it].y, r.b[it].z, r.b[it].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // dword i holds entries v = 8c + 2i (low half) and 8c + 2i + 1 (high)
-      *(unsigned*)(base + (2 * i) * 128) = __builtin_amdgcn_perm(bv[i], av[i], 0x05040100u);
-      *(unsigned*)(base + (2 * i + 1) * 128) = __builtin_amdgcn_perm(bv[i], av[i], 0x07060302u);
-    }
+    const unsigned* d = r.d[it];
+    uint4 lo, hi;      // channel pairs (2m, 2m+1) at v0 (low halves) / v0+1 (high)
+    lo.x = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
+    lo.y = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
+    lo.z = __builtin_amdgcn_perm(d[5], d[4], 0x05040100u);
+    lo.w = __builtin_amdgcn_perm(d[7], d[6], 0x05040100u);
+    hi.x = __builtin_amdgcn_perm(d[1], d[0], 0x07060302u);
+    hi.y = __builtin_amdgcn_perm(d[3], d[2], 0x07060302u);
+    hi.z = __builtin_amdgcn_perm(d[5], d[4], 0x07060302u);
+    hi.w = __builtin_amdgcn_perm(d[7], d[6], 0x07060302u);
+    *(uint4*)(smem + wbase[it]) = lo;
+    *(uint4*)(smem + wbase[it] + 128) = hi;
   }
 }
 
@@ -243,23 +259,18 @@ lut_gemm_kernel(const GemmParams p) {
   const int kb = s * p.k_chunk;
   const int ke = min(p.K, kb + p.k_chunk);
 
-  // Table-build mapping: build item q = wave*IPT + i (16 items) covers
-  // channel group og = q & 7 and v-chunk c = (q >> 3) * 16 + cc; lane
-  // (cc, pp) handles channel pair o0 + 8*og + 2*pp (+1).  Within a wave the
-  // 4-byte LDS writes hit every bank exactly twice (the minimum for 64 lanes).
-  const int cc = lane >> 2, pp = lane & 3;
-  int c[IPT], pair_col[IPT], wbase[IPT];
+  // Table-build mapping: wave w builds channel group og = w; lane t writes
+  // rows v0 = 2t + 128i and v0+1 (item i), whose chunk og sits at position
+  // og ^ ((v0 >> 1) & 7) = og ^ (t & 7).
+  static_assert(NWAVE == 8 && IPT == 2, "one wave per channel group, 256 rows");
+  const int og = __builtin_amdgcn_readfirstlane(wave);
+  int wbase[IPT];
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int q = wave * IPT + i;
-    const int og = q & 7;
-    c[i] = (q >> 3) * 16 + cc;
-    pair_col[i] = o0 + og * 8 + 2 * pp;
-    wbase[i] = c[i] * 1024 + ((og ^ (cc & 7)) << 4) + pp * 4;
-  }
+  for (int i = 0; i < IPT; ++i)
+    wbase[i] = (2 * lane + 128 * i) * 128 + ((og ^ (lane & 7)) << 4);
 
   const uint16_t* __restrict__ xt = p.xt;
-  const uint8_t* __restrict__ wt = p.wt;
+  const uint8_t* __restrict__ wrow = p.wt + o0 + og * 8;
   const uint16_t* __restrict__ lut = p.lut16t;
 
   int acc[RPL][8];
@@ -278,16 +289,12 @@ lut_gemm_kernel(const GemmParams p) {
     const int klast = ke - 1;
     constexpr unsigned BUFX = (unsigned)ETAB;               // bit 15
     XRows xc;
-    unsigned wnext[IPT];
+    uint2 wnext;
     {
-      unsigned w0[IPT];
-#pragma unroll
-      for (int i = 0; i < IPT; ++i) {
-        w0[i] = load_w(wt, p.Opad, kb, pair_col[i]);
-        wnext[i] = load_w(wt, p.Opad, min(kb + 1, klast), pair_col[i]);
-      }
+      const uint2 w0 = load_w8(wrow, p.Opad, kb);
+      wnext = load_w8(wrow, p.Opad, min(kb + 1, klast));
       Rows rows;
-      load_rows(rows, lut, w0, c);
+      load_rows(rows, lut, w0, lane);
       load_x(xc, xt, p.Rpad, kb, r0);
       write_table(smem, rows, wbase);
     }
@@ -299,21 +306,16 @@ lut_gemm_kernel(const GemmParams p) {
     for (int k = kb; k < ke; ++k) {
       XRows xn;
       Rows rows;
-      unsigned wn2[IPT];
       load_x(xn, xt, p.Rpad, min(k + 1, klast), r0);
-      load_rows(rows, lut, wnext, c);
-#pragma unroll
-      for (int i = 0; i < IPT; ++i)
-        wn2[i] = load_w(wt, p.Opad, min(k + 2, klast), pair_col[i]);
+      load_rows(rows, lut, wnext, lane);
+      const uint2 wn2 = load_w8(wrow, p.Opad, min(k + 2, klast));
       use_table<SIGNED>(acc, smem, xc, gx);
       __builtin_amdgcn_sched_barrier(0);
       write_table(smem, rows, wbase);
       xc = xn;
+      wnext = wn2;
 #pragma unroll
-      for (int i = 0; i < IPT; ++i) {
-        wnext[i] = wn2[i];
-        wbase[i] ^= ETAB;
-      }
+      for (int i = 0; i < IPT; ++i) wbase[i] ^= ETAB;
       gx ^= BUFX;
       __syncthreads();
     }

@@ -39,7 +39,58 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
+    ap.add_argument("--probe-lds", action="store_true",
+                    help="also measure the LDS read throughput (roofline denominator)")
     return ap.parse_args()
+
+
+def lds_probe(torch):
+    """Measured LDS read bandwidth per pattern (GB/s over the whole GPU)."""
+    from approxtorch_amd.backend import _lib as L
+    blocks, iters = 2 * 256, 4096
+    out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
+    res = {}
+    for mode, nbytes, name in ((0, 16, "b128_random_128B_row_per_8_lanes"),
+                               (1, 16, "b128_contiguous_1KiB_per_wave"),
+                               (2, 16, "b128_128B_row_per_8_lanes_parity_split"),
+                               (3, 16, "b128_random_256B_row_per_16_lanes"),
+                               (4, 2, "u16_random"),
+                               (5, 4, "b32_write_random_128B_row_per_32_lanes")):
+        L.call("atx_lds_probe", mode, blocks, 8, out.data_ptr(), L.stream_of(out))
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        L.call("atx_lds_probe", mode, blocks, iters, out.data_ptr(), L.stream_of(out))
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e)
+        res[name] = round(blocks * 512 * iters * 8 * nbytes / (ms * 1e-3) / 1e9, 1)
+    return res
+
+
+def bgemm_c3(torch, args):
+    """Config 3 as the timed step: y = LUT-BGEMM of int8 A [32,4096,2304] and
+    W [2304,256] with the perturbed LUT; value in G LUT-MAC/s."""
+    from approxtorch_amd import workloads
+    from approxtorch_amd.backend import ops
+    lut = torch.from_numpy(workloads.lut_perturbed(3)).cuda()
+    g = torch.Generator().manual_seed(3)
+    K = 2304
+    x = torch.randint(0, 256, (32, K, 4096), generator=g, dtype=torch.uint8).cuda()
+    w = torch.randint(-128, 128, (256, K), generator=g).float().cuda()
+    timer = GemmTimer()
+    timer.install()
+    for _ in range(args.warmup):
+        ops.bgemm_fake_int8_claude(x, w, lut)
+    torch.cuda.synchronize()
+    timer.active = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ops.bgemm_fake_int8_claude(x, w, lut)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timer.active = False
+    return dt, timer, 32 * 4096 * K * 256
 
 
 class GemmTimer:
@@ -130,7 +181,9 @@ def main():
     from approxtorch_amd import workloads
     torch.backends.cudnn.benchmark = False
     dev = torch.device("cuda:0")
-    name = args.workload if args.workload != "c3" else "c4"
+    if args.workload == "c3":
+        return main_c3(torch, args)
+    name = args.workload
     model, opt, x, y, cfg = workloads.build_training_workload(name, dev)
     macs_fwd = workloads.conv_lut_macs(model, tuple(x.shape))
     timer = GemmTimer()
@@ -145,8 +198,6 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     timer.active = False
-    gemm_ms, gemm_macs, launches = timer.summary()
-    achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
     result = {
         "metric": "ResNet-50 224^2 approx-QAT img/s (LUT-MAC/s + % LDS roofline)"
         if name == "c4" else f"{name} approx-QAT img/s",
@@ -166,24 +217,80 @@ def main():
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
                    "forward_lut_macs": macs_fwd},
-        "roofline": {
-            "kernel": "lut_gemm_kernel (+ split-K reduce)",
-            "bound": "lds",
-            "achieved": round(2 * achieved_glut, 1),
-            "peak": LDS_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(2 * achieved_glut / LDS_PEAK_GBS, 4),
-            "traffic": None,
-            "lut_mac_per_s_G": round(achieved_glut, 1),
-            "launches": launches,
-            "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
-            "share_of_step": round(gemm_ms / (dt * 1e3), 4),
-        },
+        "roofline": roofline(timer, dt),
     }
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
+    if args.probe_lds:
+        result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_sample_batch)
+    print(json.dumps(result), flush=True)
+
+
+def roofline(timer, dt):
+    gemm_ms, gemm_macs, launches = timer.summary()
+    achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
+    return {
+        "kernel": "lut_gemm_kernel (+ split-K reduce)",
+        "bound": "lds",
+        "achieved": round(2 * achieved_glut, 1),
+        "peak": LDS_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(2 * achieved_glut / LDS_PEAK_GBS, 4),
+        "traffic": None,
+        "lut_mac_per_s_G": round(achieved_glut, 1),
+        "launches": launches,
+        "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
+        "share_of_step": round(gemm_ms / (dt * 1e3), 4),
+    }
+
+
+def cpu_baseline_c3(torch):
+    """torch-CPU unfold-free restatement (index -> take -> int64 sum) of the
+    config-3 BGEMM on a bounded sample: one batch element, first 64 rows."""
+    from approxtorch_amd import workloads
+    from oracle import torch_cpu
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(3)
+    K, rows = 2304, 2048
+    xi = torch.randint(0, 256, (1, K, rows), generator=g, dtype=torch.int64)
+    wi = torch.randint(0, 256, (256, K), generator=g, dtype=torch.int64)
+    lut = torch.from_numpy(workloads.lut_perturbed(3)).to(torch.int64)
+    t0 = time.perf_counter()
+    torch_cpu.lut_sum(xi, wi, lut)
+    dt = time.perf_counter() - t0
+    macs = K * rows * 256
+    return {"value": round(macs / dt / 1e9, 4), "unit": "GLUT-MAC/s", "cores": threads,
+            "kind": "port",
+            "sample": f"1 x [{rows} rows x K={K}] times [K x 256] of config 3 "
+                      f"({macs / 1e6:.0f} M LUT-MACs, {dt:.1f} s; oracle/torch_cpu.lut_sum)"}
+
+
+def main_c3(torch, args):
+    dt, timer, macs = bgemm_c3(torch, args)
+    result = {
+        "metric": "LUT-BGEMM LUT-MAC/s (G), config 3 (B=32, 4096x2304 by 2304x256)",
+        "value": round(macs * args.steps / dt / 1e9, 1),
+        "unit": "GLUT-MAC/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 indices, int16 LUT, int32 sums",
+        "data": "synthetic (seeded uniform int8 operands, perturbed-product LUT)",
+        "config": {"workload": "c3: LUT-BGEMM B=32 A[4096x2304] W[2304x256] int8",
+                   "lut_macs_per_step": macs, "parallelism": "single GPU"},
+        "roofline": roofline(timer, dt),
+    }
+    if args.probe_lds:
+        result["lds_probe_GBs"] = lds_probe(torch)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_c3(torch)
     print(json.dumps(result), flush=True)
 
 

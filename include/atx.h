@@ -259,13 +259,23 @@ int atx_custom_grad_dw(const void* x, const void* w, int is_signed,
                        int L, int O, float* grad_w, float* workspace,
                        hipStream_t stream);
 
+/* ------------------------------------------------------------ diagnostics
+ * LDS throughput probe (no reference counterpart: it measures the LDS
+ * roofline the LUT GEMM is reported against).  blocks x 512 threads, each
+ * lane issuing iters*8 reads of pattern `mode` (0: 16-byte reads, one
+ * 128-byte row per 8-lane group; 1: 16-byte reads, 1 KiB contiguous per
+ * wave; 2: 2-byte reads, 128 contiguous bytes per wave; 3: 2-byte reads at
+ * random addresses).  out: blocks*512 uint32. */
+int atx_lds_probe(int mode, int blocks, int iters, unsigned* out,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
 
 /* Row-offset encoding of LUT index v used by the LUT GEMM's LDS tables. */
 static inline unsigned atx_row_offset(unsigned v) {
-  return v * 128u + (((v >> 3) & 7u) << 4);
+  return v * 128u + (((v >> 1) & 7u) << 4);
 }
 
 #endif /* ATX_H */
