@@ -222,7 +222,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     L.call("atx_im2col_rows", L.ptr(imgc), _dtype_code(imgc, offset == 0), g, pad_index,
            L.ptr(pad_dev), L.ptr(xt), Rpad, L.stream_of(imgc))
     wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)
-    y = torch.empty((N, O, Lc), dtype=torch.float32, device=dev)
+    ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
+    y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
     _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
     return y, wq
 

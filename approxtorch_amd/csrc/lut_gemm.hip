@@ -7,7 +7,8 @@
 //   32 KiB) from the transposed 16-bit LUT image (L2-resident, 128 KiB), then
 //   every lane looks up E_k[xi(r,k)][o..o+7] for its rows with one
 //   conflict-free 16-byte LDS read and adds the eight 16-bit entries into
-//   int32 accumulators (exact).  E is double-buffered, so one barrier per k.
+//   int32 accumulators (exact).  Four E buffers (128 KiB of LDS) let each
+//   step write the table two steps ahead, with one barrier per two steps.
 //
 //   LDS bank layout: an E row is 128 bytes (all 32 banks).  Its 16-byte
 //   chunk for channels 8g..8g+7 is stored at chunk position g ^ ((v>>1)&7).
@@ -16,7 +17,8 @@
 //   row_offset ^ (g*16): no arithmetic on the index itself.
 //
 //   Table build: wave w builds channel group w.  Its eight weight indices at
-//   k are wave-uniform (one scalar load); lane t loads the dwords
+//   k are wave-uniform (one vector load read back with v_readlane); lane t
+//   loads the dwords
 //   LUT16T[w_j][2t, 2t+1] of the eight channels j (scalar base + lane
 //   offset, 256 contiguous bytes per instruction), interleaves them with
 //   v_perm into the 16-byte chunks of rows 2t and 2t+1 and stores each with
@@ -25,8 +27,12 @@
 //   LDS writes reach only about a third of the 16-byte write bandwidth).
 //
 //   Threads: 512 (8 waves).  Lane = (row group rg 0..7, channel group g);
-//   each lane owns RPL = 16 consecutive rows x 8 channels = 128 int32
-//   accumulators (256-VGPR budget at 2 waves per SIMD).
+//   wave w owns rows 128w .. 128w+127 of the tile and lane (rg, g) the rows
+//   32h + 4rg + m (h, m = 0..3) x 8 channels = 128 int32 accumulators
+//   (256-VGPR budget at 2 waves per SIMD).  Four consecutive rows per lane
+//   let the epilogue store every (channel, h) as one 16-byte vector, and the
+//   eight row groups of a channel fill a 128-byte line, so results go from
+//   registers straight to HBM with all waves storing at once.
 //
 // Reference: bgemm_lut_u8_kernel / bgemm_mainloop
 // (csrc/claude/bgemm_lut_kernels.cuh:183-387) computes the same sum with a
@@ -46,11 +52,12 @@ constexpr int NWAVE = RT / RPW;    // waves per workgroup
 constexpr int NT = 64 * NWAVE;     // threads per workgroup
 constexpr int IPT = 1024 / NT;     // table-build items per thread
 constexpr int ETAB = 256 * OT * 2; // bytes of one E_k table (32 KiB)
-constexpr int STAGE_S = RPW + 1;   // epilogue staging stride (dwords per channel)
-constexpr int STAGE_WAVE = OT * STAGE_S * 4;  // bytes per wave
-constexpr int SMEM_BYTES = 2 * ETAB;          // static LDS: two E tables
-static_assert(STAGE_WAVE <= SMEM_BYTES, "epilogue stages one wave at a time");
+constexpr int NBUF = 4;                       // E tables resident in LDS
+constexpr int SMEM_BYTES = NBUF * ETAB;       // 128 KiB of static LDS
+constexpr int RQ = 4;              // consecutive rows per lane quad
+constexpr int NQ = RPL / RQ;       // quads per lane (stride 32 rows)
 static_assert(1024 % NT == 0, "table build needs an integral item count");
+static_assert(RPW == 8 * RQ * NQ, "a wave's rows are 8 row groups x NQ quads");
 
 // K limits for exact int32 partial sums (entries up to 32767 / 65535).
 constexpr int KMAX_I16 = 65536;
@@ -170,38 +177,48 @@ __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
 // Table-build registers: for each build item, the LUT16T dwords
 // (entries v0, v0+1) of the wave's eight channels.
 struct Rows { unsigned d[IPT][8]; };
-struct XRows { uint4 v[RPL / 8]; };
+// Row offsets of the lane's quads: v[h] = rows 32h + 4rg + 0..3, two per dword.
+struct XRows { uint2 v[NQ]; };
 
-// Eight weight indices (channels o0 + 8*og .. +7) at k: wave-uniform.
-__device__ __forceinline__ uint2 load_w8(const uint8_t* __restrict__ wrow, int Opad, int k) {
-  return *(const uint2*)(wrow + (long long)k * Opad);
+// Eight weight indices (channels o0 + 8*og .. +7) at k.  Lane parity picks
+// the dword (indices 0-3 / 4-7) so the load is a vector load: a scalar load
+// would share the LDS wait counter and, completing out of order, force every
+// LDS wait of the step to drain it.
+__device__ __forceinline__ unsigned load_w8(const uint8_t* __restrict__ wrow, int Opad,
+                                            int k, int lane) {
+  return ((const unsigned*)(wrow + (long long)k * Opad))[lane & 1];
 }
 
 // Dword at entries (v0, v0+1) of LUT16T row w_j for every channel j of the
-// group; item i covers v0 = 2*lane + 128*i.  Row bases are wave-uniform.
+// group; item i covers v0 = 2*lane + 128*i.  Row bases are wave-uniform
+// (read from lanes 0 and 1 of the weight-index register).
 __device__ __forceinline__ void load_rows(Rows& r, const uint16_t* __restrict__ lut,
-                                          uint2 w8, int lane) {
+                                          unsigned wv, int lane) {
+  const unsigned w_lo = __builtin_amdgcn_readlane(wv, 0);
+  const unsigned w_hi = __builtin_amdgcn_readlane(wv, 1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const unsigned wj = ((j < 4 ? w8.x : w8.y) >> (8 * (j & 3))) & 255u;
+    const unsigned wj = ((j < 4 ? w_lo : w_hi) >> (8 * (j & 3))) & 255u;
     const unsigned* row = (const unsigned*)(lut + wj * 256u);
 #pragma unroll
     for (int i = 0; i < IPT; ++i) r.d[i][j] = row[lane + 64 * i];
   }
 }
 
+// r0 = first row of the lane's first quad (8-byte aligned: Rpad % 1024 == 0).
 __device__ __forceinline__ void load_x(XRows& x, const uint16_t* __restrict__ xt,
                                        int Rpad, int k, int r0) {
-  const uint4* xp = (const uint4*)(xt + (long long)k * Rpad + r0);
+  const uint16_t* xp = xt + (long long)k * Rpad + r0;
 #pragma unroll
-  for (int i = 0; i < RPL / 8; ++i) x.v[i] = xp[i];
+  for (int h = 0; h < NQ; ++h) x.v[h] = *(const uint2*)(xp + 8 * RQ * h);
 }
 
 // Writes this lane's two 16-byte chunks per build item (rows v0 and v0+1,
-// channels 8*og .. 8*og+7); wbase holds the chunk address of row v0
-// including the LDS buffer.
+// channels 8*og .. 8*og+7); wbase holds the chunk address of row v0 within
+// a table, buf the byte offset of the LDS buffer.
 __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
-                                            const int (&wbase)[IPT]) {
+                                            const int (&wbase)[IPT], unsigned buf) {
+  smem += buf;
 #pragma unroll
   for (int it = 0; it < IPT; ++it) {
     const unsigned* d = r.d[it];
@@ -221,13 +238,13 @@ __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
 
 // Accumulates one table for this lane's RPL rows.  x holds the rows'
 // offsets (two per dword); gx XORs in the lane's channel chunk (bits 4-6) and
-// the LDS buffer (bit 15; offsets are below 32768).
+// the LDS buffer (bits 15-16; offsets are below 32768).
 template <bool SIGNED>
 __device__ __forceinline__ void use_table(int (&acc)[RPL][8], const unsigned char* smem,
                                           const XRows& x, unsigned gx) {
 #pragma unroll
-  for (int h = 0; h < RPL / 8; ++h) {
-    const unsigned xd[4] = {x.v[h].x, x.v[h].y, x.v[h].z, x.v[h].w};
+  for (int hh = 0; hh < NQ; hh += 2) {
+    const unsigned xd[4] = {x.v[hh].x, x.v[hh].y, x.v[hh + 1].x, x.v[hh + 1].y};
     uint4 e[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -235,7 +252,77 @@ __device__ __forceinline__ void use_table(int (&acc)[RPL][8], const unsigned cha
       e[2 * j + 1] = *(const uint4*)(smem + ((xd[j] >> 16) ^ gx));
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) add8<SIGNED>(acc[8 * h + j], e[j]);
+    for (int j = 0; j < 8; ++j) add8<SIGNED>(acc[RQ * hh + j], e[j]);
+  }
+}
+
+// Stores W consecutive results v[0..W-1] of channel o at y[yi..yi+W-1] as
+// int32 (kind ATX_OUT_I32, also the split-K partials), fp32, or dequantized
+// fp32 (sx * sw[o] * v [+ bias[o]]).
+template <int KIND, int W>
+__device__ __forceinline__ void put_rows(const GemmParams& p, void* y, long long yi,
+                                         int o, const int* v) {
+  if constexpr (KIND == ATX_OUT_I32) {
+    if constexpr (W == 4) *(int4*)((int*)y + yi) = make_int4(v[0], v[1], v[2], v[3]);
+    else ((int*)y)[yi] = v[0];
+  } else {
+    float f[W];
+    if constexpr (KIND == ATX_OUT_F32) {
+#pragma unroll
+      for (int m = 0; m < W; ++m) f[m] = (float)v[m];
+    } else {
+      const float sc = p.sx[0] * p.sw[o];
+#pragma unroll
+      for (int m = 0; m < W; ++m) {
+        const float t = (float)v[m] * sc;
+        f[m] = p.bias ? p.bias[o] + t : t;
+      }
+    }
+    if constexpr (W == 4) *(float4*)((float*)y + yi) = make_float4(f[0], f[1], f[2], f[3]);
+    else ((float*)y)[yi] = f[0];
+  }
+}
+
+// Writes the lane's accumulators: channel o0 + e, rows r + 32h + m of quad
+// h (r = first row of quad 0).  Rows beyond R and channels beyond O are
+// dropped.  With L % 4 == 0 a quad never straddles two images and is one
+// 16-byte store (r is a multiple of 4); otherwise rows are stored one by one,
+// stepping (n, l) across image boundaries.
+template <int KIND>
+__device__ __forceinline__ void store_tile(const GemmParams& p, void* y,
+                                           const int (&acc)[RPL][8], int r, int o0) {
+  const bool vec = (p.L & 3) == 0;
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    const int rq = r + 8 * RQ * h;
+    if (rq >= p.R) break;
+    const int n = rq / p.L;
+    const int l = rq - n * p.L;
+    if (vec) {
+      const long long ybase = (long long)n * p.O * p.L + l;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int o = o0 + e;
+        if (o >= p.O) break;
+        const int v[RQ] = {acc[RQ * h][e], acc[RQ * h + 1][e], acc[RQ * h + 2][e],
+                           acc[RQ * h + 3][e]};
+        put_rows<KIND, RQ>(p, y, ybase + (long long)o * p.L, o, v);
+      }
+    } else {
+      int nm = n, lm = l;
+#pragma unroll
+      for (int m = 0; m < RQ; ++m) {
+        if (rq + m >= p.R) break;
+        const long long ybase = (long long)nm * p.O * p.L + lm;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int o = o0 + e;
+          if (o >= p.O) break;
+          put_rows<KIND, 1>(p, y, ybase + (long long)o * p.L, o, &acc[RQ * h + m][e]);
+        }
+        if (++lm == p.L) { lm = 0; ++nm; }
+      }
+    }
   }
 }
 
@@ -254,8 +341,7 @@ lut_gemm_kernel(const GemmParams p) {
   const int s = lb / p.tiles_r;
 
   const int o0 = to * OT;
-  const int rtile0 = tr * RT;
-  const int r0 = rtile0 + (wave * 8 + rg) * RPL;         // this lane's rows
+  const int r0 = tr * RT + wave * RPW + rg * RQ;         // this lane's first quad
   const int kb = s * p.k_chunk;
   const int ke = min(p.K, kb + p.k_chunk);
 
@@ -280,94 +366,60 @@ lut_gemm_kernel(const GemmParams p) {
     for (int e = 0; e < 8; ++e) acc[j][e] = 0;
 
   if (kb < ke) {
-    // At step k the wave issues the loads for row offsets k+1, LUT rows of
-    // table k+1 and weight indices of k+2 (indices clamped to the range, so
-    // every load is unconditional), accumulates from table k, writes table
-    // k+1 into the other LDS buffer and meets the other waves at one barrier.
-    // The scheduling fence keeps the table write (which waits for the LUT
-    // rows) behind the accumulation, so the loads overlap a whole step.
+    // Four LDS buffers, table k in buffer k % 4 (counting k from kb), and a
+    // barrier after every second step.  Step k issues the loads for row
+    // offsets k+1, LUT rows of table k+2 and weight indices of k+3 (indices
+    // clamped to the range, so every load is unconditional), accumulates
+    // from table k and then writes table k+2.  Table k+2 overwrites table
+    // k-2, whose last reads (step k-2) precede the barrier closing the pair
+    // before step k; every table is written at least one barrier before its
+    // reads.  Halving the barriers lets waves drift apart within a pair.
+    // Scheduling fences keep the loads ahead of the accumulation and the
+    // table write (which waits for the LUT rows) behind it, so the loads
+    // overlap a whole step.
     const int klast = ke - 1;
-    constexpr unsigned BUFX = (unsigned)ETAB;               // bit 15
     XRows xc;
-    uint2 wnext;
+    unsigned wnext;                                         // indices of table k+2
     {
-      const uint2 w0 = load_w8(wrow, p.Opad, kb);
-      wnext = load_w8(wrow, p.Opad, min(kb + 1, klast));
+      const unsigned w0 = load_w8(wrow, p.Opad, kb, lane);
+      const unsigned w1 = load_w8(wrow, p.Opad, min(kb + 1, klast), lane);
+      wnext = load_w8(wrow, p.Opad, min(kb + 2, klast), lane);
       Rows rows;
       load_rows(rows, lut, w0, lane);
       load_x(xc, xt, p.Rpad, kb, r0);
-      write_table(smem, rows, wbase);
+      write_table(smem, rows, wbase, 0);                    // table kb   -> buffer 0
+      load_rows(rows, lut, w1, lane);
+      write_table(smem, rows, wbase, ETAB);                 // table kb+1 -> buffer 1
     }
-#pragma unroll
-    for (int i = 0; i < IPT; ++i) wbase[i] += ETAB;   // table kb+1 -> buffer 1
-    unsigned gx = (unsigned)(g << 4);                   // table kb in buffer 0
     __syncthreads();
 
     for (int k = kb; k < ke; ++k) {
+      const unsigned t = (unsigned)(k - kb);
       XRows xn;
       Rows rows;
       load_x(xn, xt, p.Rpad, min(k + 1, klast), r0);
       load_rows(rows, lut, wnext, lane);
-      const uint2 wn2 = load_w8(wrow, p.Opad, min(k + 2, klast));
-      use_table<SIGNED>(acc, smem, xc, gx);
+      const unsigned wn3 = load_w8(wrow, p.Opad, min(k + 3, klast), lane);
       __builtin_amdgcn_sched_barrier(0);
-      write_table(smem, rows, wbase);
+      use_table<SIGNED>(acc, smem, xc, (unsigned)(g << 4) | ((t & 3u) * ETAB));
+      __builtin_amdgcn_sched_barrier(0);
+      write_table(smem, rows, wbase, ((t + 2u) & 3u) * ETAB);
       xc = xn;
-      wnext = wn2;
-#pragma unroll
-      for (int i = 0; i < IPT; ++i) wbase[i] ^= ETAB;
-      gx ^= BUFX;
-      __syncthreads();
+      wnext = wn3;
+      if (t & 1u) __syncthreads();
     }
   }
 
-  // ---- epilogue: stage through LDS (channel-major), write rows coalesced.
-  __syncthreads();
-  const bool partial = p.splits > 1;
-  for (int round = 0; round < NWAVE; ++round) {
-    const bool mine = wave == round;
-    if (mine) {
-      // row j of row group rg is staged at position rg + 8*j (bank-spread)
-      int* stage = (int*)smem;
-#pragma unroll
-      for (int j = 0; j < RPL; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          stage[(g * 8 + e) * STAGE_S + rg + 8 * j] = acc[j][e];
-    }
-    __syncthreads();
-    if (mine) {
-      const int* stage = (const int*)smem;
-      const int rw0 = rtile0 + wave * RPW;   // first row of this wave
-#pragma unroll
-      for (int h = 0; h < RPW / 64; ++h) {
-        const int a = lane + 64 * h;             // row within the wave tile
-        const int r = rw0 + a;
-        const int n = r / p.L;
-        const int l = r - n * p.L;
-        const int q = (a / RPL) + 8 * (a % RPL); // staged position of row a
-        const long long ybase = (long long)n * p.O * p.L + l;
-        for (int oo = 0; oo < OT && r < p.R; ++oo) {
-          const int o = o0 + oo;
-          if (o >= p.O) break;
-          const int v = stage[oo * STAGE_S + q];
-          const long long yi = ybase + (long long)o * p.L;
-          if (partial) {
-            ((int*)p.y)[(long long)s * p.split_stride + yi] = v;
-          } else if (p.out_kind == ATX_OUT_I32) {
-            ((int*)p.y)[yi] = v;
-          } else if (p.out_kind == ATX_OUT_F32) {
-            ((float*)p.y)[yi] = (float)v;
-          } else {
-            const float sc = p.sx[0] * p.sw[o];
-            const float t = (float)v * sc;
-            ((float*)p.y)[yi] = p.bias ? p.bias[o] + t : t;
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
+  // ---- epilogue: registers -> HBM, every wave at once (no LDS staging).
+  const int oc = o0 + g * 8;
+  if (p.splits > 1)
+    store_tile<ATX_OUT_I32>(p, (int*)p.y + (long long)s * p.split_stride, acc, r0, oc);
+  else if (p.out_kind == ATX_OUT_I32)
+    store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
+  else if (p.out_kind == ATX_OUT_F32)
+    store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
+  else
+    store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
 }
 
 // Split-K reduction: exact int64 sum of int32 partials, then the epilogue.
@@ -420,20 +472,39 @@ __global__ void lut_gemm_f32_kernel(const GemmParams p) {
 // Split plan shared by the workspace query and the launch.
 struct Plan { int tiles_r, tiles_o, splits, k_chunk; };
 
+// Compute units of a full MI355X (one resident workgroup each: the kernel's
+// 8 waves hold 2 waves per SIMD at its register budget).  A constant, not a
+// device query, so the workspace query and the launch always agree.
+constexpr int PLAN_CUS = 256;
+
+// Split-K count by a cost model in units of one k-step of one workgroup:
+//   ceil(tiles*S / CUs) rounds x (ceil(K/S) + 3 fixed steps per workgroup)
+//   + for S > 1: 4 steps for the reduce launch and S x (R*O / 600000) steps
+//     for writing and re-reading one int32 partial slice (8 bytes per
+//     output at ~4 TB/s against ~1.2 us per k-step).
+// S is at least ceil(K / kmax), the exact-int32 bound of one pass, and the
+// smallest S among equal costs wins.
 static Plan make_plan(int N, int K, int L, int O, int kmax) {
   Plan pl;
   const long long R = (long long)N * L;
   pl.tiles_r = (int)cdiv(R, RT);
   pl.tiles_o = (int)cdiv(O, OT);
+  if (K <= 0) { pl.splits = 1; pl.k_chunk = 1; return pl; }
   const long long tiles = (long long)pl.tiles_r * pl.tiles_o;
-  // Aim for >= 2 workgroups per CU (256 CUs) when K is long enough that each
-  // split still runs >= 64 k-steps; always split when K exceeds the exact
-  // int32 bound of one pass.
-  int splits = 1;
-  while (tiles * splits < 512 && K / (splits * 2) >= 64) splits *= 2;
-  while (cdiv(K, splits) > kmax) splits *= 2;
-  pl.k_chunk = K > 0 ? (int)cdiv(K, splits) : 1;
-  pl.splits = K > 0 ? (int)cdiv(K, pl.k_chunk) : 1;
+  const long long cus = PLAN_CUS;
+  const int smin = (int)cdiv(K, kmax);
+  const double slice = (double)R * O / 600000.0;
+  int best = smin;
+  double best_cost = 0.0;
+  for (int S = smin; S <= std::max(smin, 64); ++S) {
+    const long long kc = cdiv(K, S);
+    if (S > smin && kc < 16) break;
+    const double cost = (double)cdiv(tiles * S, cus) * (double)(kc + 3) +
+                        (S > 1 ? 4.0 + S * slice : 0.0);
+    if (S == smin || cost < best_cost) { best = S; best_cost = cost; }
+  }
+  pl.k_chunk = (int)cdiv(K, best);
+  pl.splits = (int)cdiv(K, pl.k_chunk);
   return pl;
 }
 

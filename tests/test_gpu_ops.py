@@ -170,6 +170,43 @@ def test_lut_conv_forward_matches_oracle(geom):
     assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
 
 
+# (N, C, H, W, geometry): K = C*KH*KW of 8 or 27 runs in one pass; 72, 392
+# and 1152 run split-K (int32 partials + reduce); L = 256 and 64 store
+# four-row vectors, the others row by row.
+DEQ_CASES = [(3, 8, 15, 14, GEOMS[0]), (2, 8, 16, 16, GEOMS[0]), (2, 8, 16, 16, GEOMS[2]),
+             (2, 8, 17, 17, GEOMS[1]), (4, 3, 16, 16, GEOMS[0]), (1, 128, 8, 8, GEOMS[0])]
+
+
+@pytest.mark.parametrize("case", DEQ_CASES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_dequant_and_int32_epilogues(case, with_bias):
+    N, C, H, W, (k, s, p, d) = case
+    r = gen(zlib.crc32(repr((case, with_bias)).encode()))
+    img = r.integers(-127, 128, (N, C, H, W)).astype(np.float32)
+    Oc = 70
+    w = r.integers(-127, 128, (Oc, C * k[0] * k[1])).astype(np.float32)
+    lut = luts(4)["perturbed"]
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    xi = O.im2col_index(O.image_index(img, 128), k, s, p, d, 128)
+    want_i = O.lut_gemm_i64(xi, (w + 128).astype(np.uint8), lut)
+    sx = np.array([0.0173], np.float32)
+    sw = r.uniform(1e-3, 5e-2, Oc).astype(np.float32)
+    bias = r.standard_normal(Oc).astype(np.float32) if with_bias else None
+    y, _ = ops.conv_forward(t(img), t(w), t(lut, torch.float32), g, 128, 128,
+                            out_kind=ops.L.ATX_OUT_DEQUANT, sx=t(sx), sw=t(sw),
+                            bias=None if bias is None else t(bias))
+    # the epilogue's fp32 sequence: sc = sx * sw[o]; t = float(v) * sc; bias + t
+    sc = (sx[0] * sw)[None, :, None]
+    want = want_i.astype(np.float32) * sc
+    if bias is not None:
+        want = bias[None, :, None] + want
+    assert np.array_equal(y.cpu().numpy(), want)
+    yi, _ = ops.conv_forward(t(img), t(w), t(lut, torch.float32), g, 128, 128,
+                             out_kind=ops.L.ATX_OUT_I32)
+    assert yi.dtype == torch.int32
+    assert np.array_equal(yi.cpu().numpy().astype(np.int64), want_i)
+
+
 def test_lut_map_and_pad():
     r = gen(13)
     table = r.standard_normal(256).astype(np.float32)
