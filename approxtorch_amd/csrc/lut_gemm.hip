@@ -283,6 +283,15 @@ __device__ __forceinline__ void put_rows(const GemmParams& p, void* y, long long
   }
 }
 
+// Smallest entry of the waves' progress slots (wave-uniform).
+__device__ __forceinline__ unsigned min_progress(const unsigned* prog) {
+  static_assert(NWAVE == 8, "two 16-byte reads cover the slots");
+  const uint4 a = *(const uint4*)prog;
+  const uint4 b = *(const uint4*)(prog + 4);
+  const unsigned m = min(min(min(a.x, a.y), min(a.z, a.w)), min(min(b.x, b.y), min(b.z, b.w)));
+  return __builtin_amdgcn_readfirstlane(m);
+}
+
 // Writes the lane's accumulators: channel o0 + e, rows r + 32h + m of quad
 // h (r = first row of quad 0).  Rows beyond R and channels beyond O are
 // dropped.  With L % 4 == 0 a quad never straddles two images and is one
@@ -330,6 +339,7 @@ template <bool SIGNED>
 __global__ void __launch_bounds__(NT, 1)
 lut_gemm_kernel(const GemmParams p) {
   __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
+  __shared__ __align__(16) unsigned progress[NWAVE];   // k-steps finished per wave
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -365,21 +375,34 @@ lut_gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0;
 
+  if (tid < NWAVE) progress[tid] = 0u;   // ordered before use by the prologue barrier
+
   if (kb < ke) {
-    // Four LDS buffers, table k in buffer k % 4 (counting k from kb), and a
-    // barrier after every second step.  Step k issues the loads for row
-    // offsets k+1, LUT rows of table k+2 and weight indices of k+3 (indices
-    // clamped to the range, so every load is unconditional), accumulates
-    // from table k and then writes table k+2.  Table k+2 overwrites table
-    // k-2, whose last reads (step k-2) precede the barrier closing the pair
-    // before step k; every table is written at least one barrier before its
-    // reads.  Halving the barriers lets waves drift apart within a pair.
-    // Scheduling fences keep the loads ahead of the accumulation and the
+    // Four LDS buffers, table t = k - kb in buffer t % 4.  Step t issues the
+    // loads for row offsets t+1, LUT rows of table t+2 and weight indices of
+    // t+3 (indices clamped to the range, so every load is unconditional),
+    // accumulates from table t, writes table t+2 and records t+1 steps done
+    // in its progress slot.
+    //
+    // Split barrier: instead of a workgroup barrier per step, a wave starts
+    // step t once every wave has finished step t-2 (min over the progress
+    // slots >= t-1).  That covers both hazards of the step: table t was
+    // written in step t-2, and table t+2 reuses the buffer of table t-2,
+    // last read in step t-2.  Waves may drift one step apart, which keeps
+    // the VALU busy while other waves wait on LDS.  Buffers in use at once:
+    // a slow wave at step t-1 holds tables t-1 and t+1, a fast wave at step
+    // t tables t and t+2.  A wave's LDS operations execute in program
+    // order, so its progress store lands after its table writes and its
+    // reads of table t-2, and a wave that has seen the store issues its
+    // table reads after that.  Every wave waits only for steps that it has
+    // itself already finished, so the waits always end.  Compiler fences
+    // keep the LDS accesses and the progress slots in program order;
+    // scheduling fences keep the loads ahead of the accumulation and the
     // table write (which waits for the LUT rows) behind it, so the loads
     // overlap a whole step.
     const int klast = ke - 1;
     XRows xc;
-    unsigned wnext;                                         // indices of table k+2
+    unsigned wnext;                                         // indices of table t+2
     {
       const unsigned w0 = load_w8(wrow, p.Opad, kb, lane);
       const unsigned w1 = load_w8(wrow, p.Opad, min(kb + 1, klast), lane);
@@ -401,12 +424,24 @@ lut_gemm_kernel(const GemmParams p) {
       load_rows(rows, lut, wnext, lane);
       const unsigned wn3 = load_w8(wrow, p.Opad, min(k + 3, klast), lane);
       __builtin_amdgcn_sched_barrier(0);
+      const unsigned need = t ? t - 1u : 0u;
+      asm volatile("" ::: "memory");
+      unsigned seen = min_progress(progress);
+      while (seen < need) {
+        __builtin_amdgcn_s_sleep(1);
+        asm volatile("" ::: "memory");
+        seen = min_progress(progress);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
       use_table<SIGNED>(acc, smem, xc, (unsigned)(g << 4) | ((t & 3u) * ETAB));
       __builtin_amdgcn_sched_barrier(0);
       write_table(smem, rows, wbase, ((t + 2u) & 3u) * ETAB);
+      asm volatile("" ::: "memory");
+      if (lane == 0) progress[wave] = t + 1u;
+      asm volatile("" ::: "memory");
       xc = xn;
       wnext = wn3;
-      if (t & 1u) __syncthreads();
     }
   }
 
