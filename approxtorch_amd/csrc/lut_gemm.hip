@@ -41,12 +41,16 @@
 #include "atx_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace atx {
 
 constexpr int RT = ATX_ROW_TILE;   // rows per workgroup
 constexpr int OT = ATX_COL_TILE;   // channels per workgroup
-constexpr int RPL = 16;            // rows per lane
+#ifndef ATX_LUT_RPL
+#define ATX_LUT_RPL 16
+#endif
+constexpr int RPL = ATX_LUT_RPL;   // rows per lane (16: 8 waves, 8: 16 waves)
 constexpr int RPW = 8 * RPL;       // rows per wave (8 row groups)
 constexpr int NWAVE = RT / RPW;    // waves per workgroup
 constexpr int NT = 64 * NWAVE;     // threads per workgroup
@@ -180,45 +184,56 @@ struct Rows { unsigned d[IPT][8]; };
 // Row offsets of the lane's quads: v[h] = rows 32h + 4rg + 0..3, two per dword.
 struct XRows { uint2 v[NQ]; };
 
-// Eight weight indices (channels o0 + 8*og .. +7) at k.  Lane parity picks
-// the dword (indices 0-3 / 4-7) so the load is a vector load: a scalar load
-// would share the LDS wait counter and, completing out of order, force every
-// LDS wait of the step to drain it.
-__device__ __forceinline__ unsigned load_w8(const uint8_t* __restrict__ wrow, int Opad,
-                                            int k, int lane) {
-  return ((const unsigned*)(wrow + (long long)k * Opad))[lane & 1];
+// Raw buffer descriptor (word 3 of the gfx9-family descriptor: 32-bit
+// elements, no swizzle) over `bytes` bytes at a wave-uniform base.  Buffer
+// loads take the per-step offsets in scalar registers, so the loads below
+// cost no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
+                                           0x00020000);
+}
+
+// Eight weight indices (channels o0 + 8*og .. +7) at k, wcol = &wt[k][o0 +
+// 8*og].  Lane parity picks the dword (indices 0-3 / 4-7) so the load is a
+// vector load: a scalar load would share the LDS wait counter and,
+// completing out of order, force every LDS wait of the step to drain it.
+__device__ __forceinline__ unsigned load_w8(const uint8_t* wcol, int lane) {
+  return __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(wcol, 8), (lane & 1) * 4, 0, 0);
 }
 
 // Dword at entries (v0, v0+1) of LUT16T row w_j for every channel j of the
-// group; item i covers v0 = 2*lane + 128*i.  Row bases are wave-uniform
-// (read from lanes 0 and 1 of the weight-index register).
-__device__ __forceinline__ void load_rows(Rows& r, const uint16_t* __restrict__ lut,
-                                          unsigned wv, int lane) {
+// group; item i covers v0 = 2*lane + 128*i + sbase/2.  Row offsets are
+// wave-uniform (read from lanes 0 and 1 of the weight-index register).
+__device__ __forceinline__ void load_rows(Rows& r, __amdgpu_buffer_rsrc_t lut, unsigned wv,
+                                          int lane, int sbase) {
   const unsigned w_lo = __builtin_amdgcn_readlane(wv, 0);
   const unsigned w_hi = __builtin_amdgcn_readlane(wv, 1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const unsigned wj = ((j < 4 ? w_lo : w_hi) >> (8 * (j & 3))) & 255u;
-    const unsigned* row = (const unsigned*)(lut + wj * 256u);
 #pragma unroll
-    for (int i = 0; i < IPT; ++i) r.d[i][j] = row[lane + 64 * i];
+    for (int i = 0; i < IPT; ++i)
+      r.d[i][j] = __builtin_amdgcn_raw_buffer_load_b32(lut, lane * 4 + 256 * i,
+                                                        (int)(wj * 512u) + sbase, 0);
   }
 }
 
-// r0 = first row of the lane's first quad (8-byte aligned: Rpad % 1024 == 0).
-__device__ __forceinline__ void load_x(XRows& x, const uint16_t* __restrict__ xt,
-                                       int Rpad, int k, int r0) {
-  const uint16_t* xp = xt + (long long)k * Rpad + r0;
+// Row offsets of the lane's quads at k from the tile's row-offset column
+// (xcol = &xt[k][first row of the tile]); xoff = byte offset of the lane's
+// first quad within the tile.
+__device__ __forceinline__ void load_x(XRows& x, const uint16_t* xcol, int xoff) {
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(xcol, RT * 2);
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) x.v[h] = *(const uint2*)(xp + 8 * RQ * h);
+  for (int h = 0; h < NQ; ++h)
+    x.v[h] = __builtin_bit_cast(
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, xoff + 16 * RQ * h, 0, 0));
 }
 
 // Writes this lane's two 16-byte chunks per build item (rows v0 and v0+1,
 // channels 8*og .. 8*og+7); wbase holds the chunk address of row v0 within
-// a table, buf the byte offset of the LDS buffer.
+// the table at smem.
 __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
-                                            const int (&wbase)[IPT], unsigned buf) {
-  smem += buf;
+                                            const int (&wbase)[IPT]) {
 #pragma unroll
   for (int it = 0; it < IPT; ++it) {
     const unsigned* d = r.d[it];
@@ -237,22 +252,28 @@ __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
 }
 
 // Accumulates one table for this lane's RPL rows.  x holds the rows'
-// offsets (two per dword); gx XORs in the lane's channel chunk (bits 4-6) and
-// the LDS buffer (bits 15-16; offsets are below 32768).
+// offsets (two per dword, below 32768); gx XORs in the lane's channel chunk
+// (bits 4-6) and possibly bit 16 of the table's LDS address.
 template <bool SIGNED>
 __device__ __forceinline__ void use_table(int (&acc)[RPL][8], const unsigned char* smem,
                                           const XRows& x, unsigned gx) {
+  // Reads per batch: 8 (two quads) at 2 waves per SIMD, 4 (one quad) at 4
+  // waves per SIMD, where the register budget is half as large.
+  constexpr int QB = RPL >= 16 ? 2 : 1;
 #pragma unroll
-  for (int hh = 0; hh < NQ; hh += 2) {
-    const unsigned xd[4] = {x.v[hh].x, x.v[hh].y, x.v[hh + 1].x, x.v[hh + 1].y};
-    uint4 e[8];
+  for (int hh = 0; hh < NQ; hh += QB) {
+    unsigned xd[2 * QB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int q = 0; q < QB; ++q) { xd[2 * q] = x.v[hh + q].x; xd[2 * q + 1] = x.v[hh + q].y; }
+    uint4 e[4 * QB];
+#pragma unroll
+    for (int j = 0; j < 2 * QB; ++j) {
       e[2 * j] = *(const uint4*)(smem + ((xd[j] & 0xffffu) ^ gx));
       e[2 * j + 1] = *(const uint4*)(smem + ((xd[j] >> 16) ^ gx));
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) add8<SIGNED>(acc[RQ * hh + j], e[j]);
+    for (int j = 0; j < 4 * QB; ++j) add8<SIGNED>(acc[RQ * hh + j], e[j]);
+    if constexpr (QB == 1) __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -285,10 +306,13 @@ __device__ __forceinline__ void put_rows(const GemmParams& p, void* y, long long
 
 // Smallest entry of the waves' progress slots (wave-uniform).
 __device__ __forceinline__ unsigned min_progress(const unsigned* prog) {
-  static_assert(NWAVE == 8, "two 16-byte reads cover the slots");
-  const uint4 a = *(const uint4*)prog;
-  const uint4 b = *(const uint4*)(prog + 4);
-  const unsigned m = min(min(min(a.x, a.y), min(a.z, a.w)), min(min(b.x, b.y), min(b.z, b.w)));
+  static_assert(NWAVE % 4 == 0, "16-byte reads cover the slots");
+  unsigned m = ~0u;
+#pragma unroll
+  for (int i = 0; i < NWAVE / 4; ++i) {
+    const uint4 a = *(const uint4*)(prog + 4 * i);
+    m = min(m, min(min(a.x, a.y), min(a.z, a.w)));
+  }
   return __builtin_amdgcn_readfirstlane(m);
 }
 
@@ -340,6 +364,7 @@ __global__ void __launch_bounds__(NT, 1)
 lut_gemm_kernel(const GemmParams p) {
   __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
   __shared__ __align__(16) unsigned progress[NWAVE];   // k-steps finished per wave
+  __shared__ unsigned pscratch[NT];    // branch-free progress store: other lanes' sink
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -355,19 +380,33 @@ lut_gemm_kernel(const GemmParams p) {
   const int kb = s * p.k_chunk;
   const int ke = min(p.K, kb + p.k_chunk);
 
-  // Table-build mapping: wave w builds channel group og = w; lane t writes
-  // rows v0 = 2t + 128i and v0+1 (item i), whose chunk og sits at position
-  // og ^ ((v0 >> 1) & 7) = og ^ (t & 7).
-  static_assert(NWAVE == 8 && IPT == 2, "one wave per channel group, 256 rows");
-  const int og = __builtin_amdgcn_readfirstlane(wave);
-  int wbase[IPT];
+  // Table-build mapping: wave w builds channel group og = w % 8 for rows
+  // 128 hw .. 128 hw + 128 IPT - 1 (hw = w / 8); lane t writes rows
+  // v0 = 2t + 128(i + hw) and v0+1 (item i), whose chunk og sits at position
+  // og ^ ((v0 >> 1) & 7) = og ^ (t & 7).  Tables 0/1 and 2/3 of the four
+  // LDS buffers differ by an immediate offset (0 / ETAB) from the base
+  // addresses wlo / whi (whi = wlo + 2 * ETAB).
+  static_assert((NWAVE == 8 && IPT == 2) || (NWAVE == 16 && IPT == 1),
+                "eight channel groups x 256 rows per table");
+  static_assert(NBUF == 4 && 2 * ETAB == 65536, "buffer pairs split at bit 16");
+  const int og = __builtin_amdgcn_readfirstlane(wave & 7);
+  const int hw = __builtin_amdgcn_readfirstlane(wave >> 3);
+  int wlo[IPT], whi[IPT];
 #pragma unroll
-  for (int i = 0; i < IPT; ++i)
-    wbase[i] = (2 * lane + 128 * i) * 128 + ((og ^ (lane & 7)) << 4);
+  for (int i = 0; i < IPT; ++i) {
+    wlo[i] = (2 * lane + 128 * (i + hw)) * 128 + ((og ^ (lane & 7)) << 4);
+    whi[i] = wlo[i] + 2 * ETAB;
+  }
+  const unsigned gxa = (unsigned)(g << 4);              // reads of buffers 0, 1
+  const unsigned gxb = gxa | (unsigned)(2 * ETAB);      // reads of buffers 2, 3
 
-  const uint16_t* __restrict__ xt = p.xt;
-  const uint8_t* __restrict__ wrow = p.wt + o0 + og * 8;
-  const uint16_t* __restrict__ lut = p.lut16t;
+  const uint16_t* __restrict__ xtile = p.xt + (long long)tr * RT;
+  const int xoff = (wave * RPW + rg * RQ) * 2;         // lane's first quad, bytes
+  const uint8_t* __restrict__ wcol = p.wt + o0 + og * 8;
+  const __amdgpu_buffer_rsrc_t lutr = buffer_rsrc(p.lut16t, 256 * 256 * 2);
+  // Zero-length view of the image: its loads are out of range and return 0,
+  // which builds an all-zero table for the steps past the chunk's end.
+  const __amdgpu_buffer_rsrc_t lutz = buffer_rsrc(p.lut16t, 0);
 
   int acc[RPL][8];
 #pragma unroll
@@ -376,13 +415,16 @@ lut_gemm_kernel(const GemmParams p) {
     for (int e = 0; e < 8; ++e) acc[j][e] = 0;
 
   if (tid < NWAVE) progress[tid] = 0u;   // ordered before use by the prologue barrier
+  unsigned* const pslot = lane == 0 ? &progress[wave] : &pscratch[tid];
 
   if (kb < ke) {
     // Four LDS buffers, table t = k - kb in buffer t % 4.  Step t issues the
     // loads for row offsets t+1, LUT rows of table t+2 and weight indices of
     // t+3 (indices clamped to the range, so every load is unconditional),
     // accumulates from table t, writes table t+2 and records t+1 steps done
-    // in its progress slot.
+    // in its progress slot.  The loop is unrolled over the four buffers so
+    // every buffer offset is an immediate and the row-offset registers
+    // alternate between two sets without copies.
     //
     // Split barrier: instead of a workgroup barrier per step, a wave starts
     // step t once every wave has finished step t-2 (min over the progress
@@ -401,28 +443,32 @@ lut_gemm_kernel(const GemmParams p) {
     // table write (which waits for the LUT rows) behind it, so the loads
     // overlap a whole step.
     const int klast = ke - 1;
-    XRows xc;
+    const long long xstride = p.Rpad, wstride = p.Opad;
+    XRows xa, xb;
     unsigned wnext;                                         // indices of table t+2
     {
-      const unsigned w0 = load_w8(wrow, p.Opad, kb, lane);
-      const unsigned w1 = load_w8(wrow, p.Opad, min(kb + 1, klast), lane);
-      wnext = load_w8(wrow, p.Opad, min(kb + 2, klast), lane);
+      const unsigned w0 = load_w8(wcol + kb * wstride, lane);
+      const unsigned w1 = load_w8(wcol + min(kb + 1, klast) * wstride, lane);
+      wnext = load_w8(wcol + min(kb + 2, klast) * wstride, lane);
       Rows rows;
-      load_rows(rows, lut, w0, lane);
-      load_x(xc, xt, p.Rpad, kb, r0);
-      write_table(smem, rows, wbase, 0);                    // table kb   -> buffer 0
-      load_rows(rows, lut, w1, lane);
-      write_table(smem, rows, wbase, ETAB);                 // table kb+1 -> buffer 1
+      load_rows(rows, lutr, w0, lane, 256 * hw);
+      load_x(xa, xtile + kb * xstride, xoff);
+      write_table(smem, rows, wlo);                         // table kb   -> buffer 0
+      load_rows(rows, ke - kb > 1 ? lutr : lutz, w1, lane, 256 * hw);
+      write_table(smem + ETAB, rows, wlo);                  // table kb+1 -> buffer 1
     }
     __syncthreads();
 
-    for (int k = kb; k < ke; ++k) {
-      const unsigned t = (unsigned)(k - kb);
-      XRows xn;
+    const unsigned n = (unsigned)(ke - kb);
+    auto step = [&](auto bufc, unsigned t, XRows& xcur, XRows& xnext)
+        __attribute__((always_inline)) {
+      constexpr int B = decltype(bufc)::value;              // buffer of table t
+      constexpr int BW = (B + 2) & 3;                       // buffer of table t+2
+      const int k = kb + (int)t;
+      load_x(xnext, xtile + min(k + 1, klast) * xstride, xoff);
       Rows rows;
-      load_x(xn, xt, p.Rpad, min(k + 1, klast), r0);
-      load_rows(rows, lut, wnext, lane);
-      const unsigned wn3 = load_w8(wrow, p.Opad, min(k + 3, klast), lane);
+      load_rows(rows, t + 2u < n ? lutr : lutz, wnext, lane, 256 * hw);
+      const unsigned wn3 = load_w8(wcol + min(k + 3, klast) * wstride, lane);
       __builtin_amdgcn_sched_barrier(0);
       const unsigned need = t ? t - 1u : 0u;
       asm volatile("" ::: "memory");
@@ -434,14 +480,32 @@ lut_gemm_kernel(const GemmParams p) {
       }
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
-      use_table<SIGNED>(acc, smem, xc, (unsigned)(g << 4) | ((t & 3u) * ETAB));
+      use_table<SIGNED>(acc, smem + (B & 1) * ETAB, xcur, (B & 2) ? gxb : gxa);
+      // Pin the adds here: left free, the compiler sinks them into later
+      // steps, past the table write that waits for this step's loads.
+#pragma unroll
+      for (int j = 0; j < RPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[j][e]));
       __builtin_amdgcn_sched_barrier(0);
-      write_table(smem, rows, wbase, ((t + 2u) & 3u) * ETAB);
+      write_table(smem + (BW & 1) * ETAB, rows, (BW & 2) ? whi : wlo);
       asm volatile("" ::: "memory");
-      if (lane == 0) progress[wave] = t + 1u;
+      *pslot = t + 1u;          // lane 0: progress[wave]; others: scratch slots
       asm volatile("" ::: "memory");
-      xc = xn;
       wnext = wn3;
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    using B3 = std::integral_constant<int, 3>;
+    // Whole groups of four steps; the up to three steps past the chunk's
+    // end accumulate all-zero tables (built from lutz), so the accumulation
+    // needs no branch and every wave runs the same steps.
+    for (unsigned t = 0; t < n; t += 4u) {
+      step(B0{}, t, xa, xb);
+      step(B1{}, t + 1u, xb, xa);
+      step(B2{}, t + 2u, xa, xb);
+      step(B3{}, t + 3u, xb, xa);
     }
   }
 

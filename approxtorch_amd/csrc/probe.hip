@@ -1,15 +1,29 @@
-// LDS throughput probe: measures the roofline denominator of the LUT GEMM
-// (LDS bytes per clock per CU) and the bank structure its layout relies on.
-// Each workgroup fills 64 KiB of LDS; every lane issues `iters` x 8 reads.
-// Addresses come from a per-group hash (no cross-lane operations, which
-// would themselves use the LDS pipe):
-//   mode 0  ds_read_b128, each 8-lane group reads one random 128-byte row
-//   mode 1  ds_read_b128, each wave reads 1 KiB contiguous
-//   mode 2  as mode 0, but the row's parity equals the 8-lane group's parity
-//   mode 3  ds_read_b128, each 16-lane group reads one random 256-byte row
-//   mode 4  ds_read_u16 at independent random addresses (a plain LUT gather)
-//   mode 5  ds_write_b32, each 32-lane half-wave writes one random 128-byte row
-// The sum of what was read is stored so nothing is optimized away.
+// LDS throughput probe: the roofline denominator of the LUT GEMM (LDS bytes
+// per clock per CU) and the bank structure its table layout relies on.
+//
+// Each workgroup fills 64 KiB of LDS (two workgroups fit on a CU, 16 waves).
+// Every lane holds eight precomputed byte addresses; each iteration XORs
+// them with a wave-uniform mask that moves whole rows, so the pattern's
+// bank structure is the same in every iteration, and issues eight 16-byte
+// accesses.  A read costs three VALU operations (address XOR and two
+// three-input adds folding the data into one register), a write one, which
+// keeps the VALU well below the LDS time even at 256 bytes per clock.
+//   mode 0  read:  each 8-lane group reads one random 128-byte row
+//   mode 1  read:  each wave reads 1 KiB contiguous (lane * 16)
+//   mode 2  read:  as mode 0, with the row's parity equal to the group's
+//   mode 3  read:  each 16-lane group reads one random 256-byte row
+//   mode 4  read:  all lanes of a wave read the same random 128-byte row
+//   mode 5  write: the table-build pattern: lane t writes 16 bytes at row
+//                  2t + 128(u & 1), chunk position ((w + u/2) ^ t) & 7
+//   mode 6  write: each wave writes 1 KiB contiguous (lane * 16)
+//   mode 7  write: 8-byte accesses, each wave writes 512 B contiguous
+//   mode 8  write: 4-byte accesses, each wave writes 256 B contiguous
+//   mode 9  read:  each 4-lane group reads a random 64-byte row in quarter
+//                  (group % 4) of a 256-byte line (quarters rotate by group)
+//   mode 10 read:  as mode 9 with a random quarter per group
+// The sum of everything read is stored so nothing is optimized away.
+// Bytes moved per launch = blocks * 512 * iters * 8 * (16, or 8 / 4 for
+// modes 7 / 8).
 
 #include "atx_internal.h"
 
@@ -25,43 +39,59 @@ __device__ __forceinline__ unsigned mix(unsigned s) {
 template <int MODE>
 __global__ void __launch_bounds__(512) lds_probe_kernel(int iters, unsigned* out) {
   __shared__ __align__(16) unsigned char buf[PROBE_BYTES];
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < PROBE_BYTES / 4; i += blockDim.x)
     ((unsigned*)buf)[i] = (unsigned)i * 2654435761u;
   __syncthreads();
-  const unsigned grp8 = (unsigned)(tid >> 3), grp16 = (unsigned)(tid >> 4);
+
   const unsigned key = blockIdx.x * 4099u;
+  const unsigned grp8 = (unsigned)(tid >> 3), grp16 = (unsigned)(tid >> 4);
+  unsigned a[8];
+  unsigned rowbits;          // address bits that select a row (moved by the mask)
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    if constexpr (MODE == 0 || MODE == 2) {
+      unsigned row = mix(key + grp8 * 977u + u * 7919u) & 511u;
+      if (MODE == 2) row = (row & ~1u) | (grp8 & 1u);
+      a[u] = row * 128u + (lane & 7) * 16u;
+    } else if constexpr (MODE == 1 || MODE == 6) {
+      a[u] = (mix(key + wave * 977u + u * 7919u) & 63u) * 1024u + lane * 16u;
+    } else if constexpr (MODE == 9 || MODE == 10) {
+      const unsigned grp4 = (unsigned)(tid >> 2);
+      const unsigned h = mix(key + grp4 * 977u + u * 7919u);
+      const unsigned quarter = MODE == 9 ? (grp4 & 3u) : ((h >> 9) & 3u);
+      a[u] = (h & 255u) * 256u + quarter * 64u + (lane & 3) * 16u;
+    } else if constexpr (MODE == 7 || MODE == 8) {
+      a[u] = (mix(key + wave * 977u + u * 7919u) & 63u) * 1024u + lane * (MODE == 7 ? 8u : 4u);
+    } else if constexpr (MODE == 3) {
+      a[u] = (mix(key + grp16 * 977u + u * 7919u) & 255u) * 256u + (lane & 15) * 16u;
+    } else if constexpr (MODE == 4) {
+      a[u] = (mix(key + wave * 977u + u * 7919u) & 511u) * 128u + (lane & 7) * 16u;
+    } else {
+      a[u] = (2u * lane + 128u * (u & 1)) * 128u + ((((wave + (u >> 1)) ^ lane) & 7) << 4);
+    }
+  }
+  if constexpr (MODE == 3 || MODE >= 9) rowbits = 0xff00u;
+  else if constexpr (MODE == 1 || (MODE >= 6 && MODE <= 8)) rowbits = 0xfc00u;
+  else if constexpr (MODE == 5) rowbits = 0x0100u;   // keeps rows 2t / 2t+1 pairs
+  else rowbits = 0xff80u;
+
   unsigned acc = 0;
   for (int it = 0; it < iters; ++it) {
-    // one hash per 8 reads; read u derives its address with a multiply-add
-    const unsigned h8 = mix(key + grp8 * 977u + (unsigned)it * 131071u);
-    const unsigned h16 = mix(key + grp16 * 977u + (unsigned)it * 131071u);
-    const unsigned hw = mix(key + (unsigned)(tid >> 6) * 977u + (unsigned)it * 131071u);
-    const unsigned hl = mix(key + (unsigned)tid * 977u + (unsigned)it * 131071u);
-    const unsigned hh = mix(key + (unsigned)(tid >> 5) * 977u + (unsigned)it * 131071u);
+    const unsigned m = __builtin_amdgcn_readfirstlane(((unsigned)it * 0x9e3779b9u) & rowbits);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const unsigned step = (unsigned)it * 8u + u;
-      const unsigned mul = 2u * u + 1u, add = (unsigned)u * 0x9e3779b9u;
-      if constexpr (MODE == 0 || MODE == 2) {
-        unsigned row = (h8 * mul + add) >> 23;
-        if (MODE == 2) row = (row & ~1u) | (grp8 & 1u);
-        const uint4 v = *(const uint4*)(buf + row * 128u + (lane & 7) * 16u);
-        acc += v.x ^ v.y ^ v.z ^ v.w;
-      } else if constexpr (MODE == 1) {
-        const unsigned base = ((hw * mul + add) >> 26) * 1024u;
-        const uint4 v = *(const uint4*)(buf + base + lane * 16u);
-        acc += v.x ^ v.y ^ v.z ^ v.w;
-      } else if constexpr (MODE == 3) {
-        const unsigned row = (h16 * mul + add) >> 24;
-        const uint4 v = *(const uint4*)(buf + row * 256u + (lane & 15) * 16u);
-        acc += v.x ^ v.y ^ v.z ^ v.w;
-      } else if constexpr (MODE == 4) {
-        const unsigned a = ((hl * mul + add) >> 16) & 0xfffeu;
-        acc += *(const unsigned short*)(buf + a);
+      unsigned char* p = buf + (a[u] ^ m);
+      if constexpr (MODE <= 4 || MODE >= 9) {
+        const uint4 v = *(const uint4*)p;
+        acc += v.x + v.y;       // two three-input adds per read
+        acc += v.z + v.w;
+      } else if constexpr (MODE == 7) {
+        *(uint2*)p = make_uint2(acc, (unsigned)it);
+      } else if constexpr (MODE == 8) {
+        *(unsigned*)p = acc + (unsigned)it;
       } else {
-        const unsigned row = (hh * mul + add) >> 23;
-        *(unsigned*)(buf + row * 128u + (lane & 31) * 4u) = step;
+        *(uint4*)p = make_uint4(acc, (unsigned)it, (unsigned)u, 0u);
       }
     }
   }
@@ -75,9 +105,10 @@ using namespace atx;
 extern "C" {
 
 // Launches `blocks` x 512 threads of the probe; the caller times it (events
-// on `stream`).  Bytes moved = blocks * 512 * iters * 8 * {16,16,16,16,2,4}[mode].
+// on `stream`).  Bytes moved = blocks * 512 * iters * 8 * {16, 8, 4} (modes
+// 0-6 and 9-10, 7, 8).
 int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream) {
-  ATX_REQUIRE(mode >= 0 && mode <= 5 && blocks > 0 && iters > 0 && out,
+  ATX_REQUIRE(mode >= 0 && mode <= 10 && blocks > 0 && iters > 0 && out,
               "atx_lds_probe: bad arguments");
   switch (mode) {
     case 0: hipLaunchKernelGGL(lds_probe_kernel<0>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
@@ -85,7 +116,12 @@ int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t st
     case 2: hipLaunchKernelGGL(lds_probe_kernel<2>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     case 3: hipLaunchKernelGGL(lds_probe_kernel<3>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     case 4: hipLaunchKernelGGL(lds_probe_kernel<4>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
-    default: hipLaunchKernelGGL(lds_probe_kernel<5>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 5: hipLaunchKernelGGL(lds_probe_kernel<5>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 6: hipLaunchKernelGGL(lds_probe_kernel<6>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 7: hipLaunchKernelGGL(lds_probe_kernel<7>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 8: hipLaunchKernelGGL(lds_probe_kernel<8>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 9: hipLaunchKernelGGL(lds_probe_kernel<9>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    default: hipLaunchKernelGGL(lds_probe_kernel<10>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
   }
   return check_launch("lds_probe_kernel");
 }

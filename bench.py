@@ -45,17 +45,22 @@ def parse():
 
 
 def lds_probe(torch):
-    """Measured LDS read bandwidth per pattern (GB/s over the whole GPU)."""
+    """Measured LDS throughput per access pattern (GB/s over the whole GPU)."""
     from approxtorch_amd.backend import _lib as L
-    blocks, iters = 2 * 256, 4096
+    blocks, iters = 4 * 256, 2048
     out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
     res = {}
-    for mode, nbytes, name in ((0, 16, "b128_random_128B_row_per_8_lanes"),
-                               (1, 16, "b128_contiguous_1KiB_per_wave"),
-                               (2, 16, "b128_128B_row_per_8_lanes_parity_split"),
-                               (3, 16, "b128_random_256B_row_per_16_lanes"),
-                               (4, 2, "u16_random"),
-                               (5, 4, "b32_write_random_128B_row_per_32_lanes")):
+    for mode, name in ((0, "read_b128_random_128B_row_per_8_lanes"),
+                       (1, "read_b128_contiguous_1KiB_per_wave"),
+                       (2, "read_b128_128B_row_per_8_lanes_parity_split"),
+                       (3, "read_b128_random_256B_row_per_16_lanes"),
+                       (4, "read_b128_broadcast_128B_row_per_wave"),
+                       (5, "write_b128_table_build_pattern"),
+                       (6, "write_b128_contiguous_1KiB_per_wave"),
+                       (7, "write_b64_contiguous_512B_per_wave"),
+                       (8, "write_b32_contiguous_256B_per_wave"),
+                       (9, "read_b128_64B_row_per_4_lanes_rotated_quarters"),
+                       (10, "read_b128_64B_row_per_4_lanes_random_quarters")):
         L.call("atx_lds_probe", mode, blocks, 8, out.data_ptr(), L.stream_of(out))
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -64,6 +69,7 @@ def lds_probe(torch):
         e.record()
         torch.cuda.synchronize()
         ms = s.elapsed_time(e)
+        nbytes = {7: 8, 8: 4}.get(mode, 16)
         res[name] = round(blocks * 512 * iters * 8 * nbytes / (ms * 1e-3) / 1e9, 1)
     return res
 
