@@ -18,7 +18,7 @@ c_int, c_ll, c_float, c_vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ct
 
 ATX_LUT_I16, ATX_LUT_U16, ATX_LUT_F32 = 0, 1, 2
 ATX_OUT_F32, ATX_OUT_I32, ATX_OUT_DEQUANT = 0, 1, 2
-ROW_TILE, COL_TILE = 1024, 64
+ROW_TILE, COL_TILE = 2048, 32
 
 
 class ConvGeom(ctypes.Structure):
@@ -135,3 +135,8 @@ def geom(N, C, H, W, KH, KW, SH, SW, PH, PW, DH, DW):
 
 def round_up(v, m):
     return (v + m - 1) // m * m
+
+
+def operand_rows(K):
+    """k-rows of the LUT GEMM's row-offset operand: K rounded up to a quad."""
+    return round_up(K, 4)

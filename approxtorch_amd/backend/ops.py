@@ -119,7 +119,7 @@ def _bgemm_save(x, w, lut, offset, name):
     dev, s = xc.device, L.stream_of(xc)
     R = N * Lc
     Rpad = L.round_up(max(R, 1), L.ROW_TILE)
-    xt = torch.empty((K, Rpad), dtype=torch.int16, device=dev)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
     if xc.dtype == torch.uint8:
         xq = xc
         L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, s)
@@ -171,7 +171,7 @@ def lut_gemm_i32(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
     N, K, Lc = xc.shape
     O = wc.size(0)
     Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
-    xt = torch.empty((K, Rpad), dtype=torch.int16, device=xc.device)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=xc.device)
     L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, L.stream_of(xc))
     _, wt, Opad = _pack_w(wc, 0)
     y = torch.empty((N, O, Lc), dtype=torch.int32, device=xc.device)
@@ -218,7 +218,7 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
         raise RuntimeError(f"weight has {w_idx_or_val.size(1)} taps, geometry needs {K}")
     dev = imgc.device
     Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
-    xt = torch.empty((K, Rpad), dtype=torch.int16, device=dev)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
     L.call("atx_im2col_rows", L.ptr(imgc), _dtype_code(imgc, offset == 0), g, pad_index,
            L.ptr(pad_dev), L.ptr(xt), Rpad, L.stream_of(imgc))
     wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)

@@ -26,11 +26,25 @@ inline int elem_grid(long long n, int threads, int cap = 8192) {
   return (int)(b < cap ? b : cap);
 }
 
-// Byte offset of row v of a LUT GEMM table (128-byte rows of 8 16-byte
-// channel chunks; chunk g of row v sits at position g ^ ((v >> 1) & 7)).
+// Byte offset of row v in the LUT GEMM's LDS tables (256-byte lines holding
+// row v of four tables; within a table's 64-byte quarter, chunk g of row v
+// sits at position g ^ ((v >> 1) & 3)).
 __device__ __forceinline__ unsigned row_offset(unsigned v) {
-  return v * 128u + (((v >> 1) & 7u) << 4);
+  return v * 256u + (((v >> 1) & 3u) << 4);
 }
+
+// Row-offset operand layout of the LUT GEMM: the k-rows come in quads
+// (Kpad = K rounded up to 4 rows); slot s of a quad holds, for row r, tap
+// k = (s & ~3) | (((r >> 2) + s) & 3), so that the GEMM's row group reading
+// quarter ((r >> 2) + s) & 3 at sub-step s finds its tap in slot s.  Taps at
+// or beyond K hold offset 0.
+__host__ __device__ __forceinline__ int operand_tap(int slot, int r) {
+  return (slot & ~3) | (((r >> 2) + slot) & 3);
+}
+__host__ __device__ __forceinline__ int operand_slot(int k, int r) {
+  return (k & ~3) | ((k - (r >> 2)) & 3);
+}
+__host__ __device__ __forceinline__ int operand_rows(int K) { return (K + 3) & ~3; }
 
 // clamp(rint(v) + offset, 0, 255) with round-half-even; NaN maps to `offset`
 // clamped (the reference's float->int conversion of NaN is unspecified).

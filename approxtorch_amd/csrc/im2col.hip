@@ -23,7 +23,9 @@ template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int o
   return quant_index(v, offset);
 }
 
-// xt[k][r] = row_offset(index of tap k at output position r); r >= N*L -> 0.
+// xt[slot][r] = row_offset(index of tap operand_tap(slot, r) at output
+// position r); rows r >= N*L and taps k >= K hold 0.  The grid stride over r
+// is a multiple of 16, so every thread keeps one (r >> 2) & 3 and one tap.
 template <typename T>
 __global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset,
                                    int pad_index, const float* __restrict__ pad_dev,
@@ -33,17 +35,18 @@ __global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, i
   const int R = g.N * L;
   const int KK = g.KH * g.KW;
   const int K = g.C * KK;
-  for (int k = blockIdx.y; k < K; k += gridDim.y) {
+  const int r0 = blockIdx.x * blockDim.x + threadIdx.x;
+  for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
+    const int k = operand_tap(slot, r0);
     const int c = k / KK;
     const int t = k - c * KK;
     const int kh = t / g.KW;
     const int kw = t - kh * g.KW;
     const int ih0 = kh * g.DH - g.PH;
     const int iw0 = kw * g.DW - g.PW;
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < Rpad;
-         r += gridDim.x * blockDim.x) {
+    for (int r = r0; r < Rpad; r += gridDim.x * blockDim.x) {
       unsigned off = 0;
-      if (r < R) {
+      if (r < R && k < K) {
         const int n = r / L;
         const int l = r - n * L;
         const int oh = l / g.OW;
@@ -55,7 +58,7 @@ __global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, i
           v = elem_index<T>(img[(((long long)n * g.C + c) * g.H + ih) * g.W + iw], offset);
         off = row_offset(v);
       }
-      xt[(long long)k * Rpad + r] = (uint16_t)off;
+      xt[(long long)slot * Rpad + r] = (uint16_t)off;
     }
   }
 }
@@ -258,7 +261,9 @@ int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
   const int K = g.C * g.KH * g.KW;
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && (R == 0 || img), "atx_im2col_rows: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, TB), 1024), (unsigned)std::min(K, 65535));
+  static_assert(TB % 16 == 0, "grid stride keeps (r >> 2) & 3 per thread");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, TB), 1024),
+            (unsigned)std::min(operand_rows(K), 65535));
   if (dtype == 0)
     hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,
                        (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad);

@@ -1,38 +1,47 @@
 // LUT GEMM forward for gfx950: y[n,o,l] = sum_k LUT[xi(n,k,l)][wi(o,k)].
 //
-// Kernel structure ("expanded tables"):
-//   A workgroup owns a tile of ATX_ROW_TILE (1024) rows r = n*L + l and
-//   ATX_COL_TILE (64) output channels.  For every k it builds, in LDS, the
-//   table E_k[v][o] = LUT16[v][wi(o,k)] (256 rows x 64 channels x 16 bit =
-//   32 KiB) from the transposed 16-bit LUT image (L2-resident, 128 KiB), then
-//   every lane looks up E_k[xi(r,k)][o..o+7] for its rows with one
-//   conflict-free 16-byte LDS read and adds the eight 16-bit entries into
-//   int32 accumulators (exact).  Four E buffers (128 KiB of LDS) let each
-//   step write the table two steps ahead, with one barrier per two steps.
+// Kernel structure ("expanded tables", four to an LDS line):
+//   A workgroup owns a tile of ATX_ROW_TILE (2048) rows r = n*L + l and
+//   ATX_COL_TILE (32) output channels.  For every k it builds, in LDS, the
+//   table E_k[v][o] = LUT16[v][wi(o,k)] (256 rows x 32 channels x 16 bit =
+//   16 KiB) from the transposed 16-bit LUT image (L2-resident, 128 KiB), then
+//   every lane looks up E_k[xi(r,k)][o..o+7] for its rows with one 16-byte
+//   LDS read and adds the eight 16-bit entries into int32 accumulators
+//   (exact).  Table bytes written per lookup are 512 / ATX_ROW_TILE, so the
+//   tall, narrow tile halves the table-build cost of a 1024 x 64 tile with
+//   the same accumulators per lane.
 //
-//   LDS bank layout: an E row is 128 bytes (all 32 banks).  Its 16-byte
-//   chunk for channels 8g..8g+7 is stored at chunk position g ^ ((v>>1)&7).
-//   The activation operand is pre-encoded as the byte offset
-//   v*128 + ((v>>1)&7)*16 ("row offset"), so the lane's address is
-//   row_offset ^ (g*16): no arithmetic on the index itself.
+//   LDS bank layout.  gfx950's LDS has 64 banks (256 bytes per clock) and
+//   serves a 16-byte read in passes of 16 lanes.  An E row is 64 bytes, so a
+//   pass covers four rows, and rows landing in the same quarter of the banks
+//   serialize.  Four consecutive tables therefore share each 256-byte LDS
+//   line: line v holds row v of table 4j+q in quarter q.  In sub-step s of
+//   quad j, row group rg reads table 4j + ((rg + s) & 3); the four row
+//   groups of a pass read four different quarters whatever their rows, so
+//   the reads are conflict-free (130 TB/s measured, against 66 TB/s for
+//   random quarters).  Over the quad's four sub-steps every lane reads all
+//   four tables.  Within a quarter, the 16-byte chunk for channels 8g..8g+7
+//   of row v sits at position g ^ ((v >> 1) & 3).  The activation operand is
+//   pre-encoded as the byte offset v*256 + ((v >> 1) & 3)*16 ("row offset");
+//   a lane's address is row_offset ^ (g*16 | quarter*64 | buffer*65536).
 //
-//   Table build: wave w builds channel group w.  Its eight weight indices at
-//   k are wave-uniform (one vector load read back with v_readlane); lane t
-//   loads the dwords
-//   LUT16T[w_j][2t, 2t+1] of the eight channels j (scalar base + lane
-//   offset, 256 contiguous bytes per instruction), interleaves them with
-//   v_perm into the 16-byte chunks of rows 2t and 2t+1 and stores each with
-//   one ds_write_b128.  The swizzle gives the eight lanes of every write
-//   group distinct chunk positions, so the writes are conflict-free (4-byte
-//   LDS writes reach only about a third of the 16-byte write bandwidth).
+//   Table build: two quad buffers (128 KiB).  In sub-step s of quad j every
+//   wave writes its part of table 4(j+1)+s into the other buffer: wave w
+//   covers channel group w % 4 for rows 128(w / 4) .. +127; its eight
+//   weight indices are wave-uniform (one vector load read back with
+//   v_readlane); lane t loads the dwords LUT16T[w_c][v0, v0+1] (v0 = row
+//   pair of the lane) of the eight channels c (buffer loads, scalar offsets),
+//   interleaves them with v_perm into the 16-byte chunks of rows v0 and v0+1
+//   and stores each with one ds_write_b128.  One barrier per quad (four
+//   k-steps) orders the build of quad j+1 and the reads of quad j.
 //
-//   Threads: 512 (8 waves).  Lane = (row group rg 0..7, channel group g);
-//   wave w owns rows 128w .. 128w+127 of the tile and lane (rg, g) the rows
-//   32h + 4rg + m (h, m = 0..3) x 8 channels = 128 int32 accumulators
+//   Threads: 512 (8 waves).  Lane = (row group rg 0..15, channel group g);
+//   wave w owns rows 256w .. 256w+255 of the tile and lane (rg, g) the rows
+//   64h + 4rg + m (h, m = 0..3) x 8 channels = 128 int32 accumulators
 //   (256-VGPR budget at 2 waves per SIMD).  Four consecutive rows per lane
 //   let the epilogue store every (channel, h) as one 16-byte vector, and the
-//   eight row groups of a channel fill a 128-byte line, so results go from
-//   registers straight to HBM with all waves storing at once.
+//   sixteen row groups of a channel fill two 128-byte lines, so results go
+//   from registers straight to HBM with all waves storing at once.
 //
 // Reference: bgemm_lut_u8_kernel / bgemm_mainloop
 // (csrc/claude/bgemm_lut_kernels.cuh:183-387) computes the same sum with a
@@ -45,23 +54,24 @@
 
 namespace atx {
 
-constexpr int RT = ATX_ROW_TILE;   // rows per workgroup
-constexpr int OT = ATX_COL_TILE;   // channels per workgroup
-#ifndef ATX_LUT_RPL
-#define ATX_LUT_RPL 16
-#endif
-constexpr int RPL = ATX_LUT_RPL;   // rows per lane (16: 8 waves, 8: 16 waves)
-constexpr int RPW = 8 * RPL;       // rows per wave (8 row groups)
-constexpr int NWAVE = RT / RPW;    // waves per workgroup
-constexpr int NT = 64 * NWAVE;     // threads per workgroup
-constexpr int IPT = 1024 / NT;     // table-build items per thread
-constexpr int ETAB = 256 * OT * 2; // bytes of one E_k table (32 KiB)
-constexpr int NBUF = 4;                       // E tables resident in LDS
-constexpr int SMEM_BYTES = NBUF * ETAB;       // 128 KiB of static LDS
+constexpr int RT = ATX_ROW_TILE;   // rows per workgroup (2048)
+constexpr int OT = ATX_COL_TILE;   // channels per workgroup (32)
+constexpr int CG = OT / 8;         // 16-byte channel chunks per table row (4)
+constexpr int NRG = 64 / CG;       // row groups per wave (16)
 constexpr int RQ = 4;              // consecutive rows per lane quad
-constexpr int NQ = RPL / RQ;       // quads per lane (stride 32 rows)
-static_assert(1024 % NT == 0, "table build needs an integral item count");
-static_assert(RPW == 8 * RQ * NQ, "a wave's rows are 8 row groups x NQ quads");
+constexpr int NQ = 4;              // quads per lane (stride NRG * RQ rows)
+constexpr int RPL = RQ * NQ;       // rows per lane (16)
+constexpr int RPW = NRG * RPL;     // rows per wave (256)
+constexpr int NWAVE = RT / RPW;    // waves per workgroup (8)
+constexpr int NT = 64 * NWAVE;     // threads per workgroup (512)
+constexpr int TPL = 4;             // tables per LDS line (quarters)
+constexpr int LINE = 256;          // bytes per LDS line
+constexpr int QTAB = 256 * LINE;   // one quad of tables (64 KiB)
+constexpr int SMEM_BYTES = 2 * QTAB;          // two quad buffers (128 KiB)
+static_assert(CG == 4 && NRG == 16 && NWAVE == 8, "tile geometry");
+static_assert(TPL * CG * 16 == LINE, "four 64-byte table rows per line");
+static_assert(2 * NWAVE == 16 && 256 / 2 == 64 * (NWAVE / CG),
+              "a table is 8 waves x 64 lanes x one row pair");
 
 // K limits for exact int32 partial sums (entries up to 32767 / 65535).
 constexpr int KMAX_I16 = 65536;
@@ -101,17 +111,20 @@ __global__ void lut_prepare_kernel(const float* __restrict__ lut,
 }
 
 // ------------------------------------------------------------- operand pack
-// xt[k][r] for r < R from x[n][k][l] (r = n*L + l); zero offsets for r >= R.
+// xt[slot][r] = row_offset(x[n][operand_tap(slot, r)][l]) for r < R
+// (r = n*L + l); 0 for r >= R and taps >= K.  The grid stride over r is a
+// multiple of 16, so every thread keeps one tap.
 template <typename T>
 __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
                               int offset, uint8_t* __restrict__ xq,
                               uint16_t* __restrict__ xt, int Rpad) {
   const int R = N * L;
-  for (int k = blockIdx.y; k < K; k += gridDim.y) {
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < Rpad;
-         r += gridDim.x * blockDim.x) {
+  const int r0 = blockIdx.x * blockDim.x + threadIdx.x;
+  for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
+    const int k = operand_tap(slot, r0);
+    for (int r = r0; r < Rpad; r += gridDim.x * blockDim.x) {
       unsigned off = 0;
-      if (r < R) {
+      if (r < R && k < K) {
         const int n = r / L;
         const int l = r - n * L;
         const long long src = ((long long)n * K + k) * L + l;
@@ -124,7 +137,7 @@ __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
         }
         off = row_offset(v);
       }
-      xt[(long long)k * Rpad + r] = (uint16_t)off;
+      xt[(long long)slot * Rpad + r] = (uint16_t)off;
     }
   }
 }
@@ -178,16 +191,18 @@ __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
   }
 }
 
-// Table-build registers: for each build item, the LUT16T dwords
-// (entries v0, v0+1) of the wave's eight channels.
-struct Rows { unsigned d[IPT][8]; };
-// Row offsets of the lane's quads: v[h] = rows 32h + 4rg + 0..3, two per dword.
+// Table-build registers: the LUT16T dwords (entries v0, v0+1) of the wave's
+// eight channels.
+struct Rows { unsigned d[8]; };
+// Row offsets of the lane's quads: v[h] = rows NRG*RQ*h + 4rg + 0..3, two per
+// dword.
 struct XRows { uint2 v[NQ]; };
 
 // Raw buffer descriptor (word 3 of the gfx9-family descriptor: 32-bit
 // elements, no swizzle) over `bytes` bytes at a wave-uniform base.  Buffer
 // loads take the per-step offsets in scalar registers, so the loads below
-// cost no per-lane 64-bit address arithmetic.
+// cost no per-lane 64-bit address arithmetic; accesses at or beyond `bytes`
+// return 0 without touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
                                            0x00020000);
@@ -201,79 +216,65 @@ __device__ __forceinline__ unsigned load_w8(const uint8_t* wcol, int lane) {
   return __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(wcol, 8), (lane & 1) * 4, 0, 0);
 }
 
-// Dword at entries (v0, v0+1) of LUT16T row w_j for every channel j of the
-// group; item i covers v0 = 2*lane + 128*i + sbase/2.  Row offsets are
-// wave-uniform (read from lanes 0 and 1 of the weight-index register).
+// Dword at entries (v0, v0+1) of LUT16T row w_c for every channel c of the
+// group, v0 = 2*lane + sbase/2.  Row offsets are wave-uniform (read from
+// lanes 0 and 1 of the weight-index register).
 __device__ __forceinline__ void load_rows(Rows& r, __amdgpu_buffer_rsrc_t lut, unsigned wv,
                                           int lane, int sbase) {
   const unsigned w_lo = __builtin_amdgcn_readlane(wv, 0);
   const unsigned w_hi = __builtin_amdgcn_readlane(wv, 1);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const unsigned wj = ((j < 4 ? w_lo : w_hi) >> (8 * (j & 3))) & 255u;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      r.d[i][j] = __builtin_amdgcn_raw_buffer_load_b32(lut, lane * 4 + 256 * i,
-                                                        (int)(wj * 512u) + sbase, 0);
+  for (int c = 0; c < 8; ++c) {
+    const unsigned wc = ((c < 4 ? w_lo : w_hi) >> (8 * (c & 3))) & 255u;
+    r.d[c] = __builtin_amdgcn_raw_buffer_load_b32(lut, lane * 4, (int)(wc * 512u) + sbase, 0);
   }
 }
 
-// Row offsets of the lane's quads at k from the tile's row-offset column
-// (xcol = &xt[k][first row of the tile]); xoff = byte offset of the lane's
-// first quad within the tile.
-__device__ __forceinline__ void load_x(XRows& x, const uint16_t* xcol, int xoff) {
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(xcol, RT * 2);
+// Row offsets of the lane's quads from slot soff / (2 Rpad) of a quad's
+// row-offset block (xs = descriptor over the quad's four slots of the tile,
+// voff = byte offset of the lane's first quad within a slot).
+__device__ __forceinline__ void load_x(XRows& x, __amdgpu_buffer_rsrc_t xs, int voff,
+                                       int soff) {
 #pragma unroll
   for (int h = 0; h < NQ; ++h)
     x.v[h] = __builtin_bit_cast(
-        uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, xoff + 16 * RQ * h, 0, 0));
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(xs, voff + 2 * NRG * RQ * h, soff, 0));
 }
 
-// Writes this lane's two 16-byte chunks per build item (rows v0 and v0+1,
-// channels 8*og .. 8*og+7); wbase holds the chunk address of row v0 within
-// the table at smem.
-__device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r,
-                                            const int (&wbase)[IPT]) {
-#pragma unroll
-  for (int it = 0; it < IPT; ++it) {
-    const unsigned* d = r.d[it];
-    uint4 lo, hi;      // channel pairs (2m, 2m+1) at v0 (low halves) / v0+1 (high)
-    lo.x = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
-    lo.y = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
-    lo.z = __builtin_amdgcn_perm(d[5], d[4], 0x05040100u);
-    lo.w = __builtin_amdgcn_perm(d[7], d[6], 0x05040100u);
-    hi.x = __builtin_amdgcn_perm(d[1], d[0], 0x07060302u);
-    hi.y = __builtin_amdgcn_perm(d[3], d[2], 0x07060302u);
-    hi.z = __builtin_amdgcn_perm(d[5], d[4], 0x07060302u);
-    hi.w = __builtin_amdgcn_perm(d[7], d[6], 0x07060302u);
-    *(uint4*)(smem + wbase[it]) = lo;
-    *(uint4*)(smem + wbase[it] + 128) = hi;
-  }
+// Writes the lane's two 16-byte chunks (rows v0 and v0+1, channels
+// 8*og .. 8*og+7) at smem + wb (row v0's chunk; row v0+1 is one line on).
+__device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r, int wb) {
+  const unsigned* d = r.d;
+  uint4 lo, hi;      // channel pairs (2m, 2m+1) at v0 (low halves) / v0+1 (high)
+  lo.x = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
+  lo.y = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
+  lo.z = __builtin_amdgcn_perm(d[5], d[4], 0x05040100u);
+  lo.w = __builtin_amdgcn_perm(d[7], d[6], 0x05040100u);
+  hi.x = __builtin_amdgcn_perm(d[1], d[0], 0x07060302u);
+  hi.y = __builtin_amdgcn_perm(d[3], d[2], 0x07060302u);
+  hi.z = __builtin_amdgcn_perm(d[5], d[4], 0x07060302u);
+  hi.w = __builtin_amdgcn_perm(d[7], d[6], 0x07060302u);
+  *(uint4*)(smem + wb) = lo;
+  *(uint4*)(smem + wb + LINE) = hi;
 }
 
 // Accumulates one table for this lane's RPL rows.  x holds the rows'
-// offsets (two per dword, below 32768); gx XORs in the lane's channel chunk
-// (bits 4-6) and possibly bit 16 of the table's LDS address.
+// offsets (two per dword, below 65536); gx XORs in the lane's channel chunk
+// (bits 4-5), the table's quarter (bits 6-7) and the quad buffer (bit 16).
 template <bool SIGNED>
 __device__ __forceinline__ void use_table(int (&acc)[RPL][8], const unsigned char* smem,
                                           const XRows& x, unsigned gx) {
-  // Reads per batch: 8 (two quads) at 2 waves per SIMD, 4 (one quad) at 4
-  // waves per SIMD, where the register budget is half as large.
-  constexpr int QB = RPL >= 16 ? 2 : 1;
 #pragma unroll
-  for (int hh = 0; hh < NQ; hh += QB) {
-    unsigned xd[2 * QB];
+  for (int hh = 0; hh < NQ; hh += 2) {
+    const unsigned xd[4] = {x.v[hh].x, x.v[hh].y, x.v[hh + 1].x, x.v[hh + 1].y};
+    uint4 e[8];
 #pragma unroll
-    for (int q = 0; q < QB; ++q) { xd[2 * q] = x.v[hh + q].x; xd[2 * q + 1] = x.v[hh + q].y; }
-    uint4 e[4 * QB];
-#pragma unroll
-    for (int j = 0; j < 2 * QB; ++j) {
+    for (int j = 0; j < 4; ++j) {
       e[2 * j] = *(const uint4*)(smem + ((xd[j] & 0xffffu) ^ gx));
       e[2 * j + 1] = *(const uint4*)(smem + ((xd[j] >> 16) ^ gx));
     }
 #pragma unroll
-    for (int j = 0; j < 4 * QB; ++j) add8<SIGNED>(acc[RQ * hh + j], e[j]);
-    if constexpr (QB == 1) __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < 8; ++j) add8<SIGNED>(acc[RQ * hh + j], e[j]);
   }
 }
 
@@ -304,20 +305,8 @@ __device__ __forceinline__ void put_rows(const GemmParams& p, void* y, long long
   }
 }
 
-// Smallest entry of the waves' progress slots (wave-uniform).
-__device__ __forceinline__ unsigned min_progress(const unsigned* prog) {
-  static_assert(NWAVE % 4 == 0, "16-byte reads cover the slots");
-  unsigned m = ~0u;
-#pragma unroll
-  for (int i = 0; i < NWAVE / 4; ++i) {
-    const uint4 a = *(const uint4*)(prog + 4 * i);
-    m = min(m, min(min(a.x, a.y), min(a.z, a.w)));
-  }
-  return __builtin_amdgcn_readfirstlane(m);
-}
-
-// Writes the lane's accumulators: channel o0 + e, rows r + 32h + m of quad
-// h (r = first row of quad 0).  Rows beyond R and channels beyond O are
+// Writes the lane's accumulators: channel o0 + e, rows r + NRG*RQ*h + m of
+// quad h (r = first row of quad 0).  Rows beyond R and channels beyond O are
 // dropped.  With L % 4 == 0 a quad never straddles two images and is one
 // 16-byte store (r is a multiple of 4); otherwise rows are stored one by one,
 // stepping (n, l) across image boundaries.
@@ -327,7 +316,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, void* y,
   const bool vec = (p.L & 3) == 0;
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
-    const int rq = r + 8 * RQ * h;
+    const int rq = r + NRG * RQ * h;
     if (rq >= p.R) break;
     const int n = rq / p.L;
     const int l = rq - n * p.L;
@@ -363,12 +352,10 @@ template <bool SIGNED>
 __global__ void __launch_bounds__(NT, 1)
 lut_gemm_kernel(const GemmParams p) {
   __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
-  __shared__ __align__(16) unsigned progress[NWAVE];   // k-steps finished per wave
-  __shared__ unsigned pscratch[NT];    // branch-free progress store: other lanes' sink
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int rg = lane >> 3, g = lane & 7;
+  const int rg = lane / CG, g = lane % CG;
 
   int lb = logical_block();
   const int to = lb % p.tiles_o; lb /= p.tiles_o;
@@ -380,28 +367,22 @@ lut_gemm_kernel(const GemmParams p) {
   const int kb = s * p.k_chunk;
   const int ke = min(p.K, kb + p.k_chunk);
 
-  // Table-build mapping: wave w builds channel group og = w % 8 for rows
-  // 128 hw .. 128 hw + 128 IPT - 1 (hw = w / 8); lane t writes rows
-  // v0 = 2t + 128(i + hw) and v0+1 (item i), whose chunk og sits at position
-  // og ^ ((v0 >> 1) & 7) = og ^ (t & 7).  Tables 0/1 and 2/3 of the four
-  // LDS buffers differ by an immediate offset (0 / ETAB) from the base
-  // addresses wlo / whi (whi = wlo + 2 * ETAB).
-  static_assert((NWAVE == 8 && IPT == 2) || (NWAVE == 16 && IPT == 1),
-                "eight channel groups x 256 rows per table");
-  static_assert(NBUF == 4 && 2 * ETAB == 65536, "buffer pairs split at bit 16");
-  const int og = __builtin_amdgcn_readfirstlane(wave & 7);
-  const int hw = __builtin_amdgcn_readfirstlane(wave >> 3);
-  int wlo[IPT], whi[IPT];
+  // Table build: wave w writes channel group og = w % 4 for rows
+  // 128 hw .. 128 hw + 127 (hw = w / 4); lane t the row pair v0 = 128 hw + 2t,
+  // v0 + 1, whose chunk og sits at position og ^ ((v0 >> 1) & 3) =
+  // og ^ (t & 3) of quarter q.  wb0 / wb1 address row v0's chunk in quad
+  // buffer 0 / 1; the quarter is an immediate offset (q * 64).
+  const int og = __builtin_amdgcn_readfirstlane(wave % CG);
+  const int hw = __builtin_amdgcn_readfirstlane(wave / CG);
+  const int wb0 = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
+  const int wb1 = wb0 + QTAB;
+  // Read XOR masks: sub-step s of a quad reads quarter (rg + s) & 3.
+  unsigned gq[TPL];
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    wlo[i] = (2 * lane + 128 * (i + hw)) * 128 + ((og ^ (lane & 7)) << 4);
-    whi[i] = wlo[i] + 2 * ETAB;
-  }
-  const unsigned gxa = (unsigned)(g << 4);              // reads of buffers 0, 1
-  const unsigned gxb = gxa | (unsigned)(2 * ETAB);      // reads of buffers 2, 3
+  for (int q = 0; q < TPL; ++q) gq[q] = (unsigned)((g << 4) | (((rg + q) & 3) << 6));
 
+  const int xoff = (wave * RPW + rg * RQ) * 2;          // lane's first quad, bytes
   const uint16_t* __restrict__ xtile = p.xt + (long long)tr * RT;
-  const int xoff = (wave * RPW + rg * RQ) * 2;         // lane's first quad, bytes
   const uint8_t* __restrict__ wcol = p.wt + o0 + og * 8;
   const __amdgpu_buffer_rsrc_t lutr = buffer_rsrc(p.lut16t, 256 * 256 * 2);
   // Zero-length view of the image: its loads are out of range and return 0,
@@ -414,98 +395,85 @@ lut_gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0;
 
-  if (tid < NWAVE) progress[tid] = 0u;   // ordered before use by the prologue barrier
-  unsigned* const pslot = lane == 0 ? &progress[wave] : &pscratch[tid];
-
   if (kb < ke) {
-    // Four LDS buffers, table t = k - kb in buffer t % 4.  Step t issues the
-    // loads for row offsets t+1, LUT rows of table t+2 and weight indices of
-    // t+3 (indices clamped to the range, so every load is unconditional),
-    // accumulates from table t, writes table t+2 and records t+1 steps done
-    // in its progress slot.  The loop is unrolled over the four buffers so
-    // every buffer offset is an immediate and the row-offset registers
-    // alternate between two sets without copies.
-    //
-    // Split barrier: instead of a workgroup barrier per step, a wave starts
-    // step t once every wave has finished step t-2 (min over the progress
-    // slots >= t-1).  That covers both hazards of the step: table t was
-    // written in step t-2, and table t+2 reuses the buffer of table t-2,
-    // last read in step t-2.  Waves may drift one step apart, which keeps
-    // the VALU busy while other waves wait on LDS.  Buffers in use at once:
-    // a slow wave at step t-1 holds tables t-1 and t+1, a fast wave at step
-    // t tables t and t+2.  A wave's LDS operations execute in program
-    // order, so its progress store lands after its table writes and its
-    // reads of table t-2, and a wave that has seen the store issues its
-    // table reads after that.  Every wave waits only for steps that it has
-    // itself already finished, so the waits always end.  Compiler fences
-    // keep the LDS accesses and the progress slots in program order;
-    // scheduling fences keep the loads ahead of the accumulation and the
-    // table write (which waits for the LUT rows) behind it, so the loads
-    // overlap a whole step.
-    const int klast = ke - 1;
-    const long long xstride = p.Rpad, wstride = p.Opad;
+    // Sub-steps sigma = 4j + s (tables counted from kb; n of them).  Sub-step
+    // sigma issues the loads for the row offsets of sub-step sigma+1, the
+    // LUT rows of table sigma+5 and the weight indices of table sigma+6,
+    // accumulates from the lane's table of sub-step sigma and writes table
+    // sigma+4 (rows loaded one sub-step earlier).  Tables at or past n are
+    // built all-zero from lutz; row offsets past the chunk load as 0 (row 0
+    // of such a table), so whole quads run without branches.  Scheduling
+    // fences keep the loads ahead of the accumulation and the table write
+    // (which waits for its LUT rows) behind it.
+    const int n = ke - kb;
+    const int nq = (n + TPL - 1) / TPL;
+    const int slot_bytes = p.Rpad * 2;                  // one k-row of the operand
+    // The operand's quads are rotated (slot s of row r holds tap
+    // 4j + (((r >> 2) + s) & 3)), so at sub-step s every lane reads slot s:
+    // a scalar offset.  Quads past the chunk read through an empty view (0).
+    auto quad_rows = [&](int j) {                       // descriptor of quad j's slots
+      return buffer_rsrc(xtile + (long long)(kb + TPL * j) * p.Rpad,
+                         j < nq ? TPL * slot_bytes : 0);
+    };
+    auto wtab = [&](int t) {                            // weight column of table t
+      return wcol + (long long)(kb + min(t, n - 1)) * p.Opad;
+    };
+
     XRows xa, xb;
-    unsigned wnext;                                         // indices of table t+2
+    Rows rows;
+    unsigned wnext;                                     // indices of table sigma+5
     {
-      const unsigned w0 = load_w8(wcol + kb * wstride, lane);
-      const unsigned w1 = load_w8(wcol + min(kb + 1, klast) * wstride, lane);
-      wnext = load_w8(wcol + min(kb + 2, klast) * wstride, lane);
-      Rows rows;
-      load_rows(rows, lutr, w0, lane, 256 * hw);
-      load_x(xa, xtile + kb * xstride, xoff);
-      write_table(smem, rows, wlo);                         // table kb   -> buffer 0
-      load_rows(rows, ke - kb > 1 ? lutr : lutz, w1, lane, 256 * hw);
-      write_table(smem + ETAB, rows, wlo);                  // table kb+1 -> buffer 1
+      Rows r4;
+#pragma unroll
+      for (int q = 0; q < TPL; ++q) {
+        load_rows(r4, q < n ? lutr : lutz, load_w8(wtab(q), lane), lane, 256 * hw);
+        write_table(smem + q * 64, r4, wb0);            // quad 0 -> buffer 0
+      }
+      load_rows(rows, TPL < n ? lutr : lutz, load_w8(wtab(TPL), lane), lane, 256 * hw);
+      wnext = load_w8(wtab(TPL + 1), lane);
+      load_x(xa, quad_rows(0), xoff, 0);
     }
     __syncthreads();
 
-    const unsigned n = (unsigned)(ke - kb);
-    auto step = [&](auto bufc, unsigned t, XRows& xcur, XRows& xnext)
+    // One sub-step; B = quad buffer of quad j, S = sub-step within the quad.
+    auto sub = [&](auto bc, auto sc, int j, XRows& xcur, XRows& xnext)
         __attribute__((always_inline)) {
-      constexpr int B = decltype(bufc)::value;              // buffer of table t
-      constexpr int BW = (B + 2) & 3;                       // buffer of table t+2
-      const int k = kb + (int)t;
-      load_x(xnext, xtile + min(k + 1, klast) * xstride, xoff);
-      Rows rows;
-      load_rows(rows, t + 2u < n ? lutr : lutz, wnext, lane, 256 * hw);
-      const unsigned wn3 = load_w8(wcol + min(k + 3, klast) * wstride, lane);
+      constexpr int B = decltype(bc)::value;
+      constexpr int S = decltype(sc)::value;
+      const int sigma = TPL * j + S;
+      if constexpr (S + 1 < TPL) load_x(xnext, quad_rows(j), xoff, (S + 1) * slot_bytes);
+      else load_x(xnext, quad_rows(j + 1), xoff, 0);
+      Rows rn;
+      load_rows(rn, sigma + 5 < n ? lutr : lutz, wnext, lane, 256 * hw);
+      const unsigned wn = load_w8(wtab(sigma + 6), lane);
       __builtin_amdgcn_sched_barrier(0);
-      const unsigned need = t ? t - 1u : 0u;
-      asm volatile("" ::: "memory");
-      unsigned seen = min_progress(progress);
-      while (seen < need) {
-        __builtin_amdgcn_s_sleep(1);
-        asm volatile("" ::: "memory");
-        seen = min_progress(progress);
-      }
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      use_table<SIGNED>(acc, smem + (B & 1) * ETAB, xcur, (B & 2) ? gxb : gxa);
+      use_table<SIGNED>(acc, smem, xcur, gq[S] | (B ? (unsigned)QTAB : 0u));
       // Pin the adds here: left free, the compiler sinks them into later
       // steps, past the table write that waits for this step's loads.
 #pragma unroll
-      for (int j = 0; j < RPL; ++j)
+      for (int jj = 0; jj < RPL; ++jj)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[j][e]));
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
       __builtin_amdgcn_sched_barrier(0);
-      write_table(smem + (BW & 1) * ETAB, rows, (BW & 2) ? whi : wlo);
-      asm volatile("" ::: "memory");
-      *pslot = t + 1u;          // lane 0: progress[wave]; others: scratch slots
-      asm volatile("" ::: "memory");
-      wnext = wn3;
+      write_table(smem + S * 64, rows, B ? wb0 : wb1);  // table sigma+4, other buffer
+      rows = rn;
+      wnext = wn;
+      if constexpr (S == TPL - 1) __syncthreads();
     };
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    using B2 = std::integral_constant<int, 2>;
-    using B3 = std::integral_constant<int, 3>;
-    // Whole groups of four steps; the up to three steps past the chunk's
-    // end accumulate all-zero tables (built from lutz), so the accumulation
-    // needs no branch and every wave runs the same steps.
-    for (unsigned t = 0; t < n; t += 4u) {
-      step(B0{}, t, xa, xb);
-      step(B1{}, t + 1u, xb, xa);
-      step(B2{}, t + 2u, xa, xb);
-      step(B3{}, t + 3u, xb, xa);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    for (int j = 0; j < nq; j += 2) {
+      sub(I0{}, I0{}, j, xa, xb);
+      sub(I0{}, I1{}, j, xb, xa);
+      sub(I0{}, I2{}, j, xa, xb);
+      sub(I0{}, I3{}, j, xb, xa);
+      if (j + 1 >= nq) break;
+      sub(I1{}, I0{}, j + 1, xa, xb);
+      sub(I1{}, I1{}, j + 1, xb, xa);
+      sub(I1{}, I2{}, j + 1, xa, xb);
+      sub(I1{}, I3{}, j + 1, xb, xa);
     }
   }
 
@@ -553,7 +521,8 @@ __global__ void lut_gemm_f32_kernel(const GemmParams p) {
     const int r = (int)(i - (long long)o * p.R);
     float a = 0.0f;
     for (int k = 0; k < p.K; ++k) {
-      const unsigned xi = (unsigned)p.xt[(long long)k * p.Rpad + r] >> 7;
+      const unsigned xi =
+          (unsigned)p.xt[(long long)operand_slot(k, r) * p.Rpad + r] >> 8;
       const unsigned wi = p.wt[(long long)k * p.Opad + o];
       a += p.lutf32t[wi * 256u + xi];
     }
@@ -577,12 +546,13 @@ struct Plan { int tiles_r, tiles_o, splits, k_chunk; };
 constexpr int PLAN_CUS = 256;
 
 // Split-K count by a cost model in units of one k-step of one workgroup:
-//   ceil(tiles*S / CUs) rounds x (ceil(K/S) + 3 fixed steps per workgroup)
+//   ceil(tiles*S / CUs) rounds x (k-chunk + 6 fixed steps per workgroup)
 //   + for S > 1: 4 steps for the reduce launch and S x (R*O / 600000) steps
 //     for writing and re-reading one int32 partial slice (8 bytes per
 //     output at ~4 TB/s against ~1.2 us per k-step).
-// S is at least ceil(K / kmax), the exact-int32 bound of one pass, and the
-// smallest S among equal costs wins.
+// k-chunks are whole quads of tables (multiples of 4); S is at least
+// ceil(K / kmax), the exact-int32 bound of one pass, and the smallest S among
+// equal costs wins.
 static Plan make_plan(int N, int K, int L, int O, int kmax) {
   Plan pl;
   const long long R = (long long)N * L;
@@ -593,16 +563,17 @@ static Plan make_plan(int N, int K, int L, int O, int kmax) {
   const long long cus = PLAN_CUS;
   const int smin = (int)cdiv(K, kmax);
   const double slice = (double)R * O / 600000.0;
-  int best = smin;
+  long long best_kc = cdiv(cdiv(K, smin), TPL) * TPL;
   double best_cost = 0.0;
   for (int S = smin; S <= std::max(smin, 64); ++S) {
-    const long long kc = cdiv(K, S);
+    const long long kc = cdiv(cdiv(K, S), TPL) * TPL;
     if (S > smin && kc < 16) break;
-    const double cost = (double)cdiv(tiles * S, cus) * (double)(kc + 3) +
-                        (S > 1 ? 4.0 + S * slice : 0.0);
-    if (S == smin || cost < best_cost) { best = S; best_cost = cost; }
+    const long long splits = cdiv(K, kc);
+    const double cost = (double)cdiv(tiles * splits, cus) * (double)(kc + 6) +
+                        (splits > 1 ? 4.0 + splits * slice : 0.0);
+    if (S == smin || cost < best_cost) { best_kc = kc; best_cost = cost; }
   }
-  pl.k_chunk = (int)cdiv(K, best);
+  pl.k_chunk = (int)std::min<long long>(best_kc, kmax);
   pl.splits = (int)cdiv(K, pl.k_chunk);
   return pl;
 }
@@ -629,7 +600,8 @@ int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
   if ((long long)K * Rpad == 0) return ATX_OK;
   // an empty x (N*L == 0) only writes the zero padding rows
   ATX_REQUIRE(xt && ((long long)N * L == 0 || x), "atx_pack_x_f32: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024),
+            (unsigned)std::min(operand_rows(K), 65535));
   hipLaunchKernelGGL(pack_x_kernel<float>, grid, dim3(256), 0, stream, x, N, K, L,
                      offset, xq, xt, Rpad);
   return check_launch("pack_x_kernel<float>");
@@ -642,7 +614,8 @@ int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad
               "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && ((long long)N * L == 0 || xq), "atx_pack_x_u8: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024), (unsigned)std::min(K, 65535));
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024),
+            (unsigned)std::min(operand_rows(K), 65535));
   hipLaunchKernelGGL(pack_x_kernel<uint8_t>, grid, dim3(256), 0, stream, xq, N, K,
                      L, 0, (uint8_t*)nullptr, xt, Rpad);
   return check_launch("pack_x_kernel<u8>");
@@ -688,6 +661,9 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
   const long long R = (long long)N * L;
   ATX_REQUIRE(R <= 0x7fffffffLL - RT, "atx_lut_gemm: N*L too large");
   ATX_REQUIRE(Rpad >= R && Rpad % RT == 0, "atx_lut_gemm: bad Rpad %d", Rpad);
+  // Four k-rows of the row-offset operand are addressed with 32-bit offsets.
+  if ((long long)Rpad > (1LL << 27))
+    return set_error(ATX_ERANGE, "atx_lut_gemm: Rpad %d exceeds 2^27 rows", Rpad);
   ATX_REQUIRE(Opad >= O && Opad % OT == 0, "atx_lut_gemm: bad Opad %d", Opad);
   ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,
               "atx_lut_gemm: bad out_kind");

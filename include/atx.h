@@ -60,16 +60,19 @@ int atx_lut_prepare(const float* lut, uint16_t* out16t, float* outf32t,
                     int* flags, hipStream_t stream);
 
 /* --------------------------------------------------------- operand packing
- * The LUT GEMM reads its activation operand as "row offsets": a [K][Rpad]
- * uint16 array (R = N*L rows, Rpad = R rounded up to ATX_ROW_TILE) whose
- * entry for index value v is atx_row_offset(v).  Padding rows hold offset 0.
+ * The LUT GEMM reads its activation operand as "row offsets": a
+ * [Kpad][Rpad] uint16 array (R = N*L rows, Rpad = R rounded up to
+ * ATX_ROW_TILE, Kpad = K rounded up to 4) whose entry for LUT index v is
+ * atx_row_offset(v).  The k-rows come in quads rotated per row: slot s of a
+ * quad holds, for row r, tap k = (s & ~3) | (((r >> 2) + s) & 3)
+ * (atx_operand_tap).  Padding rows and taps k >= K hold offset 0.
  */
-#define ATX_ROW_TILE 1024
-#define ATX_COL_TILE 64
+#define ATX_ROW_TILE 2048
+#define ATX_COL_TILE 32
 
 /* x fp32 [N,K,L] holding quantized integer values -> xq uint8 [N,K,L]
  * (LUT index clamp(rint(v) + offset, 0, 255), nullable) and the row-offset
- * operand xt [K][Rpad].  Replaces quantize_to_u8_kernel
+ * operand xt [Kpad][Rpad].  Replaces quantize_to_u8_kernel
  * (csrc/claude/bgemm_lut_kernels.cuh:62-97) for the x operand. */
 int atx_pack_x_f32(const float* x, int N, int K, int L, int offset,
                    uint8_t* xq, uint16_t* xt, int Rpad, hipStream_t stream);
@@ -89,7 +92,7 @@ int atx_pack_w_f32(const float* w, int O, int K, int offset,
 int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
                   hipStream_t stream);
 
-/* Quantized image -> row-offset operand xt [K = C*KH*KW][Rpad] of the
+/* Quantized image -> row-offset operand xt [Kpad][Rpad] (K = C*KH*KW) of the
  * implicit im2col, k order (c, kh, kw), r = n*OH*OW + oh*OW + ow.  dtype:
  * 0 = int8 values (index v+128), 1 = uint8 (index v), 2 = fp32 signed
  * quantized values (index clamp(rint(v),-128,127)+128), 3 = fp32 unsigned
@@ -285,9 +288,15 @@ int atx_lds_probe(int mode, int blocks, int iters, unsigned* out,
 }
 #endif
 
-/* Row-offset encoding of LUT index v used by the LUT GEMM's LDS tables. */
+/* Row-offset encoding of LUT index v used by the LUT GEMM's LDS tables
+ * (256-byte lines; bits 4-5 carry the chunk swizzle (v >> 1) & 3). */
 static inline unsigned atx_row_offset(unsigned v) {
-  return v * 128u + (((v >> 1) & 7u) << 4);
+  return v * 256u + (((v >> 1) & 3u) << 4);
+}
+
+/* Tap held by slot s of the row-offset operand for row r. */
+static inline int atx_operand_tap(int s, int r) {
+  return (s & ~3) | (((r >> 2) + s) & 3);
 }
 
 #endif /* ATX_H */
