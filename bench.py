@@ -12,7 +12,11 @@ Also reported:
                 of every launch inside the timed region / their summed
                 durations (HIP events on the launch stream); bound = LDS, one
                 LUT-MAC = one 2-byte table read from LDS, peak = 256 CUs x
-                128 B/clk x 2.4 GHz.
+                256 B/clk x 2.4 GHz.  `valu_peak` is the co-bound of one
+                int32 add per LUT-MAC (256 CUs x 64 lanes x 2.4 GHz).
+                `traffic` = HBM bytes per launch measured by rocprofv3 PMC
+                passes (FETCH_SIZE, WRITE_SIZE; run with --calibrate-copy so
+                the same passes see a copy kernel of known size).
   lut_gemm      the standalone BGEMM microbench (config 3: B=32, 4096x2304 by
                 2304x256, perturbed LUT) in G LUT-MAC/s.
   cpu_baseline  the torch-CPU restatement of the same training step
@@ -27,7 +31,16 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-LDS_PEAK_GBS = 256 * 128 * 2.4      # GB/s: 256 CUs x 128 B/clk x 2.4 GHz
+LDS_PEAK_GBS = 256 * 256 * 2.4      # GB/s: 256 CUs x 256 B/clk x 2.4 GHz
+VALU_PEAK_GLUT = 256 * 64 * 2.4      # G int32 adds/s: 256 CUs x 64 lanes x 2.4 GHz
+COPY_BYTES = 512 << 20               # --calibrate-copy: bytes read and written per copy
+# HBM bytes per lut_gemm_kernel launch from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (KiB per dispatch, averaged over the launches of a
+# `bench.py --calibrate-copy` run), each divided by what the same counter
+# reads per byte of the 512 MiB copy in that run.  None = not measured.
+# profiles/lut_gemm_hbm_traffic.md holds the counter readings (copy factors:
+# FETCH 0.500, WRITE 1.000).
+GEMM_TRAFFIC = {"c3": 754695333, "c4": 163431926}
 
 
 def parse():
@@ -38,9 +51,11 @@ def parse():
     ap.add_argument("--workload", default="c4", choices=["c2", "c4", "c5", "c3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=1)
+    ap.add_argument("--cpu-sample-batch", type=int, default=4)
     ap.add_argument("--probe-lds", action="store_true",
                     help="also measure the LDS read throughput (roofline denominator)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run three 512 MiB device copies first (PMC byte-counter calibration)")
     return ap.parse_args()
 
 
@@ -72,6 +87,17 @@ def lds_probe(torch):
         nbytes = {7: 8, 8: 4}.get(mode, 16)
         res[name] = round(blocks * 512 * iters * 8 * nbytes / (ms * 1e-3) / 1e9, 1)
     return res
+
+
+def calibrate_copy(torch):
+    """Three plain device-to-device copies of COPY_BYTES: the known-size
+    kernel that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def bgemm_c3(torch, args):
@@ -187,6 +213,8 @@ def main():
     from approxtorch_amd import workloads
     torch.backends.cudnn.benchmark = False
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        calibrate_copy(torch)
     if args.workload == "c3":
         return main_c3(torch, args)
     name = args.workload
@@ -223,7 +251,7 @@ def main():
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
                    "forward_lut_macs": macs_fwd},
-        "roofline": roofline(timer, dt),
+        "roofline": roofline(timer, dt, GEMM_TRAFFIC.get(name)),
     }
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
@@ -234,18 +262,21 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def roofline(timer, dt):
+def roofline(timer, dt, traffic):
     gemm_ms, gemm_macs, launches = timer.summary()
     achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
     return {
         "kernel": "lut_gemm_kernel (+ split-K reduce)",
         "bound": "lds",
         "achieved": round(2 * achieved_glut, 1),
-        "peak": LDS_PEAK_GBS,
+        "peak": round(LDS_PEAK_GBS, 1),
         "unit": "GB/s",
         "frac": round(2 * achieved_glut / LDS_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "algorithmic_bytes_per_launch": round(2 * gemm_macs / max(launches, 1)),
         "lut_mac_per_s_G": round(achieved_glut, 1),
+        "valu_peak_lut_mac_per_s_G": round(VALU_PEAK_GLUT, 1),
+        "valu_frac": round(achieved_glut / VALU_PEAK_GLUT, 4),
         "launches": launches,
         "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
         "share_of_step": round(gemm_ms / (dt * 1e3), 4),
@@ -254,13 +285,13 @@ def roofline(timer, dt):
 
 def cpu_baseline_c3(torch):
     """torch-CPU unfold-free restatement (index -> take -> int64 sum) of the
-    config-3 BGEMM on a bounded sample: one batch element, first 64 rows."""
+    config-3 BGEMM on a bounded sample: 40960 of the 131072 rows (about 10 s)."""
     from approxtorch_amd import workloads
     from oracle import torch_cpu
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(3)
-    K, rows = 2304, 2048
+    K, rows = 2304, 40960
     xi = torch.randint(0, 256, (1, K, rows), generator=g, dtype=torch.int64)
     wi = torch.randint(0, 256, (256, K), generator=g, dtype=torch.int64)
     lut = torch.from_numpy(workloads.lut_perturbed(3)).to(torch.int64)
@@ -291,7 +322,7 @@ def main_c3(torch, args):
         "data": "synthetic (seeded uniform int8 operands, perturbed-product LUT)",
         "config": {"workload": "c3: LUT-BGEMM B=32 A[4096x2304] W[2304x256] int8",
                    "lut_macs_per_step": macs, "parallelism": "single GPU"},
-        "roofline": roofline(timer, dt),
+        "roofline": roofline(timer, dt, GEMM_TRAFFIC["c3"]),
     }
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
