@@ -10,189 +10,563 @@
 // holds).  Reference: csrc/claude/bgemm_lre_backward_claude.cu:443-524 (cuBLAS
 // SGEMMs) and nn/bgemm_int8.py:184-207,277-290 (cuDNN convolution_backward).
 //
-// Kernel: 128x128 block tile, 16-deep k-tile, 256 threads (2x2 waves of
-// 64x64, each 2x2 v_mfma_f32_32x32x2f32), double-buffered LDS tiles fed by
-// register prefetch.  gfx950 has no reduced-precision fp32 mode, so results
-// are plain fp32 products with fp32 accumulation.
+// Kernel: BM x BN block tile (64 or 128 each), 32-deep k-tiles, 256 threads
+// as 2 x 2 waves, each wave (BM/2) x (BN/2) in v_mfma_f32_16x16x4f32 tiles.
+// The 256-entry table lives in LDS.  Operand tiles go HBM -> registers (raw:
+// bytes or floats, 16-byte loads where the operand is contiguous) while the
+// previous tile is multiplied, then through the table into a second LDS
+// buffer; one barrier per k-tile.  The table lookup happens at the LDS store
+// so the global loads of the next tile stay in flight during the MFMAs.
+// LDS tiles are laid out so that the MFMA operand reads (lane = (row
+// lane & 15, k lane >> 4)) are bank-conflict-free:
+//   KMajor [BK][B + 16]  when the operand is contiguous along m in HBM,
+//   PMajor [B][BK + 4]   when it is contiguous along the contraction index.
+// The backward-data GEMM folds the batch into its columns (c = n*L + l), so
+// small images waste no tile width.  gfx950 has no reduced-precision fp32
+// mode: plain fp32 products, fp32 accumulation.
 
 #include "atx_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace atx {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
-constexpr int GT = 256;
-constexpr int LDA = BM + 4, LDB = BN + 4;   // padded LDS rows (bank spread)
+constexpr int BK = 32;          // contraction depth of one k-tile
+constexpr int GT = 256;         // threads per block (2 x 2 waves)
+constexpr int LDP = BK + 4;     // floats per row of a PMajor tile
 
-// Loader for the data-gradient GEMM, batch n = blockIdx.z:
-//   A(m = k, p = o) = Tx[wq[o*K + k]],  B(p = o, j = l) = go[n][o][l].
-struct DataOperands {
-  const uint8_t* wq; const float* go; const float* tx;
-  int K, O, L;
-  __device__ float a(int m, int p, int) const {
-    return (m < K && p < O) ? tx[wq[(long long)p * K + m]] : 0.0f;
-  }
-  __device__ float b(int p, int j, int n) const {
-    return (p < O && j < L) ? go[((long long)n * O + p) * L + j] : 0.0f;
-  }
+template <int B> struct KMajor {          // [BK][B + 16]: bank(k, i) = 16k + i
+  static constexpr int LD = B + 16;
+  static constexpr int SIZE = BK * LD;
+  __device__ static int at(int m, int k) { return k * LD + m; }
+};
+template <int B> struct PMajor {          // [B][BK + 4]: bank(i, k) = 36i + k
+  static constexpr int SIZE = B * LDP;
+  __device__ static int at(int m, int k) { return m * LDP + k; }
 };
 
-// Loader for the weight-gradient GEMM (p = n*L + l):
-//   A(m = o, p) = go[n][o][l],  B(p, j = k) = Tw[index of image tap k at l].
-template <typename T>
-struct WeightOperands {
-  const float* go; const T* img; const float* tw; const float* pad_dev;
-  atx_conv_geom g; int O, K, L, P, offset, pad_index;
-  __device__ float a(int m, int p, int) const {
-    if (m >= O || p >= P) return 0.0f;
-    const int n = p / L, l = p - (p / L) * L;
-    return go[((long long)n * O + m) * L + l];
-  }
-  __device__ float b(int p, int j, int) const {
-    if (p >= P || j >= K) return 0.0f;
-    const int n = p / L, l = p - (p / L) * L;
-    const int KK = g.KH * g.KW;
-    const int c = j / KK, t = j - (j / KK) * KK;
-    const int kh = t / g.KW, kw = t - (t / g.KW) * g.KW;
-    const int oh = l / g.OW, ow = l - (l / g.OW) * g.OW;
-    const int ih = oh * g.SH + kh * g.DH - g.PH;
-    const int iw = ow * g.SW + kw * g.DW - g.PW;
-    unsigned v = pad_dev ? quant_index(pad_dev[0], 0) : (unsigned)pad_index;
-    if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W) {
-      const T x = img[(((long long)n * g.C + c) * g.H + ih) * g.W + iw];
-      if constexpr (sizeof(T) == 4) v = quant_index((float)x, offset);
-      else if constexpr (std::is_same<T, int8_t>::value) v = (unsigned)((int)x + 128);
-      else v = (unsigned)x;
-    }
-    return tw[v];
-  }
-};
-
-// Thread -> element maps for the tile loads.  The A tile is stored [p][m],
-// B as [p][j].  `m_fast`: consecutive threads walk m (else p) for coalescing.
-template <bool M_FAST>
-__device__ __forceinline__ void tile_coord(int t, int i, int& p, int& m) {
-  const int e = t + i * GT;                 // 0 .. BM*BK-1
-  if (M_FAST) { m = e % BM; p = e / BM; }
-  else { p = e % BK; m = e / BK; }
+// Index of an image element (int8: v + 128, uint8: v, fp32: quant_index).
+template <typename T> __device__ __forceinline__ unsigned img_index(unsigned raw, int offset);
+template <> __device__ __forceinline__ unsigned img_index<int8_t>(unsigned raw, int) {
+  return (raw + 128u) & 255u;
+}
+template <> __device__ __forceinline__ unsigned img_index<uint8_t>(unsigned raw, int) {
+  return raw & 255u;
+}
+template <> __device__ __forceinline__ unsigned img_index<float>(unsigned raw, int offset) {
+  return quant_index(__uint_as_float(raw), offset);
 }
 
-template <typename OPS, bool A_M_FAST, bool B_J_FAST>
-__global__ void __launch_bounds__(GT, 2)
-mfma_gemm_kernel(OPS ops, int M, int N, int P, int p_chunk, float* __restrict__ out,
-                 long long out_bstride, long long out_sstride) {
-  __shared__ float As[2][BK][LDA];
-  __shared__ float Bs[2][BK][LDB];
+// ------------------------------------------------------------- operand loaders
+// Each loader owns a BK x B slice of one operand: fetch() issues the global
+// loads of k-tile p0 into registers, stash() maps them through the LDS table
+// (if any) and stores them into an LDS tile.  fetch() has no branches: an
+// element outside the operand loads element 0 instead and its validity bit
+// zeroes it in stash(), so the compiler never waits for a load before the
+// MFMAs that follow.  VEC: the operand's quads are 16-byte (4-byte for
+// bytes) aligned and never straddle a row, so one vector load covers them.
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int zb = blockIdx.z;
-  // grid.z enumerates (batch, split): z = batch * S + s
-  const int S = (P + p_chunk - 1) / p_chunk;
-  const int batch = zb / S, s = zb % S;
-  const int pb = s * p_chunk, pe = min(P, pb + p_chunk);
-
-  floatx16 acc[2][2];
+// Backward-data A: A(m = k, p = o) = tx[wq[o*K + k]], KMajor.
+template <int B, bool VEC> struct DataA {
+  using Lay = KMajor<B>;
+  static constexpr int QPR = B / 4, NQ = BK * B / (4 * GT), PSTEP = GT / QPR;
+  const uint8_t* wq; int K;
+  int mq, pr, gm;
+  unsigned raw[NQ], ok;
+  __device__ void init(int t, int m0) {
+    mq = (t % QPR) * 4; pr = t / QPR; gm = m0 + mq;
+  }
+  __device__ void fetch(int p0, int pe) {
+    ok = 0;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NQ; ++i) {
+      const int p = p0 + pr + i * PSTEP;
+      const long long row = (long long)p * K;
+      if constexpr (VEC) {
+        const bool v = p < pe && gm < K;
+        raw[i] = *(const unsigned*)(wq + (v ? row + gm : 0));
+        ok |= (v ? 15u : 0u) << (4 * i);
+      } else {
+        raw[i] = 0;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  constexpr int PER = BM * BK / GT;   // 8 elements per thread per tile
-  float ra[PER], rb[PER];
-  auto fetch = [&](int p0) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      int p, m;
-      tile_coord<A_M_FAST>(t, i, p, m);
-      const int gp = p0 + p;
-      ra[i] = (gp < pe) ? ops.a(m0 + m, gp, batch) : 0.0f;
-      int pj, j;
-      tile_coord<B_J_FAST>(t, i, pj, j);
-      const int gpj = p0 + pj;
-      rb[i] = (gpj < pe) ? ops.b(gpj, n0 + j, batch) : 0.0f;
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      int p, m;
-      tile_coord<A_M_FAST>(t, i, p, m);
-      As[buf][p][m] = ra[i];
-      int pj, j;
-      tile_coord<B_J_FAST>(t, i, pj, j);
-      Bs[buf][pj][j] = rb[i];
-    }
-  };
-
-  if (pb < pe) {
-    fetch(pb);
-    stash(0);
-    __syncthreads();
-    int buf = 0;
-    for (int p0 = pb; p0 < pe; p0 += BK) {
-      const bool more = p0 + BK < pe;
-      if (more) fetch(p0 + BK);
-#pragma unroll
-      for (int kk = 0; kk < BK; kk += 2) {
-        const int kr = kk + (lane >> 5);
-        float av[2], bv[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) av[i] = As[buf][kr][wm * 64 + i * 32 + (lane & 31)];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) bv[j] = Bs[buf][kr][wn * 64 + j * 32 + (lane & 31)];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          const bool v = p < pe && gm + e < K;
+          raw[i] |= (unsigned)wq[v ? row + gm + e : 0] << (8 * e);
+          ok |= (v ? 1u : 0u) << (4 * i + e);
+        }
       }
-      if (more) stash(buf ^ 1);
-      __syncthreads();
-      buf ^= 1;
     }
   }
-
-  // D layout of 32x32x2: lane holds rows 8*(r/4) + 4*(lane/32) + r%4, col lane%32.
-  float* o = out + (long long)batch * out_bstride + (long long)s * out_sstride;
+  __device__ void stash(float* s, const float* tab) const {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NQ; ++i) {
+      floatx4 v;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (row < M && col < N) o[(long long)row * N + col] = acc[i][j][r];
+      for (int e = 0; e < 4; ++e) {
+        const float x = tab[(raw[i] >> (8 * e)) & 255u];
+        v[e] = (ok >> (4 * i + e)) & 1u ? x : 0.0f;
       }
+      *(floatx4*)&s[Lay::at(mq, pr + i * PSTEP)] = v;
+    }
+  }
+  __device__ void advance() {}
+};
+
+// Backward-data B: B(p = o, j = c) = go[n][o][l] with c = n*L + l, KMajor.
+template <int B, bool VEC> struct DataB {
+  using Lay = KMajor<B>;
+  static constexpr int QPR = B / 4, NQ = BK * B / (4 * GT), PSTEP = GT / QPR;
+  const float* go; int O, L, NL;
+  int jq, pr;
+  long long base[4];        // go offset of column c + e at o = 0 (-1: no column)
+  floatx4 raw[NQ];
+  unsigned ok;
+  __device__ void init(int t, int n0) {
+    jq = (t % QPR) * 4; pr = t / QPR;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = n0 + jq + e;
+      if (c < NL) {
+        const int n = c / L;
+        base[e] = (long long)n * O * L + (c - n * L);
+      } else {
+        base[e] = -1;
+      }
+    }
+  }
+  __device__ void fetch(int p0, int pe) {
+    ok = 0;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int o = p0 + pr + i * PSTEP;
+      const long long ol = (long long)o * L;
+      if constexpr (VEC) {
+        const bool v = o < pe && base[0] >= 0;
+        raw[i] = *(const floatx4*)(go + (v ? base[0] + ol : 0));
+        ok |= (v ? 15u : 0u) << (4 * i);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool v = o < pe && base[e] >= 0;
+          raw[i][e] = go[v ? base[e] + ol : 0];
+          ok |= (v ? 1u : 0u) << (4 * i + e);
+        }
+      }
+    }
+  }
+  __device__ void stash(float* s, const float*) const {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] : 0.0f;
+      *(floatx4*)&s[Lay::at(jq, pr + i * PSTEP)] = v;
+    }
+  }
+  __device__ void advance() {}
+};
+
+// Rows r = n*L + l of the weight GEMM's contraction, tracked incrementally:
+// the thread's quad starts at r = p0 + pq and moves by BK per k-tile.
+struct RowCursor {
+  int n, l;
+  __device__ void start(int r, int L) { n = r / L; l = r - n * L; }
+  __device__ void step(int d, int L) {
+    l += d;
+    while (l >= L) { l -= L; ++n; }
+  }
+};
+
+// Backward-weight A: A(m = o, p = r) = go[n][o][l], PMajor.  VEC needs
+// L % 4 == 0 (quads of rows then share an image and P is a multiple of 4).
+template <int B, bool VEC> struct WeightA {
+  using Lay = PMajor<B>;
+  static constexpr int NQ = B / 32;        // quads per thread (rows m, m+32, ...)
+  const float* go; int O, L;
+  int pq, mr, m0;
+  RowCursor cur;
+  floatx4 raw[NQ];
+  unsigned ok;
+  __device__ void init(int t, int mbase, int pb) {
+    pq = (t & 7) * 4; mr = t >> 3; m0 = mbase;
+    cur.start(pb + pq, L);
+  }
+  __device__ void fetch(int p0, int pe) {
+    const int r = p0 + pq;
+    long long rb[4];
+    bool rv[4];
+    {
+      int n = cur.n, l = cur.l;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        rv[e] = r + e < pe;
+        rb[e] = (long long)n * O * L + l;
+        if (++l == L) { l = 0; ++n; }
+      }
+    }
+    ok = 0;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int o = m0 + mr + 32 * i;
+      const long long ol = (long long)o * L;
+      if constexpr (VEC) {
+        const bool v = o < O && rv[0];
+        raw[i] = *(const floatx4*)(go + (v ? rb[0] + ol : 0));
+        ok |= (v ? 15u : 0u) << (4 * i);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool v = o < O && rv[e];
+          raw[i][e] = go[v ? rb[e] + ol : 0];
+          ok |= (v ? 1u : 0u) << (4 * i + e);
+        }
+      }
+    }
+  }
+  __device__ void stash(float* s, const float*) const {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] : 0.0f;
+      *(floatx4*)&s[Lay::at(mr + 32 * i, pq)] = v;
+    }
+  }
+  __device__ void advance() { cur.step(BK, L); }
+};
+
+// Backward-weight B: B(p = r, j = k) = tw[index of image tap k at output
+// position r] (implicit im2col), PMajor.  Out-of-image taps use `pad`.
+template <int B, typename T> struct WeightB {
+  using Lay = PMajor<B>;
+  static constexpr int NQ = B / 32;
+  const T* img; atx_conv_geom g; int K, L, offset, pad;
+  int pq, jr;
+  int coff[NQ], dh[NQ], dw[NQ];     // per tap: c*H*W, kh*DH - PH, kw*DW - PW
+  unsigned kv;                      // bit i: tap i < K
+  int n, oh, ow;                    // output position of row p0 + pq
+  unsigned raw[NQ][4], ok, in;      // in: in-image bit, ok: valid element bit
+  __device__ void init(int t, int n0, int pb) {
+    pq = (t & 7) * 4; jr = t >> 3;
+    const int KK = g.KH * g.KW;
+    kv = 0;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int k = n0 + jr + 32 * i;
+      const int kc = k < K ? k : 0;
+      const int c = kc / KK, tt = kc - c * KK;
+      const int kh = tt / g.KW, kw = tt - kh * g.KW;
+      coff[i] = c * g.H * g.W;
+      dh[i] = kh * g.DH - g.PH;
+      dw[i] = kw * g.DW - g.PW;
+      if (k < K) kv |= 1u << i;
+    }
+    const int r = pb + pq;
+    n = r / L;
+    const int l = r - n * L;
+    oh = l / g.OW;
+    ow = l - oh * g.OW;
+  }
+  __device__ void fetch(int p0, int pe) {
+    const int r = p0 + pq;
+    ok = 0; in = 0;
+    int en = n, eh = oh, ew = ow;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool rv = r + e < pe;
+      const long long nb = (long long)en * g.C * g.H * g.W;
+      const int ih0 = eh * g.SH, iw0 = ew * g.SW;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const int ih = ih0 + dh[i], iw = iw0 + dw[i];
+        const bool v = rv && ((kv >> i) & 1u);
+        const bool inside = v && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+        const T x = img[inside ? nb + coff[i] + ih * g.W + iw : 0];
+        if constexpr (sizeof(T) == 4) raw[i][e] = __float_as_uint((float)x);
+        else raw[i][e] = (unsigned)(unsigned char)x;
+        ok |= (v ? 1u : 0u) << (4 * i + e);
+        in |= (inside ? 1u : 0u) << (4 * i + e);
+      }
+      if (++ew == g.OW) { ew = 0; if (++eh == g.OH) { eh = 0; ++en; } }
+    }
+  }
+  __device__ void stash(float* s, const float* tab) const {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int b = 4 * i + e;
+        const unsigned idx = (in >> b) & 1u ? img_index<T>(raw[i][e], offset) : (unsigned)pad;
+        const float x = tab[idx];
+        v[e] = (ok >> b) & 1u ? x : 0.0f;
+      }
+      *(floatx4*)&s[Lay::at(jr + 32 * i, pq)] = v;
+    }
+  }
+  __device__ void advance() {
+    ow += BK;
+    while (ow >= g.OW) {
+      ow -= g.OW;
+      if (++oh == g.OH) { oh = 0; ++n; }
+    }
+  }
+};
+
+// ------------------------------------------------------------------ epilogues
+// out[n][k][l] of the backward-data GEMM (rows m = k, columns c = n*L + l).
+struct DataOut { float* col; int K, L, NL; };
+// ws[s][o][k] of the backward-weight GEMM.
+struct WeightOut {
+  float* ws; int O, K; long long sst;
+  __device__ void store(int m, int c, float v, int s) const {
+    if (m < O && c < K) ws[(long long)s * sst + (long long)m * K + c] = v;
+  }
+};
+
+// ----------------------------------------------------------------- main kernel
+template <int BM, int BN, class LA, class LB>
+__device__ __forceinline__ void mma_tile(const float* As, const float* Bs,
+                                         floatx4 (&acc)[BM / 32][BN / 32]) {
+  constexpr int TM = BM / 32, TN = BN / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, lk = lane >> 4;
+#pragma unroll
+  for (int kk = 0; kk < BK; kk += 4) {
+    float a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = As[LA::Lay::at(wm * (BM / 2) + i * 16 + li, kk + lk)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j] = Bs[LB::Lay::at(wn * (BN / 2) + j * 16 + li, kk + lk)];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// acc = sum over the contraction range [pb, pe) of A tile x B tile.
+// Double-buffered: the global loads of k-tile i+1 are in flight while tile i
+// is multiplied; one barrier per k-tile.
+template <int BM, int BN, class LA, class LB>
+__device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int pb, int pe,
+                                           floatx4 (&acc)[BM / 32][BN / 32], float* As0,
+                                           float* As1, float* Bs0, float* Bs1) {
+#pragma unroll
+  for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+    for (int j = 0; j < BN / 32; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (pb >= pe) return;
+
+  la.fetch(pb, pe);
+  lb.fetch(pb, pe);
+  la.stash(As0, tab);
+  lb.stash(Bs0, tab);
+  __syncthreads();
+  float *Ac = As0, *An = As1, *Bc = Bs0, *Bn = Bs1;
+  for (int p0 = pb; p0 + BK < pe; p0 += BK) {
+    la.advance(); lb.advance();
+    la.fetch(p0 + BK, pe);
+    lb.fetch(p0 + BK, pe);
+    // Keep the next tile's loads ahead of the MFMAs and their consumers
+    // behind them: the scheduler would otherwise sink the loads, or hoist
+    // the stash's use of them, and expose the load latency.
+    __builtin_amdgcn_sched_barrier(0);
+    mma_tile<BM, BN, LA, LB>(Ac, Bc, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    la.stash(An, tab);
+    lb.stash(Bn, tab);
+    __syncthreads();
+    float* x = Ac; Ac = An; An = x;
+    x = Bc; Bc = Bn; Bn = x;
+  }
+  mma_tile<BM, BN, LA, LB>(Ac, Bc, acc);
+}
+
+// D layout of 16x16x4 f32: lane holds rows 4*(lane >> 4) + r, column lane & 15.
+template <int BM, int BN, bool VA, bool VB>
+__global__ void __launch_bounds__(GT, 2)
+data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB> lb, DataOut ep, const float* __restrict__ tx,
+                 int O) {
+  __shared__ float tab[256];
+  __shared__ __align__(16) float As[2][KMajor<BM>::SIZE];
+  __shared__ __align__(16) float Bs[2][KMajor<BN>::SIZE];
+  const int t = threadIdx.x;
+  tab[t] = tx[t];
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  la.init(t, m0);
+  lb.init(t, n0);
+  __syncthreads();
+  floatx4 acc[BM / 32][BN / 32];
+  gemm_tiles<BM, BN>(la, lb, tab, 0, O, acc, As[0], As[1], Bs[0], Bs[1]);
+  const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int j = 0; j < BN / 32; ++j) {
+    const int c = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
+    if (c >= ep.NL) continue;
+    const int n = c / ep.L;
+    float* dst = ep.col + (long long)n * ep.K * ep.L + (c - n * ep.L);
+#pragma unroll
+    for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+        if (m < ep.K) dst[(long long)m * ep.L] = acc[i][j][r];
+      }
+  }
+}
+
+template <int BM, int BN, bool VA, typename T>
+__global__ void __launch_bounds__(GT, 2)
+weight_gemm_kernel(WeightA<BM, VA> la, WeightB<BN, T> lb, WeightOut ep,
+                   const float* __restrict__ tw, const float* __restrict__ pad_dev,
+                   int P, int p_chunk) {
+  __shared__ float tab[256];
+  __shared__ __align__(16) float As[2][PMajor<BM>::SIZE];
+  __shared__ __align__(16) float Bs[2][PMajor<BN>::SIZE];
+  const int t = threadIdx.x;
+  tab[t] = tw[t];
+  if (pad_dev) lb.pad = (int)quant_index(pad_dev[0], 0);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int s = blockIdx.z;
+  const int pb = s * p_chunk, pe = min(P, pb + p_chunk);
+  la.init(t, m0, pb);
+  lb.init(t, n0, pb);
+  __syncthreads();
+  floatx4 acc[BM / 32][BN / 32];
+  gemm_tiles<BM, BN>(la, lb, tab, pb, pe, acc, As[0], As[1], Bs[0], Bs[1]);
+  const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+    for (int j = 0; j < BN / 32; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ep.store(m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r,
+                 n0 + wn * (BN / 2) + j * 16 + (lane & 15), acc[i][j][r], s);
 }
 
 // gw[i] = sum_s ws[s][i]; optional fused per-channel fake-quant backward:
-// gw = mask ? sum / max(scale[o], 1e-12) : 0 with o = i / K.
-__global__ void split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K,
-                                 const uint8_t* __restrict__ mask,
-                                 const float* __restrict__ scale, float* __restrict__ out) {
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel; i += stride) {
-    float a = 0.0f;
-    for (int s = 0; s < S; ++s) a += ws[(long long)s * numel + i];
+// gw = mask ? sum / max(scale[o], 1e-12) : 0 with o = i / K.  A block sums
+// 256 / G consecutive elements over G groups of slices (group g takes slices
+// g, g + G, ...), then adds the G partials in group order: deterministic.
+__global__ void __launch_bounds__(256)
+split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, int G,
+                 const uint8_t* __restrict__ mask, const float* __restrict__ scale,
+                 float* __restrict__ out) {
+  __shared__ float part[256];
+  const int t = threadIdx.x;
+  const int epb = 256 / G;
+  const int e = t % epb, grp = t / epb;
+  const long long i = (long long)blockIdx.x * epb + e;
+  float a = 0.0f;
+  if (i < numel)
+    for (int s = grp; s < S; s += G) a += ws[(long long)s * numel + i];
+  part[t] = a;
+  __syncthreads();
+  if (grp == 0 && i < numel) {
+    for (int g = 1; g < G; ++g) a += part[g * epb + e];
     if (mask) a = (mask[i] ? a : 0.0f) / fmaxf(scale[i / K], 1e-12f);
     out[i] = a;
   }
 }
 
-// Split of the weight-gradient contraction: enough blocks to fill 256 CUs.
-static int weight_splits(int M, int N, long long P) {
-  const long long tiles = cdiv(M, BM) * cdiv(N, BN);
+// Launch of split_sum_kernel: enough groups that the grid has >= 1024 blocks.
+static int launch_split_sum(const float* ws, int S, long long numel, int K,
+                            const uint8_t* mask, const float* scale, float* out,
+                            hipStream_t stream) {
+  int G = 1;
+  while (G < 64 && G < S && cdiv(numel, 256 / G) < 1024) G *= 2;
+  const long long blocks = cdiv(numel, 256 / G);
+  ATX_REQUIRE(blocks <= 0x7fffffffLL, "split_sum: too many elements");
+  hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, ws, S,
+                     numel, K, G, mask, scale, out);
+  return check_launch("split_sum_kernel");
+}
+
+inline int tile_of(int extent) { return extent <= 64 ? 64 : 128; }
+
+// Split of the weight-gradient contraction: enough blocks to fill 256 CUs
+// (two blocks each, four rounds), every split at least four k-tiles deep.
+static int weight_splits(int O, int K, long long P) {
+  const long long tiles = cdiv(O, tile_of(O)) * cdiv(K, tile_of(K));
   long long s = 1;
-  while (tiles * s < 1024 && P / (s * 2) >= 4 * BK) s *= 2;
+  while (tiles * s < 2048 && P / (s * 2) >= 4 * BK) s *= 2;
   return (int)s;
+}
+
+template <int BM, int BN, bool VA, bool VB>
+static void launch_data(const float* go, const uint8_t* wq, const float* tx, int N, int O, int K,
+                        int L, float* col, hipStream_t stream) {
+  const int NL = N * L;
+  DataA<BM, VA> la{};
+  la.wq = wq; la.K = K;
+  DataB<BN, VB> lb{};
+  lb.go = go; lb.O = O; lb.L = L; lb.NL = NL;
+  DataOut ep{col, K, L, NL};
+  dim3 grid((unsigned)cdiv(NL, BN), (unsigned)cdiv(K, BM), 1);
+  hipLaunchKernelGGL((data_gemm_kernel<BM, BN, VA, VB>), grid, dim3(GT), 0, stream, la, lb, ep,
+                     tx, O);
+}
+
+template <int BM>
+static void dispatch_data(const float* go, const uint8_t* wq, const float* tx, int N, int O,
+                          int K, int L, float* col, hipStream_t stream) {
+  const bool va = K % 4 == 0 && (uintptr_t)wq % 4 == 0;
+  const bool vb = L % 4 == 0 && (uintptr_t)go % 16 == 0;
+  if (va && vb) launch_data<BM, 128, true, true>(go, wq, tx, N, O, K, L, col, stream);
+  else if (va) launch_data<BM, 128, true, false>(go, wq, tx, N, O, K, L, col, stream);
+  else if (vb) launch_data<BM, 128, false, true>(go, wq, tx, N, O, K, L, col, stream);
+  else launch_data<BM, 128, false, false>(go, wq, tx, N, O, K, L, col, stream);
+}
+
+template <int BM, int BN, bool VA, typename T>
+static void launch_weight(const float* go, const T* img, atx_conv_geom g, int O, int K, int L,
+                          int P, int chunk, int S, int offset, int pad_index,
+                          const float* pad_dev, const float* tw, float* ws,
+                          hipStream_t stream) {
+  WeightA<BM, VA> la{};
+  la.go = go; la.O = O; la.L = L;
+  WeightB<BN, T> lb{};
+  lb.img = img; lb.g = g; lb.K = K; lb.L = L; lb.offset = offset; lb.pad = pad_index;
+  WeightOut ep{ws, O, K, (long long)O * K};
+  dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)S);
+  hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, T>), grid, dim3(GT), 0, stream, la, lb, ep,
+                     tw, pad_dev, P, chunk);
+}
+
+template <bool VA, typename T>
+static void dispatch_weight_tiles(const float* go, const T* img, atx_conv_geom g, int O, int K,
+                                  int L, int P, int chunk, int S, int offset, int pad_index,
+                                  const float* pad_dev, const float* tw, float* ws,
+                                  hipStream_t stream) {
+  const int bm = tile_of(O), bn = tile_of(K);
+#define ATX_LW(M_, N_)                                                                       \
+  launch_weight<M_, N_, VA, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index, pad_dev, \
+                               tw, ws, stream)
+  if (bm == 64 && bn == 64) ATX_LW(64, 64);
+  else if (bm == 64) ATX_LW(64, 128);
+  else if (bn == 64) ATX_LW(128, 64);
+  else ATX_LW(128, 128);
+#undef ATX_LW
+}
+
+template <typename T>
+static void dispatch_weight(const float* go, const T* img, atx_conv_geom g, int O, int K, int L,
+                            int P, int chunk, int S, int offset, int pad_index,
+                            const float* pad_dev, const float* tw, float* ws,
+                            hipStream_t stream) {
+  if (L % 4 == 0 && (uintptr_t)go % 16 == 0)
+    dispatch_weight_tiles<true, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index, pad_dev,
+                                   tw, ws, stream);
+  else
+    dispatch_weight_tiles<false, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index,
+                                    pad_dev, tw, ws, stream);
 }
 
 }  // namespace atx
@@ -208,19 +582,14 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx, i
   ATX_REQUIRE(col, "atx_conv_bwd_data_col: null output");
   if (O == 0) {
     // Empty contraction: the split-sum kernel with S = 0 writes zeros.
-    const long long numel = (long long)N * K * L;
-    hipLaunchKernelGGL(split_sum_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0, stream,
-                       (const float*)nullptr, 0, numel, K, (const uint8_t*)nullptr,
-                       (const float*)nullptr, col);
-    return check_launch("split_sum_kernel");
+    return launch_split_sum(nullptr, 0, (long long)N * K * L, K, nullptr, nullptr, col, stream);
   }
   ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data_col: null pointer");
-  ATX_REQUIRE(N <= 65535, "atx_conv_bwd_data_col: batch too large");
-  DataOperands ops{wq, go, tx, K, O, L};
-  dim3 grid((unsigned)cdiv(L, BN), (unsigned)cdiv(K, BM), (unsigned)N);
-  hipLaunchKernelGGL((mfma_gemm_kernel<DataOperands, true, true>), grid, dim3(GT), 0, stream,
-                     ops, K, L, O, O > 0 ? O : 1, col, (long long)K * L, 0LL);
-  return check_launch("mfma_gemm_kernel<data>");
+  ATX_REQUIRE((long long)N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
+              "atx_conv_bwd_data_col: sizes too large");
+  if (tile_of(K) == 64) dispatch_data<64>(go, wq, tx, N, O, K, L, col, stream);
+  else dispatch_data<128>(go, wq, tx, N, O, K, L, col, stream);
+  return check_launch("data_gemm_kernel");
 }
 
 long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P) {
@@ -244,38 +613,25 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_ge
   ATX_REQUIRE(gw && tw && (!mask_w || scale_w), "atx_conv_bwd_weight: null pointer");
   if (P == 0) {
     // Empty contraction: the split-sum kernel with S = 0 writes zeros.
-    hipLaunchKernelGGL(split_sum_kernel, dim3(elem_grid((long long)O * K, 256)), dim3(256), 0,
-                       stream, (const float*)nullptr, 0, (long long)O * K, K,
-                       (const uint8_t*)nullptr, scale_w, gw);
-    return check_launch("split_sum_kernel");
+    return launch_split_sum(nullptr, 0, (long long)O * K, K, nullptr, scale_w, gw, stream);
   }
   ATX_REQUIRE(go && img && workspace, "atx_conv_bwd_weight: null operand/workspace");
+  ATX_REQUIRE(cdiv(O, 64) <= 65535, "atx_conv_bwd_weight: too many output channels");
   const int S = weight_splits(O, K, P);
   const int chunk = (int)(cdiv(cdiv(P, S), BK) * BK);
   const int Sreal = (int)cdiv(P, chunk);
-  dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)Sreal);
-  const long long sst = (long long)O * K;
-  if (dtype == 0) {
-    WeightOperands<int8_t> ops{go, (const int8_t*)img, tw, pad_dev, g, O, K, L, (int)P, 128,
-                               pad_index};
-    hipLaunchKernelGGL((mfma_gemm_kernel<WeightOperands<int8_t>, false, false>), grid, dim3(GT),
-                       0, stream, ops, O, K, (int)P, chunk, workspace, 0LL, sst);
-  } else if (dtype == 1) {
-    WeightOperands<uint8_t> ops{go, (const uint8_t*)img, tw, pad_dev, g, O, K, L, (int)P, 0,
-                                pad_index};
-    hipLaunchKernelGGL((mfma_gemm_kernel<WeightOperands<uint8_t>, false, false>), grid,
-                       dim3(GT), 0, stream, ops, O, K, (int)P, chunk, workspace, 0LL, sst);
-  } else {
-    WeightOperands<float> ops{go, (const float*)img, tw, pad_dev, g, O, K, L, (int)P,
-                              f32_offset, pad_index};
-    hipLaunchKernelGGL((mfma_gemm_kernel<WeightOperands<float>, false, false>), grid, dim3(GT),
-                       0, stream, ops, O, K, (int)P, chunk, workspace, 0LL, sst);
-  }
-  int rc = check_launch("mfma_gemm_kernel<weight>");
+  if (dtype == 0)
+    dispatch_weight<int8_t>(go, (const int8_t*)img, g, O, K, L, (int)P, chunk, Sreal, 128,
+                            pad_index, pad_dev, tw, workspace, stream);
+  else if (dtype == 1)
+    dispatch_weight<uint8_t>(go, (const uint8_t*)img, g, O, K, L, (int)P, chunk, Sreal, 0,
+                             pad_index, pad_dev, tw, workspace, stream);
+  else
+    dispatch_weight<float>(go, (const float*)img, g, O, K, L, (int)P, chunk, Sreal,
+                           f32_offset, pad_index, pad_dev, tw, workspace, stream);
+  int rc = check_launch("weight_gemm_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(split_sum_kernel, dim3(elem_grid(sst, 256)), dim3(256), 0, stream,
-                     workspace, Sreal, sst, K, mask_w, scale_w, gw);
-  return check_launch("split_sum_kernel");
+  return launch_split_sum(workspace, Sreal, (long long)O * K, K, mask_w, scale_w, gw, stream);
 }
 
 }  // extern "C"

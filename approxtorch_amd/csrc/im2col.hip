@@ -24,8 +24,10 @@ template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int o
 }
 
 // xt[slot][r] = row_offset(index of tap operand_tap(slot, r) at output
-// position r); rows r >= N*L and taps k >= K hold 0.  The grid stride over r
-// is a multiple of 16, so every thread keeps one (r >> 2) & 3 and one tap.
+// position r); rows r >= N*L and taps k >= K hold 0.  A thread writes the
+// four rows of a quad (one tap: the tap changes every four rows) as one
+// 8-byte store; the grid stride over quads is a multiple of 4, so every
+// thread keeps one tap per slot and its decomposition is hoisted.
 template <typename T>
 __global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset,
                                    int pad_index, const float* __restrict__ pad_dev,
@@ -35,30 +37,42 @@ __global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, i
   const int R = g.N * L;
   const int KK = g.KH * g.KW;
   const int K = g.C * KK;
-  const int r0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int HW = g.H * g.W;
+  const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int qstride = gridDim.x * blockDim.x;
+  const int nquad = Rpad >> 2;
   for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
-    const int k = operand_tap(slot, r0);
+    const int k = operand_tap(slot, q0 << 2);
     const int c = k / KK;
     const int t = k - c * KK;
     const int kh = t / g.KW;
     const int kw = t - kh * g.KW;
     const int ih0 = kh * g.DH - g.PH;
     const int iw0 = kw * g.DW - g.PW;
-    for (int r = r0; r < Rpad; r += gridDim.x * blockDim.x) {
-      unsigned off = 0;
-      if (r < R && k < K) {
-        const int n = r / L;
-        const int l = r - n * L;
-        const int oh = l / g.OW;
-        const int ow = l - oh * g.OW;
-        const int ih = oh * g.SH + ih0;
-        const int iw = ow * g.SW + iw0;
-        unsigned v = (unsigned)pad_index;
-        if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-          v = elem_index<T>(img[(((long long)n * g.C + c) * g.H + ih) * g.W + iw], offset);
-        off = row_offset(v);
+    const long long cbase = (long long)c * HW;
+    uint16_t* dst = xt + (long long)slot * Rpad;
+    for (int q = q0; q < nquad; q += qstride) {
+      const int r0 = q << 2;
+      unsigned off[4] = {0u, 0u, 0u, 0u};
+      if (k < K && r0 < R) {
+        int n = r0 / L;
+        const int l = r0 - n * L;
+        int oh = l / g.OW;
+        int ow = l - oh * g.OW;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (r0 + e < R) {
+            const int ih = oh * g.SH + ih0;
+            const int iw = ow * g.SW + iw0;
+            unsigned v = (unsigned)pad_index;
+            if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+              v = elem_index<T>(img[(long long)n * g.C * HW + cbase + ih * g.W + iw], offset);
+            off[e] = row_offset(v);
+          }
+          if (++ow == g.OW) { ow = 0; if (++oh == g.OH) { oh = 0; ++n; } }
+        }
       }
-      xt[(long long)slot * Rpad + r] = (uint16_t)off;
+      *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
     }
   }
 }
@@ -261,8 +275,8 @@ int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
   const int K = g.C * g.KH * g.KW;
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && (R == 0 || img), "atx_im2col_rows: null pointer");
-  static_assert(TB % 16 == 0, "grid stride keeps (r >> 2) & 3 per thread");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, TB), 1024),
+  static_assert(TB % 4 == 0, "the grid stride over quads keeps q & 3 per thread");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, TB), 1024),
             (unsigned)std::min(operand_rows(K), 65535));
   if (dtype == 0)
     hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,

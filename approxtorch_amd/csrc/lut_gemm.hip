@@ -112,32 +112,61 @@ __global__ void lut_prepare_kernel(const float* __restrict__ lut,
 
 // ------------------------------------------------------------- operand pack
 // xt[slot][r] = row_offset(x[n][operand_tap(slot, r)][l]) for r < R
-// (r = n*L + l); 0 for r >= R and taps >= K.  The grid stride over r is a
-// multiple of 16, so every thread keeps one tap.
+// (r = n*L + l); 0 for r >= R and taps >= K.  A thread writes the four rows
+// of a quad (one tap) as one 8-byte store; when L % 4 == 0 the quad is four
+// consecutive elements of one x row, read with one 4- (u8) or 16-byte (fp32)
+// load (`vec`: L % 4 == 0 and the pointers aligned for it).  The grid stride over quads is a multiple of 4, so every thread keeps
+// one tap per slot.
 template <typename T>
 __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
                               int offset, uint8_t* __restrict__ xq,
-                              uint16_t* __restrict__ xt, int Rpad) {
+                              uint16_t* __restrict__ xt, int Rpad, bool vec) {
   const int R = N * L;
-  const int r0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int qstride = gridDim.x * blockDim.x;
+  const int nquad = Rpad >> 2;
   for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
-    const int k = operand_tap(slot, r0);
-    for (int r = r0; r < Rpad; r += gridDim.x * blockDim.x) {
-      unsigned off = 0;
-      if (r < R && k < K) {
-        const int n = r / L;
-        const int l = r - n * L;
-        const long long src = ((long long)n * K + k) * L + l;
-        unsigned v;
-        if constexpr (sizeof(T) == 4) {
-          v = quant_index((float)x[src], offset);
-          if (xq) xq[src] = (uint8_t)v;
+    const int k = operand_tap(slot, q0 << 2);
+    uint16_t* dst = xt + (long long)slot * Rpad;
+    for (int q = q0; q < nquad; q += qstride) {
+      const int r0 = q << 2;
+      unsigned v[4] = {0u, 0u, 0u, 0u};
+      bool any = false;
+      if (k < K && r0 < R) {
+        any = true;
+        int n = r0 / L;
+        int l = r0 - n * L;
+        if (vec) {
+          const long long src = ((long long)n * K + k) * L + l;
+          if constexpr (sizeof(T) == 4) {
+            const float4 f = *(const float4*)(x + src);
+            v[0] = quant_index(f.x, offset); v[1] = quant_index(f.y, offset);
+            v[2] = quant_index(f.z, offset); v[3] = quant_index(f.w, offset);
+            if (xq) *(uchar4*)(xq + src) = make_uchar4(v[0], v[1], v[2], v[3]);
+          } else {
+            const unsigned w = *(const unsigned*)(x + src);
+            v[0] = w & 255u; v[1] = (w >> 8) & 255u; v[2] = (w >> 16) & 255u; v[3] = w >> 24;
+          }
         } else {
-          v = (unsigned)x[src];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (r0 + e < R) {
+              const long long src = ((long long)n * K + k) * L + l;
+              if constexpr (sizeof(T) == 4) {
+                v[e] = quant_index((float)x[src], offset);
+                if (xq) xq[src] = (uint8_t)v[e];
+              } else {
+                v[e] = (unsigned)x[src];
+              }
+            }
+            if (++l == L) { l = 0; ++n; }
+          }
         }
-        off = row_offset(v);
       }
-      xt[(long long)slot * Rpad + r] = (uint16_t)off;
+      unsigned off[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) off[e] = (any && r0 + e < R) ? row_offset(v[e]) : 0u;
+      *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
     }
   }
 }
@@ -600,10 +629,11 @@ int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
   if ((long long)K * Rpad == 0) return ATX_OK;
   // an empty x (N*L == 0) only writes the zero padding rows
   ATX_REQUIRE(xt && ((long long)N * L == 0 || x), "atx_pack_x_f32: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024),
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, 256), 1024),
             (unsigned)std::min(operand_rows(K), 65535));
+  const bool vec = L % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)xq % 4 == 0;
   hipLaunchKernelGGL(pack_x_kernel<float>, grid, dim3(256), 0, stream, x, N, K, L,
-                     offset, xq, xt, Rpad);
+                     offset, xq, xt, Rpad, vec);
   return check_launch("pack_x_kernel<float>");
 }
 
@@ -614,10 +644,11 @@ int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad
               "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && ((long long)N * L == 0 || xq), "atx_pack_x_u8: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad, 256), 1024),
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, 256), 1024),
             (unsigned)std::min(operand_rows(K), 65535));
+  const bool vec = L % 4 == 0 && (uintptr_t)xq % 4 == 0;
   hipLaunchKernelGGL(pack_x_kernel<uint8_t>, grid, dim3(256), 0, stream, xq, N, K,
-                     L, 0, (uint8_t*)nullptr, xt, Rpad);
+                     L, 0, (uint8_t*)nullptr, xt, Rpad, vec);
   return check_launch("pack_x_kernel<u8>");
 }
 

@@ -378,3 +378,42 @@ def test_conv_backward_kernels(geom):
     ex, ew = O.gemm_grads(go, xi, wi, "lre", (tx, tw))
     close(gi.cpu().numpy(), O.fold(ex, img.shape, k, s, p, d))
     close(gwk.cpu().numpy(), ew)
+
+
+# (image shape, (kernel, stride, padding, dilation), O, image dtype): multi-tile
+# backward GEMMs over 64- and 128-wide tiles, partial tiles, L % 4 != 0
+# (scalar operand loads), K % 4 != 0, split contractions and every image type.
+BWD_TILED = [
+    ((2, 64, 14, 14), ((3, 3), (1, 1), (1, 1), (1, 1)), 128, "int8"),
+    ((3, 32, 7, 7), ((1, 1), (1, 1), (0, 0), (1, 1)), 64, "uint8"),
+    ((2, 16, 9, 11), ((3, 3), (2, 2), (1, 1), (1, 1)), 200, "float32"),
+    ((1, 3, 20, 20), ((5, 5), (1, 1), (2, 2), (1, 1)), 70, "int8"),
+    ((4, 128, 8, 8), ((1, 1), (1, 1), (0, 0), (1, 1)), 256, "uint8"),
+    ((8, 64, 28, 28), ((1, 1), (2, 2), (0, 0), (1, 1)), 96, "int8"),
+]
+
+
+@pytest.mark.parametrize("case", BWD_TILED)
+def test_conv_backward_kernels_tiled(case):
+    shape, (k, s, p, d), Oc, dtype = case
+    r = gen(zlib.crc32(repr(case).encode()))
+    if dtype == "int8":
+        img = r.integers(-128, 128, shape).astype(np.int8)
+    elif dtype == "uint8":
+        img = r.integers(0, 256, shape).astype(np.uint8)
+    else:
+        img = r.integers(-130, 130, shape).astype(np.float32)
+    K = shape[1] * k[0] * k[1]
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    go = r.standard_normal((shape[0], Oc, g.OH * g.OW)).astype(np.float32)
+    tx = r.standard_normal(256).astype(np.float32)
+    tw = r.standard_normal(256).astype(np.float32)
+    pad = 128 if dtype != "uint8" else 7
+    gi = ops.conv_backward_data(t(go), t(wi), t(tx), g)
+    gwk = ops.conv_backward_weight(t(go), t(img), t(tw), g, Oc, pad)
+    xi = O.im2col_index(O.image_index(img, 128), k, s, p, d, pad)
+    ex, ew = O.gemm_grads(go, xi, wi, "lre", (tx, tw))
+    ax, aw = O.gemm_grads(np.abs(go), xi, wi, "lre", (np.abs(tx), np.abs(tw)))
+    close(gi.cpu().numpy(), O.fold(ex, img.shape, k, s, p, d), O.fold(ax, img.shape, k, s, p, d))
+    close(gwk.cpu().numpy(), ew, aw)
