@@ -202,14 +202,15 @@ def conv_geom(x_shape, kernel_size, stride, padding, dilation):
 
 def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                  pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
-                 pad_dev=None):
+                 pad_dev=None, packed_w=None):
     """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
 
     img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
     offset 128 = signed operands, 0 = unsigned); w: [O, C*KH*KW] fp32
     quantized values or uint8 indices.  Out-of-image taps use pad_index, or
-    the device scalar pad_dev when given.  Returns (y, wq), wq the uint8
-    weight index image."""
+    the device scalar pad_dev when given.  packed_w = (wq, wt, Opad) from the
+    fused weight fake-quant skips the weight packing.  Returns (y, wq), wq the
+    uint8 weight index image."""
     imgc = img.contiguous()
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -221,30 +222,38 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
     L.call("atx_im2col_rows", L.ptr(imgc), _dtype_code(imgc, offset == 0), g, pad_index,
            L.ptr(pad_dev), L.ptr(xt), Rpad, L.stream_of(imgc))
-    wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)
+    if packed_w is None:
+        wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)
+    else:
+        wq, wt, Opad = packed_w
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
     _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
     return y, wq
 
 
-def conv_backward_data(go: Tensor, wq: Tensor, table: Tensor, g, mask=None, scale=None):
-    """grad wrt the quantized image: fold(sum_o go * table[wq]) (+ fused STE mask/s)."""
+def conv_backward_data(go: Tensor, wq: Tensor, table: Tensor, g, mask=None, scale=None,
+                       go_sx=None, go_sw=None):
+    """grad wrt the image: fold(sum_o go' * table[wq]) with go' = go * (sx * sw[o])
+    when go_sx/go_sw are given, and the fake-quant STE (mask ? g : 0) / max(scale, 1e-12)
+    fused when mask is given."""
     goc = go.contiguous()
-    N, K, Lc = g.N, g.C * g.KH * g.KW, g.OH * g.OW
     O = wq.size(0)
-    col = torch.empty((N, K, Lc), dtype=torch.float32, device=goc.device)
-    s = L.stream_of(goc)
-    L.call("atx_conv_bwd_data_col", L.ptr(goc), L.ptr(wq.contiguous()), L.ptr(table), N, O, K,
-           Lc, L.ptr(col), s)
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
-    L.call("atx_col2im", L.ptr(col), g, L.ptr(mask), L.ptr(scale), L.ptr(img), s)
+    wsb = L.query("atx_conv_bwd_data_workspace_bytes", g)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device) if wsb else None
+    L.call("atx_conv_bwd_data", L.ptr(goc), L.ptr(wq.contiguous()), L.ptr(table), g, O,
+           L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask), L.ptr(scale), L.ptr(img), L.ptr(ws),
+           L.stream_of(goc))
     return img
 
 
 def conv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, O: int, pad_index: int,
-                         mask_w=None, scale_w=None, pad_dev=None, unsigned=False):
-    """grad wrt the weights: sum_{n,l} go * table[xi] with implicit im2col."""
+                         mask_w=None, scale_w=None, pad_dev=None, unsigned=False,
+                         go_sx=None, go_sw=None):
+    """grad wrt the weights: sum_{n,l} go' * table[xi] with implicit im2col
+    (go' as in conv_backward_data), the per-channel fake-quant STE fused when
+    mask_w is given."""
     goc, imgc = go.contiguous(), img.contiguous()
     K = g.C * g.KH * g.KW
     P = g.N * g.OH * g.OW
@@ -252,8 +261,8 @@ def conv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, O: int, pad_
     wsb = L.query("atx_conv_bwd_weight_workspace_bytes", O, K, P)
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
     L.call("atx_conv_bwd_weight", L.ptr(goc), L.ptr(imgc), _dtype_code(imgc, unsigned), g, O,
-           pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(mask_w), L.ptr(scale_w), L.ptr(gw),
-           L.ptr(ws), L.stream_of(goc))
+           pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask_w),
+           L.ptr(scale_w), L.ptr(gw), L.ptr(ws), L.stream_of(goc))
     return gw
 
 

@@ -115,17 +115,23 @@ template <int B, bool VEC> struct DataA {
   __device__ void advance() {}
 };
 
-// Backward-data B: B(p = o, j = c) = go[n][o][l] with c = n*L + l, KMajor.
-template <int B, bool VEC> struct DataB {
+// Backward-data B: B(p = o, j = c) = go[n][o][l] (* sx * sw[o] when SCALED)
+// with c = n*L + l, KMajor.  The scale product is rounded to fp32 first and
+// then applied, the order of the layer's `y * (scale_x * scale_w)`.
+template <int B, bool VEC, bool SCALED> struct DataB {
   using Lay = KMajor<B>;
   static constexpr int QPR = B / 4, NQ = BK * B / (4 * GT), PSTEP = GT / QPR;
   const float* go; int O, L, NL;
+  const float* sx; const float* sw;
   int jq, pr;
+  float sx0;
   long long base[4];        // go offset of column c + e at o = 0 (-1: no column)
   floatx4 raw[NQ];
+  float sc[NQ];
   unsigned ok;
   __device__ void init(int t, int n0) {
     jq = (t % QPR) * 4; pr = t / QPR;
+    if constexpr (SCALED) sx0 = sx[0];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = n0 + jq + e;
@@ -143,6 +149,7 @@ template <int B, bool VEC> struct DataB {
     for (int i = 0; i < NQ; ++i) {
       const int o = p0 + pr + i * PSTEP;
       const long long ol = (long long)o * L;
+      if constexpr (SCALED) sc[i] = sw[o < pe ? o : 0];
       if constexpr (VEC) {
         const bool v = o < pe && base[0] >= 0;
         raw[i] = *(const floatx4*)(go + (v ? base[0] + ol : 0));
@@ -161,8 +168,13 @@ template <int B, bool VEC> struct DataB {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       floatx4 v;
+      float f = 1.0f;
+      if constexpr (SCALED) f = sx0 * sc[i];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] : 0.0f;
+      for (int e = 0; e < 4; ++e) {
+        const float x = SCALED ? raw[i][e] * f : raw[i][e];
+        v[e] = (ok >> (4 * i + e)) & 1u ? x : 0.0f;
+      }
       *(floatx4*)&s[Lay::at(jq, pr + i * PSTEP)] = v;
     }
   }
@@ -186,13 +198,20 @@ template <int B, bool VEC> struct WeightA {
   using Lay = PMajor<B>;
   static constexpr int NQ = B / 32;        // quads per thread (rows m, m+32, ...)
   const float* go; int O, L;
+  const float* sx; const float* sw;        // optional go scale sx * sw[o]
   int pq, mr, m0;
   RowCursor cur;
   floatx4 raw[NQ];
+  float sc[NQ];
   unsigned ok;
   __device__ void init(int t, int mbase, int pb) {
     pq = (t & 7) * 4; mr = t >> 3; m0 = mbase;
     cur.start(pb + pq, L);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int o = m0 + mr + 32 * i;
+      sc[i] = sw ? sx[0] * sw[o < O ? o : 0] : 1.0f;
+    }
   }
   __device__ void fetch(int p0, int pe) {
     const int r = p0 + pq;
@@ -231,7 +250,7 @@ template <int B, bool VEC> struct WeightA {
     for (int i = 0; i < NQ; ++i) {
       floatx4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] : 0.0f;
+      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] * sc[i] : 0.0f;
       *(floatx4*)&s[Lay::at(mr + 32 * i, pq)] = v;
     }
   }
@@ -318,7 +337,13 @@ template <int B, typename T> struct WeightB {
 
 // ------------------------------------------------------------------ epilogues
 // out[n][k][l] of the backward-data GEMM (rows m = k, columns c = n*L + l).
-struct DataOut { float* col; int K, L, NL; };
+// With `mask`, the fake-quant STE is applied on the way out:
+// v = (mask ? v : 0) / max(scale, 1e-12) (the 1x1 stride-1 conv, whose
+// columns are the image gradient itself).
+struct DataOut {
+  float* col; int K, L, NL;
+  const uint8_t* mask; const float* scale;
+};
 // ws[s][o][k] of the backward-weight GEMM.
 struct WeightOut {
   float* ws; int O, K; long long sst;
@@ -389,10 +414,10 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
 }
 
 // D layout of 16x16x4 f32: lane holds rows 4*(lane >> 4) + r, column lane & 15.
-template <int BM, int BN, bool VA, bool VB>
+template <int BM, int BN, bool VA, bool VB, bool SC>
 __global__ void __launch_bounds__(GT, 2)
-data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB> lb, DataOut ep, const float* __restrict__ tx,
-                 int O) {
+data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
+                 const float* __restrict__ tx, int O) {
   __shared__ float tab[256];
   __shared__ __align__(16) float As[2][KMajor<BM>::SIZE];
   __shared__ __align__(16) float Bs[2][KMajor<BN>::SIZE];
@@ -405,19 +430,42 @@ data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB> lb, DataOut ep, const float* __
   floatx4 acc[BM / 32][BN / 32];
   gemm_tiles<BM, BN>(la, lb, tab, 0, O, acc, As[0], As[1], Bs[0], Bs[1]);
   const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  constexpr int TM = BM / 32;
 #pragma unroll
   for (int j = 0; j < BN / 32; ++j) {
     const int c = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
-    if (c >= ep.NL) continue;
-    const int n = c / ep.L;
-    float* dst = ep.col + (long long)n * ep.K * ep.L + (c - n * ep.L);
+    const bool cv = c < ep.NL;
+    const int cc = cv ? c : 0;
+    const int n = cc / ep.L;
+    const long long off = (long long)n * ep.K * ep.L + (cc - n * ep.L);
+    if (ep.mask) {
+      // all mask bytes of the column group first (no branch around the loads)
+      const float sdiv = fmaxf(ep.scale[0], 1e-12f);
+      unsigned char mk[TM][4];
 #pragma unroll
-    for (int i = 0; i < BM / 32; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
-        if (m < ep.K) dst[(long long)m * ep.L] = acc[i][j][r];
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+          mk[i][r] = ep.mask[cv && m < ep.K ? off + (long long)m * ep.L : 0];
+        }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+          if (cv && m < ep.K)
+            ep.col[off + (long long)m * ep.L] = (mk[i][r] ? acc[i][j][r] : 0.0f) / sdiv;
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+          if (cv && m < ep.K) ep.col[off + (long long)m * ep.L] = acc[i][j][r];
+        }
+    }
   }
 }
 
@@ -500,38 +548,53 @@ static int weight_splits(int O, int K, long long P) {
   return (int)s;
 }
 
-template <int BM, int BN, bool VA, bool VB>
-static void launch_data(const float* go, const uint8_t* wq, const float* tx, int N, int O, int K,
-                        int L, float* col, hipStream_t stream) {
-  const int NL = N * L;
+struct DataArgs {
+  const float* go; const uint8_t* wq; const float* tx; int N, O, K, L;
+  const float* sx; const float* sw;          // optional go scale sx * sw[o]
+  float* out; const uint8_t* mask; const float* scale;
+};
+
+template <int BM, bool VA, bool VB, bool SC>
+static void launch_data(const DataArgs& a, hipStream_t stream) {
+  constexpr int BN = 128;
+  const int NL = a.N * a.L;
   DataA<BM, VA> la{};
-  la.wq = wq; la.K = K;
-  DataB<BN, VB> lb{};
-  lb.go = go; lb.O = O; lb.L = L; lb.NL = NL;
-  DataOut ep{col, K, L, NL};
-  dim3 grid((unsigned)cdiv(NL, BN), (unsigned)cdiv(K, BM), 1);
-  hipLaunchKernelGGL((data_gemm_kernel<BM, BN, VA, VB>), grid, dim3(GT), 0, stream, la, lb, ep,
-                     tx, O);
+  la.wq = a.wq; la.K = a.K;
+  DataB<BN, VB, SC> lb{};
+  lb.go = a.go; lb.O = a.O; lb.L = a.L; lb.NL = NL; lb.sx = a.sx; lb.sw = a.sw;
+  DataOut ep{a.out, a.K, a.L, NL, a.mask, a.scale};
+  dim3 grid((unsigned)cdiv(NL, BN), (unsigned)cdiv(a.K, BM), 1);
+  hipLaunchKernelGGL((data_gemm_kernel<BM, BN, VA, VB, SC>), grid, dim3(GT), 0, stream, la, lb,
+                     ep, a.tx, a.O);
 }
 
-template <int BM>
-static void dispatch_data(const float* go, const uint8_t* wq, const float* tx, int N, int O,
-                          int K, int L, float* col, hipStream_t stream) {
-  const bool va = K % 4 == 0 && (uintptr_t)wq % 4 == 0;
-  const bool vb = L % 4 == 0 && (uintptr_t)go % 16 == 0;
-  if (va && vb) launch_data<BM, 128, true, true>(go, wq, tx, N, O, K, L, col, stream);
-  else if (va) launch_data<BM, 128, true, false>(go, wq, tx, N, O, K, L, col, stream);
-  else if (vb) launch_data<BM, 128, false, true>(go, wq, tx, N, O, K, L, col, stream);
-  else launch_data<BM, 128, false, false>(go, wq, tx, N, O, K, L, col, stream);
+template <int BM, bool SC>
+static void dispatch_data_vec(const DataArgs& a, hipStream_t stream) {
+  const bool va = a.K % 4 == 0 && (uintptr_t)a.wq % 4 == 0;
+  const bool vb = a.L % 4 == 0 && (uintptr_t)a.go % 16 == 0;
+  if (va && vb) launch_data<BM, true, true, SC>(a, stream);
+  else if (va) launch_data<BM, true, false, SC>(a, stream);
+  else if (vb) launch_data<BM, false, true, SC>(a, stream);
+  else launch_data<BM, false, false, SC>(a, stream);
+}
+
+static int run_data_gemm(const DataArgs& a, hipStream_t stream) {
+  const bool sc = a.sw != nullptr;
+  if (tile_of(a.K) == 64) {
+    if (sc) dispatch_data_vec<64, true>(a, stream); else dispatch_data_vec<64, false>(a, stream);
+  } else {
+    if (sc) dispatch_data_vec<128, true>(a, stream); else dispatch_data_vec<128, false>(a, stream);
+  }
+  return check_launch("data_gemm_kernel");
 }
 
 template <int BM, int BN, bool VA, typename T>
 static void launch_weight(const float* go, const T* img, atx_conv_geom g, int O, int K, int L,
                           int P, int chunk, int S, int offset, int pad_index,
-                          const float* pad_dev, const float* tw, float* ws,
-                          hipStream_t stream) {
+                          const float* pad_dev, const float* tw, const float* go_sx,
+                          const float* go_sw, float* ws, hipStream_t stream) {
   WeightA<BM, VA> la{};
-  la.go = go; la.O = O; la.L = L;
+  la.go = go; la.O = O; la.L = L; la.sx = go_sx; la.sw = go_sw;
   WeightB<BN, T> lb{};
   lb.img = img; lb.g = g; lb.K = K; lb.L = L; lb.offset = offset; lb.pad = pad_index;
   WeightOut ep{ws, O, K, (long long)O * K};
@@ -543,12 +606,12 @@ static void launch_weight(const float* go, const T* img, atx_conv_geom g, int O,
 template <bool VA, typename T>
 static void dispatch_weight_tiles(const float* go, const T* img, atx_conv_geom g, int O, int K,
                                   int L, int P, int chunk, int S, int offset, int pad_index,
-                                  const float* pad_dev, const float* tw, float* ws,
-                                  hipStream_t stream) {
+                                  const float* pad_dev, const float* tw, const float* go_sx,
+                                  const float* go_sw, float* ws, hipStream_t stream) {
   const int bm = tile_of(O), bn = tile_of(K);
 #define ATX_LW(M_, N_)                                                                       \
   launch_weight<M_, N_, VA, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index, pad_dev, \
-                               tw, ws, stream)
+                               tw, go_sx, go_sw, ws, stream)
   if (bm == 64 && bn == 64) ATX_LW(64, 64);
   else if (bm == 64) ATX_LW(64, 128);
   else if (bn == 64) ATX_LW(128, 64);
@@ -559,14 +622,14 @@ static void dispatch_weight_tiles(const float* go, const T* img, atx_conv_geom g
 template <typename T>
 static void dispatch_weight(const float* go, const T* img, atx_conv_geom g, int O, int K, int L,
                             int P, int chunk, int S, int offset, int pad_index,
-                            const float* pad_dev, const float* tw, float* ws,
-                            hipStream_t stream) {
+                            const float* pad_dev, const float* tw, const float* go_sx,
+                            const float* go_sw, float* ws, hipStream_t stream) {
   if (L % 4 == 0 && (uintptr_t)go % 16 == 0)
     dispatch_weight_tiles<true, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index, pad_dev,
-                                   tw, ws, stream);
+                                   tw, go_sx, go_sw, ws, stream);
   else
     dispatch_weight_tiles<false, T>(go, img, g, O, K, L, P, chunk, S, offset, pad_index,
-                                    pad_dev, tw, ws, stream);
+                                    pad_dev, tw, go_sx, go_sw, ws, stream);
 }
 
 }  // namespace atx
@@ -587,9 +650,58 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx, i
   ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data_col: null pointer");
   ATX_REQUIRE((long long)N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
               "atx_conv_bwd_data_col: sizes too large");
-  if (tile_of(K) == 64) dispatch_data<64>(go, wq, tx, N, O, K, L, col, stream);
-  else dispatch_data<128>(go, wq, tx, N, O, K, L, col, stream);
-  return check_launch("data_gemm_kernel");
+  const DataArgs a{go, wq, tx, N, O, K, L, nullptr, nullptr, col, nullptr, nullptr};
+  return run_data_gemm(a, stream);
+}
+
+// A 1x1, stride-1, unpadded conv's columns are its image gradient.
+static bool direct_columns(const atx_conv_geom& g) {
+  return g.KH == 1 && g.KW == 1 && g.SH == 1 && g.SW == 1 && g.PH == 0 && g.PW == 0;
+}
+
+long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g) {
+  if (direct_columns(g)) return 0;
+  return (long long)g.N * g.C * g.KH * g.KW * g.OH * g.OW * 4;
+}
+
+int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_conv_geom g,
+                      int O, const float* go_sx, const float* go_sw, const uint8_t* mask,
+                      const float* scale, float* gx, float* workspace, hipStream_t stream) {
+  ATX_REQUIRE(O >= 0 && g.N >= 0 && g.C >= 0 && g.H >= 0 && g.W >= 0 && g.KH > 0 && g.KW > 0,
+              "atx_conv_bwd_data: bad geometry");
+  ATX_REQUIRE((go_sx == nullptr) == (go_sw == nullptr),
+              "atx_conv_bwd_data: go_sx and go_sw come together");
+  ATX_REQUIRE(!mask || scale, "atx_conv_bwd_data: mask needs scale");
+  const long long img = (long long)g.N * g.C * g.H * g.W;
+  if (img == 0) return ATX_OK;
+  ATX_REQUIRE(gx, "atx_conv_bwd_data: null output");
+  const int K = g.C * g.KH * g.KW;
+  const int L = g.OH * g.OW;
+  if (direct_columns(g)) {
+    if (O == 0 || L == 0)
+      return launch_split_sum(nullptr, 0, img, 1, nullptr, nullptr, gx, stream);
+    ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
+    ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
+                "atx_conv_bwd_data: sizes too large");
+    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, gx, mask, scale};
+    return run_data_gemm(a, stream);
+  }
+  ATX_REQUIRE(workspace, "atx_conv_bwd_data: null workspace");
+  if ((long long)K * L == 0 || O == 0) {
+    const long long n = (long long)g.N * K * L;
+    if (n) {
+      int rc = launch_split_sum(nullptr, 0, n, 1, nullptr, nullptr, workspace, stream);
+      if (rc) return rc;
+    }
+  } else {
+    ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
+    ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
+                "atx_conv_bwd_data: sizes too large");
+    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, workspace, nullptr, nullptr};
+    int rc = run_data_gemm(a, stream);
+    if (rc) return rc;
+  }
+  return atx_col2im(workspace, g, mask, scale, gx, stream);
 }
 
 long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P) {
@@ -599,9 +711,12 @@ long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P) {
 
 int atx_conv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_geom g, int O,
                         int pad_index, const float* pad_dev, const float* tw,
+                        const float* go_sx, const float* go_sw,
                         const uint8_t* mask_w, const float* scale_w, float* gw,
                         float* workspace, hipStream_t stream) {
   ATX_REQUIRE(O >= 0 && dtype >= 0 && dtype <= 3, "atx_conv_bwd_weight: bad arguments");
+  ATX_REQUIRE((go_sx == nullptr) == (go_sw == nullptr),
+              "atx_conv_bwd_weight: go_sx and go_sw come together");
   const int f32_offset = dtype == 3 ? 0 : 128;   // 3: fp32 unsigned quantized values
   if (dtype == 3) dtype = 2;
   ATX_REQUIRE(pad_index >= 0 && pad_index <= 255, "atx_conv_bwd_weight: bad pad_index");
@@ -622,13 +737,13 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_ge
   const int Sreal = (int)cdiv(P, chunk);
   if (dtype == 0)
     dispatch_weight<int8_t>(go, (const int8_t*)img, g, O, K, L, (int)P, chunk, Sreal, 128,
-                            pad_index, pad_dev, tw, workspace, stream);
+                            pad_index, pad_dev, tw, go_sx, go_sw, workspace, stream);
   else if (dtype == 1)
     dispatch_weight<uint8_t>(go, (const uint8_t*)img, g, O, K, L, (int)P, chunk, Sreal, 0,
-                             pad_index, pad_dev, tw, workspace, stream);
+                             pad_index, pad_dev, tw, go_sx, go_sw, workspace, stream);
   else
     dispatch_weight<float>(go, (const float*)img, g, O, K, L, (int)P, chunk, Sreal,
-                           f32_offset, pad_index, pad_dev, tw, workspace, stream);
+                           f32_offset, pad_index, pad_dev, tw, go_sx, go_sw, workspace, stream);
   int rc = check_launch("weight_gemm_kernel");
   if (rc) return rc;
   return launch_split_sum(workspace, Sreal, (long long)O * K, K, mask_w, scale_w, gw, stream);

@@ -189,13 +189,25 @@ class Conv2d_int8(nn.Module):
             self._update_scale(x)
             self._update_scale_w()
 
-        x = quantization.static_quantize_int8(x, self.scale_x, self.qmin, self.qmax)
         qmax_w = 2 ** (self.weight_bits - 1) - 1
+        geom = ((kH, kW), self.stride, self.padding, self.dilation, self.groups)
+        if self.grad in ('ste', 'lre'):
+            # fake-quant, LUT conv and dequant in one Function (same values and
+            # gradients as the composition below, without the fp32 fake-quantized
+            # tensors)
+            if self.grad == 'lre':
+                tx, tw = self.dx, self.dw
+            else:
+                tx = tw = bgemm_int8.decode_table(x.device)
+            return bgemm_int8.conv2d_int8_fused(x, self.weight, self.bias, self.scale_x,
+                                                self.scale_w, self.lut, tx, tw, geom,
+                                                self.qmin, self.qmax, qmax_w)
+
+        x = quantization.static_quantize_int8(x, self.scale_x, self.qmin, self.qmax)
         w = quantization.static_quantize_int8(self.weight, self.scale_w, -qmax_w, qmax_w,
                                               ch_axis=0)
         s_w = self.scale_w
 
-        geom = ((kH, kW), self.stride, self.padding, self.dilation, self.groups)
         if self.grad == 'lre':
             y = bgemm_int8.conv2d_int8_lre(x, w.view(O, -1), self.lut, self.dx, self.dw, geom)
         elif self.grad == 'custom':

@@ -186,6 +186,60 @@ def conv2d_int8_lre(x, w, lut, dx, dw, geom):
     return _conv2d_int8_lre.apply(x, w, lut, dx, dw, geom)
 
 
+class _conv2d_int8_fused(Function):
+    """Conv2d_int8's forward and STE / LRE backward as one Function: the
+    composition of nn/Conv2d_int8.py:192-212 (fake-quant of x and W, LUT conv,
+    `addcmul(bias, y, scale_x * scale_w)`), the conv Functions above and the
+    fake-quant Functions (nn/quantization.py:37-62,98-113), without the fp32
+    fake-quantized tensors in between:
+      forward:  x -> int8 image + mask, W -> uint8 GEMM operand + mask, LUT
+                conv with the dequant epilogue bias + y * (scale_x * scale_w[o]);
+      backward: go * (scale_x * scale_w[o]) applied in the MFMA operand loads,
+                the x fake-quant STE fused into the fold (or the GEMM epilogue of
+                a 1x1 conv), the W one into the split-K sum; grad_bias = sum go.
+    tx / tw: the estimator's tables (STE: decode tables, LRE: dx / dw)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w):
+        g = _conv_setup(x, weight, geom)
+        O = weight.size(0)
+        _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
+                                                  q8_dtype=torch.int8)
+        _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, -qmax_w, qmax_w,
+                                                            offset=128, want_wt=True)
+        y, _ = ops.conv_forward(xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
+                                sx=scale_x, sw=scale_w,
+                                bias=None if bias is None else bias.detach().contiguous(),
+                                packed_w=(wq, wt, Opad))
+        ctx.save_for_backward(xq8, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
+                              tx.contiguous(), tw.contiguous())
+        ctx.g, ctx.has_bias, ctx.wshape = g, bias is not None, weight.shape
+        return y.view(g.N, O, g.OH, g.OW)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xq8, mask_x, wq, mask_w, sx, sw, tx, tw = ctx.saved_tensors
+        g = ctx.g
+        go = grad_output.contiguous()
+        gx = gw = gb = None
+        if ctx.needs_input_grad[0]:
+            gx = ops.conv_backward_data(go, wq, tx, g, mask=mask_x, scale=sx, go_sx=sx,
+                                        go_sw=sw)
+        if ctx.needs_input_grad[1]:
+            gw = ops.conv_backward_weight(go, xq8, tw, g, wq.size(0), 128, mask_w=mask_w,
+                                          scale_w=sw, go_sx=sx,
+                                          go_sw=sw).view(ctx.wshape)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            gb = go.sum(dim=(0, 2, 3))
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None
+
+
+def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax,
+                      qmax_w):
+    return _conv2d_int8_fused.apply(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom,
+                                    qmin, qmax, qmax_w)
+
+
 class _conv2d_int8_custom(Function):
     """Conv wrapper of the pair-wise custom-gradient kernels
     (nn/bgemm_int8.py:87-123): saves the unfolded uint8 index image."""

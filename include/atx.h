@@ -233,17 +233,33 @@ int atx_lut_map_pad(const void* in, int dtype, int N, int C, int H, int W,
  *   gw[o,k]    = sum_{n,l} go[n,o,l] * tw[xi(n,k,l)]
  * STE: tx/tw decode indices to quantized values; LRE: the dx / dw slope
  * tables.  xi is read from the saved image (dtype as atx_im2col_rows,
- * out-of-image taps -> tw[pad_index]).  mask_w/scale_w (nullable) fuse the
- * per-channel weight fake-quant backward.  Replace the cuBLAS / cuDNN calls
- * of csrc/claude/bgemm_lre_backward_claude.cu:443-524 and
+ * out-of-image taps -> tw[pad_index]).  go_sx/go_sw (nullable, together)
+ * scale go by the fp32 product sx[0] * sw[o] first: the backward of the
+ * layer's dequant y * (scale_x * scale_w).  mask_w/scale_w (nullable) fuse
+ * the per-channel weight fake-quant backward.  Replace the cuBLAS / cuDNN
+ * calls of csrc/claude/bgemm_lre_backward_claude.cu:443-524 and
  * nn/bgemm_int8.py:184-207,277-290. */
 int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx,
                           int N, int O, int K, int L, float* col,
                           hipStream_t stream);
+/* Image gradient of the conv: col as above (with the go scale), folded into
+ * gx [N,C,H,W] with the per-tensor fake-quant STE fused when mask != NULL:
+ * gx = (mask ? g : 0) / max(scale[0], 1e-12).  A 1x1 stride-1 unpadded conv
+ * writes gx straight from the GEMM (no workspace); otherwise the workspace
+ * holds col (atx_conv_bwd_data_workspace_bytes).  Replaces the same calls
+ * plus the fold and the fake-quant backward (nn/bgemm_int8.py:116-118,
+ * csrc/claude/quantization.cu:223-258). */
+long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g);
+int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx,
+                      atx_conv_geom g, int O, const float* go_sx,
+                      const float* go_sw, const uint8_t* mask,
+                      const float* scale, float* gx, float* workspace,
+                      hipStream_t stream);
 long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P);
 int atx_conv_bwd_weight(const float* go, const void* img, int dtype,
                         atx_conv_geom g, int O, int pad_index,
                         const float* pad_dev, const float* tw,
+                        const float* go_sx, const float* go_sw,
                         const uint8_t* mask_w, const float* scale_w, float* gw,
                         float* workspace, hipStream_t stream);
 

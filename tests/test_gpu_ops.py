@@ -417,3 +417,39 @@ def test_conv_backward_kernels_tiled(case):
     ax, aw = O.gemm_grads(np.abs(go), xi, wi, "lre", (np.abs(tx), np.abs(tw)))
     close(gi.cpu().numpy(), O.fold(ex, img.shape, k, s, p, d), O.fold(ax, img.shape, k, s, p, d))
     close(gwk.cpu().numpy(), ew, aw)
+
+
+@pytest.mark.parametrize("geom", [GEOMS[0], ((1, 1), (1, 1), (0, 0), (1, 1)), GEOMS[2]])
+def test_conv_backward_fused_scale_and_masks(geom):
+    """The fused layer backward: go * fp32(sx * sw[o]) in the operand loads,
+    the x fake-quant STE (mask ? g : 0) / max(sx, 1e-12) on the image gradient
+    (fold, or the GEMM epilogue of the 1x1 stride-1 conv), the per-channel W
+    STE in the split-K sum."""
+    k, s, p, d = geom
+    r = gen(zlib.crc32(repr(geom).encode()) + 7)
+    img = r.integers(-127, 128, (3, 40, 11, 12)).astype(np.int8)
+    Oc = 72
+    K = 40 * k[0] * k[1]
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    go = r.standard_normal((3, Oc, g.OH * g.OW)).astype(np.float32)
+    tx = r.standard_normal(256).astype(np.float32)
+    tw = r.standard_normal(256).astype(np.float32)
+    sx = np.array([0.0213], np.float32)
+    sw = r.uniform(1e-3, 4e-2, Oc).astype(np.float32)
+    mask_x = r.random(img.shape) < 0.9
+    mask_w = r.random((Oc, K)) < 0.9
+    gi = ops.conv_backward_data(t(go), t(wi), t(tx), g, mask=t(mask_x), scale=t(sx),
+                                go_sx=t(sx), go_sw=t(sw))
+    gwk = ops.conv_backward_weight(t(go), t(img), t(tw), g, Oc, 128, mask_w=t(mask_w),
+                                   scale_w=t(sw), go_sx=t(sx), go_sw=t(sw))
+    gos = go * (sx[0] * sw)[None, :, None]            # fp32 product, then fp32 scale
+    xi = O.im2col_index(O.image_index(img), k, s, p, d, 128)
+    ex, ew = O.gemm_grads(gos, xi, wi, "lre", (tx, tw))
+    ax, aw = O.gemm_grads(np.abs(gos), xi, wi, "lre", (np.abs(tx), np.abs(tw)))
+    fx = O.fold(ex, img.shape, k, s, p, d)
+    fa = O.fold(ax, img.shape, k, s, p, d)
+    ex_img = np.where(mask_x, fx, 0.0) / max(float(sx[0]), 1e-12)
+    close(gi.cpu().numpy(), ex_img, fa / float(sx[0]))
+    ew_m = np.where(mask_w, ew, 0.0) / np.maximum(sw, 1e-12)[:, None]
+    close(gwk.cpu().numpy(), ew_m, aw / sw[:, None])
