@@ -68,6 +68,10 @@ _SIGS = {
                                 c_vp, c_vp]),
     "atx_conv_bwd_data_col": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp,
                                       c_vp]),
+    "atx_pack_rows_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
+                                      c_int, c_vp]),
+    "atx_pack_cols_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
+                                      c_int, c_vp]),
     "atx_conv_bwd_data_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_conv_bwd_data": (c_int, [c_vp, c_vp, c_vp, ConvGeom, c_int, c_vp, c_vp, c_vp, c_vp,
                                   c_vp, c_vp, c_vp]),

@@ -23,7 +23,9 @@ __all__ = [
     "bgemm_lre_backward_claude", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
     "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "fakequant_per_tensor",
     "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
-    "conv_backward_data", "conv_backward_weight", "col2im",
+    "conv_backward_data", "conv_backward_weight", "col2im", "gemm_fake_int8_claude",
+    "gemm_fake_int8_claude_save", "gemm_fake_int8_claude_cfg", "gemm_fake_uint8_claude",
+    "gemm_fake_uint8_claude_save", "gemm_fake_uint8_claude_cfg",
 ]
 
 # --------------------------------------------------------------------- LUTs
@@ -41,21 +43,26 @@ def _check_lut(lut, name="lut"):
         raise RuntimeError(f"{name} must have 65536 elements")
 
 
-def lut_image(lut: Tensor):
+def lut_image(lut: Tensor, transposed: bool = False):
     """(lut16t, lutf32t, class) for an fp32 [65536] LUT, cached per tensor.
 
     The 16-bit transposed image and its class (int16 / uint16 / fp32
     fallback) are computed once per (storage, version) -- the reference
     rebuilds them inside every forward (csrc/claude/bgemm_float_claude.cu:161-192).
+    transposed=True gives the image of the transposed LUT (lut[w][x] roles
+    swapped), for a GEMM whose row operand is the LUT's second index.
     """
     _check_lut(lut)
-    key = (lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset())
+    key = (lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset(), transposed)
     with _LUT_LOCK:
         hit = _LUT_CACHE.get(key)
         if hit is not None:
             _LUT_CACHE.move_to_end(key)
             return hit
     lc = lut.contiguous()
+    src = lut                   # kept alive by the cache entry: its pointer is the key
+    if transposed:
+        lc = lc.view(256, 256).t().contiguous().view(-1)
     dev = lut.device
     img16 = torch.empty(65536, dtype=torch.int16, device=dev)
     imgf = torch.empty(65536, dtype=torch.float32, device=dev)
@@ -64,7 +71,7 @@ def lut_image(lut: Tensor):
            L.stream_of(lc))
     f = flags.tolist()          # one host sync per new LUT
     cls = L.ATX_LUT_I16 if f[0] == 0 else (L.ATX_LUT_U16 if f[1] == 0 else L.ATX_LUT_F32)
-    val = (img16, imgf, cls, lc)   # keep the source alive: its pointer is the key
+    val = (img16, imgf, cls, src)
     with _LUT_LOCK:
         _LUT_CACHE[key] = val
         while len(_LUT_CACHE) > _LUT_CACHE_MAX:
@@ -73,8 +80,9 @@ def lut_image(lut: Tensor):
 
 
 # -------------------------------------------------------------- LUT GEMM
-def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None):
-    img16, imgf, cls, _ = lut_image(lut)
+def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None,
+          transposed=False):
+    img16, imgf, cls, _ = lut_image(lut, transposed)
     dev = y.device
     wsb = L.query("atx_lut_gemm_workspace_bytes", N, K, Lc, O) if cls != L.ATX_LUT_F32 else 0
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
@@ -176,6 +184,90 @@ def lut_gemm_i32(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
     _, wt, Opad = _pack_w(wc, 0)
     y = torch.empty((N, O, Lc), dtype=torch.int32, device=xc.device)
     return _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_I32, y)
+
+
+# ------------------------------------------- plain LUT GEMM (torch.mm layout)
+def _gemm2d_save(A, B, lut, offset, name):
+    """y [M,N] = sum_k lut[idx(A[m,k]) * 256 + idx(B[k,n])] and the u8 images
+    aq [M,K] (aliases a contiguous uint8 A) and bq [N,K] (B transposed):
+    csrc/claude/gemm.cu:93-230.  A, B: fp32 quantized values or uint8 indices,
+    any strides.  The rows of the gfx950 tile (2048 deep) run along the larger
+    of M and N: rows = M reads A as the row operand and writes y as N_b = M
+    images of one position (y[m][n] = out[m][n][0]); rows = N reads B^T as the
+    row operand with the transposed LUT image, and y = out[0][m][n]."""
+    if not (A.is_cuda and B.is_cuda and lut.is_cuda):
+        raise RuntimeError(f"{name}: A, B and lut must be CUDA tensors")
+    for nm, t in (("A", A), ("B", B)):
+        if t.dtype not in (torch.float32, torch.uint8):
+            raise RuntimeError(f"{nm} must be float32 or uint8 (LUT indices)")
+    _check_lut(lut)
+    if A.dim() != 2:
+        raise RuntimeError("A must have shape [M, K]")
+    if B.dim() != 2:
+        raise RuntimeError("B must have shape [K, N]")
+    if A.size(1) != B.size(0):
+        raise RuntimeError(f"A.size(1) must equal B.size(0), got {A.size(1)} vs {B.size(0)}")
+    M, K = A.shape
+    N = B.size(1)
+    if max(M, K, N) > 2 ** 31 - 1:
+        raise RuntimeError("dimensions too large")
+    dev, s = A.device, L.stream_of(A)
+    u8 = dict(dtype=torch.uint8, device=dev)
+    a_u8 = A.dtype == torch.uint8
+    aq = A.contiguous() if a_u8 else torch.empty((M, K), **u8)
+    bq = torch.empty((N, K), **u8)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    rows_m = M >= N
+    if rows_m:
+        R, C, Nb, Lc = M, N, M, 1
+        X, sr, sk, xq = A, A.stride(0), A.stride(1), None if a_u8 else aq
+        Y, sc, skc, yq = B, B.stride(1), B.stride(0), bq
+    else:
+        R, C, Nb, Lc = N, M, 1, N
+        X, sr, sk, xq = B, B.stride(1), B.stride(0), bq
+        Y, sc, skc, yq = A, A.stride(0), A.stride(1), None if a_u8 else aq
+    Rpad = L.round_up(max(R, 1), L.ROW_TILE)
+    Opad = L.round_up(max(C, 1), L.COL_TILE)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
+    wt = torch.empty((K, Opad), **u8)
+    L.call("atx_pack_rows_strided", L.ptr(X), int(X.dtype == torch.uint8), R, K, sr, sk,
+           offset, L.ptr(xq), L.ptr(xt), Rpad, s)
+    L.call("atx_pack_cols_strided", L.ptr(Y), int(Y.dtype == torch.uint8), C, K, sc, skc,
+           offset, L.ptr(yq), L.ptr(wt), Opad, s)
+    if y.numel():
+        _gemm(xt, Rpad, wt, Opad, Nb, K, Lc, C, lut, L.ATX_OUT_F32, y, transposed=not rows_m)
+    return y, aq, bq
+
+
+def gemm_fake_int8_claude_save(A: Tensor, B: Tensor, lut: Tensor):
+    """(y, aq, bq): y[m,n] = sum_k lut[(A[m,k]+128)*256 + (B[k,n]+128)]
+    (csrc/claude/gemm.cu:1-40, 232-262)."""
+    return _gemm2d_save(A, B, lut, 128, "gemm_fake_int8_claude_save")
+
+
+def gemm_fake_int8_claude(A: Tensor, B: Tensor, lut: Tensor) -> Tensor:
+    return gemm_fake_int8_claude_save(A, B, lut)[0]
+
+
+def gemm_fake_int8_claude_cfg(A: Tensor, B: Tensor, lut: Tensor, cfg: int) -> Tensor:
+    """`cfg` forced one of the reference's CUDA tile configurations or
+    orientations; the gfx950 kernel picks its orientation from the shape, so
+    it is accepted and ignored."""
+    return gemm_fake_int8_claude(A, B, lut)
+
+
+def gemm_fake_uint8_claude_save(A: Tensor, B: Tensor, lut: Tensor):
+    """uint8 x uint8 variant: y[m,n] = sum_k lut[A[m,k]*256 + B[k,n]]
+    (csrc/claude/gemm.cu:264-290)."""
+    return _gemm2d_save(A, B, lut, 0, "gemm_fake_uint8_claude_save")
+
+
+def gemm_fake_uint8_claude(A: Tensor, B: Tensor, lut: Tensor) -> Tensor:
+    return gemm_fake_uint8_claude_save(A, B, lut)[0]
+
+
+def gemm_fake_uint8_claude_cfg(A: Tensor, B: Tensor, lut: Tensor, cfg: int) -> Tensor:
+    return gemm_fake_uint8_claude(A, B, lut)
 
 
 # ------------------------------------------------------------- conv path

@@ -171,6 +171,61 @@ __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
   }
 }
 
+// Strided operands of the plain (torch.mm-layout) LUT GEMM.  Row operand:
+// X[r][k] at X + r*sr + k*sk -> xt[slot][r] = row_offset(index), as pack_x
+// (quads of rows share a tap); column operand: Y[c][k] at Y + c*sc + k*sk ->
+// wt[k][c] = index.  index = clamp(rint(v) + offset, 0, 255) for fp32, the
+// byte for uint8; the optional u8 images get q[r*K + k] / q[c*K + k].
+template <typename T>
+__global__ void pack_rows_strided_kernel(const T* __restrict__ x, int R, int K, long long sr,
+                                         long long sk, int offset, uint8_t* __restrict__ xq,
+                                         uint16_t* __restrict__ xt, int Rpad) {
+  const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int qstride = gridDim.x * blockDim.x;
+  const int nquad = Rpad >> 2;
+  for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
+    const int k = operand_tap(slot, q0 << 2);
+    uint16_t* dst = xt + (long long)slot * Rpad;
+    for (int q = q0; q < nquad; q += qstride) {
+      const int r0 = q << 2;
+      unsigned off[4] = {0u, 0u, 0u, 0u};
+      if (k < K) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r0 + e;
+          if (r < R) {
+            unsigned v;
+            if constexpr (sizeof(T) == 4) v = quant_index((float)x[r * sr + k * sk], offset);
+            else v = (unsigned)x[r * sr + k * sk];
+            if (xq) xq[(long long)r * K + k] = (uint8_t)v;
+            off[e] = row_offset(v);
+          }
+        }
+      }
+      *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
+    }
+  }
+}
+
+template <typename T>
+__global__ void pack_cols_strided_kernel(const T* __restrict__ y, int C, int K, long long sc,
+                                         long long sk, int offset, uint8_t* __restrict__ yq,
+                                         uint8_t* __restrict__ wt, int Opad) {
+  const long long total = (long long)K * Opad;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int k = (int)(i / Opad);
+    const int c = (int)(i - (long long)k * Opad);
+    unsigned v = 0;
+    if (c < C) {
+      if constexpr (sizeof(T) == 4) v = quant_index((float)y[c * sc + k * sk], offset);
+      else v = (unsigned)y[c * sc + k * sk];
+      if (yq) yq[(long long)c * K + k] = (uint8_t)v;
+    }
+    wt[i] = (uint8_t)v;
+  }
+}
+
 template <typename T>
 __global__ void pack_w_kernel(const T* __restrict__ w, int O, int K, int offset,
                               uint8_t* __restrict__ wq, uint8_t* __restrict__ wt,
@@ -675,6 +730,43 @@ int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
   hipLaunchKernelGGL(pack_w_kernel<uint8_t>, dim3(elem_grid((long long)K * Opad, 256)),
                      dim3(256), 0, stream, wq, O, K, 0, (uint8_t*)nullptr, wt, Opad);
   return check_launch("pack_w_kernel<u8>");
+}
+
+int atx_pack_rows_strided(const void* x, int dtype, int R, int K, long long sr, long long sk,
+                          int offset, uint8_t* xq, uint16_t* xt, int Rpad, hipStream_t stream) {
+  ATX_REQUIRE(R >= 0 && K >= 0 && (dtype == 0 || dtype == 1),
+              "atx_pack_rows_strided: bad arguments");
+  ATX_REQUIRE(Rpad >= R && Rpad % RT == 0,
+              "atx_pack_rows_strided: Rpad must be a multiple of %d covering R", RT);
+  if ((long long)K * Rpad == 0) return ATX_OK;
+  ATX_REQUIRE(xt && (R == 0 || x), "atx_pack_rows_strided: null pointer");
+  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, 256), 1024),
+            (unsigned)std::min(operand_rows(K), 65535));
+  if (dtype == 0)
+    hipLaunchKernelGGL(pack_rows_strided_kernel<float>, grid, dim3(256), 0, stream,
+                       (const float*)x, R, K, sr, sk, offset, xq, xt, Rpad);
+  else
+    hipLaunchKernelGGL(pack_rows_strided_kernel<uint8_t>, grid, dim3(256), 0, stream,
+                       (const uint8_t*)x, R, K, sr, sk, 0, xq, xt, Rpad);
+  return check_launch("pack_rows_strided_kernel");
+}
+
+int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc, long long sk,
+                          int offset, uint8_t* yq, uint8_t* wt, int Opad, hipStream_t stream) {
+  ATX_REQUIRE(C >= 0 && K >= 0 && (dtype == 0 || dtype == 1),
+              "atx_pack_cols_strided: bad arguments");
+  ATX_REQUIRE(Opad >= C && Opad % OT == 0,
+              "atx_pack_cols_strided: Opad must be a multiple of %d covering C", OT);
+  if ((long long)K * Opad == 0) return ATX_OK;
+  ATX_REQUIRE(wt && (C == 0 || y), "atx_pack_cols_strided: null pointer");
+  const dim3 grid(elem_grid((long long)K * Opad, 256));
+  if (dtype == 0)
+    hipLaunchKernelGGL(pack_cols_strided_kernel<float>, grid, dim3(256), 0, stream,
+                       (const float*)y, C, K, sc, sk, offset, yq, wt, Opad);
+  else
+    hipLaunchKernelGGL(pack_cols_strided_kernel<uint8_t>, grid, dim3(256), 0, stream,
+                       (const uint8_t*)y, C, K, sc, sk, 0, yq, wt, Opad);
+  return check_launch("pack_cols_strided_kernel");
 }
 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O) {

@@ -19,6 +19,7 @@ Also reported:
                 the same passes see a copy kernel of known size).
   lut_gemm      the standalone BGEMM microbench (config 3: B=32, 4096x2304 by
                 2304x256, perturbed LUT) in G LUT-MAC/s.
+  gemm2d        the plain torch.mm-layout LUT GEMM on Linear-shaped operands.
   cpu_baseline  the torch-CPU restatement of the same training step
                 (oracle/torch_cpu.py) on a bounded sample (batch 1), scaled to img/s.
 """
@@ -181,6 +182,32 @@ def lut_gemm_microbench(torch, reps=5):
     return out
 
 
+def gemm2d_microbench(torch, reps=5):
+    """Plain torch.mm-layout LUT GEMM (gemm_fake_int8_claude) on Linear-shaped
+    int8 operands, both orientations (rows along M, rows along N), in
+    G LUT-MAC/s end to end (operand packing included)."""
+    from approxtorch_amd import workloads
+    from approxtorch_amd.backend import ops
+    out = {}
+    lut = torch.from_numpy(workloads.lut_perturbed(3)).cuda()
+    g = torch.Generator().manual_seed(4)
+    for M, K, N in ((8192, 4096, 1024), (256, 4096, 8192)):
+        A = torch.randint(-128, 128, (M, K), generator=g).float().cuda()
+        W = torch.randint(-128, 128, (N, K), generator=g).float().cuda()
+        ops.gemm_fake_int8_claude(A, W.t(), lut)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            ops.gemm_fake_int8_claude(A, W.t(), lut)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        out[f"{M}x{K}x{N}"] = round(M * K * N / (ms * 1e-3) / 1e9, 1)
+        del A, W
+    return out
+
+
 def cpu_baseline(model, cfg, sample_batch):
     import torch
     from approxtorch_amd import workloads
@@ -255,6 +282,7 @@ def main():
     }
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
+        result["gemm2d_GLUTMACs"] = gemm2d_microbench(torch)
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:

@@ -92,6 +92,20 @@ int atx_pack_w_f32(const float* w, int O, int K, int offset,
 int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
                   hipStream_t stream);
 
+/* Operands of the plain (torch.mm-layout) LUT GEMM from strided 2-D inputs.
+ * dtype 0: fp32 values, index clamp(rint(v) + offset, 0, 255); 1: uint8
+ * indices.  Rows: X[r][k] at x + r*sr + k*sk -> xt [Kpad][Rpad] (as
+ * atx_pack_x_u8, R rows) and the u8 image xq [R][K] (nullable).  Columns:
+ * Y[c][k] at y + c*sc + k*sk -> wt [K][Opad] and yq [C][K] (nullable).
+ * Replace the quantize and fused quantize-transpose prepasses of
+ * csrc/claude/gemm.cu:57-100,128-166. */
+int atx_pack_rows_strided(const void* x, int dtype, int R, int K, long long sr,
+                          long long sk, int offset, uint8_t* xq, uint16_t* xt,
+                          int Rpad, hipStream_t stream);
+int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc,
+                          long long sk, int offset, uint8_t* yq, uint8_t* wt,
+                          int Opad, hipStream_t stream);
+
 /* Quantized image -> row-offset operand xt [Kpad][Rpad] (K = C*KH*KW) of the
  * implicit im2col, k order (c, kh, kw), r = n*OH*OW + oh*OW + ow.  dtype:
  * 0 = int8 values (index v+128), 1 = uint8 (index v), 2 = fp32 signed
