@@ -72,6 +72,13 @@ _SIGS = {
                                       c_int, c_vp]),
     "atx_pack_cols_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
                                       c_int, c_vp]),
+    "atx_dwconv_fwd": (c_int, [c_vp, c_int, ConvGeom, c_int, c_vp, c_vp, c_vp, c_int,
+                               GemmEpilogue, c_vp, c_vp]),
+    "atx_dwconv_bwd_data": (c_int, [c_vp, c_vp, c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                    c_vp]),
+    "atx_dwconv_bwd_weight_workspace_bytes": (c_ll, [ConvGeom]),
+    "atx_dwconv_bwd_weight": (c_int, [c_vp, c_vp, c_int, ConvGeom, c_int, c_vp, c_vp, c_vp,
+                                      c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_conv_bwd_data_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_conv_bwd_data": (c_int, [c_vp, c_vp, c_vp, ConvGeom, c_int, c_vp, c_vp, c_vp, c_vp,
                                   c_vp, c_vp, c_vp]),

@@ -25,7 +25,8 @@ __all__ = [
     "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
     "conv_backward_data", "conv_backward_weight", "col2im", "gemm_fake_int8_claude",
     "gemm_fake_int8_claude_save", "gemm_fake_int8_claude_cfg", "gemm_fake_uint8_claude",
-    "gemm_fake_uint8_claude_save", "gemm_fake_uint8_claude_cfg",
+    "gemm_fake_uint8_claude_save", "gemm_fake_uint8_claude_cfg", "dwconv_fake_int8_claude",
+    "dwconv_forward", "dwconv_backward_data", "dwconv_backward_weight",
 ]
 
 # --------------------------------------------------------------------- LUTs
@@ -353,6 +354,73 @@ def conv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, O: int, pad_
     wsb = L.query("atx_conv_bwd_weight_workspace_bytes", O, K, P)
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
     L.call("atx_conv_bwd_weight", L.ptr(goc), L.ptr(imgc), _dtype_code(imgc, unsigned), g, O,
+           pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask_w),
+           L.ptr(scale_w), L.ptr(gw), L.ptr(ws), L.stream_of(goc))
+    return gw
+
+
+# ---------------------------------------------------------- depthwise conv
+def dwconv_forward(img: Tensor, wq: Tensor, lut: Tensor, g, pad_index: int,
+                   out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None, unsigned=False):
+    """Depthwise LUT conv: y [N,C,OH,OW] = sum_taps lut[xi][wq[c,t]] (taps in
+    ascending (i, j); out-of-image taps index pad_index), with the LUT GEMM's
+    epilogues (sw / bias per channel).  wq: uint8 [C, KH*KW] indices."""
+    imgc = img.contiguous()
+    img16, imgf, cls, _ = lut_image(lut)
+    ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
+    y = torch.empty((g.N, g.C, g.OH, g.OW), dtype=ydt, device=imgc.device)
+    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
+    L.call("atx_dwconv_fwd", L.ptr(imgc), _dtype_code(imgc, unsigned), g, pad_index,
+           L.ptr(wq.contiguous()), L.ptr(img16), L.ptr(imgf), cls, ep, L.ptr(y),
+           L.stream_of(imgc))
+    return y
+
+
+def dwconv_fake_int8_claude(x: Tensor, w: Tensor, lut: Tensor, kernel_size, stride=1,
+                            padding=0, dilation=1):
+    """(y [N,C,OH,OW] fp32, wq [C, kh*kw] uint8): depthwise (groups == C, channel
+    multiplier 1) LUT conv of a quantized image (int8 / uint8 / fp32 values)
+    with fp32 quantized weights; equal to the LUT-BGEMM run per channel with
+    the same tap order (csrc/claude/dwconv_claude.cu:1-285, ops.py:252-263)."""
+    if not (x.is_cuda and w.is_cuda and lut.is_cuda):
+        raise RuntimeError("x, w and lut must be CUDA tensors")
+    if x.dtype not in (torch.float32, torch.int8, torch.uint8):
+        raise RuntimeError("x must be float32, int8 or uint8")
+    if w.dtype != torch.float32:
+        raise RuntimeError("w must be float32")
+    _check_lut(lut)
+    if x.dim() != 4:
+        raise RuntimeError("x must have shape [N, C, H, W]")
+    g = conv_geom(tuple(x.shape), kernel_size, stride, padding, dilation)
+    if w.dim() != 2 or w.size(0) != g.C or w.size(1) != g.KH * g.KW:
+        raise RuntimeError(f"w must have shape [C, kh*kw] = [{g.C}, {g.KH * g.KW}]")
+    if g.OH <= 0 or g.OW <= 0:
+        raise RuntimeError("empty output geometry")
+    wq, _, _ = _pack_w(w.contiguous(), 128)
+    return dwconv_forward(x, wq, lut, g, 128), wq
+
+
+def dwconv_backward_data(go: Tensor, wq: Tensor, table: Tensor, g, mask=None, scale=None,
+                         go_sx=None, go_sw=None) -> Tensor:
+    """grad wrt the image of the depthwise conv (go' and the fused STE as in
+    conv_backward_data)."""
+    goc = go.contiguous()
+    gx = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
+    L.call("atx_dwconv_bwd_data", L.ptr(goc), L.ptr(wq.contiguous()), L.ptr(table), g,
+           L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask), L.ptr(scale), L.ptr(gx), L.stream_of(goc))
+    return gx
+
+
+def dwconv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, pad_index: int,
+                           mask_w=None, scale_w=None, pad_dev=None, unsigned=False,
+                           go_sx=None, go_sw=None) -> Tensor:
+    """grad wrt the depthwise weights [C, KH*KW] (go' and the fused per-channel
+    STE as in conv_backward_weight)."""
+    goc, imgc = go.contiguous(), img.contiguous()
+    gw = torch.empty((g.C, g.KH * g.KW), dtype=torch.float32, device=goc.device)
+    wsb = L.query("atx_dwconv_bwd_weight_workspace_bytes", g)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
+    L.call("atx_dwconv_bwd_weight", L.ptr(goc), L.ptr(imgc), _dtype_code(imgc, unsigned), g,
            pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask_w),
            L.ptr(scale_w), L.ptr(gw), L.ptr(ws), L.stream_of(goc))
     return gw

@@ -19,6 +19,16 @@ int check_launch(const char* what);
 
 inline long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 
+// Validates a conv geometry (sizes, strides, OH/OW consistent); ATX_OK or
+// ATX_EINVAL with a message.
+int check_geom(const atx_conv_geom& g);
+
+// out[i] = sum_s ws[s*numel + i] in a fixed order (deterministic), with the
+// optional per-channel fake-quant STE out = (mask ? sum : 0) / max(scale[i/K],
+// 1e-12); S = 0 writes zeros.
+int launch_split_sum(const float* ws, int S, long long numel, int K, const uint8_t* mask,
+                     const float* scale, float* out, hipStream_t stream);
+
 // Grid size for grid-stride elementwise kernels.
 inline int elem_grid(long long n, int threads, int cap = 8192) {
   long long b = cdiv(n, threads);

@@ -1,0 +1,332 @@
+// Depthwise LUT conv (groups == C == O, one filter per channel) and its STE /
+// LRE backward.
+//
+//   y[n,c,oh,ow] = sum_{i,j} LUT[xi(n, c, oh*SH - PH + i*DH, ow*SW - PW + j*DW)][wi(c, i, j)]
+//
+// Out-of-image taps take LUT row pad_index (128 = quantized zero of int8),
+// as the im2col pipeline's zero padding does.  Reference:
+// csrc/claude/dwconv_claude.cu:1-285 (forward) and the grouped
+// convolution_backward of nn/bgemm_int8.py:162-212,259-295.
+//
+// Forward: a block owns one (image, channel) plane slice; the channel's
+// KH*KW table columns LUT[.][wi(c,t)] (512 B each in the 16-bit image) are
+// staged in LDS, every thread walks output pixels and sums its taps in
+// ascending (i, j) order: exact int32 for the integer LUT classes, fp32 in
+// the same order for the fp32 fallback (bit-identical to a per-channel LUT
+// GEMM).  The work is small next to the dense convs (K = KH*KW per output),
+// so the kernel is bound by the image and output traffic.
+//
+// Backward (per channel, tables indexed by the other operand):
+//   gx[n,c,h,w] = sum over taps (i,j) and outputs (oh,ow) reading (h,w) of
+//                 go'[n,c,oh,ow] * tx[wi(c,i,j)]
+//   gw[c,i,j]   = sum_{n,oh,ow} go'[n,c,oh,ow] * tw[xi(n,c,tap)]
+// with go' = go * fp32(sx * sw[c]) when a go scale is given, and the
+// fake-quant STE masks fused into the outputs.
+
+#include "atx_internal.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace atx {
+
+constexpr int DW_THREADS = 256;
+constexpr int DW_MAX_TAPS = 64;         // LDS: 64 taps x 256 entries x 4 B = 64 KiB
+constexpr int DW_WSPLIT_ROWS = 4096;    // contraction rows per weight-gradient block
+
+template <typename T> __device__ __forceinline__ unsigned dw_index(T v, int offset);
+template <> __device__ __forceinline__ unsigned dw_index<int8_t>(int8_t v, int) {
+  return (unsigned)((int)v + 128);
+}
+template <> __device__ __forceinline__ unsigned dw_index<uint8_t>(uint8_t v, int) {
+  return (unsigned)v;
+}
+template <> __device__ __forceinline__ unsigned dw_index<float>(float v, int offset) {
+  return quant_index(v, offset);
+}
+
+struct DwEpilogue {
+  int out_kind; const float* sx; const float* sw; const float* bias;
+};
+
+// ENTRY: int (16-bit classes, sign-extended or not) or float (fp32 class).
+template <typename T, typename ENTRY, bool SIGNED>
+__global__ void __launch_bounds__(DW_THREADS)
+dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad,
+                  const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
+                  const float* __restrict__ lutf32t, DwEpilogue ep, void* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char dw_smem[];
+  ENTRY* tab = (ENTRY*)dw_smem;
+  const int c = blockIdx.y, n = blockIdx.z;
+  const int KK = g.KH * g.KW;
+  for (int e = threadIdx.x; e < KK * 256; e += blockDim.x) {
+    const int t = e >> 8, x = e & 255;
+    const unsigned w = wq[(long long)c * KK + t];
+    if constexpr (sizeof(ENTRY) == 4 && !std::is_integral<ENTRY>::value) {
+      tab[e] = lutf32t[w * 256u + x];
+    } else {
+      const unsigned v = lut16t[w * 256u + x];
+      tab[e] = SIGNED ? (int)(short)(unsigned short)v : (int)v;
+    }
+  }
+  __syncthreads();
+  const int L = g.OH * g.OW;
+  const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
+  float sc = 1.0f, bi = 0.0f;
+  if (ep.out_kind == ATX_OUT_DEQUANT) {
+    sc = ep.sx[0] * ep.sw[c];
+    if (ep.bias) bi = ep.bias[c];
+  }
+  const long long ybase = ((long long)n * g.C + c) * L;
+  for (int l = blockIdx.x * blockDim.x + threadIdx.x; l < L; l += gridDim.x * blockDim.x) {
+    const int oh = l / g.OW, ow = l - oh * g.OW;
+    ENTRY acc = 0;
+    for (int i = 0; i < g.KH; ++i) {
+      const int ih = oh * g.SH - g.PH + i * g.DH;
+      const bool hin = (unsigned)ih < (unsigned)g.H;
+      for (int j = 0; j < g.KW; ++j) {
+        const int iw = ow * g.SW - g.PW + j * g.DW;
+        unsigned xi = (unsigned)pad;
+        if (hin && (unsigned)iw < (unsigned)g.W) xi = dw_index<T>(plane[ih * g.W + iw], offset);
+        acc += tab[(i * g.KW + j) * 256 + xi];
+      }
+    }
+    if (ep.out_kind == ATX_OUT_I32) {
+      ((int*)y)[ybase + l] = (int)acc;
+    } else if (ep.out_kind == ATX_OUT_DEQUANT) {
+      const float t = (float)acc * sc;
+      ((float*)y)[ybase + l] = ep.bias ? bi + t : t;
+    } else {
+      ((float*)y)[ybase + l] = (float)acc;
+    }
+  }
+}
+
+// gx for one image pixel: taps in ascending (i, j) order.
+__global__ void __launch_bounds__(DW_THREADS)
+dwconv_bwd_data_kernel(const float* __restrict__ go, const uint8_t* __restrict__ wq,
+                       const float* __restrict__ tx, atx_conv_geom g,
+                       const float* __restrict__ go_sx, const float* __restrict__ go_sw,
+                       const uint8_t* __restrict__ mask, const float* __restrict__ scale,
+                       float* __restrict__ gx) {
+  __shared__ float stx[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) stx[i] = tx[i];
+  __syncthreads();
+  const int KK = g.KH * g.KW;
+  const long long HW = (long long)g.H * g.W;
+  const long long total = (long long)g.N * g.C * HW;
+  const int L = g.OH * g.OW;
+  const float sdiv = mask ? fmaxf(scale[0], 1e-12f) : 1.0f;
+  for (long long e = blockIdx.x * (long long)blockDim.x + threadIdx.x; e < total;
+       e += (long long)gridDim.x * blockDim.x) {
+    const long long nc = e / HW;
+    const int hw = (int)(e - nc * HW);
+    const int h = hw / g.W, w = hw - (hw / g.W) * g.W;
+    const int c = (int)(nc % g.C);
+    const float s = go_sw ? go_sx[0] * go_sw[c] : 1.0f;
+    const float* gp = go + nc * L;
+    float a = 0.0f;
+    for (int i = 0; i < g.KH; ++i) {
+      const int th = h + g.PH - i * g.DH;
+      if (th < 0 || th % g.SH) continue;
+      const int oh = th / g.SH;
+      if (oh >= g.OH) continue;
+      for (int j = 0; j < g.KW; ++j) {
+        const int tw_ = w + g.PW - j * g.DW;
+        if (tw_ < 0 || tw_ % g.SW) continue;
+        const int ow = tw_ / g.SW;
+        if (ow >= g.OW) continue;
+        const float gv = go_sw ? gp[oh * g.OW + ow] * s : gp[oh * g.OW + ow];
+        a += gv * stx[wq[(long long)c * KK + i * g.KW + j]];
+      }
+    }
+    if (mask) a = (mask[e] ? a : 0.0f) / sdiv;
+    gx[e] = a;
+  }
+}
+
+// Partial weight gradients: block (c, s) sums contraction rows
+// [s*DW_WSPLIT_ROWS, ...) of P = N*OH*OW for every tap of channel c and
+// writes ws[s][c][t].  Threads keep up to 16 taps at a time; the block
+// reduction runs in a fixed order (deterministic).
+template <typename T>
+__global__ void __launch_bounds__(DW_THREADS)
+dwconv_bwd_weight_kernel(const float* __restrict__ go, const T* __restrict__ img,
+                         atx_conv_geom g, int offset, int pad, const float* __restrict__ pad_dev,
+                         const float* __restrict__ tw, const float* __restrict__ go_sx,
+                         const float* __restrict__ go_sw, float* __restrict__ ws) {
+  __shared__ float stw[256];
+  __shared__ float red[16][DW_THREADS + 1];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) stw[i] = tw[i];
+  if (pad_dev) pad = (int)quant_index(pad_dev[0], 0);
+  __syncthreads();
+  const int c = blockIdx.x, s = blockIdx.y;
+  const int KK = g.KH * g.KW;
+  const int L = g.OH * g.OW;
+  const long long P = (long long)g.N * L;
+  const long long p0 = (long long)s * DW_WSPLIT_ROWS;
+  const long long p1 = min(P, p0 + DW_WSPLIT_ROWS);
+  const float sc = go_sw ? go_sx[0] * go_sw[c] : 1.0f;
+  for (int t0 = 0; t0 < KK; t0 += 16) {
+    float acc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+    for (long long p = p0 + threadIdx.x; p < p1; p += blockDim.x) {
+      const int n = (int)(p / L), l = (int)(p - (long long)n * L);
+      const int oh = l / g.OW, ow = l - oh * g.OW;
+      const float gv = go_sw ? go[((long long)n * g.C + c) * L + l] * sc
+                             : go[((long long)n * g.C + c) * L + l];
+      const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int t = t0 + q;
+        if (t < KK) {
+          const int i = t / g.KW, j = t - (t / g.KW) * g.KW;
+          const int ih = oh * g.SH - g.PH + i * g.DH;
+          const int iw = ow * g.SW - g.PW + j * g.DW;
+          unsigned xi = (unsigned)pad;
+          if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+            xi = dw_index<T>(plane[ih * g.W + iw], offset);
+          acc[q] += gv * stw[xi];
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) red[q][threadIdx.x] = acc[q];
+    __syncthreads();
+    if (threadIdx.x < 16 && t0 + (int)threadIdx.x < KK) {
+      const int q = threadIdx.x;
+      float a = 0.0f;
+      for (int k = 0; k < DW_THREADS; ++k) a += red[q][k];
+      ws[((long long)s * g.C + c) * KK + t0 + q] = a;
+    }
+    __syncthreads();
+  }
+}
+
+static int dw_check(const atx_conv_geom& g, int dtype, int pad_index, const char* what) {
+  int rc = check_geom(g);
+  if (rc) return rc;
+  ATX_REQUIRE(dtype >= 0 && dtype <= 3, "%s: bad dtype %d", what, dtype);
+  ATX_REQUIRE(pad_index >= 0 && pad_index <= 255, "%s: bad pad_index", what);
+  ATX_REQUIRE(g.KH * g.KW <= DW_MAX_TAPS, "%s: at most %d taps", what, DW_MAX_TAPS);
+  ATX_REQUIRE(g.C <= 65535 && g.N <= 65535, "%s: C and N must be <= 65535", what);
+  return ATX_OK;
+}
+
+template <typename T>
+static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int pad,
+                          const uint8_t* wq, const uint16_t* l16, const float* lf32, int cls,
+                          const DwEpilogue& ep, void* y, hipStream_t stream) {
+  const int L = g.OH * g.OW;
+  const int KK = g.KH * g.KW;
+  dim3 grid((unsigned)std::max<long long>(1, std::min<long long>(cdiv(L, DW_THREADS), 64)),
+            (unsigned)g.C, (unsigned)g.N);
+  const size_t smem = (size_t)KK * 256 * 4;
+  if (cls == ATX_LUT_F32)
+    hipLaunchKernelGGL((dwconv_fwd_kernel<T, float, false>), grid, dim3(DW_THREADS), smem,
+                       stream, img, g, offset, pad, wq, l16, lf32, ep, y);
+  else if (cls == ATX_LUT_I16)
+    hipLaunchKernelGGL((dwconv_fwd_kernel<T, int, true>), grid, dim3(DW_THREADS), smem, stream,
+                       img, g, offset, pad, wq, l16, lf32, ep, y);
+  else
+    hipLaunchKernelGGL((dwconv_fwd_kernel<T, int, false>), grid, dim3(DW_THREADS), smem, stream,
+                       img, g, offset, pad, wq, l16, lf32, ep, y);
+}
+
+}  // namespace atx
+
+using namespace atx;
+
+extern "C" {
+
+int atx_dwconv_fwd(const void* img, int dtype, atx_conv_geom g, int pad_index,
+                   const uint8_t* wq, const uint16_t* lut16t, const float* lutf32t,
+                   int lut_class, atx_gemm_epilogue ep, void* y, hipStream_t stream) {
+  int rc = dw_check(g, dtype, pad_index, "atx_dwconv_fwd");
+  if (rc) return rc;
+  ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,
+              "atx_dwconv_fwd: bad out_kind");
+  ATX_REQUIRE(lut_class >= ATX_LUT_I16 && lut_class <= ATX_LUT_F32,
+              "atx_dwconv_fwd: bad lut_class");
+  ATX_REQUIRE(!(lut_class == ATX_LUT_F32 && ep.out_kind == ATX_OUT_I32),
+              "atx_dwconv_fwd: int32 output needs an integer LUT");
+  ATX_REQUIRE(ep.out_kind != ATX_OUT_DEQUANT || (ep.scale_x && ep.scale_w),
+              "atx_dwconv_fwd: dequant epilogue needs scale_x and scale_w");
+  if ((long long)g.N * g.C == 0) return ATX_OK;
+  ATX_REQUIRE(img && wq && y && lut16t && lutf32t, "atx_dwconv_fwd: null pointer");
+  const int offset = dtype == 3 ? 0 : 128;
+  const DwEpilogue dep{ep.out_kind, ep.scale_x, ep.scale_w, ep.bias};
+  if (dtype == 0)
+    launch_dw_fwd<int8_t>((const int8_t*)img, g, offset, pad_index, wq, lut16t, lutf32t,
+                          lut_class, dep, y, stream);
+  else if (dtype == 1)
+    launch_dw_fwd<uint8_t>((const uint8_t*)img, g, offset, pad_index, wq, lut16t, lutf32t,
+                           lut_class, dep, y, stream);
+  else
+    launch_dw_fwd<float>((const float*)img, g, offset, pad_index, wq, lut16t, lutf32t,
+                         lut_class, dep, y, stream);
+  return check_launch("dwconv_fwd_kernel");
+}
+
+int atx_dwconv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_conv_geom g,
+                        const float* go_sx, const float* go_sw, const uint8_t* mask,
+                        const float* scale, float* gx, hipStream_t stream) {
+  int rc = dw_check(g, 0, 0, "atx_dwconv_bwd_data");
+  if (rc) return rc;
+  ATX_REQUIRE((go_sx == nullptr) == (go_sw == nullptr),
+              "atx_dwconv_bwd_data: go_sx and go_sw come together");
+  ATX_REQUIRE(!mask || scale, "atx_dwconv_bwd_data: mask needs scale");
+  const long long total = (long long)g.N * g.C * g.H * g.W;
+  if (total == 0) return ATX_OK;
+  ATX_REQUIRE(go && wq && tx && gx, "atx_dwconv_bwd_data: null pointer");
+  hipLaunchKernelGGL(dwconv_bwd_data_kernel, dim3(elem_grid(total, DW_THREADS)),
+                     dim3(DW_THREADS), 0, stream, go, wq, tx, g, go_sx, go_sw, mask, scale, gx);
+  return check_launch("dwconv_bwd_data_kernel");
+}
+
+long long atx_dwconv_bwd_weight_workspace_bytes(atx_conv_geom g) {
+  const long long P = (long long)g.N * g.OH * g.OW;
+  if (P <= 0 || g.C <= 0) return 0;
+  return cdiv(P, DW_WSPLIT_ROWS) * g.C * g.KH * g.KW * 4;
+}
+
+int atx_dwconv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_geom g,
+                          int pad_index, const float* pad_dev, const float* tw,
+                          const float* go_sx, const float* go_sw, const uint8_t* mask_w,
+                          const float* scale_w, float* gw, float* workspace,
+                          hipStream_t stream) {
+  int rc = dw_check(g, dtype, pad_index, "atx_dwconv_bwd_weight");
+  if (rc) return rc;
+  ATX_REQUIRE((go_sx == nullptr) == (go_sw == nullptr),
+              "atx_dwconv_bwd_weight: go_sx and go_sw come together");
+  ATX_REQUIRE(!mask_w || scale_w, "atx_dwconv_bwd_weight: mask_w needs scale_w");
+  const int KK = g.KH * g.KW;
+  const long long numel = (long long)g.C * KK;
+  if (numel == 0) return ATX_OK;
+  ATX_REQUIRE(gw && tw, "atx_dwconv_bwd_weight: null pointer");
+  const long long P = (long long)g.N * g.OH * g.OW;
+  if (P == 0) return launch_split_sum(nullptr, 0, numel, KK, nullptr, nullptr, gw, stream);
+  ATX_REQUIRE(go && img && workspace, "atx_dwconv_bwd_weight: null operand/workspace");
+  const long long S = cdiv(P, DW_WSPLIT_ROWS);
+  ATX_REQUIRE(S <= 65535, "atx_dwconv_bwd_weight: N*OH*OW too large");
+  const int offset = dtype == 3 ? 0 : 128;
+  dim3 grid((unsigned)g.C, (unsigned)S);
+  if (dtype == 0)
+    hipLaunchKernelGGL(dwconv_bwd_weight_kernel<int8_t>, grid, dim3(DW_THREADS), 0, stream,
+                       go, (const int8_t*)img, g, offset, pad_index, pad_dev, tw, go_sx, go_sw,
+                       workspace);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(dwconv_bwd_weight_kernel<uint8_t>, grid, dim3(DW_THREADS), 0, stream,
+                       go, (const uint8_t*)img, g, offset, pad_index, pad_dev, tw, go_sx, go_sw,
+                       workspace);
+  else
+    hipLaunchKernelGGL(dwconv_bwd_weight_kernel<float>, grid, dim3(DW_THREADS), 0, stream,
+                       go, (const float*)img, g, offset, pad_index, pad_dev, tw, go_sx, go_sw,
+                       workspace);
+  rc = check_launch("dwconv_bwd_weight_kernel");
+  if (rc) return rc;
+  return launch_split_sum(workspace, (int)S, numel, KK, mask_w, scale_w, gw, stream);
+}
+
+}  // extern "C"

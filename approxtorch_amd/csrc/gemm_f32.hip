@@ -525,7 +525,7 @@ split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, in
 }
 
 // Launch of split_sum_kernel: enough groups that the grid has >= 1024 blocks.
-static int launch_split_sum(const float* ws, int S, long long numel, int K,
+int launch_split_sum(const float* ws, int S, long long numel, int K,
                             const uint8_t* mask, const float* scale, float* out,
                             hipStream_t stream) {
   int G = 1;

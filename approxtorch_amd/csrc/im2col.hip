@@ -242,11 +242,7 @@ __global__ void tap_sum_bwd_kernel(const float* __restrict__ go, atx_conv_geom g
   }
 }
 
-}  // namespace atx
-
-using namespace atx;
-
-static int check_geom(const atx_conv_geom& g) {
+int check_geom(const atx_conv_geom& g) {
   ATX_REQUIRE(g.N >= 0 && g.C >= 0 && g.H >= 0 && g.W >= 0, "conv geometry: negative size");
   ATX_REQUIRE(g.KH > 0 && g.KW > 0 && g.SH > 0 && g.SW > 0 && g.DH > 0 && g.DW > 0 &&
                   g.PH >= 0 && g.PW >= 0,
@@ -257,6 +253,10 @@ static int check_geom(const atx_conv_geom& g) {
   ATX_REQUIRE(g.OH > 0 && g.OW > 0, "conv geometry: empty output");
   return ATX_OK;
 }
+
+}  // namespace atx
+
+using namespace atx;
 
 extern "C" {
 

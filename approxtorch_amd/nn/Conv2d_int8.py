@@ -53,9 +53,6 @@ class Conv2d_int8(nn.Module):
                 "Conv2d_int8 supports groups=1 or depthwise "
                 f"(groups == in_channels == out_channels), got groups={groups}, "
                 f"in={in_channels}, out={out_channels}")
-        if groups != 1:
-            raise NotImplementedError(
-                "depthwise Conv2d_int8 (groups == in_channels) is not built for gfx950 yet")
         self.groups = groups
         if grad not in ('ste', 'lre', 'custom'):
             raise ValueError(f"grad must be 'ste', 'lre' or 'custom', got {grad}")

@@ -117,41 +117,67 @@ def bgemm_int8_custom(x, w, lut, dx_lut, dw_lut):
 
 
 # ------------------------------------------------------------- conv level
-def _check_groups(groups):
-    if groups != 1:
-        raise NotImplementedError(
-            "the gfx950 LUT conv supports groups=1; depthwise LUT conv is not built yet")
-
-
 def _conv_setup(x, w, geom):
+    """Geometry and whether the conv is depthwise (groups == C == O, the only
+    grouped form the reference supports: nn/Conv2d_int8.py:35-41)."""
     kernel_size, stride, padding, dilation, groups = geom
-    _check_groups(groups)
     g = ops.conv_geom(tuple(x.shape), kernel_size, stride, padding, dilation)
-    return g
+    if groups == 1:
+        return g, False
+    if groups == g.C and w.size(0) == g.C and w[0].numel() == g.KH * g.KW:
+        return g, True
+    raise NotImplementedError(
+        "Conv2d_int8 supports groups=1 or depthwise (groups == in_channels == "
+        f"out_channels), got groups={groups}, in={g.C}, out={w.size(0)}")
+
+
+def _lut_conv(x, w, lut, g, depthwise):
+    """LUT conv of the fp32 fake-quantized image x with fp32 quantized weights
+    w [O, K]: (y [N, O, OH*OW], wq)."""
+    if depthwise:
+        wq, _, _ = ops._pack_w(w.reshape(g.C, -1).contiguous(), 128)
+        return ops.dwconv_forward(x, wq, lut, g, 128).view(g.N, g.C, -1), wq
+    return ops.conv_forward(x, w, lut, g, 128, 128)
+
+
+def _lut_conv_backward(go, xq8, wq, tx, tw, g, depthwise, **fused):
+    """(grad_x, grad_w [O, K]) of the LUT conv under a per-operand table
+    estimator; `fused` carries the go scale and fake-quant masks."""
+    mx, sx_m = fused.get("mask"), fused.get("scale")
+    mw, sw_m = fused.get("mask_w"), fused.get("scale_w")
+    gsx, gsw = fused.get("go_sx"), fused.get("go_sw")
+    if depthwise:
+        gx = ops.dwconv_backward_data(go, wq, tx, g, mask=mx, scale=sx_m, go_sx=gsx, go_sw=gsw)
+        gw = ops.dwconv_backward_weight(go, xq8, tw, g, 128, mask_w=mw, scale_w=sw_m,
+                                        go_sx=gsx, go_sw=gsw)
+        return gx, gw
+    gx = ops.conv_backward_data(go, wq, tx, g, mask=mx, scale=sx_m, go_sx=gsx, go_sw=gsw)
+    gw = ops.conv_backward_weight(go, xq8, tw, g, wq.size(0), 128, mask_w=mw, scale_w=sw_m,
+                                  go_sx=gsx, go_sw=gsw)
+    return gx, gw
 
 
 class _conv2d_int8_ste(Function):
     """Conv-level STE (nn/bgemm_int8.py:229-297).  Forward: implicit-im2col LUT
-    conv of the quantized image; saves the int8 image and uint8 weight
-    indices.  Backward: fp32-MFMA backward-data (+ fold) and backward-weight
-    on the decoded quantized values (zero padding decodes to 0)."""
+    conv (or the depthwise LUT conv for groups == C) of the quantized image;
+    saves the int8 image and uint8 weight indices.  Backward: fp32-MFMA
+    backward-data (+ fold) and backward-weight on the decoded quantized values
+    (zero padding decodes to 0)."""
 
     @staticmethod
     def forward(ctx, x, w, lut, geom):
-        g = _conv_setup(x, w, geom)
-        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
+        g, depthwise = _conv_setup(x, w, geom)
+        y, wq = _lut_conv(x, w, lut, g, depthwise)
         ctx.save_for_backward(x.detach().to(torch.int8), wq)
-        ctx.g = g
+        ctx.g, ctx.depthwise = g, depthwise
         return y
 
     @staticmethod
     def backward(ctx, grad_outputs):
         xq8, wq = ctx.saved_tensors
-        g = ctx.g
         dec = decode_table(xq8.device)
         go = grad_outputs.contiguous()
-        grad_x = ops.conv_backward_data(go, wq, dec, g)
-        grad_w = ops.conv_backward_weight(go, xq8, dec, g, wq.size(0), 128)
+        grad_x, grad_w = _lut_conv_backward(go, xq8, wq, dec, dec, ctx.g, ctx.depthwise)
         return grad_x, grad_w, None, None
 
 
@@ -166,19 +192,18 @@ class _conv2d_int8_lre(Function):
 
     @staticmethod
     def forward(ctx, x, w, lut, dx, dw, geom):
-        g = _conv_setup(x, w, geom)
-        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
+        g, depthwise = _conv_setup(x, w, geom)
+        y, wq = _lut_conv(x, w, lut, g, depthwise)
         ctx.save_for_backward(x.detach().to(torch.int8), wq)
-        ctx.g, ctx.dx, ctx.dw = g, dx, dw
+        ctx.g, ctx.dx, ctx.dw, ctx.depthwise = g, dx, dw, depthwise
         return y
 
     @staticmethod
     def backward(ctx, grad_outputs):
         xq8, wq = ctx.saved_tensors
-        g = ctx.g
         go = grad_outputs.contiguous()
-        grad_x = ops.conv_backward_data(go, wq, ctx.dx.contiguous(), g)
-        grad_w = ops.conv_backward_weight(go, xq8, ctx.dw.contiguous(), g, wq.size(0), 128)
+        grad_x, grad_w = _lut_conv_backward(go, xq8, wq, ctx.dx.contiguous(),
+                                            ctx.dw.contiguous(), ctx.g, ctx.depthwise)
         return grad_x, grad_w, None, None, None, None
 
 
@@ -201,19 +226,24 @@ class _conv2d_int8_fused(Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w):
-        g = _conv_setup(x, weight, geom)
+        g, depthwise = _conv_setup(x, weight, geom)
         O = weight.size(0)
         _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
                                                   q8_dtype=torch.int8)
         _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, -qmax_w, qmax_w,
-                                                            offset=128, want_wt=True)
-        y, _ = ops.conv_forward(xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
-                                sx=scale_x, sw=scale_w,
-                                bias=None if bias is None else bias.detach().contiguous(),
-                                packed_w=(wq, wt, Opad))
+                                                            offset=128,
+                                                            want_wt=not depthwise)
+        b = None if bias is None else bias.detach().contiguous()
+        if depthwise:
+            y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
+                                   sx=scale_x, sw=scale_w, bias=b)
+        else:
+            y, _ = ops.conv_forward(xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
+                                    sx=scale_x, sw=scale_w, bias=b, packed_w=(wq, wt, Opad))
         ctx.save_for_backward(xq8, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
                               tx.contiguous(), tw.contiguous())
         ctx.g, ctx.has_bias, ctx.wshape = g, bias is not None, weight.shape
+        ctx.depthwise = depthwise
         return y.view(g.N, O, g.OH, g.OW)
 
     @staticmethod
@@ -222,13 +252,12 @@ class _conv2d_int8_fused(Function):
         g = ctx.g
         go = grad_output.contiguous()
         gx = gw = gb = None
-        if ctx.needs_input_grad[0]:
-            gx = ops.conv_backward_data(go, wq, tx, g, mask=mask_x, scale=sx, go_sx=sx,
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+            gx, gw = _lut_conv_backward(go, xq8, wq, tx, tw, g, ctx.depthwise, mask=mask_x,
+                                        scale=sx, mask_w=mask_w, scale_w=sw, go_sx=sx,
                                         go_sw=sw)
-        if ctx.needs_input_grad[1]:
-            gw = ops.conv_backward_weight(go, xq8, tw, g, wq.size(0), 128, mask_w=mask_w,
-                                          scale_w=sw, go_sx=sx,
-                                          go_sw=sw).view(ctx.wshape)
+            gx = gx if ctx.needs_input_grad[0] else None
+            gw = gw.view(ctx.wshape) if ctx.needs_input_grad[1] else None
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
         return gx, gw, gb, None, None, None, None, None, None, None, None, None
@@ -249,7 +278,7 @@ class _conv2d_int8_custom(Function):
         kernel_size, stride, padding, dilation, groups = geom
         if groups != 1:
             raise NotImplementedError("custom gradient currently supports only groups=1")
-        g = _conv_setup(x, w, geom)
+        g, _ = _conv_setup(x, w, geom)
         y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
         xu8 = ops.im2col_u8(x.detach(), kernel_size, stride, padding, dilation)
         ctx.save_for_backward(xu8, wq, dx_lut, dw_lut)

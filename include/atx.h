@@ -277,6 +277,35 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype,
                         const uint8_t* mask_w, const float* scale_w, float* gw,
                         float* workspace, hipStream_t stream);
 
+/* ------------------------------------------------- depthwise LUT conv
+ * groups == C == O: y[n,c,oh,ow] = sum_{i,j} LUT[xi(n,c,tap)][wq[c][i*KW+j]]
+ * (taps in ascending (i, j); out-of-image taps -> index pad_index), exact
+ * int32 for the integer LUT classes, fp32 in tap order for ATX_LUT_F32.
+ * img dtype as atx_im2col_rows; wq [C][KH*KW] LUT indices; y [N,C,OH,OW]
+ * with the atx_lut_gemm epilogues (sw / bias indexed by channel).  At most
+ * 64 taps.  Replaces dwconv_fake_int8_claude
+ * (csrc/claude/dwconv_claude.cu:1-285). */
+int atx_dwconv_fwd(const void* img, int dtype, atx_conv_geom g, int pad_index,
+                   const uint8_t* wq, const uint16_t* lut16t, const float* lutf32t,
+                   int lut_class, atx_gemm_epilogue ep, void* y, hipStream_t stream);
+/* STE / LRE backward of the depthwise conv (the grouped
+ * convolution_backward of nn/bgemm_int8.py:162-212,259-295):
+ *   gx[n,c,h,w] = sum over taps/outputs reading (h,w) of go' * tx[wq[c][t]]
+ *   gw[c,t]     = sum_{n,oh,ow} go' * tw[xi(n,c,tap t)]
+ * go' = go * fp32(sx[0] * sw[c]) when go_sx/go_sw are given; mask/scale and
+ * mask_w/scale_w fuse the fake-quant STE as in atx_conv_bwd_data /
+ * atx_conv_bwd_weight. */
+int atx_dwconv_bwd_data(const float* go, const uint8_t* wq, const float* tx,
+                        atx_conv_geom g, const float* go_sx, const float* go_sw,
+                        const uint8_t* mask, const float* scale, float* gx,
+                        hipStream_t stream);
+long long atx_dwconv_bwd_weight_workspace_bytes(atx_conv_geom g);
+int atx_dwconv_bwd_weight(const float* go, const void* img, int dtype,
+                          atx_conv_geom g, int pad_index, const float* pad_dev,
+                          const float* tw, const float* go_sx, const float* go_sw,
+                          const uint8_t* mask_w, const float* scale_w, float* gw,
+                          float* workspace, hipStream_t stream);
+
 /* ------------------------------------------------------- custom gradients
  * grad_x[n,k,l] = sum_o dy[n,o,l] * dx_lut[xi(n,k,l)*256 + wi(o,k)] (ascending o)
  * grad_w[o,k]   = sum_{n,l} dy[n,o,l] * dw_lut[xi(n,k,l)*256 + wi(o,k)]

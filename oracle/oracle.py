@@ -337,6 +337,33 @@ def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d):
     return gx, gw.reshape(ctx["mw"].shape), gb
 
 
+def dwconv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weight_bits=8):
+    """Depthwise Conv2d_int8 (groups == C == O): the LUT conv run per channel,
+    which is how the reference defines its depthwise kernel
+    (csrc/claude/dwconv_claude.cu:3-12; nn/Conv2d_int8.py:35-41,198-205)."""
+    C = x.shape[1]
+    bias = None if bias is None else np.asarray(bias)
+    sw = np.asarray(scale_w, dtype=f32).reshape(-1)
+    ys, ctxs = [], []
+    for c in range(C):
+        y, ctx = conv_int8_forward(x[:, c:c + 1], weight[c:c + 1],
+                                   None if bias is None else bias[c:c + 1], lut, scale_x,
+                                   sw[c:c + 1], k, s, p, d, weight_bits)
+        ys.append(y)
+        ctxs.append(ctx)
+    return np.concatenate(ys, axis=1), ctxs
+
+
+def dwconv_int8_backward(go, ctxs, scale_x, scale_w, kind, tables, k, s, p, d):
+    """Gradients of the depthwise layer: conv_int8_backward per channel."""
+    sw = np.asarray(scale_w, dtype=f32).reshape(-1)
+    parts = [conv_int8_backward(go[:, c:c + 1], ctxs[c], scale_x, sw[c:c + 1], kind, tables,
+                                k, s, p, d) for c in range(len(ctxs))]
+    return (np.concatenate([q[0] for q in parts], axis=1),
+            np.concatenate([q[1] for q in parts], axis=0),
+            np.concatenate([q[2] for q in parts], axis=0))
+
+
 def conv_uint8_forward(x, weight, bias, lut, scale_x, zero_x, scale_w, zero_w, k, s, p, d,
                        qmax_w=255):
     """Conv2d_uint8.forward with given qparams (nn/Conv2d_uint8.py:257-325)."""

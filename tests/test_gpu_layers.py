@@ -77,6 +77,44 @@ def test_conv2d_int8_forward_backward(kind, gi):
     close(layer.bias.grad, gb)
 
 
+@pytest.mark.parametrize("kind", ["ste", "lre"])
+@pytest.mark.parametrize("gi", [0, 1, 4, 5])
+def test_conv2d_int8_depthwise_forward_backward(kind, gi):
+    """groups == in == out (MobileNet's depthwise conv) through the depthwise
+    LUT kernel, against the oracle's per-channel layer."""
+    gm = GEOMS[gi]
+    torch.manual_seed(20 + gi)
+    lut = perturbed_lut(20 + gi)
+    dx, dw = tables(kind, lut)
+    C = 12
+    layer = at.nn.Conv2d_int8(C, C, gm["k"], torch.from_numpy(lut).to(DEV), grad=kind,
+                              dx=None if dx is None else torch.from_numpy(dx).to(DEV),
+                              dw=None if dw is None else torch.from_numpy(dw).to(DEV),
+                              bias=True, stride=gm["s"], padding=gm["p"], dilation=gm["d"],
+                              groups=C).to(DEV)
+    layer.eval()
+    x = torch.randn(3, C, 13, 12, device=DEV)
+    with torch.no_grad():
+        layer.scale_x.fill_(float(x.abs().max()) / 110.0)
+    xr = x.clone().requires_grad_()
+    y = layer(xr)
+    k2, s2, p2, d2 = (gm["k"],) * 2, (gm["s"],) * 2, (gm["p"],) * 2, (gm["d"],) * 2
+    sx = np.float32(layer.scale_x.item())
+    sw = layer.scale_w.cpu().numpy()
+    want, ctxs = O.dwconv_int8_forward(x.cpu().numpy(), layer.weight.detach().cpu().numpy(),
+                                       layer.bias.detach().cpu().numpy(), lut, sx, sw,
+                                       k2, s2, p2, d2)
+    close(y, want)
+    go = torch.randn_like(y)
+    y.backward(go)
+    tb = None if kind == "ste" else (dx, dw)
+    gx, gw, gb = O.dwconv_int8_backward(go.cpu().numpy(), ctxs, sx, sw, kind, tb, k2, s2, p2,
+                                        d2)
+    close(xr.grad, gx)
+    close(layer.weight.grad, gw)
+    close(layer.bias.grad, gb)
+
+
 @pytest.mark.parametrize("kind", ["ste", "lre", "custom"])
 @pytest.mark.parametrize("gi", [0, 1, 2, 5])
 def test_conv2d_uint8_forward_backward(kind, gi):

@@ -453,3 +453,92 @@ def test_conv_backward_fused_scale_and_masks(geom):
     close(gi.cpu().numpy(), ex_img, fa / float(sx[0]))
     ew_m = np.where(mask_w, ew, 0.0) / np.maximum(sw, 1e-12)[:, None]
     close(gwk.cpu().numpy(), ew_m, aw / sw[:, None])
+
+
+# ------------------------------------------------------------ depthwise conv
+DW_GEOMS = [((3, 3), (1, 1), (1, 1), (1, 1)), ((3, 3), (2, 2), (1, 1), (1, 1)),
+            ((5, 5), (1, 1), (2, 2), (1, 1)), ((7, 7), (2, 2), (3, 3), (1, 1)),
+            ((3, 3), (1, 1), (2, 2), (2, 2)), ((3, 1), (1, 2), (1, 0), (1, 1))]
+
+
+@pytest.mark.parametrize("geom", DW_GEOMS)
+@pytest.mark.parametrize("dtype", ["int8", "uint8", "float32"])
+def test_dwconv_fake_int8_claude(geom, dtype):
+    """y = per-channel LUT conv (exact int64 oracle), out-of-image taps row 128,
+    and wq = clamp(rint(w) + 128)."""
+    k, s, p, d = geom
+    r = gen(zlib.crc32(repr((geom, dtype)).encode()))
+    C = 24
+    if dtype == "int8":
+        img = r.integers(-128, 128, (3, C, 15, 14)).astype(np.int8)
+    elif dtype == "uint8":
+        img = r.integers(0, 256, (3, C, 15, 14)).astype(np.uint8)
+    else:
+        img = r.integers(-130, 130, (3, C, 15, 14)).astype(np.float32)
+    w = r.integers(-128, 128, (C, k[0] * k[1])).astype(np.float32)
+    lut = luts(5)["perturbed"]
+    y, wq = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
+    xi = O.image_index(img, 128)
+    wi = (w + 128).astype(np.uint8)
+    assert np.array_equal(wq.cpu().numpy(), wi)
+    want = np.concatenate([O.lut_gemm_i64(O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128),
+                                          wi[c:c + 1], lut) for c in range(C)], axis=1)
+    OH, OW = O.out_size(15, 14, k, s, p, d)
+    assert y.shape == (3, C, OH, OW)
+    assert np.array_equal(y.cpu().numpy().reshape(3, C, -1), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("lut_name", ["u16_c5", "fp32"])
+def test_dwconv_lut_classes(lut_name):
+    r = gen(21)
+    k, s, p, d = DW_GEOMS[0]
+    img = r.integers(-128, 128, (2, 9, 10, 11)).astype(np.int8)
+    w = r.integers(-128, 128, (9, 9)).astype(np.float32)
+    xi = O.im2col_index(O.image_index(img, 128), k, s, p, d, 128)
+    wi = (w + 128).astype(np.uint8)
+    if lut_name == "fp32":
+        lut = (r.standard_normal(65536) * 3).astype(np.float32)
+        want = np.concatenate([O.lut_gemm_f32(xi[:, 9 * c:9 * c + 9], wi[c:c + 1], lut)
+                               for c in range(9)], axis=1)
+        y, _ = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut), k, s, p, d)
+        assert np.array_equal(y.cpu().numpy().reshape(2, 9, -1), want)
+    else:
+        lut = luts(5)[lut_name]
+        want = np.concatenate([O.lut_gemm_i64(xi[:, 9 * c:9 * c + 9], wi[c:c + 1], lut)
+                               for c in range(9)], axis=1)
+        y, _ = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
+        assert np.array_equal(y.cpu().numpy().reshape(2, 9, -1), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("geom", DW_GEOMS)
+def test_dwconv_backward_kernels(geom):
+    """Per-channel table gradients (gemm_grads + fold per channel) with the
+    go scale and both fake-quant STE masks fused."""
+    k, s, p, d = geom
+    r = gen(zlib.crc32(repr(geom).encode()) + 3)
+    C = 20
+    img = r.integers(-127, 128, (3, C, 13, 12)).astype(np.int8)
+    wi = r.integers(0, 256, (C, k[0] * k[1]), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    go = r.standard_normal((3, C, g.OH, g.OW)).astype(np.float32)
+    tx = r.standard_normal(256).astype(np.float32)
+    tw = r.standard_normal(256).astype(np.float32)
+    sx = np.array([0.031], np.float32)
+    sw = r.uniform(1e-3, 4e-2, C).astype(np.float32)
+    mask_x = r.random(img.shape) < 0.9
+    mask_w = r.random(wi.shape) < 0.9
+    gi = ops.dwconv_backward_data(t(go), t(wi), t(tx), g, mask=t(mask_x), scale=t(sx),
+                                  go_sx=t(sx), go_sw=t(sw)).cpu().numpy()
+    gwk = ops.dwconv_backward_weight(t(go), t(img), t(tw), g, 128, mask_w=t(mask_w),
+                                     scale_w=t(sw), go_sx=t(sx), go_sw=t(sw)).cpu().numpy()
+    xi = O.image_index(img)
+    for c in range(C):
+        gos = go[:, c:c + 1].reshape(3, 1, -1) * (sx[0] * sw[c])
+        xc = O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128)
+        ex, ew = O.gemm_grads(gos, xc, wi[c:c + 1], "lre", (tx, tw))
+        ax, aw = O.gemm_grads(np.abs(gos), xc, wi[c:c + 1], "lre", (np.abs(tx), np.abs(tw)))
+        shp = (3, 1, 13, 12)
+        fx, fa = O.fold(ex, shp, k, s, p, d), O.fold(ax, shp, k, s, p, d)
+        close(gi[:, c:c + 1], np.where(mask_x[:, c:c + 1], fx, 0.0) / float(sx[0]),
+              fa / float(sx[0]))
+        close(gwk[c:c + 1], np.where(mask_w[c:c + 1], ew, 0.0) / float(sw[c]), aw / float(sw[c]))

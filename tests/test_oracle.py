@@ -291,3 +291,57 @@ def test_uint8_layer_exact_lut_is_centred_conv_and_grads_match_autograd():
     (yy * torch.from_numpy(go)).sum().backward()
     assert np.allclose(gx, xt.grad.numpy(), rtol=1e-9, atol=1e-8)
     assert np.allclose(gw, wt.grad.numpy(), rtol=1e-9, atol=1e-8)
+
+
+@pytest.mark.parametrize("geom", [((3, 3), (1, 1), (1, 1), (1, 1)), ((3, 3), (2, 2), (1, 1), (1, 1)),
+                                  ((5, 3), (1, 2), (2, 0), (2, 1))])
+def test_dwconv_oracle_bruteforce_and_ste_autograd(geom):
+    """Depthwise oracle (per-channel LUT conv): the forward against a direct
+    loop over pixels and taps with an asymmetric LUT (out-of-image taps = row
+    128), the STE gradients of an exact-product LUT against torch's grouped
+    conv2d autograd in fp64."""
+    k, s, p, d = geom
+    C = 3
+    x = rng.standard_normal((2, C, 7, 6)).astype(np.float32)
+    w = rng.standard_normal((C, 1, *k)).astype(np.float32) * 0.4
+    b = rng.standard_normal(C).astype(np.float32)
+    sx = np.float32(np.abs(x).max() / 100)
+    sw = (np.abs(w).reshape(C, -1).max(axis=1) / 100).astype(np.float32)
+    v = np.arange(256)
+    lut = (37 * v[:, None] - 19 * v[None, :] + 11).reshape(-1)
+    y, _ = O.dwconv_int8_forward(x, w, b, lut, sx, sw, k, s, p, d)
+    qx, _ = O.fakequant(x, sx, -127, 127)
+    qw, _ = O.fakequant(w, sw.reshape(C, 1, 1, 1), -127, 127)
+    xi = O.image_index(qx, 128)
+    wi = O.image_index(qw.reshape(C, -1), 128)
+    OH, OW = O.out_size(7, 6, k, s, p, d)
+    sc = (sx * sw).astype(np.float32).astype(np.float64)
+    for n in range(2):
+        for c in range(C):
+            for oh in range(OH):
+                for ow in range(OW):
+                    acc = 0
+                    for i in range(k[0]):
+                        for j in range(k[1]):
+                            ih, iw = oh * s[0] - p[0] + i * d[0], ow * s[1] - p[1] + j * d[1]
+                            xv = int(xi[n, c, ih, iw]) if 0 <= ih < 7 and 0 <= iw < 6 else 128
+                            acc += int(lut[xv * 256 + int(wi[c, i * k[1] + j])])
+                    assert y[n, c, oh, ow] == acc * sc[c] + np.float64(b[c])
+    a = v - 128
+    plut = (a[:, None] * a[None, :]).reshape(-1)
+    go = rng.standard_normal((2, C, OH, OW))
+    _, ctxs = O.dwconv_int8_forward(x, w, None, plut, sx, sw, k, s, p, d)
+    gx, gw, _ = O.dwconv_int8_backward(go, ctxs, sx, sw, "ste", None, k, s, p, d)
+    xt = torch.from_numpy(x).double().requires_grad_()
+    wt = torch.from_numpy(w).double().requires_grad_()
+    vx = xt / float(sx)
+    mx = ((vx >= -127) & (vx <= 127)).double()
+    qxt = torch.clamp(torch.round(vx), -127, 127).detach() + (vx - vx.detach()) * mx
+    vw = wt / torch.from_numpy(sw).double().view(-1, 1, 1, 1)
+    mw = ((vw >= -127) & (vw <= 127)).double()
+    qwt = torch.clamp(torch.round(vw), -127, 127).detach() + (vw - vw.detach()) * mw
+    yt = F.conv2d(qxt, qwt, None, s, p, d, groups=C)
+    sct = torch.from_numpy((sx * sw).astype(np.float32)).double().view(1, -1, 1, 1)
+    (yt * sct * torch.from_numpy(go)).sum().backward()
+    assert np.allclose(gx, xt.grad.numpy(), rtol=1e-9, atol=1e-9)
+    assert np.allclose(gw, wt.grad.numpy(), rtol=1e-9, atol=1e-9)
