@@ -8,7 +8,7 @@
 // csrc/claude/dwconv_claude.cu:1-285 (forward) and the grouped
 // convolution_backward of nn/bgemm_int8.py:162-212,259-295.
 //
-// Forward: a block owns one (image, channel) plane slice; the channel's
+// Forward: a block owns a run of one channel's N*OH*OW outputs; the channel's
 // KH*KW table columns LUT[.][wi(c,t)] (512 B each in the 16-bit image) are
 // staged in LDS, every thread walks output pixels and sums its taps in
 // ascending (i, j) order: exact int32 for the integer LUT classes, fp32 in
@@ -54,10 +54,11 @@ template <typename T, typename ENTRY, bool SIGNED>
 __global__ void __launch_bounds__(DW_THREADS)
 dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad,
                   const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
-                  const float* __restrict__ lutf32t, DwEpilogue ep, void* __restrict__ y) {
+                  const float* __restrict__ lutf32t, DwEpilogue ep, void* __restrict__ y,
+                  int chunk) {
   extern __shared__ __align__(16) unsigned char dw_smem[];
   ENTRY* tab = (ENTRY*)dw_smem;
-  const int c = blockIdx.y, n = blockIdx.z;
+  const int c = blockIdx.y;
   const int KK = g.KH * g.KW;
   for (int e = threadIdx.x; e < KK * 256; e += blockDim.x) {
     const int t = e >> 8, x = e & 255;
@@ -71,14 +72,19 @@ dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pa
   }
   __syncthreads();
   const int L = g.OH * g.OW;
-  const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
   float sc = 1.0f, bi = 0.0f;
   if (ep.out_kind == ATX_OUT_DEQUANT) {
     sc = ep.sx[0] * ep.sw[c];
     if (ep.bias) bi = ep.bias[c];
   }
-  const long long ybase = ((long long)n * g.C + c) * L;
-  for (int l = blockIdx.x * blockDim.x + threadIdx.x; l < L; l += gridDim.x * blockDim.x) {
+  // this block's run of the channel's N*L outputs (p = n*L + l)
+  const long long P = (long long)g.N * L;
+  const long long pb = (long long)blockIdx.x * chunk;
+  const long long pe = min(P, pb + chunk);
+  for (long long p = pb + threadIdx.x; p < pe; p += blockDim.x) {
+    const int n = (int)(p / L), l = (int)(p - (long long)n * L);
+    const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
+    const long long ybase = ((long long)n * g.C + c) * L;
     const int oh = l / g.OW, ow = l - oh * g.OW;
     ENTRY acc = 0;
     for (int i = 0; i < g.KH; ++i) {
@@ -210,7 +216,7 @@ static int dw_check(const atx_conv_geom& g, int dtype, int pad_index, const char
   ATX_REQUIRE(dtype >= 0 && dtype <= 3, "%s: bad dtype %d", what, dtype);
   ATX_REQUIRE(pad_index >= 0 && pad_index <= 255, "%s: bad pad_index", what);
   ATX_REQUIRE(g.KH * g.KW <= DW_MAX_TAPS, "%s: at most %d taps", what, DW_MAX_TAPS);
-  ATX_REQUIRE(g.C <= 65535 && g.N <= 65535, "%s: C and N must be <= 65535", what);
+  ATX_REQUIRE(g.C <= 65535, "%s: C must be <= 65535", what);
   return ATX_OK;
 }
 
@@ -218,20 +224,24 @@ template <typename T>
 static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int pad,
                           const uint8_t* wq, const uint16_t* l16, const float* lf32, int cls,
                           const DwEpilogue& ep, void* y, hipStream_t stream) {
-  const int L = g.OH * g.OW;
   const int KK = g.KH * g.KW;
-  dim3 grid((unsigned)std::max<long long>(1, std::min<long long>(cdiv(L, DW_THREADS), 64)),
-            (unsigned)g.C, (unsigned)g.N);
+  // about 2048 blocks in all, each a run of at least 1024 outputs of one
+  // channel, so the channel's table is staged once per run
+  const long long P = (long long)g.N * g.OH * g.OW;
+  const long long per_c = std::max<long long>(1, cdiv(2048, g.C));
+  const long long chunk = std::min<long long>(
+      1LL << 30, std::max<long long>(1024, cdiv(cdiv(P, per_c), DW_THREADS) * DW_THREADS));
+  dim3 grid((unsigned)cdiv(P, chunk), (unsigned)g.C);
   const size_t smem = (size_t)KK * 256 * 4;
   if (cls == ATX_LUT_F32)
     hipLaunchKernelGGL((dwconv_fwd_kernel<T, float, false>), grid, dim3(DW_THREADS), smem,
-                       stream, img, g, offset, pad, wq, l16, lf32, ep, y);
+                       stream, img, g, offset, pad, wq, l16, lf32, ep, y, (int)chunk);
   else if (cls == ATX_LUT_I16)
     hipLaunchKernelGGL((dwconv_fwd_kernel<T, int, true>), grid, dim3(DW_THREADS), smem, stream,
-                       img, g, offset, pad, wq, l16, lf32, ep, y);
+                       img, g, offset, pad, wq, l16, lf32, ep, y, (int)chunk);
   else
     hipLaunchKernelGGL((dwconv_fwd_kernel<T, int, false>), grid, dim3(DW_THREADS), smem, stream,
-                       img, g, offset, pad, wq, l16, lf32, ep, y);
+                       img, g, offset, pad, wq, l16, lf32, ep, y, (int)chunk);
 }
 
 }  // namespace atx

@@ -20,6 +20,7 @@ Also reported:
   lut_gemm      the standalone BGEMM microbench (config 3: B=32, 4096x2304 by
                 2304x256, perturbed LUT) in G LUT-MAC/s.
   gemm2d        the plain torch.mm-layout LUT GEMM on Linear-shaped operands.
+  dwconv        the depthwise LUT conv over MobileNetV2's depthwise layers.
   cpu_baseline  the torch-CPU restatement of the same training step
                 (oracle/torch_cpu.py) on a bounded sample (batch 1), scaled to img/s.
 """
@@ -208,6 +209,38 @@ def gemm2d_microbench(torch, reps=5):
     return out
 
 
+def dwconv_microbench(torch, reps=10):
+    """Depthwise LUT conv forward (dwconv_fake_int8_claude) over the distinct
+    MobileNetV2 depthwise layers (width 1.0, 224^2 input, batch 64, 3x3): total
+    G LUT-MAC/s and the HBM rate of its algorithmic bytes (int8 image read
+    once, fp32 output written once) -- the kernel is HBM-bound."""
+    from approxtorch_amd import workloads
+    from approxtorch_amd.backend import ops
+    lut = torch.from_numpy(workloads.lut_perturbed(3)).cuda()
+    g = torch.Generator().manual_seed(6)
+    B, ms_total, macs, nbytes = 64, 0.0, 0, 0
+    for C, H, st in ((32, 112, 1), (96, 112, 2), (144, 56, 1), (144, 56, 2), (192, 28, 1),
+                     (192, 28, 2), (384, 14, 1), (576, 14, 1), (576, 14, 2), (960, 7, 1)):
+        x = torch.randint(-127, 128, (B, C, H, H), generator=g, dtype=torch.int8).cuda()
+        w = torch.randint(-127, 128, (C, 9), generator=g).float().cuda()
+        ops.dwconv_fake_int8_claude(x, w, lut, 3, st, 1, 1)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            ops.dwconv_fake_int8_claude(x, w, lut, 3, st, 1, 1)
+        e.record()
+        torch.cuda.synchronize()
+        ms_total += s.elapsed_time(e) / reps
+        OH = (H - 1) // st + 1
+        macs += B * C * OH * OH * 9
+        nbytes += B * C * H * H + B * C * OH * OH * 4
+        del x, w
+    return {"lut_mac_per_s_G": round(macs / (ms_total * 1e-3) / 1e9, 1),
+            "hbm_GBs": round(nbytes / (ms_total * 1e-3) / 1e9, 1),
+            "ms_all_layers": round(ms_total, 3)}
+
+
 def cpu_baseline(model, cfg, sample_batch):
     import torch
     from approxtorch_amd import workloads
@@ -283,6 +316,7 @@ def main():
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
         result["gemm2d_GLUTMACs"] = gemm2d_microbench(torch)
+        result["dwconv_mobilenetv2"] = dwconv_microbench(torch)
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:
