@@ -11,5 +11,6 @@ from . import nn
 from .convert_model import convert_model
 from . import load_lut
 from . import grad_lut
+from . import calib
 
-__all__ = ["backend", "nn", "convert_model", "load_lut", "grad_lut"]
+__all__ = ["backend", "nn", "convert_model", "load_lut", "grad_lut", "calib"]

@@ -1,0 +1,145 @@
+"""calib.calibrate_int8 / calibrate_uint8 (approxtorch/calib.py): layer
+selection, statistics, parameter formulas, state_dict layout, errors, and
+that a calibrated checkpoint loads into a converted model.  The CPU tests
+check the host logic with torch's reductions; the GPU test checks that the
+device-reduction path gives the same state_dict bit for bit."""
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from approxtorch_amd import calib, convert_model
+from approxtorch_amd.nn import Conv2d_int8, Conv2d_uint8
+
+LUT = torch.zeros(65536)
+
+
+def small_model():
+    torch.manual_seed(0)
+    m = nn.Sequential(nn.Conv2d(3, 4, 3, padding=1), nn.ReLU(), nn.Conv2d(4, 5, 3, bias=False),
+                      nn.BatchNorm2d(5), nn.Conv2d(5, 6, 1))
+    with torch.no_grad():
+        m[2].weight[1].zero_()                    # an all-zero output channel
+    return m
+
+
+def batches(n=3, b=4, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(b, 3, 8, 8, generator=g), torch.zeros(b)) for _ in range(n)]
+
+
+def layer_inputs(model, data):
+    """Inputs of model[2] and model[4] over the batches (independent forward)."""
+    ins = {"2": [], "4": []}
+    with torch.no_grad():
+        for x, _ in data:
+            h = model[1](model[0](x))
+            ins["2"].append(h)
+            ins["4"].append(model[3](model[2](h)))
+    return {k: torch.cat(v) for k, v in ins.items()}
+
+
+def test_calibrate_int8_values_and_layout(tmp_path):
+    model = small_model()
+    data = batches()
+    path = os.path.join(tmp_path, "int8.pt")
+    sd = calib.calibrate_int8(model, data, 12, path, weight_bits=6)
+    ins = layer_inputs(model, data)
+    keys = list(sd.keys())
+    # first conv skipped; scale_x / scale_w follow each layer's last entry
+    assert "0.scale_x" not in sd
+    assert keys[keys.index("2.weight") + 1:keys.index("2.weight") + 3] == ["2.scale_x", "2.scale_w"]
+    assert keys[keys.index("4.bias") + 1:keys.index("4.bias") + 3] == ["4.scale_x", "4.scale_w"]
+    for name in ("2", "4"):
+        absmax = float(ins[name].abs().max())
+        assert sd[f"{name}.scale_x"].dtype == torch.float32
+        assert sd[f"{name}.scale_x"].item() == np.float32(absmax / 127.0)
+        w = model[int(name)].weight.detach()
+        want = w.abs().amax(dim=(1, 2, 3)) / 31
+        want = torch.where(want > 0, want, torch.ones_like(want))
+        assert torch.equal(sd[f"{name}.scale_w"], want)
+    assert sd["2.scale_w"][1].item() == 1.0
+    loaded = torch.load(path, weights_only=True)
+    assert list(loaded.keys()) == keys
+    # the calibrated checkpoint loads into the converted model
+    conv = convert_model(small_model(), LUT, qtype="int8", weight_bits=6)
+    assert isinstance(conv[2], Conv2d_int8) and isinstance(conv[4], Conv2d_int8)
+    missing, unexpected = conv.load_state_dict(sd, strict=False)
+    assert set(missing) == {"2.lut", "4.lut"} and not unexpected   # the LUT is not a float-model key
+    assert conv[4].scale_x.item() == sd["4.scale_x"].item()
+    with pytest.raises(ValueError, match="weight_bits"):
+        calib.calibrate_int8(model, data, 4, path, weight_bits=9)
+
+
+def test_calibrate_uint8_values_truncation_and_state(tmp_path):
+    model = small_model()
+    model.train()
+    model[3].eval()                                    # mixed train/eval flags are kept
+    data = batches(n=3, b=5)
+    sd = calib.calibrate_uint8(model, data, 7)         # 5 + 2 of the second batch
+    assert model.training and not model[3].training
+    ins = layer_inputs(model, [data[0], (data[1][0][:2], None)])
+    for name in ("2", "4"):
+        x = ins[name]
+        x_min = torch.clamp(x.min(), max=0.0)
+        x_max = torch.clamp(x.max(), min=0.0)
+        assert torch.equal(sd[f"{name}.x_min"], x_min) and torch.equal(sd[f"{name}.x_max"], x_max)
+        scale = torch.clamp((x_max - x_min) / 255, min=1e-12)
+        assert torch.equal(sd[f"{name}.scale_x"], scale)
+        assert torch.equal(sd[f"{name}.zero_x"], torch.round(-x_min / scale).clamp(0, 255))
+        w = model[int(name)].weight.detach()
+        w_min = torch.clamp(w.amin(dim=(1, 2, 3)), max=0.0)
+        w_max = torch.clamp(w.amax(dim=(1, 2, 3)), min=0.0)
+        assert torch.equal(sd[f"{name}.w_min"], w_min) and torch.equal(sd[f"{name}.w_max"], w_max)
+        assert sd[f"{name}.zero_w"].dtype == torch.float32
+    conv = convert_model(small_model(), LUT, qtype="uint8")
+    assert isinstance(conv[2], Conv2d_uint8)
+    missing, unexpected = conv.load_state_dict(sd, strict=False)
+    assert set(missing) == {"2.lut", "4.lut"} and not unexpected
+    assert torch.equal(conv[2].zero_w, sd["2.zero_w"])
+    path = os.path.join(tmp_path, "u8.pt")
+    calib.calibrate_uint8(model, data, None, save_path=path)
+    assert set(torch.load(path, weights_only=True).keys()) >= {"2.zero_x", "4.w_max"}
+
+
+def test_calibrate_uint8_errors():
+    model = small_model()
+    data = batches()
+    with pytest.raises(TypeError):
+        calib.calibrate_uint8(model, data, True)
+    with pytest.raises(ValueError):
+        calib.calibrate_uint8(model, data, 0)
+    with pytest.raises(ValueError, match="no Conv2d"):
+        calib.calibrate_uint8(nn.Sequential(nn.Conv2d(3, 3, 1)), data, 4)
+    with pytest.raises(ValueError, match="no calibration samples"):
+        calib.calibrate_uint8(model, [], 4)
+    with pytest.raises(TypeError):
+        calib.calibrate_uint8(model, [("not a tensor",)], 4)
+    bad = [(torch.full((2, 3, 8, 8), float("nan")), None)]
+    with pytest.raises(ValueError, match="non-finite"):
+        calib.calibrate_uint8(model, bad, 4)
+    only_first = calib.calibrate_uint8(nn.Sequential(nn.Conv2d(3, 3, 1)), data, 4,
+                                       ignore_first_conv=False)
+    assert "0.scale_x" in only_first and "scale_x" not in only_first
+
+
+@pytest.mark.gpu
+def test_calibration_device_reductions_match_torch(tmp_path, monkeypatch):
+    """On a CUDA model the statistics come from atx_absmax / atx_minmax; they
+    equal torch's reductions of the same activations bit for bit, so the
+    whole calibrated state_dict does."""
+    data = batches(n=2, b=6, seed=5)
+    model = small_model().cuda()
+    dev8 = calib.calibrate_int8(model, data, 12, os.path.join(tmp_path, "a.pt"))
+    dev_u = calib.calibrate_uint8(model, data, 9)
+    monkeypatch.setattr(calib, "_absmax", lambda x: x.abs().max().to(torch.float32))
+    monkeypatch.setattr(calib, "_minmax",
+                        lambda x: (x.amin().to(torch.float32), x.amax().to(torch.float32)))
+    ref8 = calib.calibrate_int8(model, data, 12, os.path.join(tmp_path, "b.pt"))
+    ref_u = calib.calibrate_uint8(model, data, 9)
+    for a, b in ((dev8, ref8), (dev_u, ref_u)):
+        assert list(a.keys()) == list(b.keys())
+        for k in a:
+            assert torch.equal(a[k], b[k]), k
