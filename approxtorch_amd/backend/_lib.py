@@ -72,6 +72,9 @@ _SIGS = {
                                       c_int, c_vp]),
     "atx_pack_cols_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
                                       c_int, c_vp]),
+    "atx_parse_text_table": (c_int, [ctypes.c_char_p, c_int, c_vp, c_ll, c_vp]),
+    "atx_lre_tables": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp]),
+    "atx_date_tables": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp]),
     "atx_dwconv_fwd": (c_int, [c_vp, c_int, ConvGeom, c_int, c_vp, c_vp, c_vp, c_int,
                                GemmEpilogue, c_vp, c_vp]),
     "atx_dwconv_bwd_data": (c_int, [c_vp, c_vp, c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp, c_vp,

@@ -7,6 +7,7 @@ launches the HIP kernels on the current stream.  The GEMM operands are
 re-laid out for the gfx950 kernels (row-offset activations, transposed
 weights) inside these wrappers; callers see the reference's shapes.
 """
+import os
 import threading
 from collections import OrderedDict
 
@@ -26,7 +27,8 @@ __all__ = [
     "conv_backward_data", "conv_backward_weight", "col2im", "gemm_fake_int8_claude",
     "gemm_fake_int8_claude_save", "gemm_fake_int8_claude_cfg", "gemm_fake_uint8_claude",
     "gemm_fake_uint8_claude_save", "gemm_fake_uint8_claude_cfg", "dwconv_fake_int8_claude",
-    "dwconv_forward", "dwconv_backward_data", "dwconv_backward_weight",
+    "dwconv_forward", "dwconv_backward_data", "dwconv_backward_weight", "parse_text_table",
+    "lre_tables", "date_tables",
 ]
 
 # --------------------------------------------------------------------- LUTs
@@ -78,6 +80,74 @@ def lut_image(lut: Tensor, transposed: bool = False):
         while len(_LUT_CACHE) > _LUT_CACHE_MAX:
             _LUT_CACHE.popitem(last=False)
     return val
+
+
+# ------------------------------------------------ LUT files and gradient tables
+def parse_text_table(path, integral=False, capacity=1 << 24):
+    """fp32 numpy array of the numbers in a text table file (whitespace or
+    comma separated, '#' comments): the native replacement of the
+    numpy.loadtxt calls in load_lut.py:5-55.  Malformed files raise ValueError
+    (numpy.loadtxt's error type)."""
+    import numpy as np
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not found.")
+    out = np.empty(capacity, dtype=np.float32)
+    count = np.zeros(1, dtype=np.int64)
+    lib = L.load()
+    rc = lib.atx_parse_text_table(os.fsencode(os.fspath(path)), int(bool(integral)),
+                                  out.ctypes.data, capacity, count.ctypes.data)
+    if rc != 0:
+        raise ValueError(lib.atx_last_error().decode(errors="replace"))
+    return out[:int(count[0])].copy()
+
+
+_TABLE_CACHE = OrderedDict()
+
+
+def _cached_tables(kind, lut, param, launch):
+    _check_lut(lut)
+    key = (kind, param, lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset())
+    with _LUT_LOCK:
+        hit = _TABLE_CACHE.get(key)
+        if hit is not None:
+            _TABLE_CACHE.move_to_end(key)
+            return hit[0], hit[1]
+    lc = lut.contiguous()
+    a, b = launch(lc)
+    with _LUT_LOCK:
+        _TABLE_CACHE[key] = (a, b, lut)   # keep the LUT alive: its pointer is the key
+        while len(_TABLE_CACHE) > _LUT_CACHE_MAX:
+            _TABLE_CACHE.popitem(last=False)
+    return a, b
+
+
+def lre_tables(lut: Tensor, qtype: str = "int8"):
+    """(grad_a [256], grad_b [256]) LRE slope tables of a CUDA fp32 LUT, on the
+    device, cached per LUT (grad_lut.py:14-37; uint8 operands: qtype='uint8')."""
+    if qtype not in ("int8", "uint8"):
+        raise ValueError(f"qtype must be 'int8' or 'uint8', got {qtype!r}")
+    offset = 128 if qtype == "int8" else 0
+
+    def launch(lc):
+        ga = torch.empty(256, dtype=torch.float32, device=lc.device)
+        gb = torch.empty(256, dtype=torch.float32, device=lc.device)
+        L.call("atx_lre_tables", L.ptr(lc), offset, L.ptr(ga), L.ptr(gb), L.stream_of(lc))
+        return ga, gb
+    return _cached_tables("lre", lut, offset, launch)
+
+
+def date_tables(lut: Tensor, half_ws: int = 32):
+    """(grad_a, grad_b) [65536] DATE tables of a CUDA fp32 LUT, on the device,
+    cached per LUT (grad_lut.py:39-142)."""
+    if not 0 <= half_ws <= 127:
+        raise ValueError(f"half_ws must be in [0, 127], got {half_ws}")
+
+    def launch(lc):
+        ga = torch.empty(65536, dtype=torch.float32, device=lc.device)
+        gb = torch.empty(65536, dtype=torch.float32, device=lc.device)
+        L.call("atx_date_tables", L.ptr(lc), half_ws, L.ptr(ga), L.ptr(gb), L.stream_of(lc))
+        return ga, gb
+    return _cached_tables("date", lut, half_ws, launch)
 
 
 # -------------------------------------------------------------- LUT GEMM

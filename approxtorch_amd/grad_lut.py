@@ -11,11 +11,24 @@ DATE(multiplier, half_ws, save_path)   approxtorch/grad_lut.py:39-142
     edges), then central differences inside (h, 255-h) and the end-to-end
     slope (s[255]-s[0])/255 elsewhere.
 
-`multiplier` may be a text-file path (as in the reference) or a 256 x 256
-array / tensor.  Extension: lre also handles qtype='uint8' (operands 0..255);
-the reference returns None there.
+`multiplier` may be a text-file path (as in the reference), a 256 x 256
+array, or a tensor.  A CUDA tensor is handled on the device by the
+library's generators (ops.lre_tables / ops.date_tables, cached per LUT) and
+gives CUDA tensors; the other inputs give numpy arrays as in the reference,
+the same values (the device DATE kernel reproduces numpy's float32 window
+means).  Extension: lre also handles qtype='uint8' (operands 0..255); the
+reference returns None there.
 """
 import numpy as np
+import torch
+
+from .backend import ops
+
+
+def _device_lut(multiplier):
+    if isinstance(multiplier, torch.Tensor) and multiplier.is_cuda:
+        return multiplier.detach().to(torch.float32).reshape(-1).contiguous()
+    return None
 
 
 def _as_table(multiplier):
@@ -24,7 +37,7 @@ def _as_table(multiplier):
     elif hasattr(multiplier, "detach"):
         lut = multiplier.detach().cpu().numpy()
     else:
-        lut = np.loadtxt(multiplier, dtype=np.float32)
+        lut = ops.parse_text_table(multiplier)
     lut = np.asarray(lut, dtype=np.float32).reshape(256, 256)
     return lut
 
@@ -39,6 +52,13 @@ def _ols_slopes(values, lines):
 
 
 def lre(multiplier, qtype, save_path=None):
+    dev = _device_lut(multiplier)
+    if dev is not None and qtype in ('int8', 'uint8'):
+        grad_a, grad_b = ops.lre_tables(dev, qtype)
+        if save_path is not None:
+            np.savetxt(f'{save_path}_lre_grad_a.txt', grad_a.cpu().numpy(), fmt='%.4f')
+            np.savetxt(f'{save_path}_lre_grad_b.txt', grad_b.cpu().numpy(), fmt='%.4f')
+        return grad_a.clone(), grad_b.clone()
     lut = _as_table(multiplier)
     if qtype == 'int8':
         vals = np.arange(-128, 128)
@@ -78,6 +98,14 @@ def _diff(smooth_lines, half_ws):
 def DATE(multiplier, half_ws=32, save_path=None):
     """Smoothing + difference gradients: returns (grad_a, grad_b), each 256 x 256
     float32, the derivative along the row operand a and the column operand b."""
+    dev = _device_lut(multiplier)
+    if dev is not None and 0 <= half_ws <= 127:
+        ga, gb = ops.date_tables(dev, half_ws)
+        ga, gb = ga.view(256, 256).clone(), gb.view(256, 256).clone()
+        if save_path is not None:
+            np.savetxt(f'{save_path}_date_{half_ws}_grad_a.txt', ga.cpu().numpy())
+            np.savetxt(f'{save_path}_date_{half_ws}_grad_b.txt', gb.cpu().numpy())
+        return ga, gb
     lut = _as_table(multiplier)
     grad_a = _diff(_smooth(lut.T.copy(), half_ws), half_ws).T.copy()
     grad_b = _diff(_smooth(lut.copy(), half_ws), half_ws)

@@ -277,6 +277,20 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype,
                         const uint8_t* mask_w, const float* scale_w, float* gw,
                         float* workspace, hipStream_t stream);
 
+/* ----------------------------------------------- LUT files and gradient tables
+ * Host: parses a text table (numbers separated by whitespace or commas, '#'
+ * comments; integral != 0 rejects non-integers) into out[capacity]; *count
+ * = values read.  Replaces the numpy.loadtxt calls of load_lut.py:5-55.
+ * Device: LRE slope tables (grad_lut.py:14-37; offset 128 = int8 operands,
+ * 0 = uint8) and DATE tables (grad_lut.py:39-142; half_ws in [0, 127],
+ * grad_a/grad_b [65536] indexed like the LUT) of an fp32 LUT [65536]. */
+int atx_parse_text_table(const char* path, int integral, float* out,
+                         long long capacity, long long* count);
+int atx_lre_tables(const float* lut, int offset, float* grad_a, float* grad_b,
+                   hipStream_t stream);
+int atx_date_tables(const float* lut, int half_ws, float* grad_a, float* grad_b,
+                    hipStream_t stream);
+
 /* ------------------------------------------------- depthwise LUT conv
  * groups == C == O: y[n,c,oh,ow] = sum_{i,j} LUT[xi(n,c,tap)][wq[c][i*KW+j]]
  * (taps in ascending (i, j); out-of-image taps -> index pad_index), exact
