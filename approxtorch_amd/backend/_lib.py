@@ -82,10 +82,12 @@ _SIGS = {
     "atx_dwconv_bwd_weight_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_dwconv_bwd_weight": (c_int, [c_vp, c_vp, c_int, ConvGeom, c_int, c_vp, c_vp, c_vp,
                                       c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
-    "atx_conv_bwd_data_workspace_bytes": (c_ll, [ConvGeom]),
+    "atx_conv_bwd_data_workspace_bytes": (c_ll, [ConvGeom, c_int]),
     "atx_conv_bwd_data": (c_int, [c_vp, c_vp, c_vp, ConvGeom, c_int, c_vp, c_vp, c_vp, c_vp,
                                   c_vp, c_vp, c_vp]),
     "atx_conv_bwd_weight_workspace_bytes": (c_ll, [c_int, c_int, c_ll]),
+    "atx_conv_bwd_weight_rows": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp,
+                                         c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_conv_bwd_weight": (c_int, [c_vp, c_vp, c_int, ConvGeom, c_int, c_int, c_vp, c_vp,
                                     c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_custom_grad_dx": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int,

@@ -24,7 +24,8 @@ __all__ = [
     "bgemm_lre_backward_claude", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
     "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "fakequant_per_tensor",
     "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
-    "conv_backward_data", "conv_backward_weight", "col2im", "gemm_fake_int8_claude",
+    "conv_backward_data", "conv_backward_weight", "conv_backward_weight_rows", "col2im",
+    "gemm_fake_int8_claude",
     "gemm_fake_int8_claude_save", "gemm_fake_int8_claude_cfg", "gemm_fake_uint8_claude",
     "gemm_fake_uint8_claude_save", "gemm_fake_uint8_claude_cfg", "dwconv_fake_int8_claude",
     "dwconv_forward", "dwconv_backward_data", "dwconv_backward_weight", "parse_text_table",
@@ -365,7 +366,7 @@ def conv_geom(x_shape, kernel_size, stride, padding, dilation):
 
 def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                  pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
-                 pad_dev=None, packed_w=None):
+                 pad_dev=None, packed_w=None, return_operand=False):
     """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
 
     img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
@@ -373,7 +374,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     quantized values or uint8 indices.  Out-of-image taps use pad_index, or
     the device scalar pad_dev when given.  packed_w = (wq, wt, Opad) from the
     fused weight fake-quant skips the weight packing.  Returns (y, wq), wq the
-    uint8 weight index image."""
+    uint8 weight index image; with return_operand, (y, wq, (xt, Rpad)), the
+    row-offset operand for conv_backward_weight_rows."""
     imgc = img.contiguous()
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -392,6 +394,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
     _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
+    if return_operand:
+        return y, wq, (xt, Rpad)
     return y, wq
 
 
@@ -403,7 +407,7 @@ def conv_backward_data(go: Tensor, wq: Tensor, table: Tensor, g, mask=None, scal
     goc = go.contiguous()
     O = wq.size(0)
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
-    wsb = L.query("atx_conv_bwd_data_workspace_bytes", g)
+    wsb = L.query("atx_conv_bwd_data_workspace_bytes", g, O)
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device) if wsb else None
     L.call("atx_conv_bwd_data", L.ptr(goc), L.ptr(wq.contiguous()), L.ptr(table), g, O,
            L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask), L.ptr(scale), L.ptr(img), L.ptr(ws),
@@ -493,6 +497,23 @@ def dwconv_backward_weight(go: Tensor, img: Tensor, table: Tensor, g, pad_index:
     L.call("atx_dwconv_bwd_weight", L.ptr(goc), L.ptr(imgc), _dtype_code(imgc, unsigned), g,
            pad_index, L.ptr(pad_dev), L.ptr(table), L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask_w),
            L.ptr(scale_w), L.ptr(gw), L.ptr(ws), L.stream_of(goc))
+    return gw
+
+
+def conv_backward_weight_rows(go: Tensor, operand, table: Tensor, g, O: int, mask_w=None,
+                              scale_w=None, go_sx=None, go_sw=None):
+    """conv_backward_weight with the activation indices read from the
+    forward's row-offset operand `operand` = (xt, Rpad) of conv_forward."""
+    xt, Rpad = operand
+    goc = go.contiguous()
+    K = g.C * g.KH * g.KW
+    Lc = g.OH * g.OW
+    gw = torch.empty((O, K), dtype=torch.float32, device=goc.device)
+    wsb = L.query("atx_conv_bwd_weight_workspace_bytes", O, K, g.N * Lc)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
+    L.call("atx_conv_bwd_weight_rows", L.ptr(goc), L.ptr(xt), Rpad, g.N, K, Lc, O, L.ptr(table),
+           L.ptr(go_sx), L.ptr(go_sw), L.ptr(mask_w), L.ptr(scale_w), L.ptr(gw), L.ptr(ws),
+           L.stream_of(goc))
     return gw
 
 

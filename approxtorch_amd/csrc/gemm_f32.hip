@@ -335,6 +335,61 @@ template <int B, typename T> struct WeightB {
   }
 };
 
+// Backward-weight B from the forward's row-offset operand: B(p = r, j = k) =
+// tw[xt[slot(k, r)][r] >> 8] (xt as the LUT GEMM reads it: [Kpad][Rpad]
+// uint16, slot(k, r) = (k & ~3) | ((k - (r >> 2)) & 3), padding taps and
+// rows hold offset 0).  A thread's four rows are one quad and the quad index
+// moves by BK / 4 = 8 per k-tile, so each of its taps stays in one slot: one
+// 8-byte load per (tap, k-tile) and a bit-field extract per element.
+template <int B> struct WeightBRows {
+  using Lay = PMajor<B>;
+  static constexpr int NQ = B / 32;
+  const uint16_t* xt; long long Rpad; int K, Kpad;
+  int pq, jr;
+  const uint16_t* src[NQ];          // slot row of tap i, at the thread's current quad
+  unsigned kv;                      // bit i: tap i < K
+  uint2 raw[NQ];
+  unsigned ok;                      // bit e: row p0 + pq + e valid
+  __device__ void init(int t, int n0, int pb) {
+    pq = (t & 7) * 4; jr = t >> 3;
+    kv = 0;
+    const int r0 = pb + pq;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int k = n0 + jr + 32 * i;
+      const int slot = k < Kpad ? ((k & ~3) | ((k - (r0 >> 2)) & 3)) : 0;
+      src[i] = xt + (long long)slot * Rpad + r0;
+      if (k < K) kv |= 1u << i;
+    }
+  }
+  __device__ void fetch(int p0, int pe) {
+    const int r = p0 + pq;
+    ok = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ok |= (r + e < pe ? 1u : 0u) << e;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) raw[i] = *(const uint2*)src[i];
+  }
+  __device__ void stash(float* s, const float* tab) const {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const unsigned w[2] = {raw[i].x, raw[i].y};
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned idx = (w[e >> 1] >> (16 * (e & 1) + 8)) & 255u;
+        const float x = tab[idx];
+        v[e] = (((kv >> i) & (ok >> e)) & 1u) ? x : 0.0f;
+      }
+      *(floatx4*)&s[Lay::at(jr + 32 * i, pq)] = v;
+    }
+  }
+  __device__ void advance() {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) src[i] += BK;
+  }
+};
+
 // ------------------------------------------------------------------ epilogues
 // out[n][k][l] of the backward-data GEMM (rows m = k, columns c = n*L + l).
 // With `mask`, the fake-quant STE is applied on the way out:
@@ -343,6 +398,7 @@ template <int B, typename T> struct WeightB {
 struct DataOut {
   float* col; int K, L, NL;
   const uint8_t* mask; const float* scale;
+  long long split_stride;   // elements per partial slice (blockIdx.z = slice)
 };
 // ws[s][o][k] of the backward-weight GEMM.
 struct WeightOut {
@@ -417,7 +473,7 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
 template <int BM, int BN, bool VA, bool VB, bool SC>
 __global__ void __launch_bounds__(GT, 2)
 data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
-                 const float* __restrict__ tx, int O) {
+                 const float* __restrict__ tx, int O, int o_chunk) {
   __shared__ float tab[256];
   __shared__ __align__(16) float As[2][KMajor<BM>::SIZE];
   __shared__ __align__(16) float Bs[2][KMajor<BN>::SIZE];
@@ -427,8 +483,12 @@ data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
   la.init(t, m0);
   lb.init(t, n0);
   __syncthreads();
+  // contraction slice of this block (grid.z splits O; each slice writes its
+  // own partial output, summed afterwards in a fixed order)
+  const int ob = blockIdx.z * o_chunk, oe = min(O, ob + o_chunk);
+  ep.col += (long long)blockIdx.z * ep.split_stride;
   floatx4 acc[BM / 32][BN / 32];
-  gemm_tiles<BM, BN>(la, lb, tab, 0, O, acc, As[0], As[1], Bs[0], Bs[1]);
+  gemm_tiles<BM, BN>(la, lb, tab, ob, oe, acc, As[0], As[1], Bs[0], Bs[1]);
   const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   constexpr int TM = BM / 32;
 #pragma unroll
@@ -469,9 +529,15 @@ data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
   }
 }
 
-template <int BM, int BN, bool VA, typename T>
+template <class LB> __device__ __forceinline__ void set_pad(LB&, const float*) {}
+template <int B, typename T>
+__device__ __forceinline__ void set_pad(WeightB<B, T>& lb, const float* pad_dev) {
+  if (pad_dev) lb.pad = (int)quant_index(pad_dev[0], 0);
+}
+
+template <int BM, int BN, bool VA, class LB>
 __global__ void __launch_bounds__(GT, 2)
-weight_gemm_kernel(WeightA<BM, VA> la, WeightB<BN, T> lb, WeightOut ep,
+weight_gemm_kernel(WeightA<BM, VA> la, LB lb, WeightOut ep,
                    const float* __restrict__ tw, const float* __restrict__ pad_dev,
                    int P, int p_chunk) {
   __shared__ float tab[256];
@@ -479,7 +545,7 @@ weight_gemm_kernel(WeightA<BM, VA> la, WeightB<BN, T> lb, WeightOut ep,
   __shared__ __align__(16) float Bs[2][PMajor<BN>::SIZE];
   const int t = threadIdx.x;
   tab[t] = tw[t];
-  if (pad_dev) lb.pad = (int)quant_index(pad_dev[0], 0);
+  set_pad(lb, pad_dev);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int s = blockIdx.z;
   const int pb = s * p_chunk, pe = min(P, pb + p_chunk);
@@ -552,7 +618,19 @@ struct DataArgs {
   const float* go; const uint8_t* wq; const float* tx; int N, O, K, L;
   const float* sx; const float* sw;          // optional go scale sx * sw[o]
   float* out; const uint8_t* mask; const float* scale;
+  int splits, o_chunk;                       // contraction split (1 = none)
+  float* partials;                           // [splits][N*K*L] when splits > 1
 };
+
+// Split of the backward-data contraction: when the output tiles leave more
+// than half of the CUs idle and O is long enough for several 4-k-tile
+// slices, O is split into deterministic partial slices (measured on c4
+// shapes: with 200-400 blocks the partial traffic costs more than it wins).
+static int data_splits(int N, int O, int K, int L) {
+  const long long blocks = cdiv((long long)N * L, 128) * cdiv(K, tile_of(K));
+  if (blocks >= 128 || O < 256 || (long long)N * K * L > 0x7fffffffLL) return 1;
+  return (int)std::max<long long>(1, std::min<long long>(cdiv(1024, blocks), O / 128));
+}
 
 template <int BM, bool VA, bool VB, bool SC>
 static void launch_data(const DataArgs& a, hipStream_t stream) {
@@ -562,10 +640,12 @@ static void launch_data(const DataArgs& a, hipStream_t stream) {
   la.wq = a.wq; la.K = a.K;
   DataB<BN, VB, SC> lb{};
   lb.go = a.go; lb.O = a.O; lb.L = a.L; lb.NL = NL; lb.sx = a.sx; lb.sw = a.sw;
-  DataOut ep{a.out, a.K, a.L, NL, a.mask, a.scale};
-  dim3 grid((unsigned)cdiv(NL, BN), (unsigned)cdiv(a.K, BM), 1);
+  const bool split = a.splits > 1;
+  DataOut ep{split ? a.partials : a.out, a.K, a.L, NL, split ? nullptr : a.mask,
+             split ? nullptr : a.scale, (long long)NL * a.K};
+  dim3 grid((unsigned)cdiv(NL, BN), (unsigned)cdiv(a.K, BM), (unsigned)a.splits);
   hipLaunchKernelGGL((data_gemm_kernel<BM, BN, VA, VB, SC>), grid, dim3(GT), 0, stream, la, lb,
-                     ep, a.tx, a.O);
+                     ep, a.tx, a.O, a.o_chunk);
 }
 
 template <int BM, bool SC>
@@ -578,14 +658,25 @@ static void dispatch_data_vec(const DataArgs& a, hipStream_t stream) {
   else launch_data<BM, false, false, SC>(a, stream);
 }
 
-static int run_data_gemm(const DataArgs& a, hipStream_t stream) {
+// Runs the backward-data GEMM into a.out; with a.splits > 1 the partial
+// slices go to a.partials and are summed into a.out (with the optional
+// per-tensor STE mask) by split_sum_kernel.
+static int run_data_gemm(DataArgs a, hipStream_t stream) {
+  if (a.splits < 1) a.splits = 1;
+  a.o_chunk = (int)(cdiv(cdiv(a.O, a.splits), BK) * BK);
+  a.splits = (int)cdiv(a.O, a.o_chunk);
   const bool sc = a.sw != nullptr;
   if (tile_of(a.K) == 64) {
     if (sc) dispatch_data_vec<64, true>(a, stream); else dispatch_data_vec<64, false>(a, stream);
   } else {
     if (sc) dispatch_data_vec<128, true>(a, stream); else dispatch_data_vec<128, false>(a, stream);
   }
-  return check_launch("data_gemm_kernel");
+  int rc = check_launch("data_gemm_kernel");
+  if (rc || a.splits == 1) return rc;
+  const long long numel = (long long)a.N * a.K * a.L;
+  // split_sum's per-channel scale index i / K: K = numel makes it per tensor
+  return launch_split_sum(a.partials, a.splits, numel, (int)numel, a.mask, a.scale, a.out,
+                          stream);
 }
 
 template <int BM, int BN, bool VA, typename T>
@@ -599,8 +690,8 @@ static void launch_weight(const float* go, const T* img, atx_conv_geom g, int O,
   lb.img = img; lb.g = g; lb.K = K; lb.L = L; lb.offset = offset; lb.pad = pad_index;
   WeightOut ep{ws, O, K, (long long)O * K};
   dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)S);
-  hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, T>), grid, dim3(GT), 0, stream, la, lb, ep,
-                     tw, pad_dev, P, chunk);
+  hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, WeightB<BN, T>>), grid, dim3(GT), 0,
+                     stream, la, lb, ep, tw, pad_dev, P, chunk);
 }
 
 template <bool VA, typename T>
@@ -632,6 +723,36 @@ static void dispatch_weight(const float* go, const T* img, atx_conv_geom g, int 
                                     pad_dev, tw, go_sx, go_sw, ws, stream);
 }
 
+template <int BM, int BN, bool VA>
+static void launch_weight_rows(const float* go, const uint16_t* xt, long long Rpad, int O,
+                               int K, int L, int P, int chunk, int S, const float* tw,
+                               const float* go_sx, const float* go_sw, float* ws,
+                               hipStream_t stream) {
+  WeightA<BM, VA> la{};
+  la.go = go; la.O = O; la.L = L; la.sx = go_sx; la.sw = go_sw;
+  WeightBRows<BN> lb{};
+  lb.xt = xt; lb.Rpad = Rpad; lb.K = K; lb.Kpad = (K + 3) & ~3;
+  WeightOut ep{ws, O, K, (long long)O * K};
+  dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)S);
+  hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, WeightBRows<BN>>), grid, dim3(GT), 0,
+                     stream, la, lb, ep, tw, (const float*)nullptr, P, chunk);
+}
+
+template <bool VA>
+static void dispatch_weight_rows(const float* go, const uint16_t* xt, long long Rpad, int O,
+                                 int K, int L, int P, int chunk, int S, const float* tw,
+                                 const float* go_sx, const float* go_sw, float* ws,
+                                 hipStream_t stream) {
+  const int bm = tile_of(O), bn = tile_of(K);
+#define ATX_LWR(M_, N_) \
+  launch_weight_rows<M_, N_, VA>(go, xt, Rpad, O, K, L, P, chunk, S, tw, go_sx, go_sw, ws, stream)
+  if (bm == 64 && bn == 64) ATX_LWR(64, 64);
+  else if (bm == 64) ATX_LWR(64, 128);
+  else if (bn == 64) ATX_LWR(128, 64);
+  else ATX_LWR(128, 128);
+#undef ATX_LWR
+}
+
 }  // namespace atx
 
 using namespace atx;
@@ -650,7 +771,8 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx, i
   ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data_col: null pointer");
   ATX_REQUIRE((long long)N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
               "atx_conv_bwd_data_col: sizes too large");
-  const DataArgs a{go, wq, tx, N, O, K, L, nullptr, nullptr, col, nullptr, nullptr};
+  const DataArgs a{go, wq, tx, N, O, K, L, nullptr, nullptr, col, nullptr, nullptr, 1, 0,
+                   nullptr};
   return run_data_gemm(a, stream);
 }
 
@@ -659,9 +781,13 @@ static bool direct_columns(const atx_conv_geom& g) {
   return g.KH == 1 && g.KW == 1 && g.SH == 1 && g.SW == 1 && g.PH == 0 && g.PW == 0;
 }
 
-long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g) {
-  if (direct_columns(g)) return 0;
-  return (long long)g.N * g.C * g.KH * g.KW * g.OH * g.OW * 4;
+// Workspace of atx_conv_bwd_data: [split partials][col (unless direct)].
+long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g, int O) {
+  const int K = g.C * g.KH * g.KW, L = g.OH * g.OW;
+  if (g.N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
+  const long long numel = (long long)g.N * K * L;
+  const int S = data_splits(g.N, O, K, L);
+  return ((S > 1 ? S : 0) + (direct_columns(g) ? 0 : 1)) * numel * 4;
 }
 
 int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_conv_geom g,
@@ -677,31 +803,36 @@ int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_c
   ATX_REQUIRE(gx, "atx_conv_bwd_data: null output");
   const int K = g.C * g.KH * g.KW;
   const int L = g.OH * g.OW;
+  const long long numel = (long long)g.N * K * L;
+  const int S = (O > 0 && numel > 0) ? data_splits(g.N, O, K, L) : 1;
+  float* partials = S > 1 ? workspace : nullptr;
+  float* col = workspace ? workspace + (S > 1 ? S * numel : 0) : nullptr;
+  ATX_REQUIRE(S == 1 || workspace, "atx_conv_bwd_data: null workspace");
   if (direct_columns(g)) {
     if (O == 0 || L == 0)
       return launch_split_sum(nullptr, 0, img, 1, nullptr, nullptr, gx, stream);
     ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
     ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
                 "atx_conv_bwd_data: sizes too large");
-    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, gx, mask, scale};
+    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, gx, mask, scale, S, 0, partials};
     return run_data_gemm(a, stream);
   }
   ATX_REQUIRE(workspace, "atx_conv_bwd_data: null workspace");
   if ((long long)K * L == 0 || O == 0) {
-    const long long n = (long long)g.N * K * L;
-    if (n) {
-      int rc = launch_split_sum(nullptr, 0, n, 1, nullptr, nullptr, workspace, stream);
+    if (numel) {
+      int rc = launch_split_sum(nullptr, 0, numel, 1, nullptr, nullptr, col, stream);
       if (rc) return rc;
     }
   } else {
     ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
     ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
                 "atx_conv_bwd_data: sizes too large");
-    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, workspace, nullptr, nullptr};
+    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, col, nullptr, nullptr, S, 0,
+                     partials};
     int rc = run_data_gemm(a, stream);
     if (rc) return rc;
   }
-  return atx_col2im(workspace, g, mask, scale, gx, stream);
+  return atx_col2im(col, g, mask, scale, gx, stream);
 }
 
 long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P) {
@@ -745,6 +876,37 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_ge
     dispatch_weight<float>(go, (const float*)img, g, O, K, L, (int)P, chunk, Sreal,
                            f32_offset, pad_index, pad_dev, tw, go_sx, go_sw, workspace, stream);
   int rc = check_launch("weight_gemm_kernel");
+  if (rc) return rc;
+  return launch_split_sum(workspace, Sreal, (long long)O * K, K, mask_w, scale_w, gw, stream);
+}
+
+int atx_conv_bwd_weight_rows(const float* go, const uint16_t* xt, int Rpad, int N, int K,
+                             int L, int O, const float* tw, const float* go_sx,
+                             const float* go_sw, const uint8_t* mask_w, const float* scale_w,
+                             float* gw, float* workspace, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_conv_bwd_weight_rows: negative size");
+  ATX_REQUIRE((go_sx == nullptr) == (go_sw == nullptr),
+              "atx_conv_bwd_weight_rows: go_sx and go_sw come together");
+  const long long P = (long long)N * L;
+  ATX_REQUIRE(P < 0x7fffffffLL, "atx_conv_bwd_weight_rows: N*L too large");
+  ATX_REQUIRE(Rpad >= P && Rpad % ATX_ROW_TILE == 0, "atx_conv_bwd_weight_rows: bad Rpad %d",
+              Rpad);
+  if ((long long)O * K == 0) return ATX_OK;
+  ATX_REQUIRE(gw && tw && (!mask_w || scale_w), "atx_conv_bwd_weight_rows: null pointer");
+  if (P == 0)
+    return launch_split_sum(nullptr, 0, (long long)O * K, K, nullptr, scale_w, gw, stream);
+  ATX_REQUIRE(go && xt && workspace, "atx_conv_bwd_weight_rows: null operand/workspace");
+  ATX_REQUIRE(cdiv(O, 64) <= 65535, "atx_conv_bwd_weight_rows: too many output channels");
+  const int S = weight_splits(O, K, P);
+  const int chunk = (int)(cdiv(cdiv(P, S), BK) * BK);
+  const int Sreal = (int)cdiv(P, chunk);
+  if (L % 4 == 0 && (uintptr_t)go % 16 == 0)
+    dispatch_weight_rows<true>(go, xt, Rpad, O, K, L, (int)P, chunk, Sreal, tw, go_sx, go_sw,
+                               workspace, stream);
+  else
+    dispatch_weight_rows<false>(go, xt, Rpad, O, K, L, (int)P, chunk, Sreal, tw, go_sx, go_sw,
+                                workspace, stream);
+  int rc = check_launch("weight_gemm_kernel<rows>");
   if (rc) return rc;
   return launch_split_sum(workspace, Sreal, (long long)O * K, K, mask_w, scale_w, gw, stream);
 }

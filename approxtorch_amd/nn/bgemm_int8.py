@@ -237,10 +237,15 @@ class _conv2d_int8_fused(Function):
         if depthwise:
             y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
                                    sx=scale_x, sw=scale_w, bias=b)
+            saved_x, ctx.rpad = xq8, None
         else:
-            y, _ = ops.conv_forward(xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
-                                    sx=scale_x, sw=scale_w, bias=b, packed_w=(wq, wt, Opad))
-        ctx.save_for_backward(xq8, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
+            # the row-offset operand is kept for the weight gradient: its
+            # indices feed the backward GEMM with no im2col in the loop
+            y, _, (xt, Rpad) = ops.conv_forward(
+                xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
+                sw=scale_w, bias=b, packed_w=(wq, wt, Opad), return_operand=True)
+            saved_x, ctx.rpad = xt, Rpad
+        ctx.save_for_backward(saved_x, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
                               tx.contiguous(), tw.contiguous())
         ctx.g, ctx.has_bias, ctx.wshape = g, bias is not None, weight.shape
         ctx.depthwise = depthwise
@@ -248,16 +253,25 @@ class _conv2d_int8_fused(Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        xq8, mask_x, wq, mask_w, sx, sw, tx, tw = ctx.saved_tensors
+        saved_x, mask_x, wq, mask_w, sx, sw, tx, tw = ctx.saved_tensors
         g = ctx.g
         go = grad_output.contiguous()
         gx = gw = gb = None
-        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-            gx, gw = _lut_conv_backward(go, xq8, wq, tx, tw, g, ctx.depthwise, mask=mask_x,
-                                        scale=sx, mask_w=mask_w, scale_w=sw, go_sx=sx,
-                                        go_sw=sw)
-            gx = gx if ctx.needs_input_grad[0] else None
-            gw = gw.view(ctx.wshape) if ctx.needs_input_grad[1] else None
+        if ctx.depthwise:
+            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+                gx, gw = _lut_conv_backward(go, saved_x, wq, tx, tw, g, True, mask=mask_x,
+                                            scale=sx, mask_w=mask_w, scale_w=sw, go_sx=sx,
+                                            go_sw=sw)
+                gx = gx if ctx.needs_input_grad[0] else None
+                gw = gw.view(ctx.wshape) if ctx.needs_input_grad[1] else None
+        else:
+            if ctx.needs_input_grad[0]:
+                gx = ops.conv_backward_data(go, wq, tx, g, mask=mask_x, scale=sx, go_sx=sx,
+                                            go_sw=sw)
+            if ctx.needs_input_grad[1]:
+                gw = ops.conv_backward_weight_rows(go, (saved_x, ctx.rpad), tw, g, wq.size(0),
+                                                   mask_w=mask_w, scale_w=sw, go_sx=sx,
+                                                   go_sw=sw).view(ctx.wshape)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
         return gx, gw, gb, None, None, None, None, None, None, None, None, None

@@ -259,17 +259,29 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx,
 /* Image gradient of the conv: col as above (with the go scale), folded into
  * gx [N,C,H,W] with the per-tensor fake-quant STE fused when mask != NULL:
  * gx = (mask ? g : 0) / max(scale[0], 1e-12).  A 1x1 stride-1 unpadded conv
- * writes gx straight from the GEMM (no workspace); otherwise the workspace
- * holds col (atx_conv_bwd_data_workspace_bytes).  Replaces the same calls
+ * writes gx straight from the GEMM; otherwise the workspace holds col.  When
+ * the output tiles cannot fill the GPU the contraction over O is split into
+ * partial slices (in the workspace) summed in a fixed order.  Size:
+ * atx_conv_bwd_data_workspace_bytes(g, O).  Replaces the same calls
  * plus the fold and the fake-quant backward (nn/bgemm_int8.py:116-118,
  * csrc/claude/quantization.cu:223-258). */
-long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g);
+long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g, int O);
 int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx,
                       atx_conv_geom g, int O, const float* go_sx,
                       const float* go_sw, const uint8_t* mask,
                       const float* scale, float* gx, float* workspace,
                       hipStream_t stream);
 long long atx_conv_bwd_weight_workspace_bytes(int O, int K, long long P);
+/* atx_conv_bwd_weight with xi read from the forward's row-offset operand
+ * xt [Kpad][Rpad] (as atx_im2col_rows / atx_pack_x_* wrote it; index =
+ * entry >> 8, padding taps already hold the pad index): no implicit im2col
+ * in the loop.  Rows r = n*L + l, P = N*L; same workspace as
+ * atx_conv_bwd_weight. */
+int atx_conv_bwd_weight_rows(const float* go, const uint16_t* xt, int Rpad,
+                             int N, int K, int L, int O, const float* tw,
+                             const float* go_sx, const float* go_sw,
+                             const uint8_t* mask_w, const float* scale_w,
+                             float* gw, float* workspace, hipStream_t stream);
 int atx_conv_bwd_weight(const float* go, const void* img, int dtype,
                         atx_conv_geom g, int O, int pad_index,
                         const float* pad_dev, const float* tw,

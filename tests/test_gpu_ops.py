@@ -419,20 +419,23 @@ def test_conv_backward_kernels_tiled(case):
     close(gwk.cpu().numpy(), ew, aw)
 
 
-@pytest.mark.parametrize("geom", [GEOMS[0], ((1, 1), (1, 1), (0, 0), (1, 1)), GEOMS[2]])
-def test_conv_backward_fused_scale_and_masks(geom):
+@pytest.mark.parametrize("geom,shape,Oc", [
+    (GEOMS[0], (3, 40, 11, 12), 72), (((1, 1), (1, 1), (0, 0), (1, 1)), (3, 40, 11, 12), 72),
+    (GEOMS[2], (3, 40, 11, 12), 72),
+    # few output tiles and a long contraction: split into partial slices
+    (((1, 1), (1, 1), (0, 0), (1, 1)), (2, 96, 7, 7), 512), (GEOMS[0], (2, 32, 7, 7), 520)])
+def test_conv_backward_fused_scale_and_masks(geom, shape, Oc):
     """The fused layer backward: go * fp32(sx * sw[o]) in the operand loads,
     the x fake-quant STE (mask ? g : 0) / max(sx, 1e-12) on the image gradient
     (fold, or the GEMM epilogue of the 1x1 stride-1 conv), the per-channel W
     STE in the split-K sum."""
     k, s, p, d = geom
-    r = gen(zlib.crc32(repr(geom).encode()) + 7)
-    img = r.integers(-127, 128, (3, 40, 11, 12)).astype(np.int8)
-    Oc = 72
-    K = 40 * k[0] * k[1]
+    r = gen(zlib.crc32(repr((geom, shape, Oc)).encode()) + 7)
+    img = r.integers(-127, 128, shape).astype(np.int8)
+    K = shape[1] * k[0] * k[1]
     wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
     g = ops.conv_geom(img.shape, k, s, p, d)
-    go = r.standard_normal((3, Oc, g.OH * g.OW)).astype(np.float32)
+    go = r.standard_normal((shape[0], Oc, g.OH * g.OW)).astype(np.float32)
     tx = r.standard_normal(256).astype(np.float32)
     tw = r.standard_normal(256).astype(np.float32)
     sx = np.array([0.0213], np.float32)
@@ -542,3 +545,32 @@ def test_dwconv_backward_kernels(geom):
         close(gi[:, c:c + 1], np.where(mask_x[:, c:c + 1], fx, 0.0) / float(sx[0]),
               fa / float(sx[0]))
         close(gwk[c:c + 1], np.where(mask_w[c:c + 1], ew, 0.0) / float(sw[c]), aw / float(sw[c]))
+
+
+@pytest.mark.parametrize("case", BWD_TILED)
+def test_conv_backward_weight_rows_equals_image_path(case):
+    """The weight gradient from the forward's row-offset operand is the
+    image-path result bit for bit (same tiles, same summation order)."""
+    shape, (k, s, p, d), Oc, dtype = case
+    r = gen(zlib.crc32(repr(case).encode()) + 11)
+    if dtype == "int8":
+        img = r.integers(-128, 128, shape).astype(np.int8)
+        offset, pad = 128, 128
+    elif dtype == "uint8":
+        img = r.integers(0, 256, shape).astype(np.uint8)
+        offset, pad = 0, 7
+    else:
+        img = r.integers(-130, 130, shape).astype(np.float32)
+        offset, pad = 128, 128
+    K = shape[1] * k[0] * k[1]
+    w = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    lut = t(luts(2)["perturbed"], torch.float32)
+    _, _, operand = ops.conv_forward(t(img), t(w), lut, g, offset, pad, return_operand=True)
+    go = t(r.standard_normal((shape[0], Oc, g.OH * g.OW)).astype(np.float32))
+    tw = t(r.standard_normal(256).astype(np.float32))
+    sx = t(np.array([0.02], np.float32))
+    sw = t(r.uniform(1e-3, 4e-2, Oc).astype(np.float32))
+    a = ops.conv_backward_weight(go, t(img), tw, g, Oc, pad, go_sx=sx, go_sw=sw)
+    b = ops.conv_backward_weight_rows(go, operand, tw, g, Oc, go_sx=sx, go_sw=sw)
+    assert torch.equal(a, b)
