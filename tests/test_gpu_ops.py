@@ -423,7 +423,13 @@ def test_conv_backward_kernels_tiled(case):
     (GEOMS[0], (3, 40, 11, 12), 72), (((1, 1), (1, 1), (0, 0), (1, 1)), (3, 40, 11, 12), 72),
     (GEOMS[2], (3, 40, 11, 12), 72),
     # few output tiles and a long contraction: split into partial slices
-    (((1, 1), (1, 1), (0, 0), (1, 1)), (2, 96, 7, 7), 512), (GEOMS[0], (2, 32, 7, 7), 520)])
+    (((1, 1), (1, 1), (0, 0), (1, 1)), (2, 96, 7, 7), 512), (GEOMS[0], (2, 32, 7, 7), 520),
+    # stride 1 with O % 32 == 0 but few image tiles: col path
+    (GEOMS[0], (3, 40, 11, 12), 64), (((5, 5), (1, 1), (0, 0), (1, 1)), (1, 8, 12, 9), 256),
+    # stride 1, O % 32 == 0 and >= 512 image tiles: implicit backward-data GEMM
+    (GEOMS[0], (2, 8, 128, 256), 32), (((3, 3), (1, 1), (2, 2), (2, 2)), (1, 8, 256, 257), 96),
+    (((3, 1), (1, 1), (1, 0), (1, 1)), (1, 130, 256, 129), 32),
+    (((5, 5), (1, 1), (0, 0), (1, 1)), (4, 4, 132, 131), 64)])
 def test_conv_backward_fused_scale_and_masks(geom, shape, Oc):
     """The fused layer backward: go * fp32(sx * sw[o]) in the operand loads,
     the x fake-quant STE (mask ? g : 0) / max(sx, 1e-12) on the image gradient
