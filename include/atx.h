@@ -259,7 +259,9 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx,
 /* Image gradient of the conv: col as above (with the go scale), folded into
  * gx [N,C,H,W] with the per-tensor fake-quant STE fused when mask != NULL:
  * gx = (mask ? g : 0) / max(scale[0], 1e-12).  A 1x1 stride-1 unpadded conv
- * writes gx straight from the GEMM; otherwise the workspace holds col.  When
+ * writes gx straight from the GEMM, and so does a stride-1 conv with
+ * O % 32 == 0 whose C x N*H*W output fills >= 512 tiles (implicit GEMM over
+ * (tap, o), workspace size 0); otherwise the workspace holds col.  When
  * the output tiles cannot fill the GPU the contraction over O is split into
  * partial slices (in the workspace) summed in a fixed order.  Size:
  * atx_conv_bwd_data_workspace_bytes(g, O).  Replaces the same calls
