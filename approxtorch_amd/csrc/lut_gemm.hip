@@ -50,6 +50,8 @@
 #include "atx_internal.h"
 
 #include <algorithm>
+#include <stdlib.h>
+#include <string.h>
 #include <type_traits>
 
 namespace atx {
@@ -88,6 +90,14 @@ struct GemmParams {
   void* y;
   long long split_stride;       // elements per partial slice
   const float* sx; const float* sw; const float* bias;
+  // Stream-K schedule (sk_per > 0) of G workgroups: workgroup w first runs
+  // the whole tiles w, w + G, ... below sk_dp (sk_dp = G * full rounds),
+  // then quads [w * sk_per, (w + 1) * sk_per) of the tile-major (tile, quad)
+  // space of the remaining tiles, nqt quads per tile; a remaining tile cut by
+  // a workgroup boundary adds its int32 sums into slot
+  // floor(tail tile * nqt / sk_per) of skws.
+  int sk_per, nqt, sk_dp, sk_g;
+  int* skws;
 };
 
 // ------------------------------------------------------------------ prepare
@@ -432,24 +442,14 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, void* y,
   }
 }
 
+// Sums of one tile segment: rows tile tr, channels tile to, k in [kb, ke).
 template <bool SIGNED>
-__global__ void __launch_bounds__(NT, 1)
-lut_gemm_kernel(const GemmParams p) {
-  __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
-
+__device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* smem, int tr,
+                                         int to, int kb, int ke, int (&acc)[RPL][8]) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int rg = lane / CG, g = lane % CG;
-
-  int lb = logical_block();
-  const int to = lb % p.tiles_o; lb /= p.tiles_o;
-  const int tr = lb % p.tiles_r;
-  const int s = lb / p.tiles_r;
-
   const int o0 = to * OT;
-  const int r0 = tr * RT + wave * RPW + rg * RQ;         // this lane's first quad
-  const int kb = s * p.k_chunk;
-  const int ke = min(p.K, kb + p.k_chunk);
 
   // Table build: wave w writes channel group og = w % 4 for rows
   // 128 hw .. 128 hw + 127 (hw = w / 4); lane t the row pair v0 = 128 hw + 2t,
@@ -473,7 +473,6 @@ lut_gemm_kernel(const GemmParams p) {
   // which builds an all-zero table for the steps past the chunk's end.
   const __amdgpu_buffer_rsrc_t lutz = buffer_rsrc(p.lut16t, 0);
 
-  int acc[RPL][8];
 #pragma unroll
   for (int j = 0; j < RPL; ++j)
 #pragma unroll
@@ -560,17 +559,131 @@ lut_gemm_kernel(const GemmParams p) {
       sub(I1{}, I3{}, j + 1, xb, xa);
     }
   }
+}
 
-  // ---- epilogue: registers -> HBM, every wave at once (no LDS staging).
-  const int oc = o0 + g * 8;
-  if (p.splits > 1)
-    store_tile<ATX_OUT_I32>(p, (int*)p.y + (long long)s * p.split_stride, acc, r0, oc);
-  else if (p.out_kind == ATX_OUT_I32)
-    store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
-  else if (p.out_kind == ATX_OUT_F32)
-    store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
-  else
-    store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
+// Slot layout of a cut tile (stream-K): value (h, m, e) of thread tid at
+// ((RQ * h + m) * 8 + e) * NT + tid, so each atomic of a wave covers 256
+// contiguous bytes.
+__device__ __forceinline__ long long sk_index(int j, int e, int tid) {
+  return (long long)(j * 8 + e) * NT + tid;
+}
+
+// Slot of stream-K boundary b (quad position (b + 1) * per), or -1 when that
+// boundary does not open a cut tile: the tile containing it must start at or
+// after boundary b's predecessor (its first boundary is this one).
+// Returns the tail tile index (0-based among the remaining tiles).
+__device__ __forceinline__ int sk_slot_tile(const GemmParams& p, int b, long long total) {
+  const long long B = (long long)(b + 1) * p.sk_per;
+  if (B >= total || B % p.nqt == 0) return -1;
+  const long long t = B / p.nqt;
+  return (t * p.nqt) / p.sk_per == b ? (int)t : -1;
+}
+
+template <bool SIGNED>
+__global__ void __launch_bounds__(NT, 1)
+lut_gemm_kernel(const GemmParams p) {
+  __shared__ __align__(16) unsigned char smem[SMEM_BYTES];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / CG, g = lane % CG;
+  const int lb = logical_block();
+  int acc[RPL][8];
+
+  if (p.sk_per == 0) {
+    int l = lb;
+    const int to = l % p.tiles_o; l /= p.tiles_o;
+    const int tr = l % p.tiles_r;
+    const int s = l / p.tiles_r;
+    const int kb = s * p.k_chunk;
+    lut_tile<SIGNED>(p, smem, tr, to, kb, min(p.K, kb + p.k_chunk), acc);
+    // ---- epilogue: registers -> HBM, every wave at once (no LDS staging).
+    const int r0 = tr * RT + wave * RPW + rg * RQ;       // this lane's first quad
+    const int oc = to * OT + g * 8;
+    if (p.splits > 1)
+      store_tile<ATX_OUT_I32>(p, (int*)p.y + (long long)s * p.split_stride, acc, r0, oc);
+    else if (p.out_kind == ATX_OUT_I32)
+      store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
+    else if (p.out_kind == ATX_OUT_F32)
+      store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
+    else
+      store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
+    return;
+  }
+
+  // Whole tiles first (the full rounds), then this workgroup's run of the
+  // remaining tiles' quads, tile segment by tile segment.
+  for (int tile = lb; tile < p.sk_dp; tile += p.sk_g) {
+    const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
+    __syncthreads();                         // the previous segment's tables are read
+    lut_tile<SIGNED>(p, smem, tr, to, 0, p.K, acc);
+    const int r0 = tr * RT + wave * RPW + rg * RQ;
+    const int oc = to * OT + g * 8;
+    if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
+    else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
+    else store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
+  }
+  const long long total = ((long long)p.tiles_r * p.tiles_o - p.sk_dp) * p.nqt;
+  long long it = (long long)lb * p.sk_per;
+  const long long end = min(total, it + p.sk_per);
+  while (it < end) {
+    const int tt = (int)(it / p.nqt);        // tail tile
+    const int q0 = (int)(it - (long long)tt * p.nqt);
+    const int q1 = (int)min((long long)p.nqt, q0 + (end - it));
+    const int tile = p.sk_dp + tt;
+    const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
+    __syncthreads();                         // the previous segment's tables are read
+    lut_tile<SIGNED>(p, smem, tr, to, TPL * q0, min(p.K, TPL * q1), acc);
+    if (q0 == 0 && q1 == p.nqt) {
+      const int r0 = tr * RT + wave * RPW + rg * RQ;
+      const int oc = to * OT + g * 8;
+      if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
+      else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
+      else store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
+    } else {
+      int* slot = p.skws + (((long long)tt * p.nqt) / p.sk_per) * (long long)(RPL * 8 * NT);
+#pragma unroll
+      for (int j = 0; j < RPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          __hip_atomic_fetch_add(slot + sk_index(j, e, tid), acc[j][e], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+    it += q1 - q0;
+  }
+}
+
+// Zeroes the slots of the cut tiles (block b = slot b).
+__global__ void __launch_bounds__(NT)
+sk_clear_kernel(const GemmParams p) {
+  const long long total = ((long long)p.tiles_r * p.tiles_o - p.sk_dp) * p.nqt;
+  if (sk_slot_tile(p, blockIdx.x, total) < 0) return;
+  int* slot = p.skws + (long long)blockIdx.x * (RPL * 8 * NT);
+  for (int j = 0; j < RPL * 8; ++j) slot[(long long)j * NT + threadIdx.x] = 0;
+}
+
+// Epilogue of the cut tiles: each thread reloads the sums it would have held
+// and stores them as the main kernel does.
+__global__ void __launch_bounds__(NT)
+sk_finish_kernel(const GemmParams p) {
+  const long long total = ((long long)p.tiles_r * p.tiles_o - p.sk_dp) * p.nqt;
+  const int tt = sk_slot_tile(p, blockIdx.x, total);
+  if (tt < 0) return;
+  const int tile = p.sk_dp + tt;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / CG, g = lane % CG;
+  const int* slot = p.skws + (long long)blockIdx.x * (RPL * 8 * NT);
+  int acc[RPL][8];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = slot[sk_index(j, e, tid)];
+  const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
+  const int r0 = tr * RT + wave * RPW + rg * RQ;
+  const int oc = to * OT + g * 8;
+  if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
+  else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
+  else store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
 }
 
 // Split-K reduction: exact int64 sum of int32 partials, then the epilogue.
@@ -621,8 +734,9 @@ __global__ void lut_gemm_f32_kernel(const GemmParams p) {
   }
 }
 
-// Split plan shared by the workspace query and the launch.
-struct Plan { int tiles_r, tiles_o, splits, k_chunk; };
+// Split plan shared by the workspace query and the launch.  sk_per > 0
+// selects the stream-K schedule (PLAN_CUS workgroups, sk_per quads each).
+struct Plan { int tiles_r, tiles_o, splits, k_chunk, sk_per, nqt, sk_dp; };
 
 // Compute units of a full MI355X (one resident workgroup each: the kernel's
 // 8 waves hold 2 waves per SIMD at its register budget).  A constant, not a
@@ -637,11 +751,23 @@ constexpr int PLAN_CUS = 256;
 // k-chunks are whole quads of tables (multiples of 4); S is at least
 // ceil(K / kmax), the exact-int32 bound of one pass, and the smallest S among
 // equal costs wins.
+// Stream-K (K <= kmax): floor(tiles / CUs) full rounds of whole tiles, then
+// the T = tail tiles * ceil(K/4) quads of the rest dealt out evenly,
+// per = ceil(T / CUs) quads per workgroup, which ends the partial last
+// round.  Cost, fitted to the split-K / stream-K times of the 19 distinct
+// ResNet-50 layer shapes at batch 64 (~0.95 us per k-step):
+//   rounds * (K + 14) + 4 * per + 14 per tail segment a workgroup runs
+//   (ceil(per / nqt) + 1 at most; table prologue and atomic sums) + 0.1 per
+//   cut tile (its 256 KiB slot) + 45 for the clear / finish launches.
+// It is taken when cheaper than the best split-K plan.  ATX_LUT_SCHEDULE
+// (environment: auto | split | stream_k) overrides the choice.
 static Plan make_plan(int N, int K, int L, int O, int kmax) {
   Plan pl;
   const long long R = (long long)N * L;
   pl.tiles_r = (int)cdiv(R, RT);
   pl.tiles_o = (int)cdiv(O, OT);
+  pl.sk_per = 0;
+  pl.nqt = (int)cdiv(K, TPL);
   if (K <= 0) { pl.splits = 1; pl.k_chunk = 1; return pl; }
   const long long tiles = (long long)pl.tiles_r * pl.tiles_o;
   const long long cus = PLAN_CUS;
@@ -659,6 +785,24 @@ static Plan make_plan(int N, int K, int L, int O, int kmax) {
   }
   pl.k_chunk = (int)std::min<long long>(best_kc, kmax);
   pl.splits = (int)cdiv(K, pl.k_chunk);
+  pl.sk_dp = 0;
+  const char* sched = getenv("ATX_LUT_SCHEDULE");
+  const int force = !sched ? 0 : !strcmp(sched, "stream_k") ? 1 : !strcmp(sched, "split") ? -1 : 0;
+  if (K <= kmax && tiles % cus != 0 && force >= 0) {
+    const long long rounds = tiles / cus;
+    const long long tail = tiles - rounds * cus;
+    const long long T = tail * pl.nqt;
+    const long long per = cdiv(T, cus);
+    if (per >= 2) {
+      const long long cuts = std::min<long long>(tail, cdiv(T, per) - 1);
+      const double sk_cost = (double)rounds * (K + 14) + 4.0 * per +
+                             14.0 * (double)(cdiv(per, pl.nqt) + 1) + 0.1 * cuts + 45.0;
+      if (force > 0 || sk_cost < best_cost) {
+        pl.sk_per = (int)per;
+        pl.sk_dp = (int)(rounds * cus);
+      }
+    }
+  }
   return pl;
 }
 
@@ -772,6 +916,7 @@ int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc, 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O) {
   if (N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
   const Plan pl = make_plan(N, K, L, O, KMAX_U16);
+  if (pl.sk_per > 0) return (long long)(PLAN_CUS - 1) * RT * OT * 4;
   if (pl.splits <= 1) return 0;
   return (long long)pl.splits * N * O * L * 4;
 }
@@ -820,6 +965,29 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
   p.tiles_r = pl.tiles_r; p.tiles_o = pl.tiles_o;
   p.splits = pl.splits; p.k_chunk = pl.k_chunk;
   const long long numel = R * O;
+  if (pl.sk_per > 0) {
+    ATX_REQUIRE(workspace, "atx_lut_gemm: stream-K plan needs a workspace of %lld bytes",
+                (long long)(PLAN_CUS - 1) * RT * OT * 4);
+    p.sk_per = pl.sk_per; p.nqt = pl.nqt; p.skws = (int*)workspace;
+    p.sk_dp = pl.sk_dp; p.sk_g = PLAN_CUS;
+    p.splits = 1;
+    const long long T = ((long long)pl.tiles_r * pl.tiles_o - pl.sk_dp) * pl.nqt;
+    const unsigned Gt = (unsigned)cdiv(T, pl.sk_per);         // tail workgroups, <= PLAN_CUS
+    const unsigned G = pl.sk_dp > 0 ? (unsigned)PLAN_CUS : Gt;
+    if (Gt > 1) {
+      hipLaunchKernelGGL(sk_clear_kernel, dim3(Gt - 1), dim3(NT), 0, stream, p);
+      int rc = check_launch("sk_clear_kernel");
+      if (rc != ATX_OK) return rc;
+    }
+    if (lut_class == ATX_LUT_I16)
+      hipLaunchKernelGGL(lut_gemm_kernel<true>, dim3(G), dim3(NT), 0, stream, p);
+    else
+      hipLaunchKernelGGL(lut_gemm_kernel<false>, dim3(G), dim3(NT), 0, stream, p);
+    int rc = check_launch("lut_gemm_kernel");
+    if (rc != ATX_OK || Gt <= 1) return rc;
+    hipLaunchKernelGGL(sk_finish_kernel, dim3(Gt - 1), dim3(NT), 0, stream, p);
+    return check_launch("sk_finish_kernel");
+  }
   if (pl.splits > 1) {
     ATX_REQUIRE(workspace, "atx_lut_gemm: split-K plan needs a workspace of %lld bytes",
                 (long long)pl.splits * numel * 4);

@@ -63,6 +63,92 @@ def test_bgemm_int8_u8_input_bit_exact(shape, lut_name):
     assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
 
 
+# Stream-K schedule of the LUT GEMM: full rounds of whole tiles, then the
+# (tile, 4-table quad) iterations of the remaining tiles dealt out evenly over
+# 256 workgroups; a tile cut by a workgroup boundary sums its int32 parts
+# atomically into a slot.  Its workspace is 255 slots of 2048 x 32 int32,
+# which is how these tests know the schedule was taken.  ATX_LUT_SCHEDULE
+# forces it on shapes small enough for the full oracle:
+#   (1, 1000, 4096, 40): 4 tiles cut into ~60 segments each, K % 4 != 0,
+#                        O % 32 != 0;
+#   (2, 2002, 3000, 40): 6 tiles, the last row tile partial, K % 4 != 0;
+#   (150, 64, 2048, 64): 300 tiles: one round of 256 whole tiles, then 44
+#                        tiles over 256 workgroups (sampled check).
+SK_WORKSPACE = 255 * 2048 * 32 * 4
+SK_SHAPES = [(1, 1000, 4096, 40), (2, 2002, 3000, 40)]
+
+
+def _sampled_lut_sums(xi, wi, lut, n, o, l):
+    k = np.arange(xi.shape[1])
+    idx = xi[n[:, None], k[None, :], l[:, None]].astype(np.int64) * 256 + wi[o][:, :]
+    return np.asarray(lut, np.int64)[idx].sum(axis=1)
+
+
+def _check_sampled(y, xi, wi, lut, r, tiles_o):
+    N, K, L = xi.shape
+    Oc = wi.shape[0]
+    n, o, l = r.integers(0, N, 4096), r.integers(0, Oc, 4096), r.integers(0, L, 4096)
+    assert np.array_equal(y[n, o, l].astype(np.int64), _sampled_lut_sums(xi, wi, lut, n, o, l))
+    R = N * L
+    for tile in range(-(-R // 2048) * tiles_o):    # first / last row and channel of every tile
+        tr, to = divmod(tile, tiles_o)
+        for rr in (tr * 2048, min(R, tr * 2048 + 2048) - 1):
+            nn, ll = divmod(rr, L)
+            oo = np.array([to * 32, min(Oc, to * 32 + 32) - 1])
+            want = _sampled_lut_sums(xi, wi, lut, np.array([nn, nn]), oo, np.array([ll, ll]))
+            assert np.array_equal(y[nn, oo, ll].astype(np.int64), want), (tile, rr)
+
+
+@pytest.mark.parametrize("shape", SK_SHAPES)
+@pytest.mark.parametrize("lut_name", ["perturbed", "u16_c5"])
+def test_lut_gemm_stream_k_exact(shape, lut_name, monkeypatch):
+    monkeypatch.setenv("ATX_LUT_SCHEDULE", "stream_k")
+    N, K, L, Oc = shape
+    assert ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc) == SK_WORKSPACE
+    r = gen(zlib.crc32(repr((shape, lut_name)).encode()))
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(5)[lut_name]
+    want = O.lut_gemm_i64(xi, wi, lut)
+    for _ in range(2):                       # the slots are cleared on every call
+        y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32))
+        assert np.array_equal(y.cpu().numpy().astype(np.int64), want)
+    if lut_name == "perturbed":              # fp32 epilogue of the finished tiles
+        wv = wi.astype(np.float32) - 128
+        yf = ops.bgemm_fake_int8_claude(t(xi), t(wv), t(lut, torch.float32))
+        assert np.array_equal(yf.cpu().numpy(), want.astype(np.float32))
+    monkeypatch.setenv("ATX_LUT_SCHEDULE", "split")
+    assert ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc) != SK_WORKSPACE
+    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32))
+    assert np.array_equal(y.cpu().numpy().astype(np.int64), want)
+
+
+def test_lut_gemm_stream_k_full_round_then_tail_sampled(monkeypatch):
+    monkeypatch.setenv("ATX_LUT_SCHEDULE", "stream_k")
+    N, K, L, Oc = 150, 64, 2048, 64
+    assert ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc) == SK_WORKSPACE
+    r = gen(23)
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(6)["i16_edge"]
+    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32)).cpu().numpy()
+    _check_sampled(y, xi, wi, lut, r, 2)
+
+
+def test_lut_gemm_auto_schedule_takes_stream_k_on_resnet_layer(monkeypatch):
+    """ResNet-50 layer2 1x1 conv at batch 64 (R = 200704, K = 256, O = 128,
+    392 tiles): the cost model picks stream-K; dequant epilogue, sampled."""
+    monkeypatch.delenv("ATX_LUT_SCHEDULE", raising=False)
+    N, K, L, Oc = 64, 256, 3136, 128
+    assert ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc) == SK_WORKSPACE
+    r = gen(29)
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(8)["perturbed"]
+    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32)).cpu().numpy()
+    _check_sampled(y, xi, wi, lut, r, 4)
+
+
 @pytest.mark.parametrize("lut_name", ["asym", "exact_int8", "trunc4", "u16_c5", "i16_edge"])
 def test_lut_gemm_int32_exact_all_integer_classes(lut_name):
     r = gen(11)
