@@ -138,7 +138,11 @@ int atx_im2col_u8(const void* img, int dtype, atx_conv_geom g, uint8_t* out,
  *   ATX_OUT_DEQUANT y fp32 [N,O,L] = bias[o] + (float) sum * (sx[0]*sw[o])
  *                   (bias nullable)  — nn/Conv2d_int8.py:213-218 fused.
  * workspace: int32 scratch of atx_lut_gemm_workspace_bytes() bytes (split-K
- * partial sums); may be null when that function returns 0.
+ * partial sums, or the stream-K slots of tiles cut between workgroups:
+ * 255 x 2048 x 32 int32); may be null when that function returns 0.  The
+ * schedule (whole tiles, split-K, or whole-tile rounds then stream-K) is
+ * chosen by a cost model; the environment variable ATX_LUT_SCHEDULE
+ * (auto | split | stream_k) overrides it, read by both functions.
  * Replaces bgemm_lut_u8_kernel + reduce_splits_kernel + launch/dispatch
  * (csrc/claude/bgemm_lut_kernels.cuh:148-163,183-506). */
 enum { ATX_OUT_F32 = 0, ATX_OUT_I32 = 1, ATX_OUT_DEQUANT = 2 };
