@@ -24,55 +24,89 @@ template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int o
 }
 
 // xt[slot][r] = row_offset(index of tap operand_tap(slot, r) at output
-// position r); rows r >= N*L and taps k >= K hold 0.  A thread writes the
-// four rows of a quad (one tap: the tap changes every four rows) as one
-// 8-byte store; the grid stride over quads is a multiple of 4, so every
-// thread keeps one tap per slot and its decomposition is hoisted.
+// position r); rows r >= N*L and taps k >= K hold 0.  A thread owns one quad
+// of rows (four output positions, decomposed once) and walks the block's
+// run of IM_SLOTS slots, writing the quad of each slot as one 8-byte store
+// (consecutive threads: consecutive 8-byte pieces of a slot row).  The taps
+// of the block's slots (channel, kh, kw) are decomposed once into an LDS
+// table; slot s of quad q holds tap (s & ~3) | ((q + s) & 3).
+constexpr int IM_SLOTS = 32;
 template <typename T>
-__global__ void im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset,
-                                   int pad_index, const float* __restrict__ pad_dev,
-                                   uint16_t* __restrict__ xt, int Rpad) {
-  if (pad_dev) pad_index = (int)quant_index(pad_dev[0], 0);
-  const int L = g.OH * g.OW;
-  const int R = g.N * L;
+__global__ void __launch_bounds__(TB)
+im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad_index,
+                   const float* __restrict__ pad_dev, uint16_t* __restrict__ xt, int Rpad) {
+  __shared__ int toff[IM_SLOTS];             // c*H*W + kh*DH*W + kw*DW
+  __shared__ int tdh[IM_SLOTS], tdw[IM_SLOTS];
   const int KK = g.KH * g.KW;
   const int K = g.C * KK;
   const int HW = g.H * g.W;
-  const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
-  const int qstride = gridDim.x * blockDim.x;
-  const int nquad = Rpad >> 2;
-  for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
-    const int k = operand_tap(slot, q0 << 2);
-    const int c = k / KK;
-    const int t = k - c * KK;
-    const int kh = t / g.KW;
-    const int kw = t - kh * g.KW;
-    const int ih0 = kh * g.DH - g.PH;
-    const int iw0 = kw * g.DW - g.PW;
-    const long long cbase = (long long)c * HW;
-    uint16_t* dst = xt + (long long)slot * Rpad;
-    for (int q = q0; q < nquad; q += qstride) {
-      const int r0 = q << 2;
-      unsigned off[4] = {0u, 0u, 0u, 0u};
-      if (k < K && r0 < R) {
-        int n = r0 / L;
-        const int l = r0 - n * L;
-        int oh = l / g.OW;
-        int ow = l - oh * g.OW;
+  const int k0 = blockIdx.y * IM_SLOTS;
+  if (threadIdx.x < IM_SLOTS) {
+    const int k = min(k0 + (int)threadIdx.x, K - 1);
+    const int c = k / KK, t = k - c * KK;
+    const int kh = t / g.KW, kw = t - kh * g.KW;
+    tdh[threadIdx.x] = kh * g.DH;
+    tdw[threadIdx.x] = kw * g.DW;
+    toff[threadIdx.x] = c * HW + kh * g.DH * g.W + kw * g.DW;
+  }
+  __syncthreads();
+  const int q = blockIdx.x * TB + threadIdx.x;
+  if (q >= (Rpad >> 2)) return;
+  if (pad_dev) pad_index = (int)quant_index(pad_dev[0], 0);
+  const int L = g.OH * g.OW;
+  const int R = g.N * L;
+  const int r0 = q << 2;
+  // the quad's four output positions
+  long long base[4];
+  int ihb[4], iwb[4];
+  unsigned valid = 0;
+  {
+    int n = min(r0, max(R - 1, 0)) / L;
+    const int l = min(r0, max(R - 1, 0)) - n * L;
+    int oh = l / g.OW, ow = l - oh * g.OW;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (r0 + e < R) {
-            const int ih = oh * g.SH + ih0;
-            const int iw = ow * g.SW + iw0;
-            unsigned v = (unsigned)pad_index;
-            if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-              v = elem_index<T>(img[(long long)n * g.C * HW + cbase + ih * g.W + iw], offset);
-            off[e] = row_offset(v);
-          }
-          if (++ow == g.OW) { ow = 0; if (++oh == g.OH) { oh = 0; ++n; } }
-        }
+    for (int e = 0; e < 4; ++e) {
+      if (r0 + e < R) valid |= 1u << e;
+      ihb[e] = oh * g.SH - g.PH;
+      iwb[e] = ow * g.SW - g.PW;
+      base[e] = (long long)n * g.C * HW + (long long)ihb[e] * g.W + iwb[e];
+      if (++ow == g.OW) { ow = 0; if (++oh == g.OH) { oh = 0; ++n; } }
+    }
+  }
+  const int nslots = min(IM_SLOTS, operand_rows(K) - k0);   // a multiple of 4
+  uint16_t* dst = xt + (long long)k0 * Rpad + r0;
+  for (int s4 = 0; s4 < nslots; s4 += 4) {
+    // one quad of taps per iteration: its 16 loads are in flight together
+    T raw[4][4];
+    unsigned in = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int kl = s4 | ((q + u) & 3);        // this quad's tap of slot k0 + s4 + u
+      const bool kv = k0 + kl < K;
+      const int dh = tdh[kl], dw = tdw[kl], to = toff[kl];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ih = ihb[e] + dh, iw = iwb[e] + dw;
+        // rows past R (padding) load nothing: their position may lie past
+        // the last image
+        const bool b = kv && ((valid >> e) & 1u) && (unsigned)ih < (unsigned)g.H &&
+                       (unsigned)iw < (unsigned)g.W;
+        raw[u][e] = img[b ? base[e] + to : 0];
+        in |= (b ? 1u : 0u) << (4 * u + e);
       }
-      *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool kv = k0 + (s4 | ((q + u) & 3)) < K;
+      unsigned off[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned v = (in >> (4 * u + e)) & 1u ? elem_index<T>(raw[u][e], offset)
+                                                    : (unsigned)pad_index;
+        off[e] = kv && ((valid >> e) & 1u) ? row_offset(v) : 0u;
+      }
+      *(uint2*)(dst + (long long)(s4 + u) * Rpad) =
+          make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
     }
   }
 }
@@ -275,9 +309,9 @@ int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
   const int K = g.C * g.KH * g.KW;
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && (R == 0 || img), "atx_im2col_rows: null pointer");
-  static_assert(TB % 4 == 0, "the grid stride over quads keeps q & 3 per thread");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, TB), 1024),
-            (unsigned)std::min(operand_rows(K), 65535));
+  static_assert(IM_SLOTS % 4 == 0, "slot runs are whole quads of taps");
+  ATX_REQUIRE(cdiv(operand_rows(K), IM_SLOTS) <= 65535, "atx_im2col_rows: K too large");
+  dim3 grid((unsigned)cdiv(Rpad / 4, TB), (unsigned)cdiv(operand_rows(K), IM_SLOTS));
   if (dtype == 0)
     hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,
                        (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad);
