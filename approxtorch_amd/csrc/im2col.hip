@@ -179,40 +179,58 @@ __global__ void lut_map_pad_kernel(const T* __restrict__ in, int N, int C, int H
 // col2im: img[n,c,h,w] = sum over taps (kh,kw) hitting (h,w) of
 // col[n, (c,kh,kw), (oh,ow)], taps in ascending (kh, kw) order (F.fold).
 // Optional fused STE: img = mask ? img / s : 0 (s = max(scale[0], 1e-12)).
-__global__ void col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
-                              const uint8_t* __restrict__ mask,
-                              const float* __restrict__ scale, float* __restrict__ img) {
+// One thread per image element; I = int when the image has fewer than 2^31
+// elements (32-bit index arithmetic), long long otherwise.  The taps are
+// loaded in batches of CT with no branches (a tap that does not hit the
+// element loads element 0 and is skipped in the sum), so a thread has CT
+// loads in flight; the sum keeps ascending (kh, kw) order (CT = 1 for a
+// one-tap kernel).  ST = the stride when both strides equal 1 or 2
+// (divisions become shifts), 0 for the general case.
+template <typename I, int ST, int CT>
+__global__ void __launch_bounds__(TB)
+col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
+              const uint8_t* __restrict__ mask, const float* __restrict__ scale,
+              float* __restrict__ img) {
   const int L = g.OH * g.OW;
   const int KK = g.KH * g.KW;
-  const long long total = (long long)g.N * g.C * g.H * g.W;
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-       i += stride) {
-    const int w = (int)(i % g.W);
-    long long t = i / g.W;
-    const int h = (int)(t % g.H);
-    t /= g.H;
-    const int c = (int)(t % g.C);
-    const int n = (int)(t / g.C);
-    const float* cn = col + ((long long)n * g.C * KK + (long long)c * KK) * L;
+  const I HW = (I)g.H * g.W;
+  const I total = (I)g.N * g.C * HW;
+  const float s = mask ? fmaxf(scale[0], 1e-12f) : 1.0f;
+  for (I i = (I)blockIdx.x * TB + threadIdx.x; i < total; i += (I)gridDim.x * TB) {
+    const I plane = i / HW;                   // n * C + c
+    const int p = (int)(i - plane * HW);
+    const int h = p / g.W, w = p - h * g.W;
+    const float* cn = col + (long long)plane * KK * L;   // col[n][c*KK ..][L]
     float a = 0.0f;
-    for (int kh = 0; kh < g.KH; ++kh) {
-      const int y = h + g.PH - kh * g.DH;
-      if (y < 0 || y % g.SH) continue;
-      const int oh = y / g.SH;
-      if (oh >= g.OH) continue;
-      for (int kw = 0; kw < g.KW; ++kw) {
-        const int x = w + g.PW - kw * g.DW;
-        if (x < 0 || x % g.SW) continue;
-        const int ow = x / g.SW;
-        if (ow >= g.OW) continue;
-        a += cn[(long long)(kh * g.KW + kw) * L + oh * g.OW + ow];
+    int kh = 0, kw = 0;
+    for (int t0 = 0; t0 < KK; t0 += CT) {
+      float v[CT];
+      unsigned ok = 0;
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        const int y = h + g.PH - kh * g.DH, x = w + g.PW - kw * g.DW;
+        int oh, ow;
+        bool hit;
+        if constexpr (ST == 1) {
+          oh = y; ow = x;
+          hit = true;
+        } else if constexpr (ST == 2) {
+          oh = y >> 1; ow = x >> 1;
+          hit = ((y | x) & 1) == 0;
+        } else {
+          oh = y >= 0 ? y / g.SH : 0; ow = x >= 0 ? x / g.SW : 0;
+          hit = oh * g.SH == y && ow * g.SW == x;
+        }
+        hit = hit && t0 + j < KK && y >= 0 && x >= 0 && oh < g.OH && ow < g.OW;
+        v[j] = cn[hit ? (long long)(t0 + j) * L + oh * g.OW + ow : 0];
+        ok |= (hit ? 1u : 0u) << j;
+        if (++kw == g.KW) { kw = 0; ++kh; }
       }
+#pragma unroll
+      for (int j = 0; j < CT; ++j)
+        if ((ok >> j) & 1u) a += v[j];
     }
-    if (mask) {
-      const float s = fmaxf(scale[0], 1e-12f);
-      a = (mask[i] ? a : 0.0f) / s;
-    }
+    if (mask) a = (mask[i] ? a : 0.0f) / s;
     img[i] = a;
   }
 }
@@ -416,8 +434,18 @@ int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const flo
   const long long total = (long long)g.N * g.C * g.H * g.W;
   if (total == 0) return ATX_OK;
   ATX_REQUIRE(col && img && (!mask || scale), "atx_col2im: null pointer");
-  hipLaunchKernelGGL(col2im_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, col, g,
-                     mask, scale, img);
+  const dim3 grid(elem_grid(total, TB));
+  const bool small = total < 0x7fffffffLL - (long long)grid.x * TB;
+  const int st = g.SH == g.SW && (g.SH == 1 || g.SH == 2) ? g.SH : 0;
+  const bool one = g.KH * g.KW == 1;
+#define ATX_COL2IM(I, S, C)                                                              \
+  hipLaunchKernelGGL((col2im_kernel<I, S, C>), grid, dim3(TB), 0, stream, col, g, mask,   \
+                     scale, img)
+  if (!small) ATX_COL2IM(long long, 0, 9);
+  else if (st == 1) { if (one) ATX_COL2IM(int, 1, 1); else ATX_COL2IM(int, 1, 9); }
+  else if (st == 2) { if (one) ATX_COL2IM(int, 2, 1); else ATX_COL2IM(int, 2, 9); }
+  else { if (one) ATX_COL2IM(int, 0, 1); else ATX_COL2IM(int, 0, 9); }
+#undef ATX_COL2IM
   return check_launch("col2im_kernel");
 }
 
