@@ -57,6 +57,9 @@ _SIGS = {
     "atx_absmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp]),
     "atx_minmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_vp]),
     "atx_ema_absmax_apply": (c_int, [c_vp, c_float, c_float, c_float, c_vp, c_vp]),
+    "atx_absmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_float, c_float, c_float, c_vp, c_vp]),
+    "atx_minmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_float, c_float, c_int, c_vp,
+                               c_vp, c_vp, c_vp, c_vp]),
     "atx_ema_minmax_apply": (c_int, [c_vp, c_vp, c_float, c_float, c_int, c_vp, c_vp, c_vp,
                                      c_vp, c_vp]),
     "atx_weight_scale_ema": (c_int, [c_vp, c_int, c_ll, c_float, c_float, c_float, c_int,

@@ -137,10 +137,18 @@ __global__ void minmax_partial_kernel(const float* __restrict__ x, long long n,
   if (threadIdx.x == 0) { part[2 * blockIdx.x] = mn; part[2 * blockIdx.x + 1] = mx; }
 }
 
-// Pass 2: one block folds the partials.
+// EMA of the statistics, applied by the final reduction block when fused.
+struct EmaArgs {
+  int kind;                 // 0: none, 1: int8 absmax scale, 2: uint8 min/max qparams
+  float denom, m32, om32, qmax;
+  float* scale; float* zero; float* x_min; float* x_max;
+};
+__device__ void apply_ema(const EmaArgs& e, float mn, float mx);
+
+// Pass 2: one block folds the partials (and applies the EMA when fused).
 template <bool ABS>
 __global__ void minmax_final_kernel(const float* __restrict__ part, int nb,
-                                    float* mn_out, float* mx_out) {
+                                    float* mn_out, float* mx_out, EmaArgs ema) {
   float mn = __builtin_inff(), mx = ABS ? 0.0f : -__builtin_inff();
   for (int i = threadIdx.x; i < nb; i += blockDim.x) {
     mn = nmin(mn, part[2 * i]);
@@ -150,18 +158,23 @@ __global__ void minmax_final_kernel(const float* __restrict__ part, int nb,
   if (threadIdx.x == 0) {
     if (mn_out) *mn_out = mn;
     if (mx_out) *mx_out = mx;
+    if (ema.kind) apply_ema(ema, mn, mx);
   }
 }
 
 constexpr int RED_BLOCKS = 1024;   // partial-result slots (2 floats each)
 
 // nn/Conv2d_int8.py:144-146 — cur = stat / denom; new = m*cur + (1-m)*old.
-__global__ void ema_absmax_kernel(const float* stat, float denom, float m32, float om32,
-                                  float* scale) {
-  const float cur = stat[0] / denom;
+__device__ __forceinline__ void ema_absmax(float stat, float denom, float m32, float om32,
+                                           float* scale) {
+  const float cur = stat / denom;
   const float a = m32 * cur;
   const float b = om32 * scale[0];
   scale[0] = a + b;
+}
+__global__ void ema_absmax_kernel(const float* stat, float denom, float m32, float om32,
+                                  float* scale) {
+  ema_absmax(stat[0], denom, m32, om32, scale);
 }
 
 // nn/Conv2d_uint8.py:11-23 (uint8_qparams) for one (min, max) pair.
@@ -175,12 +188,22 @@ __device__ __forceinline__ void uint8_qparams(float mn, float mx, float qmax,
 }
 
 // nn/Conv2d_uint8.py:234-240.
+__device__ __forceinline__ void ema_minmax(float mn, float mx, float m32, float om32,
+                                           float qmax, float* x_min, float* x_max,
+                                           float* scale, float* zero) {
+  x_min[0] = m32 * mn + om32 * x_min[0];
+  x_max[0] = m32 * mx + om32 * x_max[0];
+  uint8_qparams(x_min[0], x_max[0], qmax, scale[0], zero[0]);
+}
 __global__ void ema_minmax_kernel(const float* mn, const float* mx, float m32, float om32,
                                   float qmax, float* x_min, float* x_max, float* scale,
                                   float* zero) {
-  x_min[0] = m32 * mn[0] + om32 * x_min[0];
-  x_max[0] = m32 * mx[0] + om32 * x_max[0];
-  uint8_qparams(x_min[0], x_max[0], qmax, scale[0], zero[0]);
+  ema_minmax(mn[0], mx[0], m32, om32, qmax, x_min, x_max, scale, zero);
+}
+
+__device__ void apply_ema(const EmaArgs& e, float mn, float mx) {
+  if (e.kind == 1) ema_absmax(mx, e.denom, e.m32, e.om32, e.scale);
+  else ema_minmax(mn, mx, e.m32, e.om32, e.qmax, e.x_min, e.x_max, e.scale, e.zero);
 }
 
 // Per-channel reductions of a weight [O, inner]: one block per channel.
@@ -259,7 +282,8 @@ int atx_fakequant_channel_fwd(const float* w, int O, long long inner, const floa
 }
 
 static int minmax_impl(const float* x, long long n, unsigned int* ws, float* mn_out,
-                       float* mx_out, bool absmode, hipStream_t stream) {
+                       float* mx_out, bool absmode, hipStream_t stream,
+                       EmaArgs ema = EmaArgs{}) {
   ATX_REQUIRE(n > 0, "min/max of an empty tensor is undefined");
   ATX_REQUIRE(x && ws, "minmax: null pointer");
   const int nb = elem_grid(n, EW, RED_BLOCKS);
@@ -272,10 +296,10 @@ static int minmax_impl(const float* x, long long n, unsigned int* ws, float* mn_
   if (rc) return rc;
   if (absmode)
     hipLaunchKernelGGL(minmax_final_kernel<true>, dim3(1), dim3(EW), 0, stream, part, nb,
-                       mn_out, mx_out);
+                       mn_out, mx_out, ema);
   else
     hipLaunchKernelGGL(minmax_final_kernel<false>, dim3(1), dim3(EW), 0, stream, part, nb,
-                       mn_out, mx_out);
+                       mn_out, mx_out, ema);
   return check_launch("minmax_final_kernel");
 }
 
@@ -291,6 +315,24 @@ int atx_minmax(const float* x, long long n, unsigned int* ws, float* mn_out, flo
                hipStream_t stream) {
   ATX_REQUIRE(mn_out && mx_out, "atx_minmax: null output");
   return minmax_impl(x, n, ws, mn_out, mx_out, false, stream);
+}
+
+int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_out,
+                   float denom, float m32, float om32, float* scale, hipStream_t stream) {
+  ATX_REQUIRE(stat_out && scale, "atx_absmax_ema: null output");
+  EmaArgs e{};
+  e.kind = 1; e.denom = denom; e.m32 = m32; e.om32 = om32; e.scale = scale;
+  return minmax_impl(x, n, ws, nullptr, stat_out, true, stream, e);
+}
+
+int atx_minmax_ema(const float* x, long long n, unsigned int* ws, float* mn_out,
+                   float* mx_out, float m32, float om32, int qmax, float* x_min, float* x_max,
+                   float* scale, float* zero, hipStream_t stream) {
+  ATX_REQUIRE(mn_out && mx_out && x_min && x_max && scale && zero, "atx_minmax_ema: null");
+  EmaArgs e{};
+  e.kind = 2; e.m32 = m32; e.om32 = om32; e.qmax = (float)qmax;
+  e.scale = scale; e.zero = zero; e.x_min = x_min; e.x_max = x_max;
+  return minmax_impl(x, n, ws, mn_out, mx_out, false, stream, e);
 }
 
 int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32, float* scale,

@@ -139,12 +139,17 @@ class Conv2d_int8(nn.Module):
             stat = torch.empty((), dtype=torch.float32, device=x.device)
             ws = ops._reduce_ws(x.device)
             s = L.stream_of(xc)
-            L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
-            if dist.is_available() and dist.is_initialized():
-                dist.all_reduce(stat, op=dist.ReduceOp.MAX)
             m32, om32 = _ema_coeffs(self.scale_momentum)
-            L.call("atx_ema_absmax_apply", L.ptr(stat),
-                   float((self.qmax - self.qmin) / 2), m32, om32, L.ptr(self.scale_x), s)
+            denom = float((self.qmax - self.qmin) / 2)
+            if not (dist.is_available() and dist.is_initialized()):
+                # no all-reduce in between: the EMA runs in the reduction's last launch
+                L.call("atx_absmax_ema", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), denom,
+                       m32, om32, L.ptr(self.scale_x), s)
+                return
+            L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
+            dist.all_reduce(stat, op=dist.ReduceOp.MAX)
+            L.call("atx_ema_absmax_apply", L.ptr(stat), denom, m32, om32,
+                   L.ptr(self.scale_x), s)
 
     def _update_scale_w(self):
         """Per-channel EMA of absmax(W)/qmax_w; zero channels keep their scale

@@ -191,11 +191,16 @@ class Conv2d_uint8(nn.Module):
             mx = torch.empty((), dtype=torch.float32, device=x.device)
             ws = ops._reduce_ws(x.device)
             s = L.stream_of(xc)
-            L.call("atx_minmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn), L.ptr(mx), s)
-            if dist.is_available() and dist.is_initialized():
-                dist.all_reduce(mn, op=dist.ReduceOp.MIN)
-                dist.all_reduce(mx, op=dist.ReduceOp.MAX)
             m32, om32 = _ema_coeffs(self.scale_momentum)
+            if not (dist.is_available() and dist.is_initialized()):
+                # no all-reduce in between: the EMA runs in the reduction's last launch
+                L.call("atx_minmax_ema", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn),
+                       L.ptr(mx), m32, om32, self.qmax, L.ptr(self.x_min), L.ptr(self.x_max),
+                       L.ptr(self.scale_x), L.ptr(self.zero_x), s)
+                return
+            L.call("atx_minmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn), L.ptr(mx), s)
+            dist.all_reduce(mn, op=dist.ReduceOp.MIN)
+            dist.all_reduce(mx, op=dist.ReduceOp.MAX)
             L.call("atx_ema_minmax_apply", L.ptr(mn), L.ptr(mx), m32, om32, self.qmax,
                    L.ptr(self.x_min), L.ptr(self.x_max), L.ptr(self.scale_x),
                    L.ptr(self.zero_x), s)

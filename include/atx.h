@@ -207,9 +207,9 @@ int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img,
 /* --------------------------------------------------------------- EMA stats
  * absmax EMA (nn/Conv2d_int8.py:137-146):
  *   stat = max|x|; scale <- m*(stat/denom) + (1-m)*scale, in fp32 with
- *   torch's operation order.  ws: 2 uint32 of scratch.  If stat_out is
- *   non-null the raw statistic is also written there (for an all-reduce by
- *   the caller between atx_absmax and atx_ema_apply). */
+ *   torch's operation order.  ws: atx_reduce_workspace_bytes() of scratch.
+ *   The statistic is written to stat_out, so a caller can all-reduce it
+ *   between atx_absmax and atx_ema_absmax_apply (data parallel). */
 long long atx_reduce_workspace_bytes(void);
 int atx_absmax(const float* x, long long n, unsigned int* ws, float* stat_out,
                hipStream_t stream);
@@ -218,6 +218,15 @@ int atx_minmax(const float* x, long long n, unsigned int* ws, float* mn_out,
 /* scale[0] <- m32 * (stat[0] / denom) + om32 * scale[0] */
 int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32,
                          float* scale, hipStream_t stream);
+/* atx_absmax then atx_ema_absmax_apply in one less launch (the EMA is applied
+ * by the reduction's final block); same results.  For callers with no
+ * all-reduce of the statistic in between (single process). */
+int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_out,
+                   float denom, float m32, float om32, float* scale, hipStream_t stream);
+/* atx_minmax then atx_ema_minmax_apply, fused the same way. */
+int atx_minmax_ema(const float* x, long long n, unsigned int* ws, float* mn_out,
+                   float* mx_out, float m32, float om32, int qmax, float* x_min,
+                   float* x_max, float* scale, float* zero, hipStream_t stream);
 /* uint8 activation qparams (nn/Conv2d_uint8.py:11-23,225-240): EMA of
  * min/max then scale = max((mx'-mn')/qmax, 1e-12), zero = clamp(rint(-mn'/scale)). */
 int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32,

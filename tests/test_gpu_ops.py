@@ -359,6 +359,12 @@ def test_ema_kernels_bitwise(m):
     L.call("atx_absmax", xg.data_ptr(), x.size, ws.data_ptr(), stat.data_ptr(), st)
     L.call("atx_ema_absmax_apply", stat.data_ptr(), 127.0, m32, om32, scale.data_ptr(), st)
     assert scale.item() == O.ema_absmax(x, np.float32(0.0371), m)
+    # the fused reduction + EMA (single-process layers) gives the same bits
+    scale2 = t(np.array([0.0371], dtype=np.float32))
+    stat2 = torch.empty((), device=DEV)
+    L.call("atx_absmax_ema", xg.data_ptr(), x.size, ws.data_ptr(), stat2.data_ptr(), 127.0,
+           m32, om32, scale2.data_ptr(), st)
+    assert stat2.item() == stat.item() and scale2.item() == scale.item()
     w = (r.standard_normal((33, 3, 3, 3)) * 0.1).astype(np.float32)
     w[5] = 0
     sw = (r.random(33) * 0.01).astype(np.float32)
@@ -376,6 +382,12 @@ def test_ema_kernels_bitwise(m):
            *[b.data_ptr() for b in bufs], st)
     want = O.ema_minmax(x, np.float32(-0.2), np.float32(1.7), m)
     assert [b.item() for b in bufs] == [float(v) for v in want]
+    bufs2 = [t(np.array([v], dtype=np.float32)) for v in (-0.2, 1.7, 0.0, 0.0)]
+    mn2, mx2 = torch.empty((), device=DEV), torch.empty((), device=DEV)
+    L.call("atx_minmax_ema", xg.data_ptr(), x.size, ws.data_ptr(), mn2.data_ptr(),
+           mx2.data_ptr(), m32, om32, 255, *[b.data_ptr() for b in bufs2], st)
+    assert (mn2.item(), mx2.item()) == (mn.item(), mx.item())
+    assert [b.item() for b in bufs2] == [float(v) for v in want]
     # uint8 weights
     wmin, wmax = (r.standard_normal(33) * 0.1).astype(np.float32), \
         (r.random(33) * 0.1).astype(np.float32)
