@@ -760,13 +760,26 @@ int launch_split_sum(const float* ws, int S, long long numel, int K,
 
 inline int tile_of(int extent) { return extent <= 64 ? 64 : 128; }
 
-// Split of the weight-gradient contraction: enough blocks to fill 256 CUs
-// (two blocks each, four rounds), every split at least four k-tiles deep.
+// Split of the weight-gradient contraction, every split at least four
+// k-tiles deep.  Cost in k-tiles: rounds of 512 blocks (256 CUs x two) x
+// (k-tiles per block + 4 for the block's prologue and epilogue) + 2 + S x
+// O*K / 1.5e6 for writing and summing the S partial slices.  Any S, not just
+// powers of two: on the ResNet-50 weight gradients at batch 64 this fills
+// one round with 13-62 k-tiles per block and is 10-14% faster than filling
+// four rounds (a 2048-block target) with 4-16.
 static int weight_splits(int O, int K, long long P) {
   const long long tiles = cdiv(O, tile_of(O)) * cdiv(K, tile_of(K));
-  long long s = 1;
-  while (tiles * s < 2048 && P / (s * 2) >= 4 * BK) s *= 2;
-  return (int)s;
+  const long long kt = cdiv(P, BK);                 // k-tiles of the contraction
+  const long long smax = std::max<long long>(1, std::min<long long>(P / (4 * BK), 4096));
+  double best = 0.0;
+  long long pick = 1;
+  for (long long s = 1; s <= smax; ++s) {
+    const long long kc = cdiv(kt, s), sr = cdiv(kt, kc);
+    const double cost = (double)cdiv(tiles * sr, 512) * (kc + 4) +
+                        (sr > 1 ? 2.0 + (double)sr * O * K / 1.5e6 : 0.0);
+    if (s == 1 || cost < best) { best = cost; pick = sr; }
+  }
+  return (int)pick;
 }
 
 struct DataArgs {
