@@ -790,14 +790,27 @@ struct DataArgs {
   float* partials;                           // [splits][N*K*L] when splits > 1
 };
 
-// Split of the backward-data contraction: when the output tiles leave more
-// than half of the CUs idle and O is long enough for several 4-k-tile
-// slices, O is split into deterministic partial slices (measured on c4
-// shapes: with 200-400 blocks the partial traffic costs more than it wins).
+// Split of the backward-data contraction over O into deterministic partial
+// slices, each at least four k-tiles deep.  Cost in k-tiles, as for the
+// weight gradient: rounds of 512 blocks x (k-tiles per block + 4) + 2 + S x
+// N*K*L / 1.5e6 for writing and summing the partials (the output is the
+// col buffer or the image gradient, so a split pays only when the tiles
+// leave most of a round idle).
 static int data_splits(int N, int O, int K, int L) {
   const long long blocks = cdiv((long long)N * L, 128) * cdiv(K, tile_of(K));
-  if (blocks >= 128 || O < 256 || (long long)N * K * L > 0x7fffffffLL) return 1;
-  return (int)std::max<long long>(1, std::min<long long>(cdiv(1024, blocks), O / 128));
+  const long long numel = (long long)N * K * L;
+  if (numel > 0x7fffffffLL) return 1;
+  const long long kt = cdiv(O, BK);
+  const long long smax = std::max<long long>(1, std::min<long long>(kt / 4, 64));
+  double best = 0.0;
+  long long pick = 1;
+  for (long long s = 1; s <= smax; ++s) {
+    const long long kc = cdiv(kt, s), sr = cdiv(kt, kc);
+    const double cost = (double)cdiv(blocks * sr, 512) * (kc + 4) +
+                        (sr > 1 ? 2.0 + (double)sr * numel / 1.5e6 : 0.0);
+    if (s == 1 || cost < best) { best = cost; pick = sr; }
+  }
+  return (int)pick;
 }
 
 template <int BM, bool VA, bool VB, bool SC>
