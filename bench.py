@@ -328,7 +328,7 @@ def roofline(timer, dt, traffic):
     gemm_ms, gemm_macs, launches = timer.summary()
     achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
     return {
-        "kernel": "lut_gemm_kernel (+ split-K reduce)",
+        "kernel": "lut_gemm_kernel (+ its split-K reduce / stream-K clear and finish launches)",
         "bound": "lds",
         "achieved": round(2 * achieved_glut, 1),
         "peak": round(LDS_PEAK_GBS, 1),
