@@ -66,27 +66,34 @@ __global__ void fakequant_bwd_kernel(const float* __restrict__ go,
 }
 
 // Weight [O, inner] per-channel fake-quant; wt is the LUT GEMM's transposed
-// weight operand [inner][Opad] (columns >= O hold index 0).
-__global__ void fakequant_channel_kernel(const float* __restrict__ w, int O,
-                                         long long inner, const float* __restrict__ scale,
-                                         const float* __restrict__ zero, float qmin,
-                                         float qmax, int offset, float* __restrict__ q,
-                                         uint8_t* __restrict__ mask, uint8_t* __restrict__ wq,
-                                         uint8_t* __restrict__ wt, int Opad) {
-  const long long total = inner * Opad;
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
-       t += stride) {
-    // t enumerates the transposed operand so its stores are coalesced.
-    const long long k = t / Opad;
-    const int o = (int)(t - k * Opad);
+// weight operand [inner][Opad] (columns >= O hold index 0).  A block owns a
+// tile of FQ_O channels x FQ_K taps: it reads w and writes q / mask / wq
+// along the taps (coalesced), stages the LUT indices in LDS and writes the
+// tile's wt rows (FQ_O bytes each) as 4-byte pieces.
+constexpr int FQ_O = 32, FQ_K = 64;
+__global__ void __launch_bounds__(256)
+fakequant_channel_kernel(const float* __restrict__ w, int O, long long inner,
+                         const float* __restrict__ scale, const float* __restrict__ zero,
+                         float qmin, float qmax, int offset, float* __restrict__ q,
+                         uint8_t* __restrict__ mask, uint8_t* __restrict__ wq,
+                         uint8_t* __restrict__ wt, int Opad) {
+  __shared__ uint8_t tile[FQ_K][FQ_O + 4];
+  const long long k0 = (long long)blockIdx.x * FQ_K;
+  const int o0 = blockIdx.y * FQ_O;
+  const bool asym = zero != nullptr;
+  // quantize: thread t handles taps (t & 63) of channels o0 + (t >> 6) + 4j
+  const int kl = threadIdx.x & (FQ_K - 1);
+  const long long k = k0 + kl;
+#pragma unroll
+  for (int j = 0; j < FQ_O / 4; ++j) {
+    const int ol = (threadIdx.x >> 6) + 4 * j;
+    const int o = o0 + ol;
     unsigned idx = 0;
-    if (o < O) {
-      const float s = fmaxf(scale[o], 1e-12f);
-      const bool asym = zero != nullptr;
+    if (o < O && k < inner) {
+      const float sc = fmaxf(scale[o], 1e-12f);
       bool m;
       const long long i = (long long)o * inner + k;
-      const float r = fake_quant(w[i], s, asym ? zero[o] : 0.0f, asym, qmin, qmax, m);
+      const float r = fake_quant(w[i], sc, asym ? zero[o] : 0.0f, asym, qmin, qmax, m);
       if (q) q[i] = r;
       if (mask) mask[i] = m;
       int v = to_int(r) + offset;
@@ -94,7 +101,21 @@ __global__ void fakequant_channel_kernel(const float* __restrict__ w, int O,
       idx = (unsigned)v;
       if (wq) wq[i] = (uint8_t)idx;
     }
-    if (wt) wt[t] = (uint8_t)idx;
+    tile[kl][ol] = (uint8_t)idx;
+  }
+  if (!wt) return;
+  __syncthreads();
+  // wt rows: FQ_K rows of FQ_O bytes = 512 pieces of 4 bytes
+#pragma unroll
+  for (int j = 0; j < (FQ_K * FQ_O / 4) / 256; ++j) {
+    const int piece = threadIdx.x + 256 * j;
+    const int r = piece / (FQ_O / 4), c4 = (piece % (FQ_O / 4)) * 4;
+    const long long kk = k0 + r;
+    if (kk < inner && o0 + c4 < Opad) {
+      const unsigned v = (unsigned)tile[r][c4] | ((unsigned)tile[r][c4 + 1] << 8) |
+                         ((unsigned)tile[r][c4 + 2] << 16) | ((unsigned)tile[r][c4 + 3] << 24);
+      *(unsigned*)(wt + kk * Opad + o0 + c4) = v;
+    }
   }
 }
 
@@ -275,9 +296,12 @@ int atx_fakequant_channel_fwd(const float* w, int O, long long inner, const floa
   const long long cols = wt ? Opad : O;
   if (inner * cols == 0) return ATX_OK;
   ATX_REQUIRE(w && scale, "atx_fakequant_channel_fwd: null pointer");
-  hipLaunchKernelGGL(fakequant_channel_kernel, dim3(elem_grid(inner * cols, EW)), dim3(EW),
-                     0, stream, w, O, inner, scale, zero, (float)qmin, (float)qmax, offset, q,
-                     mask, wq, wt, (int)cols);
+  ATX_REQUIRE(cdiv(inner, FQ_K) <= 0x7fffffffLL && cdiv(cols, FQ_O) <= 65535,
+              "atx_fakequant_channel_fwd: weight too large");
+  ATX_REQUIRE(((uintptr_t)wt & 3) == 0, "atx_fakequant_channel_fwd: wt must be 4-byte aligned");
+  const dim3 grid((unsigned)cdiv(inner, FQ_K), (unsigned)cdiv(cols, FQ_O));
+  hipLaunchKernelGGL(fakequant_channel_kernel, grid, dim3(256), 0, stream, w, O, inner, scale,
+                     zero, (float)qmin, (float)qmax, offset, q, mask, wq, wt, (int)cols);
   return check_launch("fakequant_channel_kernel");
 }
 

@@ -181,7 +181,7 @@ int atx_fakequant_bwd(const float* go, const uint8_t* mask, long long n,
 
 /* Per-channel fake-quant of a weight [O, inner]: q, mask, and the LUT index
  * image wq = q + offset (nullable), the transposed operand wt [inner][Opad]
- * (nullable).  nn/quantization.py:98-133. */
+ * (nullable, 4-byte aligned).  nn/quantization.py:98-133. */
 int atx_fakequant_channel_fwd(const float* w, int O, long long inner,
                               const float* scale, const float* zero,
                               int qmin, int qmax, int offset, float* q,
