@@ -34,6 +34,9 @@ __device__ __forceinline__ float fake_quant(float x, float s, float z, bool asym
 // Byte image of a quantized value; NaN maps to 0.
 __device__ __forceinline__ int to_int(float r) { return (r == r) ? (int)r : 0; }
 
+// VEC: four elements per thread (16-byte loads, 4-byte mask / byte-image
+// stores); needs n % 4 == 0 and aligned pointers.
+template <bool VEC>
 __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
                                      const float* __restrict__ scale,
                                      const float* __restrict__ zero, float qmin,
@@ -43,12 +46,32 @@ __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
   const bool asym = zero != nullptr;
   const float z = asym ? zero[0] : 0.0f;
   const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
-    bool m;
-    const float r = fake_quant(x[i], s, z, asym, qmin, qmax, m);
-    if (q) q[i] = r;
-    if (mask) mask[i] = m;
-    if (q8) q8[i] = (uint8_t)to_int(r);
+  if constexpr (VEC) {
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < (n >> 2);
+         i += stride) {
+      const float4 v = ((const float4*)x)[i];
+      const float xv[4] = {v.x, v.y, v.z, v.w};
+      float r[4];
+      unsigned mk = 0, b8 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bool m;
+        r[e] = fake_quant(xv[e], s, z, asym, qmin, qmax, m);
+        mk |= (m ? 1u : 0u) << (8 * e);
+        b8 |= ((unsigned)to_int(r[e]) & 255u) << (8 * e);
+      }
+      if (q) ((float4*)q)[i] = make_float4(r[0], r[1], r[2], r[3]);
+      if (mask) ((unsigned*)mask)[i] = mk;
+      if (q8) ((unsigned*)q8)[i] = b8;
+    }
+  } else {
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+      bool m;
+      const float r = fake_quant(x[i], s, z, asym, qmin, qmax, m);
+      if (q) q[i] = r;
+      if (mask) mask[i] = m;
+      if (q8) q8[i] = (uint8_t)to_int(r);
+    }
   }
 }
 
@@ -149,7 +172,20 @@ __global__ void minmax_partial_kernel(const float* __restrict__ x, long long n,
                                       float* __restrict__ part) {
   float mn = __builtin_inff(), mx = ABS ? 0.0f : -__builtin_inff();
   const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+  const long long t0 = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  // 16-byte loads over the aligned body, then the remaining elements
+  const long long n4 = ((uintptr_t)x & 15) == 0 ? (n >> 2) : 0;
+  for (long long i = t0; i < n4; i += stride) {
+    const float4 v = ((const float4*)x)[i];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float u = ABS ? fabsf(e[j]) : e[j];
+      mn = nmin(mn, u);
+      mx = nmax(mx, u);
+    }
+  }
+  for (long long i = 4 * n4 + t0; i < n; i += stride) {
     const float v = ABS ? fabsf(x[i]) : x[i];
     mn = nmin(mn, v);
     mx = nmax(mx, v);
@@ -270,8 +306,16 @@ int atx_fakequant_fwd(const float* x, long long n, const float* scale, const flo
   ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
   if (n == 0) return ATX_OK;
   ATX_REQUIRE(x && scale, "atx_fakequant_fwd: null pointer");
-  hipLaunchKernelGGL(fakequant_fwd_kernel, dim3(elem_grid(n, EW)), dim3(EW), 0, stream,
-                     x, n, scale, zero, (float)qmin, (float)qmax, q, mask, (uint8_t*)q8);
+  const bool vec = n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 15) == 0 &&
+                   ((uintptr_t)mask & 3) == 0 && ((uintptr_t)q8 & 3) == 0;
+  if (vec)
+    hipLaunchKernelGGL(fakequant_fwd_kernel<true>, dim3(elem_grid(n / 4, EW)), dim3(EW), 0,
+                       stream, x, n, scale, zero, (float)qmin, (float)qmax, q, mask,
+                       (uint8_t*)q8);
+  else
+    hipLaunchKernelGGL(fakequant_fwd_kernel<false>, dim3(elem_grid(n, EW)), dim3(EW), 0,
+                       stream, x, n, scale, zero, (float)qmin, (float)qmax, q, mask,
+                       (uint8_t*)q8);
   return check_launch("fakequant_fwd_kernel");
 }
 
