@@ -724,24 +724,36 @@ weight_gemm_kernel(WeightA<BM, VA> la, LB lb, WeightOut ep,
 // gw = mask ? sum / max(scale[o], 1e-12) : 0 with o = i / K.  A block sums
 // 256 / G consecutive elements over G groups of slices (group g takes slices
 // g, g + G, ...), then adds the G partials in group order: deterministic.
+template <bool VEC>
 __global__ void __launch_bounds__(256)
 split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, int G,
                  const uint8_t* __restrict__ mask, const float* __restrict__ scale,
                  float* __restrict__ out) {
-  __shared__ float part[256];
+  // VEC: each item is four consecutive elements (16-byte loads and stores;
+  // numel % 4 == 0); every element keeps the same summation order.
+  constexpr int W = VEC ? 4 : 1;
+  typedef float floatw __attribute__((ext_vector_type(W)));
+  __shared__ floatw part[256];
   const int t = threadIdx.x;
   const int epb = 256 / G;
   const int e = t % epb, grp = t / epb;
-  const long long i = (long long)blockIdx.x * epb + e;
-  float a = 0.0f;
+  const long long i = ((long long)blockIdx.x * epb + e) * W;   // first element
+  floatw a = 0.0f;
   if (i < numel)
-    for (int s = grp; s < S; s += G) a += ws[(long long)s * numel + i];
+    for (int s = grp; s < S; s += G) a += *(const floatw*)(ws + (long long)s * numel + i);
   part[t] = a;
   __syncthreads();
   if (grp == 0 && i < numel) {
     for (int g = 1; g < G; ++g) a += part[g * epb + e];
-    if (mask) a = (mask[i] ? a : 0.0f) / fmaxf(scale[i / K], 1e-12f);
-    out[i] = a;
+    if (mask) {
+      long long o = i / K, r = i - o * K;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        a[j] = (mask[i + j] ? a[j] : 0.0f) / fmaxf(scale[o], 1e-12f);
+        if (++r == K) { r = 0; ++o; }
+      }
+    }
+    *(floatw*)(out + i) = a;
   }
 }
 
@@ -749,12 +761,18 @@ split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, in
 int launch_split_sum(const float* ws, int S, long long numel, int K,
                             const uint8_t* mask, const float* scale, float* out,
                             hipStream_t stream) {
+  const bool vec = numel % 4 == 0 && ((uintptr_t)ws & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  const long long items = vec ? numel / 4 : numel;
   int G = 1;
-  while (G < 64 && G < S && cdiv(numel, 256 / G) < 1024) G *= 2;
-  const long long blocks = cdiv(numel, 256 / G);
+  while (G < 64 && G < S && cdiv(items, 256 / G) < 1024) G *= 2;
+  const long long blocks = cdiv(items, 256 / G);
   ATX_REQUIRE(blocks <= 0x7fffffffLL, "split_sum: too many elements");
-  hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, ws, S,
-                     numel, K, G, mask, scale, out);
+  if (vec)
+    hipLaunchKernelGGL(split_sum_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       ws, S, numel, K, G, mask, scale, out);
+  else
+    hipLaunchKernelGGL(split_sum_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       ws, S, numel, K, G, mask, scale, out);
   return check_launch("split_sum_kernel");
 }
 

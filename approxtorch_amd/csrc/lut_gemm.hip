@@ -687,10 +687,11 @@ sk_finish_kernel(const GemmParams p) {
 }
 
 // Split-K reduction: exact int64 sum of int32 partials, then the epilogue.
-__global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
-                                    long long numel, int O, int L, int out_kind,
-                                    void* __restrict__ y, const float* sx,
-                                    const float* sw, const float* bias) {
+// One output per thread (any size / alignment).
+__global__ void split_reduce1_kernel(const int* __restrict__ ws, int S,
+                                     long long numel, int O, int L, int out_kind,
+                                     void* __restrict__ y, const float* sx,
+                                     const float* sw, const float* bias) {
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
        i += (long long)gridDim.x * blockDim.x) {
     long long a = 0;
@@ -704,6 +705,40 @@ __global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
       const float sc = sx[0] * sw[o];
       const float t = (float)a * sc;
       ((float*)y)[i] = bias ? bias[o] + t : t;
+    }
+  }
+}
+
+// Four consecutive outputs per thread (16-byte partial loads); numel % 4 == 0.
+__global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
+                                    long long numel, int O, int L, int out_kind,
+                                    void* __restrict__ y, const float* sx,
+                                    const float* sw, const float* bias) {
+  for (long long q = blockIdx.x * (long long)blockDim.x + threadIdx.x; q < (numel >> 2);
+       q += (long long)gridDim.x * blockDim.x) {
+    const long long i = q << 2;
+    long long a[4] = {0, 0, 0, 0};
+    for (int s = 0; s < S; ++s) {
+      const int4 v = *(const int4*)(ws + (long long)s * numel + i);
+      a[0] += v.x; a[1] += v.y; a[2] += v.z; a[3] += v.w;
+    }
+    if (out_kind == ATX_OUT_I32) {
+      *(int4*)((int*)y + i) = make_int4((int)a[0], (int)a[1], (int)a[2], (int)a[3]);
+    } else if (out_kind == ATX_OUT_F32) {
+      *(float4*)((float*)y + i) =
+          make_float4((float)a[0], (float)a[1], (float)a[2], (float)a[3]);
+    } else {
+      long long nl = i / L;                    // n * O + o
+      int l = (int)(i - nl * L), o = (int)(nl % O);
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float sc = sx[0] * sw[o];
+        const float t = (float)a[e] * sc;
+        f[e] = bias ? bias[o] + t : t;
+        if (++l == L) { l = 0; if (++o == O) o = 0; }
+      }
+      *(float4*)((float*)y + i) = make_float4(f[0], f[1], f[2], f[3]);
     }
   }
 }
@@ -1004,9 +1039,14 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
                        stream, p);
   int rc = check_launch("lut_gemm_kernel");
   if (rc != ATX_OK || pl.splits == 1) return rc;
-  hipLaunchKernelGGL(split_reduce_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
-                     stream, (const int*)workspace, pl.splits, numel, O, L,
-                     ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
+  if (numel % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)workspace & 15) == 0)
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(elem_grid(numel / 4, 256)), dim3(256), 0,
+                       stream, (const int*)workspace, pl.splits, numel, O, L,
+                       ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
+  else
+    hipLaunchKernelGGL(split_reduce1_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
+                       stream, (const int*)workspace, pl.splits, numel, O, L,
+                       ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
   return check_launch("split_reduce_kernel");
 }
 
