@@ -42,7 +42,7 @@ COPY_BYTES = 512 << 20               # --calibrate-copy: bytes read and written 
 # reads per byte of the 512 MiB copy in that run.  None = not measured.
 # profiles/lut_gemm_hbm_traffic.md holds the counter readings (copy factors:
 # FETCH 0.500, WRITE 1.000).
-GEMM_TRAFFIC = {"c3": 754695333, "c4": 164475583}
+GEMM_TRAFFIC = {"c3": 759738368, "c4": 203479040}
 
 
 def parse():
