@@ -699,6 +699,47 @@ def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_po
     return q, mask, q8
 
 
+def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
+                   zero_point=None):
+    """Input fake-quant of a 1x1, stride-1, unpadded conv fused with its
+    operand packing: x [N,K,H,W] -> (mask bool [N,K,H,W], (xt, Rpad)), the
+    row-offset operand that fakequant_per_tensor's byte image would give
+    through conv_forward's im2col (offset 128: int8 image, 0: uint8)."""
+    if qmin >= qmax:
+        raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
+    xc = x.contiguous()
+    N, K = xc.size(0), xc.size(1)
+    Lc = xc.numel() // max(N * K, 1)
+    Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
+    mask = torch.empty(xc.shape, dtype=torch.bool, device=xc.device)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=xc.device)
+    L.call("atx_fakequant_rows", L.ptr(xc), N, K, Lc, L.ptr(scale), L.ptr(zero_point), qmin,
+           qmax, offset, L.ptr(mask), L.ptr(xt), Rpad, L.stream_of(xc))
+    return mask, (xt, Rpad)
+
+
+def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
+                      out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None, packed_w=None):
+    """LUT conv from a prepacked row-offset operand (xt, Rpad) of geometry g
+    (fakequant_rows, or conv_forward's return_operand): (y, wq)."""
+    xt, Rpad = xt_rpad
+    N, K = g.N, g.C * g.KH * g.KW
+    Lc = g.OH * g.OW
+    O = w_idx_or_val.size(0)
+    if w_idx_or_val.size(1) != K:
+        raise RuntimeError(f"weight has {w_idx_or_val.size(1)} taps, geometry needs {K}")
+    if xt.size(0) != L.operand_rows(K) or Rpad < N * Lc or xt.size(1) != Rpad:
+        raise RuntimeError(f"operand {tuple(xt.shape)} does not match K={K}, rows={N * Lc}")
+    if packed_w is None:
+        wq, wt, Opad = _pack_w(w_idx_or_val.contiguous(), offset)
+    else:
+        wq, wt, Opad = packed_w
+    ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
+    y = torch.empty((N, O, Lc), dtype=ydt, device=xt.device)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
+    return y, wq
+
+
 def fakequant_per_tensor_backward(grad_output: Tensor, mask: Tensor, scale: Tensor,
                                   channels: int = 1, inner: int = 1) -> Tensor:
     """gx = (mask ? go : 0) / max(scale, 1e-12) (csrc/claude/quantization.cu:223-258)."""

@@ -26,22 +26,25 @@ template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int o
 // xt[slot][r] = row_offset(index of tap operand_tap(slot, r) at output
 // position r); rows r >= N*L and taps k >= K hold 0.  A thread owns one quad
 // of rows (four output positions, decomposed once) and walks the block's
-// run of IM_SLOTS slots, writing the quad of each slot as one 8-byte store
+// run of slots, writing the quad of each slot as one 8-byte store
 // (consecutive threads: consecutive 8-byte pieces of a slot row).  The taps
 // of the block's slots (channel, kh, kw) are decomposed once into an LDS
-// table; slot s of quad q holds tap (s & ~3) | ((q + s) & 3).
+// table; slot s of quad q holds tap (s & ~3) | ((q + s) & 3).  The run is
+// `slots` long (a multiple of 4, at most IM_SLOTS): shorter runs give small
+// images (few row quads) more blocks.
 constexpr int IM_SLOTS = 32;
 template <typename T>
 __global__ void __launch_bounds__(TB)
 im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad_index,
-                   const float* __restrict__ pad_dev, uint16_t* __restrict__ xt, int Rpad) {
+                   const float* __restrict__ pad_dev, uint16_t* __restrict__ xt, int Rpad,
+                   int slots) {
   __shared__ int toff[IM_SLOTS];             // c*H*W + kh*DH*W + kw*DW
   __shared__ int tdh[IM_SLOTS], tdw[IM_SLOTS];
   const int KK = g.KH * g.KW;
   const int K = g.C * KK;
   const int HW = g.H * g.W;
-  const int k0 = blockIdx.y * IM_SLOTS;
-  if (threadIdx.x < IM_SLOTS) {
+  const int k0 = blockIdx.y * slots;
+  if (threadIdx.x < slots) {
     const int k = min(k0 + (int)threadIdx.x, K - 1);
     const int c = k / KK, t = k - c * KK;
     const int kh = t / g.KW, kw = t - kh * g.KW;
@@ -73,7 +76,7 @@ im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int p
       if (++ow == g.OW) { ow = 0; if (++oh == g.OH) { oh = 0; ++n; } }
     }
   }
-  const int nslots = min(IM_SLOTS, operand_rows(K) - k0);   // a multiple of 4
+  const int nslots = min(slots, operand_rows(K) - k0);   // a multiple of 4
   uint16_t* dst = xt + (long long)k0 * Rpad + r0;
   for (int s4 = 0; s4 < nslots; s4 += 4) {
     // one quad of taps per iteration: its 16 loads are in flight together
@@ -328,17 +331,21 @@ int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && (R == 0 || img), "atx_im2col_rows: null pointer");
   static_assert(IM_SLOTS % 4 == 0, "slot runs are whole quads of taps");
-  ATX_REQUIRE(cdiv(operand_rows(K), IM_SLOTS) <= 65535, "atx_im2col_rows: K too large");
-  dim3 grid((unsigned)cdiv(Rpad / 4, TB), (unsigned)cdiv(operand_rows(K), IM_SLOTS));
+  // the longest slot run that still gives the chip 2048 blocks (8 per CU)
+  const long long xblocks = cdiv(Rpad / 4, TB);
+  int slots = IM_SLOTS;
+  while (slots > 4 && xblocks * cdiv(operand_rows(K), slots) < 2048) slots >>= 1;
+  ATX_REQUIRE(cdiv(operand_rows(K), slots) <= 65535, "atx_im2col_rows: K too large");
+  dim3 grid((unsigned)xblocks, (unsigned)cdiv(operand_rows(K), slots));
   if (dtype == 0)
     hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,
-                       (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad);
+                       (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad, slots);
   else if (dtype == 1)
     hipLaunchKernelGGL(im2col_rows_kernel<uint8_t>, grid, dim3(TB), 0, stream,
-                       (const uint8_t*)img, g, 0, pad_index, pad_dev, xt, Rpad);
+                       (const uint8_t*)img, g, 0, pad_index, pad_dev, xt, Rpad, slots);
   else
     hipLaunchKernelGGL(im2col_rows_kernel<float>, grid, dim3(TB), 0, stream,
-                       (const float*)img, g, offset, pad_index, pad_dev, xt, Rpad);
+                       (const float*)img, g, offset, pad_index, pad_dev, xt, Rpad, slots);
   return check_launch("im2col_rows_kernel");
 }
 

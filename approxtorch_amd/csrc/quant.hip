@@ -75,6 +75,91 @@ __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
   }
 }
 
+// Fake-quant of a 1x1, stride-1, unpadded conv's input x [N,K,L] straight
+// into the LUT GEMM's row-offset operand: tap k of row r = n*L + l is
+// x[n][k][l], so xt[slot][r] = row_offset((to_int(q) + offset) & 255) for
+// the quantized value q of x[n][operand_tap(slot, r)][l] (the index the byte
+// image of fakequant_fwd_kernel gets from the im2col), and mask as
+// fakequant_fwd_kernel writes it.  A thread owns one quad of rows and one
+// quad of slots (blockIdx.y): it loads the 4 taps x 4 rows together (16-byte
+// loads under VEC: L % 4 == 0, x 16-byte and mask 4-byte aligned), then
+// writes one 8-byte xt piece per slot and one mask word per tap.  One quad
+// of taps per thread keeps the grid large when N*L is small (late layers).
+// Rows r >= N*L and taps k >= K hold offset 0 and write no mask.
+template <bool VEC>
+__global__ void __launch_bounds__(EW)
+fakequant_rows_kernel(const float* __restrict__ x, int N, int K, int L,
+                      const float* __restrict__ scale, const float* __restrict__ zero,
+                      float qmin, float qmax, int offset, uint8_t* __restrict__ mask,
+                      uint16_t* __restrict__ xt, int Rpad) {
+  const int q = blockIdx.x * EW + threadIdx.x;
+  if (q >= (Rpad >> 2)) return;
+  const float s = fmaxf(scale[0], 1e-12f);
+  const bool asym = zero != nullptr;
+  const float z = asym ? zero[0] : 0.0f;
+  const int R = N * L;
+  const int r0 = q << 2;
+  long long base[4];          // x offset of tap 0 at each of the quad's rows
+  unsigned valid = 0;
+  if (R > 0) {
+    const int rr = min(r0, R - 1);
+    int n = rr / L, l = rr - n * L;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (r0 + e < R) valid |= 1u << e;
+      base[e] = (long long)n * K * L + l;
+      if (++l == L) { l = 0; ++n; }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) base[e] = 0;
+  }
+  const int k4 = blockIdx.y * 4;
+  float v[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = k4 | ((q + u) & 3);          // this quad's tap of slot k4 + u
+    const long long kl = (long long)min(k, K - 1) * L;
+    if constexpr (VEC) {
+      // L % 4 == 0: the quad is four consecutive elements of one x row,
+      // wholly inside R or wholly padding
+      const float4 f = (k < K && valid) ? *(const float4*)(x + base[0] + kl)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[u][e] = (k < K && ((valid >> e) & 1u)) ? x[base[e] + kl] : 0.0f;
+    }
+  }
+  uint16_t* dst = xt + (long long)k4 * Rpad + r0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = k4 | ((q + u) & 3);
+    const long long kl = (long long)k * L;
+    unsigned off[4], mk = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bool m;
+      const float r = fake_quant(v[u][e], s, z, asym, qmin, qmax, m);
+      const unsigned idx = (unsigned)(to_int(r) + offset) & 255u;
+      off[e] = (k < K && ((valid >> e) & 1u)) ? row_offset(idx) : 0u;
+      mk |= (m ? 1u : 0u) << (8 * e);
+    }
+    *(uint2*)(dst + (long long)u * Rpad) =
+        make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
+    if (k < K) {
+      if constexpr (VEC) {
+        if (valid) *(unsigned*)(mask + base[0] + kl) = mk;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((valid >> e) & 1u) mask[base[e] + kl] = (uint8_t)((mk >> (8 * e)) & 1u);
+      }
+    }
+  }
+}
+
 // gx = (mask ? go : 0) / s[c], c = (i / inner) % C.
 __global__ void fakequant_bwd_kernel(const float* __restrict__ go,
                                      const uint8_t* __restrict__ mask, long long n,
@@ -317,6 +402,30 @@ int atx_fakequant_fwd(const float* x, long long n, const float* scale, const flo
                        stream, x, n, scale, zero, (float)qmin, (float)qmax, q, mask,
                        (uint8_t*)q8);
   return check_launch("fakequant_fwd_kernel");
+}
+
+int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
+                       const float* zero, int qmin, int qmax, int offset, uint8_t* mask,
+                       uint16_t* xt, int Rpad, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_fakequant_rows: negative size");
+  ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
+  ATX_REQUIRE(offset == 0 || offset == 128, "atx_fakequant_rows: offset must be 0 or 128");
+  ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % ATX_ROW_TILE == 0,
+              "atx_fakequant_rows: Rpad must be a multiple of %d covering N*L", ATX_ROW_TILE);
+  if ((long long)K * Rpad == 0) return ATX_OK;
+  // an empty x (N*L == 0) only writes the zero padding rows
+  ATX_REQUIRE(xt && scale && ((long long)N * L == 0 || (x && mask)),
+              "atx_fakequant_rows: null pointer");
+  ATX_REQUIRE(operand_rows(K) / 4 <= 65535, "atx_fakequant_rows: K too large");
+  const dim3 grid((unsigned)cdiv(Rpad / 4, EW), (unsigned)(operand_rows(K) / 4));
+  const bool vec = L % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)mask & 3) == 0;
+  if (vec)
+    hipLaunchKernelGGL(fakequant_rows_kernel<true>, grid, dim3(EW), 0, stream, x, N, K, L,
+                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad);
+  else
+    hipLaunchKernelGGL(fakequant_rows_kernel<false>, grid, dim3(EW), 0, stream, x, N, K, L,
+                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad);
+  return check_launch("fakequant_rows_kernel");
 }
 
 int atx_fakequant_bwd(const float* go, const uint8_t* mask, long long n, const float* scale,

@@ -228,13 +228,25 @@ class _conv2d_int8_fused(Function):
     def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w):
         g, depthwise = _conv_setup(x, weight, geom)
         O = weight.size(0)
-        _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
-                                                  q8_dtype=torch.int8)
+        # a 1x1, stride-1, unpadded conv reads x itself as its operand: the
+        # fake-quant writes the row-offset operand directly, no byte image
+        pointwise = (not depthwise and g.KH == 1 and g.KW == 1 and g.SH == 1 and g.SW == 1
+                     and g.PH == 0 and g.PW == 0)
+        if pointwise:
+            mask_x, xt_rpad = ops.fakequant_rows(x, scale_x, qmin, qmax, 128)
+        else:
+            _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
+                                                      q8_dtype=torch.int8)
         _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, -qmax_w, qmax_w,
                                                             offset=128,
                                                             want_wt=not depthwise)
         b = None if bias is None else bias.detach().contiguous()
-        if depthwise:
+        if pointwise:
+            y, _ = ops.conv_forward_rows(xt_rpad, wq, lut, g, 128,
+                                         out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
+                                         sw=scale_w, bias=b, packed_w=(wq, wt, Opad))
+            saved_x, ctx.rpad = xt_rpad
+        elif depthwise:
             y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
                                    sx=scale_x, sw=scale_w, bias=b)
             saved_x, ctx.rpad = xq8, None

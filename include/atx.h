@@ -172,6 +172,20 @@ int atx_fakequant_fwd(const float* x, long long n, const float* scale,
                       const float* zero, int qmin, int qmax, float* q,
                       uint8_t* mask, void* q8, hipStream_t stream);
 
+/* The input fake-quant of a 1x1, stride-1, unpadded, ungrouped conv fused
+ * with its operand packing: x fp32 [N,K,L] -> mask uint8 [N,K,L] (as
+ * atx_fakequant_fwd) and the row-offset operand xt [Kpad][Rpad] whose LUT
+ * index for x[n][k][l] is (q + offset) & 255, q the quantized value as an
+ * integer (offset 128: the int8 byte image read with index v+128; 0: the
+ * uint8 one).  Bit-identical to atx_fakequant_fwd's q8 followed by
+ * atx_im2col_rows of that 1x1 geometry, without the byte image.  Replaces
+ * the fake-quant of x (nn/quantization.py:37-62) and the im2col prepass
+ * (csrc/claude/bgemm_lre_backward_claude.cu:215-269) of a 1x1 conv in
+ * nn/Conv2d_int8.py:192-212. */
+int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
+                       const float* zero, int qmin, int qmax, int offset,
+                       uint8_t* mask, uint16_t* xt, int Rpad, hipStream_t stream);
+
 /* gx = (mask ? go : 0) / max(scale, 1e-12); scale has 1 (per-tensor) or
  * C (per-channel, channel = (i / inner) % C) elements.
  * csrc/claude/quantization.cu:112-143; nn/quantization.py:110-113. */

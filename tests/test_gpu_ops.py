@@ -326,6 +326,97 @@ def test_fakequant_symmetric_bitwise(scale):
     assert np.array_equal(gx.cpu().numpy(), O.fakequant_backward(go, mo, s))
 
 
+def decode_operand(xt, K, R):
+    """LUT indices [K, R] of a row-offset operand xt [Kpad][Rpad]: slot s of
+    row r holds tap (s & ~3) | ((r//4 + s) & 3) as v*256 + ((v >> 1) & 3)*16;
+    asserts the padding entries are 0."""
+    xt = xt.astype(np.int64) & 0xFFFF
+    Kp, Rp = xt.shape
+    s = np.arange(Kp)[:, None]
+    r = np.arange(Rp)[None, :]
+    tap = (s & ~3) | (((r >> 2) + s) & 3)
+    v = xt >> 8
+    assert np.array_equal(xt, np.where((tap < K) & (r < R), v * 256 + ((v >> 1) & 3) * 16, 0))
+    out = np.zeros((K, R), np.int64)
+    keep = (tap < K) & (r < R)
+    out[tap[keep], np.broadcast_to(r, tap.shape)[keep]] = v[keep]
+    return out
+
+
+# Implicit-im2col operand at sizes whose grids take slot runs of 32, 16 and
+# 8 (the launch shortens the run until it has 2048 blocks; the small conv
+# tests above take runs of 4): (N, C, H, W, padding).
+IM_RUN_CASES = [(2, 256, 128, 128, 1), (2, 128, 128, 128, 1), (1, 512, 64, 64, 0)]
+
+
+@pytest.mark.parametrize("case", IM_RUN_CASES)
+def test_im2col_rows_slot_runs_sampled(case):
+    N, C, H, W, p = case
+    r = gen(zlib.crc32(repr(case).encode()))
+    img = r.integers(-128, 128, (N, C, H, W)).astype(np.int8)
+    g = ops.conv_geom(img.shape, (3, 3), (1, 1), (p, p), (1, 1))
+    _, _, (xt, Rpad) = ops.conv_forward(t(img), torch.zeros(1, C * 9, device=DEV),
+                                        t(np.zeros(65536, np.float32)), g, 128, 128,
+                                        return_operand=True)
+    K, OH, OW = C * 9, g.OH, g.OW
+    R = N * OH * OW
+    # sampled (slot, row) pairs plus every row of the first and last slots
+    slot = np.concatenate([r.integers(0, K, 30000), np.zeros(R, np.int64),
+                           np.full(R, K - 1)])
+    row = np.concatenate([r.integers(0, Rpad, 30000), np.arange(R), np.arange(R)])
+    got = xt[t(slot), t(row)].cpu().numpy().astype(np.int64) & 0xFFFF
+    k = (slot & ~3) | (((row >> 2) + slot) & 3)
+    live = (k < K) & (row < R)
+    c, kh, kw = k // 9, (k % 9) // 3, k % 3
+    n, rem = row // (OH * OW), row % (OH * OW)
+    ih, iw = rem // OW - p + kh, rem % OW - p + kw
+    inside = live & (ih >= 0) & (ih < H) & (iw >= 0) & (iw < W)
+    v = np.full(slot.shape, 128, np.int64)       # padding taps read index 128
+    v[inside] = img[n[inside], c[inside], ih[inside], iw[inside]].astype(np.int64) + 128
+    want = np.where(live, v * 256 + ((v >> 1) & 3) * 16, 0)
+    assert np.array_equal(got, want)
+
+
+# (N, C, H, W): L = 49 and K = 6 take the element-wise path, L = 64 / 784
+# the 16-byte one; K = 40 and 64 span two slot runs; the last is a 1x1 pixel.
+FQ_ROWS_CASES = [(2, 6, 7, 7), (3, 40, 8, 8), (2, 64, 28, 28), (5, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("shape", FQ_ROWS_CASES)
+@pytest.mark.parametrize("signed", [True, False])
+@pytest.mark.parametrize("misalign", [False, True])
+def test_fakequant_rows_matches_fakequant_then_im2col(shape, signed, misalign):
+    N, C, H, W = shape
+    n = N * C * H * W
+    x = special_x(zlib.crc32(repr(shape).encode()), max(n, 12))[:n]
+    base = torch.zeros(n + 1, device=DEV)
+    base[int(misalign):int(misalign) + n] = t(x)
+    xd = base[int(misalign):int(misalign) + n].view(N, C, H, W)
+    s = np.float32(0.023)
+    if signed:
+        qmin, qmax, off, z, zt = -128, 127, 128, None, None
+    else:
+        qmin, qmax, off = 0, 255, 0
+        z = np.float32(113)
+        zt = t(np.array([z]))
+    mask, (xt, Rpad) = ops.fakequant_rows(xd, t(np.array([s])), qmin, qmax, off,
+                                          zero_point=zt)
+    qo, mo = O.fakequant(x, s, qmin, qmax, zero=z)
+    assert np.array_equal(mask.cpu().numpy().reshape(-1), mo)
+    idx = O.quant_index(qo, off).reshape(N, C, H * W)
+    want = idx.transpose(1, 0, 2).reshape(C, N * H * W)
+    assert np.array_equal(decode_operand(xt.cpu().numpy(), C, N * H * W), want)
+    # bit-identical to the byte image through the conv's im2col
+    _, m2, q8 = ops.fakequant_per_tensor(xd, t(np.array([s])), qmin, qmax, zero_point=zt,
+                                         want_q=False,
+                                         q8_dtype=torch.int8 if signed else torch.uint8)
+    g = ops.conv_geom((N, C, H, W), (1, 1), (1, 1), (0, 0), (1, 1))
+    _, _, (xt2, Rpad2) = ops.conv_forward(q8, torch.zeros(1, C, device=DEV),
+                                          t(np.zeros(65536, np.float32)), g, off, off,
+                                          return_operand=True)
+    assert Rpad == Rpad2 and torch.equal(xt, xt2) and torch.equal(mask, m2)
+
+
 def test_fakequant_asymmetric_and_per_channel_bitwise():
     x = special_x(3).reshape(20, 1000)
     s, z = np.float32(0.031), np.float32(113)
