@@ -533,7 +533,10 @@ struct WeightOut {
 };
 
 // ----------------------------------------------------------------- main kernel
-template <int BM, int BN, class LA, class LB>
+// TR: the MFMA takes the B fragment as its first operand, so the 16x16
+// result block is stored transposed (lane holds columns 4*(lane >> 4) + r of
+// row lane & 15); the products and their order are the same.
+template <int BM, int BN, class LA, class LB, bool TR = false>
 __device__ __forceinline__ void mma_tile(const float* As, const float* Bs,
                                          floatx4 (&acc)[BM / 32][BN / 32]) {
   constexpr int TM = BM / 32, TN = BN / 32;
@@ -551,14 +554,15 @@ __device__ __forceinline__ void mma_tile(const float* As, const float* Bs,
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = TR ? __builtin_amdgcn_mfma_f32_16x16x4f32(b[j], a[i], acc[i][j], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
   }
 }
 
 // acc = sum over the contraction range [pb, pe) of A tile x B tile.
 // Double-buffered: the global loads of k-tile i+1 are in flight while tile i
 // is multiplied; one barrier per k-tile.
-template <int BM, int BN, class LA, class LB>
+template <int BM, int BN, bool TR = false, class LA, class LB>
 __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int pb, int pe,
                                            floatx4 (&acc)[BM / 32][BN / 32], float* As0,
                                            float* As1, float* Bs0, float* Bs1) {
@@ -582,7 +586,7 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
     // behind them: the scheduler would otherwise sink the loads, or hoist
     // the stash's use of them, and expose the load latency.
     __builtin_amdgcn_sched_barrier(0);
-    mma_tile<BM, BN, LA, LB>(Ac, Bc, acc);
+    mma_tile<BM, BN, LA, LB, TR>(Ac, Bc, acc);
     __builtin_amdgcn_sched_barrier(0);
     la.stash(An, tab);
     lb.stash(Bn, tab);
@@ -590,58 +594,102 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
     float* x = Ac; Ac = An; An = x;
     x = Bc; Bc = Bn; Bn = x;
   }
-  mma_tile<BM, BN, LA, LB>(Ac, Bc, acc);
+  mma_tile<BM, BN, LA, LB, TR>(Ac, Bc, acc);
 }
 
-// D layout of 16x16x4 f32: lane holds rows 4*(lane >> 4) + r, column lane & 15.
 // Data-GEMM epilogue: out[n][m][l] for column c = n*L + l (rows m), with the
 // optional per-tensor fake-quant STE (mask ? v : 0) / max(scale, 1e-12).
-template <int BM, int BN>
+// VEC (L % 4 == 0, out 16-byte and mask 4-byte aligned): the tiles are
+// multiplied with TR (transposed 16x16 blocks), so a lane holds the four
+// consecutive columns c0..c0+3 of one row m; the quad lies in one image and
+// is wholly inside N*L or wholly outside, so it is one 16-byte store and one
+// 4-byte mask load.  Otherwise the blocks are untransposed and every element
+// is stored on its own.
+template <int BM, int BN, bool VEC>
 __device__ __forceinline__ void data_epilogue(const DataOut& ep,
                                               const floatx4 (&acc)[BM / 32][BN / 32], int m0,
                                               int n0) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   constexpr int TM = BM / 32;
+  const float sdiv = ep.mask ? fmaxf(ep.scale[0], 1e-12f) : 1.0f;
+  if constexpr (VEC) {
 #pragma unroll
   for (int j = 0; j < BN / 32; ++j) {
-    const int c = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
-    const bool cv = c < ep.NL;
-    const int cc = cv ? c : 0;
-    const int n = cc / ep.L;
-    const long long off = (long long)n * ep.K * ep.L + (cc - n * ep.L);
-    if (ep.mask) {
-      // all mask bytes of the column group first (no branch around the loads)
-      const float sdiv = fmaxf(ep.scale[0], 1e-12f);
-      unsigned char mk[TM][4];
+    const int c0 = n0 + wn * (BN / 2) + j * 16 + 4 * (lane >> 4);
+    {
+      const bool cv = c0 < ep.NL;
+      const int cc = cv ? c0 : 0;
+      const int n = cc / ep.L;
+      const long long off = (long long)n * ep.K * ep.L + (cc - n * ep.L);
+      if (ep.mask) {
+        unsigned mk[TM];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
-          mk[i][r] = ep.mask[cv && m < ep.K ? off + (long long)m * ep.L : 0];
+        for (int i = 0; i < TM; ++i) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + (lane & 15);
+          mk[i] = *(const unsigned*)(ep.mask + (cv && m < ep.K ? off + (long long)m * ep.L : 0));
         }
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + (lane & 15);
+          floatx4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
-          if (cv && m < ep.K)
-            ep.col[off + (long long)m * ep.L] = (mk[i][r] ? acc[i][j][r] : 0.0f) / sdiv;
+          for (int r = 0; r < 4; ++r)
+            v[r] = ((mk[i] >> (8 * r)) & 255u ? acc[i][j][r] : 0.0f) / sdiv;
+          if (cv && m < ep.K) *(floatx4*)(ep.col + off + (long long)m * ep.L) = v;
         }
-    } else {
+      } else {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
-          if (cv && m < ep.K) ep.col[off + (long long)m * ep.L] = acc[i][j][r];
+        for (int i = 0; i < TM; ++i) {
+          const int m = m0 + wm * (BM / 2) + i * 16 + (lane & 15);
+          if (cv && m < ep.K) *(floatx4*)(ep.col + off + (long long)m * ep.L) = acc[i][j];
         }
+      }
+    }
+  }
+  } else {
+    // untransposed blocks (lane holds rows 4*(lane >> 4) + r of column
+    // lane & 15): per element, 16 consecutive columns per store
+#pragma unroll
+    for (int j = 0; j < BN / 32; ++j) {
+      const int c = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
+      const bool cv = c < ep.NL;
+      const int cc = cv ? c : 0;
+      const int n = cc / ep.L;
+      const long long off = (long long)n * ep.K * ep.L + (cc - n * ep.L);
+      if (ep.mask) {
+        unsigned char mk[TM][4];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+            mk[i][r] = ep.mask[cv && m < ep.K ? off + (long long)m * ep.L : 0];
+          }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+            if (cv && m < ep.K)
+              ep.col[off + (long long)m * ep.L] = (mk[i][r] ? acc[i][j][r] : 0.0f) / sdiv;
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+            if (cv && m < ep.K) ep.col[off + (long long)m * ep.L] = acc[i][j][r];
+          }
+      }
     }
   }
 }
 
 
+// VB: go quads (L % 4 == 0) are 16-byte loads and the output quads 16-byte
+// stores (data_epilogue VEC).
 template <int BM, int BN, bool VA, bool VB, bool SC>
 __global__ void __launch_bounds__(GT, 2)
 data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
@@ -660,13 +708,13 @@ data_gemm_kernel(DataA<BM, VA> la, DataB<BN, VB, SC> lb, DataOut ep,
   const int ob = blockIdx.z * o_chunk, oe = min(O, ob + o_chunk);
   ep.col += (long long)blockIdx.z * ep.split_stride;
   floatx4 acc[BM / 32][BN / 32];
-  gemm_tiles<BM, BN>(la, lb, tab, ob, oe, acc, As[0], As[1], Bs[0], Bs[1]);
-  data_epilogue<BM, BN>(ep, acc, m0, n0);
+  gemm_tiles<BM, BN, VB>(la, lb, tab, ob, oe, acc, As[0], As[1], Bs[0], Bs[1]);
+  data_epilogue<BM, BN, VB>(ep, acc, m0, n0);
 }
 
 // Implicit backward-data kernel: the data GEMM's epilogue (direct image
 // output with the optional fused STE) over DgradA x DgradB.
-template <int BM, int BN, bool SC>
+template <int BM, int BN, bool SC, bool VO>
 __global__ void __launch_bounds__(GT, 2)
 dgrad_gemm_kernel(DgradA<BM> la, DgradB<BN, SC> lb, DataOut ep, const float* __restrict__ tx,
                   int P) {
@@ -680,8 +728,8 @@ dgrad_gemm_kernel(DgradA<BM> la, DgradB<BN, SC> lb, DataOut ep, const float* __r
   lb.init(t, n0);
   __syncthreads();
   floatx4 acc[BM / 32][BN / 32];
-  gemm_tiles<BM, BN>(la, lb, tab, 0, P, acc, As[0], As[1], Bs[0], Bs[1]);
-  data_epilogue<BM, BN>(ep, acc, m0, n0);
+  gemm_tiles<BM, BN, VO>(la, lb, tab, 0, P, acc, As[0], As[1], Bs[0], Bs[1]);
+  data_epilogue<BM, BN, VO>(ep, acc, m0, n0);
 }
 
 template <class LB> __device__ __forceinline__ void set_pad(LB&, const float*) {}
@@ -850,7 +898,9 @@ static void launch_data(const DataArgs& a, hipStream_t stream) {
 template <int BM, bool SC>
 static void dispatch_data_vec(const DataArgs& a, hipStream_t stream) {
   const bool va = a.K % 4 == 0 && (uintptr_t)a.wq % 4 == 0;
-  const bool vb = a.L % 4 == 0 && (uintptr_t)a.go % 16 == 0;
+  const float* out = a.splits > 1 ? a.partials : a.out;
+  const bool vb = a.L % 4 == 0 && (uintptr_t)a.go % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                  (a.splits > 1 || (uintptr_t)a.mask % 4 == 0);
   if (va && vb) launch_data<BM, true, true, SC>(a, stream);
   else if (va) launch_data<BM, true, false, SC>(a, stream);
   else if (vb) launch_data<BM, false, true, SC>(a, stream);
@@ -965,8 +1015,12 @@ static int launch_dgrad(const float* go, const uint8_t* wq, const float* tx,
   lb.go = go; lb.g = g; lb.O = O; lb.NHW = NHW; lb.sx = sx; lb.sw = sw;
   DataOut ep{gx, g.C, HW, NHW, mask, scale, 0};
   dim3 grid((unsigned)cdiv(NHW, BN), (unsigned)cdiv(g.C, BM), 1);
-  hipLaunchKernelGGL((dgrad_gemm_kernel<BM, BN, SC>), grid, dim3(GT), 0, stream, la, lb, ep, tx,
-                     KK * O);
+  if (HW % 4 == 0 && (uintptr_t)gx % 16 == 0 && (uintptr_t)mask % 4 == 0)
+    hipLaunchKernelGGL((dgrad_gemm_kernel<BM, BN, SC, true>), grid, dim3(GT), 0, stream, la, lb,
+                       ep, tx, KK * O);
+  else
+    hipLaunchKernelGGL((dgrad_gemm_kernel<BM, BN, SC, false>), grid, dim3(GT), 0, stream, la,
+                       lb, ep, tx, KK * O);
   return check_launch("dgrad_gemm_kernel");
 }
 
