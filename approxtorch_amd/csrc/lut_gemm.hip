@@ -181,6 +181,60 @@ __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
   }
 }
 
+// u8 row operand with one quad of rows and one quad of slots per thread
+// (blockIdx.y = slot quad): the four taps' bytes of the quad are read
+// together (one 4-byte load each when `vec`, as in pack_x_kernel) and
+// written as four 8-byte pieces, so every thread moves 16 elements.
+__global__ void __launch_bounds__(256)
+pack_x_u8_quads_kernel(const uint8_t* __restrict__ x, int N, int K, int L,
+                       uint16_t* __restrict__ xt, int Rpad, bool vec) {
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  if (q >= (Rpad >> 2)) return;
+  const int R = N * L;
+  const int r0 = q << 2;
+  long long base[4];
+  unsigned valid = 0;
+  if (R > 0) {
+    const int rr = min(r0, R - 1);
+    int n = rr / L, l = rr - n * L;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (r0 + e < R) valid |= 1u << e;
+      base[e] = (long long)n * K * L + l;
+      if (++l == L) { l = 0; ++n; }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) base[e] = 0;
+  }
+  const int k4 = blockIdx.y * 4;
+  unsigned v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = k4 | ((q + u) & 3);            // this quad's tap of slot k4 + u
+    const long long kl = (long long)min(k, K - 1) * L;
+    if (vec) {
+      v[u] = (k < K && valid) ? *(const unsigned*)(x + base[0] + kl) : 0u;
+    } else {
+      v[u] = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (k < K && ((valid >> e) & 1u)) v[u] |= (unsigned)x[base[e] + kl] << (8 * e);
+    }
+  }
+  uint16_t* dst = xt + (long long)k4 * Rpad + r0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = k4 | ((q + u) & 3);
+    unsigned off[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      off[e] = (k < K && ((valid >> e) & 1u)) ? row_offset((v[u] >> (8 * e)) & 255u) : 0u;
+    *(uint2*)(dst + (long long)u * Rpad) =
+        make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
+  }
+}
+
 // Strided operands of the plain (torch.mm-layout) LUT GEMM.  Row operand:
 // X[r][k] at X + r*sr + k*sk -> xt[slot][r] = row_offset(index), as pack_x
 // (quads of rows share a tap); column operand: Y[c][k] at Y + c*sc + k*sk ->
@@ -878,12 +932,12 @@ int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad
               "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
   if ((long long)K * Rpad == 0) return ATX_OK;
   ATX_REQUIRE(xt && ((long long)N * L == 0 || xq), "atx_pack_x_u8: null pointer");
-  dim3 grid((unsigned)std::min<long long>(cdiv(Rpad / 4, 256), 1024),
-            (unsigned)std::min(operand_rows(K), 65535));
+  ATX_REQUIRE(operand_rows(K) / 4 <= 65535, "atx_pack_x_u8: K too large");
+  const dim3 grid((unsigned)cdiv(Rpad / 4, 256), (unsigned)(operand_rows(K) / 4));
   const bool vec = L % 4 == 0 && (uintptr_t)xq % 4 == 0;
-  hipLaunchKernelGGL(pack_x_kernel<uint8_t>, grid, dim3(256), 0, stream, xq, N, K,
-                     L, 0, (uint8_t*)nullptr, xt, Rpad, vec);
-  return check_launch("pack_x_kernel<u8>");
+  hipLaunchKernelGGL(pack_x_u8_quads_kernel, grid, dim3(256), 0, stream, xq, N, K, L, xt, Rpad,
+                     vec);
+  return check_launch("pack_x_u8_quads_kernel");
 }
 
 int atx_pack_w_f32(const float* w, int O, int K, int offset, uint8_t* wq,
