@@ -417,6 +417,13 @@ def test_fakequant_rows_matches_fakequant_then_im2col(shape, signed, misalign):
     assert Rpad == Rpad2 and torch.equal(xt, xt2) and torch.equal(mask, m2)
 
 
+def test_fakequant_rows_empty_batch_writes_only_padding():
+    x = torch.zeros(0, 6, 7, 7, device=DEV)
+    mask, (xt, Rpad) = ops.fakequant_rows(x, t(np.array([np.float32(0.5)])), -128, 127, 128)
+    assert mask.shape == x.shape and Rpad == 2048 and tuple(xt.shape) == (8, 2048)
+    assert int(xt.abs().sum()) == 0
+
+
 def test_fakequant_asymmetric_and_per_channel_bitwise():
     x = special_x(3).reshape(20, 1000)
     s, z = np.float32(0.031), np.float32(113)
