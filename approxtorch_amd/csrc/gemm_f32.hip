@@ -1029,8 +1029,9 @@ static int launch_dgrad(const float* go, const uint8_t* wq, const float* tx,
 // (>= 512 blocks); 1x1 unpadded convs take the direct path.  With fewer
 // tiles the col GEMM (M = C*KH*KW) plus col2im is faster: measured on the
 // ResNet-50 3x3 layers at batch 64, a split implicit GEMM took 241 us where
-// the col path takes 198 us (14x14) and 214 us (7x7), while at 56x56 the
-// unsplit implicit GEMM takes 262-290 us against 462 us.
+// the col path takes 198 us (14x14) and 214 us (7x7); at 28x28 (392 tiles)
+// the implicit GEMM takes 255 us against 221 us; at 56x56 the unsplit
+// implicit GEMM takes 262-290 us against 462 us.
 static bool implicit_dgrad(const atx_conv_geom& g, int O) {
   const long long tiles = cdiv((long long)g.N * g.H * g.W, 128) * cdiv(g.C, tile_of(g.C));
   return g.SH == 1 && g.SW == 1 && O % BK == 0 && O > 0 && tiles >= 512 &&

@@ -620,6 +620,8 @@ def test_conv_backward_kernels_tiled(case):
     (GEOMS[2], (3, 40, 11, 12), 72),
     # few output tiles and a long contraction: split into partial slices
     (((1, 1), (1, 1), (0, 0), (1, 1)), (2, 96, 7, 7), 512), (GEOMS[0], (2, 32, 7, 7), 520),
+    # the same with L % 4 == 0: partial slices written as 16-byte column quads
+    (((1, 1), (1, 1), (0, 0), (1, 1)), (2, 96, 8, 8), 512), (GEOMS[0], (2, 32, 8, 8), 520),
     # stride 1 with O % 32 == 0 but few image tiles: col path
     (GEOMS[0], (3, 40, 11, 12), 64), (((5, 5), (1, 1), (0, 0), (1, 1)), (1, 8, 12, 9), 256),
     # stride 1, O % 32 == 0 and >= 512 image tiles: implicit backward-data GEMM
