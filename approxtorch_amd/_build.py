@@ -1,8 +1,10 @@
 """Builds libatx.so (the HIP kernels + C ABI) in-tree for gfx950.
 
 Every translation unit under csrc/ is compiled by hipcc in parallel and
-linked into approxtorch_amd/libatx.so.  The built library travels with the
-source tree; nothing is installed elsewhere.
+linked into approxtorch_amd/libatx.so; the measurement probes under diag/
+go into a separate approxtorch_amd/libatx_diag.so that only bench.py
+--probe-lds loads.  The built libraries travel with the source tree; nothing
+is installed elsewhere.
 """
 import concurrent.futures as cf
 import os
@@ -12,7 +14,9 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
+DIAG = os.path.join(PKG_DIR, "diag")
 LIB_PATH = os.path.join(PKG_DIR, "libatx.so")
+DIAG_LIB_PATH = os.path.join(PKG_DIR, "libatx_diag.so")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
 ARCH = "gfx950"
@@ -28,11 +32,11 @@ COMMON_FLAGS = [
 ]
 
 
-def _sources():
+def _sources(folder):
     out = []
-    for name in sorted(os.listdir(CSRC)):
+    for name in sorted(os.listdir(folder)):
         if name.endswith((".hip", ".cpp")):
-            out.append(os.path.join(CSRC, name))
+            out.append(os.path.join(folder, name))
     return out
 
 
@@ -47,23 +51,30 @@ def _compile(src):
     return obj
 
 
-def build_library(verbose=False):
-    """Compile every source and link libatx.so; returns the library path."""
-    if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
-        raise RuntimeError(f"hipcc not found at {HIPCC}")
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = _sources()
-    workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
-    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB_PATH + ".tmp"
+def _link(objs, path):
+    tmp = path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build_library(verbose=False):
+    """Compile every source, link libatx.so and libatx_diag.so; returns the
+    product library's path."""
+    if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    srcs, diag = _sources(CSRC), _sources(DIAG)
+    workers = min(len(srcs) + len(diag), max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
+        objs = list(ex.map(_compile, srcs + diag))
+    _link(objs[:len(srcs)], LIB_PATH)
+    _link(objs[len(srcs):], DIAG_LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB_PATH} from {len(srcs)} sources and {DIAG_LIB_PATH}",
+              file=sys.stderr)
     return LIB_PATH
 
 

@@ -2,9 +2,10 @@
 
 Importing this package loads the library and registers the reference's op
 schemas under torch.ops.approxtorch (csrc/claude/bgemm_float_claude.cu:281-297,
-bgemm_lre_backward_claude.cu:892-908, quantization.cu:313-325,
-csrc/cuda/bgemm_custom_grad_optimize.cu:590-602), implemented for the CUDA
-dispatch key (PyTorch-ROCm's key for GPU tensors) only, as in the reference.
+bgemm_lre_backward_claude.cu:892-908, gemm.cu:292-307, dwconv_claude.cu:279-285,
+quantization.cu:313-325, csrc/cuda/bgemm_custom_grad_optimize.cu:590-602),
+implemented for the CUDA dispatch key (PyTorch-ROCm's key for GPU tensors)
+only, as in the reference.
 """
 import torch
 
@@ -27,6 +28,25 @@ _SCHEMAS = {
     "bgemm_fake_uint8_forward_cuda_claude_save":
         ("(Tensor x, Tensor w, Tensor lut) -> (Tensor, Tensor, Tensor)",
          ops.bgemm_fake_uint8_claude_save),
+    "gemm_fake_int8_forward_cuda_claude":
+        ("(Tensor A, Tensor B, Tensor lut) -> Tensor", ops.gemm_fake_int8_claude),
+    "gemm_fake_int8_forward_cuda_claude_cfg":
+        ("(Tensor A, Tensor B, Tensor lut, int cfg) -> Tensor", ops.gemm_fake_int8_claude_cfg),
+    "gemm_fake_int8_forward_cuda_claude_save":
+        ("(Tensor A, Tensor B, Tensor lut) -> (Tensor, Tensor, Tensor)",
+         ops.gemm_fake_int8_claude_save),
+    "gemm_fake_uint8_forward_cuda_claude":
+        ("(Tensor A, Tensor B, Tensor lut) -> Tensor", ops.gemm_fake_uint8_claude),
+    "gemm_fake_uint8_forward_cuda_claude_cfg":
+        ("(Tensor A, Tensor B, Tensor lut, int cfg) -> Tensor", ops.gemm_fake_uint8_claude_cfg),
+    "gemm_fake_uint8_forward_cuda_claude_save":
+        ("(Tensor A, Tensor B, Tensor lut) -> (Tensor, Tensor, Tensor)",
+         ops.gemm_fake_uint8_claude_save),
+    "dwconv_fake_int8_claude":
+        ("(Tensor x, Tensor w, Tensor lut, int kh, int kw, int sh, int sw, int ph, int pw, "
+         "int dilh, int dilw) -> (Tensor, Tensor)",
+         lambda x, w, lut, kh, kw, sh, sw, ph, pw, dh, dw: ops.dwconv_fake_int8_claude(
+             x, w, lut, (kh, kw), (sh, sw), (ph, pw), (dh, dw))),
     "im2col_u8":
         ("(Tensor x, int kh, int kw, int sh, int sw, int ph, int pw, int dilh, int dilw) -> Tensor",
          lambda x, kh, kw, sh, sw, ph, pw, dh, dw: ops.im2col_u8(x, (kh, kw), (sh, sw), (ph, pw),
@@ -38,6 +58,15 @@ _SCHEMAS = {
     "bgemm_lre_backward_claude":
         ("(Tensor grad_output, Tensor x, Tensor w, Tensor dx, Tensor dw) -> (Tensor, Tensor)",
          ops.bgemm_lre_backward_claude),
+    "bgemm_lre_backward_claude_cfg":
+        ("(Tensor grad_output, Tensor x, Tensor w, Tensor dx, Tensor dw, int cfg) "
+         "-> (Tensor, Tensor)", ops.bgemm_lre_backward_claude_cfg),
+    "bgemm_lre_backward_claude_im2col":
+        ("(Tensor grad_output, Tensor x, Tensor w, Tensor dx, Tensor dw, int kh, int kw, "
+         "int sh, int sw, int ph, int pw, int dilh, int dilw) -> (Tensor, Tensor)",
+         lambda go, x, w, dx, dw, kh, kw, sh, sw, ph, pw, dh, dwl:
+             ops.bgemm_lre_backward_claude_im2col(go, x, w, dx, dw, (kh, kw), (sh, sw),
+                                                  (ph, pw), (dh, dwl))),
     "bgemm_custom_grad_uint8_dx":
         ("(Tensor X, Tensor W, Tensor dY, Tensor lut) -> Tensor", ops.bgemm_custom_grad_uint8_dx),
     "bgemm_custom_grad_uint8_dw":

@@ -9,7 +9,7 @@ weights) inside these wrappers; callers see the reference's shapes.
 """
 import os
 import threading
-from collections import OrderedDict
+import weakref
 
 import torch
 from torch import Tensor
@@ -21,7 +21,8 @@ __all__ = [
     "lut_image", "bgemm_fake_int8_claude", "bgemm_fake_int8_claude_save",
     "bgemm_fake_uint8_claude", "bgemm_fake_uint8_claude_save", "bgemm_fake_int8_claude_cfg",
     "bgemm_fake_uint8_claude_cfg", "lut_gemm_i32", "im2col_u8", "lut_map", "lut_map_pad",
-    "bgemm_lre_backward_claude", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
+    "bgemm_lre_backward_claude", "bgemm_lre_backward_claude_cfg",
+    "bgemm_lre_backward_claude_im2col", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
     "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "fakequant_per_tensor",
     "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
     "conv_backward_data", "conv_backward_weight", "conv_backward_weight_rows", "col2im",
@@ -33,9 +34,16 @@ __all__ = [
 ]
 
 # --------------------------------------------------------------------- LUTs
-_LUT_CACHE = OrderedDict()
+# Derived device tables (the 16-bit LUT image, LRE / DATE tables) are cached
+# per LUT tensor.  An entry is keyed by everything that determines the bytes a
+# kernel would read -- storage address, offset, shape, strides, version --
+# and holds only a weak reference to the LUT's storage, so it goes stale (and
+# is recomputed) when that memory is freed and its address reused.  The cache is
+# unbounded: a converted ResNet-50 holds one LUT copy per layer after
+# Module.to(), and a bounded LRU smaller than that would miss on every call.
+# Edits that bypass the version counter (through .data) are not seen.
+_LUT_CACHE = {}
 _LUT_LOCK = threading.Lock()
-_LUT_CACHE_MAX = 32
 
 
 def _check_lut(lut, name="lut"):
@@ -47,40 +55,50 @@ def _check_lut(lut, name="lut"):
         raise RuntimeError(f"{name} must have 65536 elements")
 
 
+def _cache_key(kind, lut, param):
+    return (kind, param, lut.data_ptr(), lut.device.index, lut.storage_offset(),
+            tuple(lut.shape), tuple(lut.stride()), lut._version)
+
+
+def _cached(kind, lut, param, make):
+    """make(lut.contiguous()) cached per (LUT tensor, kind, param)."""
+    _check_lut(lut)
+    key = _cache_key(kind, lut, param)
+    storage = lut.untyped_storage()
+    with _LUT_LOCK:
+        hit = _LUT_CACHE.get(key)
+        if hit is not None and hit[0]() is storage:
+            return hit[1]
+    val = make(lut.contiguous())
+    with _LUT_LOCK:
+        for k in [k for k, v in _LUT_CACHE.items() if v[0]() is None]:
+            del _LUT_CACHE[k]
+        _LUT_CACHE[key] = (weakref.ref(storage), val)
+    return val
+
+
 def lut_image(lut: Tensor, transposed: bool = False):
     """(lut16t, lutf32t, class) for an fp32 [65536] LUT, cached per tensor.
 
     The 16-bit transposed image and its class (int16 / uint16 / fp32
-    fallback) are computed once per (storage, version) -- the reference
-    rebuilds them inside every forward (csrc/claude/bgemm_float_claude.cu:161-192).
+    fallback) are computed once per LUT tensor -- the reference rebuilds them
+    inside every forward (csrc/claude/bgemm_float_claude.cu:161-192).
     transposed=True gives the image of the transposed LUT (lut[w][x] roles
     swapped), for a GEMM whose row operand is the LUT's second index.
     """
-    _check_lut(lut)
-    key = (lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset(), transposed)
-    with _LUT_LOCK:
-        hit = _LUT_CACHE.get(key)
-        if hit is not None:
-            _LUT_CACHE.move_to_end(key)
-            return hit
-    lc = lut.contiguous()
-    src = lut                   # kept alive by the cache entry: its pointer is the key
-    if transposed:
-        lc = lc.view(256, 256).t().contiguous().view(-1)
-    dev = lut.device
-    img16 = torch.empty(65536, dtype=torch.int16, device=dev)
-    imgf = torch.empty(65536, dtype=torch.float32, device=dev)
-    flags = torch.zeros(2, dtype=torch.int32, device=dev)
-    L.call("atx_lut_prepare", L.ptr(lc), L.ptr(img16), L.ptr(imgf), L.ptr(flags),
-           L.stream_of(lc))
-    f = flags.tolist()          # one host sync per new LUT
-    cls = L.ATX_LUT_I16 if f[0] == 0 else (L.ATX_LUT_U16 if f[1] == 0 else L.ATX_LUT_F32)
-    val = (img16, imgf, cls, src)
-    with _LUT_LOCK:
-        _LUT_CACHE[key] = val
-        while len(_LUT_CACHE) > _LUT_CACHE_MAX:
-            _LUT_CACHE.popitem(last=False)
-    return val
+    def make(lc):
+        if transposed:
+            lc = lc.view(256, 256).t().contiguous().view(-1)
+        dev = lc.device
+        img16 = torch.empty(65536, dtype=torch.int16, device=dev)
+        imgf = torch.empty(65536, dtype=torch.float32, device=dev)
+        flags = torch.zeros(2, dtype=torch.int32, device=dev)
+        L.call("atx_lut_prepare", L.ptr(lc), L.ptr(img16), L.ptr(imgf), L.ptr(flags),
+               L.stream_of(lc))
+        f = flags.tolist()          # one host sync per new LUT tensor
+        cls = L.ATX_LUT_I16 if f[0] == 0 else (L.ATX_LUT_U16 if f[1] == 0 else L.ATX_LUT_F32)
+        return img16, imgf, cls
+    return _cached("image", lut, bool(transposed), make)
 
 
 # ------------------------------------------------ LUT files and gradient tables
@@ -102,26 +120,6 @@ def parse_text_table(path, integral=False, capacity=1 << 24):
     return out[:int(count[0])].copy()
 
 
-_TABLE_CACHE = OrderedDict()
-
-
-def _cached_tables(kind, lut, param, launch):
-    _check_lut(lut)
-    key = (kind, param, lut.data_ptr(), lut.device.index, lut._version, lut.storage_offset())
-    with _LUT_LOCK:
-        hit = _TABLE_CACHE.get(key)
-        if hit is not None:
-            _TABLE_CACHE.move_to_end(key)
-            return hit[0], hit[1]
-    lc = lut.contiguous()
-    a, b = launch(lc)
-    with _LUT_LOCK:
-        _TABLE_CACHE[key] = (a, b, lut)   # keep the LUT alive: its pointer is the key
-        while len(_TABLE_CACHE) > _LUT_CACHE_MAX:
-            _TABLE_CACHE.popitem(last=False)
-    return a, b
-
-
 def lre_tables(lut: Tensor, qtype: str = "int8"):
     """(grad_a [256], grad_b [256]) LRE slope tables of a CUDA fp32 LUT, on the
     device, cached per LUT (grad_lut.py:14-37; uint8 operands: qtype='uint8')."""
@@ -134,7 +132,7 @@ def lre_tables(lut: Tensor, qtype: str = "int8"):
         gb = torch.empty(256, dtype=torch.float32, device=lc.device)
         L.call("atx_lre_tables", L.ptr(lc), offset, L.ptr(ga), L.ptr(gb), L.stream_of(lc))
         return ga, gb
-    return _cached_tables("lre", lut, offset, launch)
+    return _cached("lre", lut, offset, launch)
 
 
 def date_tables(lut: Tensor, half_ws: int = 32):
@@ -148,13 +146,13 @@ def date_tables(lut: Tensor, half_ws: int = 32):
         gb = torch.empty(65536, dtype=torch.float32, device=lc.device)
         L.call("atx_date_tables", L.ptr(lc), half_ws, L.ptr(ga), L.ptr(gb), L.stream_of(lc))
         return ga, gb
-    return _cached_tables("date", lut, half_ws, launch)
+    return _cached("date", lut, half_ws, launch)
 
 
 # -------------------------------------------------------------- LUT GEMM
 def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None,
           transposed=False):
-    img16, imgf, cls, _ = lut_image(lut, transposed)
+    img16, imgf, cls = lut_image(lut, transposed)
     dev = y.device
     wsb = L.query("atx_lut_gemm_workspace_bytes", N, K, Lc, O) if cls != L.ATX_LUT_F32 else 0
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
@@ -440,7 +438,7 @@ def dwconv_forward(img: Tensor, wq: Tensor, lut: Tensor, g, pad_index: int,
     ascending (i, j); out-of-image taps index pad_index), with the LUT GEMM's
     epilogues (sw / bias per channel).  wq: uint8 [C, KH*KW] indices."""
     imgc = img.contiguous()
-    img16, imgf, cls, _ = lut_image(lut)
+    img16, imgf, cls = lut_image(lut)
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((g.N, g.C, g.OH, g.OW), dtype=ydt, device=imgc.device)
     ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
@@ -602,32 +600,99 @@ def _weight_index(w: Tensor) -> Tensor:
     raise RuntimeError(f"unsupported weight dtype {w.dtype}")
 
 
+def _lre_checks(grad_output, x, w, dx, dw, x_dims):
+    """csrc/claude/bgemm_lre_backward_claude.cu:547-560 / 664-677."""
+    for t, nm in ((grad_output, "grad_output"), (x, "x"), (w, "w"), (dx, "dx"), (dw, "dw")):
+        if not t.is_cuda:
+            raise RuntimeError("all tensors must be CUDA")
+    if not (grad_output.dtype == dx.dtype == dw.dtype == torch.float32):
+        raise RuntimeError("grad_output/dx/dw must be float32")
+    for t, nm in ((x, "x"), (w, "w")):
+        if t.dtype not in (torch.float32, torch.int8, torch.uint8):
+            raise RuntimeError(f"{nm} must be float32, int8 or uint8")
+    if grad_output.dim() != 3:
+        raise RuntimeError("grad_output must have shape [N, O, L]")
+    if x.dim() != x_dims:
+        raise RuntimeError("x must have shape " + ("[N, K, L]" if x_dims == 3 else "[N, C, H, W]"))
+    if w.dim() != 2:
+        raise RuntimeError("w must have shape [K, O]")
+    if dx.numel() != 256:
+        raise RuntimeError("dx must have 256 elements")
+    if dw.numel() != 256:
+        raise RuntimeError("dw must have 256 elements")
+
+
+def _lre_grads(go, x_img, w, dx, dw, g, N, K, Lc, O):
+    """(grad_x [N,K,L] unfolded, grad_w [K,O]) of the LRE estimator:
+    grad_x[n,k,l] = sum_o go[n,o,l] * dx[idx(w[k,o])] and
+    grad_w[k,o] = sum_{n,l} go[n,o,l] * dw[idx(x[n,k,l])], out-of-image taps
+    of the implicit im2col taking dw[128] (the quantized zero)."""
+    dev = go.device
+    if N == 0 or K == 0 or Lc == 0 or O == 0:
+        return (torch.zeros((N, K, Lc), dtype=torch.float32, device=dev),
+                torch.zeros((K, O), dtype=torch.float32, device=dev))
+    wq = _weight_index(w.t().contiguous())                 # [O, K] LUT indices
+    goc = go.contiguous()
+    col = torch.empty((N, K, Lc), dtype=torch.float32, device=dev)
+    L.call("atx_conv_bwd_data_col", L.ptr(goc), L.ptr(wq), L.ptr(dx.contiguous()), N, O, K, Lc,
+           L.ptr(col), L.stream_of(goc))
+    gw = conv_backward_weight(goc, x_img, dw.contiguous(), g, O, 128)
+    return col, gw.t().contiguous()
+
+
 def bgemm_lre_backward_claude(grad_output: Tensor, x: Tensor, w: Tensor, dx: Tensor,
                               dw: Tensor):
     """LRE backward of the LUT BGEMM (csrc/claude/bgemm_lre_backward_claude.cu:539-647):
       grad_x[n,k,l] = sum_o go[n,o,l] * dx[idx(w[k,o])]
       grad_w[k,o]   = sum_{n,l} go[n,o,l] * dw[idx(x[n,k,l])]
     x [N,K,L] and w [K,O] are uint8 indices, int8 values or fp32 values."""
-    for t, nm in ((grad_output, "grad_output"), (x, "x"), (w, "w"), (dx, "dx"), (dw, "dw")):
-        if not t.is_cuda:
-            raise RuntimeError(f"{nm} must be a CUDA tensor")
-    if dx.numel() != 256 or dw.numel() != 256 or dx.dtype != torch.float32 or \
-            dw.dtype != torch.float32:
-        raise RuntimeError("dx and dw must be float32 tables with 256 elements")
-    if x.dim() != 3 or w.dim() != 2 or grad_output.dim() != 3:
-        raise RuntimeError("expected grad_output [N,O,L], x [N,K,L], w [K,O]")
+    _lre_checks(grad_output, x, w, dx, dw, 3)
     N, K, Lc = x.shape
     O = w.size(1)
-    if w.size(0) != K or tuple(grad_output.shape) != (N, O, Lc):
-        raise RuntimeError("shape mismatch between grad_output, x and w")
-    wq = _weight_index(w.t().contiguous())                 # [O, K]
-    go = grad_output.contiguous().float()
-    col = torch.empty((N, K, Lc), dtype=torch.float32, device=go.device)
-    L.call("atx_conv_bwd_data_col", L.ptr(go), L.ptr(wq), L.ptr(dx.contiguous()), N, O, K, Lc,
-           L.ptr(col), L.stream_of(go))
+    if w.size(0) != K:
+        raise RuntimeError("w.shape[0] must equal K")
+    if tuple(grad_output.shape) != (N, O, Lc):
+        raise RuntimeError("grad_output shape must be [N, O, L]")
     g = L.geom(N, K, 1, Lc, 1, 1, 1, 1, 0, 0, 1, 1)
-    gw = conv_backward_weight(go, x.contiguous().view(N, K, 1, Lc), dw.contiguous(), g, O, 128)
-    return col, gw.t().contiguous()
+    return _lre_grads(grad_output, x.contiguous().view(N, K, 1, Lc), w, dx, dw, g, N, K, Lc, O)
+
+
+def bgemm_lre_backward_claude_cfg(grad_output: Tensor, x: Tensor, w: Tensor, dx: Tensor,
+                                  dw: Tensor, cfg: int):
+    """`cfg` chose between the reference's cuBLAS grad_w formulations
+    (csrc/claude/bgemm_lre_backward_claude.cu:545,603-611); the gfx950 MFMA
+    weight-gradient GEMM picks its own split, so it is accepted and ignored."""
+    return bgemm_lre_backward_claude(grad_output, x, w, dx, dw)
+
+
+def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, dx: Tensor,
+                                     dw: Tensor, kernel_size, stride, padding, dilation):
+    """bgemm_lre_backward_claude with x the pre-unfold quantized image
+    [N,C,H,W] (int8 / uint8 / fp32 values): the weight-gradient GEMM reads its
+    im2col indices on the fly, padding taps = index 128
+    (csrc/claude/bgemm_lre_backward_claude.cu:649-733; ops.py:266-275).
+    Returns (grad_x [N, C*kh*kw, L] unfolded, grad_w [C*kh*kw, O])."""
+    _lre_checks(grad_output, x, w, dx, dw, 4)
+    kh, kw = _pair(kernel_size)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw_ = _pair(dilation)
+    if not (kh >= 1 and kw >= 1 and sh >= 1 and sw >= 1 and ph >= 0 and pw >= 0 and dh >= 1
+            and dw_ >= 1):
+        raise RuntimeError("invalid conv geometry")
+    xc = x.contiguous()
+    g = conv_geom(tuple(xc.shape), (kh, kw), (sh, sw), (ph, pw), (dh, dw_))
+    N, K = g.N, g.C * kh * kw
+    O = w.size(1)
+    if w.size(0) != K:
+        raise RuntimeError("w.shape[0] must equal C*kh*kw")
+    if g.OH < 1 or g.OW < 1:
+        raise RuntimeError("conv geometry yields empty output")
+    Lc = g.OH * g.OW
+    if tuple(grad_output.shape) != (N, O, Lc):
+        raise RuntimeError(f"grad_output shape must be [N, O, OH*OW] for this geometry, got "
+                           f"{tuple(grad_output.shape)} expected L={Lc}")
+    return _lre_grads(grad_output, xc, w, dx, dw, g, N, K, Lc, O)
 
 
 # --------------------------------------------------------- custom backward
@@ -684,18 +749,45 @@ def _reduce_ws(dev):
                        device=dev)
 
 
+def require_cuda_f32(t: Tensor, name: str):
+    """The reference's TORCH_CHECK(x.is_cuda() / scalar_type() == kFloat32)
+    (csrc/claude/quantization.cu:190-193): the kernels read fp32 device memory."""
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32, got {t.dtype}")
+
+
+def require_param(p, x: Tensor, name: str, numel: int = 1):
+    """A scale / zero-point operand: fp32, `numel` elements, on x's device
+    (csrc/claude/quantization.cu:190-193,269-274)."""
+    if p is None:
+        return
+    if not p.is_cuda or p.device != x.device:
+        raise RuntimeError(f"{name} must be a CUDA tensor on {x.device}")
+    if p.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32, got {p.dtype}")
+    if p.numel() != numel:
+        what = "a scalar tensor" if numel == 1 else f"a tensor of {numel} elements"
+        raise RuntimeError(f"{name} must be {what}, got {p.numel()} elements")
+
+
 def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
                          want_q=True, q8_dtype=None):
     """(q fp32, mask bool[, q8]) of the fused per-tensor fake-quant
     (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric)."""
+    require_cuda_f32(x, "x")
+    require_param(scale, x, "scale")
+    require_param(zero_point, x, "zero_point")
     if qmin >= qmax:
         raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
     xc = x.contiguous()
     q = torch.empty_like(xc) if want_q else None
     mask = torch.empty(xc.shape, dtype=torch.bool, device=xc.device)
     q8 = torch.empty(xc.shape, dtype=q8_dtype, device=xc.device) if q8_dtype else None
-    L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale), L.ptr(zero_point), qmin,
-           qmax, L.ptr(q), L.ptr(mask), L.ptr(q8), L.stream_of(xc))
+    L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale.contiguous()),
+           L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax,
+           L.ptr(q), L.ptr(mask), L.ptr(q8), L.stream_of(xc))
     return q, mask, q8
 
 
@@ -705,6 +797,11 @@ def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
     operand packing: x [N,K,H,W] -> (mask bool [N,K,H,W], (xt, Rpad)), the
     row-offset operand that fakequant_per_tensor's byte image would give
     through conv_forward's im2col (offset 128: int8 image, 0: uint8)."""
+    require_cuda_f32(x, "x")
+    require_param(scale, x, "scale")
+    require_param(zero_point, x, "zero_point")
+    if x.dim() < 2:
+        raise RuntimeError(f"x must have at least 2 dimensions [N, C, ...], got {x.dim()}")
     if qmin >= qmax:
         raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
     xc = x.contiguous()
@@ -713,8 +810,9 @@ def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
     Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
     mask = torch.empty(xc.shape, dtype=torch.bool, device=xc.device)
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=xc.device)
-    L.call("atx_fakequant_rows", L.ptr(xc), N, K, Lc, L.ptr(scale), L.ptr(zero_point), qmin,
-           qmax, offset, L.ptr(mask), L.ptr(xt), Rpad, L.stream_of(xc))
+    L.call("atx_fakequant_rows", L.ptr(xc), N, K, Lc, L.ptr(scale.contiguous()),
+           L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax, offset,
+           L.ptr(mask), L.ptr(xt), Rpad, L.stream_of(xc))
     return mask, (xt, Rpad)
 
 
@@ -742,11 +840,25 @@ def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int
 
 def fakequant_per_tensor_backward(grad_output: Tensor, mask: Tensor, scale: Tensor,
                                   channels: int = 1, inner: int = 1) -> Tensor:
-    """gx = (mask ? go : 0) / max(scale, 1e-12) (csrc/claude/quantization.cu:223-258)."""
+    """gx = (mask ? go : 0) / max(scale, 1e-12) (csrc/claude/quantization.cu:223-258);
+    scale has one element, or `channels` for a per-channel mask of
+    channels x inner elements."""
+    require_cuda_f32(grad_output, "grad_output")
+    if not mask.is_cuda or mask.device != grad_output.device:
+        raise RuntimeError(f"mask must be a CUDA tensor on {grad_output.device}")
+    if mask.dtype != torch.bool:
+        raise RuntimeError(f"mask must be bool, got {mask.dtype}")
+    if grad_output.shape != mask.shape:
+        raise RuntimeError(f"grad_output/mask shape mismatch: {tuple(grad_output.shape)} vs "
+                           f"{tuple(mask.shape)}")
+    require_param(scale, grad_output, "scale", channels)
+    if channels != 1 and channels * inner != grad_output.numel():
+        raise RuntimeError(f"{channels} channels x {inner} do not cover "
+                           f"{grad_output.numel()} elements")
     go = grad_output.contiguous()
     gx = torch.empty_like(go)
-    L.call("atx_fakequant_bwd", L.ptr(go), L.ptr(mask.contiguous()), go.numel(), L.ptr(scale),
-           channels, inner, L.ptr(gx), L.stream_of(go))
+    L.call("atx_fakequant_bwd", L.ptr(go), L.ptr(mask.contiguous()), go.numel(),
+           L.ptr(scale.contiguous()), channels, inner, L.ptr(gx), L.stream_of(go))
     return gx
 
 
@@ -754,10 +866,15 @@ def fakequant_per_channel(w: Tensor, scale: Tensor, qmin: int, qmax: int, zero_p
                           offset=None, want_wt=False):
     """Per-channel (axis 0) fake-quant of a weight: (q, mask, wq index image,
     wt GEMM operand or None, Opad)."""
+    require_cuda_f32(w, "w")
+    if w.dim() < 1:
+        raise RuntimeError("w must have a channel dimension")
+    O = w.size(0)
+    require_param(scale, w, "scale", O)
+    require_param(zero_point, w, "zero_point", O)
     if qmin >= qmax:
         raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
     wc = w.contiguous()
-    O = wc.size(0)
     inner = wc.numel() // max(O, 1)
     q = torch.empty_like(wc)
     mask = torch.empty(wc.shape, dtype=torch.bool, device=wc.device)
@@ -765,7 +882,8 @@ def fakequant_per_channel(w: Tensor, scale: Tensor, qmin: int, qmax: int, zero_p
         else None
     Opad = L.round_up(max(O, 1), L.COL_TILE)
     wt = torch.empty((inner, Opad), dtype=torch.uint8, device=wc.device) if want_wt else None
-    L.call("atx_fakequant_channel_fwd", L.ptr(wc), O, inner, L.ptr(scale), L.ptr(zero_point),
-           qmin, qmax, offset if offset is not None else 0, L.ptr(q), L.ptr(mask), L.ptr(wq),
-           L.ptr(wt), Opad, L.stream_of(wc))
+    L.call("atx_fakequant_channel_fwd", L.ptr(wc), O, inner, L.ptr(scale.contiguous()),
+           L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax,
+           offset if offset is not None else 0, L.ptr(q), L.ptr(mask), L.ptr(wq), L.ptr(wt),
+           Opad, L.stream_of(wc))
     return q, mask, wq, wt, Opad

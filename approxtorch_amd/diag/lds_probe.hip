@@ -25,9 +25,11 @@
 // Bytes moved per launch = blocks * 512 * iters * 8 * (16, or 8 / 4 for
 // modes 7 / 8).
 
-#include "atx_internal.h"
+#include <hip/hip_runtime.h>
 
-namespace atx {
+#include "../../include/atx_diag.h"
+
+namespace atx_diag {
 
 constexpr int PROBE_BYTES = 65536;
 
@@ -98,18 +100,35 @@ __global__ void __launch_bounds__(512) lds_probe_kernel(int iters, unsigned* out
   out[blockIdx.x * blockDim.x + tid] = acc;
 }
 
-}  // namespace atx
+// int32 add rate: 8 independent chains per lane, 64 v_add_u32 per iteration
+// (inline asm so the adds are neither folded nor vectorized).
+__global__ void __launch_bounds__(512) valu_probe_kernel(int iters, unsigned* out) {
+  unsigned a[8], b[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    a[u] = threadIdx.x + u;
+    b[u] = threadIdx.x * 7u + 3u * u + blockIdx.x;
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[u]) : "v"(b[(u + r) & 7]));
+  }
+  unsigned t = 0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) t += a[u];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
 
-using namespace atx;
+}  // namespace atx_diag
+
+using namespace atx_diag;
 
 extern "C" {
 
-// Launches `blocks` x 512 threads of the probe; the caller times it (events
-// on `stream`).  Bytes moved = blocks * 512 * iters * 8 * {16, 8, 4} (modes
-// 0-6 and 9-10, 7, 8).
 int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream) {
-  ATX_REQUIRE(mode >= 0 && mode <= 10 && blocks > 0 && iters > 0 && out,
-              "atx_lds_probe: bad arguments");
+  if (!(mode >= 0 && mode <= 10 && blocks > 0 && iters > 0 && out)) return (int)hipErrorInvalidValue;
   switch (mode) {
     case 0: hipLaunchKernelGGL(lds_probe_kernel<0>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     case 1: hipLaunchKernelGGL(lds_probe_kernel<1>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
@@ -123,7 +142,13 @@ int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t st
     case 9: hipLaunchKernelGGL(lds_probe_kernel<9>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     default: hipLaunchKernelGGL(lds_probe_kernel<10>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
   }
-  return check_launch("lds_probe_kernel");
+  return (int)hipGetLastError();
+}
+
+int atx_valu_probe(int blocks, int iters, unsigned* out, hipStream_t stream) {
+  if (!(blocks > 0 && iters > 0 && out)) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(valu_probe_kernel, dim3(blocks), dim3(512), 0, stream, iters, out);
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -16,6 +16,25 @@ from ..backend import _lib as L
 from ..backend import ops
 
 
+def _check_stat_inputs(x, *buffers):
+    """The kernels behind the statistic updates read x as fp32 device memory
+    and write the scale buffers in place: check both before any launch (the
+    reference's ops reject the same inputs, csrc/claude/quantization.cu:190-193)."""
+    ops.require_cuda_f32(x, "x")
+    for name, b in buffers:
+        if not b.is_cuda or b.device != x.device or b.dtype != torch.float32:
+            raise RuntimeError(f"buffer {name} must be a float32 CUDA tensor on {x.device}; "
+                               f"move the layer to the input's device first")
+
+
+def _bump(*buffers):
+    """The EMA kernels write the buffers through raw pointers; bump their
+    version counters as torch's in-place copy_() in the reference does, so a
+    backward that saved an earlier value raises instead of reading the new one."""
+    for b in buffers:
+        torch.autograd.graph.increment_version(b)
+
+
 def _ema_coeffs(m):
     # torch evaluates `m * cur + (1 - m) * old` with both python scalars cast
     # to fp32: reproduce those two constants exactly.
@@ -134,6 +153,7 @@ class Conv2d_int8(nn.Module):
         """scale_x <- m * absmax(x)/127 + (1-m) * scale_x (nn/Conv2d_int8.py:137-146).
         The absmax reduction and the EMA run on the device; under DDP the
         statistic is MAX-all-reduced in between so every rank's scale agrees."""
+        _check_stat_inputs(x, ("scale_x", self.scale_x))
         with torch.no_grad():
             xc = x.contiguous()
             stat = torch.empty((), dtype=torch.float32, device=x.device)
@@ -145,15 +165,17 @@ class Conv2d_int8(nn.Module):
                 # no all-reduce in between: the EMA runs in the reduction's last launch
                 L.call("atx_absmax_ema", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), denom,
                        m32, om32, L.ptr(self.scale_x), s)
-                return
-            L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
-            dist.all_reduce(stat, op=dist.ReduceOp.MAX)
-            L.call("atx_ema_absmax_apply", L.ptr(stat), denom, m32, om32,
-                   L.ptr(self.scale_x), s)
+            else:
+                L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
+                dist.all_reduce(stat, op=dist.ReduceOp.MAX)
+                L.call("atx_ema_absmax_apply", L.ptr(stat), denom, m32, om32,
+                       L.ptr(self.scale_x), s)
+        _bump(self.scale_x)
 
     def _update_scale_w(self):
         """Per-channel EMA of absmax(W)/qmax_w; zero channels keep their scale
         (nn/Conv2d_int8.py:148-158)."""
+        _check_stat_inputs(self.weight, ("scale_w", self.scale_w))
         with torch.no_grad():
             w = self.weight.detach().contiguous()
             O = w.size(0)
@@ -161,6 +183,7 @@ class Conv2d_int8(nn.Module):
             L.call("atx_weight_scale_ema", L.ptr(w), O, w.numel() // max(O, 1),
                    float(2 ** (self.weight_bits - 1) - 1), m32, om32, 0,
                    L.ptr(self.scale_w), L.stream_of(w))
+        _bump(self.scale_w)
 
     def _reset_scale_w_from_weight(self):
         """scale_w = absmax(W)/qmax_w per channel (1 for zero channels); runs at
@@ -170,10 +193,12 @@ class Conv2d_int8(nn.Module):
             qmax_w = 2 ** (self.weight_bits - 1) - 1
             w = self.weight.detach()
             if w.is_cuda:
+                _check_stat_inputs(w, ("scale_w", self.scale_w))
                 wc = w.contiguous()
                 O = wc.size(0)
                 L.call("atx_weight_scale_ema", L.ptr(wc), O, wc.numel() // max(O, 1),
                        float(qmax_w), 1.0, 0.0, 1, L.ptr(self.scale_w), L.stream_of(wc))
+                _bump(self.scale_w)
                 return
             absmax = w.abs().amax(dim=tuple(range(1, w.dim())))
             self.scale_w.copy_(torch.where(absmax > 0, absmax / qmax_w, torch.ones_like(absmax)))

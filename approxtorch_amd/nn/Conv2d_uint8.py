@@ -19,7 +19,7 @@ from torch.nn.modules.utils import _pair
 from . import bgemm_uint8, quantization
 from ..backend import _lib as L
 from ..backend import ops
-from .Conv2d_int8 import _ema_coeffs
+from .Conv2d_int8 import _bump, _check_stat_inputs, _ema_coeffs
 
 
 def uint8_qparams(mn, mx, qmax=255):
@@ -185,6 +185,8 @@ class Conv2d_uint8(nn.Module):
     def _update_scale(self, x):
         """min/max EMA of the activations, then qparams, on the device; MIN/MAX
         all-reduce under DDP (nn/Conv2d_uint8.py:225-240)."""
+        _check_stat_inputs(x, ("x_min", self.x_min), ("x_max", self.x_max),
+                           ("scale_x", self.scale_x), ("zero_x", self.zero_x))
         with torch.no_grad():
             xc = x.contiguous()
             mn = torch.empty((), dtype=torch.float32, device=x.device)
@@ -197,16 +199,19 @@ class Conv2d_uint8(nn.Module):
                 L.call("atx_minmax_ema", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn),
                        L.ptr(mx), m32, om32, self.qmax, L.ptr(self.x_min), L.ptr(self.x_max),
                        L.ptr(self.scale_x), L.ptr(self.zero_x), s)
-                return
-            L.call("atx_minmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn), L.ptr(mx), s)
-            dist.all_reduce(mn, op=dist.ReduceOp.MIN)
-            dist.all_reduce(mx, op=dist.ReduceOp.MAX)
-            L.call("atx_ema_minmax_apply", L.ptr(mn), L.ptr(mx), m32, om32, self.qmax,
-                   L.ptr(self.x_min), L.ptr(self.x_max), L.ptr(self.scale_x),
-                   L.ptr(self.zero_x), s)
+            else:
+                L.call("atx_minmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(mn), L.ptr(mx), s)
+                dist.all_reduce(mn, op=dist.ReduceOp.MIN)
+                dist.all_reduce(mx, op=dist.ReduceOp.MAX)
+                L.call("atx_ema_minmax_apply", L.ptr(mn), L.ptr(mx), m32, om32, self.qmax,
+                       L.ptr(self.x_min), L.ptr(self.x_max), L.ptr(self.scale_x),
+                       L.ptr(self.zero_x), s)
+        _bump(self.x_min, self.x_max, self.scale_x, self.zero_x)
 
     def _update_scale_w(self):
         """Per-channel min/max EMA of the weights + qparams (nn/Conv2d_uint8.py:242-255)."""
+        _check_stat_inputs(self.weight, ("w_min", self.w_min), ("w_max", self.w_max),
+                           ("scale_w", self.scale_w), ("zero_w", self.zero_w))
         with torch.no_grad():
             w = self.weight.detach().contiguous()
             O = w.size(0)
@@ -214,6 +219,7 @@ class Conv2d_uint8(nn.Module):
             L.call("atx_weight_minmax_ema", L.ptr(w), O, w.numel() // max(O, 1), m32, om32,
                    self.qmax_w, L.ptr(self.w_min), L.ptr(self.w_max), L.ptr(self.scale_w),
                    L.ptr(self.zero_w), L.stream_of(w))
+        _bump(self.w_min, self.w_max, self.scale_w, self.zero_w)
 
     def forward(self, x: torch.Tensor):
         B, C, H, W = x.shape

@@ -62,10 +62,28 @@ def parse():
 
 
 def lds_probe(torch):
-    """Measured LDS throughput per access pattern (GB/s over the whole GPU)."""
-    from approxtorch_amd.backend import _lib as L
+    """Measured LDS throughput per access pattern (GB/s over the whole GPU)
+    and the int32 VALU add rate (G adds/s), from libatx_diag.so."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "approxtorch_amd", "libatx_diag.so"))
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+    lib.atx_lds_probe.argtypes = [ci, ci, ci, vp, vp]
+    lib.atx_valu_probe.argtypes = [ci, ci, vp, vp]
     blocks, iters = 4 * 256, 2048
     out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def timed(launch):
+        if launch(8) != 0:
+            raise RuntimeError("probe launch failed")
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch(iters)
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e)
+
     res = {}
     for mode, name in ((0, "read_b128_random_128B_row_per_8_lanes"),
                        (1, "read_b128_contiguous_1KiB_per_wave"),
@@ -78,16 +96,11 @@ def lds_probe(torch):
                        (8, "write_b32_contiguous_256B_per_wave"),
                        (9, "read_b128_64B_row_per_4_lanes_rotated_quarters"),
                        (10, "read_b128_64B_row_per_4_lanes_random_quarters")):
-        L.call("atx_lds_probe", mode, blocks, 8, out.data_ptr(), L.stream_of(out))
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        L.call("atx_lds_probe", mode, blocks, iters, out.data_ptr(), L.stream_of(out))
-        e.record()
-        torch.cuda.synchronize()
-        ms = s.elapsed_time(e)
+        ms = timed(lambda it: lib.atx_lds_probe(mode, blocks, it, out.data_ptr(), stream))
         nbytes = {7: 8, 8: 4}.get(mode, 16)
         res[name] = round(blocks * 512 * iters * 8 * nbytes / (ms * 1e-3) / 1e9, 1)
+    ms = timed(lambda it: lib.atx_valu_probe(blocks, it, out.data_ptr(), stream))
+    res["valu_int32_add_G_per_s"] = round(blocks * 512 * iters * 64 / (ms * 1e-3) / 1e9, 1)
     return res
 
 

@@ -376,28 +376,6 @@ int atx_custom_grad_dw(const void* x, const void* w, int is_signed,
                        int L, int O, float* grad_w, float* workspace,
                        hipStream_t stream);
 
-/* ------------------------------------------------------------ diagnostics
- * LDS throughput probe (no reference counterpart: it measures the LDS
- * roofline the LUT GEMM is reported against).  blocks x 512 threads, each
- * lane issuing iters*8 accesses of pattern `mode`:
- *   0 read, one random 128-byte row per 8-lane group;
- *   1 read, 1 KiB contiguous per wave;
- *   2 read, as 0 with the row parity equal to the group parity;
- *   3 read, one random 256-byte row per 16-lane group;
- *   4 read, one random 128-byte row per wave (broadcast);
- *   5 write, the LUT GEMM table-build pattern;
- *   6 write, 1 KiB contiguous per wave;
- *   7 write, 8-byte accesses, 512 B contiguous per wave;
- *   8 write, 4-byte accesses, 256 B contiguous per wave;
- *   9 read, one random 64-byte row per 4-lane group, in quarter (group % 4)
- *     of a 256-byte line;
- *  10 read, as 9 with a random quarter.
- * Bytes moved = blocks * 512 * iters * 8 * {16, 8, 4} (modes 0-6 and 9-10,
- * 7, 8).
- * out: blocks*512 uint32. */
-int atx_lds_probe(int mode, int blocks, int iters, unsigned* out,
-                  hipStream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

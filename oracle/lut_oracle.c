@@ -47,3 +47,36 @@ void oracle_lut_gemm_f32(const uint8_t* xi, const uint8_t* wi, const float* lut,
       }
     }
 }
+
+/* Pair-table ("custom" estimator) gradients of the LUT GEMM in fp64:
+ *   gx[n,k,l] = sum_o go[n,o,l] * dx[xi[n,k,l] * 256 + wi[o,k]]   (ascending o)
+ *   gw[o,k]   = sum_{n,l} go[n,o,l] * dw[xi[n,k,l] * 256 + wi[o,k]]
+ * csrc/naive_cuda/bgemm_custom_grad_naive.cu:28-92 (one output per thread). */
+void oracle_custom_grads_f64(const uint8_t* xi, const uint8_t* wi, const double* go,
+                             const double* dx, const double* dw, int N, int K, int L, int O,
+                             double* gx, double* gw) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < K; ++k) {
+      const uint8_t* x = xi + ((long long)n * K + k) * L;
+      double* g = gx + ((long long)n * K + k) * L;
+      for (int l = 0; l < L; ++l) g[l] = 0.0;
+      for (int o = 0; o < O; ++o) {
+        const double* col = dx + wi[(long long)o * K + k];
+        const double* gr = go + ((long long)n * O + o) * L;
+        for (int l = 0; l < L; ++l) g[l] += gr[l] * col[(int)x[l] << 8];
+      }
+    }
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int o = 0; o < O; ++o)
+    for (int k = 0; k < K; ++k) {
+      const double* col = dw + wi[(long long)o * K + k];
+      double s = 0.0;
+      for (int n = 0; n < N; ++n) {
+        const uint8_t* x = xi + ((long long)n * K + k) * L;
+        const double* gr = go + ((long long)n * O + o) * L;
+        for (int l = 0; l < L; ++l) s += gr[l] * col[(int)x[l] << 8];
+      }
+      gw[(long long)o * K + k] = s;
+    }
+}

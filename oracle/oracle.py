@@ -34,6 +34,7 @@ def _c():
         vp, ci = ctypes.c_void_p, ctypes.c_int
         _lib.oracle_lut_gemm_i64.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp]
         _lib.oracle_lut_gemm_f32.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp]
+        _lib.oracle_custom_grads_f64.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, vp, vp]
     return _lib
 
 
@@ -268,33 +269,48 @@ def weight_minmax_ema(w, w_min, w_max, m, qmax=255):
 
 
 # ----------------------------------------------------------- GEMM gradients
-def gemm_grads(go, xi, wi, kind, tables=None, signed=True):
+def gemm_grads(go, xi, wi, kind, tables=None, signed=True, absolute=False):
     """fp64 gradients of y = sum_k f(xi, wi) for the three estimators.
     STE: nn/bgemm_int8.py:15-25 (values idx-128, or idx for uint8);
     LRE: csrc/naive_cuda/bgeem_lre_navie.cu:28-88 / NAIVE-README:222-232
          (grad_x uses dx[wi], grad_w uses dw[xi]);
     custom: csrc/naive_cuda/bgemm_custom_grad_naive.cu:28-92
-         (dx_lut[xi][wi], dw_lut[xi][wi]).
+         (dx_lut[xi][wi], dw_lut[xi][wi]; evaluated by lut_oracle.c).
+    absolute=True evaluates the same sums over |go| and |tables| (the sum of
+    |terms| of each output, which bounds any fp32 summation order's error).
     Returns grad_x [N,K,L], grad_w [O,K]."""
     go = np.asarray(go, dtype=np.float64)
-    xi = np.asarray(xi, dtype=np.int64)
-    wi = np.asarray(wi, dtype=np.int64)
+    if absolute:
+        go = np.abs(go)
+    xi = np.ascontiguousarray(xi, dtype=np.uint8)
+    wi = np.ascontiguousarray(wi, dtype=np.uint8)
     if kind in ("ste", "lre"):
         if kind == "ste":
             off = 128 if signed else 0
             tx = np.arange(256, dtype=np.float64) - off
             tw = tx
         else:
-            tx = np.asarray(tables[0], dtype=np.float64)
-            tw = np.asarray(tables[1], dtype=np.float64)
-        gx = np.einsum("nol,ok->nkl", go, tx[wi])
-        gw = np.einsum("nol,nkl->ok", go, tw[xi])
+            tx = np.asarray(tables[0], dtype=np.float64).reshape(-1)
+            tw = np.asarray(tables[1], dtype=np.float64).reshape(-1)
+        if absolute:
+            tx, tw = np.abs(tx), np.abs(tw)
+        a = tx[wi.astype(np.int64)]                          # [O, K]
+        gx = np.matmul(a.T[None], go)                        # [N, K, L]
+        b = tw[xi.astype(np.int64)]                          # [N, K, L]
+        gw = np.matmul(go, b.transpose(0, 2, 1)).sum(axis=0)  # [O, K]
         return gx, gw
-    dxl = np.asarray(tables[0], dtype=np.float64).reshape(256, 256)
-    dwl = np.asarray(tables[1], dtype=np.float64).reshape(256, 256)
-    # pairwise tables: index [xi[n,k,l], wi[o,k]]
-    gx = np.einsum("nol,nokl->nkl", go, dxl[xi[:, None, :, :], wi[None, :, :, None]])
-    gw = np.einsum("nol,nokl->ok", go, dwl[xi[:, None, :, :], wi[None, :, :, None]])
+    dxl = np.ascontiguousarray(np.asarray(tables[0], dtype=np.float64).reshape(-1))
+    dwl = np.ascontiguousarray(np.asarray(tables[1], dtype=np.float64).reshape(-1))
+    if absolute:
+        dxl, dwl = np.abs(dxl), np.abs(dwl)
+    go = np.ascontiguousarray(go)
+    N, K, L = xi.shape
+    O = wi.shape[0]
+    gx = np.zeros((N, K, L), dtype=np.float64)
+    gw = np.zeros((O, K), dtype=np.float64)
+    if gx.size and gw.size:
+        _c().oracle_custom_grads_f64(_p(xi), _p(wi), _p(go), _p(dxl), _p(dwl), N, K, L, O,
+                                     _p(gx), _p(gw))
     return gx, gw
 
 
@@ -314,20 +330,27 @@ def conv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weight
     N, _, H, W = x.shape
     OH, OW = out_size(H, W, k, s, p, d)
     y = acc.astype(np.float64) * sc.astype(np.float64)[None, :, None]
+    yabs = np.abs(y)
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float64)[None, :, None]
-    ctx = dict(xi=xi, wi=wi, mx=mx, mw=mw, sc=sc, shape=x.shape, acc=acc)
+        yabs = yabs + np.abs(np.asarray(bias, dtype=np.float64))[None, :, None]
+    # yabs: sum of |terms| of each output (tolerance bound of fp32 evaluations)
+    ctx = dict(xi=xi, wi=wi, mx=mx, mw=mw, sc=sc, shape=x.shape, acc=acc,
+               yabs=yabs.reshape(N, O, OH, OW))
     return y.reshape(N, O, OH, OW), ctx
 
 
-def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d):
+def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d, absolute=False):
     """Gradients of the int8 layer (fp64): the reference's composition of the
     fake-quant STE backward, the conv Function backward (nn/bgemm_int8.py
-    conv level) and the dequant addcmul."""
+    conv level) and the dequant addcmul.  absolute=True gives the sum of
+    |terms| of every gradient element instead (a tolerance bound)."""
     N, O = go.shape[:2]
+    go = np.abs(go) if absolute else go
     g = np.asarray(go, dtype=np.float64).reshape(N, O, -1) * \
         ctx["sc"].astype(np.float64)[None, :, None]
-    gcol, gwq = gemm_grads(g, ctx["xi"], ctx["wi"], kind, tables, signed=True)
+    gcol, gwq = gemm_grads(g, ctx["xi"], ctx["wi"], kind, tables, signed=True,
+                           absolute=absolute)
     gqx = fold(gcol, ctx["shape"], k, s, p, d)
     sx = max(float(f32(scale_x)), 1e-12)
     gx = np.where(ctx["mx"], gqx, 0.0) / sx
@@ -354,11 +377,17 @@ def dwconv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weig
     return np.concatenate(ys, axis=1), ctxs
 
 
-def dwconv_int8_backward(go, ctxs, scale_x, scale_w, kind, tables, k, s, p, d):
+def dwconv_yabs(ctxs):
+    """Sum of |terms| of each depthwise output (tolerance bound)."""
+    return np.concatenate([c["yabs"] for c in ctxs], axis=1)
+
+
+def dwconv_int8_backward(go, ctxs, scale_x, scale_w, kind, tables, k, s, p, d,
+                         absolute=False):
     """Gradients of the depthwise layer: conv_int8_backward per channel."""
     sw = np.asarray(scale_w, dtype=f32).reshape(-1)
     parts = [conv_int8_backward(go[:, c:c + 1], ctxs[c], scale_x, sw[c:c + 1], kind, tables,
-                                k, s, p, d) for c in range(len(ctxs))]
+                                k, s, p, d, absolute) for c in range(len(ctxs))]
     return (np.concatenate([q[0] for q in parts], axis=1),
             np.concatenate([q[1] for q in parts], axis=0),
             np.concatenate([q[2] for q in parts], axis=0))
@@ -380,29 +409,39 @@ def conv_uint8_forward(x, weight, bias, lut, scale_x, zero_x, scale_w, zero_w, k
     wsum = wi.astype(np.float64).sum(axis=1)                 # [O]
     zw = np.asarray(zero_w, dtype=np.float64)
     zxf = float(zero_x)
-    y = lutsum - zw[None, :, None] * xsum[:, None, :] - (zxf * wsum)[None, :, None] \
-        + K * zxf * zw[None, :, None]
+    terms = (lutsum, zw[None, :, None] * xsum[:, None, :], (zxf * wsum)[None, :, None],
+             K * zxf * zw[None, :, None])
+    y = terms[0] - terms[1] - terms[2] + terms[3]
+    yabs = sum(np.abs(v) for v in terms)
     sc = (f32(scale_x) * np.asarray(scale_w, dtype=f32)).astype(f32)
     y = y * sc.astype(np.float64)[None, :, None]
+    yabs = yabs * sc.astype(np.float64)[None, :, None]
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float64)[None, :, None]
+        yabs = yabs + np.abs(np.asarray(bias, dtype=np.float64))[None, :, None]
     N, _, H, W = x.shape
     OH, OW = out_size(H, W, k, s, p, d)
-    ctx = dict(xi=xi, wi=wi, mx=mx, mw=mw, sc=sc, shape=x.shape, zw=zw, zx=zxf)
+    # yabs: sum of |terms| of each output (tolerance bound of fp32 evaluations)
+    ctx = dict(xi=xi, wi=wi, mx=mx, mw=mw, sc=sc, shape=x.shape, zw=zw, zx=zxf,
+               yabs=np.broadcast_to(yabs, (N, O, yabs.shape[2])).reshape(N, O, OH, OW))
     return y.reshape(N, O, OH, OW), ctx
 
 
-def conv_uint8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d):
+def conv_uint8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d, absolute=False):
     """Gradients of the uint8 layer (fp64) including the zero-point terms that
-    autograd adds through xsum / wsum (nn/Conv2d_uint8.py:36-51,308-315)."""
+    autograd adds through xsum / wsum (nn/Conv2d_uint8.py:36-51,308-315).
+    absolute=True gives the sum of |terms| of every gradient element."""
     N, O = go.shape[:2]
+    go = np.abs(go) if absolute else go
     g = np.asarray(go, dtype=np.float64).reshape(N, O, -1) * \
         ctx["sc"].astype(np.float64)[None, :, None]
-    gcol, gwq = gemm_grads(g, ctx["xi"], ctx["wi"], kind, tables, signed=False)
+    gcol, gwq = gemm_grads(g, ctx["xi"], ctx["wi"], kind, tables, signed=False,
+                           absolute=absolute)
+    sign = 1.0 if absolute else -1.0
     # -z_w * xsum  ->  d xu[n,k,l] -= sum_o z_w[o] g[n,o,l]
-    gcol = gcol - np.einsum("o,nol->nl", ctx["zw"], g)[:, None, :]
+    gcol = gcol + sign * np.einsum("o,nol->nl", ctx["zw"], g)[:, None, :]
     # -z_x * wsum  ->  d wu[o,k] -= z_x * sum_{n,l} g[n,o,l]
-    gwq = gwq - ctx["zx"] * g.sum(axis=(0, 2))[:, None]
+    gwq = gwq + sign * ctx["zx"] * g.sum(axis=(0, 2))[:, None]
     gqx = fold(gcol, ctx["shape"], k, s, p, d)
     sx = max(float(f32(scale_x)), 1e-12)
     gx = np.where(ctx["mx"], gqx, 0.0) / sx

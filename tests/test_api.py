@@ -113,7 +113,7 @@ def test_uint8_legacy_state_dict_and_zero_point_validation():
 
 def test_product_path_refuses_cpu_tensors():
     conv = Conv2d_int8(2, 3, 3, LUT)
-    with pytest.raises(RuntimeError, match="GPU"):
+    with pytest.raises(RuntimeError, match="CUDA"):
         conv(torch.randn(1, 2, 5, 5))
 
 

@@ -11,8 +11,8 @@ from approxtorch_amd.backend import _lib as L
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_functions():
-    text = open(os.path.join(ROOT, "include", "atx.h")).read()
+def header_functions(name="atx.h"):
+    text = open(os.path.join(ROOT, "include", name)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return re.findall(r"^(?:int|long long|const char\*)\s+(atx_\w+)\(", text, flags=re.M)
 
@@ -25,6 +25,17 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, n), n
     assert sorted(names) == L.exported_symbols()
     assert lib.atx_version() == 1
+
+
+def test_diag_probes_live_in_their_own_library():
+    """The measurement probes (include/atx_diag.h) are exported by
+    libatx_diag.so and not by the product library."""
+    diag = ctypes.CDLL(os.path.join(ROOT, "approxtorch_amd", "libatx_diag.so"))
+    lib = L.load()
+    names = header_functions("atx_diag.h")
+    assert sorted(names) == ["atx_lds_probe", "atx_valu_probe"]
+    for n in names:
+        assert hasattr(diag, n) and not hasattr(lib, n), n
 
 
 def test_invalid_arguments_return_einval_without_gpu():

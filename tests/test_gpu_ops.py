@@ -149,6 +149,26 @@ def test_lut_gemm_auto_schedule_takes_stream_k_on_resnet_layer(monkeypatch):
     _check_sampled(y, xi, wi, lut, r, 4)
 
 
+def test_lut_gemm_config3_full_shape_sampled():
+    """Config 3 at its headline shape: B=32 x [4096 x 2304] int8 by [2304 x 256],
+    perturbed LUT.  The int32 sums (exact) and the fp32 output of the
+    reference op (bgemm_fake_int8_forward_cuda_claude, the bench path) are
+    checked on 4096 random outputs plus the corners of every tile."""
+    N, K, L, Oc = 32, 2304, 4096, 256
+    r = gen(33)
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(3)["perturbed"]
+    xg, lg = t(xi), t(lut, torch.float32)
+    y = ops.lut_gemm_i32(xg, t(wi), lg).cpu().numpy()
+    _check_sampled(y, xi, wi, lut, r, Oc // 32)
+    del y
+    yf = ops.bgemm_fake_int8_claude(xg, t(wi.astype(np.float32) - 128), lg).cpu().numpy()
+    n, o, l = r.integers(0, N, 4096), r.integers(0, Oc, 4096), r.integers(0, L, 4096)
+    want = _sampled_lut_sums(xi, wi, lut, n, o, l).astype(np.float32)   # correctly rounded
+    assert np.array_equal(yf[n, o, l], want)
+
+
 @pytest.mark.parametrize("lut_name", ["asym", "exact_int8", "trunc4", "u16_c5", "i16_edge"])
 def test_lut_gemm_int32_exact_all_integer_classes(lut_name):
     r = gen(11)

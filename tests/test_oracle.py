@@ -158,6 +158,120 @@ def test_ema_and_qparams_match_torch_bitwise():
     assert np.array_equal(s, sc.numpy()) and np.array_equal(z, zr.numpy())
 
 
+def _torch_qparams(mn, mx, qmax):
+    # nn/Conv2d_uint8.py:11-23, evaluated by torch
+    mn = torch.clamp(mn, max=0.0)
+    mx = torch.clamp(mx, min=0.0)
+    scale = torch.clamp((mx - mn) / qmax, min=1e-12)
+    return scale, torch.round(-mn / scale).clamp(0.0, float(qmax))
+
+
+@pytest.mark.parametrize("m", [0.05, 0.1, 0.3333])
+def test_ema_minmax_matches_reference_torch_expression(m):
+    """oracle.ema_minmax against the reference's own torch statements
+    (nn/Conv2d_uint8.py:225-240): amin/amax, `m * mn + (1 - m) * x_min`,
+    then uint8_qparams -- bitwise, including a range that excludes 0."""
+    for shift in (0.0, 3.0, -3.0):
+        x = (rng.standard_normal(1031).astype(np.float32) * 2 + shift).astype(np.float32)
+        xmin, xmax = np.float32(-0.731), np.float32(1.913)
+        xt = torch.from_numpy(x)
+        tmin = m * xt.amin() + (1 - m) * torch.tensor(xmin)
+        tmax = m * xt.amax() + (1 - m) * torch.tensor(xmax)
+        ts, tz = _torch_qparams(tmin, tmax, 255)
+        nmin, nmax, s, z = O.ema_minmax(x, xmin, xmax, m)
+        assert nmin == tmin.item() and nmax == tmax.item()
+        assert s == ts.item() and z == tz.item()
+
+
+@pytest.mark.parametrize("qmax", [255, 15])
+def test_weight_minmax_ema_matches_reference_torch_expression(qmax):
+    """oracle.weight_minmax_ema against nn/Conv2d_uint8.py:242-255 evaluated
+    by torch (per-channel amin/amax over dims 1.., the same EMA, qparams)."""
+    w = rng.standard_normal((7, 4, 3, 3)).astype(np.float32)
+    w[3] = np.abs(w[3])            # a channel with min > 0
+    w[5] = -np.abs(w[5])           # a channel with max < 0
+    w[6] = 0
+    wmin = rng.standard_normal(7).astype(np.float32)
+    wmax = np.abs(rng.standard_normal(7)).astype(np.float32)
+    m = 0.1
+    wt = torch.from_numpy(w)
+    tmin = m * wt.amin(dim=(1, 2, 3)) + (1 - m) * torch.from_numpy(wmin)
+    tmax = m * wt.amax(dim=(1, 2, 3)) + (1 - m) * torch.from_numpy(wmax)
+    ts, tz = _torch_qparams(tmin, tmax, qmax)
+    a, b, s, z = O.weight_minmax_ema(w, wmin, wmax, m, qmax)
+    for got, want in ((a, tmin), (b, tmax), (s, ts), (z, tz)):
+        assert np.array_equal(got, want.numpy())
+
+
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_weight_scale_reset_matches_reference_torch_expression(bits):
+    """oracle.weight_scale_reset against nn/Conv2d_int8.py:160-167 in torch:
+    where(absmax > 0, absmax / qmax_w, 1), zero channels reset to 1."""
+    w = rng.standard_normal((6, 5, 3, 3)).astype(np.float32)
+    w[1] = 0
+    qmax_w = 2 ** (bits - 1) - 1
+    absmax = torch.from_numpy(w).abs().amax(dim=(1, 2, 3))
+    want = torch.where(absmax > 0, absmax / qmax_w, torch.ones_like(absmax))
+    got = O.weight_scale_reset(w, qmax_w)
+    assert np.array_equal(got, want.numpy())
+    assert got[1] == 1.0
+
+
+def test_quant_index_matches_torch_round_and_clamp():
+    """quant_index = clamp(round-half-even(v) + offset, 0, 255), the index of
+    csrc/claude/bgemm_lut_kernels.cuh:62-67, checked against torch.round /
+    clamp (half-even ties, both clip edges, large magnitudes)."""
+    v = np.concatenate([np.arange(-140, 141, 0.5, dtype=np.float32),
+                        np.array([-1e9, 1e9, -0.5, 0.5, 1.5, 2.5, -2.5, 127.5, -128.5],
+                                 dtype=np.float32),
+                        rng.uniform(-300, 300, 2000).astype(np.float32)])
+    for offset in (128, 0):
+        want = (torch.round(torch.from_numpy(v)).clamp(-1024, 1024) + offset).clamp(0, 255)
+        assert np.array_equal(O.quant_index(v, offset), want.to(torch.uint8).numpy())
+    # NaN maps to the quantized zero (documented choice: the reference's
+    # float->int conversion of NaN is unspecified)
+    assert O.quant_index(np.array([np.nan], dtype=np.float32), 128)[0] == 128
+
+
+def test_lut_map_and_pad_match_torch_take_and_pad():
+    """lut_map = table.take(idx) and lut_map_pad = F.pad(table[idx], value =
+    table[128]) (csrc/claude/bgemm_lre_backward_claude.cu:95-127,276-307)."""
+    table = rng.standard_normal(256).astype(np.float32)
+    idx = rng.integers(0, 256, (2, 3, 5, 7)).astype(np.uint8)
+    tt, it = torch.from_numpy(table), torch.from_numpy(idx.astype(np.int64))
+    assert np.array_equal(O.lut_map(idx, table), tt.take(it).numpy())
+    for p in ((1, 1), (0, 2), (3, 0)):
+        want = F.pad(tt.take(it), (p[1], p[1], p[0], p[0]), value=float(table[128]))
+        assert np.array_equal(O.lut_map_pad(idx, table, p), want.numpy())
+
+
+def test_custom_grads_match_bruteforce_loops():
+    """The C pair-table gradients (lut_oracle.c) against explicit loops over
+    the definition (csrc/naive_cuda/bgemm_custom_grad_naive.cu:28-92) with a
+    non-separable table, which catches swapped table indices or operands."""
+    N, K, L, Oc = 2, 3, 5, 4
+    xi = rng.integers(0, 256, (N, K, L)).astype(np.uint8)
+    wi = rng.integers(0, 256, (Oc, K)).astype(np.uint8)
+    go = rng.standard_normal((N, Oc, L))
+    dxl = rng.standard_normal((256, 256))
+    dwl = rng.standard_normal((256, 256))
+    gx, gw = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl))
+    ax, aw = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl), absolute=True)
+    ex, ew = np.zeros((N, K, L)), np.zeros((Oc, K))
+    bx, bw = np.zeros((N, K, L)), np.zeros((Oc, K))
+    for n in range(N):
+        for k in range(K):
+            for l in range(L):
+                for o in range(Oc):
+                    a, b = int(xi[n, k, l]), int(wi[o, k])
+                    ex[n, k, l] += go[n, o, l] * dxl[a, b]
+                    ew[o, k] += go[n, o, l] * dwl[a, b]
+                    bx[n, k, l] += abs(go[n, o, l] * dxl[a, b])
+                    bw[o, k] += abs(go[n, o, l] * dwl[a, b])
+    for got, want in ((gx, ex), (gw, ew), (ax, bx), (aw, bw)):
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
 def test_lre_tables_closed_form_and_linregress():
     a = np.arange(256) - 128
     ga, gb = O.lre_tables((a[:, None] * a[None, :]).astype(np.float32))
