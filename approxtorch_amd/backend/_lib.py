@@ -19,6 +19,7 @@ c_int, c_ll, c_float, c_vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ct
 ATX_LUT_I16, ATX_LUT_U16, ATX_LUT_F32 = 0, 1, 2
 ATX_OUT_F32, ATX_OUT_I32, ATX_OUT_DEQUANT = 0, 1, 2
 ROW_TILE, COL_TILE = 2048, 32
+NOALLOC_SCRATCH_BYTES = 64 << 20     # ATX_NOALLOC_SCRATCH_BYTES
 
 
 class ConvGeom(ctypes.Structure):
@@ -45,6 +46,8 @@ _SIGS = {
     "atx_lut_gemm_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
     "atx_lut_gemm": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp,
                              c_vp, c_int, GemmEpilogue, c_vp, c_vp, c_vp]),
+    "atx_lut_gemm_noalloc": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int,
+                                     c_vp, c_vp, c_int, GemmEpilogue, c_vp, c_vp]),
     "atx_fakequant_fwd": (c_int, [c_vp, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                   c_vp]),
     "atx_fakequant_rows": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_int, c_int,

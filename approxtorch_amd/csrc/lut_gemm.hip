@@ -50,6 +50,7 @@
 #include "atx_internal.h"
 
 #include <algorithm>
+#include <mutex>
 #include <stdlib.h>
 #include <string.h>
 #include <type_traits>
@@ -850,7 +851,13 @@ constexpr int PLAN_CUS = 256;
 //   cut tile (its 256 KiB slot) + 45 for the clear / finish launches.
 // It is taken when cheaper than the best split-K plan.  ATX_LUT_SCHEDULE
 // (environment: auto | split | stream_k) overrides the choice.
-static Plan make_plan(int N, int K, int L, int O, int kmax) {
+// ws_limit >= 0 caps the workspace: split counts whose int32 partials exceed
+// it are not considered, and neither is stream-K if its slots do; when even
+// the smallest admissible split count (set by the int32-exactness bound)
+// needs more, the plan's splits is -1.
+constexpr long long SK_SLOT_BYTES = (long long)(PLAN_CUS - 1) * RT * OT * 4;
+
+static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit = -1) {
   Plan pl;
   const long long R = (long long)N * L;
   pl.tiles_r = (int)cdiv(R, RT);
@@ -864,20 +871,24 @@ static Plan make_plan(int N, int K, int L, int O, int kmax) {
   const double slice = (double)R * O / 600000.0;
   long long best_kc = cdiv(cdiv(K, smin), TPL) * TPL;
   double best_cost = 0.0;
+  bool found = false;
   for (int S = smin; S <= std::max(smin, 64); ++S) {
     const long long kc = cdiv(cdiv(K, S), TPL) * TPL;
     if (S > smin && kc < 16) break;
     const long long splits = cdiv(K, kc);
+    if (ws_limit >= 0 && splits > 1 && splits * R * O * 4 > ws_limit) continue;
     const double cost = (double)cdiv(tiles * splits, cus) * (double)(kc + 6) +
                         (splits > 1 ? 4.0 + splits * slice : 0.0);
-    if (S == smin || cost < best_cost) { best_kc = kc; best_cost = cost; }
+    if (!found || cost < best_cost) { best_kc = kc; best_cost = cost; found = true; }
   }
+  pl.sk_dp = 0;
+  if (!found) { pl.splits = -1; pl.k_chunk = 1; return pl; }
   pl.k_chunk = (int)std::min<long long>(best_kc, kmax);
   pl.splits = (int)cdiv(K, pl.k_chunk);
-  pl.sk_dp = 0;
   const char* sched = getenv("ATX_LUT_SCHEDULE");
   const int force = !sched ? 0 : !strcmp(sched, "stream_k") ? 1 : !strcmp(sched, "split") ? -1 : 0;
-  if (K <= kmax && tiles % cus != 0 && force >= 0) {
+  if (K <= kmax && tiles % cus != 0 && force >= 0 &&
+      (ws_limit < 0 || SK_SLOT_BYTES <= ws_limit)) {
     const long long rounds = tiles / cus;
     const long long tail = tiles - rounds * cus;
     const long long T = tail * pl.nqt;
@@ -893,6 +904,50 @@ static Plan make_plan(int N, int K, int L, int O, int kmax) {
     }
   }
   return pl;
+}
+
+// ------------------------------------------------ no-allocation scratch
+// Device memory of atx_lut_gemm_noalloc: a file-scope array, one copy per GPU
+// for the life of the process.  Host code never uses its name as an address:
+// the device address of this GPU's copy comes from hipGetSymbolAddress (with
+// that device current) and is cached per device.
+static __device__ __align__(256) unsigned char scratch[ATX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[MAX_DEVICES];
+
+// Address of the current device's scratch array; the stream must belong to
+// the current device (the address is only valid there).
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(ATX_ELAUNCH, "atx_lut_gemm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= MAX_DEVICES)
+    return set_error(ATX_ERANGE, "atx_lut_gemm_noalloc: device %d out of range", dev);
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess)
+      return set_error(ATX_ELAUNCH, "atx_lut_gemm_noalloc: hipStreamGetDevice: %s",
+                       hipGetErrorString(e));
+    if (sdev != dev)
+      return set_error(ATX_EINVAL,
+                       "atx_lut_gemm_noalloc: the stream belongs to device %d, the current "
+                       "device is %d", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(ATX_ELAUNCH, "atx_lut_gemm_noalloc: hipGetSymbolAddress: %s",
+                       hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return ATX_OK;
 }
 
 }  // namespace atx
@@ -1005,15 +1060,24 @@ int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc, 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O) {
   if (N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
   const Plan pl = make_plan(N, K, L, O, KMAX_U16);
-  if (pl.sk_per > 0) return (long long)(PLAN_CUS - 1) * RT * OT * 4;
+  if (pl.sk_per > 0) return SK_SLOT_BYTES;
   if (pl.splits <= 1) return 0;
   return (long long)pl.splits * N * O * L * 4;
 }
 
-int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                 int N, int K, int L, int O, const uint16_t* lut16t,
-                 const float* lutf32t, int lut_class, atx_gemm_epilogue ep,
-                 void* y, void* workspace, hipStream_t stream) {
+}  // extern "C"
+
+namespace atx {
+
+// The body of atx_lut_gemm / atx_lut_gemm_noalloc.  ws_limit < 0: the
+// workspace holds atx_lut_gemm_workspace_bytes() (caller-sized); otherwise
+// the plan is restricted to schedules whose workspace fits ws_limit bytes,
+// and `scratch()` supplies it (called only when a launch needs it).
+template <typename ScratchFn>
+static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N, int K,
+                        int L, int O, const uint16_t* lut16t, const float* lutf32t,
+                        int lut_class, atx_gemm_epilogue ep, void* y, void* workspace,
+                        long long ws_limit, ScratchFn scratch, hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_lut_gemm: negative size");
   const long long R = (long long)N * L;
   ATX_REQUIRE(R <= 0x7fffffffLL - RT, "atx_lut_gemm: N*L too large");
@@ -1050,7 +1114,17 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
     return check_launch("lut_gemm_f32_kernel");
   }
   ATX_REQUIRE(lut16t, "atx_lut_gemm: integer class needs the 16-bit image");
-  const Plan pl = make_plan(N, K, L, O, KMAX_U16);
+  const Plan pl = make_plan(N, K, L, O, KMAX_U16, ws_limit);
+  if (pl.splits < 0)
+    return set_error(ATX_ERANGE,
+                     "atx_lut_gemm_noalloc: K = %d needs %lld bytes of int32 partial sums "
+                     "(R = %lld rows x O = %d), more than the %lld-byte scratch buffer; "
+                     "call atx_lut_gemm with a workspace", K,
+                     (long long)cdiv(K, KMAX_U16) * R * O * 4, R, O, ws_limit);
+  if (ws_limit >= 0 && (pl.sk_per > 0 || pl.splits > 1)) {
+    const int rc = scratch(&workspace);
+    if (rc != ATX_OK) return rc;
+  }
   p.tiles_r = pl.tiles_r; p.tiles_o = pl.tiles_o;
   p.splits = pl.splits; p.k_chunk = pl.k_chunk;
   const long long numel = R * O;
@@ -1102,6 +1176,27 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
                        stream, (const int*)workspace, pl.splits, numel, O, L,
                        ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
   return check_launch("split_reduce_kernel");
+}
+
+}  // namespace atx
+
+extern "C" {
+
+int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                 int N, int K, int L, int O, const uint16_t* lut16t,
+                 const float* lutf32t, int lut_class, atx_gemm_epilogue ep,
+                 void* y, void* workspace, hipStream_t stream) {
+  return lut_gemm_run(xt, Rpad, wt, Opad, N, K, L, O, lut16t, lutf32t, lut_class, ep, y,
+                      workspace, -1, [](void**) { return ATX_OK; }, stream);
+}
+
+int atx_lut_gemm_noalloc(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                         int N, int K, int L, int O, const uint16_t* lut16t,
+                         const float* lutf32t, int lut_class, atx_gemm_epilogue ep,
+                         void* y, hipStream_t stream) {
+  return lut_gemm_run(xt, Rpad, wt, Opad, N, K, L, O, lut16t, lutf32t, lut_class, ep, y,
+                      nullptr, ATX_NOALLOC_SCRATCH_BYTES,
+                      [stream](void** ws) { return noalloc_scratch(stream, ws); }, stream);
 }
 
 }  // extern "C"

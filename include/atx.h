@@ -162,6 +162,26 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
                  atx_gemm_epilogue ep, void* y, void* workspace,
                  hipStream_t stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc.  atx_lut_gemm with the same arguments and results, minus
+ * the workspace: split-K partial sums and stream-K slots live in a
+ * library-owned static device array of ATX_NOALLOC_SCRATCH_BYTES (64 MiB),
+ * one per GPU, held until the process ends.  The schedule is restricted to
+ * those whose workspace fits it (stream-K slots always do; split counts
+ * whose partials would not are skipped, which can change the speed but not
+ * the exact int32 sums); when the int32-exactness bound forces a split that
+ * does not fit (K > 32768 with R*O*4*ceil(K/32768) > 64 MiB) it returns
+ * ATX_ERANGE without launching.  It allocates nothing and calls no
+ * allocating routine.  The stream must belong to the current device.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams, threads) race and must be serialized by the caller. */
+#define ATX_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int atx_lut_gemm_noalloc(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                         int N, int K, int L, int O,
+                         const uint16_t* lut16t, const float* lutf32t, int lut_class,
+                         atx_gemm_epilogue ep, void* y, hipStream_t stream);
+
 /* ------------------------------------------------------------ fake-quant
  * Per-tensor fake-quant, fused: q = clamp(rint(x / max(s,1e-12) [+ z]),
  * qmin, qmax) (NaN passes through), mask = qmin <= v <= qmax on the
