@@ -98,11 +98,11 @@ _SIGS = {
                                          c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_conv_bwd_weight": (c_int, [c_vp, c_vp, c_int, ConvGeom, c_int, c_int, c_vp, c_vp,
                                     c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
-    "atx_custom_grad_dx": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int,
-                                   c_vp, c_vp]),
+    "atx_custom_grad_dx": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int,
+                                   c_int, c_vp, c_vp]),
     "atx_custom_grad_dw_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
-    "atx_custom_grad_dw": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int,
-                                   c_vp, c_vp, c_vp]),
+    "atx_custom_grad_dw": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int,
+                                   c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
 }
 
 _lib = None

@@ -23,7 +23,7 @@ __all__ = [
     "bgemm_fake_uint8_claude_cfg", "lut_gemm_i32", "im2col_u8", "lut_map", "lut_map_pad",
     "bgemm_lre_backward_claude", "bgemm_lre_backward_claude_cfg",
     "bgemm_lre_backward_claude_im2col", "bgemm_custom_grad_uint8_dx", "bgemm_custom_grad_uint8_dw",
-    "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "fakequant_per_tensor",
+    "bgemm_custom_grad_int8_dx", "bgemm_custom_grad_int8_dw", "custom_grads", "pack_rows_u8", "fakequant_per_tensor",
     "fakequant_per_tensor_backward", "fakequant_per_channel", "conv_forward",
     "conv_backward_data", "conv_backward_weight", "conv_backward_weight_rows", "col2im",
     "gemm_fake_int8_claude",
@@ -696,8 +696,53 @@ def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, 
 
 
 # --------------------------------------------------------- custom backward
+def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int, Lc: int,
+                 mask_w=None, scale_w=None):
+    """(grad_x [N,K,L] or None, grad_w [O,K] or None) of the pair-table
+    estimator from the LUT GEMM's row-offset operand (xt, Rpad) and the uint8
+    weight index image wq [O,K]; dx_lut / dw_lut are fp32 [65536] tables
+    indexed [x*256 + w] (None skips that gradient).  mask_w / scale_w fuse
+    the per-channel weight fake-quant STE into grad_w."""
+    xt, Rpad = operand
+    O = wq.size(0)
+    dyc = dy.contiguous()
+    if dyc.dtype != torch.float32 or tuple(dyc.shape) != (N, O, Lc):
+        raise RuntimeError(f"dY must be float32 of shape {(N, O, Lc)}")
+    _, wt, Opad = _pack_w(wq.contiguous(), 0)
+    dev, s = dyc.device, L.stream_of(dyc)
+    gx = gw = None
+    if dx_lut is not None:
+        tab = lut_image(dx_lut)[1]
+        gx = torch.empty((N, K, Lc), dtype=torch.float32, device=dev)
+        L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc), L.ptr(tab),
+               N, K, Lc, O, L.ptr(gx), s)
+    if dw_lut is not None:
+        tab = lut_image(dw_lut)[1]
+        gw = torch.empty((O, K), dtype=torch.float32, device=dev)
+        wsb = L.query("atx_custom_grad_dw_workspace_bytes", N, K, Lc, O)
+        ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
+        L.call("atx_custom_grad_dw", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc), L.ptr(tab),
+               N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w), L.ptr(gw), L.ptr(ws), s)
+    return gx, gw
+
+
+def pack_rows_u8(X: Tensor):
+    """Row-offset operand (xt, Rpad) of a uint8 index image X [N,K,L]."""
+    Xc = X.contiguous()
+    N, K, Lc = Xc.shape
+    Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
+    xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=Xc.device)
+    L.call("atx_pack_x_u8", L.ptr(Xc), N, K, Lc, L.ptr(xt), Rpad, L.stream_of(Xc))
+    return xt, Rpad
+
+
 def _custom(kind, X, W, dY, lut, signed):
+    """The reference's op-level custom-gradient kernels: X [N,K,L], W [O,K]
+    uint8 LUT indices (or int8 values, index v+128), dY [N,O,L] fp32."""
     want = torch.int8 if signed else torch.uint8
+    for t, nm in ((X, "X"), (W, "W"), (dY, "dY"), (lut, "lut")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{nm} must be a CUDA tensor")
     if X.dtype != want or W.dtype != want:
         raise RuntimeError(f"X and W must be {want}")
     if dY.dtype != torch.float32 or lut.dtype != torch.float32 or lut.numel() != 65536:
@@ -708,19 +753,12 @@ def _custom(kind, X, W, dY, lut, signed):
     O = W.size(0)
     if W.size(1) != K or tuple(dY.shape) != (N, O, Lc):
         raise RuntimeError("shape mismatch between X, W and dY")
-    Xc, Wc, dYc, lc = X.contiguous(), W.contiguous(), dY.contiguous(), lut.contiguous()
-    s = L.stream_of(Xc)
-    if kind == "dx":
-        gx = torch.empty((N, K, Lc), dtype=torch.float32, device=Xc.device)
-        L.call("atx_custom_grad_dx", L.ptr(Xc), L.ptr(Wc), int(signed), L.ptr(dYc), L.ptr(lc),
-               N, K, Lc, O, L.ptr(gx), s)
-        return gx
-    gw = torch.empty((O, K), dtype=torch.float32, device=Xc.device)
-    wsb = L.query("atx_custom_grad_dw_workspace_bytes", N, K, Lc, O)
-    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=Xc.device)
-    L.call("atx_custom_grad_dw", L.ptr(Xc), L.ptr(Wc), int(signed), L.ptr(dYc), L.ptr(lc), N, K,
-           Lc, O, L.ptr(gw), L.ptr(ws), s)
-    return gw
+    if signed:
+        X = (X.to(torch.int16) + 128).to(torch.uint8)
+        W = (W.to(torch.int16) + 128).to(torch.uint8)
+    gx, gw = custom_grads(pack_rows_u8(X), W, dY, lut if kind == "dx" else None,
+                          lut if kind == "dw" else None, N, K, Lc)
+    return gx if kind == "dx" else gw
 
 
 def bgemm_custom_grad_uint8_dx(X, W, dY, dx_lut):

@@ -1,188 +1,580 @@
 // Custom (pair-wise 256x256 table) gradients of the LUT GEMM:
-//   grad_x[n,k,l] = sum_o dy[n,o,l] * dx_lut[xi(n,k,l)*256 + wi(o,k)]   (ascending o)
-//   grad_w[o,k]   = sum_{n,l} dy[n,o,l] * dw_lut[xi(n,k,l)*256 + wi(o,k)]
-// Reference: csrc/cuda/bgemm_custom_grad_optimize.cu:30-116 and 136-205
-// (uint8 indices), 315-404 and 419-490 (int8 values, index v+128).
+//   grad_x[n,k,l] = sum_o dy[n,o,l] * DX[xi(n,k,l)][wi(o,k)]
+//   grad_w[o,k]   = sum_{n,l} dy[n,o,l] * DW[xi(n,k,l)][wi(o,k)]
+// Reference: csrc/cuda/bgemm_custom_grad_optimize.cu:30-205 (uint8 indices),
+// 315-490 (int8 values, index v+128): one output per thread, the table
+// gathered through L1 (grad_x) or one column of it staged in shared memory
+// per output (grad_w).
 //
-// The fp32 tables are 256 KiB each (more than the 160 KiB LDS), so entries
-// are gathered through the L1/L2 caches; dy and the index tiles are staged in
-// LDS.  grad_w splits the (n,l) contraction across workgroups and reduces the
-// partial sums in a second kernel.
-
+// Design (LDS-resident expanded tables, the LUT GEMM forward's layout in
+// fp32).  A workgroup (512 threads, 8 waves) owns 2048 rows r = n*L + l; its
+// lanes read the forward's row-offset operand xt [Kpad][Rpad] (no im2col of
+// the saved image).  For a tap k and a tile of 16 channels o it builds the
+// expanded table E[v][o] = T[v][wi(o,k)] (256 rows x 16 fp32 = 16 KiB) from
+// the transposed table T^T (column wi contiguous, L2-resident), four tables
+// to an LDS line with the quarter rotation of the forward, so every 16-byte
+// read (four channels of one row) is conflict-free.  Lane (rg, g) owns 16
+// rows and channels 4g..4g+3 of the tile; at sub-step s of a quad it handles
+// tap 4j + ((rg + s) & 3) for all its rows (the operand's slot rotation).
+//
+//   grad_x: a workgroup owns one quad of taps and loops over the 16-channel
+//           tiles of O (tables of the next tile built while the current one
+//           is read); the 64 accumulators acc[s][row] of a lane collect its
+//           four channels, and the four lanes of a row group are summed with
+//           DPP at the end.
+//   grad_w: a workgroup owns one 16-channel tile and loops over all quads of
+//           taps with its dy values in registers; the lane's partial sums
+//           acc[s][c] are combined over the 16 row groups of a wave with DPP
+//           (register indices chosen so every lane adds the same tap), then
+//           over the waves through LDS in a two-stage pipeline that needs no
+//           extra barrier, and written as one partial slice per row tile;
+//           the slices are summed in a fixed order.
+// The table entries must be finite (padding rows of a partial row tile read
+// table row 0 with dy = 0).
 #include "atx_internal.h"
+#include "atx_tiles.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace atx {
+namespace cg {
 
-constexpr int DX_L = 64, DX_K = 4, DX_O = 64;      // grad_x block tile
-constexpr int DW_O = 16, DW_K = 16, DW_P = 64;     // grad_w block tile
+using namespace tiles;
+constexpr int RT = ATX_ROW_TILE;   // rows per workgroup (2048)
+constexpr int CT = 16;             // channels per table tile
+constexpr int NWAVE = RT / RPW;    // 8
+constexpr int NT = 64 * NWAVE;     // 512 threads
+constexpr int TPL = 4;             // tables per LDS line (quarters)
+constexpr int LINE = 256;          // bytes per LDS line
+constexpr int QTAB = 256 * LINE;   // one quad of tables (64 KiB)
+constexpr int RED1 = NWAVE * 4 * 4 * 16;  // grad_w stage-1 floats per buffer (8 KiB)
+constexpr int RED2 = NWAVE * 64;          // grad_w stage-2 floats per buffer (2 KiB)
+static_assert(CT * 4 == LINE / TPL, "a table row fills one quarter of a line");
 
-template <bool SIGNED>
-__device__ __forceinline__ unsigned idx_of(const void* base, long long i) {
-  if (SIGNED) return (unsigned)((int)((const int8_t*)base)[i] + 128);
-  return (unsigned)((const uint8_t*)base)[i];
+struct Params {
+  const uint16_t* xt; int Rpad;
+  const uint8_t* wt; int Opad;
+  const float* tab;        // transposed pair table: tab[w * 256 + v] = T[v][w]
+  const float* dy;         // [N][O][L]
+  float* out;              // grad_x [N][K][L], or the grad_w slices [tiles_r][O][K]
+  int K, R, L, O;
+  int tiles_r, tiles_o, nq; // nq = quads of taps
+};
+
+// DPP helpers (quad_perm / row_shr controls of the VOP DPP encoding).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
+constexpr int QP_XOR1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int QP_XOR2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int ROW_SHR4 = 0x114, ROW_SHR8 = 0x118, ROW_SHR12 = 0x11C;
 
-template <bool SIGNED>
-__global__ void __launch_bounds__(DX_L * DX_K)
-custom_dx_kernel(const void* __restrict__ x, const void* __restrict__ w,
-                 const float* __restrict__ dy, const float* __restrict__ lut, int K, int L,
-                 int O, float* __restrict__ gx) {
-  __shared__ float sdy[DX_O][DX_L];
-  __shared__ unsigned short sw[DX_O][DX_K];
-  const int n = blockIdx.z;
-  const int k0 = blockIdx.y * DX_K, l0 = blockIdx.x * DX_L;
-  const int tl = threadIdx.x % DX_L, tk = threadIdx.x / DX_L;
-  const int l = l0 + tl, k = k0 + tk;
-  const bool valid = l < L && k < K;
-  const unsigned row = valid ? idx_of<SIGNED>(x, ((long long)n * K + k) * L + l) * 256u : 0u;
-  float acc = 0.0f;
-  for (int ob = 0; ob < O; ob += DX_O) {
-    for (int i = threadIdx.x; i < DX_O * DX_L; i += DX_L * DX_K) {
-      const int oo = i / DX_L, ll = i % DX_L;
-      const int o = ob + oo, lg = l0 + ll;
-      sdy[oo][ll] = (o < O && lg < L) ? dy[((long long)n * O + o) * L + lg] : 0.0f;
+// dy of the lane's rows for a run of channels, through a buffer descriptor
+// over dy (its size is checked below 2^31 bytes on the host).  DyRows holds,
+// per row quad h, the byte offset of dy[n][o_lane][l] for the quad's first
+// row (o_lane = the lane's first channel of tile 0) or, for a quad at or past
+// R, an offset beyond the buffer, which loads 0.  VEC (L % 4 == 0): a quad
+// never straddles two images and is one 16-byte load per channel; otherwise
+// each row of the quad has its own offset.
+template <bool VEC>
+struct DyRows { unsigned off[NQ][VEC ? 1 : RQ]; };
+
+constexpr unsigned DY_OOB = 0x80000000u;
+
+template <bool VEC>
+__device__ __forceinline__ void dy_rows(const Params& p, int r0, int o_lane, DyRows<VEC>& d) {
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    const int rq = r0 + NRG * RQ * h;
+    int n = rq / p.L, l = rq - n * p.L;
+#pragma unroll
+    for (int m = 0; m < (VEC ? 1 : RQ); ++m) {
+      d.off[h][m] = rq + m < p.R
+                        ? (unsigned)((((long long)n * p.O + o_lane) * p.L + l) * 4) : DY_OOB;
+      if (++l == p.L) { l = 0; ++n; }
     }
-    for (int i = threadIdx.x; i < DX_O * DX_K; i += DX_L * DX_K) {
-      const int oo = i / DX_K, kk = i % DX_K;
-      const int o = ob + oo, kg = k0 + kk;
-      sw[oo][kk] = (o < O && kg < K) ? (unsigned short)idx_of<SIGNED>(w, (long long)o * K + kg)
-                                     : (unsigned short)0;
-    }
-    __syncthreads();
-    if (valid) {
-      const int oe = min(DX_O, O - ob);
-      // fused multiply-add, as the reference's contracted acc += dy * lut
-      for (int oo = 0; oo < oe; ++oo) acc = fmaf(sdy[oo][tl], lut[row + sw[oo][tk]], acc);
-    }
-    __syncthreads();
   }
-  if (valid) gx[((long long)n * K + k) * L + l] = acc;
 }
 
-// Partial grad_w over the p-range of split s: ws[s][o][k].
-template <bool SIGNED>
-__global__ void __launch_bounds__(DW_O * DW_K)
-custom_dw_kernel(const void* __restrict__ x, const void* __restrict__ w,
-                 const float* __restrict__ dy, const float* __restrict__ lut, int K, int L,
-                 int O, long long P, long long p_chunk, float* __restrict__ ws) {
-  __shared__ float sdy[DW_P][DW_O];
-  __shared__ unsigned short sx[DW_P][DW_K];
-  const int o0 = blockIdx.y * DW_O, k0 = blockIdx.x * DW_K;
-  const int to = threadIdx.x / DW_K, tk = threadIdx.x % DW_K;
-  const int o = o0 + to, k = k0 + tk;
-  const bool valid = o < O && k < K;
-  const unsigned col = valid ? idx_of<SIGNED>(w, (long long)o * K + k) : 0u;
-  const long long pb = blockIdx.z * p_chunk;
-  const long long pe = std::min<long long>(P, pb + p_chunk);
-  float acc = 0.0f;
-  for (long long p0 = pb; p0 < pe; p0 += DW_P) {
-    for (int i = threadIdx.x; i < DW_P * DW_O; i += DW_O * DW_K) {
-      const int pp = i % DW_P, oo = i / DW_P;
-      const long long p = p0 + pp;
-      float v = 0.0f;
-      if (p < pe && o0 + oo < O) {
-        const long long nn = p / L, ll = p - nn * L;
-        v = dy[(nn * O + o0 + oo) * L + ll];
+// dy of the lane's 16 rows for channels o_lane + ob .. + 3 (ob = tile base,
+// wave-uniform); channels >= O load 0 (valid = number of the lane's four
+// channels below O).
+template <bool VEC>
+__device__ __forceinline__ void load_dy(__amdgpu_buffer_rsrc_t dyr, const DyRows<VEC>& d, int L,
+                                        int ob, int valid, float (&v)[RPL][4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int soff = (ob + c) * L * 4;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      if constexpr (VEC) {
+        const unsigned off = c < valid ? d.off[h][0] : DY_OOB;
+        const float4 f = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(dyr, off, soff, 0));
+        v[RQ * h][c] = f.x; v[RQ * h + 1][c] = f.y; v[RQ * h + 2][c] = f.z;
+        v[RQ * h + 3][c] = f.w;
+      } else {
+#pragma unroll
+        for (int m = 0; m < RQ; ++m)
+          v[RQ * h + m][c] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(dyr, c < valid ? d.off[h][m] : DY_OOB,
+                                                          soff, 0));
       }
-      sdy[pp][oo] = v;
     }
-    for (int i = threadIdx.x; i < DW_P * DW_K; i += DW_O * DW_K) {
-      const int pp = i % DW_P, kk = i / DW_P;
-      const long long p = p0 + pp;
-      unsigned v = 0;
-      if (p < pe && k0 + kk < K) {
-        const long long nn = p / L, ll = p - nn * L;
-        v = idx_of<SIGNED>(x, (nn * K + k0 + kk) * L + ll);
+  }
+}
+
+// Table-build registers: the dwords T^T[w_c][v0], [v0 + 1] of the wave's four
+// channels c (rows v0 = 128 hw + 2 lane and v0 + 1).
+struct Src { float2 d[4]; };
+
+// Four channel indices of the wave's group at tap k (one dword; a vector
+// load, read back with v_readlane -- a scalar load in the loop would drain
+// the LDS counter).
+__device__ __forceinline__ unsigned load_w4(const uint8_t* wcol) {
+  return __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(wcol, 4), 0, 0, 0);
+}
+
+__device__ __forceinline__ void load_src(Src& s, __amdgpu_buffer_rsrc_t tab, unsigned wv,
+                                         int lane, int hw) {
+  const unsigned w4 = __builtin_amdgcn_readfirstlane(wv);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const unsigned wc = (w4 >> (8 * c)) & 255u;
+    s.d[c] = __builtin_bit_cast(
+        float2, __builtin_amdgcn_raw_buffer_load_b64(tab, lane * 8, (int)(wc * 1024u) + hw * 512,
+                                                     0));
+  }
+}
+
+// Writes rows v0 and v0 + 1 (four channels each) of one table at smem + wb.
+__device__ __forceinline__ void write_src(unsigned char* smem, const Src& s, int wb) {
+  *(float4*)(smem + wb) = make_float4(s.d[0].x, s.d[1].x, s.d[2].x, s.d[3].x);
+  *(float4*)(smem + wb + LINE) = make_float4(s.d[0].y, s.d[1].y, s.d[2].y, s.d[3].y);
+}
+
+// The pipelined table stream shared by both kernels: nsteps quads of four
+// tables; table (step, s) is described by `col(step, s, og)` = pointer to the
+// 4 channel indices of wave group og (wt[k][o0 + 4 og]).  `rows(x, step, s)`
+// loads the lane's row offsets of sub-step s of quad `step`; `use(B, S, step,
+// x)` consumes sub-step S of quad `step` from buffer B; `quad_end(step)` runs
+// before each quad's closing barrier and `quad_begin(step)` right after the
+// first sub-step's reads.
+// Prefetch distances: row offsets two sub-steps ahead (four rotating
+// buffers), channel indices two ahead of the table loads they address, the
+// table entries one sub-step ahead of their LDS write.  Loads are issued
+// oldest-consumer first (table entries, indices, row offsets), so the
+// in-order vmcnt wait of each consumer never waits for a younger prefetch.
+template <typename Col, typename Rows, typename Use, typename QEnd, typename QBegin>
+__device__ __forceinline__ void table_stream(unsigned char* smem, const float* tab, int nsteps,
+                                             Col col, Rows rows, Use use, QEnd quad_end,
+                                             QBegin quad_begin) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int og = __builtin_amdgcn_readfirstlane(wave % 4);
+  const int hw = __builtin_amdgcn_readfirstlane(wave / 4);
+  const int wb0 = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
+  const int wb1 = wb0 + QTAB;
+  const __amdgpu_buffer_rsrc_t tabr = buffer_rsrc(tab, 256 * 256 * 4);
+  const int last = 4 * nsteps - 1;
+  auto colq = [&](int t) { return col(std::min(t, last) >> 2, std::min(t, last) & 3, og); };
+
+  XRows xr[TPL];
+  Src src;
+  unsigned w1, w2;                                    // indices of tables sigma+5, sigma+6
+  {
+    Src s4;
+#pragma unroll
+    for (int q = 0; q < TPL; ++q) {
+      load_src(s4, tabr, load_w4(colq(q)), lane, hw);
+      write_src(smem + q * 64, s4, wb0);                 // quad 0 -> buffer 0
+    }
+    load_src(src, tabr, load_w4(colq(TPL)), lane, hw);
+    w1 = load_w4(colq(TPL + 1));
+    w2 = load_w4(colq(TPL + 2));
+    rows(xr[0], 0, 0);
+    rows(xr[1], 0, 1);
+  }
+  __syncthreads();
+
+  auto sub = [&](auto bc, auto sc, int j) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
+    constexpr int S = decltype(sc)::value;
+    const int sigma = TPL * j + S;
+    Src sn;
+    load_src(sn, tabr, w1, lane, hw);                    // table sigma + 5
+    w1 = w2;
+    w2 = load_w4(colq(sigma + 7));
+    if constexpr (S + 2 < TPL) rows(xr[(S + 2) & 3], j, S + 2);
+    else rows(xr[(S + 2) & 3], j + 1, S - 2);
+    __builtin_amdgcn_sched_barrier(0);
+    use(bc, sc, j, xr[S]);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (S == 0) quad_begin(j);
+    write_src(smem + S * 64, src, B ? wb0 : wb1);        // table sigma + 4, other buffer
+    src = sn;
+    if constexpr (S == TPL - 1) {
+      quad_end(j);
+      __syncthreads();
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  for (int j = 0; j < nsteps; j += 2) {
+    sub(I0{}, I0{}, j);
+    sub(I0{}, I1{}, j);
+    sub(I0{}, I2{}, j);
+    sub(I0{}, I3{}, j);
+    if (j + 1 >= nsteps) break;
+    sub(I1{}, I0{}, j + 1);
+    sub(I1{}, I1{}, j + 1);
+    sub(I1{}, I2{}, j + 1);
+    sub(I1{}, I3{}, j + 1);
+  }
+}
+
+// Sub-step read addresses: rg's quarter at sub-step s, the lane's chunk and
+// the buffer bit.
+__device__ __forceinline__ unsigned read_mask(int g, int rg, int s, int b) {
+  return (unsigned)((g << 4) | (((rg + s) & 3) << 6) | (b << 16));
+}
+
+// ----------------------------------------------------------------- grad_x
+template <bool VEC>
+__global__ void __launch_bounds__(NT, 1)
+custom_dx_kernel(const Params p) {
+  __shared__ __align__(16) unsigned char smem[2 * QTAB];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / 4, g = lane % 4;
+  const int lb = logical_block();
+  const int j = lb % p.nq;                 // quad of taps (consecutive blocks: same rows)
+  const int tr = lb / p.nq;                // row tile
+  const int r0 = tr * RT + wave * RPW + rg * RQ;
+  const int xoff = (wave * RPW + rg * RQ) * 2;
+  const int slot_bytes = p.Rpad * 2;
+  const __amdgpu_buffer_rsrc_t xs =
+      buffer_rsrc(p.xt + (long long)tr * RT + (long long)TPL * j * p.Rpad, TPL * slot_bytes);
+
+  float acc[TPL][RPL];
+#pragma unroll
+  for (int s = 0; s < TPL; ++s)
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) acc[s][r] = 0.f;
+  const __amdgpu_buffer_rsrc_t dyr = buffer_rsrc(p.dy, p.R * p.O * 4);
+  DyRows<VEC> dro;
+  dy_rows<VEC>(p, r0, 4 * g, dro);
+  auto valid_of = [&](int t) { return min(4, max(0, p.O - CT * t - 4 * g)); };
+  float dyv[RPL][4];
+  load_dy<VEC>(dyr, dro, p.L, 0, valid_of(0), dyv);
+
+  auto col = [&](int t, int s, int og) {    // tile t, tap 4j + s
+    const int k = std::min(TPL * j + s, p.K - 1);
+    return p.wt + (long long)k * p.Opad + CT * t + 4 * og;
+  };
+  auto rows = [&](XRows& x, int, int s) { load_x(x, xs, xoff, s * slot_bytes); };
+  // Reads of row quad h + 2 are issued before the FMAs of quad h, so at most
+  // two quads of entries (32 registers) are in flight next to the 64
+  // accumulators and 64 dy values.
+  auto use = [&](auto bc, auto sc, int t, const XRows& x) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
+    constexpr int S = decltype(sc)::value;
+    const unsigned gx = read_mask(g, rg, S, B);
+    auto reads = [&](int h, float4 (&e)[RQ]) __attribute__((always_inline)) {
+      const unsigned xd[2] = {x.v[h].x, x.v[h].y};
+#pragma unroll
+      for (int m = 0; m < RQ; ++m)
+        e[m] = *(const float4*)(smem + (((xd[m >> 1] >> (16 * (m & 1))) & 0xffffu) ^ gx));
+    };
+    auto fmas = [&](int h, const float4 (&e)[RQ]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int m = 0; m < RQ; ++m) {
+        float a = acc[S][RQ * h + m];
+        a = fmaf(dyv[RQ * h + m][0], e[m].x, a);
+        a = fmaf(dyv[RQ * h + m][1], e[m].y, a);
+        a = fmaf(dyv[RQ * h + m][2], e[m].z, a);
+        a = fmaf(dyv[RQ * h + m][3], e[m].w, a);
+        acc[S][RQ * h + m] = a;
       }
-      sx[pp][kk] = (unsigned short)v;
+    };
+    float4 e0[RQ], e1[RQ];
+    reads(0, e0);
+    reads(1, e1);
+    __builtin_amdgcn_sched_barrier(0);
+    fmas(0, e0);
+    __builtin_amdgcn_sched_barrier(0);
+    reads(2, e0);
+    __builtin_amdgcn_sched_barrier(0);
+    fmas(1, e1);
+    __builtin_amdgcn_sched_barrier(0);
+    reads(3, e1);
+    __builtin_amdgcn_sched_barrier(0);
+    fmas(2, e0);
+    __builtin_amdgcn_sched_barrier(0);
+    fmas(3, e1);
+    // Pin the FMAs here: left free, the compiler sinks them past the next
+    // sub-steps' loads and the epilogue, which drains the reads in flight.
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) asm volatile("" : "+v"(acc[S][r]));
+  };
+  auto quad_end = [&](int t) {
+    // the next tile's dy (its tables are already in the other buffer); an
+    // unconditional load (the last tile reloads itself), so the new values
+    // can take the old registers
+    const int tn = min(t + 1, p.tiles_o - 1);
+    load_dy<VEC>(dyr, dro, p.L, CT * tn, valid_of(tn), dyv);
+  };
+  auto quad_begin = [&](int) {};
+  table_stream(smem, p.tab, p.tiles_o, col, rows, use, quad_end, quad_begin);
+
+  // sum over the row group's four chunk lanes, then lane g stores slot g
+  // (tap 4j + ((rg + g) & 3)) for its 16 rows
+#pragma unroll
+  for (int s = 0; s < TPL; ++s)
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      float a = acc[s][r];
+      a += dpp<QP_XOR1>(a);
+      a += dpp<QP_XOR2>(a);
+      acc[s][r] = a;
     }
-    __syncthreads();
-    if (valid) {
-      const int pn = (int)std::min<long long>(DW_P, pe - p0);
-      for (int pp = 0; pp < pn; ++pp)
-        acc = fmaf(sdy[pp][to], lut[sx[pp][tk] * 256u + col], acc);
+#pragma unroll
+  for (int s = 0; s < TPL; ++s) {
+    if (s != g) continue;
+    const int k = TPL * j + ((rg + s) & 3);
+    if (k >= p.K) continue;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const int rq = r0 + NRG * RQ * h;
+      if (rq >= p.R) break;
+      int n = rq / p.L, l = rq - n * p.L;
+      if constexpr (VEC) {
+        *(float4*)(p.out + ((long long)n * p.K + k) * p.L + l) =
+            make_float4(acc[s][RQ * h], acc[s][RQ * h + 1], acc[s][RQ * h + 2],
+                        acc[s][RQ * h + 3]);
+      } else {
+#pragma unroll
+        for (int m = 0; m < RQ; ++m) {
+          if (rq + m < p.R) p.out[((long long)n * p.K + k) * p.L + l] = acc[s][RQ * h + m];
+          if (++l == p.L) { l = 0; ++n; }
+        }
+      }
     }
-    __syncthreads();
-  }
-  if (valid) ws[(long long)blockIdx.z * O * K + (long long)o * K + k] = acc;
-}
-
-__global__ void custom_split_sum_kernel(const float* __restrict__ ws, int S, long long numel,
-                                        float* __restrict__ out) {
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel; i += stride) {
-    float a = 0.0f;
-    for (int s = 0; s < S; ++s) a += ws[(long long)s * numel + i];
-    out[i] = a;
   }
 }
 
-static int dw_splits(int O, int K, long long P) {
-  const long long tiles = cdiv(O, DW_O) * cdiv(K, DW_K);
-  long long s = 1;
-  while (tiles * s < 2048 && P / (s * 2) >= 4 * DW_P) s *= 2;
-  return (int)s;
+// ----------------------------------------------------------------- grad_w
+template <bool VEC>
+__global__ void __launch_bounds__(NT, 1)
+custom_dw_kernel(const Params p) {
+  __shared__ __align__(16) unsigned char smem[2 * QTAB];
+  __shared__ float red1[2][RED1];          // [buf][wave][row q][g][tap][c]
+  __shared__ float red2[2][RED2];          // [buf][wave][tap * 16 + o_local]
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / 4, g = lane % 4;
+  const int lb = logical_block();
+  const int to = lb % p.tiles_o;           // channel tile (consecutive blocks: same rows)
+  const int tr = lb / p.tiles_o;           // row tile
+  const int r0 = tr * RT + wave * RPW + rg * RQ;
+  const int xoff = (wave * RPW + rg * RQ) * 2;
+  const int slot_bytes = p.Rpad * 2;
+  const uint16_t* xtile = p.xt + (long long)tr * RT;
+  float* slice = p.out + (long long)tr * p.O * p.K;
+
+  float dyv[RPL][4];
+  {
+    DyRows<VEC> dro;
+    dy_rows<VEC>(p, r0, 4 * g, dro);
+    load_dy<VEC>(buffer_rsrc(p.dy, p.R * p.O * 4), dro, p.L, CT * to,
+                 min(4, max(0, p.O - CT * to - 4 * g)), dyv);
+  }
+  float acc[TPL][4];
+
+  auto col = [&](int j, int s, int og) {   // quad j, tap 4j + s
+    const int k = std::min(TPL * j + s, p.K - 1);
+    return p.wt + (long long)k * p.Opad + CT * to + 4 * og;
+  };
+  auto rows = [&](XRows& x, int j, int s) {
+    load_x(x, buffer_rsrc(xtile + (long long)TPL * j * p.Rpad, j < p.nq ? TPL * slot_bytes : 0),
+           xoff, s * slot_bytes);
+  };
+  auto use = [&](auto bc, auto sc, int, const XRows& x) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
+    constexpr int S = decltype(sc)::value;
+    const unsigned gx = read_mask(g, rg, S, B);
+    // all 16 reads in flight, then the FMAs in row order as they arrive
+    float4 e[RPL];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const unsigned xd[2] = {x.v[h].x, x.v[h].y};
+#pragma unroll
+      for (int m = 0; m < RQ; ++m)
+        e[RQ * h + m] =
+            *(const float4*)(smem + (((xd[m >> 1] >> (16 * (m & 1))) & 0xffffu) ^ gx));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      a[0] = fmaf(dyv[r][0], e[r].x, a[0]);
+      a[1] = fmaf(dyv[r][1], e[r].y, a[1]);
+      a[2] = fmaf(dyv[r][2], e[r].z, a[2]);
+      a[3] = fmaf(dyv[r][3], e[r].w, a[3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      asm volatile("" : "+v"(a[c]));   // keep the FMAs in this sub-step (see grad_x)
+      acc[S][c] = a[c];
+    }
+  };
+  // Stage 1 (end of quad j): lane (rg, g) holds tap (rg + s) & 3 in slot s.
+  // In a 16-lane DPP row the lanes of chunk g are rg = 4q..4q+3; lane
+  // rg & 3 == 3 adds, for tap t, its own slot (t + 1) & 3 and the slots
+  // (t + 2) & 3, (t + 3) & 3, t of the lanes 4, 8, 12 below it (the same tap)
+  // and stores the row's sums.
+  auto quad_end = [&](int j) {
+    float out[TPL][4];
+#pragma unroll
+    for (int t = 0; t < TPL; ++t)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        out[t][c] = acc[(t + 1) & 3][c] + dpp<ROW_SHR4>(acc[(t + 2) & 3][c]) +
+                    dpp<ROW_SHR8>(acc[(t + 3) & 3][c]) + dpp<ROW_SHR12>(acc[t][c]);
+    if ((rg & 3) == 3) {
+      float* d = &red1[j & 1][((wave * 4 + (rg >> 2)) * 4 + g) * 16];
+#pragma unroll
+      for (int t = 0; t < TPL; ++t)
+        *(float4*)(d + 4 * t) = make_float4(out[t][0], out[t][1], out[t][2], out[t][3]);
+    }
+  };
+  // Stage 2 (quad j + 1): thread (part w', output i) sums wave w''s four row
+  // partials of output i = tap * 16 + o_local.  Stage 3 (quad j + 2): wave 0
+  // sums the eight parts and stores the slice entry.
+  auto stage2 = [&](int j) {
+    const int i = tid & 63, w = tid >> 6;
+    const int t = i >> 4, ol = i & 15;
+    const float* s1 = &red1[j & 1][(w * 4 * 4 + (ol >> 2)) * 16 + 4 * t + (ol & 3)];
+    red2[j & 1][w * 64 + i] = s1[0] + s1[4 * 16] + s1[8 * 16] + s1[12 * 16];
+  };
+  auto stage3 = [&](int j) {
+    if (tid >= 64) return;
+    const int t = tid >> 4, ol = tid & 15;
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) a += red2[j & 1][w * 64 + tid];
+    const int k = TPL * j + t, o = CT * to + ol;
+    if (k < p.K && o < p.O) slice[(long long)o * p.K + k] = a;
+  };
+  auto quad_begin = [&](int j) {
+    if (j >= 1) stage2(j - 1);
+    if (j >= 2) stage3(j - 2);
+  };
+  table_stream(smem, p.tab, p.nq, col, rows, use, quad_end, quad_begin);
+  // drain the last two quads through stages 2 and 3
+  if (p.nq >= 2) stage3(p.nq - 2);
+  stage2(p.nq - 1);
+  __syncthreads();
+  stage3(p.nq - 1);
 }
 
+// grad_x of a contraction over no channels.
+__global__ void zero_fill_kernel(float* __restrict__ out, long long n) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    out[i] = 0.f;
+}
+
+}  // namespace cg
 }  // namespace atx
 
 using namespace atx;
 
+static int custom_params(cg::Params& p, const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                         const float* dy, const float* tabT, int N, int K, int L, int O,
+                         float* out, const char* who) {
+  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "%s: negative size", who);
+  const long long R = (long long)N * L;
+  ATX_REQUIRE(R <= 0x7fffffffLL - cg::RT, "%s: N*L too large", who);
+  ATX_REQUIRE(Rpad >= R && Rpad % cg::RT == 0, "%s: bad Rpad %d", who, Rpad);
+  if ((long long)Rpad > (1LL << 27))
+    return set_error(ATX_ERANGE, "%s: Rpad %d exceeds 2^27 rows", who, Rpad);
+  ATX_REQUIRE(Opad >= O && Opad % ATX_COL_TILE == 0, "%s: bad Opad %d", who, Opad);
+  p = cg::Params{};
+  p.xt = xt; p.Rpad = Rpad; p.wt = wt; p.Opad = Opad; p.tab = tabT; p.dy = dy; p.out = out;
+  p.K = K; p.R = (int)R; p.L = L; p.O = O;
+  if (R * O * 4 > 0x7fffffffLL)
+    return set_error(ATX_ERANGE, "%s: dy of %lld x %d fp32 exceeds 2 GiB", who, R, O);
+  p.tiles_r = (int)cdiv(R, cg::RT);
+  p.tiles_o = (int)cdiv(O, cg::CT);
+  p.nq = (int)cdiv(K, cg::TPL);
+  return ATX_OK;
+}
+
 extern "C" {
 
-int atx_custom_grad_dx(const void* x, const void* w, int is_signed, const float* dy,
-                       const float* dx_lut, int N, int K, int L, int O, float* grad_x,
-                       hipStream_t stream) {
-  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_custom_grad_dx: negative size");
-  if ((long long)N * K * L == 0) return ATX_OK;
-  ATX_REQUIRE(x && dx_lut && grad_x && (O == 0 || (w && dy)), "atx_custom_grad_dx: null");
-  ATX_REQUIRE(N <= 65535 && cdiv(K, DX_K) <= 65535, "atx_custom_grad_dx: grid too large");
-  dim3 grid((unsigned)cdiv(L, DX_L), (unsigned)cdiv(K, DX_K), (unsigned)N);
-  if (is_signed)
-    hipLaunchKernelGGL(custom_dx_kernel<true>, grid, dim3(DX_L * DX_K), 0, stream, x, w, dy,
-                       dx_lut, K, L, O, grad_x);
+int atx_custom_grad_dx(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* dy, const float* tabT, int N, int K, int L, int O,
+                       float* grad_x, hipStream_t stream) {
+  cg::Params p;
+  int rc = custom_params(p, xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, grad_x,
+                         "atx_custom_grad_dx");
+  if (rc != ATX_OK) return rc;
+  const long long numel = (long long)N * K * L;
+  if (numel == 0) return ATX_OK;
+  ATX_REQUIRE(grad_x, "atx_custom_grad_dx: null output");
+  if (O == 0) {
+    hipLaunchKernelGGL(cg::zero_fill_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0, stream,
+                       grad_x, numel);
+    return check_launch("zero_fill_kernel");
+  }
+  ATX_REQUIRE(xt && wt && dy && tabT, "atx_custom_grad_dx: null operand");
+  const long long blocks = (long long)p.tiles_r * p.nq;
+  ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dx: grid too large");
+  if (L % 4 == 0)
+    hipLaunchKernelGGL(cg::custom_dx_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL(custom_dx_kernel<false>, grid, dim3(DX_L * DX_K), 0, stream, x, w, dy,
-                       dx_lut, K, L, O, grad_x);
+    hipLaunchKernelGGL(cg::custom_dx_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
   return check_launch("custom_dx_kernel");
 }
 
 long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O) {
   if (N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
-  return (long long)dw_splits(O, K, (long long)N * L) * O * K * 4;
+  return cdiv((long long)N * L, cg::RT) * O * K * 4;
 }
 
-int atx_custom_grad_dw(const void* x, const void* w, int is_signed, const float* dy,
-                       const float* dw_lut, int N, int K, int L, int O, float* grad_w,
+int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* dy, const float* tabT, int N, int K, int L, int O,
+                       const uint8_t* mask_w, const float* scale_w, float* grad_w,
                        float* workspace, hipStream_t stream) {
-  ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_custom_grad_dw: negative size");
+  cg::Params p;
+  int rc = custom_params(p, xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, workspace,
+                         "atx_custom_grad_dw");
+  if (rc != ATX_OK) return rc;
   const long long numel = (long long)O * K;
   if (numel == 0) return ATX_OK;
-  ATX_REQUIRE(w && dw_lut && grad_w, "atx_custom_grad_dw: null pointer");
-  const long long P = (long long)N * L;
-  if (P == 0) {
-    hipLaunchKernelGGL(custom_split_sum_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
-                       stream, (const float*)nullptr, 0, numel, grad_w);
-    return check_launch("custom_split_sum_kernel");
-  }
-  ATX_REQUIRE(x && dy && workspace, "atx_custom_grad_dw: null operand/workspace");
-  const int S = dw_splits(O, K, P);
-  const long long chunk = cdiv(cdiv(P, S), DW_P) * DW_P;
-  const int Sreal = (int)cdiv(P, chunk);
-  dim3 grid((unsigned)cdiv(K, DW_K), (unsigned)cdiv(O, DW_O), (unsigned)Sreal);
-  if (is_signed)
-    hipLaunchKernelGGL(custom_dw_kernel<true>, grid, dim3(DW_O * DW_K), 0, stream, x, w, dy,
-                       dw_lut, K, L, O, P, chunk, workspace);
+  ATX_REQUIRE(grad_w && !(mask_w && !scale_w), "atx_custom_grad_dw: null output / scale");
+  if (p.R == 0)
+    return launch_split_sum(nullptr, 0, numel, K, mask_w, scale_w, grad_w, stream);
+  ATX_REQUIRE(xt && wt && dy && tabT && workspace, "atx_custom_grad_dw: null operand");
+  const long long blocks = (long long)p.tiles_r * p.tiles_o;
+  ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dw: grid too large");
+  if (L % 4 == 0)
+    hipLaunchKernelGGL(cg::custom_dw_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL(custom_dw_kernel<false>, grid, dim3(DW_O * DW_K), 0, stream, x, w, dy,
-                       dw_lut, K, L, O, P, chunk, workspace);
-  int rc = check_launch("custom_dw_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL(custom_split_sum_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0, stream,
-                     workspace, Sreal, numel, grad_w);
-  return check_launch("custom_split_sum_kernel");
+    hipLaunchKernelGGL(cg::custom_dw_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
+  rc = check_launch("custom_dw_kernel");
+  if (rc != ATX_OK) return rc;
+  return launch_split_sum(workspace, p.tiles_r, numel, K, mask_w, scale_w, grad_w, stream);
 }
 
 }  // extern "C"

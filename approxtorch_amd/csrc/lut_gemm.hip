@@ -48,6 +48,7 @@
 // 16-bit LUT gathered through L1 and fp32 accumulation.
 
 #include "atx_internal.h"
+#include "atx_tiles.h"
 
 #include <algorithm>
 #include <mutex>
@@ -315,16 +316,6 @@ __global__ void pack_w_kernel(const T* __restrict__ w, int O, int K, int offset,
 }
 
 // ------------------------------------------------------------- main kernel
-__device__ __forceinline__ int logical_block() {
-  // Blocks are dispatched round-robin over the 8 XCDs (bid % 8).  Give each
-  // XCD a contiguous range of logical tiles so tiles sharing an activation
-  // row tile (consecutive logical ids) share that XCD's L2.
-  const int bid = blockIdx.x, nb = gridDim.x;
-  const int q = nb >> 3, rem = nb & 7;
-  const int xcd = bid & 7, slot = bid >> 3;
-  return xcd < rem ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
-}
-
 template <bool SIGNED>
 __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
   const unsigned d[4] = {e.x, e.y, e.z, e.w};
@@ -343,20 +334,6 @@ __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
 // Table-build registers: the LUT16T dwords (entries v0, v0+1) of the wave's
 // eight channels.
 struct Rows { unsigned d[8]; };
-// Row offsets of the lane's quads: v[h] = rows NRG*RQ*h + 4rg + 0..3, two per
-// dword.
-struct XRows { uint2 v[NQ]; };
-
-// Raw buffer descriptor (word 3 of the gfx9-family descriptor: 32-bit
-// elements, no swizzle) over `bytes` bytes at a wave-uniform base.  Buffer
-// loads take the per-step offsets in scalar registers, so the loads below
-// cost no per-lane 64-bit address arithmetic; accesses at or beyond `bytes`
-// return 0 without touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
-                                           0x00020000);
-}
-
 // Eight weight indices (channels o0 + 8*og .. +7) at k, wcol = &wt[k][o0 +
 // 8*og].  Lane parity picks the dword (indices 0-3 / 4-7) so the load is a
 // vector load: a scalar load would share the LDS wait counter and,
@@ -377,17 +354,6 @@ __device__ __forceinline__ void load_rows(Rows& r, __amdgpu_buffer_rsrc_t lut, u
     const unsigned wc = ((c < 4 ? w_lo : w_hi) >> (8 * (c & 3))) & 255u;
     r.d[c] = __builtin_amdgcn_raw_buffer_load_b32(lut, lane * 4, (int)(wc * 512u) + sbase, 0);
   }
-}
-
-// Row offsets of the lane's quads from slot soff / (2 Rpad) of a quad's
-// row-offset block (xs = descriptor over the quad's four slots of the tile,
-// voff = byte offset of the lane's first quad within a slot).
-__device__ __forceinline__ void load_x(XRows& x, __amdgpu_buffer_rsrc_t xs, int voff,
-                                       int soff) {
-#pragma unroll
-  for (int h = 0; h < NQ; ++h)
-    x.v[h] = __builtin_bit_cast(
-        uint2, __builtin_amdgcn_raw_buffer_load_b64(xs, voff + 2 * NRG * RQ * h, soff, 0));
 }
 
 // Writes the lane's two 16-byte chunks (rows v0 and v0+1, channels

@@ -107,8 +107,11 @@ class _bgemm_int8_custom(Function):
     @staticmethod
     def backward(ctx, grad_output):
         xq, wq, dx_lut, dw_lut = ctx.saved_tensors
-        grad_x = ops.bgemm_custom_grad_uint8_dx(xq, wq, grad_output, dx_lut)
-        grad_w = ops.bgemm_custom_grad_uint8_dw(xq, wq, grad_output, dw_lut)
+        N, K, L = xq.shape
+        grad_x, grad_w = ops.custom_grads(
+            ops.pack_rows_u8(xq), wq, grad_output,
+            dx_lut if ctx.needs_input_grad[0] else None,
+            dw_lut if ctx.needs_input_grad[1] else None, N, K, L)
         return grad_x, grad_w, None, None, None
 
 
@@ -297,7 +300,10 @@ def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin
 
 class _conv2d_int8_custom(Function):
     """Conv wrapper of the pair-wise custom-gradient kernels
-    (nn/bgemm_int8.py:87-123): saves the unfolded uint8 index image."""
+    (nn/bgemm_int8.py:87-123).  The reference saves the unfolded uint8 index
+    image; here the forward's row-offset operand (the implicit im2col's
+    output, padded taps at index 128) is saved and read by the gradient
+    kernels directly."""
 
     @staticmethod
     def forward(ctx, x, w, lut, dx_lut, dw_lut, geom):
@@ -305,19 +311,19 @@ class _conv2d_int8_custom(Function):
         if groups != 1:
             raise NotImplementedError("custom gradient currently supports only groups=1")
         g, _ = _conv_setup(x, w, geom)
-        y, wq = ops.conv_forward(x, w, lut, g, 128, 128)
-        xu8 = ops.im2col_u8(x.detach(), kernel_size, stride, padding, dilation)
-        ctx.save_for_backward(xu8, wq, dx_lut, dw_lut)
-        ctx.g = g
+        y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 128, 128, return_operand=True)
+        ctx.save_for_backward(xt, wq, dx_lut, dw_lut)
+        ctx.g, ctx.rpad = g, Rpad
         return y
 
     @staticmethod
     def backward(ctx, grad_output):
-        xq, wq, dx_lut, dw_lut = ctx.saved_tensors
-        go = grad_output.contiguous()
-        grad_x_col = ops.bgemm_custom_grad_uint8_dx(xq, wq, go, dx_lut)
-        grad_w = ops.bgemm_custom_grad_uint8_dw(xq, wq, go, dw_lut)
-        grad_x = ops.col2im(grad_x_col, ctx.g)
+        xt, wq, dx_lut, dw_lut = ctx.saved_tensors
+        g = ctx.g
+        grad_col, grad_w = ops.custom_grads(
+            (xt, ctx.rpad), wq, grad_output, dx_lut if ctx.needs_input_grad[0] else None,
+            dw_lut if ctx.needs_input_grad[1] else None, g.N, g.C * g.KH * g.KW, g.OH * g.OW)
+        grad_x = ops.col2im(grad_col, g) if grad_col is not None else None
         return grad_x, grad_w, None, None, None, None
 
 

@@ -79,8 +79,11 @@ class _bgemm_uint8_custom(Function):
     @staticmethod
     def backward(ctx, grad_output):
         xq, wq, dx_lut, dw_lut = ctx.saved_tensors
-        grad_x = ops.bgemm_custom_grad_uint8_dx(xq, wq, grad_output, dx_lut)
-        grad_w = ops.bgemm_custom_grad_uint8_dw(xq, wq, grad_output, dw_lut)
+        N, K, L = xq.shape
+        grad_x, grad_w = ops.custom_grads(
+            ops.pack_rows_u8(xq), wq, grad_output,
+            dx_lut if ctx.needs_input_grad[0] else None,
+            dw_lut if ctx.needs_input_grad[1] else None, N, K, L)
         return grad_x, grad_w, None, None, None
 
 
@@ -172,35 +175,29 @@ def conv2d_uint8_lre(x, w, lut, dx, dw, zero_x, geom):
 
 
 class _conv2d_uint8_custom(_conv2d_uint8_base):
+    """Pair-table gradients of the uint8 conv: the forward's row-offset
+    operand (padded taps at the device zero point z_x) is saved and read by
+    the gradient kernels; the reference pads with z_x, unfolds and saves the
+    uint8 index image (nn/Conv2d_uint8.py:283-294, nn/bgemm_uint8.py:89-114)."""
 
     @staticmethod
     def forward(ctx, x, w, lut, dx_lut, dw_lut, zero_x, geom):
-        y, wq = _conv2d_uint8_base._forward(ctx, x, w, lut, zero_x, geom)
-        # unfolded uint8 index image with the zero point at padded taps
-        kernel_size, stride, padding, dilation, _ = geom
-        xpad = _pad_with(x.detach(), padding, zero_x)
-        xu = ops.im2col_u8(xpad.to(torch.uint8), kernel_size, stride, 0, dilation)
-        ctx.save_for_backward(xu, wq, dx_lut, dw_lut)
+        g = _geom(x, geom)
+        y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 0, 0, pad_dev=zero_x,
+                                             return_operand=True)
+        ctx.g, ctx.rpad = g, Rpad
+        ctx.save_for_backward(xt, wq, dx_lut, dw_lut)
         return y
 
     @staticmethod
     def backward(ctx, grad_output):
-        xu, wq, dx_lut, dw_lut = ctx.saved_tensors
-        go = grad_output.contiguous()
-        grad_col = ops.bgemm_custom_grad_uint8_dx(xu, wq, go, dx_lut)
-        grad_w = ops.bgemm_custom_grad_uint8_dw(xu, wq, go, dw_lut)
-        grad_x = ops.col2im(grad_col, ctx.g)
+        xt, wq, dx_lut, dw_lut = ctx.saved_tensors
+        g = ctx.g
+        grad_col, grad_w = ops.custom_grads(
+            (xt, ctx.rpad), wq, grad_output, dx_lut if ctx.needs_input_grad[0] else None,
+            dw_lut if ctx.needs_input_grad[1] else None, g.N, g.C * g.KH * g.KW, g.OH * g.OW)
+        grad_x = ops.col2im(grad_col, g) if grad_col is not None else None
         return grad_x, grad_w, None, None, None, None, None
-
-
-def _pad_with(x, padding, value):
-    ph, pw = padding
-    if ph == 0 and pw == 0:
-        return x
-    B, C, H, W = x.shape
-    xp = value.view(1, 1, 1, 1).expand(B, C, H + 2 * ph, W + 2 * pw).clone()
-    xp[:, :, ph:ph + H, pw:pw + W] = x
-    return xp
 
 
 def conv2d_uint8_custom(x, w, lut, dx_lut, dw_lut, zero_x, geom):

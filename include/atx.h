@@ -382,19 +382,29 @@ int atx_dwconv_bwd_weight(const float* go, const void* img, int dtype,
                           float* workspace, hipStream_t stream);
 
 /* ------------------------------------------------------- custom gradients
- * grad_x[n,k,l] = sum_o dy[n,o,l] * dx_lut[xi(n,k,l)*256 + wi(o,k)] (ascending o)
- * grad_w[o,k]   = sum_{n,l} dy[n,o,l] * dw_lut[xi(n,k,l)*256 + wi(o,k)]
- * x, w: LUT indices (is_signed = 0) or int8 values (is_signed = 1, idx = v+128).
- * csrc/cuda/bgemm_custom_grad_optimize.cu:30-116,136-205 (uint8),
- * 315-404,419-490 (int8), hosts 212-301,497-585. */
-int atx_custom_grad_dx(const void* x, const void* w, int is_signed,
-                       const float* dy, const float* dx_lut, int N, int K,
-                       int L, int O, float* grad_x, hipStream_t stream);
+ * Pair-table ("custom" estimator) gradients of the LUT GEMM:
+ *   grad_x[n,k,l] = sum_o dy[n,o,l] * T[xi(n,k,l)][wi(o,k)]
+ *   grad_w[o,k]   = sum_{n,l} dy[n,o,l] * T[xi(n,k,l)][wi(o,k)]
+ * T a 256x256 fp32 table (the dx / dw table), passed transposed:
+ * tabT[w * 256 + v] = T[v][w] (atx_lut_prepare's outf32t of T).  The
+ * operands are the LUT GEMM's: xt [Kpad][Rpad] row offsets (as atx_pack_x_* /
+ * atx_im2col_rows wrote them; rows r = n*L + l) and wt [K][Opad] indices.
+ * dy [N,O,L] fp32; grad_x [N,K,L] fp32 (fold it with atx_col2im for a conv);
+ * grad_w [O,K] fp32, with the per-channel weight fake-quant STE fused when
+ * mask_w / scale_w are given (as atx_conv_bwd_weight).  Table entries must
+ * be finite.  Workspace of grad_w: atx_custom_grad_dw_workspace_bytes()
+ * (one partial slice per 2048-row tile, summed in a fixed order).
+ * Replace bgemm_custom_grad_{uint8,int8}_{dx,dw}
+ * (csrc/cuda/bgemm_custom_grad_optimize.cu:30-116,136-205 uint8,
+ * 315-404,419-490 int8; hosts 212-301,497-585). */
+int atx_custom_grad_dx(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* dy, const float* tabT, int N, int K, int L, int O,
+                       float* grad_x, hipStream_t stream);
 long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O);
-int atx_custom_grad_dw(const void* x, const void* w, int is_signed,
-                       const float* dy, const float* dw_lut, int N, int K,
-                       int L, int O, float* grad_w, float* workspace,
-                       hipStream_t stream);
+int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* dy, const float* tabT, int N, int K, int L, int O,
+                       const uint8_t* mask_w, const float* scale_w, float* grad_w,
+                       float* workspace, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -576,6 +576,51 @@ def test_custom_grad_kernels(signed):
     close(gw.cpu().numpy(), ew, aw)
 
 
+CUSTOM_SHAPES = [(1, 1, 1, 1), (2, 5, 7, 3), (1, 4, 4096, 16), (3, 37, 1000, 70),
+                 (2, 576, 3136, 64), (1, 9, 2049, 17), (4, 64, 49, 300), (1, 130, 6, 2048),
+                 (2, 3, 5000, 33)]
+
+
+@pytest.mark.parametrize("shape", CUSTOM_SHAPES)
+def test_custom_grads_tiled_shapes(shape):
+    """Pair-table gradients from the row-offset operand across row tiles (R
+    above, below and one past 2048), channel tiles (O % 16 != 0, many
+    tiles), tap quads (K % 4 != 0) and L % 4 != 0, with the fused
+    per-channel STE on grad_w; against the fp64 C oracle within the sum of
+    |terms| bound."""
+    N, K, Lc, Oc = shape
+    r = gen(zlib.crc32(repr(("custom", shape)).encode()))
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    dxl = r.standard_normal(65536).astype(np.float32)
+    dwl = r.standard_normal(65536).astype(np.float32)
+    go = r.standard_normal((N, Oc, Lc)).astype(np.float32)
+    mask = r.random((Oc, K)) < 0.8
+    scale = (r.random(Oc) + 0.5).astype(np.float32)
+    gx, gw = ops.custom_grads(ops.pack_rows_u8(t(xi)), t(wi), t(go), t(dxl), t(dwl), N, K, Lc,
+                              mask_w=t(mask), scale_w=t(scale))
+    ex, ew = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl))
+    ax, aw = O.gemm_grads(go, xi, wi, "custom", (dxl, dwl), absolute=True)
+    close(gx.cpu().numpy(), ex, ax)
+    ew = np.where(mask, ew, 0.0) / scale[:, None]
+    aw = np.where(mask, aw, 0.0) / scale[:, None]
+    close(gw.cpu().numpy(), ew, aw)
+
+
+def test_custom_grads_deterministic():
+    """The grad_w partial slices are summed in a fixed order: two runs agree bitwise."""
+    N, K, Lc, Oc = 4, 288, 3136, 64
+    r = gen(77)
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    tb = t(r.standard_normal(65536).astype(np.float32))
+    go = t(r.standard_normal((N, Oc, Lc)).astype(np.float32))
+    op = ops.pack_rows_u8(t(xi))
+    a = ops.custom_grads(op, t(wi), go, tb, tb, N, K, Lc)
+    b = ops.custom_grads(op, t(wi), go, tb, tb, N, K, Lc)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 @pytest.mark.parametrize("geom", GEOMS)
 def test_conv_backward_kernels(geom):
     k, s, p, d = geom
