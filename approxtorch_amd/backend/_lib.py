@@ -56,7 +56,8 @@ _SIGS = {
     "atx_fakequant_channel_fwd": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_int, c_int, c_int,
                                           c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "atx_col2im": (c_int, [c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
-    "atx_tap_sum": (c_int, [c_vp, ConvGeom, c_vp, c_vp, c_vp]),
+    "atx_tap_sum_workspace_bytes": (c_ll, [ConvGeom]),
+    "atx_tap_sum": (c_int, [c_vp, c_int, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_bwd": (c_int, [c_vp, ConvGeom, c_vp, c_vp]),
     "atx_reduce_workspace_bytes": (c_ll, []),
     "atx_absmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp]),

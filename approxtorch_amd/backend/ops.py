@@ -516,10 +516,16 @@ def conv_backward_weight_rows(go: Tensor, operand, table: Tensor, g, O: int, mas
 
 
 def tap_sum(img: Tensor, g, pad_dev=None) -> Tensor:
-    """[N, L] column sums of the unfolded fp32 image (padding = pad_dev)."""
+    """[N, L] column sums of the unfolded image (uint8 values or fp32 holding
+    quantized integers; padding = pad_dev)."""
     ic = img.contiguous()
+    if ic.dtype not in (torch.uint8, torch.float32):
+        raise RuntimeError(f"tap_sum: image must be uint8 or float32, got {ic.dtype}")
     out = torch.empty((g.N, g.OH * g.OW), dtype=torch.float32, device=ic.device)
-    L.call("atx_tap_sum", L.ptr(ic), g, L.ptr(pad_dev), L.ptr(out), L.stream_of(ic))
+    wsb = L.query("atx_tap_sum_workspace_bytes", g)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=ic.device)
+    L.call("atx_tap_sum", L.ptr(ic), 1 if ic.dtype == torch.uint8 else 2, g, L.ptr(pad_dev),
+           L.ptr(out), L.ptr(ws), L.stream_of(ic))
     return out
 
 

@@ -241,24 +241,50 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
 // Sum over the K taps of each output position (out-of-image taps count as
 // pad_dev[0]): the column sums of the unfolded image, used by the uint8
 // zero-point correction (nn/Conv2d_uint8.py:311).
-__global__ void tap_sum_kernel(const float* __restrict__ img, atx_conv_geom g,
-                               const float* __restrict__ pad_dev, float* __restrict__ out) {
-  const int L = g.OH * g.OW;
+// Column sums of the unfolded image in two phases (every sum is of
+// quantized integers below 2^24, so exact in any order):
+//   partial[n][chunk][h*W + w] = sum over the chunk's 64 channels of img,
+//   out[n,l] = sum over the KH*KW taps of output position l of the chunk sums
+//              at the tap's pixel, or C * pad for a tap outside the image.
+constexpr int TS_CHUNK = 64;
+
+template <typename T>
+__global__ void tap_chan_sum_kernel(const T* __restrict__ img, int C, int HW, int chunks,
+                                    long long total, float* __restrict__ partial) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int p = (int)(i % HW);
+    const long long t = i / HW;
+    const int ch = (int)(t % chunks);
+    const int n = (int)(t / chunks);
+    const int c0 = ch * TS_CHUNK, c1 = min(C, c0 + TS_CHUNK);
+    const T* src = img + ((long long)n * C + c0) * HW + p;
+    float a = 0.0f;
+    for (int c = c0; c < c1; ++c, src += HW) a += (float)*src;
+    partial[i] = a;
+  }
+}
+
+__global__ void tap_window_sum_kernel(const float* __restrict__ partial, atx_conv_geom g,
+                                      int chunks, const float* __restrict__ pad_dev,
+                                      float* __restrict__ out) {
+  const int L = g.OH * g.OW, HW = g.H * g.W;
   const long long total = (long long)g.N * L;
-  const float pad = pad_dev ? pad_dev[0] : 0.0f;
+  const float padc = (pad_dev ? pad_dev[0] : 0.0f) * (float)g.C;
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
     const int n = (int)(i / L), l = (int)(i - (i / L) * L);
     const int oh = l / g.OW, ow = l - (l / g.OW) * g.OW;
+    const float* pn = partial + (long long)n * chunks * HW;
     float a = 0.0f;
-    for (int c = 0; c < g.C; ++c) {
-      const float* ic = img + ((long long)n * g.C + c) * g.H * g.W;
-      for (int kh = 0; kh < g.KH; ++kh) {
-        const int ih = oh * g.SH + kh * g.DH - g.PH;
-        for (int kw = 0; kw < g.KW; ++kw) {
-          const int iw = ow * g.SW + kw * g.DW - g.PW;
-          a += ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                   ? ic[(long long)ih * g.W + iw] : pad;
+    for (int kh = 0; kh < g.KH; ++kh) {
+      const int ih = oh * g.SH + kh * g.DH - g.PH;
+      for (int kw = 0; kw < g.KW; ++kw) {
+        const int iw = ow * g.SW + kw * g.DW - g.PW;
+        if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W) {
+          for (int ch = 0; ch < chunks; ++ch) a += pn[(long long)ch * HW + ih * g.W + iw];
+        } else {
+          a += padc;
         }
       }
     }
@@ -411,16 +437,35 @@ int atx_lut_map_pad(const void* in, int dtype, int N, int C, int H, int W, int P
   return check_launch("lut_map_pad_kernel");
 }
 
-int atx_tap_sum(const float* img, atx_conv_geom g, const float* pad_dev, float* out,
-                hipStream_t stream) {
+long long atx_tap_sum_workspace_bytes(atx_conv_geom g) {
+  if (g.N <= 0 || g.C <= 0 || g.H <= 0 || g.W <= 0) return 0;
+  return (long long)g.N * cdiv(g.C, TS_CHUNK) * g.H * g.W * 4;
+}
+
+int atx_tap_sum(const void* img, int dtype, atx_conv_geom g, const float* pad_dev, float* out,
+                float* workspace, hipStream_t stream) {
   int rc = check_geom(g);
   if (rc) return rc;
+  ATX_REQUIRE(dtype == 1 || dtype == 2, "atx_tap_sum: dtype must be 1 (uint8) or 2 (fp32)");
   const long long total = (long long)g.N * g.OH * g.OW;
   if (total == 0) return ATX_OK;
-  ATX_REQUIRE(out && ((long long)g.C * g.H * g.W == 0 || img), "atx_tap_sum: null pointer");
-  hipLaunchKernelGGL(tap_sum_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, img, g,
-                     pad_dev, out);
-  return check_launch("tap_sum_kernel");
+  ATX_REQUIRE(out, "atx_tap_sum: null output");
+  const int chunks = (int)cdiv(g.C, TS_CHUNK);
+  const long long ptotal = (long long)g.N * chunks * g.H * g.W;
+  if (ptotal > 0) {
+    ATX_REQUIRE(img && workspace, "atx_tap_sum: null image / workspace");
+    if (dtype == 1)
+      hipLaunchKernelGGL(tap_chan_sum_kernel<uint8_t>, dim3(elem_grid(ptotal, TB)), dim3(TB), 0,
+                         stream, (const uint8_t*)img, g.C, g.H * g.W, chunks, ptotal, workspace);
+    else
+      hipLaunchKernelGGL(tap_chan_sum_kernel<float>, dim3(elem_grid(ptotal, TB)), dim3(TB), 0,
+                         stream, (const float*)img, g.C, g.H * g.W, chunks, ptotal, workspace);
+    rc = check_launch("tap_chan_sum_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(tap_window_sum_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream,
+                     workspace, g, g.C > 0 ? chunks : 0, pad_dev, out);
+  return check_launch("tap_window_sum_kernel");
 }
 
 int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img, hipStream_t stream) {

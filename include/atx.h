@@ -229,12 +229,15 @@ int atx_fakequant_channel_fwd(const float* w, int O, long long inner,
 int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask,
                const float* scale, float* img, hipStream_t stream);
 
-/* Column sums of the unfolded fp32 image, out[n,l] = sum over the K taps
- * (out-of-image taps count as pad_dev[0], 0 if null), and its backward
+/* Column sums of the unfolded image (dtype 1 = uint8 values, 2 = fp32
+ * holding quantized integers), out[n,l] = sum over the K taps (out-of-image
+ * taps count as pad_dev[0], 0 if null), exact; workspace:
+ * atx_tap_sum_workspace_bytes(g) (per-64-channel sums).  And its backward
  * img[n,c,h,w] = sum of go[n,l] over the taps reading (h,w).  The uint8
  * zero-point correction term sum_k q_x of nn/Conv2d_uint8.py:308-315. */
-int atx_tap_sum(const float* img, atx_conv_geom g, const float* pad_dev,
-                float* out, hipStream_t stream);
+long long atx_tap_sum_workspace_bytes(atx_conv_geom g);
+int atx_tap_sum(const void* img, int dtype, atx_conv_geom g, const float* pad_dev,
+                float* out, float* workspace, hipStream_t stream);
 int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img,
                     hipStream_t stream);
 

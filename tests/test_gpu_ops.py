@@ -576,6 +576,27 @@ def test_custom_grad_kernels(signed):
     close(gw.cpu().numpy(), ew, aw)
 
 
+TAP_GEOMS = [((2, 5, 9, 7), (3, 3), (1, 1), (1, 1), (1, 1)), ((3, 130, 6, 5), (3, 3), (2, 2), (1, 1), (1, 1)),
+             ((2, 64, 7, 7), (1, 1), (1, 1), (0, 0), (1, 1)), ((1, 200, 11, 13), (3, 3), (1, 2), (2, 2), (2, 1)),
+             ((4, 3, 16, 16), (7, 7), (2, 2), (3, 3), (1, 1))]
+
+
+@pytest.mark.parametrize("case", TAP_GEOMS)
+@pytest.mark.parametrize("dtype", ["uint8", "float32"])
+def test_tap_sum_exact(case, dtype):
+    """Column sums of the unfolded image with out-of-image taps counting as
+    the zero point (nn/Conv2d_uint8.py:308-315): exact integers."""
+    shape, k, s_, p, d = case
+    r = gen(zlib.crc32(repr((case, dtype)).encode()))
+    img = r.integers(0, 256, shape, dtype=np.uint8)
+    z = np.float32(37.0)
+    g = ops.conv_geom(shape, k, s_, p, d)
+    src = t(img) if dtype == "uint8" else t(img.astype(np.float32))
+    got = ops.tap_sum(src, g, pad_dev=t(np.array([z], np.float32)))
+    want = O.im2col_index(img, k, s_, p, d, int(z)).astype(np.int64).sum(axis=1)
+    assert np.array_equal(got.cpu().numpy(), want.astype(np.float32))
+
+
 CUSTOM_SHAPES = [(1, 1, 1, 1), (2, 5, 7, 3), (1, 4, 4096, 16), (3, 37, 1000, 70),
                  (2, 576, 3136, 64), (1, 9, 2049, 17), (4, 64, 49, 300), (1, 130, 6, 2048),
                  (2, 3, 5000, 33)]
