@@ -1,11 +1,16 @@
-"""Replace nn.Conv2d layers with approximate convolutions.
+"""Replace nn.Conv2d layers with approximate convolutions (the API of
+approxtorch/convert_model.py:15-221).
 
-Mirrors approxtorch/convert_model.py:15-221: arguments are validated first,
-every replacement is built before the model is mutated (an unsupported conv
-leaves the model untouched), the first conv is skipped by default, weights
-and biases are copied and the weight qparams re-derived from them, and the
-source layer's training flag is kept.  Extension: qtype="uint8" accepts
-weight_bits 1..8 (the reference fixes 8).
+The conversion is two-phase: every selected conv is turned into its
+replacement first, and only when all of them were built are they installed
+in their parents, so a conv the layers cannot express (string padding, a
+non-zero padding mode, an unsupported group count) raises and leaves the
+model as it was.  A replacement adopts its source's parameters (cloned, with
+their requires_grad), its device (for every buffer except the caller's
+tables), its weight quantization parameters (re-derived from the adopted
+weight) and its train/eval flag.
+
+Extension: qtype="uint8" accepts weight_bits 1..8 (the reference fixes 8).
 """
 from typing import Literal
 
@@ -17,52 +22,82 @@ from .nn import Conv2d_int8, Conv2d_uint8
 QType = Literal["int8", "uint8"]
 GradType = Literal["ste", "lre", "custom"]
 
-
-def _move_qparams_to_device(module: nn.Module, device: torch.device) -> None:
-    # lut / dx / dw stay where the caller put them (convert_model.py:15-25)
-    external_buffers = {"lut", "dx", "dw"}
-    for name, buffer in module._buffers.items():
-        if buffer is not None and name not in external_buffers:
-            module._buffers[name] = buffer.to(device=device)
+_LAYER = {"int8": Conv2d_int8, "uint8": Conv2d_uint8}
 
 
-def _copy_conv_state(source: nn.Conv2d, target: nn.Module, qtype: QType) -> None:
+def _validate(model, lut, qtype, grad, ignore_first_conv, update_scale, scale_momentum,
+              weight_bits):
+    """Argument checks, all before the model is looked at."""
+    if not isinstance(model, nn.Module):
+        raise TypeError(f"model must be an nn.Module, got {type(model).__name__}")
+    if not isinstance(lut, torch.Tensor):
+        raise TypeError(f"lut must be a torch.Tensor, got {type(lut).__name__}")
+    if lut.numel() != 256 * 256:
+        raise ValueError(f"lut must have 65536 elements, got {lut.numel()}")
+    if qtype not in _LAYER:
+        raise ValueError(f"qtype must be 'int8' or 'uint8', got {qtype!r}")
+    if grad not in ("ste", "lre", "custom"):
+        raise ValueError(f"grad must be 'ste', 'lre' or 'custom', got {grad!r}")
+    for flag, value in (("ignore_first_conv", ignore_first_conv),
+                        ("update_scale", update_scale)):
+        if not isinstance(value, bool):
+            raise TypeError(f"{flag} must be a bool")
+    if not 0.0 <= scale_momentum <= 1.0:
+        raise ValueError(f"scale_momentum must be between 0 and 1, got {scale_momentum}")
+    if isinstance(weight_bits, bool) or not isinstance(weight_bits, int):
+        raise TypeError("weight_bits must be an int")
+    if qtype == "int8" and not 3 <= weight_bits <= 8:
+        raise ValueError(f"weight_bits must be between 3 and 8, got {weight_bits}")
+    if qtype == "uint8" and not 1 <= weight_bits <= 8:
+        raise ValueError(f"weight_bits must be between 1 and 8 for uint8, got {weight_bits}")
+
+
+def _conv_sites(root):
+    """(parent, attribute, conv) of every nn.Conv2d under root, in the order
+    of root.named_modules() and each module once (a module reachable by
+    several paths is found at the first); parent is None for the root."""
+    visited = set()
+
+    def walk(parent, attr, module):
+        if id(module) in visited:
+            return
+        visited.add(id(module))
+        if isinstance(module, nn.Conv2d):
+            yield parent, attr, module
+        for name, child in module._modules.items():
+            if child is not None:
+                yield from walk(module, name, child)
+
+    yield from walk(None, None, root)
+
+
+def _adopted(param):
+    return nn.Parameter(param.detach().clone(memory_format=torch.preserve_format),
+                        requires_grad=param.requires_grad)
+
+
+def _replacement(source, layer_cls, lut, options):
+    """A layer_cls computing what `source` computes, on source's device."""
+    if isinstance(source.padding, str):
+        raise NotImplementedError(
+            f"convert_model does not support Conv2d string padding {source.padding!r}")
+    if source.padding_mode != "zeros":
+        raise NotImplementedError(
+            f"convert_model only supports Conv2d padding_mode='zeros', got {source.padding_mode!r}")
+    layer = layer_cls(source.in_channels, source.out_channels, source.kernel_size, lut,
+                      bias=source.bias is not None, stride=source.stride,
+                      padding=source.padding, dilation=source.dilation, groups=source.groups,
+                      **options)
     device = source.weight.device
-    _move_qparams_to_device(target, device)
-    target.weight = nn.Parameter(
-        source.weight.detach().clone(memory_format=torch.preserve_format),
-        requires_grad=source.weight.requires_grad)
+    for name, buf in list(layer._buffers.items()):
+        if buf is not None and name not in layer.caller_tables:
+            layer._buffers[name] = buf.to(device=device)
+    layer.weight = _adopted(source.weight)
     if source.bias is not None:
-        target.bias = nn.Parameter(source.bias.detach().clone(),
-                                   requires_grad=source.bias.requires_grad)
-    if qtype == "int8":
-        target._reset_scale_w_from_weight()
-    else:
-        with torch.no_grad():
-            reduce_dims = tuple(range(1, target.weight.dim()))
-            target.w_min.copy_(target.weight.detach().amin(dim=reduce_dims).to(target.w_min.dtype))
-            target.w_max.copy_(target.weight.detach().amax(dim=reduce_dims).to(target.w_max.dtype))
-        target._reset_qparams_from_stats()
-    target.train(source.training)
-
-
-def _make_approx_conv(module, lut, qtype, grad, dx, dw, scale_momentum, update_scale,
-                      weight_bits):
-    if isinstance(module.padding, str):
-        raise NotImplementedError(
-            f"convert_model does not support Conv2d string padding {module.padding!r}")
-    if module.padding_mode != "zeros":
-        raise NotImplementedError(
-            f"convert_model only supports Conv2d padding_mode='zeros', got {module.padding_mode!r}")
-    common_args = dict(
-        in_channels=module.in_channels, out_channels=module.out_channels,
-        kernel_size=module.kernel_size, lut=lut, grad=grad, dx=dx, dw=dw,
-        bias=module.bias is not None, stride=module.stride, padding=module.padding,
-        dilation=module.dilation, groups=module.groups, update_scale=update_scale,
-        scale_momentum=scale_momentum, weight_bits=weight_bits)
-    new_module = Conv2d_int8(**common_args) if qtype == "int8" else Conv2d_uint8(**common_args)
-    _copy_conv_state(module, new_module, qtype)
-    return new_module
+        layer.bias = _adopted(source.bias)
+    layer.reset_weight_qparams()
+    layer.train(source.training)
+    return layer
 
 
 def convert_model(model: nn.Module, lut: torch.Tensor, qtype: QType = "int8",
@@ -75,43 +110,21 @@ def convert_model(model: nn.Module, lut: torch.Tensor, qtype: QType = "int8",
     int8: per-tensor symmetric activations, per-channel symmetric weights;
     uint8: per-tensor asymmetric activations, per-channel asymmetric weights.
     The model is modified in place and returned (a bare nn.Conv2d model
-    returns its replacement).  Convert before building the optimizer."""
-    if not isinstance(model, nn.Module):
-        raise TypeError(f"model must be an nn.Module, got {type(model).__name__}")
-    if not isinstance(lut, torch.Tensor):
-        raise TypeError(f"lut must be a torch.Tensor, got {type(lut).__name__}")
-    if lut.numel() != 256 * 256:
-        raise ValueError(f"lut must have 65536 elements, got {lut.numel()}")
-    if qtype not in ("int8", "uint8"):
-        raise ValueError(f"qtype must be 'int8' or 'uint8', got {qtype!r}")
-    if grad not in ("ste", "lre", "custom"):
-        raise ValueError(f"grad must be 'ste', 'lre' or 'custom', got {grad!r}")
-    if not isinstance(ignore_first_conv, bool):
-        raise TypeError("ignore_first_conv must be a bool")
-    if not isinstance(update_scale, bool):
-        raise TypeError("update_scale must be a bool")
-    if not 0.0 <= scale_momentum <= 1.0:
-        raise ValueError(f"scale_momentum must be between 0 and 1, got {scale_momentum}")
-    if isinstance(weight_bits, bool) or not isinstance(weight_bits, int):
-        raise TypeError("weight_bits must be an int")
-    if qtype == "int8" and not 3 <= weight_bits <= 8:
-        raise ValueError(f"weight_bits must be between 3 and 8, got {weight_bits}")
-    if qtype == "uint8" and not 1 <= weight_bits <= 8:
-        raise ValueError(f"weight_bits must be between 1 and 8 for uint8, got {weight_bits}")
-
-    named_modules = dict(model.named_modules())
-    convs = [(name, m) for name, m in named_modules.items() if isinstance(m, nn.Conv2d)]
+    returns its replacement).  Convert before building the optimizer: the
+    replacements own new Parameter objects."""
+    _validate(model, lut, qtype, grad, ignore_first_conv, update_scale, scale_momentum,
+              weight_bits)
+    sites = list(_conv_sites(model))
     if ignore_first_conv:
-        convs = convs[1:]
-    replacements = [(name, _make_approx_conv(m, lut, qtype, grad, dx, dw, scale_momentum,
-                                             update_scale, weight_bits))
-                    for name, m in convs]
-    converted_model = model
-    for name, new_module in replacements:
-        if not name:
-            converted_model = new_module
-            continue
-        parent_name, attr_name = name.rsplit(".", 1) if "." in name else ("", name)
-        parent = named_modules[parent_name] if parent_name else model
-        setattr(parent, attr_name, new_module)
-    return converted_model
+        sites = sites[1:]
+    options = dict(grad=grad, dx=dx, dw=dw, update_scale=update_scale,
+                   scale_momentum=scale_momentum, weight_bits=weight_bits)
+    built = [(parent, attr, _replacement(conv, _LAYER[qtype], lut, options))
+             for parent, attr, conv in sites]
+    result = model
+    for parent, attr, layer in built:
+        if parent is None:
+            result = layer
+        else:
+            setattr(parent, attr, layer)
+    return result

@@ -43,6 +43,9 @@ def _ema_coeffs(m):
 
 
 class Conv2d_int8(nn.Module):
+    # buffers that alias tables owned by the caller (never moved or copied
+    # when the layer adopts another layer's device)
+    caller_tables = ("lut", "dx", "dw")
 
     def __init__(self,
                  in_channels: int,
@@ -103,7 +106,7 @@ class Conv2d_int8(nn.Module):
             raise ValueError("Invalid bias type")
 
         self.reset_parameters()
-        self._reset_scale_w_from_weight()
+        self.reset_weight_qparams()
 
         if isinstance(bias, torch.Tensor):
             if bias.shape != (self.out_channels,):
@@ -185,7 +188,7 @@ class Conv2d_int8(nn.Module):
                    L.ptr(self.scale_w), L.stream_of(w))
         _bump(self.scale_w)
 
-    def _reset_scale_w_from_weight(self):
+    def reset_weight_qparams(self):
         """scale_w = absmax(W)/qmax_w per channel (1 for zero channels); runs at
         construction / conversion time, possibly on the CPU
         (nn/Conv2d_int8.py:160-167)."""

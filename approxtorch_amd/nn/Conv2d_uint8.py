@@ -33,6 +33,9 @@ def uint8_qparams(mn, mx, qmax=255):
 
 
 class Conv2d_uint8(nn.Module):
+    # buffers that alias tables owned by the caller (never moved or copied
+    # when the layer adopts another layer's device)
+    caller_tables = ("lut", "dx", "dw")
 
     def __init__(self,
                  in_channels: int,
@@ -95,11 +98,7 @@ class Conv2d_uint8(nn.Module):
             raise ValueError("Invalid bias type")
 
         self.reset_parameters()
-        with torch.no_grad():
-            reduce_dims = tuple(range(1, self.weight.dim()))
-            self.w_min.copy_(self.weight.detach().amin(dim=reduce_dims))
-            self.w_max.copy_(self.weight.detach().amax(dim=reduce_dims))
-        self._reset_qparams_from_stats()
+        self.reset_weight_qparams()
 
         if isinstance(bias, torch.Tensor):
             if bias.shape != (self.out_channels,):
@@ -151,6 +150,16 @@ class Conv2d_uint8(nn.Module):
 
     def freeze_scale(self):
         self.update_scale = False
+
+    def reset_weight_qparams(self):
+        """w_min / w_max from the current weight (per output channel), then
+        every qparam from the statistics."""
+        with torch.no_grad():
+            w = self.weight.detach()
+            dims = tuple(range(1, w.dim()))
+            self.w_min.copy_(w.amin(dim=dims))
+            self.w_max.copy_(w.amax(dim=dims))
+        self._reset_qparams_from_stats()
 
     def _reset_qparams_from_stats(self):
         with torch.no_grad():

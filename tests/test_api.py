@@ -172,3 +172,22 @@ def test_cpu_baseline_restatement_matches_oracle():
     gx, gw, _ = O.conv_int8_backward(go.numpy(), ctx, np.float32(0.02), conv.scale_w.numpy(),
                                      "lre", (ga, gb), (3, 3), (2, 2), (1, 1), (1, 1))
     np.testing.assert_allclose(xr.grad.double().numpy(), gx, rtol=1e-4, atol=1e-3)
+
+
+def test_conversion_walk_matches_named_modules_order_and_dedup():
+    """Sites come in named_modules() order with shared modules once; a conv
+    reachable by two paths is replaced at the first path only (as a
+    named_modules-driven conversion would)."""
+    from approxtorch_amd.convert_model import _conv_sites
+    shared = nn.Conv2d(4, 4, 1)
+    inner = nn.Sequential(nn.Conv2d(4, 4, 3, padding=1), shared)
+    model = nn.Sequential(nn.Conv2d(3, 4, 1), inner, nn.ReLU(), shared, inner,
+                          nn.ModuleDict({"a": nn.Conv2d(4, 2, 1)}))
+    want = [id(m) for _, m in model.named_modules() if isinstance(m, nn.Conv2d)]
+    assert [id(c) for _, _, c in _conv_sites(model)] == want
+    convert_model(model, LUT, qtype="int8")
+    assert isinstance(model[0], nn.Conv2d)                 # first conv skipped
+    assert isinstance(inner[0], Conv2d_int8) and isinstance(inner[1], Conv2d_int8)
+    assert model[3] is shared                              # second path untouched
+    assert isinstance(model[5]["a"], Conv2d_int8)
+    assert model[4] is inner

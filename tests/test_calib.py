@@ -134,9 +134,7 @@ def test_calibration_device_reductions_match_torch(tmp_path, monkeypatch):
     model = small_model().cuda()
     dev8 = calib.calibrate_int8(model, data, 12, os.path.join(tmp_path, "a.pt"))
     dev_u = calib.calibrate_uint8(model, data, 9)
-    monkeypatch.setattr(calib, "_absmax", lambda x: x.abs().max().to(torch.float32))
-    monkeypatch.setattr(calib, "_minmax",
-                        lambda x: (x.amin().to(torch.float32), x.amax().to(torch.float32)))
+    monkeypatch.setattr(calib, "_on_device", lambda x: False)     # torch's reductions
     ref8 = calib.calibrate_int8(model, data, 12, os.path.join(tmp_path, "b.pt"))
     ref_u = calib.calibrate_uint8(model, data, 9)
     for a, b in ((dev8, ref8), (dev_u, ref_u)):
