@@ -44,13 +44,28 @@ struct XRows { uint2 v[tiles::NQ]; };
 
 // Row offsets of the lane's quads from slot soff / (2 Rpad) of a quad's
 // row-offset block (xs = descriptor over the quad's four slots of the tile,
-// voff = byte offset of the lane's first quad within a slot).
+// voff = byte offset of the lane's first quad within a slot).  The quads'
+// 128-byte steps go into the scalar offset, so all four loads share the one
+// per-lane offset register.
 __device__ __forceinline__ void load_x(XRows& x, __amdgpu_buffer_rsrc_t xs, int voff, int soff) {
 #pragma unroll
   for (int h = 0; h < tiles::NQ; ++h)
     x.v[h] = __builtin_bit_cast(
-        uint2, __builtin_amdgcn_raw_buffer_load_b64(xs, voff + 2 * tiles::NRG * tiles::RQ * h,
-                                                    soff, 0));
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(xs, voff,
+                                                    soff + 2 * tiles::NRG * tiles::RQ * h, 0));
+}
+
+// Read XOR mask of sub-step S from quad buffer B for a lane with
+// base = (rg << 6) | (g << 4): chunk g in bits 4-5, table quarter
+// (rg + S) & 3 in bits 6-7, the buffer in bit 16.  Formed in place by asm
+// the compiler can neither hoist (four masks kept live across a kernel's
+// main loop cost registers that then spill) nor fold into every address.
+template <int S, int B>
+__device__ __forceinline__ unsigned quarter_mask(unsigned base) {
+  unsigned t;
+  asm volatile("v_add_u32 %0, %1, %2\n\tv_and_b32 %0, %3, %0\n\tv_or_b32 %0, %4, %0"
+               : "=&v"(t) : "n"(S << 6), "v"(base), "n"(0xf0), "n"(B << 16));
+  return t;
 }
 
 }  // namespace atx

@@ -72,6 +72,7 @@ constexpr int TPL = 4;             // tables per LDS line (quarters)
 constexpr int LINE = 256;          // bytes per LDS line
 constexpr int QTAB = 256 * LINE;   // one quad of tables (64 KiB)
 constexpr int SMEM_BYTES = 2 * QTAB;          // two quad buffers (128 KiB)
+static_assert(QTAB == 1 << 16, "quad buffer select is bit 16 of a read address");
 static_assert(CG == 4 && NRG == 16 && NWAVE == 8, "tile geometry");
 static_assert(TPL * CG * 16 == LINE, "four 64-byte table rows per line");
 static_assert(2 * NWAVE == 16 && 256 / 2 == 64 * (NWAVE / CG),
@@ -316,19 +317,43 @@ __global__ void pack_w_kernel(const T* __restrict__ w, int O, int K, int offset,
 }
 
 // ------------------------------------------------------------- main kernel
+// Accumulates one 16-byte table chunk (channels 2m, 2m+1 in dword m, the
+// even channel in the low half) into a row's pair accumulators:
+// a[2m] += d_m, the whole dword, and a[2m+1] += d_m >> 16, the high entry
+// (sign-extended for signed tables).  The even channels' sums are recovered
+// once per tile segment (pair_sums): a[2m] - (a[2m+1] << 16), less the bias
+// of the low entries for signed tables.  One add of each pair is a plain
+// 32-bit VOP2 add, which gfx950 issues at about 1.7x the rate of the SDWA
+// form that extracts a 16-bit half.
 template <bool SIGNED>
 __device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
   const unsigned d[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if constexpr (SIGNED) {
-      a[2 * i] += (int)(short)(unsigned short)(d[i] & 0xffffu);
-      a[2 * i + 1] += ((int)d[i]) >> 16;
-    } else {
-      a[2 * i] += (int)(d[i] & 0xffffu);
-      a[2 * i + 1] += (int)(d[i] >> 16);
-    }
+    a[2 * i] = (int)((unsigned)a[2 * i] + d[i]);
+    if constexpr (SIGNED) a[2 * i + 1] += ((int)d[i]) >> 16;
+    else a[2 * i + 1] += (int)(d[i] >> 16);
   }
+}
+
+// Signed tables store their low (even-channel) entries biased by 2^15, so
+// that a dword's value is exactly hi * 2^16 + (lo + 2^15) with the low part
+// in [0, 2^16): summed over T tables, the even channel's sum is
+// S - (H << 16) - 2^15 T (mod 2^32; exact within the int32 bound).
+constexpr unsigned LOW_BIAS = 0x8000u;
+
+// Turns the pair accumulators of the lane's rows into channel sums after
+// `tables` tables (every table accumulated, all-zero ones included: their
+// biased low entries are exactly LOW_BIAS).
+template <bool SIGNED>
+__device__ __forceinline__ void pair_sums(int (&acc)[RPL][8], int tables) {
+  const unsigned bias = SIGNED ? LOW_BIAS * (unsigned)tables : 0u;
+#pragma unroll
+  for (int j = 0; j < RPL; ++j)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      acc[j][2 * m] =
+          (int)((unsigned)acc[j][2 * m] - ((unsigned)acc[j][2 * m + 1] << 16) - bias);
 }
 
 // Table-build registers: the LUT16T dwords (entries v0, v0+1) of the wave's
@@ -358,8 +383,13 @@ __device__ __forceinline__ void load_rows(Rows& r, __amdgpu_buffer_rsrc_t lut, u
 
 // Writes the lane's two 16-byte chunks (rows v0 and v0+1, channels
 // 8*og .. 8*og+7) at smem + wb (row v0's chunk; row v0+1 is one line on).
+// Signed tables get their even channels' entries biased (LOW_BIAS).
+template <bool SIGNED>
 __device__ __forceinline__ void write_table(unsigned char* smem, const Rows& r, int wb) {
-  const unsigned* d = r.d;
+  unsigned d[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    d[c] = (SIGNED && (c & 1) == 0) ? r.d[c] ^ (LOW_BIAS | (LOW_BIAS << 16)) : r.d[c];
   uint4 lo, hi;      // channel pairs (2m, 2m+1) at v0 (low halves) / v0+1 (high)
   lo.x = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
   lo.y = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
@@ -475,16 +505,14 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
   // Table build: wave w writes channel group og = w % 4 for rows
   // 128 hw .. 128 hw + 127 (hw = w / 4); lane t the row pair v0 = 128 hw + 2t,
   // v0 + 1, whose chunk og sits at position og ^ ((v0 >> 1) & 3) =
-  // og ^ (t & 3) of quarter q.  wb0 / wb1 address row v0's chunk in quad
-  // buffer 0 / 1; the quarter is an immediate offset (q * 64).
+  // og ^ (t & 3) of quarter q.  wb0 addresses row v0's chunk in quad
+  // buffer 0 (buffer 1 is QTAB on); the quarter is an immediate offset
+  // (q * 64).
   const int og = __builtin_amdgcn_readfirstlane(wave % CG);
   const int hw = __builtin_amdgcn_readfirstlane(wave / CG);
   const int wb0 = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
-  const int wb1 = wb0 + QTAB;
   // Read XOR masks: sub-step s of a quad reads quarter (rg + s) & 3.
-  unsigned gq[TPL];
-#pragma unroll
-  for (int q = 0; q < TPL; ++q) gq[q] = (unsigned)((g << 4) | (((rg + q) & 3) << 6));
+  const unsigned gbase = (unsigned)((rg << 6) | (g << 4));
 
   const int xoff = (wave * RPW + rg * RQ) * 2;          // lane's first quad, bytes
   const uint16_t* __restrict__ xtile = p.xt + (long long)tr * RT;
@@ -531,7 +559,7 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
 #pragma unroll
       for (int q = 0; q < TPL; ++q) {
         load_rows(r4, q < n ? lutr : lutz, load_w8(wtab(q), lane), lane, 256 * hw);
-        write_table(smem + q * 64, r4, wb0);            // quad 0 -> buffer 0
+        write_table<SIGNED>(smem + q * 64, r4, wb0);    // quad 0 -> buffer 0
       }
       load_rows(rows, TPL < n ? lutr : lutz, load_w8(wtab(TPL), lane), lane, 256 * hw);
       wnext = load_w8(wtab(TPL + 1), lane);
@@ -545,13 +573,19 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
       constexpr int B = decltype(bc)::value;
       constexpr int S = decltype(sc)::value;
       const int sigma = TPL * j + S;
-      if constexpr (S + 1 < TPL) load_x(xnext, quad_rows(j), xoff, (S + 1) * slot_bytes);
-      else load_x(xnext, quad_rows(j + 1), xoff, 0);
-      Rows rn;
-      load_rows(rn, sigma + 5 < n ? lutr : lutz, wnext, lane, 256 * hw);
+      // Issue order = order of use in the next sub-step (the counter of
+      // outstanding loads is waited on in order): weight indices (first, to
+      // address the LUT rows), row offsets (the accumulation), LUT rows
+      // (the table write at the end).
       const unsigned wn = load_w8(wtab(sigma + 6), lane);
       __builtin_amdgcn_sched_barrier(0);
-      use_table<SIGNED>(acc, smem, xcur, gq[S] | (B ? (unsigned)QTAB : 0u));
+      if constexpr (S + 1 < TPL) load_x(xnext, quad_rows(j), xoff, (S + 1) * slot_bytes);
+      else load_x(xnext, quad_rows(j + 1), xoff, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      Rows rn;
+      load_rows(rn, sigma + 5 < n ? lutr : lutz, wnext, lane, 256 * hw);
+      __builtin_amdgcn_sched_barrier(0);
+      use_table<SIGNED>(acc, smem, xcur, quarter_mask<S, B>(gbase));
       // Pin the adds here: left free, the compiler sinks them into later
       // steps, past the table write that waits for this step's loads.
 #pragma unroll
@@ -559,7 +593,7 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
 #pragma unroll
         for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
       __builtin_amdgcn_sched_barrier(0);
-      write_table(smem + S * 64, rows, B ? wb0 : wb1);  // table sigma+4, other buffer
+      write_table<SIGNED>(smem + S * 64 + (B ? 0 : QTAB), rows, wb0);  // table sigma+4, other buffer
       rows = rn;
       wnext = wn;
       if constexpr (S == TPL - 1) __syncthreads();
@@ -579,6 +613,7 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
       sub(I1{}, I2{}, j + 1, xa, xb);
       sub(I1{}, I3{}, j + 1, xb, xa);
     }
+    pair_sums<SIGNED>(acc, TPL * nq);
   }
 }
 

@@ -102,6 +102,38 @@ __global__ void __launch_bounds__(512) lds_probe_kernel(int iters, unsigned* out
 
 // int32 add rate: 8 independent chains per lane, 64 v_add_u32 per iteration
 // (inline asm so the adds are neither folded nor vectorized).
+// VALU issue rate of one instruction form: 8 independent register chains
+// per lane, 64 instructions per lane per iteration.
+//   mode 0  v_add_u32                      (int32 add)
+//   mode 1  v_add_u32_sdwa, sext WORD_1    (add of a dword's high signed half)
+//   mode 2  v_add_u32_sdwa, sext WORD_0    (add of a dword's low signed half)
+//   mode 3  v_bfe_i32                      (signed 16-bit field extract)
+//   mode 4  v_pk_add_u16                   (two 16-bit adds)
+//   mode 5  v_add3_u32                     (two int32 adds)
+//   mode 6  v_perm_b32                     (byte permute)
+//   mode 7  v_dot2_i32_i16                 (two 16x16 products + int32 add)
+//   mode 8  v_add_u32 and v_add_u32_sdwa (sext WORD_1) alternating
+//   mode 9  v_xor_b32
+//   mode 10 v_ashrrev_i32
+template <int MODE>
+__device__ __forceinline__ void valu_op(unsigned& a, unsigned b) {
+  if constexpr (MODE == 0) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 1)
+    asm volatile("v_add_u32_sdwa %0, sext(%1), %0 dst_sel:DWORD dst_unused:UNUSED_PAD "
+                 "src0_sel:WORD_1 src1_sel:DWORD" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 2)
+    asm volatile("v_add_u32_sdwa %0, sext(%1), %0 dst_sel:DWORD dst_unused:UNUSED_PAD "
+                 "src0_sel:WORD_0 src1_sel:DWORD" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 3) asm volatile("v_bfe_i32 %0, %1, 16, 16" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 4) asm volatile("v_pk_add_u16 %0, %0, %1" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 5) asm volatile("v_add3_u32 %0, %0, %1, %1" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 6) asm volatile("v_perm_b32 %0, %0, %1, %1" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 7) asm volatile("v_dot2_i32_i16 %0, %1, %1, %0" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 9) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(a) : "v"(b));
+  else if constexpr (MODE == 10) asm volatile("v_ashrrev_i32 %0, 16, %1" : "=v"(a) : "v"(b));
+}
+
+template <int MODE>
 __global__ void __launch_bounds__(512) valu_probe_kernel(int iters, unsigned* out) {
   unsigned a[8], b[8];
 #pragma unroll
@@ -113,7 +145,14 @@ __global__ void __launch_bounds__(512) valu_probe_kernel(int iters, unsigned* ou
 #pragma unroll
     for (int r = 0; r < 8; ++r)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[u]) : "v"(b[(u + r) & 7]));
+      for (int u = 0; u < 8; ++u) {
+        if constexpr (MODE == 8) {
+          if (u & 1) valu_op<1>(a[u], b[(u + r) & 7]);
+          else valu_op<0>(a[u], b[(u + r) & 7]);
+        } else {
+          valu_op<MODE>(a[u], b[(u + r) & 7]);
+        }
+      }
   }
   unsigned t = 0;
 #pragma unroll
@@ -145,9 +184,21 @@ int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t st
   return (int)hipGetLastError();
 }
 
-int atx_valu_probe(int blocks, int iters, unsigned* out, hipStream_t stream) {
-  if (!(blocks > 0 && iters > 0 && out)) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(valu_probe_kernel, dim3(blocks), dim3(512), 0, stream, iters, out);
+int atx_valu_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream) {
+  if (!(mode >= 0 && mode <= 10 && blocks > 0 && iters > 0 && out)) return (int)hipErrorInvalidValue;
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 1: hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 2: hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 3: hipLaunchKernelGGL(valu_probe_kernel<3>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 4: hipLaunchKernelGGL(valu_probe_kernel<4>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 5: hipLaunchKernelGGL(valu_probe_kernel<5>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 6: hipLaunchKernelGGL(valu_probe_kernel<6>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 7: hipLaunchKernelGGL(valu_probe_kernel<7>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 8: hipLaunchKernelGGL(valu_probe_kernel<8>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 9: hipLaunchKernelGGL(valu_probe_kernel<9>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    default: hipLaunchKernelGGL(valu_probe_kernel<10>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+  }
   return (int)hipGetLastError();
 }
 

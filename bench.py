@@ -68,7 +68,7 @@ def lds_probe(torch):
     lib = ctypes.CDLL(os.path.join(ROOT, "approxtorch_amd", "libatx_diag.so"))
     vp, ci = ctypes.c_void_p, ctypes.c_int
     lib.atx_lds_probe.argtypes = [ci, ci, ci, vp, vp]
-    lib.atx_valu_probe.argtypes = [ci, ci, vp, vp]
+    lib.atx_valu_probe.argtypes = [ci, ci, ci, vp, vp]
     blocks, iters = 4 * 256, 2048
     out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
@@ -99,8 +99,13 @@ def lds_probe(torch):
         ms = timed(lambda it: lib.atx_lds_probe(mode, blocks, it, out.data_ptr(), stream))
         nbytes = {7: 8, 8: 4}.get(mode, 16)
         res[name] = round(blocks * 512 * iters * 8 * nbytes / (ms * 1e-3) / 1e9, 1)
-    ms = timed(lambda it: lib.atx_valu_probe(blocks, it, out.data_ptr(), stream))
-    res["valu_int32_add_G_per_s"] = round(blocks * 512 * iters * 64 / (ms * 1e-3) / 1e9, 1)
+    for mode, name in ((0, "v_add_u32"), (1, "v_add_u32_sdwa_word1"), (2, "v_add_u32_sdwa_word0"),
+                       (3, "v_bfe_i32"), (4, "v_pk_add_u16"), (5, "v_add3_u32"),
+                       (6, "v_perm_b32"), (7, "v_dot2_i32_i16"),
+                       (8, "v_add_u32_and_sdwa_alternating"), (9, "v_xor_b32"),
+                       (10, "v_ashrrev_i32")):
+        ms = timed(lambda it: lib.atx_valu_probe(mode, blocks, it, out.data_ptr(), stream))
+        res[f"valu_{name}_G_lane_ops_per_s"] = round(blocks * 512 * iters * 64 / (ms * 1e-3) / 1e9, 1)
     return res
 
 

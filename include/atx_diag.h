@@ -34,10 +34,16 @@ extern "C" {
  * 7, 8).  out: blocks*512 uint32. */
 int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream);
 
-/* int32 VALU add rate: blocks x 512 threads, each lane running 8 independent
- * accumulator chains of iters*8 adds (64 adds per lane per iteration).
- * Adds = blocks * 512 * iters * 64.  out: blocks*512 uint32. */
-int atx_valu_probe(int blocks, int iters, unsigned* out, hipStream_t stream);
+/* VALU issue rate of one instruction form: blocks x 512 threads, each lane
+ * running 8 independent register chains of iters*8 instructions (64 per
+ * lane per iteration) of form `mode`:
+ *   0 v_add_u32;  1 v_add_u32_sdwa (sext WORD_1);  2 v_add_u32_sdwa (sext
+ *   WORD_0);  3 v_bfe_i32;  4 v_pk_add_u16;  5 v_add3_u32;  6 v_perm_b32;
+ *   7 v_dot2_i32_i16;  8 v_add_u32 and the mode-1 form alternating;
+ *   9 v_xor_b32;  10 v_ashrrev_i32.
+ * Instructions = blocks * 512 * iters * 64 (lane operations).  out:
+ * blocks*512 uint32. */
+int atx_valu_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }
