@@ -29,6 +29,14 @@ int check_geom(const atx_conv_geom& g);
 int launch_split_sum(const float* ws, int S, long long numel, int K, const uint8_t* mask,
                      const float* scale, float* out, hipStream_t stream);
 
+// fp32-class LUT GEMM (ascending-k fp32 sums, tiled over LDS tables built
+// from the transposed fp32 LUT image); out_kind ATX_OUT_F32 or
+// ATX_OUT_DEQUANT.  Arguments validated by atx_lut_gemm.
+int lut_gemm_f32_tiled(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* lutf32t, int N, int K, int L, int O, int out_kind,
+                       const float* sx, const float* sw, const float* bias, float* y,
+                       hipStream_t stream);
+
 // Grid size for grid-stride elementwise kernels.
 inline int elem_grid(long long n, int threads, int cap = 8192) {
   long long b = cdiv(n, threads);

@@ -483,6 +483,136 @@ custom_dw_kernel(const Params p) {
   stage3(p.nq - 1);
 }
 
+// ------------------------------------------------- fp32-class LUT GEMM
+// y[n,o,l] = sum_k LUT[xi][wi] for a LUT whose entries are not all integers
+// (csrc/claude/bgemm_lut_kernels.cuh:344-359 runs such LUTs through its
+// tiled mainloop in fp32).  The sum is fp32 in ascending k, the reference's
+// non-split order, so every output element is one chain of adds from 0.
+// Tiles of 2048 rows x 16 channels use the pair-table stream above with the
+// transposed fp32 LUT image as its source: lane (rg, g) adds channels
+// 4g..4g+3 of its 16 rows, tap 4j + S at sub-step S of quad j (ascending),
+// reading its row offsets from operand slot (S - rg) & 3, where the
+// rotation put that tap.  All row groups read the same table quarter at a
+// sub-step (the price of the ascending order: four-way LDS bank conflicts
+// where the integer kernel has none).
+struct F32Params {
+  const uint16_t* xt; int Rpad;
+  const uint8_t* wt; int Opad;
+  const float* tab;        // transposed fp32 LUT: tab[w * 256 + x]
+  int K, R, L, O, tiles_o, nq;
+  int out_kind;            // ATX_OUT_F32 or ATX_OUT_DEQUANT
+  const float* sx; const float* sw; const float* bias;
+  float* y;                // [N][O][L]
+};
+
+template <bool VEC>
+__global__ void __launch_bounds__(NT, 1)
+lut_f32_kernel(const F32Params p) {
+  __shared__ __align__(16) unsigned char smem[2 * QTAB];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / 4, g = lane % 4;
+  const int lb = logical_block();
+  const int to = lb % p.tiles_o;           // channel tile (consecutive blocks: same rows)
+  const int tr = lb / p.tiles_o;           // row tile
+  const int r0 = tr * RT + wave * RPW + rg * RQ;
+  const int slot_bytes = p.Rpad * 2;
+  const int xoff = (wave * RPW + rg * RQ) * 2;
+  const uint16_t* xtile = p.xt + (long long)tr * RT;
+
+  float acc[RPL][4];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+
+  auto col = [&](int j, int s, int og) {   // quad j, tap 4j + s
+    const int k = std::min(TPL * j + s, p.K - 1);
+    return p.wt + (long long)k * p.Opad + CT * to + 4 * og;
+  };
+  auto rows = [&](XRows& x, int j, int s) {
+    load_x(x, buffer_rsrc(xtile + (long long)TPL * j * p.Rpad, j < p.nq ? TPL * slot_bytes : 0),
+           xoff + ((s - rg) & 3) * slot_bytes, 0);
+  };
+  auto use = [&](auto bc, auto sc, int j, const XRows& x) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
+    constexpr int S = decltype(sc)::value;
+    if (TPL * j + S >= p.K) return;        // the last quad's taps past K
+    const unsigned gx = (unsigned)((g << 4) | (S << 6) | (B << 16));
+    float4 e[RPL];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const unsigned xd[2] = {x.v[h].x, x.v[h].y};
+#pragma unroll
+      for (int m = 0; m < RQ; ++m)
+        e[RQ * h + m] =
+            *(const float4*)(smem + (((xd[m >> 1] >> (16 * (m & 1))) & 0xffffu) ^ gx));
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      acc[r][0] += e[r].x;
+      acc[r][1] += e[r].y;
+      acc[r][2] += e[r].z;
+      acc[r][3] += e[r].w;
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(acc[r][c]));
+  };
+  auto none = [&](int) {};
+  table_stream(smem, p.tab, p.nq, col, rows, use, none, none);
+
+  // epilogue: channel o = 16 to + 4g + c, rows r0 + 64h + m
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int o = CT * to + 4 * g + c;
+    if (o >= p.O) break;
+    float sc = 0.f, b = 0.f;
+    if (p.out_kind == ATX_OUT_DEQUANT) {
+      sc = p.sx[0] * p.sw[o];
+      if (p.bias) b = p.bias[o];
+    }
+    auto fin = [&](float a) {
+      if (p.out_kind != ATX_OUT_DEQUANT) return a;
+      const float t = a * sc;
+      return p.bias ? b + t : t;
+    };
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const int rq = r0 + NRG * RQ * h;
+      if (rq >= p.R) break;
+      int n = rq / p.L, l = rq - n * p.L;
+      if constexpr (VEC) {
+        *(float4*)(p.y + ((long long)n * p.O + o) * p.L + l) =
+            make_float4(fin(acc[RQ * h][c]), fin(acc[RQ * h + 1][c]), fin(acc[RQ * h + 2][c]),
+                        fin(acc[RQ * h + 3][c]));
+      } else {
+#pragma unroll
+        for (int m = 0; m < RQ; ++m) {
+          if (rq + m < p.R) p.y[((long long)n * p.O + o) * p.L + l] = fin(acc[RQ * h + m][c]);
+          if (++l == p.L) { l = 0; ++n; }
+        }
+      }
+    }
+  }
+}
+
+// Epilogue of an empty contraction (K = 0): every sum is 0.
+__global__ void f32_empty_kernel(const F32Params p) {
+  const long long numel = (long long)p.R * p.O;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int o = (int)((i / p.L) % p.O);
+    float v = 0.f;
+    if (p.out_kind == ATX_OUT_DEQUANT) {
+      const float t = v * (p.sx[0] * p.sw[o]);
+      v = p.bias ? p.bias[o] + t : t;
+    }
+    p.y[i] = v;
+  }
+}
+
 // grad_x of a contraction over no channels.
 __global__ void zero_fill_kernel(float* __restrict__ out, long long n) {
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
@@ -515,6 +645,37 @@ static int custom_params(cg::Params& p, const uint16_t* xt, int Rpad, const uint
   p.nq = (int)cdiv(K, cg::TPL);
   return ATX_OK;
 }
+
+namespace atx {
+
+int lut_gemm_f32_tiled(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                       const float* lutf32t, int N, int K, int L, int O, int out_kind,
+                       const float* sx, const float* sw, const float* bias, float* y,
+                       hipStream_t stream) {
+  cg::F32Params p{};
+  p.xt = xt; p.Rpad = Rpad; p.wt = wt; p.Opad = Opad; p.tab = lutf32t;
+  p.K = K; p.R = N * L; p.L = L; p.O = O;
+  p.tiles_o = (int)cdiv(O, cg::CT);
+  p.nq = (int)cdiv(K, cg::TPL);
+  p.out_kind = out_kind; p.sx = sx; p.sw = sw; p.bias = bias; p.y = y;
+  const long long R = (long long)N * L;
+  if (K == 0) {
+    hipLaunchKernelGGL(cg::f32_empty_kernel, dim3(elem_grid(R * O, 256)), dim3(256), 0, stream,
+                       p);
+    return check_launch("f32_empty_kernel");
+  }
+  const long long blocks = cdiv(R, cg::RT) * p.tiles_o;
+  ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_lut_gemm: grid too large");
+  if (L % 4 == 0)
+    hipLaunchKernelGGL(cg::lut_f32_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL(cg::lut_f32_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+                       stream, p);
+  return check_launch("lut_f32_kernel");
+}
+
+}  // namespace atx
 
 extern "C" {
 

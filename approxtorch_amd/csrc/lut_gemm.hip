@@ -799,32 +799,6 @@ __global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
   }
 }
 
-// fp32-LUT fallback: one thread per output, fp32 sum in ascending k (the
-// reference's non-split order, csrc/claude/bgemm_lut_kernels.cuh:276-284).
-__global__ void lut_gemm_f32_kernel(const GemmParams p) {
-  const long long numel = (long long)p.R * p.O;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
-       i += (long long)gridDim.x * blockDim.x) {
-    const int o = (int)(i / p.R);
-    const int r = (int)(i - (long long)o * p.R);
-    float a = 0.0f;
-    for (int k = 0; k < p.K; ++k) {
-      const unsigned xi =
-          (unsigned)p.xt[(long long)operand_slot(k, r) * p.Rpad + r] >> 8;
-      const unsigned wi = p.wt[(long long)k * p.Opad + o];
-      a += p.lutf32t[wi * 256u + xi];
-    }
-    const int n = r / p.L, l = r - (r / p.L) * p.L;
-    const long long yi = ((long long)n * p.O + o) * p.L + l;
-    if (p.out_kind == ATX_OUT_DEQUANT) {
-      const float t = a * (p.sx[0] * p.sw[o]);
-      ((float*)p.y)[yi] = p.bias ? p.bias[o] + t : t;
-    } else {
-      ((float*)p.y)[yi] = a;
-    }
-  }
-}
-
 // Split plan shared by the workspace query and the launch.  sk_per > 0
 // selects the stream-K schedule (PLAN_CUS workgroups, sk_per quads each).
 struct Plan { int tiles_r, tiles_o, splits, k_chunk, sk_per, nqt, sk_dp; };
@@ -1109,10 +1083,8 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
 
   if (lut_class == ATX_LUT_F32) {
     ATX_REQUIRE(lutf32t, "atx_lut_gemm: fp32 class needs the fp32 image");
-    p.tiles_r = p.tiles_o = p.splits = 1;
-    hipLaunchKernelGGL(lut_gemm_f32_kernel, dim3(elem_grid(R * O, 256)), dim3(256),
-                       0, stream, p);
-    return check_launch("lut_gemm_f32_kernel");
+    return lut_gemm_f32_tiled(xt, Rpad, wt, Opad, lutf32t, N, K, L, O, ep.out_kind, ep.scale_x,
+                              ep.scale_w, ep.bias, (float*)y, stream);
   }
   ATX_REQUIRE(lut16t, "atx_lut_gemm: integer class needs the 16-bit image");
   const Plan pl = make_plan(N, K, L, O, KMAX_U16, ws_limit);

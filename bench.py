@@ -198,6 +198,22 @@ def lut_gemm_microbench(torch, reps=5):
         ms = s.elapsed_time(e) / reps
         out[str(K)] = round(32 * 4096 * K * 256 / (ms * 1e-3) / 1e9, 1)
         del x, w
+    # the fp32-class path (a LUT with non-integer entries: fp32 tables in
+    # LDS, ascending-k fp32 sums) on the K = 2304 shape
+    K = 2304
+    lutf = lut.float() + 0.25
+    x = torch.randint(0, 256, (32, K, 4096), generator=g, dtype=torch.uint8).cuda()
+    w = torch.randint(-128, 128, (256, K), generator=g).float().cuda()
+    ops.bgemm_fake_int8_claude(x, w, lutf)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        ops.bgemm_fake_int8_claude(x, w, lutf)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    out["fp32_class_2304"] = round(32 * 4096 * K * 256 / (ms * 1e-3) / 1e9, 1)
     return out
 
 

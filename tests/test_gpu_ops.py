@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from approxtorch_amd.backend import _lib as LB
 from approxtorch_amd.backend import ops
 from oracle import oracle as O
 
@@ -213,6 +214,41 @@ def test_fp32_lut_fallback_matches_sequential_fp32():
     y = ops.bgemm_fake_int8_claude(t(xi), t(w), t(lut))
     want = O.lut_gemm_f32(xi, (w + 128).astype(np.uint8), lut)
     assert np.array_equal(y.cpu().numpy(), want)          # same ascending-k fp32 order
+
+
+F32_SHAPES = [(2, 100, 37, 11), (3, 9, 64, 40), (1, 257, 4100, 33), (2, 4, 100, 16),
+              (1, 3, 2051, 17), (2, 0, 10, 5)]
+
+
+@pytest.mark.parametrize("shape", F32_SHAPES)
+def test_fp32_lut_tiled_kernel(shape):
+    """The tiled fp32-class path (LDS tables from the fp32 image, ascending
+    k) equals the sequential fp32 sum bit for bit, through row tiles, ragged
+    channel tiles, K not a multiple of 4, L % 4 != 0 and K = 0, and its
+    dequant epilogue rounds like sx * sw[o] * y + bias in fp32."""
+    N, K, Lc, Oc = shape
+    r = gen(40 + K)
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = (r.standard_normal(65536) * 1000).astype(np.float32)
+    want = O.lut_gemm_f32(xi, wi, lut)
+    Rpad = LB.round_up(max(N * Lc, 1), LB.ROW_TILE)
+    xt = torch.zeros((max(LB.operand_rows(K), 1), Rpad), dtype=torch.int16, device=DEV)
+    xg = t(xi)
+    if K:
+        LB.call("atx_pack_x_u8", LB.ptr(xg), N, K, Lc, LB.ptr(xt), Rpad, LB.stream_of(xg))
+    _, wt, Opad = ops._pack_w(t(wi), 0)
+    lt = t(lut)
+    y = torch.full((N, Oc, Lc), float("nan"), device=DEV)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, Lc, Oc, lt, LB.ATX_OUT_F32, y)
+    assert np.array_equal(y.cpu().numpy(), want)
+    sx = np.float32([0.37])
+    sw = (r.random(Oc) + 0.5).astype(np.float32)
+    bias = r.standard_normal(Oc).astype(np.float32)
+    y2 = torch.full((N, Oc, Lc), float("nan"), device=DEV)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, Lc, Oc, lt, LB.ATX_OUT_DEQUANT, y2, t(sx), t(sw), t(bias))
+    want2 = want * (sx[0] * sw)[None, :, None] + bias[None, :, None]
+    assert np.array_equal(y2.cpu().numpy(), want2.astype(np.float32))
 
 
 def test_lut_cache_tracks_in_place_updates():
