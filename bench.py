@@ -42,7 +42,7 @@ COPY_BYTES = 512 << 20               # --calibrate-copy: bytes read and written 
 # reads per byte of the 512 MiB copy in that run.  None = not measured.
 # profiles/lut_gemm_hbm_traffic.md holds the counter readings (copy factors:
 # FETCH 0.500, WRITE 1.000).
-GEMM_TRAFFIC = {"c3": 759738368, "c4": 203479040}
+GEMM_TRAFFIC = {"c3": 756970866, "c4": 199631659}
 
 
 def parse():
@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c4", choices=["c2", "c4", "c5", "c3"])
+    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c4", "c5", "c3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=4)
@@ -311,6 +311,8 @@ def main():
         calibrate_copy(torch)
     if args.workload == "c3":
         return main_c3(torch, args)
+    if args.workload == "c1":
+        return main_c1(torch, args)
     name = args.workload
     model, opt, x, y, cfg = workloads.build_training_workload(name, dev)
     macs_fwd = workloads.conv_lut_macs(model, tuple(x.shape))
@@ -424,6 +426,77 @@ def main_c3(torch, args):
         result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_c3(torch)
+    print(json.dumps(result), flush=True)
+
+
+def c1_layer(torch):
+    """Config 1: one 3x3 64->64 conv (stride 1, pad 1, kaiming-normal weights,
+    seed 0) converted to Conv2d_int8 with the exact int8 product LUT; input
+    [8,64,32,32] ~ N(0,1).  The scales are set by one training-mode forward
+    (EMA), then the layer runs in eval mode (fixed scales)."""
+    import torch.nn as nn
+    from approxtorch_amd import workloads
+    from approxtorch_amd.convert_model import convert_model
+    torch.manual_seed(0)
+    conv = nn.Conv2d(64, 64, 3, stride=1, padding=1, bias=False)
+    nn.init.kaiming_normal_(conv.weight)
+    lut = torch.from_numpy(workloads.lut_exact_int8())
+    x = torch.randn(8, 64, 32, 32, generator=torch.Generator().manual_seed(0))
+    return convert_model(conv, lut, qtype="int8", ignore_first_conv=False,
+                         scale_momentum=1.0), x
+
+
+def main_c1(torch, args):
+    layer, x = c1_layer(torch)
+    layer = layer.cuda().train()
+    xg = x.cuda()
+    with torch.no_grad():
+        layer(xg)                      # sets scale_x from the input (momentum 1)
+        layer.eval()
+        for _ in range(max(args.warmup, 1)):
+            layer(xg)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            layer(xg)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    macs = 8 * 32 * 32 * 64 * 576
+    result = {
+        "metric": "LUT-MAC/s (G), config 1 (one approximate 3x3 conv 64->64 forward, [8,64,32,32])",
+        "value": round(macs * args.steps / dt / 1e9, 1),
+        "unit": "GLUT-MAC/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32 LUT sums (int8 operands), fp32 dequant",
+        "data": "synthetic (seeded N(0,1) input, kaiming-normal weights, exact int8 LUT)",
+        "config": {"workload": "c1: Conv2d_int8 3x3 64->64 forward, eval mode, im2col GEMM "
+                               "M=8192 N=64 K=576 + dequant", "lut_macs_per_step": macs,
+                   "parallelism": "single GPU"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import torch_cpu
+        threads = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        cpu_layer = torch_cpu.LUTConv2dCPU(layer).eval()
+        reps = 10
+        with torch.no_grad():
+            cpu_layer(x)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                cpu_layer(x)
+            dtc = (time.perf_counter() - t0) / reps
+        result["cpu_baseline"] = {
+            "value": round(macs / dtc / 1e9, 4), "unit": "GLUT-MAC/s", "cores": threads,
+            "kind": "port",
+            "sample": f"the whole config-1 forward (unfold -> int64 LUT index -> take -> "
+                      f"sum -> dequant, oracle/torch_cpu.py), mean of {reps}: "
+                      f"{dtc * 1e3:.0f} ms"}
     print(json.dumps(result), flush=True)
 
 
