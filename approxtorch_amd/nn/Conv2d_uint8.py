@@ -170,26 +170,27 @@ class Conv2d_uint8(nn.Module):
             self.scale_w.copy_(scale_w)
             self.zero_w.copy_(zero_w)
 
+    # Checkpoint compatibility (nn/Conv2d_uint8.py:195-223): a checkpoint
+    # holding only the min/max statistics gets its qparams derived from them
+    # (and they are not reported missing); a stored zero point must be an
+    # integer inside its quantized range.
+    _QPARAM_FIELDS = ('scale_x', 'zero_x', 'scale_w', 'zero_w')
+
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict,
                               missing_keys, unexpected_keys, error_msgs):
-        # checkpoints with only min/max statistics (nn/Conv2d_uint8.py:195-223)
-        qparam_names = ('scale_x', 'zero_x', 'scale_w', 'zero_w')
-        legacy_stats_only = all(prefix + name not in state_dict for name in qparam_names)
+        qparam_keys = {prefix + f for f in self._QPARAM_FIELDS}
+        derive = qparam_keys.isdisjoint(state_dict.keys())
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict,
                                       missing_keys, unexpected_keys, error_msgs)
-        if legacy_stats_only:
+        if derive:
             self._reset_qparams_from_stats()
-            for name in qparam_names:
-                key = prefix + name
-                if key in missing_keys:
-                    missing_keys.remove(key)
-        for name, hi in (('zero_x', self.qmax), ('zero_w', self.qmax_w)):
-            zero = getattr(self, name)
-            valid = (torch.isfinite(zero).all() and (zero >= self.qmin).all()
-                     and (zero <= hi).all() and torch.equal(zero, torch.round(zero)))
-            if not valid:
-                error_msgs.append(f"{prefix}{name} must contain integer-valued "
-                                  f"values in [{self.qmin}, {hi}]")
+            missing_keys[:] = [k for k in missing_keys if k not in qparam_keys]
+        for field, top in (('zero_x', self.qmax), ('zero_w', self.qmax_w)):
+            z = getattr(self, field)
+            # NaN fails z == round(z); +-inf fails the range
+            if not bool(torch.all((z == torch.round(z)) & (z >= self.qmin) & (z <= top))):
+                error_msgs.append(f"{prefix}{field} must contain integer-valued "
+                                  f"values in [{self.qmin}, {top}]")
 
     def _update_scale(self, x):
         """min/max EMA of the activations, then qparams, on the device; MIN/MAX
