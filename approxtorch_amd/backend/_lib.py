@@ -59,6 +59,8 @@ _SIGS = {
     "atx_tap_sum_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_tap_sum": (c_int, [c_vp, c_int, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_bwd": (c_int, [c_vp, ConvGeom, c_vp, c_vp]),
+    "atx_uint8_dequant": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                  c_vp, c_int, c_vp]),
     "atx_reduce_workspace_bytes": (c_ll, []),
     "atx_absmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp]),
     "atx_minmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_vp]),

@@ -529,6 +529,19 @@ def tap_sum(img: Tensor, g, pad_dev=None) -> Tensor:
     return out
 
 
+def uint8_dequant(y: Tensor, xsum: Tensor, wsum: Tensor, zero_x: Tensor, zero_w: Tensor,
+                  scale_x: Tensor, scale_w: Tensor, bias, K: int) -> Tensor:
+    """In place on y [N, O, L] (raw LUT sums of a uint8 conv): the zero-point
+    correction and dequant of nn/Conv2d_uint8.py:308-325 in one pass."""
+    N, O, Lc = y.shape
+    tensors = [y, xsum, wsum, zero_x, zero_w, scale_x, scale_w]
+    if not all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() for t in tensors):
+        raise RuntimeError("uint8_dequant: all operands must be contiguous CUDA float32")
+    L.call("atx_uint8_dequant", L.ptr(y), N, O, Lc, L.ptr(xsum), L.ptr(wsum), L.ptr(zero_x),
+           L.ptr(zero_w), L.ptr(scale_x), L.ptr(scale_w), L.ptr(bias), K, L.stream_of(y))
+    return y
+
+
 def tap_sum_backward(go: Tensor, g) -> Tensor:
     goc = go.contiguous()
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)

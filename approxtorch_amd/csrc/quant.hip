@@ -378,6 +378,57 @@ __global__ void weight_stats_kernel(const float* __restrict__ w, long long inner
   }
 }
 
+// Zero-point correction and dequant of a uint8 conv's raw LUT sums, in
+// place: y[n,o,l] = ((((y - zw[o]*xs[n,l]) - zx*ws[o]) + (K*zx)*zw[o]) *
+// (sx*sw[o])) [+ bias[o]], the fp32 operations of nn/Conv2d_uint8.py:308-325
+// in their order (xs = the taps' sum of q_x, ws[o] = sum_k q_w[o,k]).  VEC:
+// L % 4 == 0, four positions of one (n, o) per thread.
+template <bool VEC>
+__global__ void uint8_dequant_kernel(float* __restrict__ y, long long rows, int O, int L,
+                                     const float* __restrict__ xs,
+                                     const float* __restrict__ ws,
+                                     const float* __restrict__ zx,
+                                     const float* __restrict__ zw,
+                                     const float* __restrict__ sx,
+                                     const float* __restrict__ sw,
+                                     const float* __restrict__ bias, float K) {
+  const float z = zx[0];
+  const float kz = K * z;
+  const float s0 = sx[0];
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  const int W = VEC ? 4 : 1;
+  const long long per_row = L / W;                      // work items per (n, o) row
+  const long long total = rows * per_row;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const long long row = i / per_row;                  // n * O + o
+    const int l = (int)(i - row * per_row) * W;
+    const int o = (int)(row % O);
+    const long long n = row / O;
+    const float zo = zw[o], wo = z * ws[o], ko = kz * zo, so = s0 * sw[o];
+    const float b = bias ? bias[o] : 0.f;
+    float v[4], x[4];
+    float* yp = y + row * L + l;
+    const float* xp = xs + n * L + l;
+    if constexpr (VEC) {
+      const float4 a = *(const float4*)yp, c = *(const float4*)xp;
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      x[0] = c.x; x[1] = c.y; x[2] = c.z; x[3] = c.w;
+    } else {
+      v[0] = yp[0]; x[0] = xp[0];
+    }
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      float t = v[e] - zo * x[e];
+      t = t - wo;
+      t = t + ko;
+      t = t * so;
+      v[e] = bias ? b + t : t;
+    }
+    if constexpr (VEC) *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+    else yp[0] = v[0];
+  }
+}
+
 }  // namespace atx
 
 using namespace atx;
@@ -549,6 +600,26 @@ int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32, flo
   hipLaunchKernelGGL(weight_stats_kernel, dim3(O), dim3(EW), 0, stream, w, inner, 2,
                      (float)qmax, m32, om32, scale_w, zero_w, w_min, w_max);
   return check_launch("weight_stats_kernel");
+}
+
+int atx_uint8_dequant(float* y, int N, int O, int L, const float* xsum, const float* wsum,
+                      const float* zero_x, const float* zero_w, const float* scale_x,
+                      const float* scale_w, const float* bias, int K, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && O >= 0 && L >= 0 && K >= 0, "atx_uint8_dequant: negative size");
+  const long long rows = (long long)N * O;
+  if (rows * L == 0) return ATX_OK;
+  ATX_REQUIRE(y && xsum && wsum && zero_x && zero_w && scale_x && scale_w,
+              "atx_uint8_dequant: null pointer");
+  const bool vec = L % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)xsum & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(uint8_dequant_kernel<true>, dim3(elem_grid(rows * L / 4, EW)), dim3(EW),
+                       0, stream, y, rows, O, L, xsum, wsum, zero_x, zero_w, scale_x, scale_w,
+                       bias, (float)K);
+  else
+    hipLaunchKernelGGL(uint8_dequant_kernel<false>, dim3(elem_grid(rows * L, EW)), dim3(EW),
+                       0, stream, y, rows, O, L, xsum, wsum, zero_x, zero_w, scale_x, scale_w,
+                       bias, (float)K);
+  return check_launch("uint8_dequant_kernel");
 }
 
 }  // extern "C"

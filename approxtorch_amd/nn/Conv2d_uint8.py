@@ -16,7 +16,7 @@ import torch.distributed as dist
 import torch.nn as nn
 from torch.nn.modules.utils import _pair
 
-from . import bgemm_uint8, quantization
+from . import bgemm_uint8
 from ..backend import _lib as L
 from ..backend import ops
 from .Conv2d_int8 import _bump, _check_stat_inputs, _ema_coeffs
@@ -232,47 +232,16 @@ class Conv2d_uint8(nn.Module):
         _bump(self.w_min, self.w_max, self.scale_w, self.zero_w)
 
     def forward(self, x: torch.Tensor):
-        B, C, H, W = x.shape
-        O, _, kH, kW = self.weight.shape
-        sH, sW = self.stride
-        pH, pW = self.padding
-        dH, dW = self.dilation
-        OH = (H + 2 * pH - dH * (kH - 1) - 1) // sH + 1
-        OW = (W + 2 * pW - dW * (kW - 1) - 1) // sW + 1
-
+        kH, kW = self.weight.shape[2:]
         if self.training and self.update_scale:
             self._update_scale(x)
             self._update_scale_w()
 
-        scale_x, zero_x = self.scale_x, self.zero_x
-        scale_w, zero_w = self.scale_w, self.zero_w
-
-        xq = quantization.static_quantize_uint8(x, scale_x, zero_x, self.qmin, self.qmax)
-        wq = quantization.static_quantize_uint8(self.weight, scale_w, zero_w, self.qmin,
-                                                self.qmax_w, ch_axis=0)
-        wu = wq.view(O, -1)
+        # fake-quant, LUT conv, zero-point correction and dequant in one
+        # Function (the composition of nn/Conv2d_uint8.py:257-325, with the
+        # same values and gradients; see bgemm_uint8._conv2d_uint8_fused)
         geom = ((kH, kW), self.stride, self.padding, self.dilation, self.groups)
-
-        # LUT sum of the raw uint8 values; padded taps read z_x.
-        if self.grad == 'lre':
-            y = bgemm_uint8.conv2d_uint8_lre(xq, wu, self.lut, self.dx, self.dw, zero_x, geom)
-        elif self.grad == 'custom':
-            y = bgemm_uint8.conv2d_uint8_custom(xq, wu, self.lut, self.dx, self.dw, zero_x,
-                                                geom)
-        else:
-            y = bgemm_uint8.conv2d_uint8_ste(xq, wu, self.lut, zero_x, geom)
-
-        # zero-point correction (differentiable through xsum / wsum)
-        Kdim = wu.shape[1]
-        xsum = bgemm_uint8.tap_sum(xq, zero_x, geom)             # (B, L)
-        wsum = wu.sum(dim=1)                                     # (O,)
-        zw = zero_w.view(1, -1, 1)
-        y = y - zw * xsum.unsqueeze(1) - (zero_x * wsum).view(1, -1, 1) + Kdim * zero_x * zw
-
-        y = y.view(B, O, OH, OW)
-        s = (scale_x * scale_w).view(1, -1, 1, 1)
-        if self.bias is not None:
-            y = torch.addcmul(self.bias.view(1, -1, 1, 1), y, s)
-        else:
-            y = y * s
-        return y
+        tx, tw = (self.dx, self.dw) if self.grad in ('lre', 'custom') else (None, None)
+        return bgemm_uint8.conv2d_uint8_fused(x, self.weight, self.bias, self.scale_x,
+                                              self.zero_x, self.scale_w, self.zero_w, self.lut,
+                                              tx, tw, self.grad, geom, self.qmax_w)

@@ -16,7 +16,8 @@ from ..backend import ops
 from .bgemm_int8 import _gemm_grads, decode_table
 
 __all__ = ["bgemm_uint8", "bgemm_uint8_ste", "bgemm_uint8_lre", "bgemm_uint8_custom",
-           "conv2d_uint8_ste", "conv2d_uint8_lre", "conv2d_uint8_custom", "tap_sum"]
+           "conv2d_uint8_ste", "conv2d_uint8_lre", "conv2d_uint8_custom", "tap_sum",
+           "conv2d_uint8_fused"]
 
 
 class _bgemm_uint8_base(Function):
@@ -221,3 +222,86 @@ class _tap_sum(Function):
 
 def tap_sum(x, zero_x, geom):
     return _tap_sum.apply(x, zero_x, geom)
+
+
+# ---------------------------------------------------------- fused layer path
+class _conv2d_uint8_fused(Function):
+    """Conv2d_uint8's forward and backward as one Function: the composition of
+    nn/Conv2d_uint8.py:257-325 (static fake-quant of x and W, the LUT conv of
+    the raw uint8 values with z_x-padded taps, the zero-point correction
+    y - z_w*sum_k q_x - z_x*sum_k q_w + K*z_x*z_w and the dequant by
+    scale_x * scale_w), with no fp32 quantized image and no [N,O,L]
+    temporaries:
+      forward:  x -> uint8 image + mask, W -> uint8 GEMM operand + mask;
+                implicit im2col LUT conv; the taps' sums of q_x (tap_sum) and
+                sum_k q_w; one in-place pass for correction and dequant;
+      backward: g' = go * (scale_x * scale_w[o]) feeds the estimator's
+                gradient kernels; the zero-point terms add -sum_o g' z_w[o]
+                to every tap of a position (tap_sum's backward) and
+                -z_x * sum_{n,l} g' to every tap of a channel; then the two
+                fake-quant STEs.
+    kind: 'ste' | 'lre' | 'custom'; tx / tw: the estimator's tables (STE:
+    None, the identity decode table is used)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, scale_x, zero_x, scale_w, zero_w, lut, tx, tw, kind, geom,
+                qmax_w):
+        g = _geom(x, geom)
+        O = weight.size(0)
+        K = g.C * g.KH * g.KW
+        _, mask_x, q8 = ops.fakequant_per_tensor(x, scale_x, 0, 255, zero_point=zero_x,
+                                                  want_q=False, q8_dtype=torch.uint8)
+        _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, 0, qmax_w,
+                                                            zero_point=zero_w, offset=0,
+                                                            want_wt=True)
+        y, _, (xt, Rpad) = ops.conv_forward(q8, wq, lut, g, 0, 0, pad_dev=zero_x,
+                                            packed_w=(wq, wt, Opad), return_operand=True)
+        xsum = ops.tap_sum(q8, g, pad_dev=zero_x)
+        wsum = wq.sum(dim=1, dtype=torch.float32)
+        b = None if bias is None else bias.detach().contiguous()
+        ops.uint8_dequant(y, xsum, wsum, zero_x.contiguous(), zero_w.contiguous(),
+                          scale_x.contiguous(), scale_w.contiguous(), b, K)
+        ctx.save_for_backward(xt, mask_x, wq, mask_w.view(O, K), scale_x, zero_x, scale_w,
+                              zero_w, tx, tw)
+        ctx.g, ctx.rpad, ctx.kind = g, Rpad, kind
+        ctx.has_bias, ctx.wshape = bias is not None, weight.shape
+        return y.view(g.N, O, g.OH, g.OW)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xt, mask_x, wq, mask_w, sx, zx, sw, zw, tx, tw = ctx.saved_tensors
+        g = ctx.g
+        O, K = wq.shape
+        Lc = g.OH * g.OW
+        go = grad_output.contiguous().view(g.N, O, Lc)
+        gp = go * (sx * sw).view(1, -1, 1)                  # d loss / d corrected sum
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gx = gw = gb = None
+        if ctx.kind == 'custom':
+            grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, gp, tx if need_x else None,
+                                              tw if need_w else None, g.N, K, Lc)
+            grad_q = ops.col2im(grad_col, g) if need_x else None
+        else:
+            if ctx.kind == 'ste':
+                tx = tw = decode_table(gp.device, signed=False)
+            grad_q = ops.conv_backward_data(gp, wq, tx.contiguous(), g) if need_x else None
+            gw_q = ops.conv_backward_weight_rows(gp, (xt, ctx.rpad), tw.contiguous(), g, O) \
+                if need_w else None
+        if need_x:
+            gxs = (gp * zw.view(1, -1, 1)).sum(dim=1).neg_()        # [N, L]
+            grad_q += ops.tap_sum_backward(gxs, g)
+            gx = ops.fakequant_per_tensor_backward(grad_q, mask_x, sx)
+        if need_w:
+            gws = gp.sum(dim=(0, 2)).mul_(zx).neg_()                # [O]
+            gw_q += gws.view(-1, 1)
+            gw = ops.fakequant_per_tensor_backward(gw_q, mask_w, sw, channels=O,
+                                                   inner=K).view(ctx.wshape)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            gb = go.sum(dim=(0, 2))
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
+
+
+def conv2d_uint8_fused(x, weight, bias, scale_x, zero_x, scale_w, zero_w, lut, tx, tw, kind,
+                       geom, qmax_w):
+    return _conv2d_uint8_fused.apply(x, weight, bias, scale_x, zero_x, scale_w, zero_w, lut, tx,
+                                     tw, kind, geom, qmax_w)

@@ -235,6 +235,17 @@ int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask,
  * atx_tap_sum_workspace_bytes(g) (per-64-channel sums).  And its backward
  * img[n,c,h,w] = sum of go[n,l] over the taps reading (h,w).  The uint8
  * zero-point correction term sum_k q_x of nn/Conv2d_uint8.py:308-315. */
+/* Zero-point correction and dequant of a uint8 conv's raw LUT sums y
+ * [N,O,L], in place:
+ *   y = ((y - zero_w[o]*xsum[n,l] - zero_x*wsum[o] + K*zero_x*zero_w[o])
+ *        * (scale_x * scale_w[o])) (+ bias[o], nullable),
+ * each fp32 operation in that order; xsum = atx_tap_sum of the uint8 image,
+ * wsum[o] = sum_k q_w[o,k].  Replaces the elementwise tail of
+ * nn/Conv2d_uint8.py:308-325. */
+int atx_uint8_dequant(float* y, int N, int O, int L, const float* xsum, const float* wsum,
+                      const float* zero_x, const float* zero_w, const float* scale_x,
+                      const float* scale_w, const float* bias, int K, hipStream_t stream);
+
 long long atx_tap_sum_workspace_bytes(atx_conv_geom g);
 int atx_tap_sum(const void* img, int dtype, atx_conv_geom g, const float* pad_dev,
                 float* out, float* workspace, hipStream_t stream);

@@ -161,6 +161,62 @@ def test_conv2d_uint8_forward_backward(kind, gi):
     close(layer.bias.grad, gb, ab)
 
 
+@pytest.mark.parametrize("kind", ["ste", "lre", "custom"])
+@pytest.mark.parametrize("shape", [(1, 1, 0, 7, 9), (3, 2, 1, 12, 12)])
+def test_conv2d_uint8_fused_matches_composition(kind, shape):
+    """The fused layer path (one Function: uint8 image, in-place zero-point
+    correction and dequant, fused backward terms) against the reference's
+    composition of the public pieces (static_quantize_uint8, the conv-level
+    Function, tap_sum and the correction as torch ops, nn/Conv2d_uint8.py:
+    257-325): forward and every gradient, without bias, for a 1x1 conv with
+    L % 4 != 0 and a strided 3x3 conv."""
+    from approxtorch_amd.nn import bgemm_uint8, quantization
+    k, s, p, H, W = shape
+    torch.manual_seed(21)
+    v = np.arange(256)
+    lut = torch.from_numpy(((v[:, None] * v[None, :]) & ~63).astype(np.float32).reshape(-1)).to(DEV)
+    dx, dw = tables(kind, lut.cpu().numpy(), "uint8")
+    tx = None if dx is None else torch.from_numpy(dx).to(DEV)
+    tw = None if dw is None else torch.from_numpy(dw).to(DEV)
+    layer = at.nn.Conv2d_uint8(6, 20, k, lut, grad=kind, dx=tx, dw=tw, bias=False, stride=s,
+                               padding=p, weight_bits=4 if kind == "custom" else 8).to(DEV)
+    x = torch.randn(2, 6, H, W, device=DEV) + 0.3
+    layer.train()
+    with torch.no_grad():
+        layer(x)
+    layer.eval()
+    x1 = x.clone().requires_grad_()
+    y1 = layer(x1)
+    go = torch.randn_like(y1)
+    y1.backward(go)
+    g1x, g1w = x1.grad.clone(), layer.weight.grad.clone()
+    layer.weight.grad = None
+
+    x2 = x.clone().requires_grad_()
+    geom = ((k, k), layer.stride, layer.padding, layer.dilation, 1)
+    xq = quantization.static_quantize_uint8(x2, layer.scale_x, layer.zero_x, 0, 255)
+    wq = quantization.static_quantize_uint8(layer.weight, layer.scale_w, layer.zero_w, 0,
+                                            layer.qmax_w, ch_axis=0)
+    wu = wq.view(20, -1)
+    if kind == "ste":
+        y = bgemm_uint8.conv2d_uint8_ste(xq, wu, lut, layer.zero_x, geom)
+    elif kind == "lre":
+        y = bgemm_uint8.conv2d_uint8_lre(xq, wu, lut, tx, tw, layer.zero_x, geom)
+    else:
+        y = bgemm_uint8.conv2d_uint8_custom(xq, wu, lut, tx, tw, layer.zero_x, geom)
+    xsum = bgemm_uint8.tap_sum(xq, layer.zero_x, geom)
+    zw = layer.zero_w.view(1, -1, 1)
+    y = y - zw * xsum.unsqueeze(1) - (layer.zero_x * wu.sum(dim=1)).view(1, -1, 1) \
+        + wu.shape[1] * layer.zero_x * zw
+    y2 = y.view_as(y1) * (layer.scale_x * layer.scale_w).view(1, -1, 1, 1)
+    y2.backward(go)
+    # identical fp32 operations in the same order: the forward is bitwise equal
+    assert torch.equal(y1, y2)
+    for a, b in ((g1x, x2.grad), (g1w, layer.weight.grad)):
+        tol = 1e-5 * b.abs().max().item() + 1e-4
+        assert (a - b).abs().max().item() <= tol
+
+
 def test_train_mode_ema_matches_reference_rules():
     torch.manual_seed(3)
     lut = torch.from_numpy(perturbed_lut(3)).to(DEV)
