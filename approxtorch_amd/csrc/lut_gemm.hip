@@ -89,6 +89,11 @@ struct GemmParams {
   const float* lutf32t;
   int K, R, L, O;
   int k_chunk, splits, tiles_r, tiles_o;
+  // Rows per tile: RT, or fewer (a multiple of RPW) when R / RT leaves the
+  // last tile mostly empty, so every tile carries about R / tiles_r rows.
+  // Waves whose rows lie past the tile (wave * RPW >= rt) build tables but
+  // accumulate and store nothing.
+  int rt;
   int out_kind;                 // ATX_OUT_*; splits > 1 => raw int32 partials
   void* y;
   long long split_stride;       // elements per partial slice
@@ -515,7 +520,9 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
   const unsigned gbase = (unsigned)((rg << 6) | (g << 4));
 
   const int xoff = (wave * RPW + rg * RQ) * 2;          // lane's first quad, bytes
-  const uint16_t* __restrict__ xtile = p.xt + (long long)tr * RT;
+  const uint16_t* __restrict__ xtile = p.xt + (long long)tr * p.rt;
+  // wave-uniform: does this wave own rows of the tile?
+  const bool active = __builtin_amdgcn_readfirstlane(wave) * RPW < p.rt;
   const uint8_t* __restrict__ wcol = p.wt + o0 + og * 8;
   const __amdgpu_buffer_rsrc_t lutr = buffer_rsrc(p.lut16t, 256 * 256 * 2);
   // Zero-length view of the image: its loads are out of range and return 0,
@@ -585,13 +592,15 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
       Rows rn;
       load_rows(rn, sigma + 5 < n ? lutr : lutz, wnext, lane, 256 * hw);
       __builtin_amdgcn_sched_barrier(0);
-      use_table<SIGNED>(acc, smem, xcur, quarter_mask<S, B>(gbase));
-      // Pin the adds here: left free, the compiler sinks them into later
-      // steps, past the table write that waits for this step's loads.
+      if (active) {
+        use_table<SIGNED>(acc, smem, xcur, quarter_mask<S, B>(gbase));
+        // Pin the adds here: left free, the compiler sinks them into later
+        // steps, past the table write that waits for this step's loads.
 #pragma unroll
-      for (int jj = 0; jj < RPL; ++jj)
+        for (int jj = 0; jj < RPL; ++jj)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
+          for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
+      }
       __builtin_amdgcn_sched_barrier(0);
       write_table<SIGNED>(smem + S * 64 + (B ? 0 : QTAB), rows, wb0);  // table sigma+4, other buffer
       rows = rn;
@@ -644,6 +653,7 @@ lut_gemm_kernel(const GemmParams p) {
   const int rg = lane / CG, g = lane % CG;
   const int lb = logical_block();
   int acc[RPL][8];
+  const bool has_rows = wave * RPW < p.rt;   // the wave's rows lie in the tile
 
   if (p.sk_per == 0) {
     int l = lb;
@@ -653,8 +663,9 @@ lut_gemm_kernel(const GemmParams p) {
     const int kb = s * p.k_chunk;
     lut_tile<SIGNED>(p, smem, tr, to, kb, min(p.K, kb + p.k_chunk), acc);
     // ---- epilogue: registers -> HBM, every wave at once (no LDS staging).
-    const int r0 = tr * RT + wave * RPW + rg * RQ;       // this lane's first quad
+    const int r0 = tr * p.rt + wave * RPW + rg * RQ;     // this lane's first quad
     const int oc = to * OT + g * 8;
+    if (!has_rows) return;
     if (p.splits > 1)
       store_tile<ATX_OUT_I32>(p, (int*)p.y + (long long)s * p.split_stride, acc, r0, oc);
     else if (p.out_kind == ATX_OUT_I32)
@@ -672,8 +683,9 @@ lut_gemm_kernel(const GemmParams p) {
     const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
     __syncthreads();                         // the previous segment's tables are read
     lut_tile<SIGNED>(p, smem, tr, to, 0, p.K, acc);
-    const int r0 = tr * RT + wave * RPW + rg * RQ;
+    const int r0 = tr * p.rt + wave * RPW + rg * RQ;
     const int oc = to * OT + g * 8;
+    if (!has_rows) continue;
     if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
     else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
     else store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
@@ -689,8 +701,10 @@ lut_gemm_kernel(const GemmParams p) {
     const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
     __syncthreads();                         // the previous segment's tables are read
     lut_tile<SIGNED>(p, smem, tr, to, TPL * q0, min(p.K, TPL * q1), acc);
-    if (q0 == 0 && q1 == p.nqt) {
-      const int r0 = tr * RT + wave * RPW + rg * RQ;
+    if (!has_rows) {
+      // nothing to store or add (the slots' rows of this wave stay zero)
+    } else if (q0 == 0 && q1 == p.nqt) {
+      const int r0 = tr * p.rt + wave * RPW + rg * RQ;
       const int oc = to * OT + g * 8;
       if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
       else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
@@ -735,8 +749,9 @@ sk_finish_kernel(const GemmParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = slot[sk_index(j, e, tid)];
   const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
-  const int r0 = tr * RT + wave * RPW + rg * RQ;
+  const int r0 = tr * p.rt + wave * RPW + rg * RQ;
   const int oc = to * OT + g * 8;
+  if (wave * RPW >= p.rt) return;            // rows past the tile
   if (p.out_kind == ATX_OUT_I32) store_tile<ATX_OUT_I32>(p, p.y, acc, r0, oc);
   else if (p.out_kind == ATX_OUT_F32) store_tile<ATX_OUT_F32>(p, p.y, acc, r0, oc);
   else store_tile<ATX_OUT_DEQUANT>(p, p.y, acc, r0, oc);
@@ -801,7 +816,7 @@ __global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
 
 // Split plan shared by the workspace query and the launch.  sk_per > 0
 // selects the stream-K schedule (PLAN_CUS workgroups, sk_per quads each).
-struct Plan { int tiles_r, tiles_o, splits, k_chunk, sk_per, nqt, sk_dp; };
+struct Plan { int tiles_r, tiles_o, splits, k_chunk, sk_per, nqt, sk_dp, rt; };
 
 // Compute units of a full MI355X (one resident workgroup each: the kernel's
 // 8 waves hold 2 waves per SIMD at its register budget).  A constant, not a
@@ -836,6 +851,8 @@ static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit =
   Plan pl;
   const long long R = (long long)N * L;
   pl.tiles_r = (int)cdiv(R, RT);
+  // the fewest whole waves of rows that cover R in tiles_r tiles
+  pl.rt = R > 0 ? (int)std::min<long long>(RT, cdiv(cdiv(R, pl.tiles_r), RPW) * RPW) : RT;
   pl.tiles_o = (int)cdiv(O, OT);
   pl.sk_per = 0;
   pl.nqt = (int)cdiv(K, TPL);
@@ -1098,7 +1115,7 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
     const int rc = scratch(&workspace);
     if (rc != ATX_OK) return rc;
   }
-  p.tiles_r = pl.tiles_r; p.tiles_o = pl.tiles_o;
+  p.tiles_r = pl.tiles_r; p.tiles_o = pl.tiles_o; p.rt = pl.rt;
   p.splits = pl.splits; p.k_chunk = pl.k_chunk;
   const long long numel = R * O;
   if (pl.sk_per > 0) {
