@@ -60,6 +60,7 @@ struct Params {
   float* out;              // grad_x [N][K][L], or the grad_w slices [tiles_r][O][K]
   int K, R, L, O;
   int tiles_r, tiles_o, nq; // nq = quads of taps
+  int kq_chunk, kchunks;    // grad_w: quads per workgroup, workgroups per (row, channel) tile
 };
 
 // DPP helpers (quad_perm / row_shr controls of the VOP DPP encoding).
@@ -380,7 +381,10 @@ custom_dw_kernel(const Params p) {
   const int rg = lane / 4, g = lane % 4;
   const int lb = logical_block();
   const int to = lb % p.tiles_o;           // channel tile (consecutive blocks: same rows)
-  const int tr = lb / p.tiles_o;           // row tile
+  const int kc = (lb / p.tiles_o) % p.kchunks;   // chunk of tap quads
+  const int tr = lb / p.tiles_o / p.kchunks;     // row tile
+  const int j0 = kc * p.kq_chunk;          // the chunk's first quad
+  const int nsteps = min(p.kq_chunk, p.nq - j0);
   const int r0 = tr * RT + wave * RPW + rg * RQ;
   const int xoff = (wave * RPW + rg * RQ) * 2;
   const int slot_bytes = p.Rpad * 2;
@@ -396,12 +400,14 @@ custom_dw_kernel(const Params p) {
   }
   float acc[TPL][4];
 
-  auto col = [&](int j, int s, int og) {   // quad j, tap 4j + s
-    const int k = std::min(TPL * j + s, p.K - 1);
+  // quads are counted from the chunk's first quad j0
+  auto col = [&](int j, int s, int og) {   // quad j0 + j, tap 4(j0 + j) + s
+    const int k = std::min(TPL * (j0 + j) + s, p.K - 1);
     return p.wt + (long long)k * p.Opad + CT * to + 4 * og;
   };
   auto rows = [&](XRows& x, int j, int s) {
-    load_x(x, buffer_rsrc(xtile + (long long)TPL * j * p.Rpad, j < p.nq ? TPL * slot_bytes : 0),
+    load_x(x, buffer_rsrc(xtile + (long long)TPL * (j0 + j) * p.Rpad,
+                          j < nsteps ? TPL * slot_bytes : 0),
            xoff, s * slot_bytes);
   };
   auto use = [&](auto bc, auto sc, int, const XRows& x) __attribute__((always_inline)) {
@@ -468,19 +474,19 @@ custom_dw_kernel(const Params p) {
     float a = 0.f;
 #pragma unroll
     for (int w = 0; w < NWAVE; ++w) a += red2[j & 1][w * 64 + tid];
-    const int k = TPL * j + t, o = CT * to + ol;
+    const int k = TPL * (j0 + j) + t, o = CT * to + ol;
     if (k < p.K && o < p.O) slice[(long long)o * p.K + k] = a;
   };
   auto quad_begin = [&](int j) {
     if (j >= 1) stage2(j - 1);
     if (j >= 2) stage3(j - 2);
   };
-  table_stream(smem, p.tab, p.nq, col, rows, use, quad_end, quad_begin);
+  table_stream(smem, p.tab, nsteps, col, rows, use, quad_end, quad_begin);
   // drain the last two quads through stages 2 and 3
-  if (p.nq >= 2) stage3(p.nq - 2);
-  stage2(p.nq - 1);
+  if (nsteps >= 2) stage3(nsteps - 2);
+  stage2(nsteps - 1);
   __syncthreads();
-  stage3(p.nq - 1);
+  stage3(nsteps - 1);
 }
 
 // ------------------------------------------------- fp32-class LUT GEMM
@@ -643,6 +649,8 @@ static int custom_params(cg::Params& p, const uint16_t* xt, int Rpad, const uint
   p.tiles_r = (int)cdiv(R, cg::RT);
   p.tiles_o = (int)cdiv(O, cg::CT);
   p.nq = (int)cdiv(K, cg::TPL);
+  p.kq_chunk = p.nq;
+  p.kchunks = 1;
   return ATX_OK;
 }
 
@@ -725,7 +733,16 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
   if (p.R == 0)
     return launch_split_sum(nullptr, 0, numel, K, mask_w, scale_w, grad_w, stream);
   ATX_REQUIRE(xt && wt && dy && tabT && workspace, "atx_custom_grad_dw: null operand");
-  const long long blocks = (long long)p.tiles_r * p.tiles_o;
+  // Fewer (row, channel) tiles than CUs: split the tap quads over enough
+  // workgroups to fill them (each workgroup writes its own taps' entries of
+  // the row tile's slice, so no extra reduction).
+  const long long tiles = (long long)p.tiles_r * p.tiles_o;
+  if (tiles < 256 && p.nq >= 16) {
+    const int want = (int)std::min<long long>(cdiv(256, tiles), p.nq / 8);
+    p.kq_chunk = (int)cdiv(p.nq, want);
+    p.kchunks = (int)cdiv(p.nq, p.kq_chunk);
+  }
+  const long long blocks = tiles * p.kchunks;
   ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dw: grid too large");
   if (L % 4 == 0)
     hipLaunchKernelGGL(cg::custom_dw_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
