@@ -17,11 +17,12 @@
 // rows and channels 4g..4g+3 of the tile; at sub-step s of a quad it handles
 // tap 4j + ((rg + s) & 3) for all its rows (the operand's slot rotation).
 //
-//   grad_x: a workgroup owns one quad of taps and loops over the 16-channel
-//           tiles of O (tables of the next tile built while the current one
-//           is read); the 64 accumulators acc[s][row] of a lane collect its
-//           four channels, and the four lanes of a row group are summed with
-//           DPP at the end.
+//   grad_x: a workgroup owns a chunk of consecutive quads of taps and loops
+//           over (quad, 16-channel tile) steps (tables of the next step built
+//           while the current one is read); the 64 accumulators acc[s][row]
+//           of a lane collect its four channels, and after a quad's last
+//           channel tile the four lanes of a row group are summed with DPP
+//           and stored.
 //   grad_w: a workgroup owns one 16-channel tile and loops over all quads of
 //           taps with its dy values in registers; the lane's partial sums
 //           acc[s][c] are combined over the 16 row groups of a wave with DPP
@@ -246,7 +247,10 @@ __device__ __forceinline__ unsigned read_mask(int g, int rg, int s, int b) {
 }
 
 // ----------------------------------------------------------------- grad_x
-template <bool VEC>
+// MULTI: the workgroup's chunk may hold several quads (kq_chunk > 1), so the
+// flush runs inside the loop; without it the one quad is flushed after the
+// loop, which keeps the flush's registers out of the loop.
+template <bool VEC, bool MULTI>
 __global__ void __launch_bounds__(NT, 1)
 custom_dx_kernel(const Params p) {
   __shared__ __align__(16) unsigned char smem[2 * QTAB];
@@ -254,13 +258,17 @@ custom_dx_kernel(const Params p) {
   const int wave = tid >> 6, lane = tid & 63;
   const int rg = lane / 4, g = lane % 4;
   const int lb = logical_block();
-  const int j = lb % p.nq;                 // quad of taps (consecutive blocks: same rows)
-  const int tr = lb / p.nq;                // row tile
+  // A workgroup owns kq_chunk consecutive quads of taps of one row tile and
+  // streams (quad, channel tile) steps through one table pipeline, so its
+  // prologue is paid once per chunk, not once per quad.
+  const int c = lb % p.kchunks;            // chunk of quads (consecutive blocks: same rows)
+  const int tr = lb / p.kchunks;           // row tile
+  const int j0 = c * p.kq_chunk;
+  const int nsteps = MULTI ? min(p.kq_chunk, p.nq - j0) * p.tiles_o : p.tiles_o;
   const int r0 = tr * RT + wave * RPW + rg * RQ;
   const int xoff = (wave * RPW + rg * RQ) * 2;
   const int slot_bytes = p.Rpad * 2;
-  const __amdgpu_buffer_rsrc_t xs =
-      buffer_rsrc(p.xt + (long long)tr * RT + (long long)TPL * j * p.Rpad, TPL * slot_bytes);
+  const uint16_t* xtile = p.xt + (long long)tr * RT;
 
   float acc[TPL][RPL];
 #pragma unroll
@@ -274,11 +282,25 @@ custom_dx_kernel(const Params p) {
   float dyv[RPL][4];
   load_dy<VEC>(dyr, dro, p.L, 0, valid_of(0), dyv);
 
-  auto col = [&](int t, int s, int og) {    // tile t, tap 4j + s
-    const int k = std::min(TPL * j + s, p.K - 1);
-    return p.wt + (long long)k * p.Opad + CT * t + 4 * og;
+  // step t = (quad j0 + t / tiles_o, channel tile t % tiles_o)
+  auto col = [&](int t, int s, int og) {    // tap 4(j0 + t / tiles_o) + s
+    const int q = MULTI ? t / p.tiles_o : 0, to = t - q * p.tiles_o;
+    const int k = std::min(TPL * (j0 + q) + s, p.K - 1);
+    return p.wt + (long long)k * p.Opad + CT * to + 4 * og;
   };
-  auto rows = [&](XRows& x, int, int s) { load_x(x, xs, xoff, s * slot_bytes); };
+  // one quad per workgroup (!MULTI): one loop-invariant descriptor
+  const __amdgpu_buffer_rsrc_t xs0 =
+      buffer_rsrc(xtile + (long long)TPL * j0 * p.Rpad, TPL * slot_bytes);
+  auto rows = [&](XRows& x, int t, int s) {
+    if constexpr (MULTI) {
+      const int q = t / p.tiles_o;
+      load_x(x, buffer_rsrc(xtile + (long long)TPL * (j0 + q) * p.Rpad,
+                            t < nsteps ? TPL * slot_bytes : 0),
+             xoff, s * slot_bytes);
+    } else {
+      load_x(x, xs0, xoff, s * slot_bytes);
+    }
+  };
   // Reads of row quad h + 2 are issued before the FMAs of quad h, so at most
   // two quads of entries (32 registers) are in flight next to the 64
   // accumulators and 64 dy values.
@@ -323,50 +345,60 @@ custom_dx_kernel(const Params p) {
 #pragma unroll
     for (int r = 0; r < RPL; ++r) asm volatile("" : "+v"(acc[S][r]));
   };
-  auto quad_end = [&](int t) {
-    // the next tile's dy (its tables are already in the other buffer); an
-    // unconditional load (the last tile reloads itself), so the new values
-    // can take the old registers
-    const int tn = min(t + 1, p.tiles_o - 1);
-    load_dy<VEC>(dyr, dro, p.L, CT * tn, valid_of(tn), dyv);
-  };
-  auto quad_begin = [&](int) {};
-  table_stream(smem, p.tab, p.tiles_o, col, rows, use, quad_end, quad_begin);
-
-  // sum over the row group's four chunk lanes, then lane g stores slot g
-  // (tap 4j + ((rg + g) & 3)) for its 16 rows
+  // The quad j's sums: over the row group's four chunk lanes, then lane g
+  // stores slot g (tap 4j + ((rg + g) & 3)) for its 16 rows; the
+  // accumulators restart at 0.
+  auto flush = [&](int j) {
 #pragma unroll
-  for (int s = 0; s < TPL; ++s)
+    for (int s = 0; s < TPL; ++s)
 #pragma unroll
-    for (int r = 0; r < RPL; ++r) {
-      float a = acc[s][r];
-      a += dpp<QP_XOR1>(a);
-      a += dpp<QP_XOR2>(a);
-      acc[s][r] = a;
-    }
+      for (int r = 0; r < RPL; ++r) {
+        float a = acc[s][r];
+        a += dpp<QP_XOR1>(a);
+        a += dpp<QP_XOR2>(a);
+        acc[s][r] = a;
+      }
 #pragma unroll
-  for (int s = 0; s < TPL; ++s) {
-    if (s != g) continue;
-    const int k = TPL * j + ((rg + s) & 3);
-    if (k >= p.K) continue;
+    for (int s = 0; s < TPL; ++s) {
+      if (s != g) continue;
+      const int k = TPL * j + ((rg + s) & 3);
+      if (k >= p.K) continue;
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      const int rq = r0 + NRG * RQ * h;
-      if (rq >= p.R) break;
-      int n = rq / p.L, l = rq - n * p.L;
-      if constexpr (VEC) {
-        *(float4*)(p.out + ((long long)n * p.K + k) * p.L + l) =
-            make_float4(acc[s][RQ * h], acc[s][RQ * h + 1], acc[s][RQ * h + 2],
-                        acc[s][RQ * h + 3]);
-      } else {
+      for (int h = 0; h < NQ; ++h) {
+        const int rq = r0 + NRG * RQ * h;
+        if (rq >= p.R) break;
+        int n = rq / p.L, l = rq - n * p.L;
+        if constexpr (VEC) {
+          *(float4*)(p.out + ((long long)n * p.K + k) * p.L + l) =
+              make_float4(acc[s][RQ * h], acc[s][RQ * h + 1], acc[s][RQ * h + 2],
+                          acc[s][RQ * h + 3]);
+        } else {
 #pragma unroll
-        for (int m = 0; m < RQ; ++m) {
-          if (rq + m < p.R) p.out[((long long)n * p.K + k) * p.L + l] = acc[s][RQ * h + m];
-          if (++l == p.L) { l = 0; ++n; }
+          for (int m = 0; m < RQ; ++m) {
+            if (rq + m < p.R) p.out[((long long)n * p.K + k) * p.L + l] = acc[s][RQ * h + m];
+            if (++l == p.L) { l = 0; ++n; }
+          }
         }
       }
     }
-  }
+#pragma unroll
+    for (int s = 0; s < TPL; ++s)
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) acc[s][r] = 0.f;
+  };
+  auto quad_end = [&](int t) {
+    const int q = MULTI ? t / p.tiles_o : 0, to = t - q * p.tiles_o;
+    if constexpr (MULTI)
+      if (to == p.tiles_o - 1) flush(j0 + q);   // the quad's last channel tile
+    // the next step's dy (its tables are already in the other buffer); an
+    // unconditional load (the last step reloads tile 0), so the new values
+    // can take the old registers
+    const int tn = MULTI ? (to + 1 == p.tiles_o ? 0 : to + 1) : min(t + 1, p.tiles_o - 1);
+    load_dy<VEC>(dyr, dro, p.L, CT * tn, valid_of(tn), dyv);
+  };
+  auto quad_begin = [&](int) {};
+  table_stream(smem, p.tab, nsteps, col, rows, use, quad_end, quad_begin);
+  if constexpr (!MULTI) flush(j0);
 }
 
 // ----------------------------------------------------------------- grad_w
@@ -703,14 +735,32 @@ int atx_custom_grad_dx(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
     return check_launch("zero_fill_kernel");
   }
   ATX_REQUIRE(xt && wt && dy && tabT, "atx_custom_grad_dx: null operand");
-  const long long blocks = (long long)p.tiles_r * p.nq;
+  // quads per workgroup: enough (quad, channel tile) steps to amortize the
+  // pipeline's prologue (at least 16), while keeping at least 1024
+  // workgroups when there are that many quads to give out
+  {
+    const int want_steps = 16;
+    int kq = (int)std::max<long long>(1, cdiv(want_steps, p.tiles_o));
+    const long long min_blocks = 1024;
+    while (kq > 1 && (long long)p.tiles_r * cdiv(p.nq, kq) < min_blocks) --kq;
+    p.kq_chunk = std::min(kq, std::max(p.nq, 1));
+    p.kchunks = (int)cdiv(p.nq, p.kq_chunk);
+  }
+  const long long blocks = (long long)p.tiles_r * p.kchunks;
   ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dx: grid too large");
-  if (L % 4 == 0)
-    hipLaunchKernelGGL(cg::custom_dx_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
-                       stream, p);
+  const bool multi = p.kq_chunk > 1;
+  if (L % 4 == 0 && multi)
+    hipLaunchKernelGGL((cg::custom_dx_kernel<true, true>), dim3((unsigned)blocks), dim3(cg::NT),
+                       0, stream, p);
+  else if (L % 4 == 0)
+    hipLaunchKernelGGL((cg::custom_dx_kernel<true, false>), dim3((unsigned)blocks),
+                       dim3(cg::NT), 0, stream, p);
+  else if (multi)
+    hipLaunchKernelGGL((cg::custom_dx_kernel<false, true>), dim3((unsigned)blocks),
+                       dim3(cg::NT), 0, stream, p);
   else
-    hipLaunchKernelGGL(cg::custom_dx_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT), 0,
-                       stream, p);
+    hipLaunchKernelGGL((cg::custom_dx_kernel<false, false>), dim3((unsigned)blocks),
+                       dim3(cg::NT), 0, stream, p);
   return check_launch("custom_dx_kernel");
 }
 
