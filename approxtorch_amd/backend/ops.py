@@ -716,12 +716,14 @@ def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, 
 
 # --------------------------------------------------------- custom backward
 def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int, Lc: int,
-                 mask_w=None, scale_w=None):
+                 mask_w=None, scale_w=None, wbase=None):
     """(grad_x [N,K,L] or None, grad_w [O,K] or None) of the pair-table
     estimator from the LUT GEMM's row-offset operand (xt, Rpad) and the uint8
     weight index image wq [O,K]; dx_lut / dw_lut are fp32 [65536] tables
     indexed [x*256 + w] (None skips that gradient).  mask_w / scale_w fuse
-    the per-channel weight fake-quant STE into grad_w."""
+    the per-channel weight fake-quant STE into grad_w.  wbase: the caller
+    guarantees every index of wq lies in [wbase, wbase + 16) (weight_bits <=
+    4), and grad_x runs on the matrix cores (atx_custom_grad_dx_narrow)."""
     xt, Rpad = operand
     O = wq.size(0)
     dyc = dy.contiguous()
@@ -733,8 +735,12 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
     if dx_lut is not None:
         tab = lut_image(dx_lut)[1]
         gx = torch.empty((N, K, Lc), dtype=torch.float32, device=dev)
-        L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc), L.ptr(tab),
-               N, K, Lc, O, L.ptr(gx), s)
+        if wbase is not None:
+            L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+                   L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
+        else:
+            L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+                   L.ptr(tab), N, K, Lc, O, L.ptr(gx), s)
     if dw_lut is not None:
         tab = lut_image(dw_lut)[1]
         gw = torch.empty((O, K), dtype=torch.float32, device=dev)

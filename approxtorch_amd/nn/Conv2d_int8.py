@@ -242,7 +242,7 @@ class Conv2d_int8(nn.Module):
             y = bgemm_int8.conv2d_int8_lre(x, w.view(O, -1), self.lut, self.dx, self.dw, geom)
         elif self.grad == 'custom':
             y = bgemm_int8.conv2d_int8_custom(x, w.view(O, -1), self.lut, self.dx, self.dw,
-                                              geom)
+                                              geom, qmax_w)
         else:
             y = bgemm_int8.conv2d_int8_ste(x, w.view(O, -1), self.lut, geom)
 

@@ -306,7 +306,7 @@ class _conv2d_int8_custom(Function):
     kernels directly."""
 
     @staticmethod
-    def forward(ctx, x, w, lut, dx_lut, dw_lut, geom):
+    def forward(ctx, x, w, lut, dx_lut, dw_lut, geom, qmax_w=None):
         kernel_size, stride, padding, dilation, groups = geom
         if groups != 1:
             raise NotImplementedError("custom gradient currently supports only groups=1")
@@ -314,6 +314,9 @@ class _conv2d_int8_custom(Function):
         y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 128, 128, return_operand=True)
         ctx.save_for_backward(xt, wq, dx_lut, dw_lut)
         ctx.g, ctx.rpad = g, Rpad
+        # w quantized to [-qmax_w, qmax_w] with qmax_w <= 7 (weight_bits <= 4): indices
+        # w + 128 lie in [120, 136) and grad_x runs on the matrix cores
+        ctx.wbase = 120 if qmax_w is not None and qmax_w <= 7 else None
         return y
 
     @staticmethod
@@ -322,10 +325,12 @@ class _conv2d_int8_custom(Function):
         g = ctx.g
         grad_col, grad_w = ops.custom_grads(
             (xt, ctx.rpad), wq, grad_output, dx_lut if ctx.needs_input_grad[0] else None,
-            dw_lut if ctx.needs_input_grad[1] else None, g.N, g.C * g.KH * g.KW, g.OH * g.OW)
+            dw_lut if ctx.needs_input_grad[1] else None, g.N, g.C * g.KH * g.KW, g.OH * g.OW,
+            wbase=ctx.wbase)
         grad_x = ops.col2im(grad_col, g) if grad_col is not None else None
-        return grad_x, grad_w, None, None, None, None
+        return grad_x, grad_w, None, None, None, None, None
 
 
-def conv2d_int8_custom(x, w, lut, dx_lut, dw_lut, geom):
-    return _conv2d_int8_custom.apply(x, w, lut, dx_lut, dw_lut, geom)
+def conv2d_int8_custom(x, w, lut, dx_lut, dw_lut, geom, qmax_w=None):
+    """qmax_w (optional): w holds values quantized to [-qmax_w, qmax_w]."""
+    return _conv2d_int8_custom.apply(x, w, lut, dx_lut, dw_lut, geom, qmax_w)

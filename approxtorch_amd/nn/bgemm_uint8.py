@@ -265,6 +265,8 @@ class _conv2d_uint8_fused(Function):
                               zero_w, tx, tw)
         ctx.g, ctx.rpad, ctx.kind = g, Rpad, kind
         ctx.has_bias, ctx.wshape = bias is not None, weight.shape
+        # at most 16 weight indices (weight_bits <= 4): grad_x on the matrix cores
+        ctx.wbase = 0 if qmax_w <= 15 else None
         return y.view(g.N, O, g.OH, g.OW)
 
     @staticmethod
@@ -279,7 +281,8 @@ class _conv2d_uint8_fused(Function):
         gx = gw = gb = None
         if ctx.kind == 'custom':
             grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, gp, tx if need_x else None,
-                                              tw if need_w else None, g.N, K, Lc)
+                                              tw if need_w else None, g.N, K, Lc,
+                                              wbase=ctx.wbase)
             grad_q = ops.col2im(grad_col, g) if need_x else None
         else:
             if ctx.kind == 'ste':

@@ -420,6 +420,20 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        const uint8_t* mask_w, const float* scale_w, float* grad_w,
                        float* workspace, hipStream_t stream);
 
+/* atx_custom_grad_dx for weights with at most 16 distinct indices: every
+ * wt entry of the O channels lies in [wbase, wbase + 16) (weight_bits <= 4:
+ * wbase 0 for uint8 indices, 120 for int8 values v + 128).  The sum is
+ * regrouped by weight index and runs on the bf16 matrix cores with dy split
+ * exactly into three bf16 parts (fp32 sums, same error bound as
+ * atx_custom_grad_dx; entries outside the range give wrong sums, never an
+ * out-of-bounds access).  Same operands and output; Opad a multiple of 32.
+ * Replaces bgemm_custom_grad_{uint8,int8}_dx for the weight_bits <= 4 layers
+ * (csrc/cuda/bgemm_custom_grad_optimize.cu:30-116, 315-404; called from
+ * nn/bgemm_uint8.py:89-114). */
+int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                              const float* dy, const float* tabT, int wbase, int N, int K,
+                              int L, int O, float* grad_x, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -664,6 +664,48 @@ def test_custom_grads_tiled_shapes(shape):
     close(gw.cpu().numpy(), ew, aw)
 
 
+NARROW_SHAPES = CUSTOM_SHAPES + [(2, 64, 3136, 256), (3, 4608, 49, 40), (2, 20, 196, 2048)]
+
+
+@pytest.mark.parametrize("shape", NARROW_SHAPES)
+@pytest.mark.parametrize("wbase", [0, 120, 240])
+def test_custom_grad_dx_narrow(shape, wbase):
+    """grad_x of weights with 16 distinct indices on the matrix cores
+    (atx_custom_grad_dx_narrow): row tiles of 256 (R not a multiple), tap
+    tiles of 16 (K % 16 != 0), 32-channel steps (O % 32 != 0) and L % 16 != 0
+    (row blocks across images), against the fp64 C oracle within the sum of
+    |terms| bound; wbase 120 is the int8 weight_bits = 4 range v + 128."""
+    N, K, Lc, Oc = shape
+    r = gen(zlib.crc32(repr(("narrow", shape, wbase)).encode()))
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(wbase, wbase + 16, (Oc, K), dtype=np.uint8)
+    dxl = r.standard_normal(65536).astype(np.float32)
+    go = r.standard_normal((N, Oc, Lc)).astype(np.float32)
+    go[:, ::7] *= 1e-3                    # spread of magnitudes (three-part split)
+    gx, _ = ops.custom_grads(ops.pack_rows_u8(t(xi)), t(wi), t(go), t(dxl), None, N, K, Lc,
+                             wbase=wbase)
+    ex, _ = O.gemm_grads(go, xi, wi, "custom", (dxl, dxl))
+    ax, _ = O.gemm_grads(go, xi, wi, "custom", (dxl, dxl), absolute=True)
+    close(gx.cpu().numpy(), ex, ax)
+
+
+def test_custom_grad_dx_narrow_matches_general():
+    """The matrix-core grad_x and the pair-table kernel agree within the fp32
+    sum bound on a c5 layer shape (ResNet-50 3x3, 64 channels)."""
+    N, K, Lc, Oc = 2, 576, 3136, 64
+    r = gen(91)
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 16, (Oc, K), dtype=np.uint8)
+    dxl = t(r.standard_normal(65536).astype(np.float32))
+    go = t(r.standard_normal((N, Oc, Lc)).astype(np.float32))
+    op = ops.pack_rows_u8(t(xi))
+    a, _ = ops.custom_grads(op, t(wi), go, dxl, None, N, K, Lc, wbase=0)
+    b, _ = ops.custom_grads(op, t(wi), go, dxl, None, N, K, Lc)
+    ax, _ = O.gemm_grads(go.cpu().numpy(), xi, wi, "custom",
+                         (dxl.cpu().numpy().reshape(256, 256),) * 2, absolute=True)
+    close(a.cpu().numpy(), b.cpu().numpy(), 2 * ax)
+
+
 def test_custom_grads_deterministic():
     """The grad_w partial slices are summed in a fixed order: two runs agree bitwise."""
     N, K, Lc, Oc = 4, 288, 3136, 64
