@@ -48,6 +48,9 @@ _SIGS = {
                              c_vp, c_int, GemmEpilogue, c_vp, c_vp, c_vp]),
     "atx_lut_gemm_noalloc": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int,
                                      c_vp, c_vp, c_int, GemmEpilogue, c_vp, c_vp]),
+    "atx_lut_gemm_narrow_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
+    "atx_lut_gemm_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp,
+                                    c_int, c_int, GemmEpilogue, c_vp, c_vp, c_vp]),
     "atx_fakequant_fwd": (c_int, [c_vp, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                   c_vp]),
     "atx_fakequant_rows": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_int, c_int,

@@ -151,12 +151,20 @@ def date_tables(lut: Tensor, half_ws: int = 32):
 
 # -------------------------------------------------------------- LUT GEMM
 def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None,
-          transposed=False):
+          transposed=False, wbase=None):
+    """wbase: the caller guarantees every weight index lies in [wbase, wbase + 16)
+    (weight_bits <= 4); integer LUTs then run on the matrix cores."""
     img16, imgf, cls = lut_image(lut, transposed)
     dev = y.device
+    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
+    if wbase is not None and cls != L.ATX_LUT_F32:
+        wsb = L.query("atx_lut_gemm_narrow_workspace_bytes", N, K, Lc, O)
+        ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
+        L.call("atx_lut_gemm_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, N, K, Lc, O,
+               L.ptr(img16), cls, int(wbase), ep, L.ptr(y), L.ptr(ws), L.stream_of(y))
+        return y
     wsb = L.query("atx_lut_gemm_workspace_bytes", N, K, Lc, O) if cls != L.ATX_LUT_F32 else 0
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
-    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
     L.call("atx_lut_gemm", L.ptr(xt), Rpad, L.ptr(wt), Opad, N, K, Lc, O, L.ptr(img16),
            L.ptr(imgf), cls, ep, L.ptr(y), L.ptr(ws), L.stream_of(y))
     return y
@@ -364,7 +372,7 @@ def conv_geom(x_shape, kernel_size, stride, padding, dilation):
 
 def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                  pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
-                 pad_dev=None, packed_w=None, return_operand=False):
+                 pad_dev=None, packed_w=None, return_operand=False, wbase=None):
     """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
 
     img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
@@ -373,7 +381,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     the device scalar pad_dev when given.  packed_w = (wq, wt, Opad) from the
     fused weight fake-quant skips the weight packing.  Returns (y, wq), wq the
     uint8 weight index image; with return_operand, (y, wq, (xt, Rpad)), the
-    row-offset operand for conv_backward_weight_rows."""
+    row-offset operand for conv_backward_weight_rows.  wbase: every weight
+    index lies in [wbase, wbase + 16) (weight_bits <= 4; matrix-core GEMM)."""
     imgc = img.contiguous()
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -391,7 +400,7 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
         wq, wt, Opad = packed_w
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
-    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase)
     if return_operand:
         return y, wq, (xt, Rpad)
     return y, wq
@@ -880,9 +889,11 @@ def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
 
 
 def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
-                      out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None, packed_w=None):
+                      out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None, packed_w=None,
+                      wbase=None):
     """LUT conv from a prepacked row-offset operand (xt, Rpad) of geometry g
-    (fakequant_rows, or conv_forward's return_operand): (y, wq)."""
+    (fakequant_rows, or conv_forward's return_operand): (y, wq).  wbase as in
+    conv_forward."""
     xt, Rpad = xt_rpad
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -897,7 +908,7 @@ def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int
         wq, wt, Opad = packed_w
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=xt.device)
-    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase)
     return y, wq
 
 

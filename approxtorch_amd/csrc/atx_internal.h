@@ -37,6 +37,11 @@ int lut_gemm_f32_tiled(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        const float* sx, const float* sw, const float* bias, float* y,
                        hipStream_t stream);
 
+// Sum of S int32 partial slices of an [N][O][L] LUT GEMM output (ws[s *
+// numel + i], exact in int64) followed by the epilogue ep into y.
+int launch_split_reduce(const int* ws, int S, long long numel, int O, int L,
+                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream);
+
 // Grid size for grid-stride elementwise kernels.
 inline int elem_grid(long long n, int threads, int cap = 8192) {
   long long b = cdiv(n, threads);

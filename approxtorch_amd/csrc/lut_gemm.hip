@@ -1157,14 +1157,19 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
                        stream, p);
   int rc = check_launch("lut_gemm_kernel");
   if (rc != ATX_OK || pl.splits == 1) return rc;
-  if (numel % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)workspace & 15) == 0)
+  return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream);
+}
+
+int launch_split_reduce(const int* ws, int S, long long numel, int O, int L,
+                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream) {
+  if (numel % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)ws & 15) == 0)
     hipLaunchKernelGGL(split_reduce_kernel, dim3(elem_grid(numel / 4, 256)), dim3(256), 0,
-                       stream, (const int*)workspace, pl.splits, numel, O, L,
-                       ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
+                       stream, ws, S, numel, O, L, ep.out_kind, y, ep.scale_x, ep.scale_w,
+                       ep.bias);
   else
     hipLaunchKernelGGL(split_reduce1_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
-                       stream, (const int*)workspace, pl.splits, numel, O, L,
-                       ep.out_kind, y, ep.scale_x, ep.scale_w, ep.bias);
+                       stream, ws, S, numel, O, L, ep.out_kind, y, ep.scale_x, ep.scale_w,
+                       ep.bias);
   return check_launch("split_reduce_kernel");
 }
 

@@ -244,10 +244,13 @@ class _conv2d_int8_fused(Function):
                                                             offset=128,
                                                             want_wt=not depthwise)
         b = None if bias is None else bias.detach().contiguous()
+        # weight_bits <= 4: indices w + 128 in [120, 136), matrix-core LUT GEMM
+        wbase = 120 if qmax_w <= 7 else None
         if pointwise:
             y, _ = ops.conv_forward_rows(xt_rpad, wq, lut, g, 128,
                                          out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
-                                         sw=scale_w, bias=b, packed_w=(wq, wt, Opad))
+                                         sw=scale_w, bias=b, packed_w=(wq, wt, Opad),
+                                         wbase=wbase)
             saved_x, ctx.rpad = xt_rpad
         elif depthwise:
             y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
@@ -258,7 +261,8 @@ class _conv2d_int8_fused(Function):
             # indices feed the backward GEMM with no im2col in the loop
             y, _, (xt, Rpad) = ops.conv_forward(
                 xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
-                sw=scale_w, bias=b, packed_w=(wq, wt, Opad), return_operand=True)
+                sw=scale_w, bias=b, packed_w=(wq, wt, Opad), return_operand=True,
+                wbase=wbase)
             saved_x, ctx.rpad = xt, Rpad
         ctx.save_for_backward(saved_x, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
                               tx.contiguous(), tw.contiguous())
@@ -311,12 +315,13 @@ class _conv2d_int8_custom(Function):
         if groups != 1:
             raise NotImplementedError("custom gradient currently supports only groups=1")
         g, _ = _conv_setup(x, w, geom)
-        y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 128, 128, return_operand=True)
+        # w quantized to [-qmax_w, qmax_w] with qmax_w <= 7 (weight_bits <= 4): indices
+        # w + 128 lie in [120, 136); the LUT GEMM and grad_x run on the matrix cores
+        ctx.wbase = 120 if qmax_w is not None and qmax_w <= 7 else None
+        y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 128, 128, return_operand=True,
+                                             wbase=ctx.wbase)
         ctx.save_for_backward(xt, wq, dx_lut, dw_lut)
         ctx.g, ctx.rpad = g, Rpad
-        # w quantized to [-qmax_w, qmax_w] with qmax_w <= 7 (weight_bits <= 4): indices
-        # w + 128 lie in [120, 136) and grad_x runs on the matrix cores
-        ctx.wbase = 120 if qmax_w is not None and qmax_w <= 7 else None
         return y
 
     @staticmethod

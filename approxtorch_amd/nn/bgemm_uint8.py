@@ -254,8 +254,11 @@ class _conv2d_uint8_fused(Function):
         _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, 0, qmax_w,
                                                             zero_point=zero_w, offset=0,
                                                             want_wt=True)
+        # at most 16 weight indices (weight_bits <= 4): matrix-core LUT GEMM and grad_x
+        wbase = 0 if qmax_w <= 15 else None
         y, _, (xt, Rpad) = ops.conv_forward(q8, wq, lut, g, 0, 0, pad_dev=zero_x,
-                                            packed_w=(wq, wt, Opad), return_operand=True)
+                                            packed_w=(wq, wt, Opad), return_operand=True,
+                                            wbase=wbase)
         xsum = ops.tap_sum(q8, g, pad_dev=zero_x)
         wsum = wq.sum(dim=1, dtype=torch.float32)
         b = None if bias is None else bias.detach().contiguous()
@@ -265,8 +268,7 @@ class _conv2d_uint8_fused(Function):
                               zero_w, tx, tw)
         ctx.g, ctx.rpad, ctx.kind = g, Rpad, kind
         ctx.has_bias, ctx.wshape = bias is not None, weight.shape
-        # at most 16 weight indices (weight_bits <= 4): grad_x on the matrix cores
-        ctx.wbase = 0 if qmax_w <= 15 else None
+        ctx.wbase = wbase
         return y.view(g.N, O, g.OH, g.OW)
 
     @staticmethod

@@ -162,6 +162,23 @@ int atx_lut_gemm(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
                  atx_gemm_epilogue ep, void* y, void* workspace,
                  hipStream_t stream);
 
+/* atx_lut_gemm for weights with at most 16 distinct indices: every wt entry
+ * of the O channels lies in [wbase, wbase + 16) (weight_bits <= 4: wbase 0
+ * for uint8 indices, 120 for int8 values v + 128); integer LUT classes only.
+ * The sum is regrouped by weight index into a product with a 0/1 operand on
+ * the int8 matrix cores, the 16-bit entries in two exact int8 planes: the
+ * same exact int32 sums as atx_lut_gemm (entries outside the range give wrong
+ * sums, never an out-of-bounds access).  Same operands, epilogues and output;
+ * workspace of atx_lut_gemm_narrow_workspace_bytes() (split-K partials).
+ * Replaces the reference's LUT GEMM (csrc/claude/bgemm_lut_kernels.cuh:
+ * 183-387, host bgemm_float_claude.cu:80-240) for the weight_bits <= 4 layers
+ * (nn/Conv2d_uint8.py:257-325, nn/Conv2d_int8.py:178-232). */
+long long atx_lut_gemm_narrow_workspace_bytes(int N, int K, int L, int O);
+int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                        int N, int K, int L, int O, const uint16_t* lut16t, int lut_class,
+                        int wbase, atx_gemm_epilogue ep, void* y, void* workspace,
+                        hipStream_t stream);
+
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory -- code under HIP graph capture, serving loops, harnesses that
  * forbid hipMalloc.  atx_lut_gemm with the same arguments and results, minus

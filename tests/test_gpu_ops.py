@@ -64,6 +64,60 @@ def test_bgemm_int8_u8_input_bit_exact(shape, lut_name):
     assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
 
 
+NARROW_GEMM_SHAPES = SHAPES + [(1, 2304, 196, 256), (3, 130, 200, 2048), (1, 40, 3136, 300)]
+
+
+@pytest.mark.parametrize("shape", NARROW_GEMM_SHAPES)
+@pytest.mark.parametrize("lut_name", ["perturbed", "u16_c5", "i16_edge"])
+@pytest.mark.parametrize("wbase", [0, 120, 240])
+def test_lut_gemm_narrow_bit_exact(shape, lut_name, wbase):
+    """LUT GEMM of weights with 16 distinct indices on the int8 matrix cores
+    (atx_lut_gemm_narrow): exact int32 sums against the int64 oracle for
+    int16 and uint16 tables (extreme entries included), row tiles of 256 and
+    channel tiles of 128 with tails, K % 4 != 0, L % 4 != 0, and split-K
+    plans (few tiles, long K); the fp32 and dequant epilogues equal the
+    table-gather kernel's bit for bit."""
+    N, K, L, Oc = shape
+    r = gen(zlib.crc32(repr(("narrow_gemm", shape, lut_name, wbase)).encode()))
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(wbase, wbase + 16, (Oc, K), dtype=np.uint8)
+    lut = t(luts(9)[lut_name], torch.float32)
+    xt, Rpad = ops.pack_rows_u8(t(xi))
+    _, wt, Opad = ops._pack_w(t(wi), 0)
+    want = O.lut_gemm_i64(xi, wi, luts(9)[lut_name])
+    y = torch.empty((N, Oc, L), dtype=torch.int32, device=DEV)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, lut, ops.L.ATX_OUT_I32, y, wbase=wbase)
+    assert np.array_equal(y.cpu().numpy().astype(np.int64), want)
+    if lut_name == "u16_c5":
+        sx = t(np.array([0.37], np.float32))
+        sw = t((r.random(Oc) + 0.5).astype(np.float32))
+        bias = t(r.standard_normal(Oc).astype(np.float32))
+        for kind, args in ((ops.L.ATX_OUT_F32, ()), (ops.L.ATX_OUT_DEQUANT, (sx, sw, bias))):
+            a = torch.empty((N, Oc, L), dtype=torch.float32, device=DEV)
+            b = torch.empty_like(a)
+            ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, lut, kind, a, *args, wbase=wbase)
+            ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, lut, kind, b, *args)
+            assert torch.equal(a, b)
+
+
+def test_lut_gemm_narrow_beyond_int32_pass():
+    """K > 32768 with uint16 entries: the plan splits K into exact int32
+    passes and the reduce sums them in int64 (sums above 2^31)."""
+    N, K, L, Oc = 1, 40000, 8, 20
+    r = gen(57)
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 16, (Oc, K), dtype=np.uint8)
+    lut_np = r.integers(60000, 65536, 65536)        # uint16 class, large entries
+    xt, Rpad = ops.pack_rows_u8(t(xi))
+    _, wt, Opad = ops._pack_w(t(wi), 0)
+    want = O.lut_gemm_i64(xi, wi, lut_np)
+    assert want.max() > 2 ** 31
+    y = torch.empty((N, Oc, L), dtype=torch.float32, device=DEV)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, t(lut_np, torch.float32), ops.L.ATX_OUT_F32, y,
+              wbase=0)
+    assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
+
+
 # Stream-K schedule of the LUT GEMM: full rounds of whole tiles, then the
 # (tile, 4-table quad) iterations of the remaining tiles dealt out evenly over
 # 256 workgroups; a tile cut by a workgroup boundary sums its int32 parts
