@@ -23,8 +23,8 @@
 // different bank quads whatever their rows.  H is built per tap quad by the
 // eight waves (one 16-channel block each, from one index byte per lane) into
 // a double buffer, one barrier per quad.  A workgroup (8 waves) owns 256 rows
-// x 128 channels, a wave 64 rows x 64 channels (4 x 4 blocks, two planes:
-// 128 int32 accumulators per lane); workgroups are persistent over the tiles
+// x 128 channels (512 x 64 when O <= 64), a wave 64 rows x 64 channels (4 x 4
+// blocks, two planes: 128 int32 accumulators per lane); workgroups are persistent over the tiles
 // in XCD-contiguous ranges, and split-K (int32 partial slices, summed by the
 // LUT GEMM's split reduce) fills the GPU when the tiles are few.
 #include "atx_internal.h"
@@ -38,12 +38,11 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NWAVE = 8;
 constexpr int NT = 64 * NWAVE;
-constexpr int RB = 4, CB = 4;                // 16 x 16 blocks per wave
-constexpr int TR = 256, TC = 128;            // workgroup tile
+constexpr int RB = 4, CB = 4;                // 16 x 16 blocks per wave (64 x 64)
 constexpr int TROW = 512;                    // LDS bytes per table row: 2 planes x 16 copies x 16
 constexpr int TAB = 256 * TROW;              // 128 KiB
 constexpr int HBLK = 64 * 16;                // one 16-channel block's H fragments
-constexpr int HBUF = (TC / 16) * HBLK;       // one quad's H (8 KiB)
+constexpr int HBUF = 8 * HBLK;               // one quad's H, up to 128 channels (8 KiB)
 constexpr int KMAX = 32768;                  // taps per pass with exact int32 sums (uint16)
 
 struct Params {
@@ -77,13 +76,18 @@ __device__ __forceinline__ i32x4 h_fragment(unsigned wbyte, int wbase, bool vali
   return f;
 }
 
+// WCN waves along the channels: 2 -> 256 rows x 128 channels per workgroup,
+// 1 -> 512 rows x 64 channels (layers with O <= 64).
+template <int WCN>
 __global__ void __launch_bounds__(NT, 1) onehot_gemm_kernel(const Params p) {
+  constexpr int NWR = NWAVE / WCN;
+  constexpr int TR = 64 * NWR, TC = 64 * WCN;
   __shared__ __align__(16) unsigned char tab[TAB];
   __shared__ __align__(16) unsigned char hbuf[2 * HBUF];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = lane & 15, g = lane >> 4;
-  const int wr = wave & 3, wc = wave >> 2;
+  const int wr = wave % NWR, wc = wave / NWR;
 
   // planes of the table's 16 columns, 16 copies each
   {
@@ -129,10 +133,12 @@ __global__ void __launch_bounds__(NT, 1) onehot_gemm_kernel(const Params p) {
       const int k = std::min(4 * q + g, p.K - 1);
       return __builtin_amdgcn_raw_buffer_load_b8(wtr, (unsigned)(k * p.Opad + hch), 0, 0);
     };
+    const bool builds_h = wave < TC / 16;
     auto write_h = [&](int q, unsigned wbyte) {
       const bool valid = 4 * q + g < p.K;
-      *(i32x4*)(hbuf + (q & 1) * HBUF + wave * HBLK + lane * 16) =
-          h_fragment(wbyte, p.wbase, valid);
+      if (builds_h)
+        *(i32x4*)(hbuf + (q & 1) * HBUF + wave * HBLK + lane * 16) =
+            h_fragment(wbyte, p.wbase, valid);
     };
     // row offsets of the lane's four row blocks at quad q (slot 4q + slot_off)
     const unsigned xvoff = (unsigned)(slot_off * p.Rpad + r0 + m) * 2u;
@@ -250,7 +256,7 @@ __global__ void __launch_bounds__(NT, 1) onehot_gemm_kernel(const Params p) {
   }
 }
 
-struct Plan { int tiles_r, tiles_c, splits, kq; };
+struct Plan { int wcn, tiles_r, tiles_c, splits, kq; };
 
 // Split count by a cost model in quads of one workgroup: rounds of the
 // persistent grid x (quads per split + 6 for a tile's prologue and
@@ -259,8 +265,9 @@ struct Plan { int tiles_r, tiles_c, splits, kq; };
 static Plan make_plan(int N, int K, int L, int O) {
   Plan pl;
   const long long R = (long long)N * L;
-  pl.tiles_r = (int)cdiv(R, TR);
-  pl.tiles_c = (int)cdiv(O, TC);
+  pl.wcn = O <= 64 ? 1 : 2;
+  pl.tiles_r = (int)cdiv(R, 64 * (NWAVE / pl.wcn));
+  pl.tiles_c = (int)cdiv(O, 64 * pl.wcn);
   const int nq = (int)cdiv(K, 4);
   const long long tiles = (long long)pl.tiles_r * pl.tiles_c;
   const int smin = (int)cdiv(K, KMAX);
@@ -336,7 +343,10 @@ int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
     p.split_stride = numel;
   }
   const int blocks = (int)std::min<long long>(256, ((tiles + 7) / 8) * 8);
-  hipLaunchKernelGGL(ohf::onehot_gemm_kernel, dim3(blocks), dim3(ohf::NT), 0, stream, p);
+  if (pl.wcn == 1)
+    hipLaunchKernelGGL(ohf::onehot_gemm_kernel<1>, dim3(blocks), dim3(ohf::NT), 0, stream, p);
+  else
+    hipLaunchKernelGGL(ohf::onehot_gemm_kernel<2>, dim3(blocks), dim3(ohf::NT), 0, stream, p);
   int rc = check_launch("onehot_gemm_kernel");
   if (rc != ATX_OK || pl.splits == 1) return rc;
   return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream);
