@@ -59,6 +59,7 @@ _SIGS = {
     "atx_fakequant_channel_fwd": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_int, c_int, c_int,
                                           c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "atx_col2im": (c_int, [c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
+    "atx_col2im_pos": (c_int, [c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_tap_sum": (c_int, [c_vp, c_int, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_bwd": (c_int, [c_vp, ConvGeom, c_vp, c_vp]),
@@ -106,11 +107,11 @@ _SIGS = {
                                     c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_custom_grad_dx": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int,
                                    c_int, c_vp, c_vp]),
-    "atx_custom_grad_dx_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int,
-                                          c_int, c_int, c_int, c_vp, c_vp]),
+    "atx_custom_grad_dx_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
+                                          c_int, c_int, c_int, c_int, c_vp, c_vp]),
     "atx_custom_grad_dw_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
-    "atx_custom_grad_dw": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int,
-                                   c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "atx_custom_grad_dw": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int,
+                                   c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
 }
 
 _lib = None

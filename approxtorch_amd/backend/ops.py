@@ -558,10 +558,20 @@ def tap_sum_backward(go: Tensor, g) -> Tensor:
     return img
 
 
-def col2im(col: Tensor, g) -> Tensor:
+def col2im(col: Tensor, g, pos=None, mask=None, scale=None) -> Tensor:
+    """F.fold of col [N, C*KH*KW, L]; pos [N, L] (optional) adds its value at
+    every tap of a position (tap_sum's backward) and mask / scale fuse the
+    per-tensor fake-quant STE (mask ? v : 0) / max(scale, 1e-12)."""
     colc = col.contiguous()
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=colc.device)
-    L.call("atx_col2im", L.ptr(colc), g, None, None, L.ptr(img), L.stream_of(colc))
+    if pos is not None:
+        pos = pos.contiguous()
+        if pos.dtype != torch.float32 or pos.numel() != g.N * g.OH * g.OW:
+            raise RuntimeError("col2im: pos must be float32 [N, OH*OW]")
+    if mask is not None and (mask.dtype != torch.bool or mask.numel() != img.numel()):
+        raise RuntimeError("col2im: mask must be bool of the image's shape")
+    L.call("atx_col2im_pos", L.ptr(colc), g, L.ptr(pos), L.ptr(mask), L.ptr(scale), L.ptr(img),
+           L.stream_of(colc))
     return img
 
 
@@ -725,19 +735,26 @@ def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, 
 
 # --------------------------------------------------------- custom backward
 def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int, Lc: int,
-                 mask_w=None, scale_w=None, wbase=None):
+                 mask_w=None, scale_w=None, wbase=None, dy_scale=None):
     """(grad_x [N,K,L] or None, grad_w [O,K] or None) of the pair-table
     estimator from the LUT GEMM's row-offset operand (xt, Rpad) and the uint8
     weight index image wq [O,K]; dx_lut / dw_lut are fp32 [65536] tables
     indexed [x*256 + w] (None skips that gradient).  mask_w / scale_w fuse
     the per-channel weight fake-quant STE into grad_w.  wbase: the caller
     guarantees every index of wq lies in [wbase, wbase + 16) (weight_bits <=
-    4), and grad_x runs on the matrix cores (atx_custom_grad_dx_narrow)."""
+    4), and grad_x runs on the matrix cores (atx_custom_grad_dx_narrow).
+    dy_scale [O] (optional): the gradients of dy * dy_scale[o], with no scaled
+    copy of dy where the kernels take the factor."""
     xt, Rpad = operand
     O = wq.size(0)
     dyc = dy.contiguous()
     if dyc.dtype != torch.float32 or tuple(dyc.shape) != (N, O, Lc):
         raise RuntimeError(f"dY must be float32 of shape {(N, O, Lc)}")
+    if dy_scale is not None:
+        dy_scale = dy_scale.contiguous()
+        if dy_scale.dtype != torch.float32 or dy_scale.numel() != O or \
+                dy_scale.device != dyc.device:
+            raise RuntimeError(f"dy_scale must be float32 [{O}] on {dyc.device}")
     _, wt, Opad = _pack_w(wq.contiguous(), 0)
     dev, s = dyc.device, L.stream_of(dyc)
     gx = gw = None
@@ -746,17 +763,19 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
         gx = torch.empty((N, K, Lc), dtype=torch.float32, device=dev)
         if wbase is not None:
             L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
-                   L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
+                   L.ptr(dy_scale), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
         else:
-            L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+            dyx = dyc if dy_scale is None else dyc * dy_scale.view(1, -1, 1)
+            L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyx),
                    L.ptr(tab), N, K, Lc, O, L.ptr(gx), s)
     if dw_lut is not None:
         tab = lut_image(dw_lut)[1]
         gw = torch.empty((O, K), dtype=torch.float32, device=dev)
         wsb = L.query("atx_custom_grad_dw_workspace_bytes", N, K, Lc, O)
         ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
-        L.call("atx_custom_grad_dw", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc), L.ptr(tab),
-               N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w), L.ptr(gw), L.ptr(ws), s)
+        L.call("atx_custom_grad_dw", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+               L.ptr(dy_scale), L.ptr(tab), N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w),
+               L.ptr(gw), L.ptr(ws), s)
     return gx, gw
 
 

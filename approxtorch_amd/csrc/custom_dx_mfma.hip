@@ -56,6 +56,7 @@ struct Params {
   const uint8_t* wt; int Opad;               // weight indices [K][Opad]
   const float* tab;                          // tab[w * 256 + v] = DX[v][w]
   const float* dy;                           // [N][O][L]
+  const float* dys;                          // per-channel factor of dy [O] (nullable)
   float* gx;                                 // [N][K][L]
   int K, R, L, O, wbase;
   int tiles_k, tiles;
@@ -160,7 +161,7 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
       w[1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
                                            wtr, ob, kh1 * p.Opad, 0));
     };
-    auto load_dy = [&](int s, float (&d)[RB][8]) {
+    auto load_dy = [&](int s, float (&d)[RB][8], float (&f)[8]) {
       const int nvalid = s == nsteps - 1 ? ptail - 8 * g : 8;   // channels below O
 #pragma unroll
       for (int b = 0; b < RB; ++b)
@@ -169,6 +170,10 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
           d[b][c] = __builtin_bit_cast(
               float, __builtin_amdgcn_raw_buffer_load_b32(
                          dyr, c < nvalid ? dyoff[b] : OOB, (s * OC + c) * chan_bytes, 0));
+      if (p.dys) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) f[c] = p.dys[std::min(s * OC + 8 * g + c, p.O - 1)];
+      }
     };
     auto write_h = [&](int s, const uint2 (&w)[2]) {
       uint2 keep = {0xffffffffu, 0xffffffffu};
@@ -187,24 +192,30 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
 #pragma unroll
       for (int t = 0; t < KT; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    float raw[RB][8];
+    float raw[RB][8], fac[8];
     {
       uint2 w0[2];
       load_w(0, w0);
-      load_dy(0, raw);
+      load_dy(0, raw, fac);
       write_h(0, w0);
     }
     __syncthreads();
 
     for (int s = 0; s < nsteps; ++s) {
       u32x4 P[RB][3];
+      if (p.dys) {            // dy * factor[o], the product the caller would form
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) raw[b][c] *= fac[c];
+      }
 #pragma unroll
       for (int b = 0; b < RB; ++b) split_parts(raw[b], P[b]);
       const bool more = s + 1 < nsteps;
       uint2 wn[2];
       if (more) {
         load_w(s + 1, wn);
-        load_dy(s + 1, raw);
+        load_dy(s + 1, raw, fac);
       }
       // H fragments of tap quad tq + 1 are read while quad tq's MFMAs issue
       const unsigned char* hb = hbuf + (s & 1) * HBUF + lane * 16;
@@ -280,14 +291,16 @@ using namespace atx;
 extern "C" {
 
 int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                              const float* dy, const float* tabT, int wbase, int N, int K, int L,
-                              int O, float* grad_x, hipStream_t stream) {
+                              const float* dy, const float* dy_scale, const float* tabT,
+                              int wbase, int N, int K, int L, int O, float* grad_x,
+                              hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_custom_grad_dx_narrow: negative size");
   ATX_REQUIRE(wbase >= 0 && wbase <= 240, "atx_custom_grad_dx_narrow: wbase must be in [0, 240]");
   const long long R = (long long)N * L;
   const long long numel = R * K;
   if (numel == 0) return ATX_OK;
-  if (O == 0) return atx_custom_grad_dx(xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, grad_x, stream);
+  if (O == 0)   // an empty sum: zeros
+    return atx_custom_grad_dx(xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, grad_x, stream);
   ATX_REQUIRE(xt && wt && dy && tabT && grad_x, "atx_custom_grad_dx_narrow: null pointer");
   ATX_REQUIRE(Rpad >= R && Rpad % ATX_ROW_TILE == 0,
               "atx_custom_grad_dx_narrow: Rpad must be a multiple of %d and >= N*L",
@@ -298,6 +311,7 @@ int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, i
               "atx_custom_grad_dx_narrow: operand too large for 32-bit buffer offsets");
   ohx::Params p;
   p.xt = xt; p.Rpad = Rpad; p.wt = wt; p.Opad = Opad; p.tab = tabT; p.dy = dy; p.gx = grad_x;
+  p.dys = dy_scale;
   p.K = K; p.R = (int)R; p.L = L; p.O = O; p.wbase = wbase;
   p.tiles_k = (int)cdiv(K, ohx::KT);
   const long long tiles = cdiv(R, ohx::ROWS) * p.tiles_k;

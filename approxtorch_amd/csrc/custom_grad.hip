@@ -58,6 +58,7 @@ struct Params {
   const uint8_t* wt; int Opad;
   const float* tab;        // transposed pair table: tab[w * 256 + v] = T[v][w]
   const float* dy;         // [N][O][L]
+  const float* dys;        // grad_w: per-channel factor of dy [O] (nullable)
   float* out;              // grad_x [N][K][L], or the grad_w slices [tiles_r][O][K]
   int K, R, L, O;
   int tiles_r, tiles_o, nq; // nq = quads of taps
@@ -427,8 +428,16 @@ custom_dw_kernel(const Params p) {
   {
     DyRows<VEC> dro;
     dy_rows<VEC>(p, r0, 4 * g, dro);
-    load_dy<VEC>(buffer_rsrc(p.dy, p.R * p.O * 4), dro, p.L, CT * to,
-                 min(4, max(0, p.O - CT * to - 4 * g)), dyv);
+    const int nvalid = min(4, max(0, p.O - CT * to - 4 * g));
+    load_dy<VEC>(buffer_rsrc(p.dy, p.R * p.O * 4), dro, p.L, CT * to, nvalid, dyv);
+    if (p.dys) {             // dy * factor[o], the product the caller would form
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float f = c < nvalid ? p.dys[CT * to + 4 * g + c] : 0.f;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) dyv[r][c] *= f;
+      }
+    }
   }
   float acc[TPL][4];
 
@@ -770,13 +779,14 @@ long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O) {
 }
 
 int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                       const float* dy, const float* tabT, int N, int K, int L, int O,
-                       const uint8_t* mask_w, const float* scale_w, float* grad_w,
-                       float* workspace, hipStream_t stream) {
+                       const float* dy, const float* dy_scale, const float* tabT, int N, int K,
+                       int L, int O, const uint8_t* mask_w, const float* scale_w,
+                       float* grad_w, float* workspace, hipStream_t stream) {
   cg::Params p;
   int rc = custom_params(p, xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, workspace,
                          "atx_custom_grad_dw");
   if (rc != ATX_OK) return rc;
+  p.dys = dy_scale;
   const long long numel = (long long)O * K;
   if (numel == 0) return ATX_OK;
   ATX_REQUIRE(grad_w && !(mask_w && !scale_w), "atx_custom_grad_dw: null output / scale");

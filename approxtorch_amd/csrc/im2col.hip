@@ -181,6 +181,9 @@ __global__ void lut_map_pad_kernel(const T* __restrict__ in, int N, int C, int H
 
 // col2im: img[n,c,h,w] = sum over taps (kh,kw) hitting (h,w) of
 // col[n, (c,kh,kw), (oh,ow)], taps in ascending (kh, kw) order (F.fold).
+// Optional per-position term: pos [N][L] (nullable) adds, as a second sum in
+// the same tap order, sum over the hitting taps of pos[n, (oh,ow)] (the
+// backward of a per-position term broadcast over a position's taps).
 // Optional fused STE: img = mask ? img / s : 0 (s = max(scale[0], 1e-12)).
 // One thread per image element; I = int when the image has fewer than 2^31
 // elements (32-bit index arithmetic), long long otherwise.  The taps are
@@ -191,7 +194,7 @@ __global__ void lut_map_pad_kernel(const T* __restrict__ in, int N, int C, int H
 // (divisions become shifts), 0 for the general case.
 template <typename I, int ST, int CT>
 __global__ void __launch_bounds__(TB)
-col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
+col2im_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __restrict__ pos,
               const uint8_t* __restrict__ mask, const float* __restrict__ scale,
               float* __restrict__ img) {
   const int L = g.OH * g.OW;
@@ -204,10 +207,12 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
     const int p = (int)(i - plane * HW);
     const int h = p / g.W, w = p - h * g.W;
     const float* cn = col + (long long)plane * KK * L;   // col[n][c*KK ..][L]
-    float a = 0.0f;
+    const float* pn = pos ? pos + (long long)(plane / g.C) * L : nullptr;
+    float a = 0.0f, b = 0.0f;
     int kh = 0, kw = 0;
     for (int t0 = 0; t0 < KK; t0 += CT) {
       float v[CT];
+      int at[CT];
       unsigned ok = 0;
 #pragma unroll
       for (int j = 0; j < CT; ++j) {
@@ -225,14 +230,21 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g,
           hit = oh * g.SH == y && ow * g.SW == x;
         }
         hit = hit && t0 + j < KK && y >= 0 && x >= 0 && oh < g.OH && ow < g.OW;
-        v[j] = cn[hit ? (long long)(t0 + j) * L + oh * g.OW + ow : 0];
+        at[j] = hit ? oh * g.OW + ow : 0;
+        v[j] = cn[hit ? (long long)(t0 + j) * L + at[j] : 0];
         ok |= (hit ? 1u : 0u) << j;
         if (++kw == g.KW) { kw = 0; ++kh; }
       }
 #pragma unroll
       for (int j = 0; j < CT; ++j)
         if ((ok >> j) & 1u) a += v[j];
+      if (pn) {
+#pragma unroll
+        for (int j = 0; j < CT; ++j)
+          if ((ok >> j) & 1u) b += pn[at[j]];
+      }
     }
+    if (pn) a += b;
     if (mask) a = (mask[i] ? a : 0.0f) / s;
     img[i] = a;
   }
@@ -481,6 +493,11 @@ int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img, hipStream_t st
 
 int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const float* scale,
                float* img, hipStream_t stream) {
+  return atx_col2im_pos(col, g, nullptr, mask, scale, img, stream);
+}
+
+int atx_col2im_pos(const float* col, atx_conv_geom g, const float* pos, const uint8_t* mask,
+                   const float* scale, float* img, hipStream_t stream) {
   int rc = check_geom(g);
   if (rc) return rc;
   const long long total = (long long)g.N * g.C * g.H * g.W;
@@ -491,8 +508,8 @@ int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const flo
   const int st = g.SH == g.SW && (g.SH == 1 || g.SH == 2) ? g.SH : 0;
   const bool one = g.KH * g.KW == 1;
 #define ATX_COL2IM(I, S, C)                                                              \
-  hipLaunchKernelGGL((col2im_kernel<I, S, C>), grid, dim3(TB), 0, stream, col, g, mask,   \
-                     scale, img)
+  hipLaunchKernelGGL((col2im_kernel<I, S, C>), grid, dim3(TB), 0, stream, col, g, pos,    \
+                     mask, scale, img)
   if (!small) ATX_COL2IM(long long, 0, 9);
   else if (st == 1) { if (one) ATX_COL2IM(int, 1, 1); else ATX_COL2IM(int, 1, 9); }
   else if (st == 2) { if (one) ATX_COL2IM(int, 2, 1); else ATX_COL2IM(int, 2, 9); }

@@ -236,10 +236,11 @@ class _conv2d_uint8_fused(Function):
                 implicit im2col LUT conv; the taps' sums of q_x (tap_sum) and
                 sum_k q_w; one in-place pass for correction and dequant;
       backward: g' = go * (scale_x * scale_w[o]) feeds the estimator's
-                gradient kernels; the zero-point terms add -sum_o g' z_w[o]
-                to every tap of a position (tap_sum's backward) and
-                -z_x * sum_{n,l} g' to every tap of a channel; then the two
-                fake-quant STEs.
+                gradient kernels (the custom kernels take the factor, no g'
+                copy); the zero-point terms add -sum_o g' z_w[o] to every tap
+                of a position (tap_sum's backward; folded with the STE into
+                col2im on the custom path) and -z_x * sum_{n,l} g' to every
+                tap of a channel; then the two fake-quant STEs.
     kind: 'ste' | 'lre' | 'custom'; tx / tw: the estimator's tables (STE:
     None, the identity decode table is used)."""
 
@@ -278,31 +279,36 @@ class _conv2d_uint8_fused(Function):
         O, K = wq.shape
         Lc = g.OH * g.OW
         go = grad_output.contiguous().view(g.N, O, Lc)
-        gp = go * (sx * sw).view(1, -1, 1)                  # d loss / d corrected sum
+        c = (sx * sw).contiguous()          # d loss / d corrected sum = go * c[o]
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_b = ctx.has_bias and ctx.needs_input_grad[2]
         gx = gw = gb = None
+        # zero-point terms: -sum_o g' z_w[o] per position (a [1 x O] by [O x L]
+        # product per image) and -z_x sum_{n,l} g' per channel
+        gxs = torch.matmul((c * zw).view(1, O), go).view(g.N, Lc).neg_() if need_x else None
+        gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
         if ctx.kind == 'custom':
-            grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, gp, tx if need_x else None,
+            grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, go, tx if need_x else None,
                                               tw if need_w else None, g.N, K, Lc,
-                                              wbase=ctx.wbase)
-            grad_q = ops.col2im(grad_col, g) if need_x else None
+                                              wbase=ctx.wbase, dy_scale=c)
+            if need_x:   # fold, zero-point term and the STE in one pass
+                gx = ops.col2im(grad_col, g, pos=gxs, mask=mask_x, scale=sx)
         else:
+            gp = go * c.view(1, -1, 1)
             if ctx.kind == 'ste':
                 tx = tw = decode_table(gp.device, signed=False)
-            grad_q = ops.conv_backward_data(gp, wq, tx.contiguous(), g) if need_x else None
             gw_q = ops.conv_backward_weight_rows(gp, (xt, ctx.rpad), tw.contiguous(), g, O) \
                 if need_w else None
-        if need_x:
-            gxs = (gp * zw.view(1, -1, 1)).sum(dim=1).neg_()        # [N, L]
-            grad_q += ops.tap_sum_backward(gxs, g)
-            gx = ops.fakequant_per_tensor_backward(grad_q, mask_x, sx)
+            if need_x:
+                grad_q = ops.conv_backward_data(gp, wq, tx.contiguous(), g)
+                grad_q += ops.tap_sum_backward(gxs, g)
+                gx = ops.fakequant_per_tensor_backward(grad_q, mask_x, sx)
         if need_w:
-            gws = gp.sum(dim=(0, 2)).mul_(zx).neg_()                # [O]
-            gw_q += gws.view(-1, 1)
+            gw_q += (gsum * c).mul_(zx).neg_().view(-1, 1)
             gw = ops.fakequant_per_tensor_backward(gw_q, mask_w, sw, channels=O,
                                                    inner=K).view(ctx.wshape)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            gb = go.sum(dim=(0, 2))
+        if need_b:
+            gb = gsum
         return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
 
 

@@ -13,7 +13,10 @@ Also reported:
                 durations (HIP events on the launch stream); bound = LDS, one
                 LUT-MAC = one 2-byte table read from LDS, peak = 256 CUs x
                 256 B/clk x 2.4 GHz.  `valu_peak` is the co-bound of one
-                int32 add per LUT-MAC (256 CUs x 64 lanes x 2.4 GHz).
+                int32 add per LUT-MAC (256 CUs x 64 lanes x 2.4 GHz).  For
+                weight_bits <= 4 (c5) the LUT GEMM is onehot_gemm_kernel on
+                the int8 matrix cores: 64 int8 ops per LUT-MAC against 5000
+                TOP/s.
                 `traffic` = HBM bytes per launch measured by rocprofv3 PMC
                 passes (FETCH_SIZE, WRITE_SIZE; run with --calibrate-copy so
                 the same passes see a copy kernel of known size).
@@ -35,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 LDS_PEAK_GBS = 256 * 256 * 2.4      # GB/s: 256 CUs x 256 B/clk x 2.4 GHz
 VALU_PEAK_GLUT = 256 * 64 * 2.4      # G int32 adds/s: 256 CUs x 64 lanes x 2.4 GHz
+INT8_PEAK_TOPS = 5000.0              # dense int8 MFMA, TOP/s
 COPY_BYTES = 512 << 20               # --calibrate-copy: bytes read and written per copy
 # HBM bytes per lut_gemm_kernel launch from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch, averaged over the launches of a
@@ -347,7 +351,7 @@ def main():
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
                    "forward_lut_macs": macs_fwd},
-        "roofline": roofline(timer, dt, GEMM_TRAFFIC.get(name)),
+        "roofline": roofline(timer, dt, GEMM_TRAFFIC.get(name), narrow=cfg["weight_bits"] <= 4),
     }
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
@@ -360,9 +364,26 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def roofline(timer, dt, traffic):
+def roofline(timer, dt, traffic, narrow=False):
     gemm_ms, gemm_macs, launches = timer.summary()
     achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
+    if narrow:
+        # weight_bits <= 4: onehot_gemm_kernel on the int8 matrix cores, 16 index
+        # slots x 2 byte planes = 32 int8 MACs (64 ops) per LUT-MAC
+        return {
+            "kernel": "onehot_gemm_kernel (+ its split-K reduce launches)",
+            "bound": "mfma",
+            "achieved": round(64 * achieved_glut / 1e3, 1),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s (int8)",
+            "frac": round(64 * achieved_glut / 1e3 / INT8_PEAK_TOPS, 4),
+            "traffic": traffic,
+            "lut_mac_per_s_G": round(achieved_glut, 1),
+            "mfma_peak_lut_mac_per_s_G": round(INT8_PEAK_TOPS * 1e3 / 64, 1),
+            "launches": launches,
+            "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
+            "share_of_step": round(gemm_ms / (dt * 1e3), 4),
+        }
     return {
         "kernel": "lut_gemm_kernel (+ its split-K reduce / stream-K clear and finish launches)",
         "bound": "lds",

@@ -246,6 +246,17 @@ int atx_fakequant_channel_fwd(const float* w, int O, long long inner,
 int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask,
                const float* scale, float* img, hipStream_t stream);
 
+/* atx_col2im plus a per-position term: pos [N, OH*OW] fp32 (nullable) adds,
+ * summed separately in the same tap order, sum of pos[n,(oh,ow)] over the
+ * taps that read (h,w) -- the backward of a term broadcast to every tap of an
+ * output position (tap_sum's backward) -- before the fused STE.  One pass for
+ * nn/Conv2d_uint8.py:308-325's zero-point term z_w * sum_k q_x (its image
+ * gradient) with F.fold of the main term and the STE of
+ * csrc/claude/quantization.cu:223-258. */
+int atx_col2im_pos(const float* col, atx_conv_geom g, const float* pos,
+                   const uint8_t* mask, const float* scale, float* img,
+                   hipStream_t stream);
+
 /* Column sums of the unfolded image (dtype 1 = uint8 values, 2 = fp32
  * holding quantized integers), out[n,l] = sum over the K taps (out-of-image
  * taps count as pad_dev[0], 0 if null), exact; workspace:
@@ -422,7 +433,10 @@ int atx_dwconv_bwd_weight(const float* go, const void* img, int dtype,
  * atx_im2col_rows wrote them; rows r = n*L + l) and wt [K][Opad] indices.
  * dy [N,O,L] fp32; grad_x [N,K,L] fp32 (fold it with atx_col2im for a conv);
  * grad_w [O,K] fp32, with the per-channel weight fake-quant STE fused when
- * mask_w / scale_w are given (as atx_conv_bwd_weight).  Table entries must
+ * mask_w / scale_w are given (as atx_conv_bwd_weight).  dy_scale [O]
+ * (nullable): the gradients of dy[n,o,l] * dy_scale[o] (each product rounded
+ * once, as the caller's own multiply would), so a layer's per-channel output
+ * scale needs no scaled copy of dy.  Table entries must
  * be finite.  Workspace of grad_w: atx_custom_grad_dw_workspace_bytes()
  * (one partial slice per 2048-row tile, summed in a fixed order).
  * Replace bgemm_custom_grad_{uint8,int8}_{dx,dw}
@@ -433,9 +447,9 @@ int atx_custom_grad_dx(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        float* grad_x, hipStream_t stream);
 long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O);
 int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                       const float* dy, const float* tabT, int N, int K, int L, int O,
-                       const uint8_t* mask_w, const float* scale_w, float* grad_w,
-                       float* workspace, hipStream_t stream);
+                       const float* dy, const float* dy_scale, const float* tabT, int N,
+                       int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
+                       float* grad_w, float* workspace, hipStream_t stream);
 
 /* atx_custom_grad_dx for weights with at most 16 distinct indices: every
  * wt entry of the O channels lies in [wbase, wbase + 16) (weight_bits <= 4:
@@ -443,13 +457,15 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
  * regrouped by weight index and runs on the bf16 matrix cores with dy split
  * exactly into three bf16 parts (fp32 sums, same error bound as
  * atx_custom_grad_dx; entries outside the range give wrong sums, never an
- * out-of-bounds access).  Same operands and output; Opad a multiple of 32.
+ * out-of-bounds access).  Same operands and output (dy_scale as in
+ * atx_custom_grad_dw); Opad a multiple of 32.
  * Replaces bgemm_custom_grad_{uint8,int8}_dx for the weight_bits <= 4 layers
  * (csrc/cuda/bgemm_custom_grad_optimize.cu:30-116, 315-404; called from
  * nn/bgemm_uint8.py:89-114). */
 int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                              const float* dy, const float* tabT, int wbase, int N, int K,
-                              int L, int O, float* grad_x, hipStream_t stream);
+                              const float* dy, const float* dy_scale, const float* tabT,
+                              int wbase, int N, int K, int L, int O, float* grad_x,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

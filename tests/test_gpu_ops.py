@@ -718,7 +718,33 @@ def test_custom_grads_tiled_shapes(shape):
     close(gw.cpu().numpy(), ew, aw)
 
 
-NARROW_SHAPES = CUSTOM_SHAPES + [(2, 64, 3136, 256), (3, 4608, 49, 40), (2, 20, 196, 2048)]
+@pytest.mark.parametrize("case", TAP_GEOMS)
+def test_col2im_pos_ste(case):
+    """col2im with the per-position term (tap_sum's backward) and the fused
+    STE: fold(col) + fold(pos broadcast over the taps of each position), then
+    (mask ? v : 0) / scale, against the fp64 oracle fold."""
+    shape, k, s_, p, d = case
+    N, C, H, W = shape
+    r = gen(zlib.crc32(repr(("col2im_pos", case)).encode()))
+    g = ops.conv_geom(shape, k, s_, p, d)
+    Lc = g.OH * g.OW
+    col = r.standard_normal((N, C * k[0] * k[1], Lc)).astype(np.float32)
+    pos = r.standard_normal((N, Lc)).astype(np.float32)
+    mask = r.random(shape) < 0.7
+    scale = np.float32(0.37)
+    got = ops.col2im(t(col), g, pos=t(pos), mask=t(mask), scale=t(np.array([scale])))
+    fcol = O.fold(col, shape, k, s_, p, d)
+    fpos = O.fold(np.broadcast_to(pos[:, None, :], col.shape), shape, k, s_, p, d)
+    want = np.where(mask, fcol + fpos, 0.0) / scale
+    absref = np.where(mask, O.fold(np.abs(col), shape, k, s_, p, d) +
+                      O.fold(np.abs(np.broadcast_to(pos[:, None, :], col.shape)), shape, k, s_,
+                             p, d), 0.0) / scale
+    close(got.cpu().numpy(), want, absref)
+    plain = ops.col2im(t(col), g)
+    close(plain.cpu().numpy(), fcol, O.fold(np.abs(col), shape, k, s_, p, d))
+
+
+NARROW_SHAPES = CUSTOM_SHAPES +[(2, 64, 3136, 256), (3, 4608, 49, 40), (2, 20, 196, 2048)]
 
 
 @pytest.mark.parametrize("shape", NARROW_SHAPES)
@@ -741,6 +767,24 @@ def test_custom_grad_dx_narrow(shape, wbase):
     ex, _ = O.gemm_grads(go, xi, wi, "custom", (dxl, dxl))
     ax, _ = O.gemm_grads(go, xi, wi, "custom", (dxl, dxl), absolute=True)
     close(gx.cpu().numpy(), ex, ax)
+
+
+@pytest.mark.parametrize("shape", [(2, 37, 1000, 70), (1, 9, 2049, 17), (2, 64, 196, 300)])
+def test_custom_grads_dy_scale(shape):
+    """dy_scale[o] inside the kernels gives the gradients of the scaled copy
+    dy * dy_scale[o] bit for bit (the same rounded products): grad_w of the
+    pair-table kernel and grad_x of the matrix-core kernel."""
+    N, K, Lc, Oc = shape
+    r = gen(zlib.crc32(repr(("dys", shape)).encode()))
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 16, (Oc, K), dtype=np.uint8)
+    tb = t(r.standard_normal(65536).astype(np.float32))
+    go = t(r.standard_normal((N, Oc, Lc)).astype(np.float32))
+    c = t((r.random(Oc) * 3e-3 + 1e-4).astype(np.float32))
+    op = ops.pack_rows_u8(t(xi))
+    a = ops.custom_grads(op, t(wi), go, tb, tb, N, K, Lc, wbase=0, dy_scale=c)
+    b = ops.custom_grads(op, t(wi), go * c.view(1, -1, 1), tb, tb, N, K, Lc, wbase=0)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
 def test_custom_grad_dx_narrow_matches_general():
