@@ -549,10 +549,12 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
     const int slot_bytes = p.Rpad * 2;                  // one k-row of the operand
     // The operand's quads are rotated (slot s of row r holds tap
     // 4j + (((r >> 2) + s) & 3)), so at sub-step s every lane reads slot s:
-    // a scalar offset.  Quads past the chunk read through an empty view (0).
+    // a scalar offset.  Quads past the chunk, and every quad of a wave past
+    // the tile (whose rows can lie past the operand's padded rows when a
+    // short last tile ends near Rpad), read through an empty view (0).
     auto quad_rows = [&](int j) {                       // descriptor of quad j's slots
       return buffer_rsrc(xtile + (long long)(kb + TPL * j) * p.Rpad,
-                         j < nq ? TPL * slot_bytes : 0);
+                         j < nq && active ? TPL * slot_bytes : 0);
     };
     auto wtab = [&](int t) {                            // weight column of table t
       return wcol + (long long)(kb + min(t, n - 1)) * p.Opad;
@@ -823,28 +825,36 @@ struct Plan { int tiles_r, tiles_o, splits, k_chunk, sk_per, nqt, sk_dp, rt; };
 // device query, so the workspace query and the launch always agree.
 constexpr int PLAN_CUS = 256;
 
-// Split-K count by a cost model in units of one k-step of one workgroup:
-//   ceil(tiles*S / CUs) rounds x (k-chunk + 6 fixed steps per workgroup)
+// Plan by a cost model in units of one k-step of one full-tile workgroup,
+// over the rows per tile rt (2048, 1792, 1536, 1280 or 768, keeping
+// ceil(R / rt) tiles inside the operand's padded rows) and the split-K count S:
+//   ceil(tiles(rt) * S / CUs) rounds x (k-chunk + 6 fixed steps) x f(rt)
 //   + for S > 1: 4 steps for the reduce launch and S x (R*O / 600000) steps
-//     for writing and re-reading one int32 partial slice (8 bytes per
-//     output at ~4 TB/s against ~1.2 us per k-step).
+//     for writing and re-reading one int32 partial slice,
+// with f(rt) = 0.7 + 0.3 rt / 2048 the cost of a k-step of a smaller tile (the
+// table build, its loads and the quad barrier do not shrink with the rows).
+// Fitted to a sweep of (rt, S) over the 19 distinct ResNet-50 layer shapes
+// at batch 64 (the model's picks land within 0.2% of the sweep's best);
+// rt = 1024 is left out (slower than 768 or 1280 on every shape measured).
 // k-chunks are whole quads of tables (multiples of 4); S is at least
-// ceil(K / kmax), the exact-int32 bound of one pass, and the smallest S among
-// equal costs wins.
-// Stream-K (K <= kmax): floor(tiles / CUs) full rounds of whole tiles, then
-// the T = tail tiles * ceil(K/4) quads of the rest dealt out evenly,
-// per = ceil(T / CUs) quads per workgroup, which ends the partial last
-// round.  Cost, fitted to the split-K / stream-K times of the 19 distinct
-// ResNet-50 layer shapes at batch 64 (~0.95 us per k-step):
+// ceil(K / kmax), the exact-int32 bound of one pass, and the smallest cost
+// wins (ties: the larger rt, then the smaller S).
+// Stream-K (K <= kmax, at the default rt): floor(tiles / CUs) full rounds of
+// whole tiles, then the T = tail tiles * ceil(K/4) quads of the rest dealt
+// out evenly, per = ceil(T / CUs) quads per workgroup, which ends the
+// partial last round.  Cost, fitted to the split-K / stream-K times of the
+// 19 distinct ResNet-50 layer shapes at batch 64 (~0.95 us per k-step):
 //   rounds * (K + 14) + 4 * per + 14 per tail segment a workgroup runs
 //   (ceil(per / nqt) + 1 at most; table prologue and atomic sums) + 0.1 per
 //   cut tile (its 256 KiB slot) + 45 for the clear / finish launches.
-// It is taken when cheaper than the best split-K plan.  ATX_LUT_SCHEDULE
-// (environment: auto | split | stream_k) overrides the choice.
+// It is taken when cheaper than the best split-K plan (5 of the 19 shapes,
+// e.g. K = 576 at 56 x 56 with 64 channels: 460 against 491 us).
+// ATX_LUT_SCHEDULE (environment: auto | split | stream_k) overrides the
+// choice; ATX_LUT_ROWS and ATX_LUT_SPLITS force the rows per tile and the
+// split count (split-K plans), for measurement.
 // ws_limit >= 0 caps the workspace: split counts whose int32 partials exceed
-// it are not considered, and neither is stream-K if its slots do; when even
-// the smallest admissible split count (set by the int32-exactness bound)
-// needs more, the plan's splits is -1.
+// it are not considered; when even the smallest admissible split count (set
+// by the int32-exactness bound) needs more, the plan's splits is -1.
 constexpr long long SK_SLOT_BYTES = (long long)(PLAN_CUS - 1) * RT * OT * 4;
 
 static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit = -1) {
@@ -855,32 +865,61 @@ static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit =
   pl.rt = R > 0 ? (int)std::min<long long>(RT, cdiv(cdiv(R, pl.tiles_r), RPW) * RPW) : RT;
   pl.tiles_o = (int)cdiv(O, OT);
   pl.sk_per = 0;
+  pl.sk_dp = 0;
   pl.nqt = (int)cdiv(K, TPL);
   if (K <= 0) { pl.splits = 1; pl.k_chunk = 1; return pl; }
-  const long long tiles = (long long)pl.tiles_r * pl.tiles_o;
+  const char* sched = getenv("ATX_LUT_SCHEDULE");
+  const bool force_sk = sched && !strcmp(sched, "stream_k");
+  const char* force_rows = getenv("ATX_LUT_ROWS");
+  const char* force_s = getenv("ATX_LUT_SPLITS");
   const long long cus = PLAN_CUS;
   const int smin = (int)cdiv(K, kmax);
+  const int fs = force_s ? std::max(smin, atoi(force_s)) : 0;
   const double slice = (double)R * O / 600000.0;
+  const long long rows_cap = cdiv(R, RT) * RT;
+  static const int kRows[] = {2048, 1792, 1536, 1280, 768};
+  int cand[6], nc = 0;
+  if (force_rows) {
+    const int rt = atoi(force_rows);
+    if (rt >= RPW && rt <= RT && rt % RPW == 0 && R > 0 && cdiv(R, rt) * rt <= rows_cap)
+      cand[nc++] = rt;
+  }
+  if (nc == 0) {
+    if (force_sk || R <= 0) {
+      cand[nc++] = pl.rt;
+    } else {
+      cand[nc++] = pl.rt;
+      for (int rt : kRows)
+        if (rt < pl.rt && cdiv(R, rt) * rt <= rows_cap) cand[nc++] = rt;
+    }
+  }
   long long best_kc = cdiv(cdiv(K, smin), TPL) * TPL;
+  int best_rt = pl.rt;
   double best_cost = 0.0;
   bool found = false;
-  for (int S = smin; S <= std::max(smin, 64); ++S) {
-    const long long kc = cdiv(cdiv(K, S), TPL) * TPL;
-    if (S > smin && kc < 16) break;
-    const long long splits = cdiv(K, kc);
-    if (ws_limit >= 0 && splits > 1 && splits * R * O * 4 > ws_limit) continue;
-    const double cost = (double)cdiv(tiles * splits, cus) * (double)(kc + 6) +
-                        (splits > 1 ? 4.0 + splits * slice : 0.0);
-    if (!found || cost < best_cost) { best_kc = kc; best_cost = cost; found = true; }
+  for (int c = 0; c < nc; ++c) {
+    const int rt = cand[c];
+    const long long tiles = cdiv(R, rt) * pl.tiles_o;
+    const double f = 0.7 + 0.3 * rt / RT;
+    for (int S = fs ? fs : smin; S <= (fs ? fs : std::max(smin, 64)); ++S) {
+      const long long kc = cdiv(cdiv(K, S), TPL) * TPL;
+      if (S > smin && kc < 16 && !fs) break;
+      const long long splits = cdiv(K, kc);
+      if (ws_limit >= 0 && splits > 1 && splits * R * O * 4 > ws_limit) continue;
+      const double cost = (double)cdiv(tiles * splits, cus) * (double)(kc + 6) * f +
+                          (splits > 1 ? 4.0 + splits * slice : 0.0);
+      if (!found || cost < best_cost) {
+        best_kc = kc; best_cost = cost; best_rt = rt; found = true;
+      }
+    }
   }
-  pl.sk_dp = 0;
   if (!found) { pl.splits = -1; pl.k_chunk = 1; return pl; }
   pl.k_chunk = (int)std::min<long long>(best_kc, kmax);
   pl.splits = (int)cdiv(K, pl.k_chunk);
-  const char* sched = getenv("ATX_LUT_SCHEDULE");
-  const int force = !sched ? 0 : !strcmp(sched, "stream_k") ? 1 : !strcmp(sched, "split") ? -1 : 0;
-  if (K <= kmax && tiles % cus != 0 && force >= 0 &&
-      (ws_limit < 0 || SK_SLOT_BYTES <= ws_limit)) {
+  // stream-K at the default rows per tile, when forced or cheaper
+  const long long tiles = (long long)pl.tiles_r * pl.tiles_o;
+  const bool split_only = (sched && !strcmp(sched, "split")) || force_rows || force_s;
+  if (!split_only && K <= kmax && tiles % cus != 0 && (ws_limit < 0 || SK_SLOT_BYTES <= ws_limit)) {
     const long long rounds = tiles / cus;
     const long long tail = tiles - rounds * cus;
     const long long T = tail * pl.nqt;
@@ -889,12 +928,15 @@ static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit =
       const long long cuts = std::min<long long>(tail, cdiv(T, per) - 1);
       const double sk_cost = (double)rounds * (K + 14) + 4.0 * per +
                              14.0 * (double)(cdiv(per, pl.nqt) + 1) + 0.1 * cuts + 45.0;
-      if (force > 0 || sk_cost < best_cost) {
+      if (force_sk || sk_cost < best_cost) {
         pl.sk_per = (int)per;
         pl.sk_dp = (int)(rounds * cus);
+        return pl;                       // default rows per tile
       }
     }
   }
+  pl.rt = best_rt;
+  pl.tiles_r = R > 0 ? (int)cdiv(R, best_rt) : pl.tiles_r;
   return pl;
 }
 

@@ -190,18 +190,40 @@ def test_lut_gemm_stream_k_full_round_then_tail_sampled(monkeypatch):
     _check_sampled(y, xi, wi, lut, r, 2)
 
 
-def test_lut_gemm_auto_schedule_takes_stream_k_on_resnet_layer(monkeypatch):
+def test_lut_gemm_resnet_layer_plans_sampled(monkeypatch):
     """ResNet-50 layer2 1x1 conv at batch 64 (R = 200704, K = 256, O = 128,
-    392 tiles): the cost model picks stream-K; dequant epilogue, sampled."""
-    monkeypatch.delenv("ATX_LUT_SCHEDULE", raising=False)
+    392 tiles): the cost model picks stream-K; the split-K-only plan (rows
+    per tile and split count from the model) gives the same exact sums
+    (sampled)."""
     N, K, L, Oc = 64, 256, 3136, 128
-    assert ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc) == SK_WORKSPACE
     r = gen(29)
     xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
     wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
     lut = luts(8)["perturbed"]
-    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32)).cpu().numpy()
-    _check_sampled(y, xi, wi, lut, r, 4)
+    for sched in ("auto", "split"):
+        monkeypatch.setenv("ATX_LUT_SCHEDULE", sched)
+        ws = ops.L.query("atx_lut_gemm_workspace_bytes", N, K, L, Oc)
+        assert (ws == SK_WORKSPACE) == (sched == "auto")
+        y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32)).cpu().numpy()
+        _check_sampled(y, xi, wi, lut, r, 4)
+
+
+@pytest.mark.parametrize("rows", [768, 1280, 1536, 1792])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_lut_gemm_row_tiles_exact(rows, splits, monkeypatch):
+    """Tiles of fewer than 2048 rows (whole waves; the waves past the tile
+    only build tables) with and without split-K: exact against the oracle.
+    R = 3300 rows: 768 -> 5 tiles, 1280 -> 3, 1792 -> 2 (the last partial);
+    1536 would need 4608 padded rows and falls back to the default tile."""
+    monkeypatch.setenv("ATX_LUT_ROWS", str(rows))
+    monkeypatch.setenv("ATX_LUT_SPLITS", str(splits))
+    N, K, L, Oc = 3, 300, 1100, 70
+    r = gen(zlib.crc32(repr(("rows", rows, splits)).encode()))
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    lut = luts(4)["i16_edge"]
+    y = ops.lut_gemm_i32(t(xi), t(wi), t(lut, torch.float32))
+    assert np.array_equal(y.cpu().numpy().astype(np.int64), O.lut_gemm_i64(xi, wi, lut))
 
 
 def test_lut_gemm_config3_full_shape_sampled():

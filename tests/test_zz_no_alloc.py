@@ -60,16 +60,22 @@ def _run(N, K, Lc, Oc, seed, out_kind):
     return y, y_ref, wsb
 
 
-# (N, K, L, O): stream-K plan (256-KiB slots), then a smaller split-K plan,
-# then a smaller whole-tile plan (no scratch)
+# (N, K, L, O): stream-K plan (256-KiB slots, forced), then a smaller split-K
+# plan, then a smaller whole-tile plan (no scratch)
 CALLS = [(64, 256, 3136, 128), (8, 576, 1024, 64), (2, 4, 100, 20)]
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("out_kind", [1, 2])          # ATX_OUT_I32, ATX_OUT_DEQUANT
-def test_noalloc_matches_workspace_entry_point_on_consecutive_calls(out_kind):
+def test_noalloc_matches_workspace_entry_point_on_consecutive_calls(out_kind, monkeypatch):
+    """The first call forces the stream-K schedule (ATX_LUT_SCHEDULE, read by
+    both entry points); the others take the automatic plan."""
     kinds = []
     for i, (N, K, Lc, Oc) in enumerate(CALLS):
+        if i == 0:
+            monkeypatch.setenv("ATX_LUT_SCHEDULE", "stream_k")
+        else:
+            monkeypatch.delenv("ATX_LUT_SCHEDULE", raising=False)
         print(f"noalloc call {i}: N={N} K={K} L={Lc} O={Oc} out_kind={out_kind}", flush=True)
         y, y_ref, wsb = _run(N, K, Lc, Oc, 100 + i, out_kind)
         kinds.append(wsb)
@@ -79,9 +85,10 @@ def test_noalloc_matches_workspace_entry_point_on_consecutive_calls(out_kind):
 
 
 @pytest.mark.gpu
-def test_noalloc_repeated_call_clears_stale_slots():
+def test_noalloc_repeated_call_clears_stale_slots(monkeypatch):
     """The array keeps the previous call's contents; stream-K slots must be
     cleared by every call (the same problem twice gives the same sums)."""
+    monkeypatch.setenv("ATX_LUT_SCHEDULE", "stream_k")
     N, K, Lc, Oc = CALLS[0]
     y1, y_ref, _ = _run(N, K, Lc, Oc, 7, L.ATX_OUT_I32)
     y2, _, _ = _run(N, K, Lc, Oc, 7, L.ATX_OUT_I32)
