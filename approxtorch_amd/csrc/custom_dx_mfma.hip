@@ -111,6 +111,8 @@ __device__ __forceinline__ void split_parts(const float (&d)[8], u32x4 (&P)[3]) 
 __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
   __shared__ __align__(16) unsigned char hbuf[2 * HBUF];
   __shared__ __align__(16) unsigned char xtab[256 * XS];
+  // the epilogue's row offsets, per wave: 16 operand slots x 32 rows
+  __shared__ __align__(16) uint16_t xsh[NWAVE][KT][RB * 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, j = lane & 15;
@@ -192,6 +194,13 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
 #pragma unroll
       for (int t = 0; t < KT; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // row offsets of the tile's 16 slots for the wave's 32 rows: lane l loads
+    // slot l / 4, rows 8 (l % 4) .. + 7 with one 16-byte load in the last
+    // step, into the registers of dy's prefetch (free there), staged through
+    // LDS for the epilogue; slots past K read 0
+    const unsigned xq_off =
+        ((unsigned)(k0 + (lane >> 2)) * (unsigned)p.Rpad +
+         (unsigned)(rt * ROWS + wave * (RB * 16) + 8 * (lane & 3))) * 2u;
     float raw[RB][8], fac[8];
     {
       uint2 w0[2];
@@ -216,6 +225,11 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
       if (more) {
         load_w(s + 1, wn);
         load_dy(s + 1, raw, fac);
+      } else {
+        const uint4 q =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xtr, xq_off, 0, 0));
+        raw[0][0] = __uint_as_float(q.x); raw[0][1] = __uint_as_float(q.y);
+        raw[0][2] = __uint_as_float(q.z); raw[0][3] = __uint_as_float(q.w);
       }
       // H fragments of tap quad tq + 1 are read while quad tq's MFMAs issue
       const unsigned char* hb = hbuf + (s & 1) * HBUF + lane * 16;
@@ -244,18 +258,18 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
     }
 
     // epilogue: grad_x[r, k] = sum_w DX[xi(r,k)][wbase + w] * S[w][r]
+    *(uint4*)&xsh[wave][lane >> 2][8 * (lane & 3)] =
+        make_uint4(__float_as_uint(raw[0][0]), __float_as_uint(raw[0][1]),
+                   __float_as_uint(raw[0][2]), __float_as_uint(raw[0][3]));
+    __builtin_amdgcn_wave_barrier();          // the wave's own rows: no workgroup barrier
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = rt * ROWS + wave * (RB * 16) + b * 16 + j;
       unsigned xo[KT];
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const int k = std::min(k0 + t, p.K - 1);
-        xo[t] = __builtin_amdgcn_raw_buffer_load_b32(
-                    xtr, ((unsigned)operand_slot(k, r) * (unsigned)p.Rpad + (unsigned)r) * 2u &
-                             ~3u, 0, 0);
-        xo[t] = (r & 1) ? (xo[t] >> 16) : (xo[t] & 0xffffu);
-      }
+      for (int t = 0; t < KT; ++t)            // slot of tap k0 + t for row r (k0 % 4 == 0)
+        xo[t] = xsh[wave][(t & ~3) | ((t - (r >> 2)) & 3)][b * 16 + j];
 #pragma unroll
       for (int tq = 0; tq < KT / 4; ++tq) {
         float part[4];
