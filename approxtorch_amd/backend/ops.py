@@ -762,8 +762,11 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
         tab = lut_image(dx_lut)[1]
         gx = torch.empty((N, K, Lc), dtype=torch.float32, device=dev)
         if wbase is not None:
-            L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
-                   L.ptr(dy_scale), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
+            dyx, dsx = dyc, dy_scale
+            if dy_scale is not None and O > 4096:   # the kernel holds at most 4096 factors
+                dyx, dsx = dyc * dy_scale.view(1, -1, 1), None
+            L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyx),
+                   L.ptr(dsx), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
         else:
             dyx = dyc if dy_scale is None else dyc * dy_scale.view(1, -1, 1)
             L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyx),

@@ -50,6 +50,7 @@ constexpr int XS = 80;                       // bytes per table row in LDS (64 +
 constexpr int HTAP = 64 * 16;                // bytes of one tap's H fragments
 constexpr int HBUF = KT * HTAP;              // one step's H fragments (16 KiB)
 constexpr unsigned OOB = 0x80000000u;        // buffer offset past any operand
+constexpr int FMAX = 4096;                   // channels with a dy factor (LDS)
 
 struct Params {
   const uint16_t* xt; int Rpad;              // row-offset operand [Kpad][Rpad]
@@ -113,126 +114,137 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
   __shared__ __align__(16) unsigned char xtab[256 * XS];
   // the epilogue's row offsets, per wave: 16 operand slots x 32 rows
   __shared__ __align__(16) uint16_t xsh[NWAVE][KT][RB * 16];
+  // dy's per-channel factors (zero past O)
+  __shared__ __align__(16) float fsh[FMAX];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, j = lane & 15;
+  const int nsteps = (p.O + OC - 1) / OC;
 
   // the table's 16 columns wbase .. wbase + 15 as rows of 16 fp32
   for (int e = tid; e < 256 * 16; e += NT) {
     const int w = e >> 8, v = e & 255;
     *(float*)(xtab + v * XS + w * 4) = p.tab[(p.wbase + w) * 256 + v];
   }
+  if (p.dys)
+    for (int e = tid; e < nsteps * OC; e += NT) fsh[e] = e < p.O ? p.dys[e] : 0.f;
 
   const __amdgpu_buffer_rsrc_t dyr = rsrc(p.dy, p.dy_bytes);
   const __amdgpu_buffer_rsrc_t wtr = rsrc(p.wt, p.wt_bytes);
   const __amdgpu_buffer_rsrc_t xtr = rsrc(p.xt, p.xt_bytes);
   const unsigned wrep = (unsigned)j * 0x01010101u;
   const unsigned brep = (unsigned)p.wbase * 0x01010101u;
-  const int nsteps = (p.O + OC - 1) / OC;
   const int chan_bytes = p.L * 4;
   const int ptail = p.O - (nsteps - 1) * OC;           // channels of the last step
 
-  // persistent over the tiles; each XCD walks a contiguous range
+  // Persistent over the tiles (each XCD walks a contiguous range), one
+  // pipeline across tile boundaries: the last channel step of a tile
+  // prefetches the next tile's first dy block and index bytes and builds its
+  // first H fragments, so a tile starts with its operands in place.
   const int nb = gridDim.x, bid = blockIdx.x;
-  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3;   // nb is a multiple of 8
-  for (int it = 0;; ++it) {
-    const long long lt = (long long)it * nb + xcd * per + slot;
-    if (lt >= p.tiles) break;
-    const int tile = (int)lt;
-    const int rt = tile / p.tiles_k, kt = tile - rt * p.tiles_k;
-    const int k0 = kt * KT;
+  const int xcd = bid & 7, bslot = bid >> 3, per = nb >> 3;   // nb is a multiple of 8
+  auto tile_at = [&](int it) { return (long long)it * nb + xcd * per + bslot; };
 
-    // rows of the lane's two blocks
-    unsigned dyoff[RB];
-    long long gbase[RB];
-    bool rvalid[RB];
+  // per-tile operand addresses of this lane
+  struct Where { int rt, k0, kh0, kh1; unsigned dyoff[RB]; };
+  auto where = [&](int tile, Where& w) {
+    w.rt = tile / p.tiles_k;
+    w.k0 = (tile - w.rt * p.tiles_k) * KT;
+    // this wave's two taps of H (indices of tap k >= K are never stored)
+    w.kh0 = std::min(w.k0 + 2 * wave, p.K - 1);
+    w.kh1 = std::min(w.k0 + 2 * wave + 1, p.K - 1);
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const int r = rt * ROWS + wave * (RB * 16) + b * 16 + j;
+      const int r = w.rt * ROWS + wave * (RB * 16) + b * 16 + j;
       const int n = r / p.L, l = r - n * p.L;
-      rvalid[b] = r < p.R;
-      dyoff[b] = rvalid[b] ? (unsigned)((((long long)n * p.O + 8 * g) * p.L + l) * 4) : OOB;
-      gbase[b] = (long long)n * p.K * p.L + l;
+      w.dyoff[b] = r < p.R ? (unsigned)((((long long)n * p.O + 8 * g) * p.L + l) * 4) : OOB;
     }
-    // this wave's two taps of H (indices of tap k >= K are never stored)
-    const int kh0 = std::min(k0 + 2 * wave, p.K - 1), kh1 = std::min(k0 + 2 * wave + 1, p.K - 1);
-    auto load_w = [&](int s, uint2 (&w)[2]) {
-      const int ob = s * OC + 8 * g;
-      w[0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                           wtr, ob, kh0 * p.Opad, 0));
-      w[1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                           wtr, ob, kh1 * p.Opad, 0));
-    };
-    auto load_dy = [&](int s, float (&d)[RB][8], float (&f)[8]) {
-      const int nvalid = s == nsteps - 1 ? ptail - 8 * g : 8;   // channels below O
+  };
+  auto load_w = [&](const Where& w, int s, uint2 (&wv)[2]) {
+    const int ob = s * OC + 8 * g;
+    wv[0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                          wtr, ob, w.kh0 * p.Opad, 0));
+    wv[1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                          wtr, ob, w.kh1 * p.Opad, 0));
+  };
+  auto load_dy = [&](const Where& w, int s, float (&d)[RB][8]) {
+    const int nvalid = s == nsteps - 1 ? ptail - 8 * g : 8;   // channels below O
 #pragma unroll
-      for (int b = 0; b < RB; ++b)
+    for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-          d[b][c] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(
-                         dyr, c < nvalid ? dyoff[b] : OOB, (s * OC + c) * chan_bytes, 0));
-      if (p.dys) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) f[c] = p.dys[std::min(s * OC + 8 * g + c, p.O - 1)];
-      }
-    };
-    auto write_h = [&](int s, const uint2 (&w)[2]) {
-      uint2 keep = {0xffffffffu, 0xffffffffu};
-      if (s == nsteps - 1) {
-        const int nv = ptail - 8 * g;
-        keep = {byte_mask(nv), byte_mask(nv - 4)};
-      }
-      unsigned char* dst = hbuf + (s & 1) * HBUF + (2 * wave) * HTAP + lane * 16;
-      *(u32x4*)dst = h_fragment(w[0], brep, wrep, keep);
-      *(u32x4*)(dst + HTAP) = h_fragment(w[1], brep, wrep, keep);
-    };
+      for (int c = 0; c < 8; ++c)
+        d[b][c] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       dyr, c < nvalid ? w.dyoff[b] : OOB, (s * OC + c) * chan_bytes, 0));
+  };
+  auto write_h = [&](int s, const uint2 (&wv)[2], int buf) {
+    uint2 keep = {0xffffffffu, 0xffffffffu};
+    if (s == nsteps - 1) {
+      const int nv = ptail - 8 * g;
+      keep = {byte_mask(nv), byte_mask(nv - 4)};
+    }
+    unsigned char* dst = hbuf + buf * HBUF + (2 * wave) * HTAP + lane * 16;
+    *(u32x4*)dst = h_fragment(wv[0], brep, wrep, keep);
+    *(u32x4*)(dst + HTAP) = h_fragment(wv[1], brep, wrep, keep);
+  };
 
+  int it = 0;
+  if (tile_at(0) >= p.tiles) return;           // every wave of the workgroup alike
+  Where cur, nxt;
+  where((int)tile_at(0), cur);
+  float raw[RB][8];
+  {
+    uint2 w0[2];
+    load_w(cur, 0, w0);
+    load_dy(cur, 0, raw);
+    write_h(0, w0, 0);
+  }
+  __syncthreads();
+  int hsel = 0;
+
+  for (;;) {
+    const long long ln = tile_at(it + 1);
+    const bool has_next = ln < p.tiles;
+    if (has_next) where((int)ln, nxt);
     f32x4 acc[RB][KT];
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
       for (int t = 0; t < KT; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // row offsets of the tile's 16 slots for the wave's 32 rows: lane l loads
-    // slot l / 4, rows 8 (l % 4) .. + 7 with one 16-byte load in the last
-    // step, into the registers of dy's prefetch (free there), staged through
-    // LDS for the epilogue; slots past K read 0
-    const unsigned xq_off =
-        ((unsigned)(k0 + (lane >> 2)) * (unsigned)p.Rpad +
-         (unsigned)(rt * ROWS + wave * (RB * 16) + 8 * (lane & 3))) * 2u;
-    float raw[RB][8], fac[8];
-    {
-      uint2 w0[2];
-      load_w(0, w0);
-      load_dy(0, raw, fac);
-      write_h(0, w0);
-    }
-    __syncthreads();
+    uint4 xq = {0u, 0u, 0u, 0u};
 
     for (int s = 0; s < nsteps; ++s) {
-      u32x4 P[RB][3];
       if (p.dys) {            // dy * factor[o], the product the caller would form
+        const float4 f0 = *(const float4*)&fsh[s * OC + 8 * g];
+        const float4 f1 = *(const float4*)&fsh[s * OC + 8 * g + 4];
+        const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
         for (int b = 0; b < RB; ++b)
 #pragma unroll
-          for (int c = 0; c < 8; ++c) raw[b][c] *= fac[c];
+          for (int c = 0; c < 8; ++c) raw[b][c] *= f[c];
       }
+      u32x4 P[RB][3];
 #pragma unroll
       for (int b = 0; b < RB; ++b) split_parts(raw[b], P[b]);
-      const bool more = s + 1 < nsteps;
+      const bool last = s + 1 == nsteps;
       uint2 wn[2];
-      if (more) {
-        load_w(s + 1, wn);
-        load_dy(s + 1, raw, fac);
+      if (!last) {
+        load_w(cur, s + 1, wn);
+        load_dy(cur, s + 1, raw);
       } else {
-        const uint4 q =
-            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xtr, xq_off, 0, 0));
-        raw[0][0] = __uint_as_float(q.x); raw[0][1] = __uint_as_float(q.y);
-        raw[0][2] = __uint_as_float(q.z); raw[0][3] = __uint_as_float(q.w);
+        // row offsets of the tile's 16 slots for the wave's 32 rows: lane l
+        // loads slot l / 4, rows 8 (l % 4) .. + 7 (slots past K read 0)
+        const unsigned xq_off =
+            ((unsigned)(cur.k0 + (lane >> 2)) * (unsigned)p.Rpad +
+             (unsigned)(cur.rt * ROWS + wave * (RB * 16) + 8 * (lane & 3))) * 2u;
+        xq = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xtr, xq_off, 0, 0));
+        if (has_next) {
+          load_w(nxt, 0, wn);
+          load_dy(nxt, 0, raw);
+        }
       }
       // H fragments of tap quad tq + 1 are read while quad tq's MFMAs issue
-      const unsigned char* hb = hbuf + (s & 1) * HBUF + lane * 16;
+      const unsigned char* hb = hbuf + hsel * HBUF + lane * 16;
       u32x4 H[2][4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) H[0][t] = *(const u32x4*)(hb + t * HTAP);
@@ -253,19 +265,22 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
                   __builtin_bit_cast(bf16x8, H[tq & 1][t]), __builtin_bit_cast(bf16x8, P[b][q]),
                   acc[b][4 * tq + t], 0, 0, 0);
       }
-      if (more) write_h(s + 1, wn);
+      if (!last) write_h(s + 1, wn, hsel ^ 1);
+      else if (has_next) write_h(0, wn, hsel ^ 1);
       __syncthreads();
+      hsel ^= 1;
     }
 
     // epilogue: grad_x[r, k] = sum_w DX[xi(r,k)][wbase + w] * S[w][r]
-    *(uint4*)&xsh[wave][lane >> 2][8 * (lane & 3)] =
-        make_uint4(__float_as_uint(raw[0][0]), __float_as_uint(raw[0][1]),
-                   __float_as_uint(raw[0][2]), __float_as_uint(raw[0][3]));
+    *(uint4*)&xsh[wave][lane >> 2][8 * (lane & 3)] = xq;
     __builtin_amdgcn_wave_barrier();          // the wave's own rows: no workgroup barrier
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const int r = rt * ROWS + wave * (RB * 16) + b * 16 + j;
+      const int r = cur.rt * ROWS + wave * (RB * 16) + b * 16 + j;
+      const int n = r / p.L, l = r - n * p.L;
+      const bool rvalid = r < p.R;
+      const long long gbase = (long long)n * p.K * p.L + l;
       unsigned xo[KT];
 #pragma unroll
       for (int t = 0; t < KT; ++t)            // slot of tap k0 + t for row r (k0 % 4 == 0)
@@ -290,10 +305,13 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
         const float q0 = k0v + __shfl_xor(s0, 32), q1 = k1v + __shfl_xor(s1, 32);
         const float sx = lo ? q0 : q1, kx = lo ? q1 : q0;
         const float tot = kx + __shfl_xor(sx, 16);
-        const int k = k0 + 4 * tq + g;
-        if (rvalid[b] && k < p.K) p.gx[gbase[b] + (long long)k * p.L] = tot;
+        const int k = cur.k0 + 4 * tq + g;
+        if (rvalid && k < p.K) p.gx[gbase + (long long)k * p.L] = tot;
       }
     }
+    if (!has_next) break;
+    cur = nxt;
+    ++it;
   }
 }
 
@@ -320,6 +338,8 @@ int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, i
               "atx_custom_grad_dx_narrow: Rpad must be a multiple of %d and >= N*L",
               ATX_ROW_TILE);
   ATX_REQUIRE(Opad >= O && Opad % 32 == 0, "atx_custom_grad_dx_narrow: Opad must be a multiple of 32 and >= O");
+  ATX_REQUIRE(!dy_scale || O <= ohx::FMAX,
+              "atx_custom_grad_dx_narrow: dy_scale supports at most %d channels", ohx::FMAX);
   ATX_REQUIRE(R * O * 4 < 0x7fffffffLL && (long long)K * Opad < 0x7fffffffLL &&
                   (long long)operand_rows(K) * Rpad * 2 < 0x7fffffffLL,
               "atx_custom_grad_dx_narrow: operand too large for 32-bit buffer offsets");
