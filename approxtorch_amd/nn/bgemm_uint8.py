@@ -285,7 +285,7 @@ class _conv2d_uint8_fused(Function):
         gx = gw = gb = None
         # zero-point terms: -sum_o g' z_w[o] per position (a [1 x O] by [O x L]
         # product per image) and -z_x sum_{n,l} g' per channel
-        gxs = torch.matmul((c * zw).view(1, O), go).view(g.N, Lc).neg_() if need_x else None
+        gxs = torch.matmul((c * zw).neg_().view(1, O), go).view(g.N, Lc) if need_x else None
         gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
         if ctx.kind == 'custom':
             grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, go, tx if need_x else None,
@@ -304,7 +304,7 @@ class _conv2d_uint8_fused(Function):
                 grad_q += ops.tap_sum_backward(gxs, g)
                 gx = ops.fakequant_per_tensor_backward(grad_q, mask_x, sx)
         if need_w:
-            gw_q += (gsum * c).mul_(zx).neg_().view(-1, 1)
+            gw_q -= (gsum * c).mul_(zx).view(-1, 1)
             gw = ops.fakequant_per_tensor_backward(gw_q, mask_w, sw, channels=O,
                                                    inner=K).view(ctx.wshape)
         if need_b:
