@@ -26,6 +26,7 @@
 // mode: plain fp32 products, fp32 accumulation.
 
 #include "atx_internal.h"
+#include "atx_tiles.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -47,6 +48,108 @@ template <int B> struct PMajor {          // [B][BK + 4]: bank(i, k) = 36i + k
   static constexpr int SIZE = B * LDP;
   __device__ static int at(int m, int k) { return m * LDP + k; }
 };
+
+// ------------------------------------------------ split-bf16 operand planes
+// gfx950's bf16 matrix cores (v_mfma_f32_16x16x32_bf16: a 16 x 16 x 32 block
+// in 16 cycles) do 16 times the products per cycle of its fp32 ones
+// (v_mfma_f32_16x16x4f32: 16 x 16 x 4 in 32).  An fp32 value a splits exactly
+// into three bf16 parts a = ah + am + al by truncation: ah is a with its low
+// 16 bits cleared, r = a - ah is exact in fp32 with at most 16 significant
+// bits, am is r truncated the same way and al = r - am has at most 8.  The
+// product a*b is taken as the six part products of order <= 2,
+//   ah*bh + ah*bm + am*bh + ah*bl + am*bm + al*bh,
+// each exact in fp32 (8 x 8 significant bits), summed in fp32.  The dropped
+// products am*bl + al*bm + al*bl stay below 2^-20 |a b| (|am| < 2^-7 |a|,
+// |al| < 2^-14 |a|), on average about 2^-23 |a b|, the size of an fp32
+// product's own rounding.  An operand whose values are bf16 already (the
+// STE's quantized integers, or any table whose m and l parts are all zero)
+// has only its h part: three products, each exact, instead of six.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Which part products a tile multiply takes.
+enum PartProducts { PROD6 = 0, A_EXACT = 1, B_EXACT = 2 };
+
+// Operand tile of B rows x BK contraction elements as three bf16 planes
+// (h, m, l) of B x 64 bytes.  Row r is stored at s = r ^ ((r >> 2) & 1) and
+// its four 16-byte units (8 contraction elements each) are XOR-swizzled by
+// (s >> 1) & 3: the MFMA fragment reads (8 lanes = rows 0..7 of one unit)
+// and the loaders' 8-byte stores (16 lanes = two rows r, r + 1 or r, r + 4,
+// eight 8-byte groups each) are then bank-conflict-free.
+template <int B> struct Planes {
+  static constexpr int PLANE = B * 64;
+  static constexpr int SIZE = 3 * PLANE;
+  // byte offset of contraction elements k..k+3 (k % 4 == 0) of row r
+  __device__ static int at(int r, int k) {
+    const int s = r ^ ((r >> 2) & 1);
+    return s * 64 + ((((k >> 3) ^ (s >> 1)) & 3) << 4) + ((k & 4) << 1);
+  }
+};
+
+// Parts of four consecutive contraction elements, two bf16 per dword (the
+// lower element in the low half): P[0] = h, P[1] = m, P[2] = l.
+template <bool FULL>
+__device__ __forceinline__ void split4(const float (&v)[4], uint2 (&P)[3]) {
+  unsigned h[4], m[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = __float_as_uint(v[e]);
+    if constexpr (FULL) {
+      const float r = v[e] - __uint_as_float(h[e] & 0xffff0000u);
+      m[e] = __float_as_uint(r);
+      l[e] = __float_as_uint(r - __uint_as_float(m[e] & 0xffff0000u));
+    }
+  }
+  P[0] = make_uint2(__builtin_amdgcn_perm(h[1], h[0], 0x07060302u),
+                    __builtin_amdgcn_perm(h[3], h[2], 0x07060302u));
+  if constexpr (FULL) {
+    P[1] = make_uint2(__builtin_amdgcn_perm(m[1], m[0], 0x07060302u),
+                      __builtin_amdgcn_perm(m[3], m[2], 0x07060302u));
+    P[2] = make_uint2(__builtin_amdgcn_perm(l[1], l[0], 0x07060302u),
+                      __builtin_amdgcn_perm(l[3], l[2], 0x07060302u));
+  }
+}
+
+// Split table: entry i = (h | m << 16, l) of tab[i]; entry 256 is zero (the
+// index of invalid elements).  Returns whether every entry is bf16 exactly
+// (all m and l parts zero).  Needs GT == 256 threads; ends with a barrier.
+__device__ __forceinline__ bool split_table(uint2* stab, const float* tab, int t) {
+  const float v = tab[t];
+  const unsigned u = __float_as_uint(v);
+  const float r = v - __uint_as_float(u & 0xffff0000u);
+  const unsigned ru = __float_as_uint(r);
+  const unsigned lo = __float_as_uint(r - __uint_as_float(ru & 0xffff0000u));
+  stab[t] = make_uint2((u >> 16) | (ru & 0xffff0000u), lo >> 16);
+  if (t == 0) stab[256] = make_uint2(0u, 0u);
+  return __syncthreads_or(r != 0.0f) == 0;
+}
+
+// Parts of four table entries (indices into a split table) in split4's order.
+template <bool FULL>
+__device__ __forceinline__ void lookup4(const uint2* stab, const unsigned (&idx)[4],
+                                        uint2 (&P)[3]) {
+  uint2 e[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = stab[idx[i]];
+  P[0] = make_uint2(__builtin_amdgcn_perm(e[1].x, e[0].x, 0x05040100u),
+                    __builtin_amdgcn_perm(e[3].x, e[2].x, 0x05040100u));
+  if constexpr (FULL) {
+    P[1] = make_uint2(__builtin_amdgcn_perm(e[1].x, e[0].x, 0x07060302u),
+                      __builtin_amdgcn_perm(e[3].x, e[2].x, 0x07060302u));
+    P[2] = make_uint2(__builtin_amdgcn_perm(e[1].y, e[0].y, 0x05040100u),
+                      __builtin_amdgcn_perm(e[3].y, e[2].y, 0x05040100u));
+  }
+}
+
+template <int B, bool FULL>
+__device__ __forceinline__ void put_parts(char* s, int r, int k, const uint2 (&P)[3]) {
+  const int off = Planes<B>::at(r, k);
+  *(uint2*)(s + off) = P[0];
+  if constexpr (FULL) {
+    *(uint2*)(s + Planes<B>::PLANE + off) = P[1];
+    *(uint2*)(s + 2 * Planes<B>::PLANE + off) = P[2];
+  }
+}
 
 // Index of an image element (int8: v + 128, uint8: v, fp32: quant_index).
 template <typename T> __device__ __forceinline__ unsigned img_index(unsigned raw, int offset);
@@ -316,82 +419,84 @@ struct RowCursor {
   }
 };
 
-// Backward-weight A: A(m = o, p = r) = go[n][o][l], PMajor.  VEC needs
-// L % 4 == 0 (quads of rows then share an image and P is a multiple of 4).
+// Backward-weight A: A(m = o, p = r) = go[n][o][l] with r = n*L + l, read by
+// buffer loads from a descriptor that starts at image n0 (the image of the
+// block's first contraction row) and ends at the end of go: rows r >= P lie
+// past its end and read 0, so they add nothing whatever the B operand holds,
+// and rows o >= O read other images' values, whose results the epilogue
+// drops.  The go scale sx * sw[o] is applied to the results instead (it is
+// constant along the contraction).  VEC (L % 4 == 0): a quad of rows lies
+// in one image, one 16-byte load.  Offsets are 32-bit: the host keeps a
+// block's images within 2^31 bytes of go.
 template <int B, bool VEC> struct WeightA {
-  using Lay = PMajor<B>;
   static constexpr int NQ = B / 32;        // quads per thread (rows m, m+32, ...)
-  const float* go; int O, L;
-  const float* sx; const float* sw;        // optional go scale sx * sw[o]
+  __amdgpu_buffer_rsrc_t res;
+  int O, L;
   int pq, mr, m0;
-  RowCursor cur;
+  int n, l;                 // row p0 + pq: image (from n0) and position
   floatx4 raw[NQ];
-  float sc[NQ];
-  unsigned ok;
-  __device__ void init(int t, int mbase, int pb) {
+  __device__ void init(const float* go, long long go_elems, int t, int mbase, int pb) {
     pq = (t & 7) * 4; mr = t >> 3; m0 = mbase;
-    cur.start(pb + pq, L);
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int o = m0 + mr + 32 * i;
-      sc[i] = sw ? sx[0] * sw[o < O ? o : 0] : 1.0f;
-    }
+    const int n0 = pb / L;
+    const long long base = (long long)n0 * O * L;
+    const long long bytes = (go_elems - base) * 4;
+    res = buffer_rsrc(go + base, (int)(unsigned)(bytes < 0xffffffffLL ? bytes : 0xffffffffLL));
+    const int r = pb + pq - n0 * L;
+    n = r / L;
+    l = r - n * L;
   }
-  __device__ void fetch(int p0, int pe) {
-    const int r = p0 + pq;
-    long long rb[4];
-    bool rv[4];
-    {
-      int n = cur.n, l = cur.l;
+  __device__ void fetch(int, int) {
+    const int rowb = 32 * L * 4;           // bytes between a thread's rows o, o + 32
+    const unsigned ob = (unsigned)(m0 + mr);
+    if constexpr (VEC) {
+      const unsigned off = (((unsigned)n * O + ob) * L + l) * 4u;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i)
+        raw[i] = __builtin_bit_cast(floatx4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(res, off, i * rowb, 0));
+    } else {
+      unsigned off[4];
+      int en = n, el = l;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        rv[e] = r + e < pe;
-        rb[e] = (long long)n * O * L + l;
-        if (++l == L) { l = 0; ++n; }
+        off[e] = (((unsigned)en * O + ob) * L + el) * 4u;
+        if (++el == L) { el = 0; ++en; }
       }
-    }
-    ok = 0;
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int o = m0 + mr + 32 * i;
-      const long long ol = (long long)o * L;
-      if constexpr (VEC) {
-        const bool v = o < O && rv[0];
-        raw[i] = *(const floatx4*)(go + (v ? rb[0] + ol : 0));
-        ok |= (v ? 15u : 0u) << (4 * i);
-      } else {
+      for (int i = 0; i < NQ; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool v = o < O && rv[e];
-          raw[i][e] = go[v ? rb[e] + ol : 0];
-          ok |= (v ? 1u : 0u) << (4 * i + e);
-        }
-      }
+        for (int e = 0; e < 4; ++e)
+          raw[i][e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(res, off[e], i * rowb, 0));
     }
   }
-  __device__ void stash(float* s, const float*) const {
+  template <bool FULL> __device__ void put(char* s, const uint2*) const {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      floatx4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (ok >> (4 * i + e)) & 1u ? raw[i][e] * sc[i] : 0.0f;
-      *(floatx4*)&s[Lay::at(mr + 32 * i, pq)] = v;
+      const float v[4] = {raw[i][0], raw[i][1], raw[i][2], raw[i][3]};
+      uint2 P[3];
+      split4<FULL>(v, P);
+      put_parts<B, FULL>(s, mr + 32 * i, pq, P);
     }
   }
-  __device__ void advance() { cur.step(BK, L); }
+  __device__ void advance() {
+    l += BK;
+    while (l >= L) { l -= L; ++n; }
+  }
 };
 
 // Backward-weight B: B(p = r, j = k) = tw[index of image tap k at output
-// position r] (implicit im2col), PMajor.  Out-of-image taps use `pad`.
+// position r] (implicit im2col).  Out-of-image taps use `pad`.  Taps k >= K
+// and rows r >= P (whose A values are 0) take the pad entry; the table's
+// entries are finite, so those products are 0 or dropped by the epilogue.
 template <int B, typename T> struct WeightB {
-  using Lay = PMajor<B>;
   static constexpr int NQ = B / 32;
   const T* img; atx_conv_geom g; int K, L, offset, pad;
   int pq, jr;
   int coff[NQ], dh[NQ], dw[NQ];     // per tap: c*H*W, kh*DH - PH, kw*DW - PW
   unsigned kv;                      // bit i: tap i < K
   int n, oh, ow;                    // output position of row p0 + pq
-  unsigned raw[NQ][4], ok, in;      // in: in-image bit, ok: valid element bit
+  unsigned raw[NQ][4], in;          // in: element read from the image
   __device__ void init(int t, int n0, int pb) {
     pq = (t & 7) * 4; jr = t >> 3;
     const int KK = g.KH * g.KW;
@@ -415,7 +520,7 @@ template <int B, typename T> struct WeightB {
   }
   __device__ void fetch(int p0, int pe) {
     const int r = p0 + pq;
-    ok = 0; in = 0;
+    in = 0;
     int en = n, eh = oh, ew = ow;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -425,29 +530,26 @@ template <int B, typename T> struct WeightB {
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
         const int ih = ih0 + dh[i], iw = iw0 + dw[i];
-        const bool v = rv && ((kv >> i) & 1u);
-        const bool inside = v && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+        const bool inside = rv && ((kv >> i) & 1u) && (unsigned)ih < (unsigned)g.H &&
+                            (unsigned)iw < (unsigned)g.W;
         const T x = img[inside ? nb + coff[i] + ih * g.W + iw : 0];
         if constexpr (sizeof(T) == 4) raw[i][e] = __float_as_uint((float)x);
         else raw[i][e] = (unsigned)(unsigned char)x;
-        ok |= (v ? 1u : 0u) << (4 * i + e);
         in |= (inside ? 1u : 0u) << (4 * i + e);
       }
       if (++ew == g.OW) { ew = 0; if (++eh == g.OH) { eh = 0; ++en; } }
     }
   }
-  __device__ void stash(float* s, const float* tab) const {
+  template <bool FULL> __device__ void put(char* s, const uint2* stab) const {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      floatx4 v;
+      unsigned idx[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int b = 4 * i + e;
-        const unsigned idx = (in >> b) & 1u ? img_index<T>(raw[i][e], offset) : (unsigned)pad;
-        const float x = tab[idx];
-        v[e] = (ok >> b) & 1u ? x : 0.0f;
-      }
-      *(floatx4*)&s[Lay::at(jr + 32 * i, pq)] = v;
+      for (int e = 0; e < 4; ++e)
+        idx[e] = (in >> (4 * i + e)) & 1u ? img_index<T>(raw[i][e], offset) : (unsigned)pad;
+      uint2 P[3];
+      lookup4<FULL>(stab, idx, P);
+      put_parts<B, FULL>(s, jr + 32 * i, pq, P);
     }
   }
   __device__ void advance() {
@@ -464,48 +566,39 @@ template <int B, typename T> struct WeightB {
 // uint16, slot(k, r) = (k & ~3) | ((k - (r >> 2)) & 3), padding taps and
 // rows hold offset 0).  A thread's four rows are one quad and the quad index
 // moves by BK / 4 = 8 per k-tile, so each of its taps stays in one slot: one
-// 8-byte load per (tap, k-tile) and a bit-field extract per element.
+// 8-byte load per (tap, k-tile) and a bit-field extract per element.  Taps
+// k >= K and rows r >= P read padding (finite table entries): their results
+// are dropped or multiplied by A's zeros.
 template <int B> struct WeightBRows {
-  using Lay = PMajor<B>;
   static constexpr int NQ = B / 32;
   const uint16_t* xt; long long Rpad; int K, Kpad;
   int pq, jr;
   const uint16_t* src[NQ];          // slot row of tap i, at the thread's current quad
-  unsigned kv;                      // bit i: tap i < K
   uint2 raw[NQ];
-  unsigned ok;                      // bit e: row p0 + pq + e valid
   __device__ void init(int t, int n0, int pb) {
     pq = (t & 7) * 4; jr = t >> 3;
-    kv = 0;
     const int r0 = pb + pq;
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int k = n0 + jr + 32 * i;
       const int slot = k < Kpad ? ((k & ~3) | ((k - (r0 >> 2)) & 3)) : 0;
       src[i] = xt + (long long)slot * Rpad + r0;
-      if (k < K) kv |= 1u << i;
     }
   }
-  __device__ void fetch(int p0, int pe) {
-    const int r = p0 + pq;
-    ok = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ok |= (r + e < pe ? 1u : 0u) << e;
+  __device__ void fetch(int, int) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) raw[i] = *(const uint2*)src[i];
   }
-  __device__ void stash(float* s, const float* tab) const {
+  template <bool FULL> __device__ void put(char* s, const uint2* stab) const {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const unsigned w[2] = {raw[i].x, raw[i].y};
-      floatx4 v;
+      unsigned idx[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const unsigned idx = (w[e >> 1] >> (16 * (e & 1) + 8)) & 255u;
-        const float x = tab[idx];
-        v[e] = (((kv >> i) & (ok >> e)) & 1u) ? x : 0.0f;
-      }
-      *(floatx4*)&s[Lay::at(jr + 32 * i, pq)] = v;
+      for (int e = 0; e < 4; ++e) idx[e] = (w[e >> 1] >> (16 * (e & 1) + 8)) & 255u;
+      uint2 P[3];
+      lookup4<FULL>(stab, idx, P);
+      put_parts<B, FULL>(s, jr + 32 * i, pq, P);
     }
   }
   __device__ void advance() {
@@ -525,10 +618,16 @@ struct DataOut {
   long long split_stride;   // elements per partial slice (blockIdx.z = slice)
 };
 // ws[s][o][k] of the backward-weight GEMM.
+// ws[s][o][k] of the backward-weight GEMM, times the go scale sx * sw[o]
+// when sw is given.
 struct WeightOut {
   float* ws; int O, K; long long sst;
+  const float* sx; const float* sw;
   __device__ void store(int m, int c, float v, int s) const {
-    if (m < O && c < K) ws[(long long)s * sst + (long long)m * K + c] = v;
+    if (m < O && c < K) {
+      if (sw) v *= sx[0] * sw[m];
+      ws[(long long)s * sst + (long long)m * K + c] = v;
+    }
   }
 };
 
@@ -595,6 +694,82 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
     x = Bc; Bc = Bn; Bn = x;
   }
   mma_tile<BM, BN, LA, LB, TR>(Ac, Bc, acc);
+}
+
+// acc += A tile x B tile from split-bf16 planes (one 32-deep MFMA step).
+// Lane (i = lane & 15, g = lane >> 4) reads 16 bytes (contraction elements
+// 8g..8g+7) of row i of each 16-row block; the result blocks have the fp32
+// path's layout (lane holds rows 4g + r of column i).  The part products are
+// added smallest first.
+template <int BM, int BN, int PR>
+__device__ __forceinline__ void mma_planes(const char* As, const char* Bs,
+                                           floatx4 (&acc)[BM / 32][BN / 32]) {
+  constexpr int TM = BM / 32, TN = BN / 32;
+  constexpr int NA = PR == A_EXACT ? 1 : 3;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, k8 = 8 * (lane >> 4);
+  // A parts stay in registers; the B parts are read one at a time, each
+  // taking its products with the A parts of total order <= 2 (smallest
+  // first: B part q with A parts 2 - q .. 0).
+  u32x4 a[NA][TM];
+#pragma unroll
+  for (int q = 0; q < NA; ++q)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      a[q][i] = *(const u32x4*)(As + q * Planes<BM>::PLANE +
+                                Planes<BM>::at(wm * (BM / 2) + i * 16 + li, k8));
+  constexpr int NB = PR == B_EXACT ? 1 : 3;
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    u32x4 b[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      b[j] = *(const u32x4*)(Bs + q * Planes<BN>::PLANE +
+                             Planes<BN>::at(wn * (BN / 2) + j * 16 + li, k8));
+#pragma unroll
+    for (int qa = (PR == A_EXACT ? 0 : 2 - q); qa >= 0; --qa)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, a[qa][i]), __builtin_bit_cast(bf16x8, b[j]), acc[i][j],
+              0, 0, 0);
+  }
+}
+
+// acc = sum over the contraction range [pb, pe) on split-bf16 planes.  One
+// LDS tile per operand: the loaders' global loads of k-tile i+1 are in
+// flight while tile i is multiplied, then stored as planes after a barrier
+// (two barriers per k-tile; the kernels run two blocks per CU, so one
+// block's MFMAs cover the other's stores).
+template <int BM, int BN, int PR, class LA, class LB>
+__device__ __forceinline__ void gemm_planes(LA& la, LB& lb, const uint2* stab, int pb, int pe,
+                                            floatx4 (&acc)[BM / 32][BN / 32], char* As,
+                                            char* Bs) {
+#pragma unroll
+  for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+    for (int j = 0; j < BN / 32; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (pb >= pe) return;
+  la.fetch(pb, pe);
+  lb.fetch(pb, pe);
+  for (int p0 = pb;; p0 += BK) {
+    la.template put<PR != A_EXACT>(As, stab);
+    lb.template put<PR != B_EXACT>(Bs, stab);
+    __syncthreads();
+    const bool more = p0 + BK < pe;
+    if (more) {
+      la.advance(); lb.advance();
+      la.fetch(p0 + BK, pe);
+      lb.fetch(p0 + BK, pe);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma_planes<BM, BN, PR>(As, Bs, acc);
+    if (!more) break;
+    __syncthreads();
+  }
 }
 
 // Data-GEMM epilogue: out[n][m][l] for column c = n*L + l (rows m), with the
@@ -738,25 +913,27 @@ __device__ __forceinline__ void set_pad(WeightB<B, T>& lb, const float* pad_dev)
   if (pad_dev) lb.pad = (int)quant_index(pad_dev[0], 0);
 }
 
+// Backward-weight GEMM on split-bf16 planes: A = go (six part products),
+// B = the table (three when every table entry is bf16 exactly).
 template <int BM, int BN, bool VA, class LB>
 __global__ void __launch_bounds__(GT, 2)
-weight_gemm_kernel(WeightA<BM, VA> la, LB lb, WeightOut ep,
-                   const float* __restrict__ tw, const float* __restrict__ pad_dev,
-                   int P, int p_chunk) {
-  __shared__ float tab[256];
-  __shared__ __align__(16) float As[2][PMajor<BM>::SIZE];
-  __shared__ __align__(16) float Bs[2][PMajor<BN>::SIZE];
+weight_gemm_kernel(WeightA<BM, VA> la, LB lb, WeightOut ep, const float* __restrict__ go,
+                   long long go_elems, const float* __restrict__ tw,
+                   const float* __restrict__ pad_dev, int P, int p_chunk) {
+  __shared__ uint2 stab[257];
+  __shared__ __align__(16) char As[Planes<BM>::SIZE];
+  __shared__ __align__(16) char Bs[Planes<BN>::SIZE];
   const int t = threadIdx.x;
-  tab[t] = tw[t];
   set_pad(lb, pad_dev);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int s = blockIdx.z;
   const int pb = s * p_chunk, pe = min(P, pb + p_chunk);
-  la.init(t, m0, pb);
+  la.init(go, go_elems, t, m0, pb);
   lb.init(t, n0, pb);
-  __syncthreads();
+  const bool exact = split_table(stab, tw, t);
   floatx4 acc[BM / 32][BN / 32];
-  gemm_tiles<BM, BN>(la, lb, tab, pb, pe, acc, As[0], As[1], Bs[0], Bs[1]);
+  if (exact) gemm_planes<BM, BN, B_EXACT>(la, lb, stab, pb, pe, acc, As, Bs);
+  else gemm_planes<BM, BN, PROD6>(la, lb, stab, pb, pe, acc, As, Bs);
   const int lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
 #pragma unroll
   for (int i = 0; i < BM / 32; ++i)
@@ -827,12 +1004,11 @@ int launch_split_sum(const float* ws, int S, long long numel, int K,
 inline int tile_of(int extent) { return extent <= 64 ? 64 : 128; }
 
 // Split of the weight-gradient contraction, every split at least four
-// k-tiles deep.  Cost in k-tiles: rounds of 512 blocks (256 CUs x two) x
+// k-tiles deep.  Cost in k-tiles: rounds of 512 blocks (two per CU) x
 // (k-tiles per block + 4 for the block's prologue and epilogue) + 2 + S x
 // O*K / 1.5e6 for writing and summing the S partial slices.  Any S, not just
-// powers of two: on the ResNet-50 weight gradients at batch 64 this fills
-// one round with 13-62 k-tiles per block and is 10-14% faster than filling
-// four rounds (a 2048-block target) with 4-16.
+// powers of two: one round with many k-tiles per block beats several rounds
+// with few (each block's pipeline start and epilogue are paid per round).
 static int weight_splits(int O, int K, long long P) {
   const long long tiles = cdiv(O, tile_of(O)) * cdiv(K, tile_of(K));
   const long long kt = cdiv(P, BK);                 // k-tiles of the contraction
@@ -841,9 +1017,11 @@ static int weight_splits(int O, int K, long long P) {
   long long pick = 1;
   for (long long s = 1; s <= smax; ++s) {
     const long long kc = cdiv(kt, s), sr = cdiv(kt, kc);
+    // each split's rows of go within 1 GiB (32-bit buffer offsets)
+    if ((double)kc * BK * O * 4.0 > (double)(1LL << 30) && s < smax) continue;
     const double cost = (double)cdiv(tiles * sr, 512) * (kc + 4) +
                         (sr > 1 ? 2.0 + (double)sr * O * K / 1.5e6 : 0.0);
-    if (s == 1 || cost < best) { best = cost; pick = sr; }
+    if (best == 0.0 || cost < best) { best = cost; pick = sr; }
   }
   return (int)pick;
 }
@@ -934,13 +1112,13 @@ static void launch_weight(const float* go, const T* img, atx_conv_geom g, int O,
                           const float* pad_dev, const float* tw, const float* go_sx,
                           const float* go_sw, float* ws, hipStream_t stream) {
   WeightA<BM, VA> la{};
-  la.go = go; la.O = O; la.L = L; la.sx = go_sx; la.sw = go_sw;
+  la.O = O; la.L = L;
   WeightB<BN, T> lb{};
   lb.img = img; lb.g = g; lb.K = K; lb.L = L; lb.offset = offset; lb.pad = pad_index;
-  WeightOut ep{ws, O, K, (long long)O * K};
+  WeightOut ep{ws, O, K, (long long)O * K, go_sx, go_sw};
   dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)S);
   hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, WeightB<BN, T>>), grid, dim3(GT), 0,
-                     stream, la, lb, ep, tw, pad_dev, P, chunk);
+                     stream, la, lb, ep, go, (long long)P * O, tw, pad_dev, P, chunk);
 }
 
 template <bool VA, typename T>
@@ -978,13 +1156,14 @@ static void launch_weight_rows(const float* go, const uint16_t* xt, long long Rp
                                const float* go_sx, const float* go_sw, float* ws,
                                hipStream_t stream) {
   WeightA<BM, VA> la{};
-  la.go = go; la.O = O; la.L = L; la.sx = go_sx; la.sw = go_sw;
+  la.O = O; la.L = L;
   WeightBRows<BN> lb{};
   lb.xt = xt; lb.Rpad = Rpad; lb.K = K; lb.Kpad = (K + 3) & ~3;
-  WeightOut ep{ws, O, K, (long long)O * K};
+  WeightOut ep{ws, O, K, (long long)O * K, go_sx, go_sw};
   dim3 grid((unsigned)cdiv(K, BN), (unsigned)cdiv(O, BM), (unsigned)S);
   hipLaunchKernelGGL((weight_gemm_kernel<BM, BN, VA, WeightBRows<BN>>), grid, dim3(GT), 0,
-                     stream, la, lb, ep, tw, (const float*)nullptr, P, chunk);
+                     stream, la, lb, ep, go, (long long)P * O, tw, (const float*)nullptr, P,
+                     chunk);
 }
 
 template <bool VA>
@@ -1160,6 +1339,8 @@ int atx_conv_bwd_weight(const float* go, const void* img, int dtype, atx_conv_ge
   }
   ATX_REQUIRE(go && img && workspace, "atx_conv_bwd_weight: null operand/workspace");
   ATX_REQUIRE(cdiv(O, 64) <= 65535, "atx_conv_bwd_weight: too many output channels");
+  ATX_REQUIRE((long long)O * L < (1LL << 28), "%s: one image's output gradient exceeds 1 GiB",
+              __func__);
   const int S = weight_splits(O, K, P);
   const int chunk = (int)(cdiv(cdiv(P, S), BK) * BK);
   const int Sreal = (int)cdiv(P, chunk);
@@ -1194,6 +1375,8 @@ int atx_conv_bwd_weight_rows(const float* go, const uint16_t* xt, int Rpad, int 
     return launch_split_sum(nullptr, 0, (long long)O * K, K, nullptr, scale_w, gw, stream);
   ATX_REQUIRE(go && xt && workspace, "atx_conv_bwd_weight_rows: null operand/workspace");
   ATX_REQUIRE(cdiv(O, 64) <= 65535, "atx_conv_bwd_weight_rows: too many output channels");
+  ATX_REQUIRE((long long)O * L < (1LL << 28), "%s: one image's output gradient exceeds 1 GiB",
+              __func__);
   const int S = weight_splits(O, K, P);
   const int chunk = (int)(cdiv(cdiv(P, S), BK) * BK);
   const int Sreal = (int)cdiv(P, chunk);
