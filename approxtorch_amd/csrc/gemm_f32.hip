@@ -1,4 +1,4 @@
-// fp32 matrix-core (MFMA) GEMMs for the STE / LRE backward of the LUT conv.
+// Matrix-core (MFMA) GEMMs for the STE / LRE backward of the LUT conv.
 //
 // Both estimators differentiate y[n,o,l] = sum_k f(x_nkl, w_ok) as a dense
 // product of mapped operands (STE: the quantized values, LRE: 256-entry slope
@@ -10,20 +10,23 @@
 // holds).  Reference: csrc/claude/bgemm_lre_backward_claude.cu:443-524 (cuBLAS
 // SGEMMs) and nn/bgemm_int8.py:184-207,277-290 (cuDNN convolution_backward).
 //
-// Kernel: BM x BN block tile (64 or 128 each), 32-deep k-tiles, 256 threads
-// as 2 x 2 waves, each wave (BM/2) x (BN/2) in v_mfma_f32_16x16x4f32 tiles.
-// The 256-entry table lives in LDS.  Operand tiles go HBM -> registers (raw:
-// bytes or floats, 16-byte loads where the operand is contiguous) while the
-// previous tile is multiplied, then through the table into a second LDS
-// buffer; one barrier per k-tile.  The table lookup happens at the LDS store
-// so the global loads of the next tile stay in flight during the MFMAs.
-// LDS tiles are laid out so that the MFMA operand reads (lane = (row
-// lane & 15, k lane >> 4)) are bank-conflict-free:
-//   KMajor [BK][B + 16]  when the operand is contiguous along m in HBM,
-//   PMajor [B][BK + 4]   when it is contiguous along the contraction index.
-// The backward-data GEMM folds the batch into its columns (c = n*L + l), so
-// small images waste no tile width.  gfx950 has no reduced-precision fp32
-// mode: plain fp32 products, fp32 accumulation.
+// Two engines over BM x BN block tiles (64 or 128 each), 32-deep k-tiles and
+// 256 threads as 2 x 2 waves:
+// - split-bf16 (the layer paths): fp32 operands split exactly into three
+//   bf16 parts and multiplied on v_mfma_f32_16x16x32_bf16 as the six part
+//   products of order <= 2 (three when a table is bf16 already); see the
+//   "split-bf16 operand planes" section below.  Backward-weight, the
+//   backward-data GEMM of atx_conv_bwd_data (its A operand from bf16 weight
+//   planes prepared per call) and the implicit backward-data GEMM.
+// - fp32 (v_mfma_f32_16x16x4f32, plain fp32 products): the backward-data
+//   GEMM of atx_conv_bwd_data_col (no workspace for the planes) and layers
+//   whose go spans exceed the split path's 32-bit buffer offsets.  The
+//   256-entry table lives in LDS; operand tiles go HBM -> registers while
+//   the previous tile is multiplied, then through the table into a second
+//   LDS buffer ([BK][B + 16], bank 16k + i: conflict-free MFMA reads); one
+//   barrier per k-tile.
+// The backward-data GEMMs fold the batch into their columns (c = n*L + l),
+// so small images waste no tile width.
 
 #include "atx_internal.h"
 #include "atx_tiles.h"
@@ -37,16 +40,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 32;          // contraction depth of one k-tile
 constexpr int GT = 256;         // threads per block (2 x 2 waves)
-constexpr int LDP = BK + 4;     // floats per row of a PMajor tile
 
 template <int B> struct KMajor {          // [BK][B + 16]: bank(k, i) = 16k + i
   static constexpr int LD = B + 16;
   static constexpr int SIZE = BK * LD;
   __device__ static int at(int m, int k) { return k * LD + m; }
-};
-template <int B> struct PMajor {          // [B][BK + 4]: bank(i, k) = 36i + k
-  static constexpr int SIZE = B * LDP;
-  __device__ static int at(int m, int k) { return m * LDP + k; }
 };
 
 // ------------------------------------------------ split-bf16 operand planes
@@ -121,6 +119,14 @@ __device__ __forceinline__ bool split_table(uint2* stab, const float* tab, int t
   const unsigned lo = __float_as_uint(r - __uint_as_float(ru & 0xffff0000u));
   stab[t] = make_uint2((u >> 16) | (ru & 0xffff0000u), lo >> 16);
   if (t == 0) stab[256] = make_uint2(0u, 0u);
+  return __syncthreads_or(r != 0.0f) == 0;
+}
+
+// Whether every entry of a 256-entry table is bf16 exactly (GT == 256
+// threads; ends with a barrier).
+__device__ __forceinline__ bool table_exact(const float* tab, int t) {
+  const float v = tab[t];
+  const float r = v - __uint_as_float(__float_as_uint(v) & 0xffff0000u);
   return __syncthreads_or(r != 0.0f) == 0;
 }
 
@@ -607,6 +613,184 @@ template <int B> struct WeightBRows {
   }
 };
 
+// ---------------------------------------- backward-data loaders (bf16 planes)
+// Backward-data A from prepared planes [3][Kp][Opad] (the h, m, l parts of
+// tx[wq[o][k]], zero for k >= K and o >= O; Kp, Opad multiples of 128 and
+// 32): A(m = k, p = o).  Row m of a k-tile is 64 contiguous bytes per
+// plane; a thread copies 16-byte units (three planes, or only the h plane
+// when the table is bf16 exactly).  Buffer loads: rows past the planes read
+// 0.  DGRAD: rows m = input channel c of the implicit GEMM, whose k-tile
+// p0 holds tap t = p0 / O (O % 32 == 0): source row c*KK + t, columns from
+// p0 - t*O.
+template <int B, bool DGRAD> struct PlaneA {
+  static constexpr int NU = 3 * B * 4 / GT;   // 16-byte units per thread, three planes
+  const uint16_t* planes; int pbytes;        // the planes and their size
+  __amdgpu_buffer_rsrc_t res;
+  int Kp, Opad, KK, O, m0, t;
+  bool full;
+  u32x4 raw[NU];
+  __device__ void init(int tid, int mbase) {
+    t = tid; m0 = mbase;
+    res = buffer_rsrc(planes, pbytes);
+  }
+  __device__ void fetch(int p0, int) {
+    int tap = 0, o0 = p0;
+    if constexpr (DGRAD) { tap = p0 / O; o0 = p0 - tap * O; }
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      if (j >= NU / 3 && !full) break;
+      const int u = t + GT * j;
+      const int q = u / (4 * B), row = (u >> 2) % B, unit = u & 3;
+      const int src = DGRAD ? (m0 + row) * KK + tap : m0 + row;
+      const unsigned off = (((unsigned)q * Kp + src) * Opad + o0 + 8 * unit) * 2u;
+      raw[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, 0));
+    }
+  }
+  template <bool FULL> __device__ void put(char* s, const uint2*) const {
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      if (j >= NU / 3 && !FULL) break;
+      const int u = t + GT * j;
+      const int q = u / (4 * B), row = (u >> 2) % B, unit = u & 3;
+      *(u32x4*)(s + q * Planes<B>::PLANE + Planes<B>::at(row, 8 * unit)) = raw[j];
+    }
+  }
+  __device__ void advance() {}
+};
+
+// Backward-data B: B(p = o, col = c) = go[n][o][l] * fp32(sx * sw[o]) with
+// c = n*L + l (the product of scales rounded first, the order of the layer's
+// `y * (scale_x * scale_w)`).  A thread holds four columns x four
+// consecutive o (o-quad oq = t & 7, column quad cq = t >> 3) and stores each
+// column's four contraction elements as 8-byte plane groups.  Buffer loads
+// from a descriptor starting at the block's first image: columns past N*L
+// read 0 (offset 2^31, past the descriptor), o >= O reads the next image's
+// values or 0 (the A planes are 0 there).  VEC (L % 4 == 0): a column quad
+// lies in one image, one 16-byte load per o.
+template <int B, bool VEC, bool SCALED> struct GoCols {
+  static_assert(B == 128, "GoCols covers 128 columns with 256 threads");
+  __amdgpu_buffer_rsrc_t res;
+  int O, L;
+  const float* sx; const float* sw;
+  int oq, cq;
+  unsigned off[4];          // byte offset of column 4cq + e at o = 0 (VEC: off[0] only)
+  floatx4 raw[4];           // raw[i][e]: o = p0 + 4oq + i, column 4cq + e
+  float sc[4];
+  __device__ void init(const float* go, long long go_elems, int tid, int n0, int NL) {
+    oq = tid & 7; cq = tid >> 3;
+    const int nb = n0 / L;
+    const long long base = (long long)nb * O * L;
+    const long long bytes = (go_elems - base) * 4;
+    res = buffer_rsrc(go + base, (int)(bytes < 0x7fffffffLL ? bytes : 0x7fffffffLL));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = n0 + 4 * cq + e;
+      const int n = c / L;
+      off[e] = c < NL ? (unsigned)(((long long)(n - nb) * O * L + (c - n * L)) * 4) : 0x80000000u;
+    }
+  }
+  __device__ void fetch(int p0, int) {
+    const int ob = p0 + 4 * oq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned ol = (unsigned)(ob + i) * L * 4u;
+      if constexpr (SCALED) sc[i] = sx[0] * sw[ob + i < O ? ob + i : 0];
+      if constexpr (VEC) {
+        raw[i] = __builtin_bit_cast(floatx4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(res, off[0] + ol, 0, 0));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          raw[i][e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(res, off[e] + ol, 0, 0));
+      }
+    }
+  }
+  template <bool FULL> __device__ void put(char* s, const uint2*) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = SCALED ? raw[i][e] * sc[i] : raw[i][e];
+      uint2 P[3];
+      split4<FULL>(v, P);
+      put_parts<B, FULL>(s, 4 * cq + e, 4 * oq, P);
+    }
+  }
+  __device__ void advance() {}
+};
+
+// Implicit backward-data B: B(p = t*O + o, col = (n, h, w)) =
+// go'[n, o, h + PH - i*DH, w + PW - j*DW] (tap t = i*KW + j, uniform over a
+// k-tile since O % 32 == 0; zero outside go), with GoCols' thread layout
+// and scaling.  Elements outside the image use offset 2^31 (read 0).
+template <int B, bool SCALED> struct ShiftCols {
+  static_assert(B == 128, "ShiftCols covers 128 columns with 256 threads");
+  __amdgpu_buffer_rsrc_t res;
+  atx_conv_geom g; int O;
+  const float* sx; const float* sw;
+  int oq, cq;
+  int nb[4], hh[4], ww[4];  // image offset (elements, from the descriptor base; -1: none), pixel
+  floatx4 raw[4];
+  float sc[4];
+  __device__ void init(const float* go, long long go_elems, int tid, int n0, int NHW) {
+    oq = tid & 7; cq = tid >> 3;
+    const int HW = g.H * g.W;
+    const long long OHW = (long long)g.OH * g.OW;
+    const int nbase = n0 / HW;
+    const long long base = (long long)nbase * O * OHW;
+    const long long bytes = (go_elems - base) * 4;
+    res = buffer_rsrc(go + base, (int)(bytes < 0x7fffffffLL ? bytes : 0x7fffffffLL));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = n0 + 4 * cq + e;
+      if (c < NHW) {
+        const int n = c / HW, hw = c - n * HW;
+        hh[e] = hw / g.W;
+        ww[e] = hw - hh[e] * g.W;
+        nb[e] = (int)((n - nbase) * O * OHW);
+      } else {
+        nb[e] = -1; hh[e] = ww[e] = 0;
+      }
+    }
+  }
+  __device__ void fetch(int p0, int) {
+    const int tap = p0 / O, o0 = p0 - tap * O;
+    const int ki = tap / g.KW, kj = tap - ki * g.KW;
+    const int dh0 = g.PH - ki * g.DH, dw0 = g.PW - kj * g.DW;
+    const int OHW = g.OH * g.OW;
+    unsigned off[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ih = hh[e] + dh0, iw = ww[e] + dw0;
+      const bool v = nb[e] >= 0 && (unsigned)ih < (unsigned)g.OH && (unsigned)iw < (unsigned)g.OW;
+      off[e] = v ? (unsigned)(nb[e] + ih * g.OW + iw) * 4u : 0x80000000u;
+    }
+    const int ob = o0 + 4 * oq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned ol = (unsigned)(ob + i) * OHW * 4u;
+      if constexpr (SCALED) sc[i] = sx[0] * sw[ob + i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        raw[i][e] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(res, off[e] + ol, 0, 0));
+    }
+  }
+  template <bool FULL> __device__ void put(char* s, const uint2*) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = SCALED ? raw[i][e] * sc[i] : raw[i][e];
+      uint2 P[3];
+      split4<FULL>(v, P);
+      put_parts<B, FULL>(s, 4 * cq + e, 4 * oq, P);
+    }
+  }
+  __device__ void advance() {}
+};
+
 // ------------------------------------------------------------------ epilogues
 // out[n][k][l] of the backward-data GEMM (rows m = k, columns c = n*L + l).
 // With `mask`, the fake-quant STE is applied on the way out:
@@ -617,7 +801,6 @@ struct DataOut {
   const uint8_t* mask; const float* scale;
   long long split_stride;   // elements per partial slice (blockIdx.z = slice)
 };
-// ws[s][o][k] of the backward-weight GEMM.
 // ws[s][o][k] of the backward-weight GEMM, times the go scale sx * sw[o]
 // when sw is given.
 struct WeightOut {
@@ -701,7 +884,10 @@ __device__ __forceinline__ void gemm_tiles(LA& la, LB& lb, const float* tab, int
 // 8g..8g+7) of row i of each 16-row block; the result blocks have the fp32
 // path's layout (lane holds rows 4g + r of column i).  The part products are
 // added smallest first.
-template <int BM, int BN, int PR>
+// TR: the B fragment is the MFMA's first operand, so each 16x16 result block
+// comes out transposed (lane holds columns 4*(lane >> 4) + r of row
+// lane & 15), the layout of the data epilogue's vector path.
+template <int BM, int BN, int PR, bool TR = false>
 __device__ __forceinline__ void mma_planes(const char* As, const char* Bs,
                                            floatx4 (&acc)[BM / 32][BN / 32]) {
   constexpr int TM = BM / 32, TN = BN / 32;
@@ -733,9 +919,12 @@ __device__ __forceinline__ void mma_planes(const char* As, const char* Bs,
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, a[qa][i]), __builtin_bit_cast(bf16x8, b[j]), acc[i][j],
-              0, 0, 0);
+          acc[i][j] = TR ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                               __builtin_bit_cast(bf16x8, b[j]), __builtin_bit_cast(bf16x8, a[qa][i]),
+                               acc[i][j], 0, 0, 0)
+                         : __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                               __builtin_bit_cast(bf16x8, a[qa][i]), __builtin_bit_cast(bf16x8, b[j]),
+                               acc[i][j], 0, 0, 0);
   }
 }
 
@@ -744,7 +933,7 @@ __device__ __forceinline__ void mma_planes(const char* As, const char* Bs,
 // flight while tile i is multiplied, then stored as planes after a barrier
 // (two barriers per k-tile; the kernels run two blocks per CU, so one
 // block's MFMAs cover the other's stores).
-template <int BM, int BN, int PR, class LA, class LB>
+template <int BM, int BN, int PR, bool TR = false, class LA, class LB>
 __device__ __forceinline__ void gemm_planes(LA& la, LB& lb, const uint2* stab, int pb, int pe,
                                             floatx4 (&acc)[BM / 32][BN / 32], char* As,
                                             char* Bs) {
@@ -766,7 +955,7 @@ __device__ __forceinline__ void gemm_planes(LA& la, LB& lb, const uint2* stab, i
       lb.fetch(p0 + BK, pe);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mma_planes<BM, BN, PR>(As, Bs, acc);
+    mma_planes<BM, BN, PR, TR>(As, Bs, acc);
     if (!more) break;
     __syncthreads();
   }
@@ -907,6 +1096,82 @@ dgrad_gemm_kernel(DgradA<BM> la, DgradB<BN, SC> lb, DataOut ep, const float* __r
   data_epilogue<BM, BN, VO>(ep, acc, m0, n0);
 }
 
+// planes[q][k][o] (q = h, m, l part of tx[wq[o*K + k]]; zero for k >= K or
+// o >= O) over Kp x Opad, the A operand of the plane data GEMMs.  A thread
+// writes eight consecutive o of one k per plane (16 bytes).
+__global__ void __launch_bounds__(GT)
+weight_planes_kernel(const uint8_t* __restrict__ wq, const float* __restrict__ tx, int O, int K,
+                     int Kp, int Opad, uint16_t* __restrict__ planes) {
+  __shared__ uint2 stab[257];
+  split_table(stab, tx, threadIdx.x);
+  const long long idx = (long long)blockIdx.x * GT + threadIdx.x;
+  const int per_row = Opad / 8;
+  if (idx >= (long long)Kp * per_row) return;
+  const int k = (int)(idx / per_row), o8 = (int)(idx - (long long)k * per_row) * 8;
+  uint2 P[2][3];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    unsigned ix[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int o = o8 + 4 * h + e;
+      ix[e] = k < K && o < O ? wq[(long long)o * K + k] : 256u;
+    }
+    lookup4<true>(stab, ix, P[h]);
+  }
+  const long long plane = (long long)Kp * Opad;
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+    *(uint4*)(planes + q * plane + (long long)k * Opad + o8) =
+        make_uint4(P[0][q].x, P[0][q].y, P[1][q].x, P[1][q].y);
+}
+
+// Backward-data GEMM on split-bf16 planes: A from weight_planes_kernel's
+// planes (three parts, or one when the table is bf16 exactly), B = go (six
+// part products, or three).  VB (L % 4 == 0): 16-byte go loads and the
+// transposed epilogue.  Two blocks per CU.
+template <int BM, bool VB, bool SC>
+__global__ void __launch_bounds__(GT, 2)
+data_planes_kernel(PlaneA<BM, false> la, GoCols<128, VB, SC> lb, DataOut ep,
+                   const float* __restrict__ go, long long go_elems,
+                   const float* __restrict__ tx, int O, int o_chunk) {
+  __shared__ __align__(16) char As[Planes<BM>::SIZE];
+  __shared__ __align__(16) char Bs[Planes<128>::SIZE];
+  const int t = threadIdx.x;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * 128;
+  la.init(t, m0);
+  lb.init(go, go_elems, t, n0, ep.NL);
+  const bool exact = table_exact(tx, t);
+  la.full = !exact;
+  const int ob = blockIdx.z * o_chunk, oe = min(O, ob + o_chunk);
+  ep.col += (long long)blockIdx.z * ep.split_stride;
+  floatx4 acc[BM / 32][4];
+  if (exact) gemm_planes<BM, 128, A_EXACT, VB>(la, lb, nullptr, ob, oe, acc, As, Bs);
+  else gemm_planes<BM, 128, PROD6, VB>(la, lb, nullptr, ob, oe, acc, As, Bs);
+  data_epilogue<BM, 128, VB>(ep, acc, m0, n0);
+}
+
+// Implicit backward-data GEMM on split-bf16 planes (A rows c*KK + t of the
+// prepared planes, B = shifted go).  VO: 16-byte output stores.
+template <int BM, bool SC, bool VO>
+__global__ void __launch_bounds__(GT, 2)
+dgrad_planes_kernel(PlaneA<BM, true> la, ShiftCols<128, SC> lb, DataOut ep,
+                    const float* __restrict__ go, long long go_elems,
+                    const float* __restrict__ tx, int P) {
+  __shared__ __align__(16) char As[Planes<BM>::SIZE];
+  __shared__ __align__(16) char Bs[Planes<128>::SIZE];
+  const int t = threadIdx.x;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * 128;
+  la.init(t, m0);
+  lb.init(go, go_elems, t, n0, ep.NL);
+  const bool exact = table_exact(tx, t);
+  la.full = !exact;
+  floatx4 acc[BM / 32][4];
+  if (exact) gemm_planes<BM, 128, A_EXACT, VO>(la, lb, nullptr, 0, P, acc, As, Bs);
+  else gemm_planes<BM, 128, PROD6, VO>(la, lb, nullptr, 0, P, acc, As, Bs);
+  data_epilogue<BM, 128, VO>(ep, acc, m0, n0);
+}
+
 template <class LB> __device__ __forceinline__ void set_pad(LB&, const float*) {}
 template <int B, typename T>
 __device__ __forceinline__ void set_pad(WeightB<B, T>& lb, const float* pad_dev) {
@@ -1032,7 +1297,29 @@ struct DataArgs {
   float* out; const uint8_t* mask; const float* scale;
   int splits, o_chunk;                       // contraction split (1 = none)
   float* partials;                           // [splits][N*K*L] when splits > 1
+  uint16_t* planes;                          // bf16 weight planes (null: fp32 kernels)
 };
+
+// Bytes of the bf16 weight planes [3][Kp][Opad] (Kp = K rounded up to 128,
+// Opad = O rounded up to 32; a multiple of 256 bytes).
+static long long weight_planes_bytes(int K, int O) {
+  return 3LL * cdiv(K, 128) * 128 * cdiv(O, BK) * BK * 2;
+}
+
+// go spans of at most 2^31 bytes per block (32-bit buffer offsets): the
+// images a block's 128 columns touch, two partial images included.
+static bool planes_fit(long long cols_per_image, int O, long long out_per_image) {
+  return (cdiv(128, cols_per_image) + 2) * (long long)O * out_per_image * 4 < (1LL << 31);
+}
+
+static int launch_weight_planes(const uint8_t* wq, const float* tx, int O, int K,
+                                uint16_t* planes, hipStream_t stream) {
+  const int Kp = (int)(cdiv(K, 128) * 128), Opad = (int)(cdiv(O, BK) * BK);
+  const long long items = (long long)Kp * (Opad / 8);
+  hipLaunchKernelGGL(weight_planes_kernel, dim3((unsigned)cdiv(items, GT)), dim3(GT), 0, stream,
+                     wq, tx, O, K, Kp, Opad, planes);
+  return check_launch("weight_planes_kernel");
+}
 
 // Split of the backward-data contraction over O into deterministic partial
 // slices, each at least four k-tiles deep.  Cost in k-tiles, as for the
@@ -1073,12 +1360,33 @@ static void launch_data(const DataArgs& a, hipStream_t stream) {
                      ep, a.tx, a.O, a.o_chunk);
 }
 
+template <int BM, bool VB, bool SC>
+static void launch_data_planes(const DataArgs& a, hipStream_t stream) {
+  const int NL = a.N * a.L;
+  PlaneA<BM, false> la{};
+  la.planes = a.planes; la.pbytes = (int)weight_planes_bytes(a.K, a.O);
+  la.Kp = (int)(cdiv(a.K, 128) * 128); la.Opad = (int)(cdiv(a.O, BK) * BK);
+  GoCols<128, VB, SC> lb{};
+  lb.O = a.O; lb.L = a.L; lb.sx = a.sx; lb.sw = a.sw;
+  const bool split = a.splits > 1;
+  DataOut ep{split ? a.partials : a.out, a.K, a.L, NL, split ? nullptr : a.mask,
+             split ? nullptr : a.scale, (long long)NL * a.K};
+  dim3 grid((unsigned)cdiv(NL, 128), (unsigned)cdiv(a.K, BM), (unsigned)a.splits);
+  hipLaunchKernelGGL((data_planes_kernel<BM, VB, SC>), grid, dim3(GT), 0, stream, la, lb, ep,
+                     a.go, (long long)a.N * a.O * a.L, a.tx, a.O, a.o_chunk);
+}
+
 template <int BM, bool SC>
 static void dispatch_data_vec(const DataArgs& a, hipStream_t stream) {
   const bool va = a.K % 4 == 0 && (uintptr_t)a.wq % 4 == 0;
   const float* out = a.splits > 1 ? a.partials : a.out;
   const bool vb = a.L % 4 == 0 && (uintptr_t)a.go % 16 == 0 && (uintptr_t)out % 16 == 0 &&
                   (a.splits > 1 || (uintptr_t)a.mask % 4 == 0);
+  if (a.planes) {
+    if (vb) launch_data_planes<BM, true, SC>(a, stream);
+    else launch_data_planes<BM, false, SC>(a, stream);
+    return;
+  }
   if (va && vb) launch_data<BM, true, true, SC>(a, stream);
   else if (va) launch_data<BM, true, false, SC>(a, stream);
   else if (vb) launch_data<BM, false, true, SC>(a, stream);
@@ -1092,6 +1400,11 @@ static int run_data_gemm(DataArgs a, hipStream_t stream) {
   if (a.splits < 1) a.splits = 1;
   a.o_chunk = (int)(cdiv(cdiv(a.O, a.splits), BK) * BK);
   a.splits = (int)cdiv(a.O, a.o_chunk);
+  if (a.planes && !planes_fit(a.L, a.O, a.L)) a.planes = nullptr;
+  if (a.planes) {
+    const int rc = launch_weight_planes(a.wq, a.tx, a.O, a.K, a.planes, stream);
+    if (rc) return rc;
+  }
   const bool sc = a.sw != nullptr;
   if (tile_of(a.K) == 64) {
     if (sc) dispatch_data_vec<64, true>(a, stream); else dispatch_data_vec<64, false>(a, stream);
@@ -1184,17 +1497,37 @@ static void dispatch_weight_rows(const float* go, const uint16_t* xt, long long 
 template <int BM, bool SC>
 static int launch_dgrad(const float* go, const uint8_t* wq, const float* tx,
                         const atx_conv_geom& g, int O, const float* sx, const float* sw,
-                        const uint8_t* mask, const float* scale, float* gx,
+                        const uint8_t* mask, const float* scale, float* gx, uint16_t* planes,
                         hipStream_t stream) {
   constexpr int BN = 128;
   const int KK = g.KH * g.KW, K = g.C * KK, HW = g.H * g.W, NHW = g.N * HW;
+  const bool vo = HW % 4 == 0 && (uintptr_t)gx % 16 == 0 && (uintptr_t)mask % 4 == 0;
+  if (planes && planes_fit(HW, O, (long long)g.OH * g.OW)) {
+    int rc = launch_weight_planes(wq, tx, O, K, planes, stream);
+    if (rc) return rc;
+    PlaneA<BM, true> la{};
+    la.planes = planes; la.pbytes = (int)weight_planes_bytes(K, O);
+    la.Kp = (int)(cdiv(K, 128) * 128); la.Opad = O; la.KK = KK; la.O = O;
+    ShiftCols<BN, SC> lb{};
+    lb.g = g; lb.O = O; lb.sx = sx; lb.sw = sw;
+    DataOut ep{gx, g.C, HW, NHW, mask, scale, 0};
+    dim3 grid((unsigned)cdiv(NHW, BN), (unsigned)cdiv(g.C, BM), 1);
+    const long long go_elems = (long long)g.N * O * g.OH * g.OW;
+    if (vo)
+      hipLaunchKernelGGL((dgrad_planes_kernel<BM, SC, true>), grid, dim3(GT), 0, stream, la, lb,
+                         ep, go, go_elems, tx, KK * O);
+    else
+      hipLaunchKernelGGL((dgrad_planes_kernel<BM, SC, false>), grid, dim3(GT), 0, stream, la,
+                         lb, ep, go, go_elems, tx, KK * O);
+    return check_launch("dgrad_planes_kernel");
+  }
   DgradA<BM> la{};
   la.wq = wq; la.K = K; la.KK = KK; la.C = g.C; la.O = O;
   DgradB<BN, SC> lb{};
   lb.go = go; lb.g = g; lb.O = O; lb.NHW = NHW; lb.sx = sx; lb.sw = sw;
   DataOut ep{gx, g.C, HW, NHW, mask, scale, 0};
   dim3 grid((unsigned)cdiv(NHW, BN), (unsigned)cdiv(g.C, BM), 1);
-  if (HW % 4 == 0 && (uintptr_t)gx % 16 == 0 && (uintptr_t)mask % 4 == 0)
+  if (vo)
     hipLaunchKernelGGL((dgrad_gemm_kernel<BM, BN, SC, true>), grid, dim3(GT), 0, stream, la, lb,
                        ep, tx, KK * O);
   else
@@ -1237,8 +1570,9 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx, i
   ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data_col: null pointer");
   ATX_REQUIRE((long long)N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
               "atx_conv_bwd_data_col: sizes too large");
+  // no workspace here: the fp32 kernels (table lookups in the loaders)
   const DataArgs a{go, wq, tx, N, O, K, L, nullptr, nullptr, col, nullptr, nullptr, 1, 0,
-                   nullptr};
+                   nullptr, nullptr};
   return run_data_gemm(a, stream);
 }
 
@@ -1247,13 +1581,16 @@ static bool direct_columns(const atx_conv_geom& g) {
   return g.KH == 1 && g.KW == 1 && g.SH == 1 && g.SW == 1 && g.PH == 0 && g.PW == 0;
 }
 
-// Workspace of atx_conv_bwd_data: [split partials][col (unless direct)].
+// Workspace of atx_conv_bwd_data: [bf16 weight planes][split partials][col
+// (unless direct or implicit)].
 long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g, int O) {
   const int K = g.C * g.KH * g.KW, L = g.OH * g.OW;
-  if (g.N <= 0 || K <= 0 || L <= 0 || O <= 0 || implicit_dgrad(g, O)) return 0;
+  if (g.N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
+  const long long planes = weight_planes_bytes(K, O);
+  if (implicit_dgrad(g, O)) return planes;
   const long long numel = (long long)g.N * K * L;
   const int S = data_splits(g.N, O, K, L);
-  return ((S > 1 ? S : 0) + (direct_columns(g) ? 0 : 1)) * numel * 4;
+  return planes + ((S > 1 ? S : 0) + (direct_columns(g) ? 0 : 1)) * numel * 4;
 }
 
 int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_conv_geom g,
@@ -1269,31 +1606,40 @@ int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_c
   ATX_REQUIRE(gx, "atx_conv_bwd_data: null output");
   const int K = g.C * g.KH * g.KW;
   const int L = g.OH * g.OW;
+  // the bf16 weight planes lead the workspace (absent when O, K or L is 0)
+  uint16_t* planes = nullptr;
+  float* rest = workspace;
+  if (O > 0 && K > 0 && L > 0) {
+    ATX_REQUIRE(workspace, "atx_conv_bwd_data: null workspace");
+    planes = (uint16_t*)workspace;
+    rest = (float*)((char*)workspace + weight_planes_bytes(K, O));
+  }
   if (L > 0 && implicit_dgrad(g, O)) {
     ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
     ATX_REQUIRE(cdiv(g.C, 64) <= 65535, "atx_conv_bwd_data: too many channels");
     const bool sc = go_sw != nullptr;
-    if (tile_of(g.C) == 64)
-      return sc ? launch_dgrad<64, true>(go, wq, tx, g, O, go_sx, go_sw, mask, scale, gx, stream)
-                : launch_dgrad<64, false>(go, wq, tx, g, O, go_sx, go_sw, mask, scale, gx, stream);
-    return sc ? launch_dgrad<128, true>(go, wq, tx, g, O, go_sx, go_sw, mask, scale, gx, stream)
-              : launch_dgrad<128, false>(go, wq, tx, g, O, go_sx, go_sw, mask, scale, gx, stream);
+#define ATX_LD(M_, S_) \
+  launch_dgrad<M_, S_>(go, wq, tx, g, O, go_sx, go_sw, mask, scale, gx, planes, stream)
+    if (tile_of(g.C) == 64) return sc ? ATX_LD(64, true) : ATX_LD(64, false);
+    return sc ? ATX_LD(128, true) : ATX_LD(128, false);
+#undef ATX_LD
   }
   const long long numel = (long long)g.N * K * L;
   const int S = (O > 0 && numel > 0) ? data_splits(g.N, O, K, L) : 1;
-  float* partials = S > 1 ? workspace : nullptr;
-  float* col = workspace ? workspace + (S > 1 ? S * numel : 0) : nullptr;
-  ATX_REQUIRE(S == 1 || workspace, "atx_conv_bwd_data: null workspace");
+  float* partials = S > 1 ? rest : nullptr;
+  float* col = rest ? rest + (S > 1 ? S * numel : 0) : nullptr;
+  ATX_REQUIRE(S == 1 || rest, "atx_conv_bwd_data: null workspace");
   if (direct_columns(g)) {
     if (O == 0 || L == 0)
       return launch_split_sum(nullptr, 0, img, 1, nullptr, nullptr, gx, stream);
     ATX_REQUIRE(go && wq && tx, "atx_conv_bwd_data: null pointer");
     ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
                 "atx_conv_bwd_data: sizes too large");
-    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, gx, mask, scale, S, 0, partials};
+    const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, gx, mask, scale, S, 0, partials,
+                     planes};
     return run_data_gemm(a, stream);
   }
-  ATX_REQUIRE(workspace, "atx_conv_bwd_data: null workspace");
+  ATX_REQUIRE(rest, "atx_conv_bwd_data: null workspace");
   if ((long long)K * L == 0 || O == 0) {
     if (numel) {
       int rc = launch_split_sum(nullptr, 0, numel, 1, nullptr, nullptr, col, stream);
@@ -1304,7 +1650,7 @@ int atx_conv_bwd_data(const float* go, const uint8_t* wq, const float* tx, atx_c
     ATX_REQUIRE((long long)g.N * L < 0x7fffffffLL && cdiv(K, 64) <= 65535,
                 "atx_conv_bwd_data: sizes too large");
     const DataArgs a{go, wq, tx, g.N, O, K, L, go_sx, go_sw, col, nullptr, nullptr, S, 0,
-                     partials};
+                     partials, planes};
     int rc = run_data_gemm(a, stream);
     if (rc) return rc;
   }

@@ -344,7 +344,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": f"int32 LUT sums ({cfg['qtype']} operands), fp32 backward",
+        "dtype": f"int32 LUT sums ({cfg['qtype']} operands), fp32 backward "
+                 "(split-bf16 matrix-core products)",
         "data": "synthetic (seeded N(0,1) images, uniform labels, random-init weights)",
         "config": {"workload": f"{name}: {cfg['model']} batch {cfg['batch']} "
                                f"{cfg['hw']}x{cfg['hw']} {cfg['qtype']} grad={cfg['grad']} "

@@ -912,11 +912,13 @@ def test_conv_backward_kernels_tiled(case):
     (GEOMS[0], (2, 8, 128, 256), 32), (((3, 3), (1, 1), (2, 2), (2, 2)), (1, 8, 256, 257), 96),
     (((3, 1), (1, 1), (1, 0), (1, 1)), (1, 130, 256, 129), 32),
     (((5, 5), (1, 1), (0, 0), (1, 1)), (4, 4, 132, 131), 64)])
-def test_conv_backward_fused_scale_and_masks(geom, shape, Oc):
+@pytest.mark.parametrize("exact", [False, True])
+def test_conv_backward_fused_scale_and_masks(geom, shape, Oc, exact):
     """The fused layer backward: go * fp32(sx * sw[o]) in the operand loads,
     the x fake-quant STE (mask ? g : 0) / max(sx, 1e-12) on the image gradient
     (fold, or the GEMM epilogue of the 1x1 stride-1 conv), the per-channel W
-    STE in the split-K sum."""
+    STE in the split-K sum.  exact: integer-valued tables (the STE's), whose
+    bf16 split has only its high part (three part products per product)."""
     k, s, p, d = geom
     r = gen(zlib.crc32(repr((geom, shape, Oc)).encode()) + 7)
     img = r.integers(-127, 128, shape).astype(np.int8)
@@ -924,8 +926,12 @@ def test_conv_backward_fused_scale_and_masks(geom, shape, Oc):
     wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
     g = ops.conv_geom(img.shape, k, s, p, d)
     go = r.standard_normal((shape[0], Oc, g.OH * g.OW)).astype(np.float32)
-    tx = r.standard_normal(256).astype(np.float32)
-    tw = r.standard_normal(256).astype(np.float32)
+    if exact:
+        tx = (np.arange(256) - 128).astype(np.float32)
+        tw = r.permutation(tx)
+    else:
+        tx = r.standard_normal(256).astype(np.float32)
+        tw = r.standard_normal(256).astype(np.float32)
     sx = np.array([0.0213], np.float32)
     sw = r.uniform(1e-3, 4e-2, Oc).astype(np.float32)
     mask_x = r.random(img.shape) < 0.9
