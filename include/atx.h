@@ -350,10 +350,13 @@ int atx_conv_bwd_data_col(const float* go, const uint8_t* wq, const float* tx,
  * gx = (mask ? g : 0) / max(scale[0], 1e-12).  A 1x1 stride-1 unpadded conv
  * writes gx straight from the GEMM, and so does a stride-1 conv with
  * O % 32 == 0 whose C x N*H*W output fills >= 512 tiles (implicit GEMM over
- * (tap, o), workspace size 0); otherwise the workspace holds col.  When
- * the output tiles cannot fill the GPU the contraction over O is split into
- * partial slices (in the workspace) summed in a fixed order.  Size:
- * atx_conv_bwd_data_workspace_bytes(g, O).  Replaces the same calls
+ * (tap, o)); otherwise the workspace holds col.  When the output tiles
+ * cannot fill the GPU the contraction over O is split into partial slices
+ * (in the workspace) summed in a fixed order.  The workspace also holds the
+ * tx[wq] values as bf16 parts for the matrix cores (the products are the
+ * fp32 products to within 2^-20 relative; exact when tx holds bf16 values,
+ * as the STE's integers do).  Size: atx_conv_bwd_data_workspace_bytes(g, O),
+ * nonzero whenever O, K and L are.  Replaces the same calls
  * plus the fold and the fake-quant backward (nn/bgemm_int8.py:116-118,
  * csrc/claude/quantization.cu:223-258). */
 long long atx_conv_bwd_data_workspace_bytes(atx_conv_geom g, int O);
