@@ -160,6 +160,127 @@ __global__ void __launch_bounds__(512) valu_probe_kernel(int iters, unsigned* ou
   out[blockIdx.x * blockDim.x + threadIdx.x] = t;
 }
 
+
+// ----------------------------------------------------------- inner-loop probe
+// The LUT GEMM's main loop with its global loads taken out: 512 threads as 8
+// waves (one workgroup per CU: 128 KiB of LDS), 128 int32 accumulators per
+// lane, lane (row group rg = lane / 4, chunk g = lane % 4) reading its 16
+// rows' 16-byte table chunks at row offset ^ (g*16 | quarter*64 |
+// buffer*65536) with the quarter rotated per sub-step, and adding each chunk
+// as the kernel does (one 32-bit add of the whole dword, one SDWA add of its
+// high half).  The rows are pseudo-random per row group (the four lanes of a
+// group share them, as in the kernel) and fixed over the run.  MODE bits:
+// 1 LDS reads, 2 adds, 4 the table-build writes (two 16-byte stores per lane
+// per sub-step, the kernel's pattern), 8 a barrier every four sub-steps.
+// Without reads the adds take opaque register values; without adds the reads
+// are consumed by empty asm.  A sub-step is 128 lookups per lane.
+namespace inner {
+constexpr int RPL = 16, NQ = 4, LINE = 256, QTAB = 65536;
+
+template <int S, int B>
+__device__ __forceinline__ unsigned quarter_mask(unsigned base) {
+  unsigned t;
+  asm volatile("v_add_u32 %0, %1, %2\n\tv_and_b32 %0, %3, %0\n\tv_or_b32 %0, %4, %0"
+               : "=&v"(t) : "n"(S << 6), "v"(base), "n"(0xf0), "n"(B << 16));
+  return t;
+}
+
+__device__ __forceinline__ void add8(int (&a)[8], const uint4 e) {
+  const unsigned d[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[2 * i] = (int)((unsigned)a[2 * i] + d[i]);
+    a[2 * i + 1] += ((int)d[i]) >> 16;
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void sub(int (&acc)[RPL][8], unsigned char* smem,
+                                    const unsigned (&xd)[8], unsigned gx, int wb, uint4 wv,
+                                    uint4 (&fk)[8]) {
+#pragma unroll
+  for (int hh = 0; hh < NQ; hh += 2) {
+    uint4 e[8];
+    if constexpr (MODE & 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned x = xd[hh * 2 + j];
+        e[2 * j] = *(const uint4*)(smem + ((x & 0xffffu) ^ gx));
+        e[2 * j + 1] = *(const uint4*)(smem + ((x >> 16) ^ gx));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        asm volatile("" : "+v"(fk[j].x), "+v"(fk[j].y), "+v"(fk[j].z), "+v"(fk[j].w));
+        e[j] = fk[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (MODE & 2) add8(acc[4 * hh + j], e[j]);
+      else asm volatile("" :: "v"(e[j].x), "v"(e[j].y), "v"(e[j].z), "v"(e[j].w));
+    }
+  }
+  if constexpr (MODE & 2) {
+#pragma unroll
+    for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
+  }
+  if constexpr (MODE & 4) {
+    *(uint4*)(smem + wb) = wv;
+    *(uint4*)(smem + wb + LINE) = wv;
+  }
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(512, 1) inner_probe_kernel(int iters, unsigned* out) {
+  __shared__ __align__(16) unsigned char smem[2 * QTAB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = lane / 4, g = lane % 4;
+  for (int i = tid; i < 2 * QTAB / 4; i += 512) ((unsigned*)smem)[i] = i * 2654435761u;
+  __syncthreads();
+  unsigned xd[8];
+  const unsigned grp = blockIdx.x * 128u + (unsigned)(tid >> 2);   // row group
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned r0 = mix(grp * 977u + 2u * i) & 255u, r1 = mix(grp * 977u + 2u * i + 1u) & 255u;
+    const unsigned o0 = r0 * 256 + ((r0 >> 1) & 3) * 16, o1 = r1 * 256 + ((r1 >> 1) & 3) * 16;
+    xd[i] = o0 | (o1 << 16);
+  }
+  const unsigned gbase = (unsigned)((rg << 6) | (g << 4));
+  const int og = wave % 4, hw = wave / 4;
+  const int wb0 = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
+  int acc[RPL][8];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0;
+  uint4 wv = make_uint4(tid, tid + 1, tid + 2, tid + 3);
+  uint4 fk[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) fk[j] = make_uint4(xd[j], xd[j] + 1, xd[j] * 3, xd[j] ^ 5);
+  for (int it = 0; it < iters; ++it) {      // eight sub-steps (two quads) per iteration
+    sub<MODE>(acc, smem, xd, quarter_mask<0, 0>(gbase), wb0 + QTAB, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<1, 0>(gbase), wb0 + QTAB + 64, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<2, 0>(gbase), wb0 + QTAB + 128, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<3, 0>(gbase), wb0 + QTAB + 192, wv, fk);
+    if constexpr (MODE & 8) __syncthreads();
+    sub<MODE>(acc, smem, xd, quarter_mask<0, 1>(gbase), wb0, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<1, 1>(gbase), wb0 + 64, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<2, 1>(gbase), wb0 + 128, wv, fk);
+    sub<MODE>(acc, smem, xd, quarter_mask<3, 1>(gbase), wb0 + 192, wv, fk);
+    if constexpr (MODE & 8) __syncthreads();
+    wv.x += 1;
+  }
+  int t = 0;
+#pragma unroll
+  for (int j = 0; j < RPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t += acc[j][e];
+  out[blockIdx.x * 512 + tid] = (unsigned)t;
+}
+}  // namespace inner
 }  // namespace atx_diag
 
 using namespace atx_diag;
@@ -198,6 +319,21 @@ int atx_valu_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t s
     case 8: hipLaunchKernelGGL(valu_probe_kernel<8>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     case 9: hipLaunchKernelGGL(valu_probe_kernel<9>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
     default: hipLaunchKernelGGL(valu_probe_kernel<10>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+  }
+  return (int)hipGetLastError();
+}
+
+int atx_inner_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream) {
+  if (!(blocks > 0 && iters > 0 && out)) return (int)hipErrorInvalidValue;
+  switch (mode) {
+    case 1: hipLaunchKernelGGL(inner::inner_probe_kernel<1>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 2: hipLaunchKernelGGL(inner::inner_probe_kernel<2>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 3: hipLaunchKernelGGL(inner::inner_probe_kernel<3>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 4: hipLaunchKernelGGL(inner::inner_probe_kernel<4>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 7: hipLaunchKernelGGL(inner::inner_probe_kernel<7>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 11: hipLaunchKernelGGL(inner::inner_probe_kernel<11>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    case 15: hipLaunchKernelGGL(inner::inner_probe_kernel<15>, dim3(blocks), dim3(512), 0, stream, iters, out); break;
+    default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();
 }

@@ -66,8 +66,9 @@ def parse():
 
 
 def lds_probe(torch):
-    """Measured LDS throughput per access pattern (GB/s over the whole GPU)
-    and the int32 VALU add rate (G adds/s), from libatx_diag.so."""
+    """Measured LDS throughput per access pattern (GB/s over the whole GPU),
+    VALU issue rates (G lane-ops/s) and the LUT GEMM's main loop without
+    global loads (G lookups/s), from libatx_diag.so."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(ROOT, "approxtorch_amd", "libatx_diag.so"))
     vp, ci = ctypes.c_void_p, ctypes.c_int
@@ -110,6 +111,16 @@ def lds_probe(torch):
                        (10, "v_ashrrev_i32")):
         ms = timed(lambda it: lib.atx_valu_probe(mode, blocks, it, out.data_ptr(), stream))
         res[f"valu_{name}_G_lane_ops_per_s"] = round(blocks * 512 * iters * 64 / (ms * 1e-3) / 1e9, 1)
+    # the LUT GEMM's main loop without global loads, one workgroup per CU
+    lib.atx_inner_probe.argtypes = [ci, ci, ci, vp, vp]
+    iblocks, iiters = 256, 1000
+    for mode, name in ((1, "reads"), (2, "adds"), (3, "reads_adds"), (4, "writes"),
+                       (7, "reads_adds_writes"), (11, "reads_adds_barrier"),
+                       (15, "reads_adds_writes_barrier")):
+        ms = timed(lambda it: lib.atx_inner_probe(mode, iblocks, max(1, it * iiters // iters),
+                                                  out.data_ptr(), stream))
+        res[f"lut_inner_loop_{name}_G_lookups_per_s"] = round(
+            iblocks * 512 * iiters * 8 * 128 / (ms * 1e-3) / 1e9, 1)
     return res
 
 

@@ -45,6 +45,15 @@ int atx_lds_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t st
  * blocks*512 uint32. */
 int atx_valu_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream);
 
+/* The LUT GEMM's main loop without its global loads (lut_gemm_kernel's LDS
+ * table layout, read addresses and pair adds; 128 accumulators per lane,
+ * one 512-thread workgroup per CU).  mode = sum of: 1 the 16 table reads of
+ * a sub-step, 2 the 128 adds, 4 the two table-build stores, 8 a barrier per
+ * four sub-steps; modes 1, 2, 3, 4, 7, 11 and 15 are built.  Each iteration
+ * is eight sub-steps of 128 lookups per lane: lookups = blocks * 512 * iters
+ * * 8 * 128.  out: blocks*512 uint32. */
+int atx_inner_probe(int mode, int blocks, int iters, unsigned* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

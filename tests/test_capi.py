@@ -33,7 +33,7 @@ def test_diag_probes_live_in_their_own_library():
     diag = ctypes.CDLL(os.path.join(ROOT, "approxtorch_amd", "libatx_diag.so"))
     lib = L.load()
     names = header_functions("atx_diag.h")
-    assert sorted(names) == ["atx_lds_probe", "atx_valu_probe"]
+    assert sorted(names) == ["atx_inner_probe", "atx_lds_probe", "atx_valu_probe"]
     for n in names:
         assert hasattr(diag, n) and not hasattr(lib, n), n
 
