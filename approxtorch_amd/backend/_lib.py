@@ -29,7 +29,8 @@ class ConvGeom(ctypes.Structure):
 
 
 class GemmEpilogue(ctypes.Structure):
-    _fields_ = [("out_kind", c_int), ("scale_x", c_vp), ("scale_w", c_vp), ("bias", c_vp)]
+    _fields_ = [("out_kind", c_int), ("scale_x", c_vp), ("scale_w", c_vp), ("bias", c_vp),
+                ("x_upper", c_vp)]
 
 
 # name -> (restype, argtypes); mirrors include/atx.h one to one.
@@ -70,6 +71,8 @@ _SIGS = {
     "atx_minmax": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_vp]),
     "atx_ema_absmax_apply": (c_int, [c_vp, c_float, c_float, c_float, c_vp, c_vp]),
     "atx_absmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_float, c_float, c_float, c_vp, c_vp]),
+    "atx_absmax_ema_upper": (c_int, [c_vp, c_ll, c_vp, c_vp, c_float, c_float, c_float, c_vp,
+                                     c_vp, c_vp]),
     "atx_minmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_float, c_float, c_int, c_vp,
                                c_vp, c_vp, c_vp, c_vp]),
     "atx_ema_minmax_apply": (c_int, [c_vp, c_vp, c_float, c_float, c_int, c_vp, c_vp, c_vp,

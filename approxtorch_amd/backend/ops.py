@@ -151,12 +151,14 @@ def date_tables(lut: Tensor, half_ws: int = 32):
 
 # -------------------------------------------------------------- LUT GEMM
 def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None,
-          transposed=False, wbase=None):
+          transposed=False, wbase=None, x_upper=None):
     """wbase: the caller guarantees every weight index lies in [wbase, wbase + 16)
-    (weight_bits <= 4); integer LUTs then run on the matrix cores."""
+    (weight_bits <= 4); integer LUTs then run on the matrix cores.  x_upper: a
+    device int32 flag that, when nonzero, guarantees every activation index of
+    the rows is >= 128 (atx_gemm_epilogue.x_upper; upper-half tables)."""
     img16, imgf, cls = lut_image(lut, transposed)
     dev = y.device
-    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias))
+    ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias), L.ptr(x_upper))
     if wbase is not None and cls != L.ATX_LUT_F32:
         wsb = L.query("atx_lut_gemm_narrow_workspace_bytes", N, K, Lc, O)
         ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
@@ -372,7 +374,8 @@ def conv_geom(x_shape, kernel_size, stride, padding, dilation):
 
 def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                  pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
-                 pad_dev=None, packed_w=None, return_operand=False, wbase=None):
+                 pad_dev=None, packed_w=None, return_operand=False, wbase=None,
+                 x_upper=None):
     """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
 
     img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
@@ -382,7 +385,9 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     fused weight fake-quant skips the weight packing.  Returns (y, wq), wq the
     uint8 weight index image; with return_operand, (y, wq, (xt, Rpad)), the
     row-offset operand for conv_backward_weight_rows.  wbase: every weight
-    index lies in [wbase, wbase + 16) (weight_bits <= 4; matrix-core GEMM)."""
+    index lies in [wbase, wbase + 16) (weight_bits <= 4; matrix-core GEMM).
+    x_upper: device flag as in _gemm (the image's indices and pad_index are
+    all >= 128 when it is set)."""
     imgc = img.contiguous()
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -400,7 +405,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
         wq, wt, Opad = packed_w
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
-    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase,
+          x_upper=x_upper)
     if return_operand:
         return y, wq, (xt, Rpad)
     return y, wq
@@ -912,10 +918,10 @@ def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
 
 def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                       out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None, packed_w=None,
-                      wbase=None):
+                      wbase=None, x_upper=None):
     """LUT conv from a prepacked row-offset operand (xt, Rpad) of geometry g
-    (fakequant_rows, or conv_forward's return_operand): (y, wq).  wbase as in
-    conv_forward."""
+    (fakequant_rows, or conv_forward's return_operand): (y, wq).  wbase and
+    x_upper as in conv_forward."""
     xt, Rpad = xt_rpad
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -930,7 +936,8 @@ def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int
         wq, wt, Opad = packed_w
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=xt.device)
-    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase,
+          x_upper=x_upper)
     return y, wq
 
 

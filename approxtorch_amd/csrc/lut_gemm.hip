@@ -106,6 +106,10 @@ struct GemmParams {
   // floor(tail tile * nqt / sk_per) of skws.
   int sk_per, nqt, sk_dp, sk_g;
   int* skws;
+  // Device flag (or null): nonzero when every activation index of the rows
+  // below R is at least 128 (x >= 0 before an int8 fake-quant).  The tables
+  // are then built for rows 128..255 only (upper-half tables).
+  const int* x_upper;
 };
 
 // ------------------------------------------------------------------ prepare
@@ -499,7 +503,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, void* y,
 }
 
 // Sums of one tile segment: rows tile tr, channels tile to, k in [kb, ke).
-template <bool SIGNED>
+template <bool SIGNED, bool UPPER>
 __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* smem, int tr,
                                          int to, int kb, int ke, int (&acc)[RPL][8]) {
   const int tid = threadIdx.x;
@@ -513,9 +517,20 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
   // og ^ (t & 3) of quarter q.  wb0 addresses row v0's chunk in quad
   // buffer 0 (buffer 1 is QTAB on); the quarter is an immediate offset
   // (q * 64).
+  //
+  // UPPER (every activation index >= 128): tables hold rows 128..255 only.
+  // They are built in pairs, wave w writing rows 128..255 of channel group og
+  // of table 2i + hw: in an even sub-step every wave loads the weight indices
+  // of the next pair and writes its table of the current pair, in an odd one
+  // it loads the LUT rows of the next pair and writes nothing, so each wave
+  // does half the table work of full tables.  Row 0 (the operand's padding
+  // rows and taps point there) is set once per kernel to a zero entry.
   const int og = __builtin_amdgcn_readfirstlane(wave % CG);
   const int hw = __builtin_amdgcn_readfirstlane(wave / CG);
-  const int wb0 = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
+  const int vbase = UPPER ? 128 : 128 * hw;             // first table row of the lane pairs
+  const int tsel = UPPER ? hw : 0;                      // the wave's table of a pair
+  const int sbase = 2 * vbase;                          // its byte offset in a LUT16T row
+  const int wb0 = (vbase + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
   // Read XOR masks: sub-step s of a quad reads quarter (rg + s) & 3.
   const unsigned gbase = (unsigned)((rg << 6) | (g << 4));
 
@@ -562,16 +577,26 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
 
     XRows xa, xb;
     Rows rows;
-    unsigned wnext;                                     // indices of table sigma+5
+    unsigned wnext = 0;                                 // indices of table sigma+5 (UPPER:
+                                                        // of the wave's table of the next pair)
     {
       Rows r4;
+      if constexpr (UPPER) {
 #pragma unroll
-      for (int q = 0; q < TPL; ++q) {
-        load_rows(r4, q < n ? lutr : lutz, load_w8(wtab(q), lane), lane, 256 * hw);
-        write_table<SIGNED>(smem + q * 64, r4, wb0);    // quad 0 -> buffer 0
+        for (int q = 0; q < TPL; q += 2) {
+          load_rows(r4, q + tsel < n ? lutr : lutz, load_w8(wtab(q + tsel), lane), lane, sbase);
+          write_table<SIGNED>(smem + (q + tsel) * 64, r4, wb0);  // quad 0 -> buffer 0
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) {
+          load_rows(r4, q < n ? lutr : lutz, load_w8(wtab(q), lane), lane, sbase);
+          write_table<SIGNED>(smem + q * 64, r4, wb0);  // quad 0 -> buffer 0
+        }
       }
-      load_rows(rows, TPL < n ? lutr : lutz, load_w8(wtab(TPL), lane), lane, 256 * hw);
-      wnext = load_w8(wtab(TPL + 1), lane);
+      load_rows(rows, TPL + tsel < n ? lutr : lutz, load_w8(wtab(TPL + tsel), lane), lane,
+                sbase);
+      if constexpr (!UPPER) wnext = load_w8(wtab(TPL + 1), lane);
       load_x(xa, quad_rows(0), xoff, 0);
     }
     __syncthreads();
@@ -585,14 +610,20 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
       // Issue order = order of use in the next sub-step (the counter of
       // outstanding loads is waited on in order): weight indices (first, to
       // address the LUT rows), row offsets (the accumulation), LUT rows
-      // (the table write at the end).
-      const unsigned wn = load_w8(wtab(sigma + 6), lane);
+      // (the table write at the end).  UPPER: even sub-steps load the
+      // indices of the pair (sigma+6, sigma+7) and write table sigma+4+hw,
+      // odd ones load the LUT rows of table sigma+5+hw.
+      constexpr bool kIdx = !UPPER || (S & 1) == 0;     // loads weight indices
+      constexpr bool kRows = !UPPER || (S & 1) == 1;    // loads LUT rows
+      unsigned wn = wnext;
+      if constexpr (kIdx) wn = load_w8(wtab(sigma + 6 + tsel), lane);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (S + 1 < TPL) load_x(xnext, quad_rows(j), xoff, (S + 1) * slot_bytes);
       else load_x(xnext, quad_rows(j + 1), xoff, 0);
       __builtin_amdgcn_sched_barrier(0);
       Rows rn;
-      load_rows(rn, sigma + 5 < n ? lutr : lutz, wnext, lane, 256 * hw);
+      if constexpr (kRows)
+        load_rows(rn, sigma + 5 + tsel < n ? lutr : lutz, wnext, lane, sbase);
       __builtin_amdgcn_sched_barrier(0);
       if (active) {
         use_table<SIGNED>(acc, smem, xcur, quarter_mask<S, B>(gbase));
@@ -604,8 +635,9 @@ __device__ __forceinline__ void lut_tile(const GemmParams& p, unsigned char* sme
           for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(acc[jj][e]));
       }
       __builtin_amdgcn_sched_barrier(0);
-      write_table<SIGNED>(smem + S * 64 + (B ? 0 : QTAB), rows, wb0);  // table sigma+4, other buffer
-      rows = rn;
+      if constexpr (kIdx)                               // table sigma+4 (+hw), other buffer
+        write_table<SIGNED>(smem + (S + tsel) * 64 + (B ? 0 : QTAB), rows, wb0);
+      if constexpr (kRows) rows = rn;
       wnext = wn;
       if constexpr (S == TPL - 1) __syncthreads();
     };
@@ -656,6 +688,14 @@ lut_gemm_kernel(const GemmParams p) {
   const int lb = logical_block();
   int acc[RPL][8];
   const bool has_rows = wave * RPW < p.rt;   // the wave's rows lie in the tile
+  const bool upper = p.x_upper && __builtin_amdgcn_readfirstlane(*p.x_upper) != 0;
+  if (upper && tid < 2 * (LINE / 16)) {      // row 0 (line 0) of both quad buffers
+    // a zero entry as the table build stores it: signed tables hold their
+    // even channels biased by LOW_BIAS, which pair_sums takes off per table
+    const unsigned z = SIGNED ? LOW_BIAS : 0u;
+    const int c = tid % (LINE / 16);
+    *(uint4*)(smem + (tid < LINE / 16 ? 0 : QTAB) + 16 * c) = make_uint4(z, z, z, z);
+  }
 
   if (p.sk_per == 0) {
     int l = lb;
@@ -663,7 +703,8 @@ lut_gemm_kernel(const GemmParams p) {
     const int tr = l % p.tiles_r;
     const int s = l / p.tiles_r;
     const int kb = s * p.k_chunk;
-    lut_tile<SIGNED>(p, smem, tr, to, kb, min(p.K, kb + p.k_chunk), acc);
+    if (upper) lut_tile<SIGNED, true>(p, smem, tr, to, kb, min(p.K, kb + p.k_chunk), acc);
+    else lut_tile<SIGNED, false>(p, smem, tr, to, kb, min(p.K, kb + p.k_chunk), acc);
     // ---- epilogue: registers -> HBM, every wave at once (no LDS staging).
     const int r0 = tr * p.rt + wave * RPW + rg * RQ;     // this lane's first quad
     const int oc = to * OT + g * 8;
@@ -684,7 +725,8 @@ lut_gemm_kernel(const GemmParams p) {
   for (int tile = lb; tile < p.sk_dp; tile += p.sk_g) {
     const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
     __syncthreads();                         // the previous segment's tables are read
-    lut_tile<SIGNED>(p, smem, tr, to, 0, p.K, acc);
+    if (upper) lut_tile<SIGNED, true>(p, smem, tr, to, 0, p.K, acc);
+    else lut_tile<SIGNED, false>(p, smem, tr, to, 0, p.K, acc);
     const int r0 = tr * p.rt + wave * RPW + rg * RQ;
     const int oc = to * OT + g * 8;
     if (!has_rows) continue;
@@ -702,7 +744,8 @@ lut_gemm_kernel(const GemmParams p) {
     const int tile = p.sk_dp + tt;
     const int to = tile % p.tiles_o, tr = tile / p.tiles_o;
     __syncthreads();                         // the previous segment's tables are read
-    lut_tile<SIGNED>(p, smem, tr, to, TPL * q0, min(p.K, TPL * q1), acc);
+    if (upper) lut_tile<SIGNED, true>(p, smem, tr, to, TPL * q0, min(p.K, TPL * q1), acc);
+    else lut_tile<SIGNED, false>(p, smem, tr, to, TPL * q0, min(p.K, TPL * q1), acc);
     if (!has_rows) {
       // nothing to store or add (the slots' rows of this wave stay zero)
     } else if (q0 == 0 && q1 == p.nqt) {
@@ -1139,6 +1182,7 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
   p.K = K; p.R = (int)R; p.L = L; p.O = O;
   p.out_kind = ep.out_kind; p.y = y;
   p.sx = ep.scale_x; p.sw = ep.scale_w; p.bias = ep.bias;
+  p.x_upper = ep.x_upper;
 
   if (lut_class == ATX_LUT_F32) {
     ATX_REQUIRE(lutf32t, "atx_lut_gemm: fp32 class needs the fp32 image");

@@ -281,9 +281,11 @@ __global__ void minmax_partial_kernel(const float* __restrict__ x, long long n,
 
 // EMA of the statistics, applied by the final reduction block when fused.
 struct EmaArgs {
-  int kind;                 // 0: none, 1: int8 absmax scale, 2: uint8 min/max qparams
+  int kind;                 // 0: none, 1: int8 absmax scale, 2: uint8 min/max qparams,
+                            // 3: int8 absmax scale from (min, max) plus the x >= 0 flag
   float denom, m32, om32, qmax;
   float* scale; float* zero; float* x_min; float* x_max;
+  int* upper;               // kind 3: 1 when min(x) >= 0 (no NaN), else 0
 };
 __device__ void apply_ema(const EmaArgs& e, float mn, float mx);
 
@@ -298,6 +300,13 @@ __global__ void minmax_final_kernel(const float* __restrict__ part, int nb,
   }
   block_minmax<ABS>(mn, mx);
   if (threadIdx.x == 0) {
+    if (ema.kind == 3) {
+      // max |x| = max(-min x, max x) exactly (NaN propagates through both);
+      // the flag holds for every x >= 0, -0 included
+      ema.upper[0] = (mn >= 0.0f) ? 1 : 0;
+      mx = nmax(-mn, mx);
+      mn = 0.0f;
+    }
     if (mn_out) *mn_out = mn;
     if (mx_out) *mx_out = mx;
     if (ema.kind) apply_ema(ema, mn, mx);
@@ -344,7 +353,7 @@ __global__ void ema_minmax_kernel(const float* mn, const float* mx, float m32, f
 }
 
 __device__ void apply_ema(const EmaArgs& e, float mn, float mx) {
-  if (e.kind == 1) ema_absmax(mx, e.denom, e.m32, e.om32, e.scale);
+  if (e.kind == 1 || e.kind == 3) ema_absmax(mx, e.denom, e.m32, e.om32, e.scale);
   else ema_minmax(mn, mx, e.m32, e.om32, e.qmax, e.x_min, e.x_max, e.scale, e.zero);
 }
 
@@ -551,6 +560,15 @@ int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_ou
   EmaArgs e{};
   e.kind = 1; e.denom = denom; e.m32 = m32; e.om32 = om32; e.scale = scale;
   return minmax_impl(x, n, ws, nullptr, stat_out, true, stream, e);
+}
+
+int atx_absmax_ema_upper(const float* x, long long n, unsigned int* ws, float* stat_out,
+                         float denom, float m32, float om32, float* scale, int* upper,
+                         hipStream_t stream) {
+  ATX_REQUIRE(stat_out && scale && upper, "atx_absmax_ema_upper: null output");
+  EmaArgs e{};
+  e.kind = 3; e.denom = denom; e.m32 = m32; e.om32 = om32; e.scale = scale; e.upper = upper;
+  return minmax_impl(x, n, ws, nullptr, stat_out, false, stream, e);
 }
 
 int atx_minmax_ema(const float* x, long long n, unsigned int* ws, float* mn_out,

@@ -155,7 +155,9 @@ class Conv2d_int8(nn.Module):
     def _update_scale(self, x):
         """scale_x <- m * absmax(x)/127 + (1-m) * scale_x (nn/Conv2d_int8.py:137-146).
         The absmax reduction and the EMA run on the device; under DDP the
-        statistic is MAX-all-reduced in between so every rank's scale agrees."""
+        statistic is MAX-all-reduced in between so every rank's scale agrees.
+        Returns a device int32 flag, set when x >= 0 everywhere (the LUT GEMM
+        of this forward may then build half-height tables), or None."""
         _check_stat_inputs(x, ("scale_x", self.scale_x))
         with torch.no_grad():
             xc = x.contiguous()
@@ -164,16 +166,19 @@ class Conv2d_int8(nn.Module):
             s = L.stream_of(xc)
             m32, om32 = _ema_coeffs(self.scale_momentum)
             denom = float((self.qmax - self.qmin) / 2)
+            upper = None
             if not (dist.is_available() and dist.is_initialized()):
                 # no all-reduce in between: the EMA runs in the reduction's last launch
-                L.call("atx_absmax_ema", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), denom,
-                       m32, om32, L.ptr(self.scale_x), s)
+                upper = torch.empty((), dtype=torch.int32, device=x.device)
+                L.call("atx_absmax_ema_upper", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat),
+                       denom, m32, om32, L.ptr(self.scale_x), L.ptr(upper), s)
             else:
                 L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
                 dist.all_reduce(stat, op=dist.ReduceOp.MAX)
                 L.call("atx_ema_absmax_apply", L.ptr(stat), denom, m32, om32,
                        L.ptr(self.scale_x), s)
         _bump(self.scale_x)
+        return upper
 
     def _update_scale_w(self):
         """Per-channel EMA of absmax(W)/qmax_w; zero channels keep their scale
@@ -215,8 +220,9 @@ class Conv2d_int8(nn.Module):
         OH = (H + 2 * pH - dH * (kH - 1) - 1) // sH + 1
         OW = (W + 2 * pW - dW * (kW - 1) - 1) // sW + 1
 
+        upper = None
         if self.training and self.update_scale:
-            self._update_scale(x)
+            upper = self._update_scale(x)
             self._update_scale_w()
 
         qmax_w = 2 ** (self.weight_bits - 1) - 1
@@ -231,7 +237,7 @@ class Conv2d_int8(nn.Module):
                 tx = tw = bgemm_int8.decode_table(x.device)
             return bgemm_int8.conv2d_int8_fused(x, self.weight, self.bias, self.scale_x,
                                                 self.scale_w, self.lut, tx, tw, geom,
-                                                self.qmin, self.qmax, qmax_w)
+                                                self.qmin, self.qmax, qmax_w, x_upper=upper)
 
         x = quantization.static_quantize_int8(x, self.scale_x, self.qmin, self.qmax)
         w = quantization.static_quantize_int8(self.weight, self.scale_w, -qmax_w, qmax_w,

@@ -228,7 +228,8 @@ class _conv2d_int8_fused(Function):
     tx / tw: the estimator's tables (STE: decode tables, LRE: dx / dw)."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w):
+    def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w,
+                x_upper=None):
         g, depthwise = _conv_setup(x, weight, geom)
         O = weight.size(0)
         # a 1x1, stride-1, unpadded conv reads x itself as its operand: the
@@ -250,7 +251,7 @@ class _conv2d_int8_fused(Function):
             y, _ = ops.conv_forward_rows(xt_rpad, wq, lut, g, 128,
                                          out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
                                          sw=scale_w, bias=b, packed_w=(wq, wt, Opad),
-                                         wbase=wbase)
+                                         wbase=wbase, x_upper=x_upper)
             saved_x, ctx.rpad = xt_rpad
         elif depthwise:
             y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
@@ -262,7 +263,7 @@ class _conv2d_int8_fused(Function):
             y, _, (xt, Rpad) = ops.conv_forward(
                 xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
                 sw=scale_w, bias=b, packed_w=(wq, wt, Opad), return_operand=True,
-                wbase=wbase)
+                wbase=wbase, x_upper=x_upper)
             saved_x, ctx.rpad = xt, Rpad
         ctx.save_for_backward(saved_x, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
                               tx.contiguous(), tw.contiguous())
@@ -293,13 +294,16 @@ class _conv2d_int8_fused(Function):
                                                    go_sw=sw).view(ctx.wshape)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
-        return gx, gw, gb, None, None, None, None, None, None, None, None, None
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
 
 
 def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax,
-                      qmax_w):
+                      qmax_w, x_upper=None):
+    """x_upper: optional device int32 flag, written for this same x, that is
+    nonzero only when x >= 0 everywhere (Conv2d_int8's training-mode statistic,
+    atx_absmax_ema_upper); the LUT GEMM then builds half-height tables."""
     return _conv2d_int8_fused.apply(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom,
-                                    qmin, qmax, qmax_w)
+                                    qmin, qmax, qmax_w, x_upper)
 
 
 class _conv2d_int8_custom(Function):

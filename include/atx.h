@@ -152,6 +152,14 @@ typedef struct atx_gemm_epilogue {
   const float* scale_x;   /* [1]  (DEQUANT) */
   const float* scale_w;   /* [O]  (DEQUANT) */
   const float* bias;      /* [O] or null    */
+  /* Device int or null, read by atx_lut_gemm / atx_lut_gemm_noalloc at
+   * kernel start (atx_lut_gemm_narrow ignores it): nonzero promises that
+   * every activation index of the rows below N*L is at least 128, as for the
+   * int8 operand of an x >= 0 (atx_absmax_ema_upper writes such a flag).
+   * The kernel then builds only rows 128..255 of its tables, half the table
+   * work, with the same exact sums; a broken promise gives wrong sums, never
+   * an out-of-bounds access.  No counterpart in the reference. */
+  const int* x_upper;
 } atx_gemm_epilogue;
 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O);
@@ -299,6 +307,15 @@ int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32,
  * all-reduce of the statistic in between (single process). */
 int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_out,
                    float denom, float m32, float om32, float* scale, hipStream_t stream);
+/* atx_absmax_ema that also writes *upper = 1 when min(x) >= 0 (no NaN), else
+ * 0: then the int8 fake-quant of x (any positive scale) has every LUT index
+ * at or above 128, the promise of atx_gemm_epilogue.x_upper.  Same stat_out
+ * and scale update as atx_absmax_ema, bit for bit (max |x| is taken as
+ * max(-min x, max x)).  No counterpart in the reference; used by the int8
+ * layer's training-mode forward (nn/Conv2d_int8.py:137-146). */
+int atx_absmax_ema_upper(const float* x, long long n, unsigned int* ws, float* stat_out,
+                         float denom, float m32, float om32, float* scale, int* upper,
+                         hipStream_t stream);
 /* atx_minmax then atx_ema_minmax_apply, fused the same way. */
 int atx_minmax_ema(const float* x, long long n, unsigned int* ws, float* mn_out,
                    float* mx_out, float m32, float om32, int qmax, float* x_min,
