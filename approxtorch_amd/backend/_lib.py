@@ -28,9 +28,16 @@ class ConvGeom(ctypes.Structure):
                  "OH", "OW")]
 
 
+ABI_VERSION = 2                      # ATX_ABI_VERSION
+
+
 class GemmEpilogue(ctypes.Structure):
-    _fields_ = [("out_kind", c_int), ("scale_x", c_vp), ("scale_w", c_vp), ("bias", c_vp),
-                ("x_upper", c_vp)]
+    """atx_gemm_epilogue; `size` (the first field) is filled in."""
+    _fields_ = [("size", c_int), ("out_kind", c_int), ("scale_x", c_vp), ("scale_w", c_vp),
+                ("bias", c_vp), ("x_upper", c_vp)]
+
+    def __init__(self, out_kind=0, scale_x=None, scale_w=None, bias=None, x_upper=None):
+        super().__init__(ctypes.sizeof(GemmEpilogue), out_kind, scale_x, scale_w, bias, x_upper)
 
 
 # name -> (restype, argtypes); mirrors include/atx.h one to one.
@@ -133,6 +140,9 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        if lib.atx_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} implements ABI version {lib.atx_version()}, this "
+                               f"binding needs {ABI_VERSION}; rebuild the library")
         _lib = lib
     return _lib
 

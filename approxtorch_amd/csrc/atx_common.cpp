@@ -28,5 +28,5 @@ int check_launch(const char* what) {
 
 extern "C" {
 const char* atx_last_error(void) { return atx::g_err; }
-int atx_version(void) { return 1; }
+int atx_version(void) { return ATX_ABI_VERSION; }
 }

@@ -85,3 +85,11 @@ __device__ __forceinline__ unsigned quant_index(float v, int offset) {
   do {                                                           \
     if (!(cond)) return ::atx::set_error(ATX_EINVAL, __VA_ARGS__); \
   } while (0)
+
+// First check of every entry point taking an atx_gemm_epilogue: its size
+// field must be this header's sizeof (an older caller's struct is rejected).
+#define ATX_REQUIRE_EPILOGUE(ep, fn)                                              \
+  ATX_REQUIRE((ep).size == (int)sizeof(atx_gemm_epilogue),                        \
+              fn ": atx_gemm_epilogue.size is %d, expected %d (caller built "     \
+              "against another atx.h; ABI version %d)", (ep).size,                \
+              (int)sizeof(atx_gemm_epilogue), ATX_ABI_VERSION)

@@ -253,6 +253,7 @@ extern "C" {
 int atx_dwconv_fwd(const void* img, int dtype, atx_conv_geom g, int pad_index,
                    const uint8_t* wq, const uint16_t* lut16t, const float* lutf32t,
                    int lut_class, atx_gemm_epilogue ep, void* y, hipStream_t stream) {
+  ATX_REQUIRE_EPILOGUE(ep, "atx_dwconv_fwd");
   int rc = dw_check(g, dtype, pad_index, "atx_dwconv_fwd");
   if (rc) return rc;
   ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,

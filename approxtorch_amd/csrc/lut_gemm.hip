@@ -891,7 +891,13 @@ constexpr int PLAN_CUS = 256;
 //   (ceil(per / nqt) + 1 at most; table prologue and atomic sums) + 0.1 per
 //   cut tile (its 256 KiB slot) + 45 for the clear / finish launches.
 // It is taken when cheaper than the best split-K plan (5 of the 19 shapes,
-// e.g. K = 576 at 56 x 56 with 64 channels: 460 against 491 us).
+// e.g. K = 576 at 56 x 56 with 64 channels: 460 against 491 us).  With the
+// upper-half tables (x_upper given: `upper`) a k-step costs ~0.74 us instead
+// of ~0.95 while the cuts' atomics, clears and finishes do not shrink; refit
+// on the four stream-K shapes of the 52 ResNet-50 layers at batch 64, a cut
+// costs ~0.7 k-steps there (0.1 with full tables), which hands K = 576 at
+// 56 x 56 with 64 channels (513 -> 467 us) and K = 512 at 28 x 28 with 256
+// (461 -> 420 us) to split-K.
 // ATX_LUT_SCHEDULE (environment: auto | split | stream_k) overrides the
 // choice; ATX_LUT_ROWS and ATX_LUT_SPLITS force the rows per tile and the
 // split count (split-K plans), for measurement.
@@ -900,7 +906,8 @@ constexpr int PLAN_CUS = 256;
 // by the int32-exactness bound) needs more, the plan's splits is -1.
 constexpr long long SK_SLOT_BYTES = (long long)(PLAN_CUS - 1) * RT * OT * 4;
 
-static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit = -1) {
+static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit = -1,
+                      bool upper = false) {
   Plan pl;
   const long long R = (long long)N * L;
   pl.tiles_r = (int)cdiv(R, RT);
@@ -970,7 +977,8 @@ static Plan make_plan(int N, int K, int L, int O, int kmax, long long ws_limit =
     if (per >= 2) {
       const long long cuts = std::min<long long>(tail, cdiv(T, per) - 1);
       const double sk_cost = (double)rounds * (K + 14) + 4.0 * per +
-                             14.0 * (double)(cdiv(per, pl.nqt) + 1) + 0.1 * cuts + 45.0;
+                             14.0 * (double)(cdiv(per, pl.nqt) + 1) +
+                             (upper ? 0.7 : 0.1) * cuts + 45.0;
       if (force_sk || sk_cost < best_cost) {
         pl.sk_per = (int)per;
         pl.sk_dp = (int)(rounds * cus);
@@ -1136,10 +1144,14 @@ int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc, 
 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O) {
   if (N <= 0 || K <= 0 || L <= 0 || O <= 0) return 0;
-  const Plan pl = make_plan(N, K, L, O, KMAX_U16);
-  if (pl.sk_per > 0) return SK_SLOT_BYTES;
-  if (pl.splits <= 1) return 0;
-  return (long long)pl.splits * N * O * L * 4;
+  // the launch plans with or without an x_upper flag: enough for either
+  long long bytes = 0;
+  for (int upper = 0; upper < 2; ++upper) {
+    const Plan pl = make_plan(N, K, L, O, KMAX_U16, -1, upper != 0);
+    if (pl.sk_per > 0) bytes = std::max(bytes, SK_SLOT_BYTES);
+    else if (pl.splits > 1) bytes = std::max(bytes, (long long)pl.splits * N * O * L * 4);
+  }
+  return bytes;
 }
 
 }  // extern "C"
@@ -1155,6 +1167,7 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
                         int L, int O, const uint16_t* lut16t, const float* lutf32t,
                         int lut_class, atx_gemm_epilogue ep, void* y, void* workspace,
                         long long ws_limit, ScratchFn scratch, hipStream_t stream) {
+  ATX_REQUIRE_EPILOGUE(ep, "atx_lut_gemm");
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_lut_gemm: negative size");
   const long long R = (long long)N * L;
   ATX_REQUIRE(R <= 0x7fffffffLL - RT, "atx_lut_gemm: N*L too large");
@@ -1190,7 +1203,7 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
                               ep.scale_w, ep.bias, (float*)y, stream);
   }
   ATX_REQUIRE(lut16t, "atx_lut_gemm: integer class needs the 16-bit image");
-  const Plan pl = make_plan(N, K, L, O, KMAX_U16, ws_limit);
+  const Plan pl = make_plan(N, K, L, O, KMAX_U16, ws_limit, ep.x_upper != nullptr);
   if (pl.splits < 0)
     return set_error(ATX_ERANGE,
                      "atx_lut_gemm_noalloc: K = %d needs %lld bytes of int32 partial sums "

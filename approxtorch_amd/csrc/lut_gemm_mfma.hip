@@ -303,6 +303,7 @@ long long atx_lut_gemm_narrow_workspace_bytes(int N, int K, int L, int O) {
 int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N, int K,
                         int L, int O, const uint16_t* lut16t, int lut_class, int wbase,
                         atx_gemm_epilogue ep, void* y, void* workspace, hipStream_t stream) {
+  ATX_REQUIRE_EPILOGUE(ep, "atx_lut_gemm_narrow");
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_lut_gemm_narrow: negative size");
   ATX_REQUIRE(lut_class == ATX_LUT_I16 || lut_class == ATX_LUT_U16,
               "atx_lut_gemm_narrow: needs an integer LUT class (int16 or uint16)");

@@ -44,6 +44,12 @@ typedef struct atx_conv_geom {
   int OH, OW;              /* output spatial size               */
 } atx_conv_geom;
 
+/* ABI version, returned by atx_version().  2: atx_gemm_epilogue carries
+ * its own size (first field) and the x_upper flag; atx_custom_grad_dx/dw
+ * take the dy_scale and dx/dw table arguments below and atx_tap_sum its
+ * workspace.  Version 1 callers must be rebuilt against this header. */
+#define ATX_ABI_VERSION 2
+
 const char* atx_last_error(void);
 int atx_version(void);
 
@@ -148,6 +154,11 @@ int atx_im2col_u8(const void* img, int dtype, atx_conv_geom g, uint8_t* out,
 enum { ATX_OUT_F32 = 0, ATX_OUT_I32 = 1, ATX_OUT_DEQUANT = 2 };
 
 typedef struct atx_gemm_epilogue {
+  /* sizeof(atx_gemm_epilogue): set by atx_gemm_epilogue_make (or by hand).
+   * Every entry point taking the struct rejects another value with
+   * ATX_EINVAL before touching the device, so a caller built against an
+   * older header (whose first field is out_kind, 0..2) fails cleanly. */
+  int size;
   int out_kind;
   const float* scale_x;   /* [1]  (DEQUANT) */
   const float* scale_w;   /* [O]  (DEQUANT) */
@@ -161,6 +172,20 @@ typedef struct atx_gemm_epilogue {
    * an out-of-bounds access.  No counterpart in the reference. */
   const int* x_upper;
 } atx_gemm_epilogue;
+
+static inline atx_gemm_epilogue atx_gemm_epilogue_make(int out_kind, const float* scale_x,
+                                                       const float* scale_w,
+                                                       const float* bias,
+                                                       const int* x_upper) {
+  atx_gemm_epilogue ep;
+  ep.size = (int)sizeof(atx_gemm_epilogue);
+  ep.out_kind = out_kind;
+  ep.scale_x = scale_x;
+  ep.scale_w = scale_w;
+  ep.bias = bias;
+  ep.x_upper = x_upper;
+  return ep;
+}
 
 long long atx_lut_gemm_workspace_bytes(int N, int K, int L, int O);
 

@@ -24,7 +24,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(names) == L.exported_symbols()
-    assert lib.atx_version() == 1
+    assert lib.atx_version() == L.ABI_VERSION == 2
 
 
 def test_diag_probes_live_in_their_own_library():
@@ -52,6 +52,31 @@ def test_invalid_arguments_return_einval_without_gpu():
     g.OH = 7
     rc = lib.atx_im2col_u8(None, 0, g, None, None)
     assert rc == -1 and b"OH/OW" in lib.atx_last_error()
+
+
+def test_epilogue_of_another_abi_is_rejected_without_gpu():
+    """A caller built against the version-1 header passes a struct whose
+    first field is out_kind (0..2): rejected on the host, nothing launched."""
+    lib = L.load()
+
+    class EpilogueV1(ctypes.Structure):
+        _fields_ = [("out_kind", ctypes.c_int), ("scale_x", ctypes.c_void_p),
+                    ("scale_w", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
+
+    assert ctypes.sizeof(L.GemmEpilogue) == 40 and L.GemmEpilogue(2).size == 40
+    for name, args in (("atx_lut_gemm", (None, 2048, None, 32, 1, 4, 4, 4, None, None, 0)),
+                       ("atx_lut_gemm_narrow", (None, 2048, None, 32, 1, 4, 4, 4, None, 0, 0))):
+        fn = ctypes.CDLL(L.LIB_PATH)[name]          # unprototyped: any struct goes through
+        fn.restype = ctypes.c_int
+        old = EpilogueV1(2, None, None, None)
+        rc = fn(*[ctypes.c_void_p(a) if a is None else ctypes.c_int(a) for a in args], old,
+                None, None, None)
+        assert rc == -1, name
+        assert b"atx_gemm_epilogue.size" in lib.atx_last_error(), name
+    bad = L.GemmEpilogue(0)
+    bad.size = 32
+    rc = lib.atx_lut_gemm(None, 2048, None, 32, 1, 4, 4, 4, None, None, 0, bad, None, None, None)
+    assert rc == -1 and b"expected 40" in lib.atx_last_error()
 
 
 def test_workspace_queries_are_host_only():
