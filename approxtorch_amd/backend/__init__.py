@@ -68,13 +68,17 @@ _SCHEMAS = {
              ops.bgemm_lre_backward_claude_im2col(go, x, w, dx, dw, (kh, kw), (sh, sw),
                                                   (ph, pw), (dh, dwl))),
     "bgemm_custom_grad_uint8_dx":
-        ("(Tensor X, Tensor W, Tensor dY, Tensor lut) -> Tensor", ops.bgemm_custom_grad_uint8_dx),
+        ("(Tensor X, Tensor W, Tensor dY, Tensor dx_lut) -> Tensor",
+         ops.bgemm_custom_grad_uint8_dx),
     "bgemm_custom_grad_uint8_dw":
-        ("(Tensor X, Tensor W, Tensor dY, Tensor lut) -> Tensor", ops.bgemm_custom_grad_uint8_dw),
+        ("(Tensor X, Tensor W, Tensor dY, Tensor dw_lut) -> Tensor",
+         ops.bgemm_custom_grad_uint8_dw),
     "bgemm_custom_grad_int8_dx":
-        ("(Tensor X, Tensor W, Tensor dY, Tensor lut) -> Tensor", ops.bgemm_custom_grad_int8_dx),
+        ("(Tensor X, Tensor W, Tensor dY, Tensor dx_lut) -> Tensor",
+         ops.bgemm_custom_grad_int8_dx),
     "bgemm_custom_grad_int8_dw":
-        ("(Tensor X, Tensor W, Tensor dY, Tensor lut) -> Tensor", ops.bgemm_custom_grad_int8_dw),
+        ("(Tensor X, Tensor W, Tensor dY, Tensor dw_lut) -> Tensor",
+         ops.bgemm_custom_grad_int8_dw),
     "fakequant_per_tensor_claude":
         ("(Tensor x, Tensor scale, int qmin, int qmax) -> (Tensor, Tensor)",
          lambda x, s, qmin, qmax: ops.fakequant_per_tensor(x, s, qmin, qmax)[:2]),

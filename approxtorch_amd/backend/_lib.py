@@ -45,8 +45,8 @@ _SIGS = {
     "atx_last_error": (ctypes.c_char_p, []),
     "atx_version": (c_int, []),
     "atx_lut_prepare": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp]),
-    "atx_pack_x_f32": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_int, c_vp]),
-    "atx_pack_x_u8": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp]),
+    "atx_pack_x_f32": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
+    "atx_pack_x_u8": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp]),
     "atx_pack_w_f32": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_vp]),
     "atx_pack_w_u8": (c_int, [c_vp, c_int, c_int, c_vp, c_int, c_vp]),
     "atx_im2col_rows": (c_int, [c_vp, c_int, ConvGeom, c_int, c_vp, c_vp, c_int, c_vp]),
@@ -62,7 +62,7 @@ _SIGS = {
     "atx_fakequant_fwd": (c_int, [c_vp, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                   c_vp]),
     "atx_fakequant_rows": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_int, c_int,
-                                   c_vp, c_vp, c_int, c_vp]),
+                                   c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),
     "atx_fakequant_bwd": (c_int, [c_vp, c_vp, c_ll, c_vp, c_int, c_ll, c_vp, c_vp]),
     "atx_fakequant_channel_fwd": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_int, c_int, c_int,
                                           c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
@@ -70,6 +70,7 @@ _SIGS = {
     "atx_col2im_pos": (c_int, [c_vp, ConvGeom, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_tap_sum": (c_int, [c_vp, c_int, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
+    "atx_zero_point_pos": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_tap_sum_bwd": (c_int, [c_vp, ConvGeom, c_vp, c_vp]),
     "atx_uint8_dequant": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                   c_vp, c_int, c_vp]),
@@ -94,7 +95,7 @@ _SIGS = {
     "atx_conv_bwd_data_col": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp,
                                       c_vp]),
     "atx_pack_rows_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
-                                      c_int, c_vp]),
+                                      c_int, c_vp, c_vp]),
     "atx_pack_cols_strided": (c_int, [c_vp, c_int, c_int, c_int, c_ll, c_ll, c_int, c_vp, c_vp,
                                       c_int, c_vp]),
     "atx_parse_text_table": (c_int, [ctypes.c_char_p, c_int, c_vp, c_ll, c_vp]),

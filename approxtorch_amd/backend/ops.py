@@ -172,6 +172,14 @@ def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, b
     return y
 
 
+def upper_flag(device):
+    """A device int32 flag set to 1, for a fake-quant or row-packing kernel to
+    clear when some LUT index of its operand is below 128; passed on as the
+    LUT GEMM's x_upper, a flag still set lets it build half-height tables
+    (atx_gemm_epilogue.x_upper)."""
+    return torch.ones((), dtype=torch.int32, device=device)
+
+
 def _pack_w(w, offset, want_wq=True):
     """w fp32 [O,K] (quantized values) or uint8 [O,K] indices -> (wq, wt, Opad)."""
     O, K = w.shape
@@ -208,15 +216,17 @@ def _bgemm_save(x, w, lut, offset, name):
     R = N * Lc
     Rpad = L.round_up(max(R, 1), L.ROW_TILE)
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
+    up = upper_flag(dev)
     if xc.dtype == torch.uint8:
         xq = xc
-        L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, s)
+        L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, L.ptr(up), s)
     else:
         xq = torch.empty((N, K, Lc), dtype=torch.uint8, device=dev)
-        L.call("atx_pack_x_f32", L.ptr(xc), N, K, Lc, offset, L.ptr(xq), L.ptr(xt), Rpad, s)
+        L.call("atx_pack_x_f32", L.ptr(xc), N, K, Lc, offset, L.ptr(xq), L.ptr(xt), Rpad,
+               L.ptr(up), s)
     wq, wt, Opad = _pack_w(wc, offset)
     y = torch.empty((N, O, Lc), dtype=torch.float32, device=dev)
-    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_F32, y)
+    _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_F32, y, x_upper=up)
     return y, xq, wq
 
 
@@ -260,10 +270,11 @@ def lut_gemm_i32(X: Tensor, W: Tensor, lut: Tensor) -> Tensor:
     O = wc.size(0)
     Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=xc.device)
-    L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, L.stream_of(xc))
+    up = upper_flag(xc.device)
+    L.call("atx_pack_x_u8", L.ptr(xc), N, K, Lc, L.ptr(xt), Rpad, L.ptr(up), L.stream_of(xc))
     _, wt, Opad = _pack_w(wc, 0)
     y = torch.empty((N, O, Lc), dtype=torch.int32, device=xc.device)
-    return _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_I32, y)
+    return _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_I32, y, x_upper=up)
 
 
 # ------------------------------------------- plain LUT GEMM (torch.mm layout)
@@ -310,12 +321,14 @@ def _gemm2d_save(A, B, lut, offset, name):
     Opad = L.round_up(max(C, 1), L.COL_TILE)
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=dev)
     wt = torch.empty((K, Opad), **u8)
+    up = upper_flag(dev)
     L.call("atx_pack_rows_strided", L.ptr(X), int(X.dtype == torch.uint8), R, K, sr, sk,
-           offset, L.ptr(xq), L.ptr(xt), Rpad, s)
+           offset, L.ptr(xq), L.ptr(xt), Rpad, L.ptr(up), s)
     L.call("atx_pack_cols_strided", L.ptr(Y), int(Y.dtype == torch.uint8), C, K, sc, skc,
            offset, L.ptr(yq), L.ptr(wt), Opad, s)
     if y.numel():
-        _gemm(xt, Rpad, wt, Opad, Nb, K, Lc, C, lut, L.ATX_OUT_F32, y, transposed=not rows_m)
+        _gemm(xt, Rpad, wt, Opad, Nb, K, Lc, C, lut, L.ATX_OUT_F32, y, transposed=not rows_m,
+              x_upper=up)
     return y, aq, bq
 
 
@@ -557,6 +570,18 @@ def uint8_dequant(y: Tensor, xsum: Tensor, wsum: Tensor, zero_x: Tensor, zero_w:
     return y
 
 
+def zero_point_pos(go: Tensor, scale_x: Tensor, scale_w: Tensor, zero_w: Tensor) -> Tensor:
+    """pos [N, L] = sum_o -(scale_x * scale_w[o]) * zero_w[o] * go[n, o, l] for
+    go [N, O, L]: the uint8 layer's zero-point position term in backward."""
+    goc = go.contiguous()
+    N, O, Lc = goc.shape
+    pos = torch.empty((N, Lc), dtype=torch.float32, device=goc.device)
+    L.call("atx_zero_point_pos", L.ptr(goc), N, O, Lc, L.ptr(scale_x.contiguous()),
+           L.ptr(scale_w.contiguous()), L.ptr(zero_w.contiguous()), L.ptr(pos),
+           L.stream_of(goc))
+    return pos
+
+
 def tap_sum_backward(go: Tensor, g) -> Tensor:
     goc = go.contiguous()
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)
@@ -794,7 +819,7 @@ def pack_rows_u8(X: Tensor):
     N, K, Lc = Xc.shape
     Rpad = L.round_up(max(N * Lc, 1), L.ROW_TILE)
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=Xc.device)
-    L.call("atx_pack_x_u8", L.ptr(Xc), N, K, Lc, L.ptr(xt), Rpad, L.stream_of(Xc))
+    L.call("atx_pack_x_u8", L.ptr(Xc), N, K, Lc, L.ptr(xt), Rpad, None, L.stream_of(Xc))
     return xt, Rpad
 
 
@@ -873,9 +898,11 @@ def require_param(p, x: Tensor, name: str, numel: int = 1):
 
 
 def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
-                         want_q=True, q8_dtype=None):
+                         want_q=True, q8_dtype=None, nonneg=None):
     """(q fp32, mask bool[, q8]) of the fused per-tensor fake-quant
-    (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric)."""
+    (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric).
+    nonneg: optional device int32 flag (upper_flag()), cleared when some
+    quantized value is negative."""
     require_cuda_f32(x, "x")
     require_param(scale, x, "scale")
     require_param(zero_point, x, "zero_point")
@@ -887,16 +914,18 @@ def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_po
     q8 = torch.empty(xc.shape, dtype=q8_dtype, device=xc.device) if q8_dtype else None
     L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale.contiguous()),
            L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax,
-           L.ptr(q), L.ptr(mask), L.ptr(q8), L.stream_of(xc))
+           L.ptr(q), L.ptr(mask), L.ptr(q8), L.ptr(nonneg), L.stream_of(xc))
     return q, mask, q8
 
 
 def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
-                   zero_point=None):
+                   zero_point=None, upper=None):
     """Input fake-quant of a 1x1, stride-1, unpadded conv fused with its
     operand packing: x [N,K,H,W] -> (mask bool [N,K,H,W], (xt, Rpad)), the
     row-offset operand that fakequant_per_tensor's byte image would give
-    through conv_forward's im2col (offset 128: int8 image, 0: uint8)."""
+    through conv_forward's im2col (offset 128: int8 image, 0: uint8).
+    upper: optional device int32 flag (upper_flag()), cleared when some LUT
+    index of the operand is below 128."""
     require_cuda_f32(x, "x")
     require_param(scale, x, "scale")
     require_param(zero_point, x, "zero_point")
@@ -912,7 +941,7 @@ def fakequant_rows(x: Tensor, scale: Tensor, qmin: int, qmax: int, offset: int,
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=xc.device)
     L.call("atx_fakequant_rows", L.ptr(xc), N, K, Lc, L.ptr(scale.contiguous()),
            L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax, offset,
-           L.ptr(mask), L.ptr(xt), Rpad, L.stream_of(xc))
+           L.ptr(mask), L.ptr(xt), Rpad, L.ptr(upper), L.stream_of(xc))
     return mask, (xt, Rpad)
 
 

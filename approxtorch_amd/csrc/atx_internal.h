@@ -49,6 +49,15 @@ inline int elem_grid(long long n, int threads, int cap = 8192) {
   return (int)(b < cap ? b : cap);
 }
 
+// Remainder of v after its truncated bf16 high part h (the bits of v with
+// the low 16 cleared): v - h, exact for finite v.  For +-inf and NaN the
+// high part already is the whole value (inf, or a NaN), so the remainder is
+// 0 instead of the NaN that inf - inf gives.
+__device__ __forceinline__ float bf16_rest(float v) {
+  const float r = v - __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+  return __builtin_isfinite(v) ? r : 0.0f;
+}
+
 // Byte offset of row v in the LUT GEMM's LDS tables (256-byte lines holding
 // row v of four tables; within a table's 64-byte quarter, chunk g of row v
 // sits at position g ^ ((v >> 1) & 3)).

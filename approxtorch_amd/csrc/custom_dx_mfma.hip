@@ -99,8 +99,8 @@ __device__ __forceinline__ void split_parts(const float (&d)[8], u32x4 (&P)[3]) 
   for (int p = 0; p < 4; ++p) {
     const unsigned a = __float_as_uint(d[p]), b = __float_as_uint(d[4 + p]);
     P[0][p] = __builtin_amdgcn_perm(b, a, 0x07060302u);
-    const float ra = d[p] - __uint_as_float(a & 0xffff0000u);
-    const float rb = d[4 + p] - __uint_as_float(b & 0xffff0000u);
+    const float ra = bf16_rest(d[p]);
+    const float rb = bf16_rest(d[4 + p]);
     const unsigned ua = __float_as_uint(ra), ub = __float_as_uint(rb);
     P[1][p] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
     const float la = ra - __uint_as_float(ua & 0xffff0000u);

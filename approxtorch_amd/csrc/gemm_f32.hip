@@ -93,7 +93,7 @@ __device__ __forceinline__ void split4(const float (&v)[4], uint2 (&P)[3]) {
   for (int e = 0; e < 4; ++e) {
     h[e] = __float_as_uint(v[e]);
     if constexpr (FULL) {
-      const float r = v[e] - __uint_as_float(h[e] & 0xffff0000u);
+      const float r = bf16_rest(v[e]);
       m[e] = __float_as_uint(r);
       l[e] = __float_as_uint(r - __uint_as_float(m[e] & 0xffff0000u));
     }
@@ -114,7 +114,7 @@ __device__ __forceinline__ void split4(const float (&v)[4], uint2 (&P)[3]) {
 __device__ __forceinline__ bool split_table(uint2* stab, const float* tab, int t) {
   const float v = tab[t];
   const unsigned u = __float_as_uint(v);
-  const float r = v - __uint_as_float(u & 0xffff0000u);
+  const float r = bf16_rest(v);
   const unsigned ru = __float_as_uint(r);
   const unsigned lo = __float_as_uint(r - __uint_as_float(ru & 0xffff0000u));
   stab[t] = make_uint2((u >> 16) | (ru & 0xffff0000u), lo >> 16);
@@ -126,8 +126,7 @@ __device__ __forceinline__ bool split_table(uint2* stab, const float* tab, int t
 // threads; ends with a barrier).
 __device__ __forceinline__ bool table_exact(const float* tab, int t) {
   const float v = tab[t];
-  const float r = v - __uint_as_float(__float_as_uint(v) & 0xffff0000u);
-  return __syncthreads_or(r != 0.0f) == 0;
+  return __syncthreads_or(bf16_rest(v) != 0.0f) == 0;
 }
 
 // Parts of four table entries (indices into a split table) in split4's order.

@@ -304,6 +304,44 @@ __global__ void tap_window_sum_kernel(const float* __restrict__ partial, atx_con
   }
 }
 
+// The uint8 layer's zero-point position term in backward:
+// pos[n,l] = sum_o coef[o] * go[n,o,l], coef[o] = -((sx * sw[o]) * zw[o])
+// (the fp32 products of -(scale_x * scale_w) * zero_w).  A block owns P
+// positions of one image (blockIdx.y) and G channel groups (P * G = 256):
+// thread (p, gi) sums the channels gi, gi + G, ... of position p (loads of
+// P consecutive positions per channel are coalesced), then the G partials
+// are combined in a fixed order through LDS, so results are identical run to
+// run.  P = 64 for L >= 64, else 16 (small images: more channel groups).
+template <int P>
+__global__ void __launch_bounds__(256)
+channel_dot_kernel(const float* __restrict__ go, int O, int L, const float* __restrict__ sx,
+                   const float* __restrict__ sw, const float* __restrict__ zw,
+                   float* __restrict__ pos) {
+  constexpr int G = 256 / P;
+  __shared__ float part[G][P];
+  const int p = threadIdx.x % P, gi = threadIdx.x / P;
+  const int l = blockIdx.x * P + p;
+  const long long n = blockIdx.y;
+  const float s = sx[0];
+  float acc = 0.0f;
+  if (l < L) {
+    const float* src = go + n * O * L + l;
+#pragma unroll 4
+    for (int o = gi; o < O; o += G) {
+      const float c = -((s * sw[o]) * zw[o]);
+      acc += c * src[(long long)o * L];
+    }
+  }
+  part[gi][p] = acc;
+  __syncthreads();
+  if (gi == 0 && l < L) {
+    float t = part[0][p];
+#pragma unroll
+    for (int j = 1; j < G; ++j) t += part[j][p];
+    pos[n * L + l] = t;
+  }
+}
+
 // Backward of tap_sum: img_grad[n,c,h,w] = sum of go[n,l] over the taps
 // (kh, kw) that read (h, w) (independent of c).
 __global__ void tap_sum_bwd_kernel(const float* __restrict__ go, atx_conv_geom g,
@@ -489,6 +527,23 @@ int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img, hipStream_t st
   hipLaunchKernelGGL(tap_sum_bwd_kernel, dim3(elem_grid(total, TB)), dim3(TB), 0, stream, go, g,
                      img);
   return check_launch("tap_sum_bwd_kernel");
+}
+
+int atx_zero_point_pos(const float* go, int N, int O, int L, const float* scale_x,
+                       const float* scale_w, const float* zero_w, float* pos,
+                       hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && O >= 0 && L >= 0, "atx_zero_point_pos: negative size");
+  if ((long long)N * L == 0) return ATX_OK;
+  ATX_REQUIRE(pos && scale_x && (O == 0 || (go && scale_w && zero_w)),
+              "atx_zero_point_pos: null pointer");
+  ATX_REQUIRE(N <= 65535, "atx_zero_point_pos: N must be at most 65535");
+  if (L >= 64)
+    hipLaunchKernelGGL(channel_dot_kernel<64>, dim3((unsigned)cdiv(L, 64), (unsigned)N),
+                       dim3(256), 0, stream, go, O, L, scale_x, scale_w, zero_w, pos);
+  else
+    hipLaunchKernelGGL(channel_dot_kernel<16>, dim3((unsigned)cdiv(L, 16), (unsigned)N),
+                       dim3(256), 0, stream, go, O, L, scale_x, scale_w, zero_w, pos);
+  return check_launch("channel_dot_kernel");
 }
 
 int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const float* scale,

@@ -142,11 +142,13 @@ __global__ void lut_prepare_kernel(const float* __restrict__ lut,
 template <typename T>
 __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
                               int offset, uint8_t* __restrict__ xq,
-                              uint16_t* __restrict__ xt, int Rpad, bool vec) {
+                              uint16_t* __restrict__ xt, int Rpad, bool vec,
+                              int* __restrict__ upper) {
   const int R = N * L;
   const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
   const int qstride = gridDim.x * blockDim.x;
   const int nquad = Rpad >> 2;
+  bool low = false;             // some index of rows < R and taps < K is < 128
   for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
     const int k = operand_tap(slot, q0 << 2);
     uint16_t* dst = xt + (long long)slot * Rpad;
@@ -187,10 +189,15 @@ __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
       }
       unsigned off[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) off[e] = (any && r0 + e < R) ? row_offset(v[e]) : 0u;
+      for (int e = 0; e < 4; ++e) {
+        const bool live = any && r0 + e < R;
+        off[e] = live ? row_offset(v[e]) : 0u;
+        low |= live && v[e] < 128u;
+      }
       *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
     }
   }
+  if (upper && low) upper[0] = 0;        // benign race: every writer stores 0
 }
 
 // u8 row operand with one quad of rows and one quad of slots per thread
@@ -199,7 +206,7 @@ __global__ void pack_x_kernel(const T* __restrict__ x, int N, int K, int L,
 // written as four 8-byte pieces, so every thread moves 16 elements.
 __global__ void __launch_bounds__(256)
 pack_x_u8_quads_kernel(const uint8_t* __restrict__ x, int N, int K, int L,
-                       uint16_t* __restrict__ xt, int Rpad, bool vec) {
+                       uint16_t* __restrict__ xt, int Rpad, bool vec, int* __restrict__ upper) {
   const int q = blockIdx.x * 256 + threadIdx.x;
   if (q >= (Rpad >> 2)) return;
   const int R = N * L;
@@ -235,16 +242,22 @@ pack_x_u8_quads_kernel(const uint8_t* __restrict__ x, int N, int K, int L,
     }
   }
   uint16_t* dst = xt + (long long)k4 * Rpad + r0;
+  bool low = false;             // some index of rows < R and taps < K is < 128
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int k = k4 | ((q + u) & 3);
     unsigned off[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      off[e] = (k < K && ((valid >> e) & 1u)) ? row_offset((v[u] >> (8 * e)) & 255u) : 0u;
+    for (int e = 0; e < 4; ++e) {
+      const bool live = k < K && ((valid >> e) & 1u);
+      const unsigned idx = (v[u] >> (8 * e)) & 255u;
+      off[e] = live ? row_offset(idx) : 0u;
+      low |= live && idx < 128u;
+    }
     *(uint2*)(dst + (long long)u * Rpad) =
         make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
   }
+  if (upper && low) upper[0] = 0;        // benign race: every writer stores 0
 }
 
 // Strided operands of the plain (torch.mm-layout) LUT GEMM.  Row operand:
@@ -255,10 +268,12 @@ pack_x_u8_quads_kernel(const uint8_t* __restrict__ x, int N, int K, int L,
 template <typename T>
 __global__ void pack_rows_strided_kernel(const T* __restrict__ x, int R, int K, long long sr,
                                          long long sk, int offset, uint8_t* __restrict__ xq,
-                                         uint16_t* __restrict__ xt, int Rpad) {
+                                         uint16_t* __restrict__ xt, int Rpad,
+                                         int* __restrict__ upper) {
   const int q0 = blockIdx.x * blockDim.x + threadIdx.x;
   const int qstride = gridDim.x * blockDim.x;
   const int nquad = Rpad >> 2;
+  bool low = false;             // some index of rows < R and taps < K is < 128
   for (int slot = blockIdx.y; slot < operand_rows(K); slot += gridDim.y) {
     const int k = operand_tap(slot, q0 << 2);
     uint16_t* dst = xt + (long long)slot * Rpad;
@@ -275,12 +290,14 @@ __global__ void pack_rows_strided_kernel(const T* __restrict__ x, int R, int K, 
             else v = (unsigned)x[r * sr + k * sk];
             if (xq) xq[(long long)r * K + k] = (uint8_t)v;
             off[e] = row_offset(v);
+            low |= v < 128u;
           }
         }
       }
       *(uint2*)(dst + r0) = make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
     }
   }
+  if (upper && low) upper[0] = 0;        // benign race: every writer stores 0
 }
 
 template <typename T>
@@ -1050,7 +1067,7 @@ int atx_lut_prepare(const float* lut, uint16_t* out16t, float* outf32t,
 }
 
 int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
-                   uint16_t* xt, int Rpad, hipStream_t stream) {
+                   uint16_t* xt, int Rpad, int* upper, hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_pack_x_f32: negative size");
   ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
               "atx_pack_x_f32: Rpad must be a multiple of %d covering N*L", RT);
@@ -1061,12 +1078,12 @@ int atx_pack_x_f32(const float* x, int N, int K, int L, int offset, uint8_t* xq,
             (unsigned)std::min(operand_rows(K), 65535));
   const bool vec = L % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)xq % 4 == 0;
   hipLaunchKernelGGL(pack_x_kernel<float>, grid, dim3(256), 0, stream, x, N, K, L,
-                     offset, xq, xt, Rpad, vec);
+                     offset, xq, xt, Rpad, vec, upper);
   return check_launch("pack_x_kernel<float>");
 }
 
 int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad,
-                  hipStream_t stream) {
+                  int* upper, hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_pack_x_u8: negative size");
   ATX_REQUIRE(Rpad >= (long long)N * L && Rpad % RT == 0,
               "atx_pack_x_u8: Rpad must be a multiple of %d covering N*L", RT);
@@ -1076,7 +1093,7 @@ int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L, uint16_t* xt, int Rpad
   const dim3 grid((unsigned)cdiv(Rpad / 4, 256), (unsigned)(operand_rows(K) / 4));
   const bool vec = L % 4 == 0 && (uintptr_t)xq % 4 == 0;
   hipLaunchKernelGGL(pack_x_u8_quads_kernel, grid, dim3(256), 0, stream, xq, N, K, L, xt, Rpad,
-                     vec);
+                     vec, upper);
   return check_launch("pack_x_u8_quads_kernel");
 }
 
@@ -1106,7 +1123,8 @@ int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
 }
 
 int atx_pack_rows_strided(const void* x, int dtype, int R, int K, long long sr, long long sk,
-                          int offset, uint8_t* xq, uint16_t* xt, int Rpad, hipStream_t stream) {
+                          int offset, uint8_t* xq, uint16_t* xt, int Rpad, int* upper,
+                          hipStream_t stream) {
   ATX_REQUIRE(R >= 0 && K >= 0 && (dtype == 0 || dtype == 1),
               "atx_pack_rows_strided: bad arguments");
   ATX_REQUIRE(Rpad >= R && Rpad % RT == 0,
@@ -1117,10 +1135,10 @@ int atx_pack_rows_strided(const void* x, int dtype, int R, int K, long long sr, 
             (unsigned)std::min(operand_rows(K), 65535));
   if (dtype == 0)
     hipLaunchKernelGGL(pack_rows_strided_kernel<float>, grid, dim3(256), 0, stream,
-                       (const float*)x, R, K, sr, sk, offset, xq, xt, Rpad);
+                       (const float*)x, R, K, sr, sk, offset, xq, xt, Rpad, upper);
   else
     hipLaunchKernelGGL(pack_rows_strided_kernel<uint8_t>, grid, dim3(256), 0, stream,
-                       (const uint8_t*)x, R, K, sr, sk, 0, xq, xt, Rpad);
+                       (const uint8_t*)x, R, K, sr, sk, 0, xq, xt, Rpad, upper);
   return check_launch("pack_rows_strided_kernel");
 }
 

@@ -41,11 +41,13 @@ __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
                                      const float* __restrict__ scale,
                                      const float* __restrict__ zero, float qmin,
                                      float qmax, float* __restrict__ q,
-                                     uint8_t* __restrict__ mask, uint8_t* __restrict__ q8) {
+                                     uint8_t* __restrict__ mask, uint8_t* __restrict__ q8,
+                                     int* __restrict__ nonneg) {
   const float s = fmaxf(scale[0], 1e-12f);
   const bool asym = zero != nullptr;
   const float z = asym ? zero[0] : 0.0f;
   const long long stride = (long long)gridDim.x * blockDim.x;
+  bool neg = false;           // some quantized value < 0 (NaN counts as 0)
   if constexpr (VEC) {
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < (n >> 2);
          i += stride) {
@@ -59,6 +61,7 @@ __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
         r[e] = fake_quant(xv[e], s, z, asym, qmin, qmax, m);
         mk |= (m ? 1u : 0u) << (8 * e);
         b8 |= ((unsigned)to_int(r[e]) & 255u) << (8 * e);
+        neg |= r[e] < 0.0f;
       }
       if (q) ((float4*)q)[i] = make_float4(r[0], r[1], r[2], r[3]);
       if (mask) ((unsigned*)mask)[i] = mk;
@@ -71,8 +74,10 @@ __global__ void fakequant_fwd_kernel(const float* __restrict__ x, long long n,
       if (q) q[i] = r;
       if (mask) mask[i] = m;
       if (q8) q8[i] = (uint8_t)to_int(r);
+      neg |= r < 0.0f;
     }
   }
+  if (nonneg && neg) nonneg[0] = 0;      // benign race: every writer stores 0
 }
 
 // Fake-quant of a 1x1, stride-1, unpadded conv's input x [N,K,L] straight
@@ -91,7 +96,7 @@ __global__ void __launch_bounds__(EW)
 fakequant_rows_kernel(const float* __restrict__ x, int N, int K, int L,
                       const float* __restrict__ scale, const float* __restrict__ zero,
                       float qmin, float qmax, int offset, uint8_t* __restrict__ mask,
-                      uint16_t* __restrict__ xt, int Rpad) {
+                      uint16_t* __restrict__ xt, int Rpad, int* __restrict__ upper) {
   const int q = blockIdx.x * EW + threadIdx.x;
   if (q >= (Rpad >> 2)) return;
   const float s = fmaxf(scale[0], 1e-12f);
@@ -133,6 +138,7 @@ fakequant_rows_kernel(const float* __restrict__ x, int N, int K, int L,
     }
   }
   uint16_t* dst = xt + (long long)k4 * Rpad + r0;
+  bool low = false;           // some written index < 128
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int k = k4 | ((q + u) & 3);
@@ -143,7 +149,9 @@ fakequant_rows_kernel(const float* __restrict__ x, int N, int K, int L,
       bool m;
       const float r = fake_quant(v[u][e], s, z, asym, qmin, qmax, m);
       const unsigned idx = (unsigned)(to_int(r) + offset) & 255u;
-      off[e] = (k < K && ((valid >> e) & 1u)) ? row_offset(idx) : 0u;
+      const bool live = k < K && ((valid >> e) & 1u);
+      off[e] = live ? row_offset(idx) : 0u;
+      low |= live && idx < 128u;
       mk |= (m ? 1u : 0u) << (8 * e);
     }
     *(uint2*)(dst + (long long)u * Rpad) =
@@ -158,6 +166,7 @@ fakequant_rows_kernel(const float* __restrict__ x, int N, int K, int L,
       }
     }
   }
+  if (upper && low) upper[0] = 0;        // benign race: every writer stores 0
 }
 
 // gx = (mask ? go : 0) / s[c], c = (i / inner) % C.
@@ -445,7 +454,7 @@ using namespace atx;
 extern "C" {
 
 int atx_fakequant_fwd(const float* x, long long n, const float* scale, const float* zero,
-                      int qmin, int qmax, float* q, uint8_t* mask, void* q8,
+                      int qmin, int qmax, float* q, uint8_t* mask, void* q8, int* nonneg,
                       hipStream_t stream) {
   ATX_REQUIRE(n >= 0, "atx_fakequant_fwd: negative size");
   ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
@@ -456,17 +465,17 @@ int atx_fakequant_fwd(const float* x, long long n, const float* scale, const flo
   if (vec)
     hipLaunchKernelGGL(fakequant_fwd_kernel<true>, dim3(elem_grid(n / 4, EW)), dim3(EW), 0,
                        stream, x, n, scale, zero, (float)qmin, (float)qmax, q, mask,
-                       (uint8_t*)q8);
+                       (uint8_t*)q8, nonneg);
   else
     hipLaunchKernelGGL(fakequant_fwd_kernel<false>, dim3(elem_grid(n, EW)), dim3(EW), 0,
                        stream, x, n, scale, zero, (float)qmin, (float)qmax, q, mask,
-                       (uint8_t*)q8);
+                       (uint8_t*)q8, nonneg);
   return check_launch("fakequant_fwd_kernel");
 }
 
 int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
                        const float* zero, int qmin, int qmax, int offset, uint8_t* mask,
-                       uint16_t* xt, int Rpad, hipStream_t stream) {
+                       uint16_t* xt, int Rpad, int* upper, hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0, "atx_fakequant_rows: negative size");
   ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
   ATX_REQUIRE(offset == 0 || offset == 128, "atx_fakequant_rows: offset must be 0 or 128");
@@ -481,10 +490,10 @@ int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
   const bool vec = L % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)mask & 3) == 0;
   if (vec)
     hipLaunchKernelGGL(fakequant_rows_kernel<true>, grid, dim3(EW), 0, stream, x, N, K, L,
-                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad);
+                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad, upper);
   else
     hipLaunchKernelGGL(fakequant_rows_kernel<false>, grid, dim3(EW), 0, stream, x, N, K, L,
-                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad);
+                       scale, zero, (float)qmin, (float)qmax, offset, mask, xt, Rpad, upper);
   return check_launch("fakequant_rows_kernel");
 }
 

@@ -157,7 +157,10 @@ class Conv2d_int8(nn.Module):
         The absmax reduction and the EMA run on the device; under DDP the
         statistic is MAX-all-reduced in between so every rank's scale agrees.
         Returns a device int32 flag, set when x >= 0 everywhere (the LUT GEMM
-        of this forward may then build half-height tables), or None."""
+        of this forward may then build half-height tables), or None.  x >= 0
+        means every quantized x >= 0 only because the fake-quant divides by
+        max(scale_x, 1e-12) > 0 (whatever scale_x holds) and qmax >= 0;
+        conv2d_int8_fused checks the latter."""
         _check_stat_inputs(x, ("scale_x", self.scale_x))
         with torch.no_grad():
             xc = x.contiguous()

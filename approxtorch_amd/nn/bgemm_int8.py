@@ -236,17 +236,24 @@ class _conv2d_int8_fused(Function):
         # fake-quant writes the row-offset operand directly, no byte image
         pointwise = (not depthwise and g.KH == 1 and g.KW == 1 and g.SH == 1 and g.SW == 1
                      and g.PH == 0 and g.PW == 0)
+        # weight_bits <= 4: indices w + 128 in [120, 136), matrix-core LUT GEMM
+        wbase = 120 if qmax_w <= 7 else None
+        # Without a flag from the statistic (eval mode, data parallel training)
+        # the fake-quant reports whether every quantized x is >= 0 (LUT index
+        # >= 128, the im2col's padding index included) for the LUT GEMM's
+        # upper-half tables; only the gather kernel reads it.
+        fq_flag = None
+        if x_upper is None and not depthwise and wbase is None:
+            x_upper = fq_flag = ops.upper_flag(x.device)
         if pointwise:
-            mask_x, xt_rpad = ops.fakequant_rows(x, scale_x, qmin, qmax, 128)
+            mask_x, xt_rpad = ops.fakequant_rows(x, scale_x, qmin, qmax, 128, upper=fq_flag)
         else:
             _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
-                                                      q8_dtype=torch.int8)
+                                                      q8_dtype=torch.int8, nonneg=fq_flag)
         _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, -qmax_w, qmax_w,
                                                             offset=128,
                                                             want_wt=not depthwise)
         b = None if bias is None else bias.detach().contiguous()
-        # weight_bits <= 4: indices w + 128 in [120, 136), matrix-core LUT GEMM
-        wbase = 120 if qmax_w <= 7 else None
         if pointwise:
             y, _ = ops.conv_forward_rows(xt_rpad, wq, lut, g, 128,
                                          out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
@@ -301,7 +308,13 @@ def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin
                       qmax_w, x_upper=None):
     """x_upper: optional device int32 flag, written for this same x, that is
     nonzero only when x >= 0 everywhere (Conv2d_int8's training-mode statistic,
-    atx_absmax_ema_upper); the LUT GEMM then builds half-height tables."""
+    atx_absmax_ema_upper); the LUT GEMM then builds half-height tables.  The
+    promise x >= 0 => every quantized x >= 0 holds because the fake-quant
+    divides by max(scale_x, 1e-12) > 0 and qmax >= 0.  Without it, the
+    fake-quant writes such a flag from the quantized values themselves."""
+    if qmax < 0 or qmin > qmax:
+        raise RuntimeError(f"qmin/qmax must satisfy qmin <= qmax and qmax >= 0, got "
+                           f"[{qmin}, {qmax}]")
     return _conv2d_int8_fused.apply(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom,
                                     qmin, qmax, qmax_w, x_upper)
 

@@ -283,9 +283,9 @@ class _conv2d_uint8_fused(Function):
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         need_b = ctx.has_bias and ctx.needs_input_grad[2]
         gx = gw = gb = None
-        # zero-point terms: -sum_o g' z_w[o] per position (a [1 x O] by [O x L]
-        # product per image) and -z_x sum_{n,l} g' per channel
-        gxs = torch.matmul((c * zw).neg_().view(1, O), go).view(g.N, Lc) if need_x else None
+        # zero-point terms: -sum_o g' z_w[o] per position (a channel reduction
+        # per image) and -z_x sum_{n,l} g' per channel
+        gxs = ops.zero_point_pos(go, sx, sw, zw) if need_x else None
         gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
         if ctx.kind == 'custom':
             grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, go, tx if need_x else None,

@@ -47,7 +47,9 @@ typedef struct atx_conv_geom {
 /* ABI version, returned by atx_version().  2: atx_gemm_epilogue carries
  * its own size (first field) and the x_upper flag; atx_custom_grad_dx/dw
  * take the dy_scale and dx/dw table arguments below and atx_tap_sum its
- * workspace.  Version 1 callers must be rebuilt against this header. */
+ * workspace; atx_fakequant_fwd/rows and the row packers (atx_pack_x_f32/u8,
+ * atx_pack_rows_strided) take a nullable upper-half flag.  Version 1
+ * callers must be rebuilt against this header. */
 #define ATX_ABI_VERSION 2
 
 const char* atx_last_error(void);
@@ -78,14 +80,18 @@ int atx_lut_prepare(const float* lut, uint16_t* out16t, float* outf32t,
 
 /* x fp32 [N,K,L] holding quantized integer values -> xq uint8 [N,K,L]
  * (LUT index clamp(rint(v) + offset, 0, 255), nullable) and the row-offset
- * operand xt [Kpad][Rpad].  Replaces quantize_to_u8_kernel
- * (csrc/claude/bgemm_lut_kernels.cuh:62-97) for the x operand. */
+ * operand xt [Kpad][Rpad].  upper (nullable, here and in the other row
+ * packers): a device int the caller sets nonzero beforehand, cleared when an
+ * index written for rows below N*L and taps below K is under 128; nonzero
+ * afterwards, it is the promise atx_gemm_epilogue.x_upper takes for xt.
+ * Replaces quantize_to_u8_kernel (csrc/claude/bgemm_lut_kernels.cuh:62-97)
+ * for the x operand. */
 int atx_pack_x_f32(const float* x, int N, int K, int L, int offset,
-                   uint8_t* xq, uint16_t* xt, int Rpad, hipStream_t stream);
+                   uint8_t* xq, uint16_t* xt, int Rpad, int* upper, hipStream_t stream);
 
 /* x uint8 [N,K,L] (already LUT indices) -> row-offset operand xt. */
 int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L,
-                  uint16_t* xt, int Rpad, hipStream_t stream);
+                  uint16_t* xt, int Rpad, int* upper, hipStream_t stream);
 
 /* w fp32 [O,K] quantized values -> wq uint8 [O,K] (LUT index, nullable) and
  * the transposed, column-padded operand wt uint8 [K][Opad] (Opad = O rounded
@@ -107,7 +113,7 @@ int atx_pack_w_u8(const uint8_t* wq, int O, int K, uint8_t* wt, int Opad,
  * csrc/claude/gemm.cu:57-100,128-166. */
 int atx_pack_rows_strided(const void* x, int dtype, int R, int K, long long sr,
                           long long sk, int offset, uint8_t* xq, uint16_t* xt,
-                          int Rpad, hipStream_t stream);
+                          int Rpad, int* upper, hipStream_t stream);
 int atx_pack_cols_strided(const void* y, int dtype, int C, int K, long long sc,
                           long long sk, int offset, uint8_t* yq, uint8_t* wt,
                           int Opad, hipStream_t stream);
@@ -166,7 +172,9 @@ typedef struct atx_gemm_epilogue {
   /* Device int or null, read by atx_lut_gemm / atx_lut_gemm_noalloc at
    * kernel start (atx_lut_gemm_narrow ignores it): nonzero promises that
    * every activation index of the rows below N*L is at least 128, as for the
-   * int8 operand of an x >= 0 (atx_absmax_ema_upper writes such a flag).
+   * int8 operand of an x >= 0 (atx_absmax_ema_upper writes such a flag;
+   * atx_fakequant_fwd / atx_fakequant_rows and the row packers derive one
+   * from the quantized indices themselves).
    * The kernel then builds only rows 128..255 of its tables, half the table
    * work, with the same exact sums; a broken promise gives wrong sums, never
    * an out-of-bounds access.  No counterpart in the reference. */
@@ -237,10 +245,15 @@ int atx_lut_gemm_noalloc(const uint16_t* xt, int Rpad, const uint8_t* wt, int Op
  * qmin, qmax) (NaN passes through), mask = qmin <= v <= qmax on the
  * pre-round v.  zero may be null (symmetric).  q and mask may each be null.
  * q8 (nullable): the same value as a signed/unsigned byte image.
+ * nonneg (nullable): a device int the caller sets nonzero beforehand; the
+ * kernel sets it to 0 when some quantized value is negative (NaN counts as
+ * 0).  For the int8 operand (LUT index q + 128) a nonzero flag afterwards is
+ * the promise atx_gemm_epilogue.x_upper takes; it is a property of the
+ * quantized values themselves, whatever the scale.
  * csrc/claude/quantization.cu:54-75,77-110,148-183 (kernels), 187-311 (host). */
 int atx_fakequant_fwd(const float* x, long long n, const float* scale,
                       const float* zero, int qmin, int qmax, float* q,
-                      uint8_t* mask, void* q8, hipStream_t stream);
+                      uint8_t* mask, void* q8, int* nonneg, hipStream_t stream);
 
 /* The input fake-quant of a 1x1, stride-1, unpadded, ungrouped conv fused
  * with its operand packing: x fp32 [N,K,L] -> mask uint8 [N,K,L] (as
@@ -251,10 +264,14 @@ int atx_fakequant_fwd(const float* x, long long n, const float* scale,
  * atx_im2col_rows of that 1x1 geometry, without the byte image.  Replaces
  * the fake-quant of x (nn/quantization.py:37-62) and the im2col prepass
  * (csrc/claude/bgemm_lre_backward_claude.cu:215-269) of a 1x1 conv in
- * nn/Conv2d_int8.py:192-212. */
+ * nn/Conv2d_int8.py:192-212.  upper (nullable): a device int the caller sets
+ * nonzero beforehand; cleared when some index written for rows below N*L and
+ * taps below K is under 128, so that afterwards it is the promise
+ * atx_gemm_epilogue.x_upper takes for this operand. */
 int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
                        const float* zero, int qmin, int qmax, int offset,
-                       uint8_t* mask, uint16_t* xt, int Rpad, hipStream_t stream);
+                       uint8_t* mask, uint16_t* xt, int Rpad, int* upper,
+                       hipStream_t stream);
 
 /* gx = (mask ? go : 0) / max(scale, 1e-12); scale has 1 (per-tensor) or
  * C (per-channel, channel = (i / inner) % C) elements.
@@ -313,6 +330,16 @@ int atx_tap_sum(const void* img, int dtype, atx_conv_geom g, const float* pad_de
 int atx_tap_sum_bwd(const float* go, atx_conv_geom g, float* img,
                     hipStream_t stream);
 
+/* The backward of the uint8 zero-point term z_w[o] * sum_k q_x at each
+ * output position: pos[n,l] = sum_o -(scale_x * scale_w[o]) * zero_w[o] *
+ * go[n,o,l] (go [N,O,L]), fp32 products in that order, summed in a fixed
+ * order (deterministic).  Its image gradient is atx_tap_sum_bwd /
+ * atx_col2im_pos of pos.  Replaces the [1 x O] by [O x L] product of the
+ * reference's autograd through nn/Conv2d_uint8.py:308-315. */
+int atx_zero_point_pos(const float* go, int N, int O, int L, const float* scale_x,
+                       const float* scale_w, const float* zero_w, float* pos,
+                       hipStream_t stream);
+
 /* --------------------------------------------------------------- EMA stats
  * absmax EMA (nn/Conv2d_int8.py:137-146):
  *   stat = max|x|; scale <- m*(stat/denom) + (1-m)*scale, in fp32 with
@@ -333,8 +360,11 @@ int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32,
 int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_out,
                    float denom, float m32, float om32, float* scale, hipStream_t stream);
 /* atx_absmax_ema that also writes *upper = 1 when min(x) >= 0 (no NaN), else
- * 0: then the int8 fake-quant of x (any positive scale) has every LUT index
- * at or above 128, the promise of atx_gemm_epilogue.x_upper.  Same stat_out
+ * 0: then the int8 fake-quant of x has every LUT index at or above 128, the
+ * promise of atx_gemm_epilogue.x_upper, because the fake-quant divides by
+ * max(scale, 1e-12) > 0 whatever the scale holds and its qmax is >= 0 (a
+ * qmax < 0 would map x >= 0 below index 128: the caller must not use the
+ * flag then).  Same stat_out
  * and scale update as atx_absmax_ema, bit for bit (max |x| is taken as
  * max(-min x, max x)).  No counterpart in the reference; used by the int8
  * layer's training-mode forward (nn/Conv2d_int8.py:137-146). */

@@ -191,3 +191,12 @@ def test_conversion_walk_matches_named_modules_order_and_dedup():
     assert model[3] is shared                              # second path untouched
     assert isinstance(model[5]["a"], Conv2d_int8)
     assert model[4] is inner
+
+
+def test_custom_grad_schemas_name_their_tables_as_the_reference():
+    """bgemm_custom_grad_optimize.cu:591-594 declares dx_lut / dw_lut, so
+    keyword calls through torch.ops.approxtorch work unchanged."""
+    for kind in ("uint8", "int8"):
+        for d in ("dx", "dw"):
+            op = getattr(torch.ops.approxtorch, f"bgemm_custom_grad_{kind}_{d}").default
+            assert [a.name for a in op._schema.arguments] == ["X", "W", "dY", f"{d}_lut"]

@@ -312,7 +312,7 @@ def test_fp32_lut_tiled_kernel(shape):
     xt = torch.zeros((max(LB.operand_rows(K), 1), Rpad), dtype=torch.int16, device=DEV)
     xg = t(xi)
     if K:
-        LB.call("atx_pack_x_u8", LB.ptr(xg), N, K, Lc, LB.ptr(xt), Rpad, LB.stream_of(xg))
+        LB.call("atx_pack_x_u8", LB.ptr(xg), N, K, Lc, LB.ptr(xt), Rpad, None, LB.stream_of(xg))
     _, wt, Opad = ops._pack_w(t(wi), 0)
     lt = t(lut)
     y = torch.full((N, Oc, Lc), float("nan"), device=DEV)
@@ -693,6 +693,25 @@ TAP_GEOMS = [((2, 5, 9, 7), (3, 3), (1, 1), (1, 1), (1, 1)), ((3, 130, 6, 5), (3
              ((4, 3, 16, 16), (7, 7), (2, 2), (3, 3), (1, 1))]
 
 
+@pytest.mark.parametrize("shape", [(2, 37, 100), (3, 1, 64), (5, 200, 49), (1, 3, 7), (4, 2048, 9)])
+def test_zero_point_pos(shape):
+    """atx_zero_point_pos against fp64: pos[n,l] = sum_o -(sx*sw[o])*zw[o]*go[n,o,l]
+    (rel 1e-5 of the sum of |terms| + abs 1e-4), and bitwise equal run to run."""
+    N, Oc, Lc = shape
+    r = gen(zlib.crc32(repr(("zpp", shape)).encode()))
+    go = r.standard_normal(shape).astype(np.float32)
+    sx = np.float32(0.037)
+    sw = (r.random(Oc) * 0.1 + 0.01).astype(np.float32)
+    zw = r.integers(0, 16, Oc).astype(np.float32)
+    coef = -((sx * sw).astype(np.float32) * zw).astype(np.float32)
+    want = np.einsum("o,nol->nl", coef.astype(np.float64), go.astype(np.float64))
+    bound = np.einsum("o,nol->nl", np.abs(coef).astype(np.float64), np.abs(go).astype(np.float64))
+    a = ops.zero_point_pos(t(go), t(np.array(sx)), t(sw), t(zw))
+    b = ops.zero_point_pos(t(go), t(np.array(sx)), t(sw), t(zw))
+    assert torch.equal(a, b)
+    close(a.cpu().numpy(), want, bound)
+
+
 @pytest.mark.parametrize("case", TAP_GEOMS)
 @pytest.mark.parametrize("dtype", ["uint8", "float32"])
 def test_tap_sum_exact(case, dtype):
@@ -858,6 +877,43 @@ def test_conv_backward_kernels(geom):
     ex, ew = O.gemm_grads(go, xi, wi, "lre", (tx, tw))
     close(gi.cpu().numpy(), O.fold(ex, img.shape, k, s, p, d))
     close(gwk.cpu().numpy(), ew)
+
+
+@pytest.mark.parametrize("exact_tables", [False, True])
+def test_conv_backward_non_finite_operands(exact_tables):
+    """+-inf and NaN in the output gradient and in the tables: the bf16-split
+    products give a non-finite result exactly where the fp64 oracle does (the
+    set of non-finite gradients is fp32's), finite ones within the tolerance.
+    Where fp32 gives +-inf, a six-product result may be NaN instead: a part
+    product inf * 0 with a partner whose low bf16 parts are zero."""
+    k, s, p, d = (3, 3), (1, 1), (1, 1), (1, 1)
+    r = gen(57)
+    img = r.integers(-127, 128, (2, 6, 12, 13)).astype(np.int8)
+    Oc, K = 20, 6 * 9
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    go = r.standard_normal((2, Oc, g.OH * g.OW)).astype(np.float32)
+    go[0, 3, 17], go[1, 11, 40], go[1, 5, 99] = np.inf, -np.inf, np.nan
+    if exact_tables:
+        tx = r.integers(-100, 100, 256).astype(np.float32)
+        tw = r.integers(-100, 100, 256).astype(np.float32)
+    else:
+        tx = r.standard_normal(256).astype(np.float32)
+        tw = r.standard_normal(256).astype(np.float32)
+    tx[int(wi[7, 30])] = np.inf
+    tw[200] = -np.inf
+    gi = ops.conv_backward_data(t(go), t(wi), t(tx), g).cpu().numpy()
+    gwk = ops.conv_backward_weight(t(go), t(img), t(tw), g, Oc, 128).cpu().numpy()
+    xi = O.im2col_index(O.image_index(img), k, s, p, d, 128)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ex, ew = O.gemm_grads(go.astype(np.float64), xi, wi, "lre",
+                              (tx.astype(np.float64), tw.astype(np.float64)))
+        exi = O.fold(ex, img.shape, k, s, p, d)
+    for got, want in ((gi, exi), (gwk, ew)):
+        fin = np.isfinite(want)
+        assert (~fin).any() and fin.any()
+        assert np.array_equal(np.isfinite(got), fin)
+        close(got[fin], want[fin])
 
 
 # (image shape, (kernel, stride, padding, dilation), O, image dtype): multi-tile

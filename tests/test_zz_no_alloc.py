@@ -24,7 +24,7 @@ def _operands(seed, N, K, Lc, Oc):
     xt = torch.empty((L.operand_rows(K), Rpad), dtype=torch.int16, device=DEV)
     wt = torch.empty((K, Opad), dtype=torch.uint8, device=DEV)
     s = L.stream_of(xi)
-    L.call("atx_pack_x_u8", xi.data_ptr(), N, K, Lc, xt.data_ptr(), Rpad, s)
+    L.call("atx_pack_x_u8", xi.data_ptr(), N, K, Lc, xt.data_ptr(), Rpad, None, s)
     L.call("atx_pack_w_u8", wi.data_ptr(), Oc, K, wt.data_ptr(), Opad, s)
     sw = torch.as_tensor(r.random(Oc).astype(np.float32) + 0.01, device=DEV)
     sx = torch.tensor(0.0173, device=DEV)
