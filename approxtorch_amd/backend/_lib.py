@@ -60,9 +60,9 @@ _SIGS = {
     "atx_lut_gemm_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp,
                                     c_int, c_int, GemmEpilogue, c_vp, c_vp, c_vp]),
     "atx_fakequant_fwd": (c_int, [c_vp, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
-                                  c_vp]),
+                                  c_vp, c_vp]),
     "atx_fakequant_rows": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_int, c_int,
-                                   c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),
+                                   c_vp, c_vp, c_int, c_vp, c_vp]),
     "atx_fakequant_bwd": (c_int, [c_vp, c_vp, c_ll, c_vp, c_int, c_ll, c_vp, c_vp]),
     "atx_fakequant_channel_fwd": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_int, c_int, c_int,
                                           c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),

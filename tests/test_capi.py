@@ -46,7 +46,7 @@ def test_invalid_arguments_return_einval_without_gpu():
     assert b"negative size" in lib.atx_last_error()
     rc = lib.atx_lut_gemm(None, 100, None, 64, 1, 4, 4, 4, None, None, 0, ep, None, None, None)
     assert rc == -1 and b"Rpad" in lib.atx_last_error()
-    rc = lib.atx_fakequant_fwd(None, 10, None, None, 5, 5, None, None, None, None)
+    rc = lib.atx_fakequant_fwd(None, 10, None, None, 5, 5, None, None, None, None, None)
     assert rc == -1 and b"qmin" in lib.atx_last_error()
     g = L.geom(1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1)
     g.OH = 7
@@ -91,3 +91,23 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         L.load()
+
+
+def header_arities(name="atx.h"):
+    """name -> number of parameters of every function include/<name> declares."""
+    text = open(os.path.join(ROOT, "include", name)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^(?:int|long long|const char\*)\s+(atx_\w+)\(([^)]*)\)", text,
+                         flags=re.M | re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_arities_match_the_header():
+    """Every ctypes signature in backend/_lib.py has as many parameters as the
+    header's declaration (a missing slot would pass the stream as an int)."""
+    arity = header_arities()
+    for name, (_, args) in L._SIGS.items():
+        assert len(args) == arity[name], (name, len(args), arity[name])
