@@ -704,6 +704,14 @@ template <int B, bool VEC, bool SCALED> struct GoCols {
               float, __builtin_amdgcn_raw_buffer_load_b32(res, off[e] + ol, 0, 0));
       }
     }
+    // The last, partial k-tile reads rows o >= O (the next image's), whose
+    // weight planes are zero: zero them here too, so that a non-finite go
+    // there cannot add 0 * inf = NaN.  p0 is the tile start (wave-uniform).
+    if (p0 + 32 > O) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (ob + i >= O) raw[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
   }
   template <bool FULL> __device__ void put(char* s, const uint2*) const {
 #pragma unroll

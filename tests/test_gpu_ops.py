@@ -880,12 +880,17 @@ def test_conv_backward_kernels(geom):
 
 
 @pytest.mark.parametrize("exact_tables", [False, True])
-def test_conv_backward_non_finite_operands(exact_tables):
-    """+-inf and NaN in the output gradient and in the tables: the bf16-split
-    products give a non-finite result exactly where the fp64 oracle does (the
-    set of non-finite gradients is fp32's), finite ones within the tolerance.
-    Where fp32 gives +-inf, a six-product result may be NaN instead: a part
-    product inf * 0 with a partner whose low bf16 parts are zero."""
+@pytest.mark.parametrize("where", ["go", "tables"])
+def test_conv_backward_non_finite_operands(exact_tables, where):
+    """+-inf and NaN in the output gradient, or in the tables, against the
+    fp64 oracle.  Non-finite go: the bf16-split products are non-finite
+    exactly where the oracle is (fp32's set of non-finite gradients).
+    Non-finite table entries: every gradient the oracle makes non-finite is
+    non-finite here too, but a tile's masked contraction terms (go zeroed, the
+    table entry kept) can add 0 * inf = NaN to other gradients of that tile,
+    so only "some gradient is non-finite" is fp32's.  Either way a finite
+    result matches the oracle within the tolerance, and a six-product result
+    may be NaN where fp32 gives +-inf (a part product inf * 0)."""
     k, s, p, d = (3, 3), (1, 1), (1, 1), (1, 1)
     r = gen(57)
     img = r.integers(-127, 128, (2, 6, 12, 13)).astype(np.int8)
@@ -893,27 +898,35 @@ def test_conv_backward_non_finite_operands(exact_tables):
     wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
     g = ops.conv_geom(img.shape, k, s, p, d)
     go = r.standard_normal((2, Oc, g.OH * g.OW)).astype(np.float32)
-    go[0, 3, 17], go[1, 11, 40], go[1, 5, 99] = np.inf, -np.inf, np.nan
     if exact_tables:
         tx = r.integers(-100, 100, 256).astype(np.float32)
         tw = r.integers(-100, 100, 256).astype(np.float32)
     else:
         tx = r.standard_normal(256).astype(np.float32)
         tw = r.standard_normal(256).astype(np.float32)
-    tx[int(wi[7, 30])] = np.inf
-    tw[200] = -np.inf
+    if where == "go":
+        go[0, 3, 17], go[1, 11, 40], go[1, 5, 99] = np.inf, -np.inf, np.nan
+    else:
+        tx[int(wi[7, 30])] = np.inf
+        tw[200] = -np.inf
     gi = ops.conv_backward_data(t(go), t(wi), t(tx), g).cpu().numpy()
     gwk = ops.conv_backward_weight(t(go), t(img), t(tw), g, Oc, 128).cpu().numpy()
     xi = O.im2col_index(O.image_index(img), k, s, p, d, 128)
     with np.errstate(invalid="ignore", over="ignore"):
-        ex, ew = O.gemm_grads(go.astype(np.float64), xi, wi, "lre",
-                              (tx.astype(np.float64), tw.astype(np.float64)))
+        tabs = (tx.astype(np.float64), tw.astype(np.float64))
+        ex, ew = O.gemm_grads(go.astype(np.float64), xi, wi, "lre", tabs)
+        ax, aw = O.gemm_grads(go.astype(np.float64), xi, wi, "lre", tabs, absolute=True)
         exi = O.fold(ex, img.shape, k, s, p, d)
-    for got, want in ((gi, exi), (gwk, ew)):
-        fin = np.isfinite(want)
+        axi = O.fold(ax, img.shape, k, s, p, d)
+    for got, want, bound in ((gi, exi, axi), (gwk, ew, aw)):
+        fin, gfin = np.isfinite(want), np.isfinite(got)
         assert (~fin).any() and fin.any()
-        assert np.array_equal(np.isfinite(got), fin)
-        close(got[fin], want[fin])
+        if where == "go":
+            assert np.array_equal(gfin, fin)
+        else:
+            assert not (gfin & ~fin).any() and (~gfin).any()
+        both = fin & gfin
+        close(got[both], want[both], bound[both])
 
 
 # (image shape, (kernel, stride, padding, dilation), O, image dtype): multi-tile
