@@ -44,6 +44,7 @@ class GemmEpilogue(ctypes.Structure):
 _SIGS = {
     "atx_last_error": (ctypes.c_char_p, []),
     "atx_version": (c_int, []),
+    "atx_set_timing_events": (c_int, [c_vp, c_vp]),
     "atx_lut_prepare": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp]),
     "atx_pack_x_f32": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
     "atx_pack_x_u8": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp]),

@@ -24,9 +24,28 @@ int check_launch(const char* what) {
   return ATX_OK;
 }
 
+// atx_set_timing_events: the pair recorded around the LUT GEMMs' main kernel.
+static thread_local hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;
+
+int timing_mark(bool after, hipStream_t stream) {
+  const hipEvent_t ev = after ? g_ev_after : g_ev_before;
+  if (ev == nullptr) return ATX_OK;
+  const hipError_t e = hipEventRecord(ev, stream);
+  if (e != hipSuccess)
+    return set_error(ATX_ELAUNCH, "hipEventRecord (timing event): %s", hipGetErrorString(e));
+  return ATX_OK;
+}
+
 }  // namespace atx
 
 extern "C" {
 const char* atx_last_error(void) { return atx::g_err; }
 int atx_version(void) { return ATX_ABI_VERSION; }
+int atx_set_timing_events(hipEvent_t before, hipEvent_t after) {
+  if ((before == nullptr) != (after == nullptr))
+    return atx::set_error(ATX_EINVAL, "atx_set_timing_events: pass both events or neither");
+  atx::g_ev_before = before;
+  atx::g_ev_after = after;
+  return ATX_OK;
+}
 }

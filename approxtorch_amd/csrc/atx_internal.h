@@ -16,6 +16,9 @@ int set_error(int code, const char* fmt, ...);
 // Checks the launch that was just issued (hipGetLastError) and converts a
 // failure into ATX_ELAUNCH with the kernel's name in the message.
 int check_launch(const char* what);
+// Records the caller's timing event (atx_set_timing_events) on the stream:
+// `after` false = before the LUT GEMM's main kernel, true = after it.
+int timing_mark(bool after, hipStream_t stream);
 
 inline long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 

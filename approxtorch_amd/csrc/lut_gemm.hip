@@ -1217,8 +1217,11 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
 
   if (lut_class == ATX_LUT_F32) {
     ATX_REQUIRE(lutf32t, "atx_lut_gemm: fp32 class needs the fp32 image");
-    return lut_gemm_f32_tiled(xt, Rpad, wt, Opad, lutf32t, N, K, L, O, ep.out_kind, ep.scale_x,
+    int rc = timing_mark(false, stream);
+    if (rc == ATX_OK)
+      rc = lut_gemm_f32_tiled(xt, Rpad, wt, Opad, lutf32t, N, K, L, O, ep.out_kind, ep.scale_x,
                               ep.scale_w, ep.bias, (float*)y, stream);
+    return rc == ATX_OK ? timing_mark(true, stream) : rc;
   }
   ATX_REQUIRE(lut16t, "atx_lut_gemm: integer class needs the 16-bit image");
   const Plan pl = make_plan(N, K, L, O, KMAX_U16, ws_limit, ep.x_upper != nullptr);
@@ -1249,11 +1252,14 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
       int rc = check_launch("sk_clear_kernel");
       if (rc != ATX_OK) return rc;
     }
+    int rc = timing_mark(false, stream);
+    if (rc != ATX_OK) return rc;
     if (lut_class == ATX_LUT_I16)
       hipLaunchKernelGGL(lut_gemm_kernel<true>, dim3(G), dim3(NT), 0, stream, p);
     else
       hipLaunchKernelGGL(lut_gemm_kernel<false>, dim3(G), dim3(NT), 0, stream, p);
-    int rc = check_launch("lut_gemm_kernel");
+    rc = check_launch("lut_gemm_kernel");
+    if (rc == ATX_OK) rc = timing_mark(true, stream);
     if (rc != ATX_OK || Gt <= 1) return rc;
     hipLaunchKernelGGL(sk_finish_kernel, dim3(Gt - 1), dim3(NT), 0, stream, p);
     return check_launch("sk_finish_kernel");
@@ -1266,13 +1272,16 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
   }
   const long long blocks = (long long)pl.tiles_r * pl.tiles_o * pl.splits;
   ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_lut_gemm: grid too large");
+  int rc = timing_mark(false, stream);
+  if (rc != ATX_OK) return rc;
   if (lut_class == ATX_LUT_I16)
     hipLaunchKernelGGL(lut_gemm_kernel<true>, dim3((unsigned)blocks), dim3(NT), 0,
                        stream, p);
   else
     hipLaunchKernelGGL(lut_gemm_kernel<false>, dim3((unsigned)blocks), dim3(NT), 0,
                        stream, p);
-  int rc = check_launch("lut_gemm_kernel");
+  rc = check_launch("lut_gemm_kernel");
+  if (rc == ATX_OK) rc = timing_mark(true, stream);
   if (rc != ATX_OK || pl.splits == 1) return rc;
   return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream);
 }

@@ -344,11 +344,14 @@ int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
     p.split_stride = numel;
   }
   const int blocks = (int)std::min<long long>(256, ((tiles + 7) / 8) * 8);
+  int rc = timing_mark(false, stream);
+  if (rc != ATX_OK) return rc;
   if (pl.wcn == 1)
     hipLaunchKernelGGL(ohf::onehot_gemm_kernel<1>, dim3(blocks), dim3(ohf::NT), 0, stream, p);
   else
     hipLaunchKernelGGL(ohf::onehot_gemm_kernel<2>, dim3(blocks), dim3(ohf::NT), 0, stream, p);
-  int rc = check_launch("onehot_gemm_kernel");
+  rc = check_launch("onehot_gemm_kernel");
+  if (rc == ATX_OK) rc = timing_mark(true, stream);
   if (rc != ATX_OK || pl.splits == 1) return rc;
   return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream);
 }

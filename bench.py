@@ -40,13 +40,47 @@ LDS_PEAK_GBS = 256 * 256 * 2.4      # GB/s: 256 CUs x 256 B/clk x 2.4 GHz
 VALU_PEAK_GLUT = 256 * 64 * 2.4      # G int32 adds/s: 256 CUs x 64 lanes x 2.4 GHz
 INT8_PEAK_TOPS = 5000.0              # dense int8 MFMA, TOP/s
 COPY_BYTES = 512 << 20               # --calibrate-copy: bytes read and written per copy
-# HBM bytes per lut_gemm_kernel launch from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE (KiB per dispatch, averaged over the launches of a
-# `bench.py --calibrate-copy` run), each divided by what the same counter
-# reads per byte of the 512 MiB copy in that run.  None = not measured.
-# profiles/lut_gemm_hbm_traffic.md holds the counter readings (copy factors:
-# FETCH 0.500, WRITE 1.000).
-GEMM_TRAFFIC = {"c3": 756970866, "c4": 199631659}
+# HBM bytes per LUT GEMM launch come from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes (KiB per dispatch, averaged over the launches of a
+# `bench.py --calibrate-copy` run, each divided by what the same counter reads
+# per byte of the 512 MiB copy of that run), recorded in TRAFFIC_PROFILE
+# together with a hash of the kernel's sources; a figure is used only while
+# those sources are unchanged (otherwise roofline.traffic is null).
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "lut_gemm_hbm_traffic.md")
+KERNEL_SOURCES = ("approxtorch_amd/csrc/lut_gemm.hip", "approxtorch_amd/csrc/lut_gemm_mfma.hip",
+                  "approxtorch_amd/csrc/atx_tiles.h", "approxtorch_amd/csrc/atx_internal.h")
+
+
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) over the LUT GEMM kernels' sources."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(workload):
+    """(bytes per launch, note) from TRAFFIC_PROFILE's table rows
+    `| workload | source hash | read bytes | written bytes | ... |`."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, "no traffic profile"
+    want = kernel_source_hash()
+    stale = None
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == workload and all(c.isdigit() for c in cells[2:4]):
+            if cells[1] == want:
+                return int(cells[2]) + int(cells[3]), (
+                    f"PMC FETCH_SIZE + WRITE_SIZE per launch, kernel sources {want} "
+                    f"({os.path.relpath(TRAFFIC_PROFILE, ROOT)})")
+            stale = cells[1]
+    if stale:
+        return None, f"measured for kernel sources {stale}, not the current {want}"
+    return None, "not measured"
 
 
 def parse():
@@ -57,7 +91,8 @@ def parse():
     ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c4", "c5", "c3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=4)
+    ap.add_argument("--cpu-sample-batch", type=int, default=None,
+                    help="batch of the CPU baseline's training steps (default: c2 4, c4 2, c5 1)")
     ap.add_argument("--probe-lds", action="store_true",
                     help="also measure the LDS read throughput (roofline denominator)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -161,15 +196,38 @@ def bgemm_c3(torch, args):
 
 
 class GemmTimer:
-    """Brackets every atx_lut_gemm launch with events on its stream."""
+    """Times the LUT GEMM's main kernel (lut_gemm_kernel, or onehot_gemm_kernel
+    for weight_bits <= 4) of every LUT GEMM call: HIP events that the library
+    records on the launch stream right before and after that kernel
+    (atx_set_timing_events), and, around the whole call (side launches
+    included: split-K reduce, stream-K clear / finish), torch events."""
 
     def __init__(self):
-        self.events = []
+        import ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")       # the runtime torch already loaded
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                                 ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.pool, self.used = [], 0
+        self.calls = []
         self.macs = 0
         self.active = False
 
+    def _pair(self):
+        import ctypes
+        if self.used == len(self.pool):
+            evs = [ctypes.c_void_p(), ctypes.c_void_p()]
+            for ev in evs:
+                if self.hip.hipEventCreate(ctypes.byref(ev)) != 0:
+                    raise RuntimeError("hipEventCreate failed")
+            self.pool.append(evs)
+        self.used += 1
+        return self.pool[self.used - 1]
+
     def install(self):
         import torch
+        from approxtorch_amd.backend import _lib as L
         from approxtorch_amd.backend import ops
         orig = ops._gemm
         timer = self
@@ -177,18 +235,35 @@ class GemmTimer:
         def timed(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw):
             if not timer.active:
                 return orig(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw)
+            kb, ka = timer._pair()
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            L.call("atx_set_timing_events", kb, ka)
             s.record()
-            r = orig(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw)
+            try:
+                r = orig(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, *a, **kw)
+            finally:
+                L.call("atx_set_timing_events", None, None)
             e.record()
-            timer.events.append((s, e))
+            timer.calls.append((kb, ka, s, e))
             timer.macs += N * K * Lc * O
             return r
         ops._gemm = timed
 
+    def reset(self):
+        self.used, self.calls, self.macs = 0, [], 0
+
     def summary(self):
-        ms = sum(s.elapsed_time(e) for s, e in self.events)
-        return ms, self.macs, len(self.events)
+        """(kernel ms, whole-call ms, LUT-MACs, launches) over the timed calls."""
+        import ctypes
+        kern = call = 0.0
+        ms = ctypes.c_float()
+        for kb, ka, s, e in self.calls:
+            self.hip.hipEventSynchronize(ka)
+            if self.hip.hipEventElapsedTime(ctypes.byref(ms), kb, ka) != 0:
+                raise RuntimeError("hipEventElapsedTime failed (kernel not launched?)")
+            kern += ms.value
+            call += s.elapsed_time(e)
+        return kern, call, self.macs, len(self.calls)
 
 
 def lut_gemm_microbench(torch, reps=5):
@@ -290,25 +365,52 @@ def dwconv_microbench(torch, reps=10):
             "ms_all_layers": round(ms_total, 3)}
 
 
+def cpu_host():
+    """The host the CPU baseline runs on: os.cpu_count(), the torch threads
+    used (torch's default: OMP_NUM_THREADS, the box's CPU share) and the CPU
+    model from /proc/cpuinfo."""
+    import torch
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cores": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "cpu_model": model}
+
+
+def timed_median(fn, runs=3):
+    """One warm-up call, then the median of `runs` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], ts
+
+
 def cpu_baseline(model, cfg, sample_batch):
+    """The same training step with every approximate conv replaced by its
+    torch-CPU twin (oracle/torch_cpu.py) at a bounded batch, one warm-up and
+    the median of three steps."""
     import torch
     from approxtorch_amd import workloads
     from oracle import torch_cpu
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    host = cpu_host()
     cpu_model = torch_cpu.to_cpu_reference(model).train()
     opt = torch.optim.SGD(cpu_model.parameters(), lr=0.01, momentum=0.9)
     g = torch.Generator().manual_seed(1)
     x = torch.randn(sample_batch, 3, cfg["hw"], cfg["hw"], generator=g)
     y = torch.randint(0, cfg["classes"], (sample_batch,), generator=g)
-    t0 = time.perf_counter()
-    workloads.training_step(cpu_model, opt, x, y)
-    dt = time.perf_counter() - t0
-    return {"value": round(sample_batch / dt, 4), "unit": "img/s", "cores": threads,
-            "kind": "port",
-            "sample": f"1 training step of the same model at batch {sample_batch} "
-                      f"(torch-CPU restatement, oracle/torch_cpu.py), {dt:.1f} s, "
-                      f"scaled as img/s"}
+    dt, ts = timed_median(lambda: workloads.training_step(cpu_model, opt, x, y))
+    return {"value": round(sample_batch / dt, 4), "unit": "img/s", **host, "kind": "port",
+            "sample": f"training steps of the same model at batch {sample_batch} "
+                      f"(torch-CPU restatement, oracle/torch_cpu.py): one warm-up, median of "
+                      f"{len(ts)} ({', '.join(f'{t:.2f}' for t in ts)} s), as img/s"}
 
 
 def main():
@@ -336,6 +438,7 @@ def main():
     for _ in range(args.warmup):
         workloads.training_step(model, opt, x, y)
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
     timer.active = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -343,6 +446,7 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     timer.active = False
+    peak_mem = torch.cuda.max_memory_allocated()
     result = {
         "metric": "ResNet-50 224^2 approx-QAT img/s (LUT-MAC/s + % LDS roofline)"
         if name == "c4" else f"{name} approx-QAT img/s",
@@ -363,7 +467,8 @@ def main():
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
                    "forward_lut_macs": macs_fwd},
-        "roofline": roofline(timer, dt, GEMM_TRAFFIC.get(name), narrow=cfg["weight_bits"] <= 4),
+        "roofline": roofline(timer, dt, name, narrow=cfg["weight_bits"] <= 4),
+        "peak_memory_MB": round(peak_mem / 2 ** 20, 1),
     }
     if not args.no_microbench:
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
@@ -372,68 +477,72 @@ def main():
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_sample_batch)
+        batch = args.cpu_sample_batch or {"c2": 4, "c4": 2, "c5": 1}[name]
+        result["cpu_baseline"] = cpu_baseline(model, cfg, batch)
     print(json.dumps(result), flush=True)
 
 
-def roofline(timer, dt, traffic, narrow=False):
-    gemm_ms, gemm_macs, launches = timer.summary()
-    achieved_glut = gemm_macs / (gemm_ms * 1e-3) / 1e9
+def roofline(timer, dt, workload, narrow=False):
+    """The dominant kernel against its roofline: `achieved` = algorithmic
+    bytes (LDS: 2 per LUT-MAC) or ops per launch over the kernel's own average
+    launch time (HIP events around the kernel alone, GemmTimer)."""
+    kern_ms, call_ms, gemm_macs, launches = timer.summary()
+    achieved_glut = gemm_macs / (kern_ms * 1e-3) / 1e9
+    traffic, note = measured_traffic(workload)
+    common = {
+        "traffic": traffic,
+        "traffic_source": note,
+        "lut_mac_per_s_G": round(achieved_glut, 1),
+        "launches": launches,
+        "avg_launch_us": round(kern_ms * 1e3 / max(launches, 1), 2),
+        "avg_call_us_with_side_launches": round(call_ms * 1e3 / max(launches, 1), 2),
+        "share_of_step": round(call_ms / (dt * 1e3), 4),
+    }
     if narrow:
         # weight_bits <= 4: onehot_gemm_kernel on the int8 matrix cores, 16 index
         # slots x 2 byte planes = 32 int8 MACs (64 ops) per LUT-MAC
         return {
-            "kernel": "onehot_gemm_kernel (+ its split-K reduce launches)",
+            "kernel": "onehot_gemm_kernel",
             "bound": "mfma",
             "achieved": round(64 * achieved_glut / 1e3, 1),
             "peak": INT8_PEAK_TOPS,
             "unit": "TOP/s (int8)",
             "frac": round(64 * achieved_glut / 1e3 / INT8_PEAK_TOPS, 4),
-            "traffic": traffic,
-            "lut_mac_per_s_G": round(achieved_glut, 1),
+            **common,
             "mfma_peak_lut_mac_per_s_G": round(INT8_PEAK_TOPS * 1e3 / 64, 1),
-            "launches": launches,
-            "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
-            "share_of_step": round(gemm_ms / (dt * 1e3), 4),
         }
     return {
-        "kernel": "lut_gemm_kernel (+ its split-K reduce / stream-K clear and finish launches)",
+        "kernel": "lut_gemm_kernel",
         "bound": "lds",
         "achieved": round(2 * achieved_glut, 1),
         "peak": round(LDS_PEAK_GBS, 1),
         "unit": "GB/s",
         "frac": round(2 * achieved_glut / LDS_PEAK_GBS, 4),
-        "traffic": traffic,
+        **common,
         "algorithmic_bytes_per_launch": round(2 * gemm_macs / max(launches, 1)),
-        "lut_mac_per_s_G": round(achieved_glut, 1),
         "valu_peak_lut_mac_per_s_G": round(VALU_PEAK_GLUT, 1),
         "valu_frac": round(achieved_glut / VALU_PEAK_GLUT, 4),
-        "launches": launches,
-        "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
-        "share_of_step": round(gemm_ms / (dt * 1e3), 4),
     }
 
 
 def cpu_baseline_c3(torch):
     """torch-CPU unfold-free restatement (index -> take -> int64 sum) of the
-    config-3 BGEMM on a bounded sample: 40960 of the 131072 rows (about 10 s)."""
+    config-3 BGEMM on a bounded sample: 16384 of the 131072 rows, one warm-up
+    and the median of three."""
     from approxtorch_amd import workloads
     from oracle import torch_cpu
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    host = cpu_host()
     g = torch.Generator().manual_seed(3)
-    K, rows = 2304, 40960
+    K, rows = 2304, 16384
     xi = torch.randint(0, 256, (1, K, rows), generator=g, dtype=torch.int64)
     wi = torch.randint(0, 256, (256, K), generator=g, dtype=torch.int64)
     lut = torch.from_numpy(workloads.lut_perturbed(3)).to(torch.int64)
-    t0 = time.perf_counter()
-    torch_cpu.lut_sum(xi, wi, lut)
-    dt = time.perf_counter() - t0
+    dt, ts = timed_median(lambda: torch_cpu.lut_sum(xi, wi, lut))
     macs = K * rows * 256
-    return {"value": round(macs / dt / 1e9, 4), "unit": "GLUT-MAC/s", "cores": threads,
-            "kind": "port",
+    return {"value": round(macs / dt / 1e9, 4), "unit": "GLUT-MAC/s", **host, "kind": "port",
             "sample": f"1 x [{rows} rows x K={K}] times [K x 256] of config 3 "
-                      f"({macs / 1e6:.0f} M LUT-MACs, {dt:.1f} s; oracle/torch_cpu.lut_sum)"}
+                      f"({macs / 1e6:.0f} M LUT-MACs; oracle/torch_cpu.lut_sum): one warm-up, "
+                      f"median of {len(ts)} ({', '.join(f'{t:.2f}' for t in ts)} s)"}
 
 
 def main_c3(torch, args):
@@ -453,7 +562,7 @@ def main_c3(torch, args):
         "data": "synthetic (seeded uniform int8 operands, perturbed-product LUT)",
         "config": {"workload": "c3: LUT-BGEMM B=32 A[4096x2304] W[2304x256] int8",
                    "lut_macs_per_step": macs, "parallelism": "single GPU"},
-        "roofline": roofline(timer, dt, GEMM_TRAFFIC["c3"]),
+        "roofline": roofline(timer, dt, "c3"),
     }
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
@@ -483,17 +592,21 @@ def main_c1(torch, args):
     layer, x = c1_layer(torch)
     layer = layer.cuda().train()
     xg = x.cuda()
+    timer = GemmTimer()
+    timer.install()
     with torch.no_grad():
         layer(xg)                      # sets scale_x from the input (momentum 1)
         layer.eval()
         for _ in range(max(args.warmup, 1)):
             layer(xg)
         torch.cuda.synchronize()
+        timer.active = True
         t0 = time.perf_counter()
         for _ in range(args.steps):
             layer(xg)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
+        timer.active = False
     macs = 8 * 32 * 32 * 64 * 576
     result = {
         "metric": "LUT-MAC/s (G), config 1 (one approximate 3x3 conv 64->64 forward, [8,64,32,32])",
@@ -511,25 +624,19 @@ def main_c1(torch, args):
         "config": {"workload": "c1: Conv2d_int8 3x3 64->64 forward, eval mode, im2col GEMM "
                                "M=8192 N=64 K=576 + dequant", "lut_macs_per_step": macs,
                    "parallelism": "single GPU"},
+        "roofline": roofline(timer, dt, "c1"),
     }
     if not args.no_cpu_baseline:
         from oracle import torch_cpu
-        threads = min(16, os.cpu_count() or 1)
-        torch.set_num_threads(threads)
         cpu_layer = torch_cpu.LUTConv2dCPU(layer).eval()
-        reps = 10
         with torch.no_grad():
-            cpu_layer(x)
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                cpu_layer(x)
-            dtc = (time.perf_counter() - t0) / reps
+            dtc, ts = timed_median(lambda: cpu_layer(x), runs=5)
         result["cpu_baseline"] = {
-            "value": round(macs / dtc / 1e9, 4), "unit": "GLUT-MAC/s", "cores": threads,
+            "value": round(macs / dtc / 1e9, 4), "unit": "GLUT-MAC/s", **cpu_host(),
             "kind": "port",
             "sample": f"the whole config-1 forward (unfold -> int64 LUT index -> take -> "
-                      f"sum -> dequant, oracle/torch_cpu.py), mean of {reps}: "
-                      f"{dtc * 1e3:.0f} ms"}
+                      f"sum -> dequant, oracle/torch_cpu.py): one warm-up, median of "
+                      f"{len(ts)} ({', '.join(f'{t * 1e3:.0f}' for t in ts)} ms)"}
     print(json.dumps(result), flush=True)
 
 

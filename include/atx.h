@@ -55,6 +55,16 @@ typedef struct atx_conv_geom {
 const char* atx_last_error(void);
 int atx_version(void);
 
+/* Measurement hook (no counterpart in the reference; bench.py's kernel
+ * timer): while set on the calling thread, atx_lut_gemm,
+ * atx_lut_gemm_noalloc and atx_lut_gemm_narrow record `before` on their
+ * stream right before their main kernel (lut_gemm_kernel, lut_f32_kernel for
+ * the fp32 class, onehot_gemm_kernel) and `after` right after it, not around
+ * the split-K reduce or stream-K clear / finish launches, so that
+ * hipEventElapsedTime gives that kernel's own duration.  Each call records
+ * the pair again; set both to null to stop.  Both or neither. */
+int atx_set_timing_events(hipEvent_t before, hipEvent_t after);
+
 /* ---------------------------------------------------------------- LUT image
  * Re-encodes an fp32 LUT into the 16-bit transposed image used by the
  * LUT GEMM: out16t[wi * 256 + xi] = low 16 bits of lut[xi * 256 + wi]; also
