@@ -235,3 +235,39 @@ def test_config_full_size_step_properties(name):
     mods = dict(model.named_modules())
     moved = [n for n, w in w0.items() if not torch.equal(w, mods[n].weight.detach())]
     assert len(moved) == len(w0)
+
+
+def test_config1_layer_at_full_size_matches_oracle():
+    """Config 1 at its own size: Conv2d_int8 3x3 64->64 (stride 1, pad 1,
+    kaiming-normal weights, seed 0) with the exact int8 product LUT on
+    x [8,64,32,32] ~ N(0,1); one train-mode forward sets the EMA scale
+    (momentum 1), then the eval-mode forward is checked against the oracle
+    (rel 1e-5 of the sum of |terms| + abs 1e-4) and its integer sums against
+    fp64 conv2d of the quantized operands (the exact LUT)."""
+    import torch.nn as nn
+    from approxtorch_amd.convert_model import convert_model
+    torch.manual_seed(0)
+    conv = nn.Conv2d(64, 64, 3, stride=1, padding=1, bias=False)
+    nn.init.kaiming_normal_(conv.weight)
+    lut = torch.from_numpy(workloads.lut_exact_int8())
+    x = torch.randn(8, 64, 32, 32, generator=torch.Generator().manual_seed(0))
+    layer = convert_model(conv, lut, qtype="int8", ignore_first_conv=False,
+                          scale_momentum=1.0).to(DEV).train()
+    xg = x.to(DEV)
+    with torch.no_grad():
+        layer(xg)
+        layer.eval()
+        y = layer(xg).double().cpu().numpy()
+    sx = np.float32(layer.scale_x.item())
+    sw = layer.scale_w.cpu().numpy()
+    assert sx == np.float32(np.abs(x.numpy()).max() / np.float32(127.0))
+    want, ctx = O.conv_int8_forward(x.numpy(), layer.weight.detach().cpu().numpy(), None,
+                                    workloads.lut_exact_int8(), sx, sw, (3, 3), (1, 1), (1, 1),
+                                    (1, 1))
+    assert np.max(np.abs(y - want) - 1e-5 * ctx["yabs"]) <= 1e-4
+    # exact LUT: the sums are the integer conv of the quantized operands
+    xq = np.clip(np.rint(x.numpy() / max(sx, np.float32(1e-12))), -127, 127)
+    wq = np.clip(np.rint(layer.weight.detach().cpu().numpy() / sw[:, None, None, None]), -127, 127)
+    ref = F.conv2d(torch.from_numpy(xq).double(), torch.from_numpy(wq).double(), padding=1)
+    deq = ref.numpy() * (np.float64(sx) * sw.astype(np.float64))[None, :, None, None]
+    assert np.max(np.abs(y - deq) - 1e-5 * np.abs(deq)) <= 1e-4

@@ -459,3 +459,56 @@ def test_dwconv_oracle_bruteforce_and_ste_autograd(geom):
     (yt * sct * torch.from_numpy(go)).sum().backward()
     assert np.allclose(gx, xt.grad.numpy(), rtol=1e-9, atol=1e-9)
     assert np.allclose(gw, wt.grad.numpy(), rtol=1e-9, atol=1e-9)
+
+
+@pytest.mark.parametrize("h", [1, 2, 5, 32, 100])
+def test_date_boundary_indices(h):
+    """grad_lut.py:82-102 switches from the boundary fallback to the central
+    difference strictly inside (h, 255 - h).  With LUT[a][b] = a^2 the
+    smoothed line inside the window range is a^2 + h(h+1)/3, so the central
+    difference is 2a there, while the fallback is (255^2 - 0) / 255 = 255
+    (the raw ends).  Indices h, h+1, 254-h and 255-h tell the two apart, so
+    an off-by-one in either bound fails; the same along b."""
+    i = np.arange(256, dtype=np.float64)
+    sq = (i * i).astype(np.float32)
+    lut_a = np.repeat(sq[:, None], 256, axis=1)          # varies along a
+    lut_b = np.repeat(sq[None, :], 256, axis=0)          # varies along b
+    ga, _ = O.date_tables(lut_a, h)
+    _, gb = O.date_tables(lut_b, h)
+    for idx in (h, h + 1, 254 - h, 255 - h, 0, 255, 128):
+        inside = h < idx < 255 - h
+        want = 2.0 * idx if inside else 255.0
+        assert np.allclose(ga[idx, :], want, rtol=1e-4), (h, idx, ga[idx, 0], want)
+        assert np.allclose(gb[:, idx], want, rtol=1e-4), (h, idx, gb[0, idx], want)
+
+
+def test_lre_table_roles_with_distinct_slopes():
+    """grad_x reads dx at the weight index and grad_w reads dw at the
+    activation index (NAIVE-README:222-232; grad_lut.py:14-37 fits grad_a per
+    column, grad_b per row).  A LUT linear in x with a per-w slope c(w) plus a
+    per-w offset makes grad_a = c exactly and the true d/dx of the sum
+    sum_o go * c(w[o,k]); a LUT linear in w with slope e(x) gives grad_b = e
+    and d/dw = sum go * e(x).  The slopes differ per index and between the two
+    cases, so a swapped table or a swapped index fails."""
+    r = np.random.default_rng(21)
+    v = np.arange(256, dtype=np.float64) - 128
+    c = r.integers(-9, 10, 256).astype(np.float64)
+    e = r.integers(-9, 10, 256).astype(np.float64)
+    off_w = r.integers(-50, 50, 256).astype(np.float64)
+    off_x = r.integers(-50, 50, 256).astype(np.float64)
+    lut_x = v[:, None] * c[None, :] + off_w[None, :]        # LUT[x][w], linear in x
+    lut_w = v[None, :] * e[:, None] + off_x[:, None]        # linear in w
+    ga, _ = O.lre_tables(lut_x.reshape(-1))
+    _, gb = O.lre_tables(lut_w.reshape(-1))
+    assert np.allclose(ga, c, atol=1e-5) and np.allclose(gb, e, atol=1e-5)
+    xi = r.integers(0, 256, (2, 9, 5), dtype=np.uint8)
+    wi = r.integers(0, 256, (4, 9), dtype=np.uint8)
+    go = r.standard_normal((2, 4, 5))
+    gx, _ = O.gemm_grads(go, xi, wi, "lre", (ga, np.zeros(256)))
+    _, gw = O.gemm_grads(go, xi, wi, "lre", (np.zeros(256), gb))
+    want_x = np.einsum("nol,ok->nkl", go, c[wi.astype(np.int64)])
+    want_w = np.einsum("nol,nkl->ok", go, e[xi.astype(np.int64)])
+    assert np.allclose(gx, want_x, atol=1e-9) and np.allclose(gw, want_w, atol=1e-9)
+    # the roles swapped give something else
+    sx, _ = O.gemm_grads(go, xi, wi, "lre", (gb, np.zeros(256)))
+    assert not np.allclose(sx, want_x)

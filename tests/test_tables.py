@@ -1,7 +1,7 @@
 """LUT files and gradient tables: the native text parser against
 numpy.loadtxt (CPU), and the device LRE / DATE generators against the numpy
-implementations of grad_lut (GPU; DATE bit-exact, LRE to the fp32 rounding
-of an fp64 slope)."""
+implementations of grad_lut and against the oracle's restatement (GPU; DATE
+bit-exact, LRE to the fp32 rounding of an fp64 slope)."""
 import os
 
 import numpy as np
@@ -10,6 +10,7 @@ import torch
 
 from approxtorch_amd import grad_lut, load_lut
 from approxtorch_amd.backend import ops
+from oracle import oracle as O
 
 
 def write(path, text):
@@ -73,7 +74,8 @@ def test_device_lre_tables(name, qtype):
     lut = _luts()[name].astype(np.float32)
     ga, gb = grad_lut.lre(torch.from_numpy(lut).cuda(), qtype)
     wa, wb = grad_lut.lre(lut, qtype)
-    for got, want in ((ga, wa), (gb, wb)):
+    oa, ob = O.lre_tables(lut, qtype)
+    for got, want in ((ga, wa), (gb, wb), (ga, oa), (gb, ob)):
         got = got.cpu().numpy()
         assert got.dtype == np.float32
         # both are an fp64 OLS slope rounded to fp32; the sums' order may move
@@ -90,6 +92,10 @@ def test_device_date_tables_bit_exact(name, h):
     wa, wb = grad_lut.DATE(lut, h)
     assert np.array_equal(ga.cpu().numpy(), wa)
     assert np.array_equal(gb.cpu().numpy(), wb)
+    # and directly against the oracle's loop restatement of grad_lut.py:39-142
+    oa, ob = O.date_tables(lut, h)
+    assert np.array_equal(ga.cpu().numpy(), oa)
+    assert np.array_equal(gb.cpu().numpy(), ob)
 
 
 @pytest.mark.gpu
