@@ -108,6 +108,101 @@ dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pa
   }
 }
 
+// Strip form of dwconv_fwd_kernel for KW == 3, dilation 1 along W, stride
+// SW (1 or 2) along W: a thread owns four consecutive outputs of one output
+// row (a strip; strips index (n, oh, quad of ow) of the channel), decomposes
+// its index once, and per kernel row reads the 3 + 4*SW - SW input bytes its
+// four outputs need once (6 for SW = 1, 9 for SW = 2), then sums each
+// output's taps in the same ascending (i, j) order as dwconv_fwd_kernel
+// (identical results).  With OW % 4 == 0 the strip is stored as one 16-byte
+// vector (`vec`: OW % 4 == 0 and y 16-byte aligned).
+template <typename T, typename ENTRY, bool SIGNED, int SW>
+__global__ void __launch_bounds__(DW_THREADS)
+dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad,
+                        const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
+                        const float* __restrict__ lutf32t, DwEpilogue ep, void* __restrict__ y,
+                        int chunk, bool vec) {
+  constexpr int NX = 3 * SW + 3;           // input columns of a strip (SW*3 + 3)
+  extern __shared__ __align__(16) unsigned char dw_smem[];
+  ENTRY* tab = (ENTRY*)dw_smem;
+  const int c = blockIdx.y;
+  const int KK = g.KH * 3;
+  for (int e = threadIdx.x; e < KK * 256; e += blockDim.x) {
+    const int t = e >> 8, x = e & 255;
+    const unsigned w = wq[(long long)c * KK + t];
+    if constexpr (sizeof(ENTRY) == 4 && !std::is_integral<ENTRY>::value) {
+      tab[e] = lutf32t[w * 256u + x];
+    } else {
+      const unsigned v = lut16t[w * 256u + x];
+      tab[e] = SIGNED ? (int)(short)(unsigned short)v : (int)v;
+    }
+  }
+  __syncthreads();
+  const int L = g.OH * g.OW;
+  float sc = 1.0f, bi = 0.0f;
+  if (ep.out_kind == ATX_OUT_DEQUANT) {
+    sc = ep.sx[0] * ep.sw[c];
+    if (ep.bias) bi = ep.bias[c];
+  }
+  const int Q = (g.OW + 3) >> 2;                 // strips per output row
+  const int S = g.N * g.OH * Q;                  // strips of the channel
+  const int sb = blockIdx.x * chunk, se = min(S, sb + chunk);
+  for (int s = sb + (int)threadIdx.x; s < se; s += blockDim.x) {
+    const int q = s % Q, r = s / Q;
+    const int oh = r % g.OH, n = r / g.OH;
+    const int ow0 = q << 2;
+    const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
+    const int iw0 = ow0 * SW - g.PW;             // first input column of the strip
+    ENTRY acc[4] = {0, 0, 0, 0};
+    for (int i = 0; i < g.KH; ++i) {
+      const int ih = oh * g.SH - g.PH + i * g.DH;
+      const bool hin = (unsigned)ih < (unsigned)g.H;
+      unsigned xi[NX];
+#pragma unroll
+      for (int m = 0; m < NX; ++m) {
+        const int iw = iw0 + m;
+        xi[m] = (hin && (unsigned)iw < (unsigned)g.W)
+                    ? dw_index<T>(plane[(long long)ih * g.W + iw], offset) : (unsigned)pad;
+      }
+      const ENTRY* trow = tab + i * 3 * 256;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[e] += trow[j * 256 + xi[e * SW + j]];
+    }
+    float f[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (ep.out_kind == ATX_OUT_DEQUANT) {
+        const float t = (float)acc[e] * sc;
+        f[e] = ep.bias ? bi + t : t;
+      } else {
+        f[e] = (float)acc[e];
+      }
+    }
+    const long long ybase = ((long long)n * g.C + c) * L + (long long)oh * g.OW + ow0;
+    if (ep.out_kind == ATX_OUT_I32) {
+      int* yo = (int*)y + ybase;
+      if (vec) {
+        *(int4*)yo = make_int4((int)acc[0], (int)acc[1], (int)acc[2], (int)acc[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (ow0 + e < g.OW) yo[e] = (int)acc[e];
+      }
+    } else {
+      float* yo = (float*)y + ybase;
+      if (vec) {
+        *(float4*)yo = make_float4(f[0], f[1], f[2], f[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (ow0 + e < g.OW) yo[e] = f[e];
+      }
+    }
+  }
+}
+
 // gx for one image pixel: taps in ascending (i, j) order.
 __global__ void __launch_bounds__(DW_THREADS)
 dwconv_bwd_data_kernel(const float* __restrict__ go, const uint8_t* __restrict__ wq,
@@ -225,6 +320,31 @@ static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int 
                           const uint8_t* wq, const uint16_t* l16, const float* lf32, int cls,
                           const DwEpilogue& ep, void* y, hipStream_t stream) {
   const int KK = g.KH * g.KW;
+  const size_t smem = (size_t)KK * 256 * 4;
+  const long long strips = (long long)g.N * g.OH * ((g.OW + 3) / 4);
+  if (g.KW == 3 && g.DW == 1 && (g.SW == 1 || g.SW == 2) && strips < 0x7fffffffLL - 65536) {
+    // about 2048 blocks in all, each a run of at least 256 strips (1024
+    // outputs) of one channel, so the channel's table is staged once per run
+    const long long per_c = std::max<long long>(1, cdiv(2048, g.C));
+    const int chunk = (int)std::max<long long>(
+        DW_THREADS, cdiv(cdiv(strips, per_c), DW_THREADS) * DW_THREADS);
+    dim3 grid((unsigned)cdiv(strips, chunk), (unsigned)g.C);
+    const bool vec = (g.OW & 3) == 0 && ((uintptr_t)y & 15) == 0;
+#define ATX_DW_STRIP(E, S, SWV)                                                            \
+  hipLaunchKernelGGL((dwconv_fwd_strip_kernel<T, E, S, SWV>), grid, dim3(DW_THREADS), smem, \
+                     stream, img, g, offset, pad, wq, l16, lf32, ep, y, chunk, vec)
+    if (g.SW == 1) {
+      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, 1);
+      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, 1);
+      else ATX_DW_STRIP(int, false, 1);
+    } else {
+      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, 2);
+      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, 2);
+      else ATX_DW_STRIP(int, false, 2);
+    }
+#undef ATX_DW_STRIP
+    return;
+  }
   // about 2048 blocks in all, each a run of at least 1024 outputs of one
   // channel, so the channel's table is staged once per run
   const long long P = (long long)g.N * g.OH * g.OW;
@@ -232,7 +352,6 @@ static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int 
   const long long chunk = std::min<long long>(
       1LL << 30, std::max<long long>(1024, cdiv(cdiv(P, per_c), DW_THREADS) * DW_THREADS));
   dim3 grid((unsigned)cdiv(P, chunk), (unsigned)g.C);
-  const size_t smem = (size_t)KK * 256 * 4;
   if (cls == ATX_LUT_F32)
     hipLaunchKernelGGL((dwconv_fwd_kernel<T, float, false>), grid, dim3(DW_THREADS), smem,
                        stream, img, g, offset, pad, wq, l16, lf32, ep, y, (int)chunk);

@@ -1054,6 +1054,34 @@ def test_dwconv_fake_int8_claude(geom, dtype):
     assert np.array_equal(y.cpu().numpy().reshape(3, C, -1), want.astype(np.float32))
 
 
+@pytest.mark.parametrize("stride", [1, 2])
+@pytest.mark.parametrize("hw", [(16, 16), (9, 31), (1, 4)])
+def test_dwconv_strips(stride, hw):
+    """The 4-output strip kernel (3-wide kernels, stride 1 or 2 along W):
+    OW a multiple of 4 (16-byte stores), ragged strips, a single row; exact
+    against the per-channel int64 oracle, the int32 output too."""
+    H, W = hw
+    k, s, p, d = (3, 3), (stride, stride), (1, 1), (1, 1)
+    r = gen(zlib.crc32(repr(("strips", stride, hw)).encode()))
+    C = 6
+    img = r.integers(-128, 128, (2, C, H, W)).astype(np.int8)
+    w = r.integers(-128, 128, (C, 9)).astype(np.float32)
+    lut = luts(7)["asym"]
+    y, wq = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
+    xi = O.image_index(img, 128)
+    wi = (w + 128).astype(np.uint8)
+    want = np.concatenate([O.lut_gemm_i64(O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128),
+                                          wi[c:c + 1], lut) for c in range(C)], axis=1)
+    assert np.array_equal(y.cpu().numpy().reshape(2, C, -1), want.astype(np.float32))
+    g = ops.conv_geom(img.shape, k, s, p, d)
+    yi = torch.empty((2, C, g.OH, g.OW), dtype=torch.int32, device=DEV)
+    img16, imgf, cls = ops.lut_image(t(lut, torch.float32))
+    ep = LB.GemmEpilogue(LB.ATX_OUT_I32)
+    LB.call("atx_dwconv_fwd", LB.ptr(t(img)), 0, g, 128, LB.ptr(wq), LB.ptr(img16),
+            LB.ptr(imgf), cls, ep, LB.ptr(yi), LB.stream_of(yi))
+    assert np.array_equal(yi.cpu().numpy().reshape(2, C, -1), want)
+
+
 @pytest.mark.parametrize("lut_name", ["u16_c5", "fp32"])
 def test_dwconv_lut_classes(lut_name):
     r = gen(21)
