@@ -24,6 +24,7 @@
 // fake-quant STE masks fused into the outputs.
 
 #include "atx_internal.h"
+#include "atx_tiles.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -49,6 +50,36 @@ struct DwEpilogue {
   int out_kind; const float* sx; const float* sw; const float* bias;
 };
 
+// Stages the channel's KK table columns tab[t][x] = LUT[x][wi(c, t)]
+// (DW_THREADS == 256 threads, thread = x), eight taps' loads in flight at a
+// time, then a barrier.  wc = the channel's KK weight indices.
+template <typename ENTRY, bool SIGNED>
+__device__ __forceinline__ void stage_tables(ENTRY* tab, const uint8_t* __restrict__ wc, int KK,
+                                             const uint16_t* __restrict__ lut16t,
+                                             const float* __restrict__ lutf32t) {
+  static_assert(DW_THREADS == 256, "one thread per table entry");
+  const unsigned x = threadIdx.x;
+  for (int t0 = 0; t0 < KK; t0 += 8) {
+    ENTRY v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (t0 + u < KK) {
+        const unsigned w = wc[t0 + u];
+        if constexpr (sizeof(ENTRY) == 4 && !std::is_integral<ENTRY>::value) {
+          v[u] = lutf32t[w * 256u + x];
+        } else {
+          const unsigned e = lut16t[w * 256u + x];
+          v[u] = SIGNED ? (int)(short)(unsigned short)e : (int)e;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (t0 + u < KK) tab[(t0 + u) * 256 + x] = v[u];
+  }
+  __syncthreads();
+}
+
 // ENTRY: int (16-bit classes, sign-extended or not) or float (fp32 class).
 template <typename T, typename ENTRY, bool SIGNED>
 __global__ void __launch_bounds__(DW_THREADS)
@@ -60,17 +91,7 @@ dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pa
   ENTRY* tab = (ENTRY*)dw_smem;
   const int c = blockIdx.y;
   const int KK = g.KH * g.KW;
-  for (int e = threadIdx.x; e < KK * 256; e += blockDim.x) {
-    const int t = e >> 8, x = e & 255;
-    const unsigned w = wq[(long long)c * KK + t];
-    if constexpr (sizeof(ENTRY) == 4 && !std::is_integral<ENTRY>::value) {
-      tab[e] = lutf32t[w * 256u + x];
-    } else {
-      const unsigned v = lut16t[w * 256u + x];
-      tab[e] = SIGNED ? (int)(short)(unsigned short)v : (int)v;
-    }
-  }
-  __syncthreads();
+  stage_tables<ENTRY, SIGNED>(tab, wq + (long long)c * KK, KK, lut16t, lutf32t);
   const int L = g.OH * g.OW;
   float sc = 1.0f, bi = 0.0f;
   if (ep.out_kind == ATX_OUT_DEQUANT) {
@@ -115,8 +136,13 @@ dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pa
 // four outputs need once (6 for SW = 1, 9 for SW = 2), then sums each
 // output's taps in the same ascending (i, j) order as dwconv_fwd_kernel
 // (identical results).  With OW % 4 == 0 the strip is stored as one 16-byte
-// vector (`vec`: OW % 4 == 0 and y 16-byte aligned).
-template <typename T, typename ENTRY, bool SIGNED, int SW>
+// vector (`vec`: OW % 4 == 0 and y 16-byte aligned).  WORDS (byte images
+// with W % 4 == 0, PW == 1 and a 4-byte aligned image): a strip row's
+// columns 4q*SW - 1 .. 4q*SW + 3*SW + 1 lie in the three aligned dwords from
+// 4q*SW - 4, read with buffer loads over the whole image (a window before
+// the first or past the last byte reads 0; out-of-image columns take the pad
+// index either way).
+template <typename T, typename ENTRY, bool SIGNED, int SW, bool WORDS>
 __global__ void __launch_bounds__(DW_THREADS)
 dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad,
                         const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
@@ -127,17 +153,7 @@ dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, 
   ENTRY* tab = (ENTRY*)dw_smem;
   const int c = blockIdx.y;
   const int KK = g.KH * 3;
-  for (int e = threadIdx.x; e < KK * 256; e += blockDim.x) {
-    const int t = e >> 8, x = e & 255;
-    const unsigned w = wq[(long long)c * KK + t];
-    if constexpr (sizeof(ENTRY) == 4 && !std::is_integral<ENTRY>::value) {
-      tab[e] = lutf32t[w * 256u + x];
-    } else {
-      const unsigned v = lut16t[w * 256u + x];
-      tab[e] = SIGNED ? (int)(short)(unsigned short)v : (int)v;
-    }
-  }
-  __syncthreads();
+  stage_tables<ENTRY, SIGNED>(tab, wq + (long long)c * KK, KK, lut16t, lutf32t);
   const int L = g.OH * g.OW;
   float sc = 1.0f, bi = 0.0f;
   if (ep.out_kind == ATX_OUT_DEQUANT) {
@@ -147,22 +163,43 @@ dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, 
   const int Q = (g.OW + 3) >> 2;                 // strips per output row
   const int S = g.N * g.OH * Q;                  // strips of the channel
   const int sb = blockIdx.x * chunk, se = min(S, sb + chunk);
+  // WORDS: the image as one buffer (its byte size fits 31 bits, host-checked)
+  const __amdgpu_buffer_rsrc_t imr = buffer_rsrc(
+      img, WORDS ? (int)((long long)g.N * g.C * g.H * g.W) : 0);
   for (int s = sb + (int)threadIdx.x; s < se; s += blockDim.x) {
     const int q = s % Q, r = s / Q;
     const int oh = r % g.OH, n = r / g.OH;
     const int ow0 = q << 2;
-    const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
+    const long long poff = ((long long)n * g.C + c) * g.H * g.W;
+    const T* plane = img + poff;
     const int iw0 = ow0 * SW - g.PW;             // first input column of the strip
     ENTRY acc[4] = {0, 0, 0, 0};
     for (int i = 0; i < g.KH; ++i) {
       const int ih = oh * g.SH - g.PH + i * g.DH;
       const bool hin = (unsigned)ih < (unsigned)g.H;
       unsigned xi[NX];
+      if constexpr (WORDS) {
+        // dwords at byte 4q*SW - 4 + {0, 4, 8} of the row; column iw0 + m is
+        // byte 3 + m of the window (PW == 1)
+        const int wbase = (int)(poff + (long long)ih * g.W) + ow0 * SW - 4;
+        unsigned wd[3];
 #pragma unroll
-      for (int m = 0; m < NX; ++m) {
-        const int iw = iw0 + m;
-        xi[m] = (hin && (unsigned)iw < (unsigned)g.W)
-                    ? dw_index<T>(plane[(long long)ih * g.W + iw], offset) : (unsigned)pad;
+        for (int k = 0; k < 3; ++k)
+          wd[k] = __builtin_amdgcn_raw_buffer_load_b32(imr, wbase + 4 * k, 0, 0);
+#pragma unroll
+        for (int m = 0; m < NX; ++m) {
+          const int iw = iw0 + m;
+          const unsigned b = (wd[(3 + m) >> 2] >> (8 * ((3 + m) & 3))) & 255u;
+          const unsigned v = std::is_same<T, int8_t>::value ? (b ^ 128u) : b;
+          xi[m] = (hin && (unsigned)iw < (unsigned)g.W) ? v : (unsigned)pad;
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < NX; ++m) {
+          const int iw = iw0 + m;
+          xi[m] = (hin && (unsigned)iw < (unsigned)g.W)
+                      ? dw_index<T>(plane[(long long)ih * g.W + iw], offset) : (unsigned)pad;
+        }
       }
       const ENTRY* trow = tab + i * 3 * 256;
 #pragma unroll
@@ -330,18 +367,28 @@ static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int 
         DW_THREADS, cdiv(cdiv(strips, per_c), DW_THREADS) * DW_THREADS);
     dim3 grid((unsigned)cdiv(strips, chunk), (unsigned)g.C);
     const bool vec = (g.OW & 3) == 0 && ((uintptr_t)y & 15) == 0;
-#define ATX_DW_STRIP(E, S, SWV)                                                            \
-  hipLaunchKernelGGL((dwconv_fwd_strip_kernel<T, E, S, SWV>), grid, dim3(DW_THREADS), smem, \
-                     stream, img, g, offset, pad, wq, l16, lf32, ep, y, chunk, vec)
-    if (g.SW == 1) {
-      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, 1);
-      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, 1);
-      else ATX_DW_STRIP(int, false, 1);
-    } else {
-      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, 2);
-      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, 2);
-      else ATX_DW_STRIP(int, false, 2);
+    const bool words = sizeof(T) == 1 && (g.W & 3) == 0 && g.PW == 1 &&
+                       ((uintptr_t)img & 3) == 0 &&
+                       (long long)g.N * g.C * g.H * g.W < 0x7fffffffLL - 64;
+#define ATX_DW_STRIP(E, S, SWV, WV)                                                          \
+  hipLaunchKernelGGL((dwconv_fwd_strip_kernel<T, E, S, SWV, WV>), grid, dim3(DW_THREADS), \
+                     smem, stream, img, g, offset, pad, wq, l16, lf32, ep, y, chunk, vec)
+#define ATX_DW_STRIPS(SWV)                                                                   \
+    if (words) {                                                                             \
+      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, SWV, true);                         \
+      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, SWV, true);                       \
+      else ATX_DW_STRIP(int, false, SWV, true);                                              \
+    } else {                                                                                 \
+      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, SWV, false);                        \
+      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, SWV, false);                      \
+      else ATX_DW_STRIP(int, false, SWV, false);                                             \
     }
+    if (g.SW == 1) {
+      ATX_DW_STRIPS(1)
+    } else {
+      ATX_DW_STRIPS(2)
+    }
+#undef ATX_DW_STRIPS
 #undef ATX_DW_STRIP
     return;
   }

@@ -1055,16 +1055,21 @@ def test_dwconv_fake_int8_claude(geom, dtype):
 
 
 @pytest.mark.parametrize("stride", [1, 2])
-@pytest.mark.parametrize("hw", [(16, 16), (9, 31), (1, 4)])
-def test_dwconv_strips(stride, hw):
+@pytest.mark.parametrize("hw", [(16, 16), (9, 31), (1, 4), (5, 8)])
+@pytest.mark.parametrize("dtype", ["int8", "uint8"])
+def test_dwconv_strips(stride, hw, dtype):
     """The 4-output strip kernel (3-wide kernels, stride 1 or 2 along W):
-    OW a multiple of 4 (16-byte stores), ragged strips, a single row; exact
-    against the per-channel int64 oracle, the int32 output too."""
+    OW a multiple of 4 (16-byte stores), ragged strips, a single row, rows
+    read as aligned dwords (W % 4 == 0); exact against the per-channel int64
+    oracle, the int32 output too."""
     H, W = hw
     k, s, p, d = (3, 3), (stride, stride), (1, 1), (1, 1)
-    r = gen(zlib.crc32(repr(("strips", stride, hw)).encode()))
+    r = gen(zlib.crc32(repr(("strips", stride, hw, dtype)).encode()))
     C = 6
-    img = r.integers(-128, 128, (2, C, H, W)).astype(np.int8)
+    if dtype == "int8":
+        img = r.integers(-128, 128, (2, C, H, W)).astype(np.int8)
+    else:
+        img = r.integers(0, 256, (2, C, H, W)).astype(np.uint8)
     w = r.integers(-128, 128, (C, 9)).astype(np.float32)
     lut = luts(7)["asym"]
     y, wq = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
@@ -1077,8 +1082,9 @@ def test_dwconv_strips(stride, hw):
     yi = torch.empty((2, C, g.OH, g.OW), dtype=torch.int32, device=DEV)
     img16, imgf, cls = ops.lut_image(t(lut, torch.float32))
     ep = LB.GemmEpilogue(LB.ATX_OUT_I32)
-    LB.call("atx_dwconv_fwd", LB.ptr(t(img)), 0, g, 128, LB.ptr(wq), LB.ptr(img16),
-            LB.ptr(imgf), cls, ep, LB.ptr(yi), LB.stream_of(yi))
+    img_d = t(img)
+    LB.call("atx_dwconv_fwd", LB.ptr(img_d), 0 if dtype == "int8" else 1, g, 128, LB.ptr(wq),
+            LB.ptr(img16), LB.ptr(imgf), cls, ep, LB.ptr(yi), LB.stream_of(yi))
     assert np.array_equal(yi.cpu().numpy().reshape(2, C, -1), want)
 
 
