@@ -180,12 +180,17 @@ def upper_flag(device):
     return torch.ones((), dtype=torch.int32, device=device)
 
 
-def _pack_w(w, offset, want_wq=True):
-    """w fp32 [O,K] (quantized values) or uint8 [O,K] indices -> (wq, wt, Opad)."""
+def _pack_w(w, offset, want_wq=True, want_wt=True):
+    """w fp32 [O,K] (quantized values) or uint8 [O,K] indices -> (wq, wt, Opad);
+    want_wt=False (fp32 w) writes wq alone and returns wt None."""
     O, K = w.shape
     Opad = L.round_up(max(O, 1), L.COL_TILE)
-    wt = torch.empty((K, Opad), dtype=torch.uint8, device=w.device)
     s = L.stream_of(w)
+    if not want_wt and w.dtype != torch.uint8:
+        wq = torch.empty((O, K), dtype=torch.uint8, device=w.device)
+        L.call("atx_pack_w_f32", L.ptr(w), O, K, offset, L.ptr(wq), None, Opad, s)
+        return wq, None, Opad
+    wt = torch.empty((K, Opad), dtype=torch.uint8, device=w.device)
     if w.dtype == torch.uint8:
         L.call("atx_pack_w_u8", L.ptr(w), O, K, L.ptr(wt), Opad, s)
         return w, wt, Opad
@@ -496,7 +501,7 @@ def dwconv_fake_int8_claude(x: Tensor, w: Tensor, lut: Tensor, kernel_size, stri
         raise RuntimeError(f"w must have shape [C, kh*kw] = [{g.C}, {g.KH * g.KW}]")
     if g.OH <= 0 or g.OW <= 0:
         raise RuntimeError("empty output geometry")
-    wq, _, _ = _pack_w(w.contiguous(), 128)
+    wq, _, _ = _pack_w(w.contiguous(), 128, want_wt=False)
     return dwconv_forward(x, wq, lut, g, 128), wq
 
 
@@ -664,7 +669,7 @@ def _weight_index(w: Tensor) -> Tensor:
         return (w.to(torch.int16) + 128).to(torch.uint8).contiguous()
     if w.dtype == torch.float32:
         O, K = w.shape
-        wq, _, _ = _pack_w(w.contiguous(), 128)
+        wq, _, _ = _pack_w(w.contiguous(), 128, want_wt=False)
         return wq
     raise RuntimeError(f"unsupported weight dtype {w.dtype}")
 

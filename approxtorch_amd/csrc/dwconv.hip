@@ -34,6 +34,9 @@ namespace atx {
 constexpr int DW_THREADS = 256;
 constexpr int DW_MAX_TAPS = 64;         // LDS: 64 taps x 256 entries x 4 B = 64 KiB
 constexpr int DW_WSPLIT_ROWS = 4096;    // contraction rows per weight-gradient block
+#ifndef DW_STRIP_GROUP
+#define DW_STRIP_GROUP 2                // strips per in-flight group of the 3x3 strip kernel
+#endif
 
 template <typename T> __device__ __forceinline__ unsigned dw_index(T v, int offset);
 template <> __device__ __forceinline__ unsigned dw_index<int8_t>(int8_t v, int) {
@@ -129,20 +132,54 @@ dwconv_fwd_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pa
   }
 }
 
+// Stores a strip's four sums acc[] at output element ybase (int32, fp32, or
+// dequantized fp32 sc * acc + bi); `left` = outputs left in the row (only
+// min(4, left) are stored).  vec: one 16-byte store (the caller guarantees
+// OW % 4 == 0 and a 16-byte aligned y).
+template <typename ENTRY>
+__device__ __forceinline__ void store_strip(const ENTRY (&acc)[4], const DwEpilogue& ep,
+                                            float sc, float bi, void* __restrict__ y,
+                                            long long ybase, int left, bool vec) {
+  if (ep.out_kind == ATX_OUT_I32) {
+    int* yo = (int*)y + ybase;
+    if (vec) {
+      *(int4*)yo = make_int4((int)acc[0], (int)acc[1], (int)acc[2], (int)acc[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < left) yo[e] = (int)acc[e];
+    }
+    return;
+  }
+  float f[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (ep.out_kind == ATX_OUT_DEQUANT) {
+      const float t = (float)acc[e] * sc;
+      f[e] = ep.bias ? bi + t : t;
+    } else {
+      f[e] = (float)acc[e];
+    }
+  }
+  float* yo = (float*)y + ybase;
+  if (vec) {
+    *(float4*)yo = make_float4(f[0], f[1], f[2], f[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < left) yo[e] = f[e];
+  }
+}
+
 // Strip form of dwconv_fwd_kernel for KW == 3, dilation 1 along W, stride
 // SW (1 or 2) along W: a thread owns four consecutive outputs of one output
 // row (a strip; strips index (n, oh, quad of ow) of the channel), decomposes
-// its index once, and per kernel row reads the 3 + 4*SW - SW input bytes its
-// four outputs need once (6 for SW = 1, 9 for SW = 2), then sums each
+// its index once, and per kernel row reads the 3 + 4*SW - SW input values
+// its four outputs need once (6 for SW = 1, 9 for SW = 2), then sums each
 // output's taps in the same ascending (i, j) order as dwconv_fwd_kernel
 // (identical results).  With OW % 4 == 0 the strip is stored as one 16-byte
-// vector (`vec`: OW % 4 == 0 and y 16-byte aligned).  WORDS (byte images
-// with W % 4 == 0, PW == 1 and a 4-byte aligned image): a strip row's
-// columns 4q*SW - 1 .. 4q*SW + 3*SW + 1 lie in the three aligned dwords from
-// 4q*SW - 4, read with buffer loads over the whole image (a window before
-// the first or past the last byte reads 0; out-of-image columns take the pad
-// index either way).
-template <typename T, typename ENTRY, bool SIGNED, int SW, bool WORDS>
+// vector (`vec`: OW % 4 == 0 and y 16-byte aligned).
+template <typename T, typename ENTRY, bool SIGNED, int SW>
 __global__ void __launch_bounds__(DW_THREADS)
 dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad,
                         const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
@@ -163,43 +200,22 @@ dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, 
   const int Q = (g.OW + 3) >> 2;                 // strips per output row
   const int S = g.N * g.OH * Q;                  // strips of the channel
   const int sb = blockIdx.x * chunk, se = min(S, sb + chunk);
-  // WORDS: the image as one buffer (its byte size fits 31 bits, host-checked)
-  const __amdgpu_buffer_rsrc_t imr = buffer_rsrc(
-      img, WORDS ? (int)((long long)g.N * g.C * g.H * g.W) : 0);
   for (int s = sb + (int)threadIdx.x; s < se; s += blockDim.x) {
     const int q = s % Q, r = s / Q;
     const int oh = r % g.OH, n = r / g.OH;
     const int ow0 = q << 2;
-    const long long poff = ((long long)n * g.C + c) * g.H * g.W;
-    const T* plane = img + poff;
+    const T* plane = img + ((long long)n * g.C + c) * g.H * g.W;
     const int iw0 = ow0 * SW - g.PW;             // first input column of the strip
     ENTRY acc[4] = {0, 0, 0, 0};
     for (int i = 0; i < g.KH; ++i) {
       const int ih = oh * g.SH - g.PH + i * g.DH;
       const bool hin = (unsigned)ih < (unsigned)g.H;
       unsigned xi[NX];
-      if constexpr (WORDS) {
-        // dwords at byte 4q*SW - 4 + {0, 4, 8} of the row; column iw0 + m is
-        // byte 3 + m of the window (PW == 1)
-        const int wbase = (int)(poff + (long long)ih * g.W) + ow0 * SW - 4;
-        unsigned wd[3];
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-          wd[k] = __builtin_amdgcn_raw_buffer_load_b32(imr, wbase + 4 * k, 0, 0);
-#pragma unroll
-        for (int m = 0; m < NX; ++m) {
-          const int iw = iw0 + m;
-          const unsigned b = (wd[(3 + m) >> 2] >> (8 * ((3 + m) & 3))) & 255u;
-          const unsigned v = std::is_same<T, int8_t>::value ? (b ^ 128u) : b;
-          xi[m] = (hin && (unsigned)iw < (unsigned)g.W) ? v : (unsigned)pad;
-        }
-      } else {
-#pragma unroll
-        for (int m = 0; m < NX; ++m) {
-          const int iw = iw0 + m;
-          xi[m] = (hin && (unsigned)iw < (unsigned)g.W)
-                      ? dw_index<T>(plane[(long long)ih * g.W + iw], offset) : (unsigned)pad;
-        }
+      for (int m = 0; m < NX; ++m) {
+        const int iw = iw0 + m;
+        xi[m] = (hin && (unsigned)iw < (unsigned)g.W)
+                    ? dw_index<T>(plane[(long long)ih * g.W + iw], offset) : (unsigned)pad;
       }
       const ENTRY* trow = tab + i * 3 * 256;
 #pragma unroll
@@ -207,36 +223,134 @@ dwconv_fwd_strip_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, 
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[e] += trow[j * 256 + xi[e * SW + j]];
     }
-    float f[4];
+    store_strip(acc, ep, sc, bi, y, ((long long)n * g.C + c) * L + (long long)oh * g.OW + ow0,
+                g.OW - ow0, vec);
+  }
+}
+
+// The strips of dwconv_fwd_strip_kernel for 3x3 kernels (any stride and
+// dilation along H) over a byte image (int8 when INT8, else uint8) that is
+// 4-byte aligned with a byte size that is a multiple of 4 and below 2^31:
+// identical sums, but
+//  - a strip row's NX columns lie in the three aligned dwords from the
+//    dword holding its first column (shift sh = first byte & 3 <= 3,
+//    sh + NX <= 12), read with buffer loads over the whole image, so a row
+//    costs three loads for any W and padding up to 4 (out-of-image columns
+//    take the pad index).  The three loads merge into one 12-byte access:
+//    dwords of it past the image's end read 0, but one starting before the
+//    image (the first plane's top-left strips, window start -4) would read
+//    0 for all three, so such a window is read from byte 0 and moved up one
+//    dword in registers;
+//  - each thread keeps two groups of U strips in flight: the 3 x 3 dwords
+//    of the next group's strips are requested before the current group is
+//    summed, and the first group's before the tables are staged;
+//  - strip positions (q, oh, n) advance by the block's stride incrementally
+//    (one carry each) instead of by division.
+template <int U>
+struct StripGroup {
+  unsigned d[U][3][3];   // [strip][kernel row][dword]
+  int q[U], oh[U], n[U];
+};
+
+template <typename ENTRY, bool SIGNED, bool INT8, int SW, int U>
+__global__ void __launch_bounds__(DW_THREADS)
+dwconv_fwd_strip3_kernel(const uint8_t* __restrict__ img, atx_conv_geom g, int pad,
+                         const uint8_t* __restrict__ wq, const uint16_t* __restrict__ lut16t,
+                         const float* __restrict__ lutf32t, DwEpilogue ep,
+                         void* __restrict__ y, int chunk, bool vec) {
+  constexpr int NX = 3 * SW + 3;
+  constexpr int D = DW_THREADS;
+  extern __shared__ __align__(16) unsigned char dw_smem[];
+  ENTRY* tab = (ENTRY*)dw_smem;
+  const int c = blockIdx.y;
+  const int L = g.OH * g.OW;
+  const int Q = (g.OW + 3) >> 2;                 // strips per output row
+  const int S = g.N * g.OH * Q;                  // strips of the channel
+  const int sb = blockIdx.x * chunk, se = min(S, sb + chunk);
+  const unsigned HW = (unsigned)g.H * (unsigned)g.W;
+  const __amdgpu_buffer_rsrc_t imr = buffer_rsrc(img, (int)((long long)g.N * g.C * HW));
+  // position of strip s = sb + threadIdx.x, and the per-step increments
+  int s = sb + (int)threadIdx.x;
+  int q = s % Q, oh = (s / Q) % g.OH, n = (s / Q) / g.OH;
+  const int dq = D % Q, dr = D / Q, doh = dr % g.OH, dn = dr / g.OH;
+  // first dword of kernel row i of a strip at (q, oh, n): unsigned
+  // arithmetic (a strip before the image wraps to an offset past its end)
+  auto row_byte = [&](int q_, int oh_, int n_, int i) -> unsigned {
+    return ((unsigned)n_ * (unsigned)g.C + (unsigned)c) * HW +
+           (unsigned)(oh_ * g.SH - g.PH + i * g.DH) * (unsigned)g.W +
+           (unsigned)((q_ << 2) * SW - g.PW);
+  };
+  auto fetch = [&](StripGroup<U>& G) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (ep.out_kind == ATX_OUT_DEQUANT) {
-        const float t = (float)acc[e] * sc;
-        f[e] = ep.bias ? bi + t : t;
-      } else {
-        f[e] = (float)acc[e];
+    for (int u = 0; u < U; ++u) {
+      G.q[u] = q; G.oh[u] = oh; G.n[u] = n;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        unsigned a = row_byte(q, oh, n, i) & ~3u;
+        a = (int)a < 0 ? 0u : a;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          G.d[u][i][k] = __builtin_amdgcn_raw_buffer_load_b32(imr, (int)(a + 4u * k), 0, 0);
       }
+      q += dq;
+      const int cq = q >= Q;
+      q -= cq ? Q : 0;
+      oh += doh + cq;
+      const int co = oh >= g.OH;
+      oh -= co ? g.OH : 0;
+      n += dn + co;
     }
-    const long long ybase = ((long long)n * g.C + c) * L + (long long)oh * g.OW + ow0;
-    if (ep.out_kind == ATX_OUT_I32) {
-      int* yo = (int*)y + ybase;
-      if (vec) {
-        *(int4*)yo = make_int4((int)acc[0], (int)acc[1], (int)acc[2], (int)acc[3]);
-      } else {
+  };
+  StripGroup<U> cur, nxt;
+  fetch(cur);
+  stage_tables<ENTRY, SIGNED>(tab, wq + (long long)c * 9, 9, lut16t, lutf32t);
+  float sc = 1.0f, bi = 0.0f;
+  if (ep.out_kind == ATX_OUT_DEQUANT) {
+    sc = ep.sx[0] * ep.sw[c];
+    if (ep.bias) bi = ep.bias[c];
+  }
+  for (; s < se; s += U * D) {
+    const bool more = s + U * D < se;
+    if (more) fetch(nxt);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (ow0 + e < g.OW) yo[e] = (int)acc[e];
-      }
-    } else {
-      float* yo = (float*)y + ybase;
-      if (vec) {
-        *(float4*)yo = make_float4(f[0], f[1], f[2], f[3]);
-      } else {
+    for (int u = 0; u < U; ++u) {
+      if (s + u * D >= se) break;
+      const int q_ = cur.q[u], oh_ = cur.oh[u], n_ = cur.n[u];
+      const int iw0 = (q_ << 2) * SW - g.PW;
+      ENTRY acc[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (ow0 + e < g.OW) yo[e] = f[e];
+      for (int i = 0; i < 3; ++i) {
+        const int ih = oh_ * g.SH - g.PH + i * g.DH;
+        const bool hin = (unsigned)ih < (unsigned)g.H;
+        const unsigned rb = row_byte(q_, oh_, n_, i), sh = rb & 3u;
+        // the window's dwords (a window from byte -4 was read from byte 0)
+        const bool early = (int)(rb & ~3u) < 0;
+        const unsigned w0 = early ? 0u : cur.d[u][i][0];
+        const unsigned w1 = early ? cur.d[u][i][0] : cur.d[u][i][1];
+        const unsigned w2 = early ? cur.d[u][i][1] : cur.d[u][i][2];
+        // columns 0..NX-1 of the row in bytes of e[0..2]
+        unsigned e[3];
+        e[0] = __builtin_amdgcn_alignbyte(w1, w0, sh);
+        e[1] = __builtin_amdgcn_alignbyte(w2, w1, sh);
+        e[2] = w2 >> (8u * sh);
+        unsigned xi[NX];
+#pragma unroll
+        for (int m = 0; m < NX; ++m) {
+          const unsigned b = (e[m >> 2] >> (8 * (m & 3))) & 255u;
+          xi[m] = (hin && (unsigned)(iw0 + m) < (unsigned)g.W) ? (INT8 ? b ^ 128u : b)
+                                                               : (unsigned)pad;
+        }
+        const ENTRY* trow = tab + i * 3 * 256;
+#pragma unroll
+        for (int o = 0; o < 4; ++o)
+#pragma unroll
+          for (int j = 0; j < 3; ++j) acc[o] += trow[j * 256 + xi[o * SW + j]];
       }
+      store_strip(acc, ep, sc, bi, y,
+                  ((long long)n_ * g.C + c) * L + (long long)oh_ * g.OW + (q_ << 2),
+                  g.OW - (q_ << 2), vec);
     }
+    if (more) cur = nxt;
   }
 }
 
@@ -367,22 +481,36 @@ static void launch_dw_fwd(const T* img, const atx_conv_geom& g, int offset, int 
         DW_THREADS, cdiv(cdiv(strips, per_c), DW_THREADS) * DW_THREADS);
     dim3 grid((unsigned)cdiv(strips, chunk), (unsigned)g.C);
     const bool vec = (g.OW & 3) == 0 && ((uintptr_t)y & 15) == 0;
-    const bool words = sizeof(T) == 1 && (g.W & 3) == 0 && g.PW == 1 &&
-                       ((uintptr_t)img & 3) == 0 &&
-                       (long long)g.N * g.C * g.H * g.W < 0x7fffffffLL - 64;
-#define ATX_DW_STRIP(E, S, SWV, WV)                                                          \
-  hipLaunchKernelGGL((dwconv_fwd_strip_kernel<T, E, S, SWV, WV>), grid, dim3(DW_THREADS), \
-                     smem, stream, img, g, offset, pad, wq, l16, lf32, ep, y, chunk, vec)
-#define ATX_DW_STRIPS(SWV)                                                                   \
-    if (words) {                                                                             \
-      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, SWV, true);                         \
-      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, SWV, true);                       \
-      else ATX_DW_STRIP(int, false, SWV, true);                                              \
-    } else {                                                                                 \
-      if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, SWV, false);                        \
-      else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, SWV, false);                      \
-      else ATX_DW_STRIP(int, false, SWV, false);                                             \
+    if constexpr (sizeof(T) == 1) {
+      const long long bytes = (long long)g.N * g.C * g.H * g.W;
+      if (g.KH == 3 && g.PW <= 4 && ((uintptr_t)img & 3) == 0 && (bytes & 3) == 0 &&
+          bytes < 0x7fffffffLL - 64) {
+        constexpr bool I8 = std::is_same<T, int8_t>::value;
+#define ATX_DW_STRIP3(E, S, SWV)                                                           \
+  hipLaunchKernelGGL((dwconv_fwd_strip3_kernel<E, S, I8, SWV, DW_STRIP_GROUP>), grid,   \
+                     dim3(DW_THREADS), smem, stream, (const uint8_t*)img, g, pad, wq, l16, \
+                     lf32, ep, y, chunk, vec)
+#define ATX_DW_STRIP3S(SWV)                                                                \
+        if (cls == ATX_LUT_F32) ATX_DW_STRIP3(float, false, SWV);                          \
+        else if (cls == ATX_LUT_I16) ATX_DW_STRIP3(int, true, SWV);                        \
+        else ATX_DW_STRIP3(int, false, SWV);
+        if (g.SW == 1) {
+          ATX_DW_STRIP3S(1)
+        } else {
+          ATX_DW_STRIP3S(2)
+        }
+#undef ATX_DW_STRIP3S
+#undef ATX_DW_STRIP3
+        return;
+      }
     }
+#define ATX_DW_STRIP(E, S, SWV)                                                              \
+  hipLaunchKernelGGL((dwconv_fwd_strip_kernel<T, E, S, SWV>), grid, dim3(DW_THREADS), smem, \
+                     stream, img, g, offset, pad, wq, l16, lf32, ep, y, chunk, vec)
+#define ATX_DW_STRIPS(SWV)                                                                   \
+    if (cls == ATX_LUT_F32) ATX_DW_STRIP(float, false, SWV);                                 \
+    else if (cls == ATX_LUT_I16) ATX_DW_STRIP(int, true, SWV);                               \
+    else ATX_DW_STRIP(int, false, SWV);
     if (g.SW == 1) {
       ATX_DW_STRIPS(1)
     } else {

@@ -338,7 +338,7 @@ __global__ void pack_w_kernel(const T* __restrict__ w, int O, int K, int offset,
         v = (unsigned)w[src];
       }
     }
-    wt[i] = (uint8_t)v;
+    if (wt) wt[i] = (uint8_t)v;
   }
 }
 
@@ -1104,7 +1104,7 @@ int atx_pack_w_f32(const float* w, int O, int K, int offset, uint8_t* wq,
               "atx_pack_w_f32: Opad must be a multiple of %d covering O", OT);
   if ((long long)K * Opad == 0) return ATX_OK;
   // an empty w (O == 0) only writes the padding columns
-  ATX_REQUIRE(wt && (O == 0 || w), "atx_pack_w_f32: null pointer");
+  ATX_REQUIRE((wt || wq) && (O == 0 || w), "atx_pack_w_f32: null pointer");
   hipLaunchKernelGGL(pack_w_kernel<float>, dim3(elem_grid((long long)K * Opad, 256)),
                      dim3(256), 0, stream, w, O, K, offset, wq, wt, Opad);
   return check_launch("pack_w_kernel<float>");

@@ -138,7 +138,7 @@ def _lut_conv(x, w, lut, g, depthwise):
     """LUT conv of the fp32 fake-quantized image x with fp32 quantized weights
     w [O, K]: (y [N, O, OH*OW], wq)."""
     if depthwise:
-        wq, _, _ = ops._pack_w(w.reshape(g.C, -1).contiguous(), 128)
+        wq, _, _ = ops._pack_w(w.reshape(g.C, -1).contiguous(), 128, want_wt=False)
         return ops.dwconv_forward(x, wq, lut, g, 128).view(g.N, g.C, -1), wq
     return ops.conv_forward(x, w, lut, g, 128, 128)
 

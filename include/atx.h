@@ -103,10 +103,11 @@ int atx_pack_x_f32(const float* x, int N, int K, int L, int offset,
 int atx_pack_x_u8(const uint8_t* xq, int N, int K, int L,
                   uint16_t* xt, int Rpad, int* upper, hipStream_t stream);
 
-/* w fp32 [O,K] quantized values -> wq uint8 [O,K] (LUT index, nullable) and
- * the transposed, column-padded operand wt uint8 [K][Opad] (Opad = O rounded
- * up to ATX_COL_TILE; padding columns hold index 0).  Replaces the weight
- * prepass of csrc/claude/bgemm_float_claude.cu:108-130. */
+/* w fp32 [O,K] quantized values -> wq uint8 [O,K] (LUT index) and the
+ * transposed, column-padded operand wt uint8 [K][Opad] (Opad = O rounded up
+ * to ATX_COL_TILE; padding columns hold index 0); either output may be NULL,
+ * not both (the depthwise conv needs wq alone).  Replaces the weight prepass
+ * of csrc/claude/bgemm_float_claude.cu:108-130. */
 int atx_pack_w_f32(const float* w, int O, int K, int offset,
                    uint8_t* wq, uint8_t* wt, int Opad, hipStream_t stream);
 

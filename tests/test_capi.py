@@ -79,6 +79,14 @@ def test_epilogue_of_another_abi_is_rejected_without_gpu():
     assert rc == -1 and b"expected 40" in lib.atx_last_error()
 
 
+def test_pack_w_needs_an_output_without_gpu():
+    """atx_pack_w_f32 writes wq, wt or both; with neither it fails on the
+    host before launching anything."""
+    lib = L.load()
+    rc = lib.atx_pack_w_f32(None, 4, 9, 128, None, None, 32, None)
+    assert rc == -1 and b"null pointer" in lib.atx_last_error()
+
+
 def test_workspace_queries_are_host_only():
     assert L.query("atx_lut_gemm_workspace_bytes", 32, 2304, 4096, 256) == 0      # 512 tiles
     assert L.query("atx_lut_gemm_workspace_bytes", 8, 576, 1024, 64) > 0          # split-K

@@ -1054,14 +1054,43 @@ def test_dwconv_fake_int8_claude(geom, dtype):
     assert np.array_equal(y.cpu().numpy().reshape(3, C, -1), want.astype(np.float32))
 
 
+def test_pack_w_index_image_alone():
+    """want_wt=False writes the same weight index image as the full pack
+    (clamp(rint(w) + 128, 0, 255), halves to even, out-of-range values
+    clamped) and no transposed operand."""
+    r = gen(31)
+    w = np.concatenate([r.integers(-140, 141, 200).astype(np.float32),
+                        np.array([-0.5, 0.5, 1.5, 2.5, -127.5, 127.5], np.float32)])
+    w = np.resize(w, (23, 9))
+    wq, wt, Opad = ops._pack_w(t(w), 128, want_wt=False)
+    assert wt is None and Opad == 32
+    wq_full, wt_full, _ = ops._pack_w(t(w), 128)
+    assert torch.equal(wq, wq_full)
+    assert np.array_equal(wq.cpu().numpy(), O.quant_index(w, 128))
+    assert np.array_equal(wt_full.cpu().numpy()[:, :23], O.quant_index(w, 128).T)
+
+
+def misaligned(a):
+    """a copied to the device at a byte address that is 1 mod 4 (a
+    contiguous view one byte into a larger buffer)."""
+    flat = np.ascontiguousarray(a).reshape(-1)
+    buf = torch.empty(flat.size * flat.itemsize + 8, dtype=torch.uint8, device=DEV)
+    v = buf[1:1 + flat.size * flat.itemsize].view(t(flat[:0]).dtype).view(a.shape)
+    v.copy_(t(a))
+    assert v.data_ptr() % 4 == 1
+    return v
+
+
+@pytest.mark.parametrize("aligned", [True, False])
 @pytest.mark.parametrize("stride", [1, 2])
 @pytest.mark.parametrize("hw", [(16, 16), (9, 31), (1, 4), (5, 8)])
 @pytest.mark.parametrize("dtype", ["int8", "uint8"])
-def test_dwconv_strips(stride, hw, dtype):
-    """The 4-output strip kernel (3-wide kernels, stride 1 or 2 along W):
-    OW a multiple of 4 (16-byte stores), ragged strips, a single row, rows
-    read as aligned dwords (W % 4 == 0); exact against the per-channel int64
-    oracle, the int32 output too."""
+def test_dwconv_strips(stride, hw, dtype, aligned):
+    """The 4-output strip kernels (3-wide kernels, stride 1 or 2 along W):
+    OW a multiple of 4 (16-byte stores), ragged strips, a single row; a
+    4-byte aligned image takes the 3x3 kernel reading rows as aligned dwords
+    (W % 4 == 0 or not), a misaligned one the per-byte strip kernel; exact
+    against the per-channel int64 oracle, the int32 output too."""
     H, W = hw
     k, s, p, d = (3, 3), (stride, stride), (1, 1), (1, 1)
     r = gen(zlib.crc32(repr(("strips", stride, hw, dtype)).encode()))
@@ -1072,7 +1101,8 @@ def test_dwconv_strips(stride, hw, dtype):
         img = r.integers(0, 256, (2, C, H, W)).astype(np.uint8)
     w = r.integers(-128, 128, (C, 9)).astype(np.float32)
     lut = luts(7)["asym"]
-    y, wq = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
+    img_d = t(img) if aligned else misaligned(img)
+    y, wq = ops.dwconv_fake_int8_claude(img_d, t(w), t(lut, torch.float32), k, s, p, d)
     xi = O.image_index(img, 128)
     wi = (w + 128).astype(np.uint8)
     want = np.concatenate([O.lut_gemm_i64(O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128),
@@ -1082,10 +1112,66 @@ def test_dwconv_strips(stride, hw, dtype):
     yi = torch.empty((2, C, g.OH, g.OW), dtype=torch.int32, device=DEV)
     img16, imgf, cls = ops.lut_image(t(lut, torch.float32))
     ep = LB.GemmEpilogue(LB.ATX_OUT_I32)
-    img_d = t(img)
     LB.call("atx_dwconv_fwd", LB.ptr(img_d), 0 if dtype == "int8" else 1, g, 128, LB.ptr(wq),
             LB.ptr(img16), LB.ptr(imgf), cls, ep, LB.ptr(yi), LB.stream_of(yi))
     assert np.array_equal(yi.cpu().numpy().reshape(2, C, -1), want)
+
+
+@pytest.mark.parametrize("case", [((2, 3, 1, 2), (1, 1), (1, 3)), ((2, 3, 1, 2), (1, 2), (2, 4)),
+                                  ((3, 4, 15, 14), (1, 1), (1, 1)), ((2, 2, 5, 9), (2, 2), (1, 1)),
+                                  ((4, 1, 2, 2), (1, 1), (1, 4))])
+@pytest.mark.parametrize("dtype", ["int8", "uint8"])
+def test_dwconv_strip_windows_before_the_image(case, dtype):
+    """Rows whose dword window starts before the image's first byte (the
+    first plane's top-left strips, and planes smaller than the padding,
+    where later planes' windows start in an earlier plane) and windows past
+    its last byte: exact against the int64 oracle through the 3x3 strip
+    kernel."""
+    shape, s, p = case
+    k, d = (3, 3), (1, 1)
+    r = gen(zlib.crc32(repr(("windows", case, dtype)).encode()))
+    lo, hi = (-128, 128) if dtype == "int8" else (0, 256)
+    img = r.integers(lo, hi, shape).astype(np.int8 if dtype == "int8" else np.uint8)
+    C = shape[1]
+    w = r.integers(-128, 128, (C, 9)).astype(np.float32)
+    lut = luts(9)["asym"]
+    y, _ = ops.dwconv_fake_int8_claude(t(img), t(w), t(lut, torch.float32), k, s, p, d)
+    xi = O.image_index(img, 128)
+    wi = (w + 128).astype(np.uint8)
+    want = np.concatenate([O.lut_gemm_i64(O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128),
+                                          wi[c:c + 1], lut) for c in range(C)], axis=1)
+    assert np.array_equal(y.cpu().numpy().reshape(shape[0], C, -1), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("geom", [((1, 1), (1, 1), (1, 1)), ((2, 2), (1, 1), (1, 1)),
+                                  ((1, 2), (2, 0), (2, 1)), ((3, 1), (0, 3), (1, 1))])
+@pytest.mark.parametrize("dtype", ["int8", "uint8"])
+def test_dwconv_strip_groups(geom, dtype):
+    """MobileNet-sized depthwise convs (64 x 64 x 112 x 112, 3x3), where each
+    thread of the 3x3 strip kernel walks many groups of strips (positions
+    advanced incrementally, the next group's rows read before the current
+    one is summed): the aligned image (3x3 kernel) and the same image at a
+    misaligned address (per-byte strip kernel) give identical outputs, and
+    two channels match the int64 oracle; stride, padding and dilation along
+    H differ from those along W."""
+    s, p, d = geom
+    k = (3, 3)
+    r = gen(zlib.crc32(repr(("strip groups", geom, dtype)).encode()))
+    N, C, H, W = 64, 64, 112, 112
+    lo, hi = (-128, 128) if dtype == "int8" else (0, 256)
+    img = r.integers(lo, hi, (N, C, H, W)).astype(np.int8 if dtype == "int8" else np.uint8)
+    w = r.integers(-128, 128, (C, 9)).astype(np.float32)
+    lut = t(luts(8)["asym"], torch.float32)
+    y, wq = ops.dwconv_fake_int8_claude(t(img), t(w), lut, k, s, p, d)
+    ym, _ = ops.dwconv_fake_int8_claude(misaligned(img), t(w), lut, k, s, p, d)
+    assert torch.equal(y, ym)
+    xi = O.image_index(img, 128)
+    wi = (w + 128).astype(np.uint8)
+    yc = y.cpu().numpy()
+    for c in (0, C - 1):
+        want = O.lut_gemm_i64(O.im2col_index(xi[:, c:c + 1], k, s, p, d, 128), wi[c:c + 1],
+                              luts(8)["asym"])
+        assert np.array_equal(yc[:, c].reshape(N, -1), want[:, 0].astype(np.float32))
 
 
 @pytest.mark.parametrize("lut_name", ["u16_c5", "fp32"])
