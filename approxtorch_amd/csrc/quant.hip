@@ -324,10 +324,17 @@ __global__ void minmax_final_kernel(const float* __restrict__ part, int nb,
 
 constexpr int RED_BLOCKS = 1024;   // partial-result slots (2 floats each)
 
+// torch on the GPU evaluates `tensor / number` (a python number) as the
+// tensor times the fp32 reciprocal 1.0f / float(number), not as a division
+// (its true-divide kernel's scalar path); the statistics below follow that.
+__device__ __forceinline__ float div_by_number(float v, float number) {
+  return v * (1.0f / number);
+}
+
 // nn/Conv2d_int8.py:144-146 — cur = stat / denom; new = m*cur + (1-m)*old.
 __device__ __forceinline__ void ema_absmax(float stat, float denom, float m32, float om32,
                                            float* scale) {
-  const float cur = stat / denom;
+  const float cur = div_by_number(stat, denom);
   const float a = m32 * cur;
   const float b = om32 * scale[0];
   scale[0] = a + b;
@@ -342,7 +349,7 @@ __device__ __forceinline__ void uint8_qparams(float mn, float mx, float qmax,
                                               float& scale, float& zero) {
   mn = clamp_hi(mn, 0.0f);
   mx = clamp_lo(mx, 0.0f);
-  scale = clamp_lo((mx - mn) / qmax, 1e-12f);
+  scale = clamp_lo(div_by_number(mx - mn, qmax), 1e-12f);
   const float z = __builtin_rintf(-mn / scale);
   zero = clamp_hi(clamp_lo(z, 0.0f), qmax);
 }
@@ -385,10 +392,10 @@ __global__ void weight_stats_kernel(const float* __restrict__ w, long long inner
   block_minmax<false>(mn, mx);
   if (threadIdx.x != 0) return;
   if (mode == 0) {
-    const float cur = (mx > 0.0f) ? mx / qmax : scale_w[o];
+    const float cur = (mx > 0.0f) ? div_by_number(mx, qmax) : scale_w[o];
     scale_w[o] = m32 * cur + om32 * scale_w[o];
   } else if (mode == 1) {
-    scale_w[o] = (mx > 0.0f) ? mx / qmax : 1.0f;
+    scale_w[o] = (mx > 0.0f) ? div_by_number(mx, qmax) : 1.0f;
   } else {
     w_min[o] = m32 * mn + om32 * w_min[o];
     w_max[o] = m32 * mx + om32 * w_max[o];

@@ -215,11 +215,20 @@ def ema_scalar(m, cur, old):
     return f32(a + b)
 
 
+def div_by_number(v, number):
+    """`tensor / number` (number a python scalar) as torch evaluates it on the
+    GPU: v * fp32(1 / fp32(number)), rounded to fp32 (its true-divide kernel
+    multiplies by the reciprocal when the divisor is a host scalar; exact
+    division differs in the last bit for a few percent of values)."""
+    return (np.asarray(v, dtype=f32) * (f32(1) / f32(number))).astype(f32)
+
+
 def ema_absmax(x, scale_x, m, denom=127.0):
-    """nn/Conv2d_int8.py:137-146."""
+    """nn/Conv2d_int8.py:137-146, the statements as torch runs them on the
+    GPU (abs_max / 127 through div_by_number)."""
     x = np.asarray(x, dtype=f32)
     absmax = np.max(np.abs(x)) if not np.isnan(x).any() else f32(np.nan)
-    cur = f32(f32(absmax) / f32(denom))
+    cur = f32(div_by_number(absmax, denom))
     return ema_scalar(m, cur, scale_x)
 
 
@@ -227,7 +236,7 @@ def weight_scale_ema(w, scale_w, m, qmax_w):
     """nn/Conv2d_int8.py:148-158 (zero channels keep their scale)."""
     w = np.asarray(w, dtype=f32).reshape(w.shape[0], -1)
     absmax = np.abs(w).max(axis=1)
-    cur = np.where(absmax > 0, (absmax / f32(qmax_w)).astype(f32), scale_w).astype(f32)
+    cur = np.where(absmax > 0, div_by_number(absmax, qmax_w), scale_w).astype(f32)
     a = (f32(m) * cur).astype(f32)
     b = (f32(1 - m) * np.asarray(scale_w, dtype=f32)).astype(f32)
     return (a + b).astype(f32)
@@ -237,14 +246,14 @@ def weight_scale_reset(w, qmax_w):
     """nn/Conv2d_int8.py:160-167."""
     w = np.asarray(w, dtype=f32).reshape(w.shape[0], -1)
     absmax = np.abs(w).max(axis=1)
-    return np.where(absmax > 0, (absmax / f32(qmax_w)).astype(f32), f32(1)).astype(f32)
+    return np.where(absmax > 0, div_by_number(absmax, qmax_w), f32(1)).astype(f32)
 
 
 def uint8_qparams(mn, mx, qmax=255):
     """nn/Conv2d_uint8.py:11-23."""
     mn = np.minimum(np.asarray(mn, dtype=f32), f32(0))
     mx = np.maximum(np.asarray(mx, dtype=f32), f32(0))
-    scale = np.maximum(((mx - mn) / f32(qmax)).astype(f32), f32(1e-12)).astype(f32)
+    scale = np.maximum(div_by_number((mx - mn).astype(f32), qmax), f32(1e-12)).astype(f32)
     zero = np.clip(np.rint((-mn / scale).astype(f32)), f32(0), f32(qmax)).astype(f32)
     return scale, zero
 

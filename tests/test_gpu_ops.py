@@ -629,6 +629,29 @@ def test_ema_kernels_bitwise(m):
         assert np.array_equal(got.cpu().numpy(), exp)
 
 
+def test_torch_gpu_divides_by_numbers_via_the_reciprocal():
+    """The reference's scale statements run by torch on this GPU -- abs_max /
+    ((qmax - qmin) / 2), absmax / qmax_w, (mx - mn) / qmax with python-number
+    divisors (nn/Conv2d_int8.py:144,155,166; nn/Conv2d_uint8.py:21) -- equal
+    the oracle's v * fp32(1 / number) bit for bit, where exact division would
+    differ: the device semantics the statistic kernels and the oracle follow."""
+    r = gen(23)
+    v = (r.random(100000) * 50).astype(np.float32)
+    vg = t(v)
+    for number in (127.0, 7, 255, 15):
+        got = (vg / number).cpu().numpy()
+        assert np.array_equal(got, O.div_by_number(v, number))
+    assert ((vg / 127.0).cpu().numpy() != v / np.float32(127)).sum() > 100
+    # the EMA statement itself, on a 0-dim device statistic, for many inputs
+    m = 0.05
+    old = torch.tensor(0.0371, device=DEV)
+    for i in range(200):
+        x = (r.standard_normal(257) * (1 + i)).astype(np.float32)
+        abs_max = t(x).abs().max()
+        want = (m * (abs_max / ((127 - -127) / 2)) + (1 - m) * old).item()
+        assert want == O.ema_absmax(x, np.float32(0.0371), m)
+
+
 # ------------------------------------------------------------ backward ops
 def close(a, b, absref=None):
     """rel 1e-5 / abs 1e-4.  With absref (the sum of |terms| of each output),

@@ -133,12 +133,32 @@ def test_fakequant_hand_cases():
     assert g.tolist() == [2.0, 2.0, 2.0, 0.0, 0.0]
 
 
+def gpu_div(t, number):
+    """`t / number` (number a python scalar) as torch evaluates it on the GPU,
+    where the reference runs: t times the fp32 reciprocal of the number (its
+    true-divide kernel's host-scalar path).  The CPU kernel divides exactly,
+    so the reference statements below are evaluated on the CPU with this
+    substitution; test_gpu_ops.py's
+    test_torch_gpu_divides_by_numbers_via_the_reciprocal checks the device
+    behaviour itself."""
+    return t * torch.tensor(np.float32(1) / np.float32(number))
+
+
+def test_div_by_number_is_the_reciprocal_product():
+    """oracle.div_by_number differs from exact fp32 division for some values
+    (so the choice matters) and equals v * fl(1/n) for every one."""
+    v = (rng.random(20000) * 100).astype(np.float32)
+    got = O.div_by_number(v, 127.0)
+    assert np.array_equal(got, gpu_div(torch.from_numpy(v), 127.0).numpy())
+    assert (got != (v / np.float32(127))).sum() > 100
+
+
 def test_ema_and_qparams_match_torch_bitwise():
     for m in (0.05, 0.1, 0.3333):
         x = rng.standard_normal(777).astype(np.float32) * 4
         old = np.float32(0.0371)
         xt = torch.from_numpy(x)
-        cur = xt.abs().max() / ((127 - -127) / 2)
+        cur = gpu_div(xt.abs().max(), (127 - -127) / 2)
         want = (m * cur + (1 - m) * torch.tensor(old)).item()
         assert O.ema_absmax(x, old, m) == np.float32(want)
         w = rng.standard_normal((6, 3, 3, 3)).astype(np.float32)
@@ -146,13 +166,13 @@ def test_ema_and_qparams_match_torch_bitwise():
         sw = rng.random(6).astype(np.float32)
         wt = torch.from_numpy(w)
         absmax = wt.abs().amax(dim=(1, 2, 3))
-        cur_w = torch.where(absmax > 0, absmax / 7, torch.from_numpy(sw))
+        cur_w = torch.where(absmax > 0, gpu_div(absmax, 7), torch.from_numpy(sw))
         want_w = (m * cur_w + (1 - m) * torch.from_numpy(sw)).numpy()
         assert np.array_equal(O.weight_scale_ema(w, sw, m, 7), want_w)
     mn = torch.tensor([-1.3, 0.4, -0.0, -5.0])
     mx = torch.tensor([2.2, 3.0, 0.0, -1.0])
     mnc, mxc = torch.clamp(mn, max=0.0), torch.clamp(mx, min=0.0)
-    sc = torch.clamp((mxc - mnc) / 255, min=1e-12)
+    sc = torch.clamp(gpu_div(mxc - mnc, 255), min=1e-12)
     zr = torch.round(-mnc / sc).clamp(0.0, 255.0)
     s, z = O.uint8_qparams(mn.numpy(), mx.numpy())
     assert np.array_equal(s, sc.numpy()) and np.array_equal(z, zr.numpy())
@@ -162,7 +182,7 @@ def _torch_qparams(mn, mx, qmax):
     # nn/Conv2d_uint8.py:11-23, evaluated by torch
     mn = torch.clamp(mn, max=0.0)
     mx = torch.clamp(mx, min=0.0)
-    scale = torch.clamp((mx - mn) / qmax, min=1e-12)
+    scale = torch.clamp(gpu_div(mx - mn, qmax), min=1e-12)
     return scale, torch.round(-mn / scale).clamp(0.0, float(qmax))
 
 
@@ -211,7 +231,7 @@ def test_weight_scale_reset_matches_reference_torch_expression(bits):
     w[1] = 0
     qmax_w = 2 ** (bits - 1) - 1
     absmax = torch.from_numpy(w).abs().amax(dim=(1, 2, 3))
-    want = torch.where(absmax > 0, absmax / qmax_w, torch.ones_like(absmax))
+    want = torch.where(absmax > 0, gpu_div(absmax, qmax_w), torch.ones_like(absmax))
     got = O.weight_scale_reset(w, qmax_w)
     assert np.array_equal(got, want.numpy())
     assert got[1] == 1.0
