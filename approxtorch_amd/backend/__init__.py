@@ -13,6 +13,18 @@ from . import _lib, ops
 
 _lib.load()
 
+
+def _fp32_fq(x, s, qmin, qmax, z=None):
+    # the reference's fused ops take fp32 x only (csrc/claude/quantization.cu:190-193)
+    ops.require_cuda_f32(x, "x")
+    return ops.fakequant_per_tensor(x, s, qmin, qmax, z)[:2]
+
+
+def _fp32_fq_bwd(go, m, s):
+    ops.require_cuda_f32(go, "grad_output")
+    return ops.fakequant_per_tensor_backward(go, m, s)
+
+
 _SCHEMAS = {
     "bgemm_fake_int8_forward_cuda_claude":
         ("(Tensor x, Tensor w, Tensor lut) -> Tensor", ops.bgemm_fake_int8_claude),
@@ -81,16 +93,16 @@ _SCHEMAS = {
          ops.bgemm_custom_grad_int8_dw),
     "fakequant_per_tensor_claude":
         ("(Tensor x, Tensor scale, int qmin, int qmax) -> (Tensor, Tensor)",
-         lambda x, s, qmin, qmax: ops.fakequant_per_tensor(x, s, qmin, qmax)[:2]),
+         lambda x, s, qmin, qmax: _fp32_fq(x, s, qmin, qmax)),
     "fakequant_per_tensor_backward_claude":
         ("(Tensor grad_output, Tensor mask, Tensor scale) -> Tensor",
-         lambda go, m, s: ops.fakequant_per_tensor_backward(go, m, s)),
+         lambda go, m, s: _fp32_fq_bwd(go, m, s)),
     "fakequant_per_tensor_asymmetric_claude":
         ("(Tensor x, Tensor scale, Tensor zero_point, int qmin, int qmax) -> (Tensor, Tensor)",
-         lambda x, s, z, qmin, qmax: ops.fakequant_per_tensor(x, s, qmin, qmax, z)[:2]),
+         lambda x, s, z, qmin, qmax: _fp32_fq(x, s, qmin, qmax, z)),
     "fakequant_per_tensor_asymmetric_backward_claude":
         ("(Tensor grad_output, Tensor mask, Tensor scale) -> Tensor",
-         lambda go, m, s: ops.fakequant_per_tensor_backward(go, m, s)),
+         lambda go, m, s: _fp32_fq_bwd(go, m, s)),
 }
 
 

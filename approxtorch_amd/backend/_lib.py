@@ -18,6 +18,7 @@ c_int, c_ll, c_float, c_vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ct
 
 ATX_LUT_I16, ATX_LUT_U16, ATX_LUT_F32 = 0, 1, 2
 ATX_OUT_F32, ATX_OUT_I32, ATX_OUT_DEQUANT = 0, 1, 2
+ATX_DT_F32, ATX_DT_F16, ATX_DT_BF16 = 0, 1, 2
 ROW_TILE, COL_TILE = 2048, 32
 NOALLOC_SCRATCH_BYTES = 64 << 20     # ATX_NOALLOC_SCRATCH_BYTES
 
@@ -82,6 +83,15 @@ _SIGS = {
     "atx_absmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_float, c_float, c_float, c_vp, c_vp]),
     "atx_absmax_ema_upper": (c_int, [c_vp, c_ll, c_vp, c_vp, c_float, c_float, c_float, c_vp,
                                      c_vp, c_vp]),
+    "atx_absmax_dt": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_vp]),
+    "atx_ema_absmax_apply_dt": (c_int, [c_vp, c_int, c_float, c_float, c_float, c_vp, c_vp]),
+    "atx_absmax_ema_upper_dt": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_float, c_float,
+                                        c_float, c_vp, c_vp, c_vp]),
+    "atx_fakequant_fwd_dt": (c_int, [c_vp, c_int, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp,
+                                     c_vp, c_vp, c_vp]),
+    "atx_fakequant_bwd_dt": (c_int, [c_vp, c_int, c_vp, c_ll, c_vp, c_int, c_vp, c_vp]),
+    "atx_weight_scale_ema_dt": (c_int, [c_vp, c_int, c_int, c_ll, c_float, c_float, c_float,
+                                        c_int, c_vp, c_vp]),
     "atx_minmax_ema": (c_int, [c_vp, c_ll, c_vp, c_vp, c_vp, c_float, c_float, c_int, c_vp,
                                c_vp, c_vp, c_vp, c_vp]),
     "atx_ema_minmax_apply": (c_int, [c_vp, c_vp, c_float, c_float, c_int, c_vp, c_vp, c_vp,

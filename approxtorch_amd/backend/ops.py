@@ -888,6 +888,28 @@ def require_cuda_f32(t: Tensor, name: str):
         raise RuntimeError(f"{name} must be float32, got {t.dtype}")
 
 
+# activation dtypes the *_dt kernels read besides fp32
+LOWP = {torch.float16: L.ATX_DT_F16, torch.bfloat16: L.ATX_DT_BF16}
+
+
+def dtype_code(t: Tensor) -> int:
+    """ATX_DT_* code of an fp32 / fp16 / bf16 tensor."""
+    if t.dtype == torch.float32:
+        return L.ATX_DT_F32
+    if t.dtype in LOWP:
+        return LOWP[t.dtype]
+    raise RuntimeError(f"expected a float32, float16 or bfloat16 tensor, got {t.dtype}")
+
+
+def require_cuda_float(t: Tensor, name: str):
+    """A CUDA tensor of fp32, fp16 or bf16 (the activation dtypes the
+    statistic and fake-quant kernels read)."""
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"{name} must be float32, float16 or bfloat16, got {t.dtype}")
+
+
 def require_param(p, x: Tensor, name: str, numel: int = 1):
     """A scale / zero-point operand: fp32, `numel` elements, on x's device
     (csrc/claude/quantization.cu:190-193,269-274)."""
@@ -904,11 +926,13 @@ def require_param(p, x: Tensor, name: str, numel: int = 1):
 
 def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
                          want_q=True, q8_dtype=None, nonneg=None):
-    """(q fp32, mask bool[, q8]) of the fused per-tensor fake-quant
-    (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric).
+    """(q, mask bool[, q8]) of the fused per-tensor fake-quant
+    (csrc/claude/quantization.cu:187-221 symmetric, 260-311 asymmetric); q
+    has x's dtype.  An fp16 / bf16 x takes the reference's unfused statements
+    in that dtype (nn/quantization.py:44-52,72-80; atx_fakequant_fwd_dt).
     nonneg: optional device int32 flag (upper_flag()), cleared when some
     quantized value is negative."""
-    require_cuda_f32(x, "x")
+    require_cuda_float(x, "x")
     require_param(scale, x, "scale")
     require_param(zero_point, x, "zero_point")
     if qmin >= qmax:
@@ -917,9 +941,14 @@ def fakequant_per_tensor(x: Tensor, scale: Tensor, qmin: int, qmax: int, zero_po
     q = torch.empty_like(xc) if want_q else None
     mask = torch.empty(xc.shape, dtype=torch.bool, device=xc.device)
     q8 = torch.empty(xc.shape, dtype=q8_dtype, device=xc.device) if q8_dtype else None
-    L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale.contiguous()),
-           L.ptr(None if zero_point is None else zero_point.contiguous()), qmin, qmax,
-           L.ptr(q), L.ptr(mask), L.ptr(q8), L.ptr(nonneg), L.stream_of(xc))
+    zp = L.ptr(None if zero_point is None else zero_point.contiguous())
+    if xc.dtype in LOWP:
+        L.call("atx_fakequant_fwd_dt", L.ptr(xc), LOWP[xc.dtype], xc.numel(),
+               L.ptr(scale.contiguous()), zp, qmin, qmax, L.ptr(q), L.ptr(mask), L.ptr(q8),
+               L.ptr(nonneg), L.stream_of(xc))
+    else:
+        L.call("atx_fakequant_fwd", L.ptr(xc), xc.numel(), L.ptr(scale.contiguous()), zp, qmin,
+               qmax, L.ptr(q), L.ptr(mask), L.ptr(q8), L.ptr(nonneg), L.stream_of(xc))
     return q, mask, q8
 
 
@@ -976,10 +1005,28 @@ def conv_forward_rows(xt_rpad, w_idx_or_val: Tensor, lut: Tensor, g, offset: int
 
 
 def fakequant_per_tensor_backward(grad_output: Tensor, mask: Tensor, scale: Tensor,
-                                  channels: int = 1, inner: int = 1) -> Tensor:
+                                  channels: int = 1, inner: int = 1, dtype=None) -> Tensor:
     """gx = (mask ? go : 0) / max(scale, 1e-12) (csrc/claude/quantization.cu:223-258);
     scale has one element, or `channels` for a per-channel mask of
-    channels x inner elements."""
+    channels x inner elements.  dtype (default: grad_output's) fp16 / bf16:
+    the per-tensor gradient of an x of that dtype, go * mask / s in it
+    (nn/quantization.py:58-62; grad_output fp32 or that dtype,
+    atx_fakequant_bwd_dt)."""
+    dtype = grad_output.dtype if dtype is None else dtype
+    if dtype in LOWP:
+        if not grad_output.is_cuda or grad_output.dtype not in (torch.float32, dtype):
+            raise RuntimeError(f"grad_output must be a CUDA float32 or {dtype} tensor")
+        if mask.dtype != torch.bool or mask.device != grad_output.device or \
+                mask.shape != grad_output.shape:
+            raise RuntimeError("mask must be a bool CUDA tensor of grad_output's shape")
+        if channels != 1:
+            raise RuntimeError("fp16 / bf16 fake-quant gradients are per tensor")
+        require_param(scale, grad_output, "scale")
+        go = grad_output.contiguous()
+        gx = torch.empty(go.shape, dtype=dtype, device=go.device)
+        L.call("atx_fakequant_bwd_dt", L.ptr(go), dtype_code(go), L.ptr(mask.contiguous()),
+               go.numel(), L.ptr(scale.contiguous()), LOWP[dtype], L.ptr(gx), L.stream_of(go))
+        return gx
     require_cuda_f32(grad_output, "grad_output")
     if not mask.is_cuda or mask.device != grad_output.device:
         raise RuntimeError(f"mask must be a CUDA tensor on {grad_output.device}")

@@ -18,6 +18,44 @@ constexpr int EW = 256;   // threads per elementwise block
 __device__ __forceinline__ float clamp_lo(float v, float lo) { return v < lo ? lo : v; }
 __device__ __forceinline__ float clamp_hi(float v, float hi) { return v > hi ? hi : v; }
 
+// ------------------------------------------- fp16 / bf16 activations
+// DT: ATX_DT_F32, ATX_DT_F16 or ATX_DT_BF16.  A low-precision element is
+// read as its exact fp32 value; lp_round(v) rounds an fp32 result to the
+// dtype and back (round to nearest even: fp16 by the hardware conversion,
+// bf16 as torch's c10::BFloat16 does, NaN to the canonical 0x7fc0), i.e.
+// the value torch's elementwise kernels store after computing in fp32.
+template <int DT> __device__ __forceinline__ float lp_load(const void* p, long long i) {
+  if constexpr (DT == ATX_DT_F32) {
+    return ((const float*)p)[i];
+  } else if constexpr (DT == ATX_DT_F16) {
+    return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)p)[i]);
+  } else {
+    return __uint_as_float((unsigned)((const uint16_t*)p)[i] << 16);
+  }
+}
+template <int DT> __device__ __forceinline__ uint16_t lp_bits(float v) {
+  if constexpr (DT == ATX_DT_F16) {
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+  } else {
+    if (v != v) return 0x7fc0;
+    const unsigned u = __float_as_uint(v);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+}
+template <int DT> __device__ __forceinline__ float lp_round(float v) {
+  if constexpr (DT == ATX_DT_F32) {
+    return v;
+  } else if constexpr (DT == ATX_DT_F16) {
+    return (float)(_Float16)v;
+  } else {
+    return __uint_as_float((unsigned)lp_bits<DT>(v) << 16);
+  }
+}
+template <int DT> __device__ __forceinline__ void lp_store(void* p, long long i, float v) {
+  if constexpr (DT == ATX_DT_F32) ((float*)p)[i] = v;
+  else ((uint16_t*)p)[i] = lp_bits<DT>(v);
+}
+
 // nn/quantization.py:48-52 (symmetric) and :76-80 (asymmetric);
 // csrc/claude/quantization.cu:54-75.
 __device__ __forceinline__ float fake_quant(float x, float s, float z, bool asym,
@@ -182,6 +220,57 @@ __global__ void fakequant_bwd_kernel(const float* __restrict__ go,
   }
 }
 
+// Per-tensor fake-quant of a low-precision x, the statements of
+// nn/quantization.py:44-52 / 72-80 (the unfused path the reference takes for
+// a non-fp32 x) as torch evaluates them in the input's dtype D: s =
+// clamp(scale, 1e-12) in fp32; v = x / s with s first cast to D, computed in
+// fp32 and rounded to D; (+ zero_point, cast to D, rounded to D); mask =
+// qmin <= v <= qmax; q = clamp(round(v)) (exact in D).  q in D, mask and the
+// byte image q8 (NaN -> 0) as fakequant_fwd_kernel writes them.
+template <int DT>
+__global__ void fakequant_fwd_lp_kernel(const void* __restrict__ x, long long n,
+                                        const float* __restrict__ scale,
+                                        const float* __restrict__ zero, float qmin, float qmax,
+                                        void* __restrict__ q, uint8_t* __restrict__ mask,
+                                        uint8_t* __restrict__ q8, int* __restrict__ nonneg) {
+  const float s = lp_round<DT>(fmaxf(scale[0], 1e-12f));
+  const bool asym = zero != nullptr;
+  const float z = asym ? lp_round<DT>(zero[0]) : 0.0f;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  bool neg = false;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    float v = lp_round<DT>(lp_load<DT>(x, i) / s);
+    if (asym) v = lp_round<DT>(v + z);
+    const bool m = (v >= qmin) && (v <= qmax);
+    float r = __builtin_rintf(v);
+    r = clamp_hi(clamp_lo(r, qmin), qmax);
+    if (q) lp_store<DT>(q, i, r);
+    if (mask) mask[i] = m;
+    if (q8) q8[i] = (uint8_t)to_int(r);
+    neg |= r < 0.0f;
+  }
+  if (nonneg && neg) nonneg[0] = 0;      // benign race: every writer stores 0
+}
+
+// grad_x = grad_output * mask.to(D) / s (nn/quantization.py:58-62) in the
+// dtype D of x: the incoming gradient in GT (fp32: first rounded to D, as
+// autograd casts a gradient to its input's dtype, or D itself), times the
+// mask (an exact product, -0 and NaN from 0 * inf included), divided by s
+// cast to D and rounded to D.
+template <int GT, int DT>
+__global__ void fakequant_bwd_lp_kernel(const void* __restrict__ go,
+                                        const uint8_t* __restrict__ mask, long long n,
+                                        const float* __restrict__ scale,
+                                        void* __restrict__ gx) {
+  const float s = lp_round<DT>(fmaxf(scale[0], 1e-12f));
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float g = lp_round<DT>(lp_load<GT>(go, i));
+    const float gm = g * (mask[i] ? 1.0f : 0.0f);
+    lp_store<DT>(gx, i, lp_round<DT>(gm / s));
+  }
+}
+
 // Weight [O, inner] per-channel fake-quant; wt is the LUT GEMM's transposed
 // weight operand [inner][Opad] (columns >= O hold index 0).  A block owns a
 // tile of FQ_O channels x FQ_K taps: it reads w and writes q / mask / wq
@@ -260,27 +349,38 @@ __device__ __forceinline__ void block_minmax(float& mn, float& mx) {
   }
 }
 
-// Pass 1: per-block min / max (or |x| max) into part[2*block].
-template <bool ABS>
-__global__ void minmax_partial_kernel(const float* __restrict__ x, long long n,
+// Pass 1: per-block min / max (or |x| max) into part[2*block].  DT: the
+// input's dtype (low-precision elements are exact in fp32, so the extrema
+// are the dtype's own).
+template <bool ABS, int DT = ATX_DT_F32>
+__global__ void minmax_partial_kernel(const void* __restrict__ xv, long long n,
                                       float* __restrict__ part) {
   float mn = __builtin_inff(), mx = ABS ? 0.0f : -__builtin_inff();
   const long long stride = (long long)gridDim.x * blockDim.x;
   const long long t0 = blockIdx.x * (long long)blockDim.x + threadIdx.x;
   // 16-byte loads over the aligned body, then the remaining elements
-  const long long n4 = ((uintptr_t)x & 15) == 0 ? (n >> 2) : 0;
-  for (long long i = t0; i < n4; i += stride) {
-    const float4 v = ((const float4*)x)[i];
-    const float e[4] = {v.x, v.y, v.z, v.w};
+  constexpr int PER = DT == ATX_DT_F32 ? 4 : 8;        // elements per 16 bytes
+  const long long nv = ((uintptr_t)xv & 15) == 0 ? n / PER : 0;
+  for (long long i = t0; i < nv; i += stride) {
+    const uint4 v = ((const uint4*)xv)[i];
+    const unsigned w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float u = ABS ? fabsf(e[j]) : e[j];
+    for (int j = 0; j < PER; ++j) {
+      float e;
+      if constexpr (DT == ATX_DT_F32) {
+        e = __uint_as_float(w[j]);
+      } else {
+        const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+        e = lp_load<DT>(&h, 0);
+      }
+      const float u = ABS ? fabsf(e) : e;
       mn = nmin(mn, u);
       mx = nmax(mx, u);
     }
   }
-  for (long long i = 4 * n4 + t0; i < n; i += stride) {
-    const float v = ABS ? fabsf(x[i]) : x[i];
+  for (long long i = PER * nv + t0; i < n; i += stride) {
+    const float e = lp_load<DT>(xv, i);
+    const float v = ABS ? fabsf(e) : e;
     mn = nmin(mn, v);
     mx = nmax(mx, v);
   }
@@ -295,6 +395,7 @@ struct EmaArgs {
   float denom, m32, om32, qmax;
   float* scale; float* zero; float* x_min; float* x_max;
   int* upper;               // kind 3: 1 when min(x) >= 0 (no NaN), else 0
+  int dt;                   // kinds 1, 3: the input's dtype (ema_absmax_dt)
 };
 __device__ void apply_ema(const EmaArgs& e, float mn, float mx);
 
@@ -332,16 +433,26 @@ __device__ __forceinline__ float div_by_number(float v, float number) {
 }
 
 // nn/Conv2d_int8.py:144-146 — cur = stat / denom; new = m*cur + (1-m)*old.
-__device__ __forceinline__ void ema_absmax(float stat, float denom, float m32, float om32,
-                                           float* scale) {
-  const float cur = div_by_number(stat, denom);
-  const float a = m32 * cur;
+// For an x of dtype D (fp16 / bf16) abs_max is a D scalar, so torch rounds
+// cur and m * cur to D; (1 - m) * scale_x and the sum stay fp32 (a D and an
+// fp32 0-dim tensor promote to fp32).
+template <int DT>
+__device__ __forceinline__ void ema_absmax_t(float stat, float denom, float m32, float om32,
+                                             float* scale) {
+  const float cur = lp_round<DT>(div_by_number(stat, denom));
+  const float a = lp_round<DT>(m32 * cur);
   const float b = om32 * scale[0];
   scale[0] = a + b;
 }
+__device__ __forceinline__ void ema_absmax(float stat, float denom, float m32, float om32,
+                                           float* scale, int dt = ATX_DT_F32) {
+  if (dt == ATX_DT_F16) ema_absmax_t<ATX_DT_F16>(stat, denom, m32, om32, scale);
+  else if (dt == ATX_DT_BF16) ema_absmax_t<ATX_DT_BF16>(stat, denom, m32, om32, scale);
+  else ema_absmax_t<ATX_DT_F32>(stat, denom, m32, om32, scale);
+}
 __global__ void ema_absmax_kernel(const float* stat, float denom, float m32, float om32,
-                                  float* scale) {
-  ema_absmax(stat[0], denom, m32, om32, scale);
+                                  float* scale, int dt) {
+  ema_absmax(stat[0], denom, m32, om32, scale, dt);
 }
 
 // nn/Conv2d_uint8.py:11-23 (uint8_qparams) for one (min, max) pair.
@@ -369,7 +480,7 @@ __global__ void ema_minmax_kernel(const float* mn, const float* mx, float m32, f
 }
 
 __device__ void apply_ema(const EmaArgs& e, float mn, float mx) {
-  if (e.kind == 1 || e.kind == 3) ema_absmax(mx, e.denom, e.m32, e.om32, e.scale);
+  if (e.kind == 1 || e.kind == 3) ema_absmax(mx, e.denom, e.m32, e.om32, e.scale, e.dt);
   else ema_minmax(mn, mx, e.m32, e.om32, e.qmax, e.x_min, e.x_max, e.scale, e.zero);
 }
 
@@ -377,25 +488,30 @@ __device__ void apply_ema(const EmaArgs& e, float mn, float mx) {
 // mode 0: int8 absmax EMA (nn/Conv2d_int8.py:148-158)
 // mode 1: int8 absmax reset (nn/Conv2d_int8.py:160-167)
 // mode 2: uint8 min/max EMA + qparams (nn/Conv2d_uint8.py:242-255)
-__global__ void weight_stats_kernel(const float* __restrict__ w, long long inner, int mode,
+// DT: the weight's dtype.  For an fp16 / bf16 weight torch's absmax / qmax_w
+// is a tensor of that dtype (rounded to it); torch.where with the fp32
+// scale then promotes it back to fp32 exactly.
+template <int DT>
+__global__ void weight_stats_kernel(const void* __restrict__ w, long long inner, int mode,
                                     float qmax, float m32, float om32, float* scale_w,
                                     float* zero_w, float* w_min, float* w_max) {
   const int o = blockIdx.x;
-  const float* row = w + (long long)o * inner;
+  const long long base = (long long)o * inner;
   const bool absmode = mode != 2;
   float mn = __builtin_inff(), mx = absmode ? 0.0f : -__builtin_inff();
   for (long long i = threadIdx.x; i < inner; i += blockDim.x) {
-    const float v = absmode ? fabsf(row[i]) : row[i];
+    const float e = lp_load<DT>(w, base + i);
+    const float v = absmode ? fabsf(e) : e;
     mn = nmin(mn, v);
     mx = nmax(mx, v);
   }
   block_minmax<false>(mn, mx);
   if (threadIdx.x != 0) return;
   if (mode == 0) {
-    const float cur = (mx > 0.0f) ? div_by_number(mx, qmax) : scale_w[o];
+    const float cur = (mx > 0.0f) ? lp_round<DT>(div_by_number(mx, qmax)) : scale_w[o];
     scale_w[o] = m32 * cur + om32 * scale_w[o];
   } else if (mode == 1) {
-    scale_w[o] = (mx > 0.0f) ? div_by_number(mx, qmax) : 1.0f;
+    scale_w[o] = (mx > 0.0f) ? lp_round<DT>(div_by_number(mx, qmax)) : 1.0f;
   } else {
     w_min[o] = m32 * mn + om32 * w_min[o];
     w_max[o] = m32 * mx + om32 * w_max[o];
@@ -534,17 +650,22 @@ int atx_fakequant_channel_fwd(const float* w, int O, long long inner, const floa
   return check_launch("fakequant_channel_kernel");
 }
 
-static int minmax_impl(const float* x, long long n, unsigned int* ws, float* mn_out,
+static int minmax_impl(const void* x, long long n, unsigned int* ws, float* mn_out,
                        float* mx_out, bool absmode, hipStream_t stream,
-                       EmaArgs ema = EmaArgs{}) {
+                       EmaArgs ema = EmaArgs{}, int dt = ATX_DT_F32) {
   ATX_REQUIRE(n > 0, "min/max of an empty tensor is undefined");
   ATX_REQUIRE(x && ws, "minmax: null pointer");
+  ATX_REQUIRE(dt == ATX_DT_F32 || dt == ATX_DT_F16 || dt == ATX_DT_BF16,
+              "minmax: bad dtype %d", dt);
   const int nb = elem_grid(n, EW, RED_BLOCKS);
   float* part = (float*)ws;
-  if (absmode)
-    hipLaunchKernelGGL(minmax_partial_kernel<true>, dim3(nb), dim3(EW), 0, stream, x, n, part);
-  else
-    hipLaunchKernelGGL(minmax_partial_kernel<false>, dim3(nb), dim3(EW), 0, stream, x, n, part);
+  ema.dt = dt;
+#define ATX_MM(A, D) \
+  hipLaunchKernelGGL((minmax_partial_kernel<A, D>), dim3(nb), dim3(EW), 0, stream, x, n, part)
+  if (dt == ATX_DT_F16) { if (absmode) ATX_MM(true, ATX_DT_F16); else ATX_MM(false, ATX_DT_F16); }
+  else if (dt == ATX_DT_BF16) { if (absmode) ATX_MM(true, ATX_DT_BF16); else ATX_MM(false, ATX_DT_BF16); }
+  else { if (absmode) ATX_MM(true, ATX_DT_F32); else ATX_MM(false, ATX_DT_F32); }
+#undef ATX_MM
   int rc = check_launch("minmax_partial_kernel");
   if (rc) return rc;
   if (absmode)
@@ -601,8 +722,74 @@ int atx_ema_absmax_apply(const float* stat, float denom, float m32, float om32, 
                          hipStream_t stream) {
   ATX_REQUIRE(stat && scale, "atx_ema_absmax_apply: null pointer");
   hipLaunchKernelGGL(ema_absmax_kernel, dim3(1), dim3(1), 0, stream, stat, denom, m32, om32,
-                     scale);
+                     scale, (int)ATX_DT_F32);
   return check_launch("ema_absmax_kernel");
+}
+
+int atx_absmax_dt(const void* x, int dtype, long long n, unsigned int* ws, float* stat_out,
+                  hipStream_t stream) {
+  ATX_REQUIRE(stat_out, "atx_absmax_dt: null output");
+  return minmax_impl(x, n, ws, nullptr, stat_out, true, stream, EmaArgs{}, dtype);
+}
+
+int atx_ema_absmax_apply_dt(const float* stat, int dtype, float denom, float m32, float om32,
+                            float* scale, hipStream_t stream) {
+  ATX_REQUIRE(stat && scale, "atx_ema_absmax_apply_dt: null pointer");
+  ATX_REQUIRE(dtype == ATX_DT_F32 || dtype == ATX_DT_F16 || dtype == ATX_DT_BF16,
+              "atx_ema_absmax_apply_dt: bad dtype %d", dtype);
+  hipLaunchKernelGGL(ema_absmax_kernel, dim3(1), dim3(1), 0, stream, stat, denom, m32, om32,
+                     scale, dtype);
+  return check_launch("ema_absmax_kernel");
+}
+
+int atx_absmax_ema_upper_dt(const void* x, int dtype, long long n, unsigned int* ws,
+                            float* stat_out, float denom, float m32, float om32, float* scale,
+                            int* upper, hipStream_t stream) {
+  ATX_REQUIRE(stat_out && scale && upper, "atx_absmax_ema_upper_dt: null output");
+  EmaArgs e{};
+  e.kind = 3; e.denom = denom; e.m32 = m32; e.om32 = om32; e.scale = scale; e.upper = upper;
+  return minmax_impl(x, n, ws, nullptr, stat_out, false, stream, e, dtype);
+}
+
+int atx_fakequant_fwd_dt(const void* x, int dtype, long long n, const float* scale,
+                         const float* zero, int qmin, int qmax, void* q, uint8_t* mask,
+                         void* q8, int* nonneg, hipStream_t stream) {
+  ATX_REQUIRE(n >= 0, "atx_fakequant_fwd_dt: negative size");
+  ATX_REQUIRE(qmin < qmax, "qmin must be < qmax, got [%d, %d]", qmin, qmax);
+  ATX_REQUIRE(dtype == ATX_DT_F16 || dtype == ATX_DT_BF16,
+              "atx_fakequant_fwd_dt: dtype must be ATX_DT_F16 or ATX_DT_BF16, got %d", dtype);
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(x && scale, "atx_fakequant_fwd_dt: null pointer");
+  const dim3 grid(elem_grid(n, EW));
+  if (dtype == ATX_DT_F16)
+    hipLaunchKernelGGL(fakequant_fwd_lp_kernel<ATX_DT_F16>, grid, dim3(EW), 0, stream, x, n,
+                       scale, zero, (float)qmin, (float)qmax, q, mask, (uint8_t*)q8, nonneg);
+  else
+    hipLaunchKernelGGL(fakequant_fwd_lp_kernel<ATX_DT_BF16>, grid, dim3(EW), 0, stream, x, n,
+                       scale, zero, (float)qmin, (float)qmax, q, mask, (uint8_t*)q8, nonneg);
+  return check_launch("fakequant_fwd_lp_kernel");
+}
+
+int atx_fakequant_bwd_dt(const void* go, int go_dtype, const uint8_t* mask, long long n,
+                         const float* scale, int dtype, void* gx, hipStream_t stream) {
+  ATX_REQUIRE(n >= 0, "atx_fakequant_bwd_dt: negative size");
+  ATX_REQUIRE(dtype == ATX_DT_F16 || dtype == ATX_DT_BF16,
+              "atx_fakequant_bwd_dt: dtype must be ATX_DT_F16 or ATX_DT_BF16, got %d", dtype);
+  ATX_REQUIRE(go_dtype == ATX_DT_F32 || go_dtype == dtype,
+              "atx_fakequant_bwd_dt: go must be fp32 or the dtype of x");
+  if (n == 0) return ATX_OK;
+  ATX_REQUIRE(go && mask && scale && gx, "atx_fakequant_bwd_dt: null pointer");
+  const dim3 grid(elem_grid(n, EW));
+#define ATX_FQB(G, D) \
+  hipLaunchKernelGGL((fakequant_bwd_lp_kernel<G, D>), grid, dim3(EW), 0, stream, go, mask, n, \
+                     scale, gx)
+  if (dtype == ATX_DT_F16) {
+    if (go_dtype == ATX_DT_F32) ATX_FQB(ATX_DT_F32, ATX_DT_F16); else ATX_FQB(ATX_DT_F16, ATX_DT_F16);
+  } else {
+    if (go_dtype == ATX_DT_F32) ATX_FQB(ATX_DT_F32, ATX_DT_BF16); else ATX_FQB(ATX_DT_BF16, ATX_DT_BF16);
+  }
+#undef ATX_FQB
+  return check_launch("fakequant_bwd_lp_kernel");
 }
 
 int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32, int qmax,
@@ -614,15 +801,29 @@ int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32
   return check_launch("ema_minmax_kernel");
 }
 
-int atx_weight_scale_ema(const float* w, int O, long long inner, float qmax_w, float m32,
-                         float om32, int reset, float* scale_w, hipStream_t stream) {
+int atx_weight_scale_ema_dt(const void* w, int dtype, int O, long long inner, float qmax_w,
+                            float m32, float om32, int reset, float* scale_w,
+                            hipStream_t stream) {
   ATX_REQUIRE(O >= 0 && inner > 0, "atx_weight_scale_ema: bad size");
+  ATX_REQUIRE(dtype == ATX_DT_F32 || dtype == ATX_DT_F16 || dtype == ATX_DT_BF16,
+              "atx_weight_scale_ema: bad dtype %d", dtype);
   if (O == 0) return ATX_OK;
   ATX_REQUIRE(w && scale_w, "atx_weight_scale_ema: null pointer");
-  hipLaunchKernelGGL(weight_stats_kernel, dim3(O), dim3(EW), 0, stream, w, inner,
-                     reset ? 1 : 0, qmax_w, m32, om32, scale_w, (float*)nullptr,
-                     (float*)nullptr, (float*)nullptr);
+#define ATX_WS(D)                                                                         \
+  hipLaunchKernelGGL(weight_stats_kernel<D>, dim3(O), dim3(EW), 0, stream, w, inner,     \
+                     reset ? 1 : 0, qmax_w, m32, om32, scale_w, (float*)nullptr,          \
+                     (float*)nullptr, (float*)nullptr)
+  if (dtype == ATX_DT_F16) ATX_WS(ATX_DT_F16);
+  else if (dtype == ATX_DT_BF16) ATX_WS(ATX_DT_BF16);
+  else ATX_WS(ATX_DT_F32);
+#undef ATX_WS
   return check_launch("weight_stats_kernel");
+}
+
+int atx_weight_scale_ema(const float* w, int O, long long inner, float qmax_w, float m32,
+                         float om32, int reset, float* scale_w, hipStream_t stream) {
+  return atx_weight_scale_ema_dt(w, ATX_DT_F32, O, inner, qmax_w, m32, om32, reset, scale_w,
+                                 stream);
 }
 
 int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32, float om32,
@@ -631,7 +832,7 @@ int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32, flo
   ATX_REQUIRE(O >= 0 && inner > 0, "atx_weight_minmax_ema: bad size");
   if (O == 0) return ATX_OK;
   ATX_REQUIRE(w && w_min && w_max && scale_w && zero_w, "atx_weight_minmax_ema: null");
-  hipLaunchKernelGGL(weight_stats_kernel, dim3(O), dim3(EW), 0, stream, w, inner, 2,
+  hipLaunchKernelGGL(weight_stats_kernel<ATX_DT_F32>, dim3(O), dim3(EW), 0, stream, w, inner, 2,
                      (float)qmax, m32, om32, scale_w, zero_w, w_min, w_max);
   return check_launch("weight_stats_kernel");
 }

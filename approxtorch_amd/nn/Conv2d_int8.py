@@ -16,11 +16,15 @@ from ..backend import _lib as L
 from ..backend import ops
 
 
-def _check_stat_inputs(x, *buffers):
+def _check_stat_inputs(x, *buffers, lowp=False):
     """The kernels behind the statistic updates read x as fp32 device memory
-    and write the scale buffers in place: check both before any launch (the
-    reference's ops reject the same inputs, csrc/claude/quantization.cu:190-193)."""
-    ops.require_cuda_f32(x, "x")
+    (fp16 / bf16 as well with lowp: the *_dt kernels) and write the fp32
+    scale buffers in place: check both before any launch (the reference's
+    ops reject the same inputs, csrc/claude/quantization.cu:190-193)."""
+    if lowp:
+        ops.require_cuda_float(x, "x")
+    else:
+        ops.require_cuda_f32(x, "x")
     for name, b in buffers:
         if not b.is_cuda or b.device != x.device or b.dtype != torch.float32:
             raise RuntimeError(f"buffer {name} must be a float32 CUDA tensor on {x.device}; "
@@ -161,7 +165,7 @@ class Conv2d_int8(nn.Module):
         means every quantized x >= 0 only because the fake-quant divides by
         max(scale_x, 1e-12) > 0 (whatever scale_x holds) and qmax >= 0;
         conv2d_int8_fused checks the latter."""
-        _check_stat_inputs(x, ("scale_x", self.scale_x))
+        _check_stat_inputs(x, ("scale_x", self.scale_x), lowp=True)
         with torch.no_grad():
             xc = x.contiguous()
             stat = torch.empty((), dtype=torch.float32, device=x.device)
@@ -170,15 +174,17 @@ class Conv2d_int8(nn.Module):
             m32, om32 = _ema_coeffs(self.scale_momentum)
             denom = float((self.qmax - self.qmin) / 2)
             upper = None
+            # an fp16 / bf16 x: abs_max and the first EMA terms are that dtype's
+            dt = ops.dtype_code(xc)
             if not (dist.is_available() and dist.is_initialized()):
                 # no all-reduce in between: the EMA runs in the reduction's last launch
                 upper = torch.empty((), dtype=torch.int32, device=x.device)
-                L.call("atx_absmax_ema_upper", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat),
-                       denom, m32, om32, L.ptr(self.scale_x), L.ptr(upper), s)
+                L.call("atx_absmax_ema_upper_dt", L.ptr(xc), dt, xc.numel(), L.ptr(ws),
+                       L.ptr(stat), denom, m32, om32, L.ptr(self.scale_x), L.ptr(upper), s)
             else:
-                L.call("atx_absmax", L.ptr(xc), xc.numel(), L.ptr(ws), L.ptr(stat), s)
+                L.call("atx_absmax_dt", L.ptr(xc), dt, xc.numel(), L.ptr(ws), L.ptr(stat), s)
                 dist.all_reduce(stat, op=dist.ReduceOp.MAX)
-                L.call("atx_ema_absmax_apply", L.ptr(stat), denom, m32, om32,
+                L.call("atx_ema_absmax_apply_dt", L.ptr(stat), dt, denom, m32, om32,
                        L.ptr(self.scale_x), s)
         _bump(self.scale_x)
         return upper
@@ -186,13 +192,13 @@ class Conv2d_int8(nn.Module):
     def _update_scale_w(self):
         """Per-channel EMA of absmax(W)/qmax_w; zero channels keep their scale
         (nn/Conv2d_int8.py:148-158)."""
-        _check_stat_inputs(self.weight, ("scale_w", self.scale_w))
+        _check_stat_inputs(self.weight, ("scale_w", self.scale_w), lowp=True)
         with torch.no_grad():
             w = self.weight.detach().contiguous()
             O = w.size(0)
             m32, om32 = _ema_coeffs(self.scale_momentum)
-            L.call("atx_weight_scale_ema", L.ptr(w), O, w.numel() // max(O, 1),
-                   float(2 ** (self.weight_bits - 1) - 1), m32, om32, 0,
+            L.call("atx_weight_scale_ema_dt", L.ptr(w), ops.dtype_code(w), O,
+                   w.numel() // max(O, 1), float(2 ** (self.weight_bits - 1) - 1), m32, om32, 0,
                    L.ptr(self.scale_w), L.stream_of(w))
         _bump(self.scale_w)
 
@@ -204,11 +210,12 @@ class Conv2d_int8(nn.Module):
             qmax_w = 2 ** (self.weight_bits - 1) - 1
             w = self.weight.detach()
             if w.is_cuda:
-                _check_stat_inputs(w, ("scale_w", self.scale_w))
+                _check_stat_inputs(w, ("scale_w", self.scale_w), lowp=True)
                 wc = w.contiguous()
                 O = wc.size(0)
-                L.call("atx_weight_scale_ema", L.ptr(wc), O, wc.numel() // max(O, 1),
-                       float(qmax_w), 1.0, 0.0, 1, L.ptr(self.scale_w), L.stream_of(wc))
+                L.call("atx_weight_scale_ema_dt", L.ptr(wc), ops.dtype_code(wc), O,
+                       wc.numel() // max(O, 1), float(qmax_w), 1.0, 0.0, 1,
+                       L.ptr(self.scale_w), L.stream_of(wc))
                 _bump(self.scale_w)
                 return
             absmax = w.abs().amax(dim=tuple(range(1, w.dim())))

@@ -232,6 +232,9 @@ class Conv2d_uint8(nn.Module):
         _bump(self.w_min, self.w_max, self.scale_w, self.zero_w)
 
     def forward(self, x: torch.Tensor):
+        # the uint8 layer's kernels read fp32 activations and weights only
+        ops.require_cuda_f32(x, "x")
+        ops.require_cuda_f32(self.weight, "weight")
         kH, kW = self.weight.shape[2:]
         if self.training and self.update_scale:
             self._update_scale(x)

@@ -120,6 +120,14 @@ def bgemm_int8_custom(x, w, lut, dx_lut, dw_lut):
 
 
 # ------------------------------------------------------------- conv level
+def _image(x):
+    """The quantized image a conv Function reads: fp32 / int8 / uint8 as
+    given; the integer values of an fp16 / bf16 fake-quantized x as int8
+    (exact: |q| <= 128), the reference's `x.detach().to(torch.int8)`
+    (nn/bgemm_int8.py:246)."""
+    return x.detach().to(torch.int8) if x.dtype in ops.LOWP else x
+
+
 def _conv_setup(x, w, geom):
     """Geometry and whether the conv is depthwise (groups == C == O, the only
     grouped form the reference supports: nn/Conv2d_int8.py:35-41)."""
@@ -170,7 +178,7 @@ class _conv2d_int8_ste(Function):
     @staticmethod
     def forward(ctx, x, w, lut, geom):
         g, depthwise = _conv_setup(x, w, geom)
-        y, wq = _lut_conv(x, w, lut, g, depthwise)
+        y, wq = _lut_conv(_image(x), w, lut, g, depthwise)
         ctx.save_for_backward(x.detach().to(torch.int8), wq)
         ctx.g, ctx.depthwise = g, depthwise
         return y
@@ -196,7 +204,7 @@ class _conv2d_int8_lre(Function):
     @staticmethod
     def forward(ctx, x, w, lut, dx, dw, geom):
         g, depthwise = _conv_setup(x, w, geom)
-        y, wq = _lut_conv(x, w, lut, g, depthwise)
+        y, wq = _lut_conv(_image(x), w, lut, g, depthwise)
         ctx.save_for_backward(x.detach().to(torch.int8), wq)
         ctx.g, ctx.dx, ctx.dw, ctx.depthwise = g, dx, dw, depthwise
         return y
@@ -232,10 +240,13 @@ class _conv2d_int8_fused(Function):
                 x_upper=None):
         g, depthwise = _conv_setup(x, weight, geom)
         O = weight.size(0)
+        # an fp16 / bf16 x: fake-quant in its dtype, the STE applied in it in
+        # backward (the fused fp32 STE would round differently)
+        lowp = x.dtype if x.dtype in ops.LOWP else None
         # a 1x1, stride-1, unpadded conv reads x itself as its operand: the
         # fake-quant writes the row-offset operand directly, no byte image
-        pointwise = (not depthwise and g.KH == 1 and g.KW == 1 and g.SH == 1 and g.SW == 1
-                     and g.PH == 0 and g.PW == 0)
+        pointwise = (lowp is None and not depthwise and g.KH == 1 and g.KW == 1 and
+                     g.SH == 1 and g.SW == 1 and g.PH == 0 and g.PW == 0)
         # weight_bits <= 4: indices w + 128 in [120, 136), matrix-core LUT GEMM
         wbase = 120 if qmax_w <= 7 else None
         # Without a flag from the statistic (eval mode, data parallel training)
@@ -250,10 +261,13 @@ class _conv2d_int8_fused(Function):
         else:
             _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
                                                       q8_dtype=torch.int8, nonneg=fq_flag)
-        _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, -qmax_w, qmax_w,
-                                                            offset=128,
+        # per-channel scales promote an fp16 / bf16 weight's x / s to fp32
+        # (nn/quantization.py:100-105): the fp32 kernels on its exact values
+        _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight.detach().float(), scale_w,
+                                                            -qmax_w, qmax_w, offset=128,
                                                             want_wt=not depthwise)
-        b = None if bias is None else bias.detach().contiguous()
+        # addcmul(bias, y, s) promotes a low-precision bias to fp32 as well
+        b = None if bias is None else bias.detach().float().contiguous()
         if pointwise:
             y, _ = ops.conv_forward_rows(xt_rpad, wq, lut, g, 128,
                                          out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
@@ -275,7 +289,7 @@ class _conv2d_int8_fused(Function):
         ctx.save_for_backward(saved_x, mask_x, wq, mask_w.view(O, -1), scale_x, scale_w,
                               tx.contiguous(), tw.contiguous())
         ctx.g, ctx.has_bias, ctx.wshape = g, bias is not None, weight.shape
-        ctx.depthwise = depthwise
+        ctx.depthwise, ctx.lowp = depthwise, lowp
         return y.view(g.N, O, g.OH, g.OW)
 
     @staticmethod
@@ -284,21 +298,27 @@ class _conv2d_int8_fused(Function):
         g = ctx.g
         go = grad_output.contiguous()
         gx = gw = gb = None
+        # fp32 x: the STE fused into the data gradient; fp16 / bf16 x: the
+        # gradient wrt the quantized x in fp32, then the STE in x's dtype
+        mx, msx = (None, None) if ctx.lowp else (mask_x, sx)
         if ctx.depthwise:
             if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-                gx, gw = _lut_conv_backward(go, saved_x, wq, tx, tw, g, True, mask=mask_x,
-                                            scale=sx, mask_w=mask_w, scale_w=sw, go_sx=sx,
+                gx, gw = _lut_conv_backward(go, saved_x, wq, tx, tw, g, True, mask=mx,
+                                            scale=msx, mask_w=mask_w, scale_w=sw, go_sx=sx,
                                             go_sw=sw)
                 gx = gx if ctx.needs_input_grad[0] else None
                 gw = gw.view(ctx.wshape) if ctx.needs_input_grad[1] else None
         else:
             if ctx.needs_input_grad[0]:
-                gx = ops.conv_backward_data(go, wq, tx, g, mask=mask_x, scale=sx, go_sx=sx,
+                gx = ops.conv_backward_data(go, wq, tx, g, mask=mx, scale=msx, go_sx=sx,
                                             go_sw=sw)
             if ctx.needs_input_grad[1]:
                 gw = ops.conv_backward_weight_rows(go, (saved_x, ctx.rpad), tw, g, wq.size(0),
                                                    mask_w=mask_w, scale_w=sw, go_sx=sx,
                                                    go_sw=sw).view(ctx.wshape)
+        if gx is not None and ctx.lowp:
+            gx = ops.fakequant_per_tensor_backward(gx.view(mask_x.shape), mask_x, sx,
+                                                   dtype=ctx.lowp)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
         return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
@@ -335,8 +355,8 @@ class _conv2d_int8_custom(Function):
         # w quantized to [-qmax_w, qmax_w] with qmax_w <= 7 (weight_bits <= 4): indices
         # w + 128 lie in [120, 136); the LUT GEMM and grad_x run on the matrix cores
         ctx.wbase = 120 if qmax_w is not None and qmax_w <= 7 else None
-        y, wq, (xt, Rpad) = ops.conv_forward(x, w, lut, g, 128, 128, return_operand=True,
-                                             wbase=ctx.wbase)
+        y, wq, (xt, Rpad) = ops.conv_forward(_image(x), w, lut, g, 128, 128,
+                                             return_operand=True, wbase=ctx.wbase)
         ctx.save_for_backward(xt, wq, dx_lut, dw_lut)
         ctx.g, ctx.rpad = g, Rpad
         return y

@@ -7,7 +7,12 @@ per-tensor (ch_axis=None) or per-channel (ch_axis=int).  STE backward:
 gx = go * mask / s with mask = qmin <= x/s (+z) <= qmax on the pre-round value.
 
 Mirrors approxtorch/nn/quantization.py:37-191.  Every path runs the fused
-HIP kernels (atx_fakequant_*); tensors must live on the GPU and be fp32.
+HIP kernels (atx_fakequant_*); tensors must live on the GPU and be fp32,
+fp16 or bf16.  An fp16 / bf16 x gets torch's semantics for the reference's
+statements: with 0-dim scale (and zero point) the per-tensor v = x / s is
+computed in x's dtype and q keeps it (atx_fakequant_fwd_dt); a per-channel
+or 1-element (1-dim) scale promotes x / s, and q, to fp32, which the fp32
+kernels compute from x's exact fp32 value.
 """
 import torch
 from torch.autograd import Function
@@ -15,11 +20,27 @@ from torch.autograd import Function
 from ..backend import ops
 
 
-def _require_gpu_fp32(x, name="x"):
+def _require_gpu_float(x, name="x"):
     if not x.is_cuda:
         raise RuntimeError(f"{name} must be a GPU tensor (approxtorch_amd runs on the GPU)")
-    if x.dtype != torch.float32:
-        raise RuntimeError(f"{name} must be float32, got {x.dtype}")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"{name} must be float32, float16 or bfloat16, got {x.dtype}")
+
+
+def _promoted(x, scale, zero_point=None):
+    """x as the fp32 kernels must read it: a low-precision x stays in its
+    dtype only when torch would compute x / s (+ z) in it, i.e. with 0-dim
+    scale and zero point; a dimensioned scale promotes the statements to
+    fp32 (x converted exactly).  A 0-dim scale with a dimensioned zero point
+    (fp32 added to a low-precision quotient) is not supported."""
+    if x.dtype == torch.float32:
+        return x
+    if scale.dim() > 0:
+        return x.float()
+    if zero_point is not None and zero_point.dim() > 0:
+        raise NotImplementedError(
+            "fp16/bf16 fake-quant with a 0-dim scale needs a 0-dim zero_point")
+    return x
 
 
 def _param(p, x):
@@ -108,12 +129,13 @@ def static_quantize_int8(x, scale, qmin=-127, qmax=127, ch_axis=None):
     nn/quantization.py:153-171."""
     if qmin >= qmax:
         raise ValueError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
-    _require_gpu_fp32(x)
+    _require_gpu_float(x)
     scale = _as_f32(scale, x)
     if ch_axis is None:
-        return _static_quantize_per_tensor_symmetric.apply(x, scale, qmin, qmax)
+        return _static_quantize_per_tensor_symmetric.apply(_promoted(x, scale), scale, qmin,
+                                                           qmax)
     _check_per_channel_param('scale', scale, x, ch_axis)
-    return _static_quantize_per_channel.apply(x, scale, None, ch_axis, qmin, qmax)
+    return _static_quantize_per_channel.apply(x.float(), scale, None, ch_axis, qmin, qmax)
 
 
 def static_quantize_uint8(x, scale, zero_point, qmin=0, qmax=255, ch_axis=None):
@@ -121,11 +143,13 @@ def static_quantize_uint8(x, scale, zero_point, qmin=0, qmax=255, ch_axis=None):
     qmin, qmax).  nn/quantization.py:174-191."""
     if qmin >= qmax:
         raise ValueError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
-    _require_gpu_fp32(x)
+    _require_gpu_float(x)
     scale = _as_f32(scale, x)
     zero_point = _as_f32(zero_point, x)
     if ch_axis is None:
-        return _static_quantize_per_tensor_asymmetric.apply(x, scale, zero_point, qmin, qmax)
+        return _static_quantize_per_tensor_asymmetric.apply(_promoted(x, scale, zero_point),
+                                                            scale, zero_point, qmin, qmax)
     _check_per_channel_param('scale', scale, x, ch_axis)
     _check_per_channel_param('zero_point', zero_point, x, ch_axis)
-    return _static_quantize_per_channel.apply(x, scale, zero_point, ch_axis, qmin, qmax)
+    return _static_quantize_per_channel.apply(x.float(), scale, zero_point, ch_axis, qmin,
+                                              qmax)

@@ -36,6 +36,13 @@ enum {
   ATX_LUT_F32 = 2,   /* anything else: fp32 accumulation fallback      */
 };
 
+/* Element types of activations read by the *_dt entry points. */
+enum {
+  ATX_DT_F32 = 0,
+  ATX_DT_F16 = 1,    /* IEEE binary16                 */
+  ATX_DT_BF16 = 2,   /* bfloat16 (the high half of an fp32) */
+};
+
 /* Convolution geometry (NCHW input, OIHW weight). */
 typedef struct atx_conv_geom {
   int N, C, H, W;          /* input image                       */
@@ -284,6 +291,23 @@ int atx_fakequant_rows(const float* x, int N, int K, int L, const float* scale,
                        uint8_t* mask, uint16_t* xt, int Rpad, int* upper,
                        hipStream_t stream);
 
+/* Per-tensor fake-quant of an fp16 / bf16 x (dtype ATX_DT_F16 or
+ * ATX_DT_BF16), the reference's unfused statements for a non-fp32 input
+ * (nn/quantization.py:44-52,72-80) as torch evaluates them in x's dtype D:
+ * s = max(scale, 1e-12) cast to D; v = x / s rounded to D (+ zero cast to D,
+ * rounded to D); mask = qmin <= v <= qmax; q = clamp(round(v), qmin, qmax)
+ * in D (nullable).  mask, q8 and nonneg as atx_fakequant_fwd. */
+int atx_fakequant_fwd_dt(const void* x, int dtype, long long n, const float* scale,
+                         const float* zero, int qmin, int qmax, void* q, uint8_t* mask,
+                         void* q8, int* nonneg, hipStream_t stream);
+
+/* Its backward, gx = go * mask / s in D (nn/quantization.py:58-62,86-91):
+ * go of go_dtype ATX_DT_F32 (rounded to D first, as autograd casts a
+ * gradient to its input's dtype) or D; the product with the mask exact (a
+ * 0 * inf is NaN), the quotient by s cast to D rounded to D. */
+int atx_fakequant_bwd_dt(const void* go, int go_dtype, const uint8_t* mask, long long n,
+                         const float* scale, int dtype, void* gx, hipStream_t stream);
+
 /* gx = (mask ? go : 0) / max(scale, 1e-12); scale has 1 (per-tensor) or
  * C (per-channel, channel = (i / inner) % C) elements.
  * csrc/claude/quantization.cu:112-143; nn/quantization.py:110-113. */
@@ -382,6 +406,19 @@ int atx_absmax_ema(const float* x, long long n, unsigned int* ws, float* stat_ou
 int atx_absmax_ema_upper(const float* x, long long n, unsigned int* ws, float* stat_out,
                          float denom, float m32, float om32, float* scale, int* upper,
                          hipStream_t stream);
+/* The absmax statistic and EMA of an activation x of any ATX_DT_* dtype
+ * (nn/Conv2d_int8.py:137-146 evaluated by torch in x's dtype D): stat =
+ * max|x| (exact), cur = stat / denom and m * cur rounded to D (abs_max is a
+ * D scalar), (1 - m) * scale and the sum in fp32.  ATX_DT_F32 gives the
+ * fp32 entry points' results.  No counterpart in the reference's kernels:
+ * its layer runs these statements in torch for a non-fp32 x. */
+int atx_absmax_dt(const void* x, int dtype, long long n, unsigned int* ws, float* stat_out,
+                  hipStream_t stream);
+int atx_ema_absmax_apply_dt(const float* stat, int dtype, float denom, float m32, float om32,
+                            float* scale, hipStream_t stream);
+int atx_absmax_ema_upper_dt(const void* x, int dtype, long long n, unsigned int* ws,
+                            float* stat_out, float denom, float m32, float om32, float* scale,
+                            int* upper, hipStream_t stream);
 /* atx_minmax then atx_ema_minmax_apply, fused the same way. */
 int atx_minmax_ema(const float* x, long long n, unsigned int* ws, float* mn_out,
                    float* mx_out, float m32, float om32, int qmax, float* x_min,
@@ -396,6 +433,12 @@ int atx_ema_minmax_apply(const float* mn, const float* mx, float m32, float om32
 int atx_weight_scale_ema(const float* w, int O, long long inner, float qmax_w,
                          float m32, float om32, int reset, float* scale_w,
                          hipStream_t stream);
+/* atx_weight_scale_ema over a weight of any ATX_DT_* dtype: for fp16 / bf16
+ * absmax / qmax_w is rounded to that dtype, as torch computes it for such a
+ * weight (nn/Conv2d_int8.py:155,166); the EMA itself stays fp32. */
+int atx_weight_scale_ema_dt(const void* w, int dtype, int O, long long inner, float qmax_w,
+                            float m32, float om32, int reset, float* scale_w,
+                            hipStream_t stream);
 /* Per-channel weight min/max EMA + uint8 qparams (nn/Conv2d_uint8.py:242-255). */
 int atx_weight_minmax_ema(const float* w, int O, long long inner, float m32,
                           float om32, int qmax, float* w_min, float* w_max,

@@ -207,6 +207,79 @@ def fakequant_backward(go, mask, scale):
     return (np.where(mask, np.asarray(go, dtype=f32), f32(0)) / s).astype(f32)
 
 
+# ------------------------------------------------ fp16 / bf16 activations
+def round_to(v, dtype):
+    """fp32 values rounded to dtype ("f16" or "bf16", round to nearest even;
+    bf16 NaN -> the canonical 0x7fc0) and returned as fp32: the value torch
+    stores for an elementwise result of that dtype computed in fp32."""
+    v = np.asarray(v, dtype=f32)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):
+            return v.astype(np.float16).astype(f32)
+    if dtype == "bf16":
+        u = v.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
+        r = np.where(np.isnan(v), np.uint32(0x7FC00000), r).astype(np.uint32)
+        return r.view(f32)
+    raise ValueError(dtype)
+
+
+def fakequant_lowp(x, scale, qmin, qmax, dtype, zero=None):
+    """(q, mask) of an fp16 / bf16 x with 0-dim scale (and zero point): the
+    reference's unfused statements (nn/quantization.py:44-52,72-80) as torch
+    evaluates them in that dtype -- s = clamp(scale, 1e-12) cast to it, v =
+    x / s rounded to it (+ zero cast to it, rounded), mask on v, q =
+    clamp(round(v)).  x holds the dtype's values as fp32."""
+    x = np.asarray(x, dtype=f32)
+    s = round_to(np.maximum(f32(scale), f32(1e-12)), dtype)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        v = round_to(x / s, dtype)
+        if zero is not None:
+            v = round_to(v + round_to(f32(zero), dtype), dtype)
+        mask = (v >= qmin) & (v <= qmax)
+        q = np.clip(np.rint(v), f32(qmin), f32(qmax)).astype(f32)
+    return q, mask
+
+
+def fakequant_lowp_backward(go, mask, scale, dtype):
+    """grad_x = grad_output * mask.to(dtype) / s in dtype (nn/quantization.py:
+    58-62): go (fp32 or the dtype's values) rounded to the dtype as autograd
+    casts it, the exact product with the mask, the quotient by s cast to the
+    dtype rounded to it."""
+    g = round_to(go, dtype)
+    s = round_to(np.maximum(f32(scale), f32(1e-12)), dtype)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        gm = (g * np.asarray(mask, dtype=f32)).astype(f32)
+        return round_to(gm / s, dtype)
+
+
+def ema_absmax_lowp(x, scale_x, m, dtype, denom=127.0):
+    """nn/Conv2d_int8.py:137-146 for an x of dtype: abs_max is a scalar of
+    that dtype, so cur = abs_max / denom and m * cur are rounded to it;
+    (1 - m) * scale_x and the sum are fp32 (the 0-dim tensors promote)."""
+    x = np.asarray(x, dtype=f32)
+    absmax = np.max(np.abs(x)) if not np.isnan(x).any() else f32(np.nan)
+    cur = round_to(div_by_number(absmax, denom), dtype)
+    a = round_to(f32(m) * cur, dtype)
+    b = f32(f32(1 - m) * f32(scale_x))
+    return f32(f32(a) + b)
+
+
+def weight_scale_ema_lowp(w, scale_w, m, qmax_w, dtype, reset=False):
+    """nn/Conv2d_int8.py:148-158 (reset: 160-167) for an fp16 / bf16 weight:
+    absmax / qmax_w is rounded to the weight's dtype, torch.where with the fp32
+    scale promotes it back exactly, the EMA is fp32."""
+    w = np.asarray(w, dtype=f32).reshape(w.shape[0], -1)
+    absmax = np.abs(w).max(axis=1)
+    cur_d = round_to(div_by_number(absmax, qmax_w), dtype)
+    if reset:
+        return np.where(absmax > 0, cur_d, f32(1)).astype(f32)
+    cur = np.where(absmax > 0, cur_d, scale_w).astype(f32)
+    a = (f32(m) * cur).astype(f32)
+    b = (f32(1 - m) * np.asarray(scale_w, dtype=f32)).astype(f32)
+    return (a + b).astype(f32)
+
+
 def ema_scalar(m, cur, old):
     """m*cur + (1-m)*old with both python scalars cast to fp32 and each
     operation rounded to fp32 (the torch op sequence of nn/Conv2d_int8.py:145)."""
@@ -324,11 +397,17 @@ def gemm_grads(go, xi, wi, kind, tables=None, signed=True, absolute=False):
 
 
 # ---------------------------------------------------------------- the layers
-def conv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weight_bits=8):
+def conv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weight_bits=8,
+                      x_dtype=None):
     """Conv2d_int8.forward with given scales (nn/Conv2d_int8.py:171-220).
-    Returns y (fp64), and the intermediates needed by the backward."""
+    Returns y (fp64), and the intermediates needed by the backward.  x_dtype
+    "f16" / "bf16": x holds that dtype's values and is fake-quantized in it
+    (fakequant_lowp); the weight stays fp32 (its per-channel scale promotes)."""
     qmax_w = 2 ** (weight_bits - 1) - 1
-    qx, mx = fakequant(x, scale_x, -127, 127)
+    if x_dtype is None:
+        qx, mx = fakequant(x, scale_x, -127, 127)
+    else:
+        qx, mx = fakequant_lowp(x, scale_x, -127, 127, x_dtype)
     O = weight.shape[0]
     qw, mw = fakequant(weight, np.asarray(scale_w, dtype=f32).reshape(O, 1, 1, 1), -qmax_w,
                        qmax_w)
@@ -349,11 +428,15 @@ def conv_int8_forward(x, weight, bias, lut, scale_x, scale_w, k, s, p, d, weight
     return y.reshape(N, O, OH, OW), ctx
 
 
-def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d, absolute=False):
+def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d, absolute=False,
+                       x_dtype=None):
     """Gradients of the int8 layer (fp64): the reference's composition of the
     fake-quant STE backward, the conv Function backward (nn/bgemm_int8.py
     conv level) and the dequant addcmul.  absolute=True gives the sum of
-    |terms| of every gradient element instead (a tolerance bound)."""
+    |terms| of every gradient element instead (a tolerance bound).  x_dtype
+    "f16" / "bf16": gx is the x fake-quant's gradient in that dtype
+    (fakequant_lowp_backward of the fp32-rounded gradient of the quantized x;
+    with absolute, the bound of that gradient before the STE, divided by s)."""
     N, O = go.shape[:2]
     go = np.abs(go) if absolute else go
     g = np.asarray(go, dtype=np.float64).reshape(N, O, -1) * \
@@ -362,7 +445,10 @@ def conv_int8_backward(go, ctx, scale_x, scale_w, kind, tables, k, s, p, d, abso
                            absolute=absolute)
     gqx = fold(gcol, ctx["shape"], k, s, p, d)
     sx = max(float(f32(scale_x)), 1e-12)
-    gx = np.where(ctx["mx"], gqx, 0.0) / sx
+    if x_dtype is not None and not absolute:
+        gx = fakequant_lowp_backward(gqx.astype(f32), ctx["mx"], scale_x, x_dtype)
+    else:
+        gx = np.where(ctx["mx"], gqx, 0.0) / sx
     sw = np.maximum(np.asarray(scale_w, dtype=np.float64), 1e-12)
     gw = np.where(ctx["mw"].reshape(O, -1), gwq, 0.0) / sw[:, None]
     gb = np.asarray(go, dtype=np.float64).sum(axis=(0, 2, 3))

@@ -273,7 +273,7 @@ def test_fakequant_rejects_inputs_the_reference_rejects():
     x = torch.randn(64, device=DEV)
     s = torch.tensor(0.1, device=DEV)
     with pytest.raises(RuntimeError, match="float32"):
-        ops.fakequant_per_tensor(x.half(), s, -127, 127)
+        ops.fakequant_per_tensor(x.double(), s, -127, 127)
     with pytest.raises(RuntimeError, match="CUDA"):
         ops.fakequant_per_tensor(x, s.cpu(), -127, 127)
     with pytest.raises(RuntimeError, match="scalar"):
@@ -293,14 +293,19 @@ def test_fakequant_rejects_inputs_the_reference_rejects():
         ops.fakequant_per_channel(x.view(4, 16), torch.ones(3, device=DEV), -7, 7)
     with pytest.raises(RuntimeError, match="float32"):
         torch.ops.approxtorch.fakequant_per_tensor_claude.default(x.half(), s, -127, 127)
+    with pytest.raises(RuntimeError, match="float32"):
+        torch.ops.approxtorch.fakequant_per_tensor_backward_claude.default(x.half(), m, s)
     torch.cuda.synchronize()
 
 
-def test_layers_reject_non_fp32_inputs():
+def test_layers_reject_inputs_they_cannot_read():
+    """Conv2d_int8 reads fp32 / fp16 / bf16 activations (fp64 is refused);
+    Conv2d_uint8 reads fp32 only."""
     lut = t(perturbed_lut(1))
     l8 = at.nn.Conv2d_int8(3, 4, 3, lut, padding=1).to(DEV).train()
-    with pytest.raises(RuntimeError, match="float32"):
-        l8(torch.randn(1, 3, 5, 5, device=DEV).half())
+    with pytest.raises(RuntimeError, match="float32, float16 or bfloat16"):
+        l8(torch.randn(1, 3, 5, 5, device=DEV).double())
+    assert l8(torch.randn(1, 3, 5, 5, device=DEV).half()).dtype == torch.float32
     lu = at.nn.Conv2d_uint8(3, 4, 3, lut, padding=1).to(DEV).train()
     with pytest.raises(RuntimeError, match="float32"):
         lu(torch.randn(1, 3, 5, 5, device=DEV).to(torch.bfloat16))

@@ -532,3 +532,36 @@ def test_lre_table_roles_with_distinct_slopes():
     # the roles swapped give something else
     sx, _ = O.gemm_grads(go, xi, wi, "lre", (gb, np.zeros(256)))
     assert not np.allclose(sx, want_x)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_round_to_matches_torch_conversion(dtype):
+    """oracle.round_to against torch's fp32 -> fp16 / bf16 conversion (round
+    to nearest even): ties at both parities, subnormals, overflow, inf, NaN."""
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    v = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 10,
+                        rng.standard_normal(2000).astype(np.float32) * 1e-6,
+                        np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -8, 1 + 3 * 2 ** -8,
+                                  65519.0, 65520.0, 3.4e38, -3.4e38, np.inf, -np.inf, 0.0,
+                                  -0.0], np.float32)])
+    want = torch.from_numpy(v).to(tdt).float().numpy()
+    got = O.round_to(v, dtype)
+    assert np.array_equal(got, want)
+    assert np.isnan(O.round_to(np.array([np.nan], np.float32), dtype)).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_fakequant_lowp_differs_from_fp32_and_keeps_integers(dtype):
+    """The dtype's rounding of s and of x / s changes some quantized values
+    against the fp32 fake-quant of the same x (so the semantics matter), q
+    is integer-valued and within [qmin, qmax], and the gradient is nonzero
+    exactly on the mask."""
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    x = torch.from_numpy((rng.standard_normal(50000) * 3).astype(np.float32)).to(tdt).float()
+    x = x.numpy()
+    q, m = O.fakequant_lowp(x, np.float32(0.0371), -127, 127, dtype)
+    q32, _ = O.fakequant(x, np.float32(0.0371), -127, 127)
+    assert (q != q32).sum() > 0
+    assert np.array_equal(q, np.rint(q)) and q.min() >= -127 and q.max() <= 127
+    g = O.fakequant_lowp_backward(np.ones_like(x), m, np.float32(0.0371), dtype)
+    assert np.all((g != 0) == m)
