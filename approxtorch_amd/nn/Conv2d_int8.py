@@ -66,7 +66,8 @@ class Conv2d_int8(nn.Module):
                  groups: int = 1,
                  update_scale: bool = True,
                  scale_momentum: float = 0.05,
-                 weight_bits: int = 8):
+                 weight_bits: int = 8,
+                 save_image: bool = False):
         super().__init__()
         self.in_channels = in_channels
         self.out_channels = out_channels
@@ -94,6 +95,13 @@ class Conv2d_int8(nn.Module):
             raise ValueError(f"scale_momentum must be between 0 and 1, got {scale_momentum}")
         self.scale_momentum = scale_momentum
         self.update_scale = update_scale
+        # No counterpart in the reference's constructor (an added keyword):
+        # False keeps the forward's row-offset operand (uint16 per unfolded
+        # tap) for grad_w; True keeps the int8 image instead (1 byte per
+        # input element, the reference's saved tensor) and grad_w unfolds it
+        # again in its loads (atx_conv_bwd_weight): less memory, slower
+        # backward.
+        self.save_image = save_image
 
         self.register_buffer('lut', lut)
         self.weight = nn.Parameter(torch.empty(self.out_channels,
@@ -247,7 +255,8 @@ class Conv2d_int8(nn.Module):
                 tx = tw = bgemm_int8.decode_table(x.device)
             return bgemm_int8.conv2d_int8_fused(x, self.weight, self.bias, self.scale_x,
                                                 self.scale_w, self.lut, tx, tw, geom,
-                                                self.qmin, self.qmax, qmax_w, x_upper=upper)
+                                                self.qmin, self.qmax, qmax_w, x_upper=upper,
+                                                save_image=getattr(self, "save_image", False))
 
         x = quantization.static_quantize_int8(x, self.scale_x, self.qmin, self.qmax)
         w = quantization.static_quantize_int8(self.weight, self.scale_w, -qmax_w, qmax_w,

@@ -237,7 +237,7 @@ class _conv2d_int8_fused(Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax, qmax_w,
-                x_upper=None):
+                x_upper=None, save_image=False):
         g, depthwise = _conv_setup(x, weight, geom)
         O = weight.size(0)
         # an fp16 / bf16 x: fake-quant in its dtype, the STE applied in it in
@@ -245,8 +245,8 @@ class _conv2d_int8_fused(Function):
         lowp = x.dtype if x.dtype in ops.LOWP else None
         # a 1x1, stride-1, unpadded conv reads x itself as its operand: the
         # fake-quant writes the row-offset operand directly, no byte image
-        pointwise = (lowp is None and not depthwise and g.KH == 1 and g.KW == 1 and
-                     g.SH == 1 and g.SW == 1 and g.PH == 0 and g.PW == 0)
+        pointwise = (lowp is None and not save_image and not depthwise and g.KH == 1 and
+                     g.KW == 1 and g.SH == 1 and g.SW == 1 and g.PH == 0 and g.PW == 0)
         # weight_bits <= 4: indices w + 128 in [120, 136), matrix-core LUT GEMM
         wbase = 120 if qmax_w <= 7 else None
         # Without a flag from the statistic (eval mode, data parallel training)
@@ -277,6 +277,13 @@ class _conv2d_int8_fused(Function):
         elif depthwise:
             y = ops.dwconv_forward(xq8, wq, lut, g, 128, out_kind=ops.L.ATX_OUT_DEQUANT,
                                    sx=scale_x, sw=scale_w, bias=b)
+            saved_x, ctx.rpad = xq8, None
+        elif save_image:
+            # keep the int8 image (1 byte per input element); grad_w unfolds
+            # it again in its loads
+            y, _ = ops.conv_forward(
+                xq8, wq, lut, g, 128, 128, out_kind=ops.L.ATX_OUT_DEQUANT, sx=scale_x,
+                sw=scale_w, bias=b, packed_w=(wq, wt, Opad), wbase=wbase, x_upper=x_upper)
             saved_x, ctx.rpad = xq8, None
         else:
             # the row-offset operand is kept for the weight gradient: its
@@ -312,7 +319,11 @@ class _conv2d_int8_fused(Function):
             if ctx.needs_input_grad[0]:
                 gx = ops.conv_backward_data(go, wq, tx, g, mask=mx, scale=msx, go_sx=sx,
                                             go_sw=sw)
-            if ctx.needs_input_grad[1]:
+            if ctx.needs_input_grad[1] and ctx.rpad is None:
+                gw = ops.conv_backward_weight(go, saved_x, tw, g, wq.size(0), 128,
+                                              mask_w=mask_w, scale_w=sw, go_sx=sx,
+                                              go_sw=sw).view(ctx.wshape)
+            elif ctx.needs_input_grad[1]:
                 gw = ops.conv_backward_weight_rows(go, (saved_x, ctx.rpad), tw, g, wq.size(0),
                                                    mask_w=mask_w, scale_w=sw, go_sx=sx,
                                                    go_sw=sw).view(ctx.wshape)
@@ -321,22 +332,24 @@ class _conv2d_int8_fused(Function):
                                                    dtype=ctx.lowp)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
-        return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None, None, None
 
 
 def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax,
-                      qmax_w, x_upper=None):
+                      qmax_w, x_upper=None, save_image=False):
     """x_upper: optional device int32 flag, written for this same x, that is
     nonzero only when x >= 0 everywhere (Conv2d_int8's training-mode statistic,
     atx_absmax_ema_upper); the LUT GEMM then builds half-height tables.  The
     promise x >= 0 => every quantized x >= 0 holds because the fake-quant
     divides by max(scale_x, 1e-12) > 0 and qmax >= 0.  Without it, the
-    fake-quant writes such a flag from the quantized values themselves."""
+    fake-quant writes such a flag from the quantized values themselves.
+    save_image: keep the int8 image for grad_w instead of the row-offset
+    operand (less memory; grad_w unfolds the image in its loads)."""
     if qmax < 0 or qmin > qmax:
         raise RuntimeError(f"qmin/qmax must satisfy qmin <= qmax and qmax >= 0, got "
                            f"[{qmin}, {qmax}]")
     return _conv2d_int8_fused.apply(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom,
-                                    qmin, qmax, qmax_w, x_upper)
+                                    qmin, qmax, qmax_w, x_upper, save_image)
 
 
 class _conv2d_int8_custom(Function):

@@ -97,6 +97,8 @@ def parse():
                     help="also measure the LDS read throughput (roofline denominator)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run three 512 MiB device copies first (PMC byte-counter calibration)")
+    ap.add_argument("--save-image", action="store_true",
+                    help="int8 layers keep the int8 image for grad_w (Conv2d_int8 save_image)")
     return ap.parse_args()
 
 
@@ -384,6 +386,43 @@ def dwconv_microbench(torch, reps=20):
             "op_ms_all_layers": round(ms_op, 3), "layers": per_layer}
 
 
+def layer_memory(torch):
+    """Forward + backward peak memory (MiB) of one Conv2d_int8 (LRE, training mode)
+    on the reference's memory benchmark layer (B64, C64, 56^2, 3x3 64 -> 64;
+    its NOTES quote 1207 -> 277 MB for its own layer), above the memory held
+    before the forward (input, parameters, tables): the default, which keeps
+    the forward's row-offset operand for grad_w, and save_image=True, which
+    keeps the int8 image instead."""
+    from approxtorch_amd import workloads
+    out = {}
+    lut = torch.from_numpy(workloads.lut_perturbed(0)).cuda()
+    dx, dw = (t.float().cuda() for t in workloads.lre_tables(lut.cpu().numpy()))
+    for save_image in (False, True):
+        torch.manual_seed(0)
+        layer = at_nn().Conv2d_int8(64, 64, 3, lut, grad="lre", dx=dx, dw=dw, padding=1,
+                                    save_image=save_image).cuda().train()
+        x = torch.randn(64, 64, 56, 56, device="cuda", requires_grad=True)
+        go = torch.randn(64, 64, 56, 56, device="cuda")
+        layer(x).backward(go)                       # first call: LUT images, workspaces
+        x.grad = None
+        layer.weight.grad = None
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        m0 = torch.cuda.memory_allocated()
+        layer(x).backward(go)
+        torch.cuda.synchronize()
+        key = "save_image" if save_image else "default"
+        out[key] = round((torch.cuda.max_memory_allocated() - m0) / 2 ** 20, 1)
+        del layer, x, go
+    out["reference_notes"] = {"before": 1207, "after": 277}
+    return out
+
+
+def at_nn():
+    import approxtorch_amd
+    return approxtorch_amd.nn
+
+
 def cpu_host():
     """The host the CPU baseline runs on: os.cpu_count(), the torch threads
     used (torch's default: OMP_NUM_THREADS, the box's CPU share) and the CPU
@@ -451,6 +490,11 @@ def main():
         return main_c1(torch, args)
     name = args.workload
     model, opt, x, y, cfg = workloads.build_training_workload(name, dev)
+    if args.save_image:
+        import approxtorch_amd
+        for mod in model.modules():
+            if isinstance(mod, approxtorch_amd.nn.Conv2d_int8):
+                mod.save_image = True
     macs_fwd = workloads.conv_lut_macs(model, tuple(x.shape))
     timer = GemmTimer()
     timer.install()
@@ -485,7 +529,7 @@ def main():
                                f"{cfg['hw']}x{cfg['hw']} {cfg['qtype']} grad={cfg['grad']} "
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
-                   "forward_lut_macs": macs_fwd},
+                   "forward_lut_macs": macs_fwd, "save_image": bool(args.save_image)},
         "roofline": roofline(timer, dt, name, narrow=cfg["weight_bits"] <= 4),
         "peak_memory_MB": round(peak_mem / 2 ** 20, 1),
     }
@@ -493,6 +537,7 @@ def main():
         result["lut_gemm_c3_GLUTMACs"] = lut_gemm_microbench(torch)
         result["gemm2d_GLUTMACs"] = gemm2d_microbench(torch)
         result["dwconv_mobilenetv2"] = dwconv_microbench(torch)
+        result["layer_memory_MB"] = layer_memory(torch)
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
     if not args.no_cpu_baseline:

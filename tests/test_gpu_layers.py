@@ -81,6 +81,44 @@ def test_conv2d_int8_forward_backward(kind, gi):
     close(layer.bias.grad, gb, ab)
 
 
+@pytest.mark.parametrize("gi", [0, 1, 2])
+def test_conv2d_int8_save_image_mode(gi):
+    """save_image=True keeps the int8 image instead of the row-offset operand
+    and unfolds it again for grad_w: identical forward sums and grad_x, grad_w
+    against the oracle (the memory it saves is measured at size by bench.py's
+    layer_memory)."""
+    gm = GEOMS[gi]
+    lut = perturbed_lut(11)
+    dx, dw = O.lre_tables(lut)
+    outs = []
+    for save_image in (False, True):
+        torch.manual_seed(3)
+        layer = at.nn.Conv2d_int8(16, 32, gm["k"], torch.from_numpy(lut).to(DEV), grad="lre",
+                                  dx=torch.from_numpy(dx).to(DEV), dw=torch.from_numpy(dw).to(DEV),
+                                  bias=True, stride=gm["s"], padding=gm["p"], dilation=gm["d"],
+                                  save_image=save_image).to(DEV).eval()
+        x = torch.randn(4, 16, 20, 20, device=DEV, generator=torch.Generator(DEV).manual_seed(1))
+        with torch.no_grad():
+            layer.scale_x.fill_(float(x.abs().max()) / 120.0)
+        xr = x.clone().requires_grad_()
+        y = layer(xr)
+        go = torch.randn(y.shape, device=DEV, generator=torch.Generator(DEV).manual_seed(2))
+        y.backward(go)
+        outs.append((y.detach(), xr.grad, layer.weight.grad, layer, x, go))
+    (y0, gx0, gw0, l0, x, go), (y1, gx1, gw1, _, _, _) = outs
+    assert torch.equal(y0, y1) and torch.equal(gx0, gx1)
+    k2, s2, p2, d2 = (gm["k"],) * 2, (gm["s"],) * 2, (gm["p"],) * 2, (gm["d"],) * 2
+    sx, sw = np.float32(l0.scale_x.item()), l0.scale_w.cpu().numpy()
+    _, ctx = O.conv_int8_forward(x.cpu().numpy(), l0.weight.detach().cpu().numpy(),
+                                 l0.bias.detach().cpu().numpy(), lut, sx, sw, k2, s2, p2, d2)
+    _, gw, _ = O.conv_int8_backward(go.cpu().numpy(), ctx, sx, sw, "lre", (dx, dw), k2, s2, p2,
+                                    d2)
+    _, aw, _ = O.conv_int8_backward(go.cpu().numpy(), ctx, sx, sw, "lre", (dx, dw), k2, s2, p2,
+                                    d2, absolute=True)
+    close(gw1, gw, aw)
+    close(gw0, gw, aw)
+
+
 @pytest.mark.parametrize("kind", ["ste", "lre"])
 @pytest.mark.parametrize("gi", [0, 1, 4, 5])
 def test_conv2d_int8_depthwise_forward_backward(kind, gi):
