@@ -23,13 +23,15 @@
 //           of a lane collect its four channels, and after a quad's last
 //           channel tile the four lanes of a row group are summed with DPP
 //           and stored.
-//   grad_w: a workgroup owns one 16-channel tile and loops over all quads of
-//           taps with its dy values in registers; the lane's partial sums
-//           acc[s][c] are combined over the 16 row groups of a wave with DPP
-//           (register indices chosen so every lane adds the same tap), then
-//           over the waves through LDS in a two-stage pipeline that needs no
-//           extra barrier, and written as one partial slice per row tile;
-//           the slices are summed in a fixed order.
+//   grad_w: contracts over the rows.  L % 4 == 0: a workgroup keeps eight
+//           taps' tables resident and walks a chunk of row steps, loading dy
+//           per step (custom_dw_kernel).  Otherwise a workgroup owns one
+//           16-channel tile of one row tile and streams all tap quads with
+//           its dy in registers (custom_dw_tile_kernel).  Either way the
+//           lane's partial sums are combined over the 16 row groups of a wave
+//           with DPP (register indices chosen so every lane adds the same
+//           tap), then over the waves through LDS, into one partial slice
+//           per row chunk / row tile; the slices are summed in a fixed order.
 // The table entries must be finite (padding rows of a partial row tile read
 // table row 0 with dy = 0).
 #include "atx_internal.h"
@@ -37,6 +39,10 @@
 
 #include <algorithm>
 #include <type_traits>
+
+#ifndef ATX_DW_WAVES
+#define ATX_DW_WAVES 8           // waves per grad_w workgroup (resident tables)
+#endif
 
 namespace atx {
 namespace cg {
@@ -59,10 +65,11 @@ struct Params {
   const float* tab;        // transposed pair table: tab[w * 256 + v] = T[v][w]
   const float* dy;         // [N][O][L]
   const float* dys;        // grad_w: per-channel factor of dy [O] (nullable)
-  float* out;              // grad_x [N][K][L], or the grad_w slices [tiles_r][O][K]
+  float* out;              // grad_x [N][K][L], or the grad_w slices [row chunks][O][K]
   int K, R, L, O;
   int tiles_r, tiles_o, nq; // nq = quads of taps
-  int kq_chunk, kchunks;    // grad_w: quads per workgroup, workgroups per (row, channel) tile
+  int kq_chunk, kchunks;    // quads per workgroup, tap chunks
+  int rchunk, rsteps;       // grad_w (resident tables): steps per workgroup, steps over R
 };
 
 // DPP helpers (quad_perm / row_shr controls of the VOP DPP encoding).
@@ -402,10 +409,18 @@ custom_dx_kernel(const Params p) {
   if constexpr (!MULTI) flush(j0);
 }
 
-// ----------------------------------------------------------------- grad_w
+// ---------------------------------------- grad_w, tables rebuilt per row tile
+// For L % 4 != 0 (rows of a quad straddle images, so dy is read one float at
+// a time): a workgroup owns one 16-channel tile over 2048 rows, loads its dy
+// once into registers and streams the tap quads through the table pipeline
+// (split over several workgroups when the (row, channel) tile grid is smaller
+// than the GPU, each writing its own taps' entries of the row tile's slice).
+// The lane's partials are reduced over the 16 row groups of a wave with DPP
+// row_shr, then over the waves through a two-stage LDS pipeline that needs no
+// extra barrier, into one partial slice per row tile.
 template <bool VEC>
 __global__ void __launch_bounds__(NT, 1)
-custom_dw_kernel(const Params p) {
+custom_dw_tile_kernel(const Params p) {
   __shared__ __align__(16) unsigned char smem[2 * QTAB];
   __shared__ float red1[2][RED1];          // [buf][wave][row q][g][tap][c]
   __shared__ float red2[2][RED2];          // [buf][wave][tap * 16 + o_local]
@@ -528,6 +543,259 @@ custom_dw_kernel(const Params p) {
   stage2(nsteps - 1);
   __syncthreads();
   stage3(nsteps - 1);
+}
+
+// ----------------------------------------------------------------- grad_w
+// For L % 4 == 0.  grad_w contracts over the rows, so a workgroup keeps the
+// tables of NB quads of taps resident for its whole run (NB = 2: eight taps,
+// 128 KiB) and walks a range of row tiles: a tap's 16 KiB table is built once
+// per workgroup, not once per (row tile, tap), and the loop over the rows
+// has no LDS writes and no barriers.  Workgroup (channel tile to, tap chunk kc = quads
+// NB kc .. NB kc + NB - 1, row chunk rc = row tiles rc * rchunk ..).  Lane
+// (rg, g) owns channels 4g..4g+3 of the tile and rows 256 wave + 64 h +
+// 4 rg + m of every row tile; per row quad h it loads its rows' dy (four
+// channels) and the rows' offsets in the quads' tap slots, and accumulates
+// acc[b][s][c] for tap 4(NB kc + b) + ((rg + s) & 3) (the operand's slot
+// rotation, which keeps the reads conflict-free) over all its rows.  The
+// loads of the next row quad are issued before the current one is summed.
+// At the end the partials are combined over the row groups of a wave with
+// DPP row_shr, then over the waves and row quads through LDS in a fixed
+// order into the row chunk's slice [rchunks][O][K]; split_sum adds the slices
+// in a fixed order.
+
+// dy offsets of the lane's row quads (L % 4 == 0: a quad of rows never
+// straddles two images, so its dy is one 16-byte load per channel), advanced
+// one step of rows at a time without divisions: per quad h the byte offset
+// of dy[n][o_lane][l] of its first row, l and the row.
+struct DyWalk {
+  unsigned off[NQ];
+  int l[NQ];
+  int r[NQ];
+};
+
+__device__ __forceinline__ void dy_walk_init(const Params& p, int r0, int o_lane, DyWalk& d) {
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    const int rq = r0 + NRG * RQ * h;
+    const int n = rq / p.L, l = rq - n * p.L;
+    d.r[h] = rq;
+    d.l[h] = l;
+    d.off[h] = (unsigned)((((long long)n * p.O + o_lane) * p.L + l) * 4);
+  }
+}
+
+// A step of RS = q L + rem rows: step = 4 (q O L + rem), wrap = 4 (O L - L)
+// when l passes L (unsigned arithmetic; the offsets stay below 2^32, checked
+// on the host).
+__device__ __forceinline__ void dy_walk_next(DyWalk& d, int h, int RS, int L, int rem,
+                                             unsigned step, unsigned wrap) {
+  const int l = d.l[h] + rem;
+  const bool w = l >= L;             // selects, no branch
+  d.r[h] += RS;
+  d.l[h] = w ? l - L : l;
+  d.off[h] = d.off[h] + step + (w ? wrap : 0u);
+}
+
+// dy of row quad h for the lane's four channels (ob = tile base): v[m][c].
+// Valid offsets are below 2^31 (dy < 2 GiB); bit 31 set puts a load past the
+// buffer, which returns 0 (arithmetic, not a branch: the loads stay
+// unconditional).
+__device__ __forceinline__ void load_dy_quad(__amdgpu_buffer_rsrc_t dyr, const DyWalk& d, int h,
+                                             int R, int L, int ob, int valid,
+                                             float (&v)[RQ][4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const unsigned bad = (unsigned)((c >= valid) | (d.r[h] >= R));
+    const float4 f = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(dyr, d.off[h] | (bad << 31),
+                                                      (ob + c) * L * 4, 0));
+    v[0][c] = f.x; v[1][c] = f.y; v[2][c] = f.z; v[3][c] = f.w;
+  }
+}
+
+// DPP quad_perm broadcast of lane L of each group of four lanes.
+template <int L>
+__device__ __forceinline__ unsigned quad_bcast(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, L * 0x55, 0xf, 0xf, false);
+}
+
+template <int NB, int NW>
+__global__ void __launch_bounds__(64 * NW, 1)
+custom_dw_kernel(const Params p) {
+  constexpr int RS = NW * RPW;                    // rows per step
+  __shared__ __align__(16) unsigned char smem[NB * QTAB];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = lane / 4, g = lane % 4;
+  const int lb = logical_block();
+  const int to = lb % p.tiles_o;                  // channel tile (consecutive blocks: same rows)
+  const int kc = (lb / p.tiles_o) % p.kchunks;    // tap chunk
+  const int rc = lb / p.tiles_o / p.kchunks;      // row chunk
+  const int j0 = kc * NB;                         // the chunk's first quad
+  const int st0 = rc * p.rchunk, st1 = min(p.rsteps, st0 + p.rchunk);    // steps of RS rows
+  const int slot_bytes = p.Rpad * 2;
+
+  if (wave < 8) {  // the chunk's 4 NB tables, once, by eight waves
+    const int og = __builtin_amdgcn_readfirstlane(wave % 4);
+    const int hw = __builtin_amdgcn_readfirstlane(wave / 4);
+    const int wb = (128 * hw + 2 * lane) * LINE + ((og ^ (lane & 3)) << 4);
+    const __amdgpu_buffer_rsrc_t tabr = buffer_rsrc(p.tab, 256 * 256 * 4);
+    unsigned w4[TPL * NB];
+#pragma unroll
+    for (int q = 0; q < TPL * NB; ++q) {
+      const int k = min(TPL * j0 + q, p.K - 1);
+      w4[q] = load_w4(p.wt + (long long)k * p.Opad + CT * to + 4 * og);
+    }
+    Src src[TPL * NB];
+#pragma unroll
+    for (int q = 0; q < TPL * NB; ++q) load_src(src[q], tabr, w4[q], lane, hw);
+#pragma unroll
+    for (int q = 0; q < TPL * NB; ++q)
+      write_src(smem + (q / TPL) * QTAB + (q % TPL) * 64, src[q], wb);
+  }
+
+  const int nvalid = min(4, max(0, p.O - CT * to - 4 * g));
+  float fac[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) fac[c] = p.dys && c < nvalid ? p.dys[CT * to + 4 * g + c] : 1.f;
+  const __amdgpu_buffer_rsrc_t dyr = buffer_rsrc(p.dy, p.R * p.O * 4);
+  // The chunk's 4 NB slots (fewer at the end of K) under one descriptor;
+  // every part of a row-offset address is in the range-checked vector
+  // offset, so rows past Rpad in the last slot read 0.  Lane g of a row
+  // group loads slots NB g .. NB g + NB - 1 of its rows, and the group's four
+  // lanes share them through DPP broadcasts.
+  const __amdgpu_buffer_rsrc_t xall = buffer_rsrc(
+      p.xt + (long long)TPL * j0 * p.Rpad, min(NB, p.nq - j0) * TPL * slot_bytes);
+  unsigned xv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    xv[i] = (unsigned)((wave * RPW + rg * RQ) * 2) + (unsigned)(NB * g + i) * (unsigned)slot_bytes;
+  DyWalk dw;
+  dy_walk_init(p, st0 * RS + wave * RPW + rg * RQ, 4 * g, dw);
+  const int qt = RS / p.L, rem = RS - qt * p.L;
+  const unsigned step = 4u * ((unsigned)qt * (unsigned)p.O * (unsigned)p.L + (unsigned)rem);
+  const unsigned wrap = 4u * ((unsigned)p.O * (unsigned)p.L - (unsigned)p.L);
+  const int ob = CT * to;
+
+  // loads of row quad h of the step whose rows start at byte tb of a slot
+  auto load_quad = [&](int h, unsigned tb, uint2 (&xo)[NB][TPL], float (&dv)[RQ][4])
+      __attribute__((always_inline)) {
+    uint2 own[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      own[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             xall, xv[i] + tb + 2 * NRG * RQ * h, 0, 0));
+    load_dy_quad(dyr, dw, h, p.R, p.L, ob, nvalid, dv);
+    dy_walk_next(dw, h, RS, p.L, rem, step, wrap);
+    auto put = [&](auto qc) __attribute__((always_inline)) {
+      constexpr int q = decltype(qc)::value;
+      xo[q / TPL][q % TPL] = make_uint2(quad_bcast<q / NB>(own[q % NB].x),
+                                        quad_bcast<q / NB>(own[q % NB].y));
+    };
+    put(std::integral_constant<int, 0>{});
+    put(std::integral_constant<int, 1>{});
+    put(std::integral_constant<int, 2>{});
+    put(std::integral_constant<int, 3>{});
+    if constexpr (NB == 2) {
+      put(std::integral_constant<int, 4>{});
+      put(std::integral_constant<int, 5>{});
+      put(std::integral_constant<int, 6>{});
+      put(std::integral_constant<int, 7>{});
+    }
+  };
+
+  float acc[NB][TPL][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int s = 0; s < TPL; ++s)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[b][s][c] = 0.f;
+
+  // reads in batches of two slots (eight 16-byte reads in flight), each
+  // followed by its FMAs
+  auto sum_quad = [&](const uint2 (&xo)[NB][TPL], const float (&dv0)[RQ][4])
+      __attribute__((always_inline)) {
+    float dv[RQ][4];
+#pragma unroll
+    for (int m = 0; m < RQ; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dv[m][c] = dv0[m][c] * fac[c];   // exact when fac = 1
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int sh = 0; sh < TPL; sh += 2) {
+        float4 e[2][RQ];
+#pragma unroll
+        for (int s = sh; s < sh + 2; ++s) {
+          const unsigned gx = read_mask(g, rg, s, b);
+          const unsigned xd[2] = {xo[b][s].x, xo[b][s].y};
+#pragma unroll
+          for (int m = 0; m < RQ; ++m)
+            e[s - sh][m] =
+                *(const float4*)(smem + (((xd[m >> 1] >> (16 * (m & 1))) & 0xffffu) ^ gx));
+        }
+#pragma unroll
+        for (int s = sh; s < sh + 2; ++s)
+#pragma unroll
+          for (int m = 0; m < RQ; ++m) {
+            acc[b][s][0] = fmaf(dv[m][0], e[s - sh][m].x, acc[b][s][0]);
+            acc[b][s][1] = fmaf(dv[m][1], e[s - sh][m].y, acc[b][s][1]);
+            acc[b][s][2] = fmaf(dv[m][2], e[s - sh][m].z, acc[b][s][2]);
+            acc[b][s][3] = fmaf(dv[m][3], e[s - sh][m].w, acc[b][s][3]);
+          }
+      }
+  };
+
+  __syncthreads();                                 // tables written
+  uint2 xa[NB][TPL], xb[NB][TPL];
+  float da[RQ][4], db[RQ][4];
+  load_quad(0, (unsigned)(st0 * RS * 2), xa, da);
+  for (int st = st0; st < st1; ++st) {
+    const unsigned tb = (unsigned)(st * RS * 2);
+    // quad h + 1 (the next step's quad 0 after quad 3) is requested before
+    // quad h is summed; after the chunk's last step those loads are unused
+    load_quad(1, tb, xb, db);
+    sum_quad(xa, da);
+    load_quad(2, tb, xa, da);
+    sum_quad(xb, db);
+    load_quad(3, tb, xb, db);
+    sum_quad(xa, da);
+    load_quad(0, tb + RS * 2, xa, da);
+    sum_quad(xb, db);
+  }
+
+  __syncthreads();                                 // every wave is done with the tables
+  // over the four row groups of a DPP row: lane rg & 3 == 3 adds, for tap t,
+  // its slot (t + 1) & 3 and the slots (t + 2) & 3, (t + 3) & 3, t of the
+  // lanes 4, 8, 12 below it (the same tap) and stores the row's sums
+  float* red = (float*)smem;                       // [b][wave][row q][g][tap][c]
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int t = 0; t < TPL; ++t) {
+      float o4[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        o4[c] = acc[b][(t + 1) & 3][c] + dpp<ROW_SHR4>(acc[b][(t + 2) & 3][c]) +
+                dpp<ROW_SHR8>(acc[b][(t + 3) & 3][c]) + dpp<ROW_SHR12>(acc[b][t][c]);
+      if ((rg & 3) == 3)
+        *(float4*)(red + (((b * NW + wave) * 4 + (rg >> 2)) * 4 + g) * 16 + 4 * t) =
+            make_float4(o4[0], o4[1], o4[2], o4[3]);
+    }
+  }
+  __syncthreads();
+  if (tid < NB * 64) {                             // output (b, tap t, channel ol)
+    const int b = tid >> 6, t = (tid >> 4) & 3, ol = tid & 15;
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        a += red[(((b * NW + w) * 4 + q) * 4 + (ol >> 2)) * 16 + 4 * t + (ol & 3)];
+    const int k = TPL * (j0 + b) + t, o = CT * to + ol;
+    if (k < p.K && o < p.O) p.out[((long long)rc * p.O + o) * p.K + k] = a;
+  }
 }
 
 // ------------------------------------------------- fp32-class LUT GEMM
@@ -793,26 +1061,64 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
   if (p.R == 0)
     return launch_split_sum(nullptr, 0, numel, K, mask_w, scale_w, grad_w, stream);
   ATX_REQUIRE(xt && wt && dy && tabT && workspace, "atx_custom_grad_dw: null operand");
-  // Fewer (row, channel) tiles than CUs: split the tap quads over enough
-  // workgroups to fill them (each workgroup writes its own taps' entries of
-  // the row tile's slice, so no extra reduction).
-  const long long tiles = (long long)p.tiles_r * p.tiles_o;
-  if (tiles < 256 && p.nq >= 16) {
-    const int want = (int)std::min<long long>(cdiv(256, tiles), p.nq / 8);
-    p.kq_chunk = (int)cdiv(p.nq, want);
-    p.kchunks = (int)cdiv(p.nq, p.kq_chunk);
+  if (L % 4 != 0 || (long long)Rpad * 16 > 0x7fffffffLL) {
+    // Fewer (row, channel) tiles than CUs: split the tap quads over enough
+    // workgroups to fill them (each workgroup writes its own taps' entries of
+    // the row tile's slice, so no extra reduction).
+    const long long tiles = (long long)p.tiles_r * p.tiles_o;
+    if (tiles < 256 && p.nq >= 16) {
+      const int want = (int)std::min<long long>(cdiv(256, tiles), p.nq / 8);
+      p.kq_chunk = (int)cdiv(p.nq, want);
+      p.kchunks = (int)cdiv(p.nq, p.kq_chunk);
+    }
+    const long long blocks = tiles * p.kchunks;
+    ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dw: grid too large");
+    hipLaunchKernelGGL(cg::custom_dw_tile_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT),
+                       0, stream, p);
+    rc = check_launch("custom_dw_tile_kernel");
+    if (rc != ATX_OK) return rc;
+    return launch_split_sum(workspace, p.tiles_r, numel, K, mask_w, scale_w, grad_w, stream);
   }
-  const long long blocks = tiles * p.kchunks;
+  // Workgroups of (channel tile, chunk of NB tap quads, chunk of row steps),
+  // one per CU (128 KiB of tables), NW waves of 256 rows each.  Row chunks:
+  // the fewest rounds of 256 workgroups x (steps per workgroup + the table
+  // build, ~0.6 step), plus writing and summing one O x K slice per row chunk
+  // (cost model in microseconds: 4.4 per 2048 rows x 16 channels x 8 taps).
+  constexpr int NW = ATX_DW_WAVES;
+  constexpr int RS = NW * 256;
+  const int NB = p.nq >= 2 ? 2 : 1;
+  ATX_REQUIRE((long long)(p.R + RS) * O * 4 <= 0xffffffffLL,
+              "atx_custom_grad_dw: dy offsets exceed 32 bits");
+  p.kq_chunk = NB;
+  p.kchunks = (int)cdiv(p.nq, NB);
+  p.rsteps = (int)cdiv(p.R, RS);
+  const long long nw = (long long)p.tiles_o * p.kchunks;
+  {
+    double best = 0.0;
+    int best_chunk = p.rsteps;
+    for (int c = 1; c <= p.rsteps; ++c) {
+      const int chunk = (int)cdiv(p.rsteps, c);
+      if (c > 1 && chunk == (int)cdiv(p.rsteps, c - 1)) continue;
+      const long long ce = cdiv(p.rsteps, chunk);
+      const double rounds = (double)cdiv(nw * ce, 256);
+      const double cost = rounds * (chunk * RS / 2048.0 + 0.6) * 4.4 * NB / 2 +
+                          ce * (double)numel * 8 / 4e6;
+      if (c == 1 || cost < best) { best = cost; best_chunk = chunk; }
+    }
+    p.rchunk = best_chunk;
+  }
+  const int slices = (int)cdiv(p.rsteps, p.rchunk);
+  const long long blocks = nw * slices;
   ATX_REQUIRE(blocks < 0x7fffffffLL, "atx_custom_grad_dw: grid too large");
-  if (L % 4 == 0)
-    hipLaunchKernelGGL(cg::custom_dw_kernel<true>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+  if (NB == 2)
+    hipLaunchKernelGGL((cg::custom_dw_kernel<2, NW>), dim3((unsigned)blocks), dim3(64 * NW), 0,
                        stream, p);
   else
-    hipLaunchKernelGGL(cg::custom_dw_kernel<false>, dim3((unsigned)blocks), dim3(cg::NT), 0,
+    hipLaunchKernelGGL((cg::custom_dw_kernel<1, NW>), dim3((unsigned)blocks), dim3(64 * NW), 0,
                        stream, p);
   rc = check_launch("custom_dw_kernel");
   if (rc != ATX_OK) return rc;
-  return launch_split_sum(workspace, p.tiles_r, numel, K, mask_w, scale_w, grad_w, stream);
+  return launch_split_sum(workspace, slices, numel, K, mask_w, scale_w, grad_w, stream);
 }
 
 }  // extern "C"
