@@ -9,8 +9,10 @@ backward, SGD update.  `value` is img/s of the whole job (1 GPU).
 
 Also reported:
   roofline      the dominant kernel, the LUT GEMM (lut_gemm_kernel): LUT-MACs
-                of every launch inside the timed region / their summed
-                durations (HIP events on the launch stream); bound = LDS, one
+                of every launch / their summed durations (HIP events on the
+                launch stream, recorded around the kernel alone) over a second
+                pass of the timed steps, so that the events' host cost stays
+                out of `value`; bound = LDS, one
                 LUT-MAC = one 2-byte table read from LDS, peak = 256 CUs x
                 256 B/clk x 2.4 GHz.  `valu_peak` is the co-bound of one
                 int32 add per LUT-MAC (256 CUs x 64 lanes x 2.4 GHz).  For
@@ -502,14 +504,14 @@ def main():
         workloads.training_step(model, opt, x, y)
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
-    timer.active = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
         workloads.training_step(model, opt, x, y)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    timer.active = False
     peak_mem = torch.cuda.max_memory_allocated()
+    dt_kern = timed_gemm_pass(torch, timer, args.steps,
+                              lambda: workloads.training_step(model, opt, x, y))
     result = {
         "metric": "ResNet-50 224^2 approx-QAT img/s (LUT-MAC/s + % LDS roofline)"
         if name == "c4" else f"{name} approx-QAT img/s",
@@ -530,7 +532,7 @@ def main():
                                f"weight_bits={cfg['weight_bits']} lut={cfg['lut']}",
                    "global_batch": cfg["batch"], "parallelism": "single GPU",
                    "forward_lut_macs": macs_fwd, "save_image": bool(args.save_image)},
-        "roofline": roofline(timer, dt, name, narrow=cfg["weight_bits"] <= 4),
+        "roofline": roofline(timer, dt_kern, name, narrow=cfg["weight_bits"] <= 4),
         "peak_memory_MB": round(peak_mem / 2 ** 20, 1),
     }
     if not args.no_microbench:
@@ -544,6 +546,23 @@ def main():
         batch = args.cpu_sample_batch or {"c2": 4, "c4": 2, "c5": 1}[name]
         result["cpu_baseline"] = cpu_baseline(model, cfg, batch)
     print(json.dumps(result), flush=True)
+
+
+def timed_gemm_pass(torch, timer, steps, step):
+    """The timed steps again with the GemmTimer's per-call HIP events (the
+    roofline's kernel durations), after the timed region that gives `value`:
+    the events' host cost (a few Python calls per LUT GEMM call) stays out of
+    `value`, which matters where a step is as short as its host issue (c1).
+    Returns the pass's wall time (for the kernel's share of a step)."""
+    torch.cuda.synchronize()
+    timer.active = True
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timer.active = False
+    return dt
 
 
 def roofline(timer, dt, workload, narrow=False):
@@ -664,13 +683,12 @@ def main_c1(torch, args):
         for _ in range(max(args.warmup, 1)):
             layer(xg)
         torch.cuda.synchronize()
-        timer.active = True
         t0 = time.perf_counter()
         for _ in range(args.steps):
             layer(xg)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
-        timer.active = False
+        dt_kern = timed_gemm_pass(torch, timer, args.steps, lambda: layer(xg))
     macs = 8 * 32 * 32 * 64 * 576
     result = {
         "metric": "LUT-MAC/s (G), config 1 (one approximate 3x3 conv 64->64 forward, [8,64,32,32])",
@@ -688,7 +706,7 @@ def main_c1(torch, args):
         "config": {"workload": "c1: Conv2d_int8 3x3 64->64 forward, eval mode, im2col GEMM "
                                "M=8192 N=64 K=576 + dequant", "lut_macs_per_step": macs,
                    "parallelism": "single GPU"},
-        "roofline": roofline(timer, dt, "c1"),
+        "roofline": roofline(timer, dt_kern, "c1"),
     }
     if not args.no_cpu_baseline:
         from oracle import torch_cpu

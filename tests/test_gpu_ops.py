@@ -753,7 +753,13 @@ def test_tap_sum_exact(case, dtype):
 
 CUSTOM_SHAPES = [(1, 1, 1, 1), (2, 5, 7, 3), (1, 4, 4096, 16), (3, 37, 1000, 70),
                  (2, 576, 3136, 64), (1, 9, 2049, 17), (4, 64, 49, 300), (1, 130, 6, 2048),
-                 (2, 3, 5000, 33)]
+                 (2, 3, 5000, 33),
+                 # L % 4 == 0 (resident tables): an odd number of tap quads (the last
+                 # chunk holds one), one channel tile over many row steps (one slice
+                 # per step), a partial last step with O % 16 != 0, row chunks of two
+                 # steps, and one chunk of five steps whose rows cross images
+                 (2, 9, 1024, 20), (2, 130, 12, 48), (5, 8, 4096, 16), (3, 18, 2500, 24),
+                 (4, 144, 2600, 64), (2, 576, 4400, 48)]
 
 
 @pytest.mark.parametrize("shape", CUSTOM_SHAPES)
