@@ -714,8 +714,11 @@ custom_dw_kernel(const Params p) {
 
   // reads in batches of two slots (eight 16-byte reads in flight), each
   // followed by its FMAs
-  auto sum_quad = [&](const uint2 (&xo)[NB][TPL], const float (&dv0)[RQ][4])
+  // A wave whose rows of quad h all lie at or past R skips it (uniform: the
+  // partial last step of a layer whose rows are not a multiple of the step).
+  auto sum_quad = [&](const uint2 (&xo)[NB][TPL], const float (&dv0)[RQ][4], int st, int h)
       __attribute__((always_inline)) {
+    if (st * RS + wave * RPW + NRG * RQ * h >= p.R) return;
     float dv[RQ][4];
 #pragma unroll
     for (int m = 0; m < RQ; ++m)
@@ -756,13 +759,13 @@ custom_dw_kernel(const Params p) {
     // quad h + 1 (the next step's quad 0 after quad 3) is requested before
     // quad h is summed; after the chunk's last step those loads are unused
     load_quad(1, tb, xb, db);
-    sum_quad(xa, da);
+    sum_quad(xa, da, st, 0);
     load_quad(2, tb, xa, da);
-    sum_quad(xb, db);
+    sum_quad(xb, db, st, 1);
     load_quad(3, tb, xb, db);
-    sum_quad(xa, da);
+    sum_quad(xa, da, st, 2);
     load_quad(0, tb + RS * 2, xa, da);
-    sum_quad(xb, db);
+    sum_quad(xb, db, st, 3);
   }
 
   __syncthreads();                                 // every wave is done with the tables
