@@ -194,17 +194,24 @@ def close_lowp(got, want, absref, scale, dt):
     assert (np.abs(got - want) <= tol).all(), f"max err {np.abs(got - want).max():.3g}"
 
 
-@pytest.mark.parametrize("kind", ["ste", "lre"])
+@pytest.mark.parametrize("kind", ["ste", "lre", "custom"])
 @pytest.mark.parametrize("geom", [(3, 1, 1), (1, 1, 0), (3, 2, 1)])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_conv2d_int8_lowp_input(dt, geom, kind):
     """Conv2d_int8 fed an fp16 / bf16 x in training mode (fp32 weights): the
     EMA scale as torch computes it for that dtype, y (fp32) against the
-    oracle layer with the dtype's fake-quant, gx in the dtype, gw / gb fp32."""
+    oracle layer with the dtype's fake-quant, gx in the dtype, gw / gb fp32.
+    custom: the pair-table estimator with DATE tables (the unfused path:
+    static fake-quant in the dtype, then the conv Function)."""
     k, st, p = geom
     torch.manual_seed(7)
     lut = lut_perturbed(3)
-    dx, dw = (None, None) if kind == "ste" else O.lre_tables(lut, "int8")
+    if kind == "ste":
+        dx, dw = None, None
+    elif kind == "lre":
+        dx, dw = O.lre_tables(lut, "int8")
+    else:
+        dx, dw = (t.reshape(-1) for t in O.date_tables(lut.reshape(256, 256), 2))
     layer = at.nn.Conv2d_int8(6, 20, k, torch.from_numpy(lut).to(DEV), grad=kind,
                               dx=None if dx is None else torch.from_numpy(dx).to(DEV),
                               dw=None if dw is None else torch.from_numpy(dw).to(DEV),
