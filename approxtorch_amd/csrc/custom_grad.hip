@@ -548,20 +548,21 @@ custom_dw_tile_kernel(const Params p) {
 // ----------------------------------------------------------------- grad_w
 // For L % 4 == 0.  grad_w contracts over the rows, so a workgroup keeps the
 // tables of NB quads of taps resident for its whole run (NB = 2: eight taps,
-// 128 KiB) and walks a range of row tiles: a tap's 16 KiB table is built once
-// per workgroup, not once per (row tile, tap), and the loop over the rows
-// has no LDS writes and no barriers.  Workgroup (channel tile to, tap chunk kc = quads
-// NB kc .. NB kc + NB - 1, row chunk rc = row tiles rc * rchunk ..).  Lane
-// (rg, g) owns channels 4g..4g+3 of the tile and rows 256 wave + 64 h +
-// 4 rg + m of every row tile; per row quad h it loads its rows' dy (four
-// channels) and the rows' offsets in the quads' tap slots, and accumulates
-// acc[b][s][c] for tap 4(NB kc + b) + ((rg + s) & 3) (the operand's slot
-// rotation, which keeps the reads conflict-free) over all its rows.  The
-// loads of the next row quad are issued before the current one is summed.
-// At the end the partials are combined over the row groups of a wave with
-// DPP row_shr, then over the waves and row quads through LDS in a fixed
-// order into the row chunk's slice [rchunks][O][K]; split_sum adds the slices
-// in a fixed order.
+// 128 KiB) and walks a chunk of row steps (NW waves x 256 rows each): a tap's
+// 16 KiB table is built once per workgroup, not once per (row tile, tap), and
+// the loop over the rows has no LDS writes and no barriers.  Workgroup
+// (channel tile to, tap chunk kc = quads NB kc .. NB kc + NB - 1, row chunk
+// rc = steps rc * rchunk ..).  Lane (rg, g) owns channels 4g..4g+3 of the
+// tile and rows 256 wave + 64 h + 4 rg + m of every step; per row quad h it
+// loads its rows' dy (four channels) and the rows' offsets in the quads' tap
+// slots (lane g of a row group loads NB of the slots, DPP broadcasts share
+// them), and accumulates acc[b][s][c] for tap 4(NB kc + b) + ((rg + s) & 3)
+// (the operand's slot rotation, which keeps the reads conflict-free) over all
+// its rows.  The loads of the next row quad are issued before the current one
+// is summed; a wave skips row quads that lie wholly past R.  At the end the
+// partials are combined over the row groups of a wave with DPP row_shr, then
+// over the waves and row quads through LDS in a fixed order into the row
+// chunk's slice [rchunks][O][K]; split_sum adds the slices in a fixed order.
 
 // dy offsets of the lane's row quads (L % 4 == 0: a quad of rows never
 // straddles two images, so its dy is one 16-byte load per channel), advanced
