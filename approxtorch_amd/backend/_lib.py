@@ -131,6 +131,9 @@ _SIGS = {
                                    c_int, c_vp, c_vp]),
     "atx_custom_grad_dx_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
                                           c_int, c_int, c_int, c_int, c_vp, c_vp]),
+    "atx_custom_grad_dx_narrow_img": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
+                                              c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp,
+                                              c_vp, c_vp]),
     "atx_custom_grad_dw_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
     "atx_custom_grad_dw": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int,
                                    c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),

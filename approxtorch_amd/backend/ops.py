@@ -771,7 +771,7 @@ def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, 
 
 # --------------------------------------------------------- custom backward
 def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int, Lc: int,
-                 mask_w=None, scale_w=None, wbase=None, dy_scale=None):
+                 mask_w=None, scale_w=None, wbase=None, dy_scale=None, img_ste=None):
     """(grad_x [N,K,L] or None, grad_w [O,K] or None) of the pair-table
     estimator from the LUT GEMM's row-offset operand (xt, Rpad) and the uint8
     weight index image wq [O,K]; dx_lut / dw_lut are fp32 [65536] tables
@@ -780,7 +780,11 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
     guarantees every index of wq lies in [wbase, wbase + 16) (weight_bits <=
     4), and grad_x runs on the matrix cores (atx_custom_grad_dx_narrow).
     dy_scale [O] (optional): the gradients of dy * dy_scale[o], with no scaled
-    copy of dy where the kernels take the factor."""
+    copy of dy where the kernels take the factor.
+    img_ste (with wbase; a 1x1 stride-1 unpadded conv, whose column gradient
+    is the image gradient): (pos [N, L] or None, mask [N, K, L] or None,
+    scale [1]) -- grad_x comes back as col2im(grad_x, pos, mask, scale) of
+    that geometry, computed in the grad_x kernel's epilogue."""
     xt, Rpad = operand
     O = wq.size(0)
     dyc = dy.contiguous()
@@ -801,8 +805,21 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
             dyx, dsx = dyc, dy_scale
             if dy_scale is not None and O > 4096:   # the kernel holds at most 4096 factors
                 dyx, dsx = dyc * dy_scale.view(1, -1, 1), None
-            L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyx),
-                   L.ptr(dsx), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
+            if img_ste is not None:
+                pos, mask, scale = img_ste
+                pos = None if pos is None else pos.contiguous()
+                mask = None if mask is None else mask.contiguous()
+                if mask is not None and (mask.dtype != torch.bool or mask.numel() != N * K * Lc):
+                    raise RuntimeError(f"mask must be bool with {N * K * Lc} elements")
+                if pos is not None and (pos.dtype != torch.float32 or pos.numel() != N * Lc):
+                    raise RuntimeError(f"pos must be float32 with {N * Lc} elements")
+                L.call("atx_custom_grad_dx_narrow_img", L.ptr(xt), Rpad, L.ptr(wt), Opad,
+                       L.ptr(dyx), L.ptr(dsx), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(pos),
+                       L.ptr(mask), L.ptr(None if scale is None else scale.contiguous()),
+                       L.ptr(gx), s)
+            else:
+                L.call("atx_custom_grad_dx_narrow", L.ptr(xt), Rpad, L.ptr(wt), Opad,
+                       L.ptr(dyx), L.ptr(dsx), L.ptr(tab), int(wbase), N, K, Lc, O, L.ptr(gx), s)
         else:
             dyx = dyc if dy_scale is None else dyc * dy_scale.view(1, -1, 1)
             L.call("atx_custom_grad_dx", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyx),

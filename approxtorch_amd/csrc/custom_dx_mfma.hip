@@ -59,6 +59,11 @@ struct Params {
   const float* dy;                           // [N][O][L]
   const float* dys;                          // per-channel factor of dy [O] (nullable)
   float* gx;                                 // [N][K][L]
+  // img: grad_x of a 1x1 stride-1 unpadded conv is the image gradient; the
+  // epilogue then adds pos[n][l] (nullable) and applies the fake-quant STE
+  // (mask nullable, scale with it), atx_col2im_pos's operations for that
+  // geometry
+  const float* pos; const uint8_t* mask; const float* scale;
   int K, R, L, O, wbase;
   int tiles_k, tiles;
   unsigned dy_bytes, wt_bytes, xt_bytes;
@@ -109,6 +114,7 @@ __device__ __forceinline__ void split_parts(const float (&d)[8], u32x4 (&P)[3]) 
   }
 }
 
+template <bool IMG>
 __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
   __shared__ __align__(16) unsigned char hbuf[2 * HBUF];
   __shared__ __align__(16) unsigned char xtab[256 * XS];
@@ -306,7 +312,16 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
         const float sx = lo ? q0 : q1, kx = lo ? q1 : q0;
         const float tot = kx + __shfl_xor(sx, 16);
         const int k = cur.k0 + 4 * tq + g;
-        if (rvalid && k < p.K) p.gx[gbase + (long long)k * p.L] = tot;
+        if (rvalid && k < p.K) {
+          const long long i = gbase + (long long)k * p.L;
+          float v = tot;
+          if constexpr (IMG) {    // the col2im sum of one tap, in its order
+            v = 0.0f + tot;
+            if (p.pos) v += 0.0f + p.pos[(long long)n * p.L + l];
+            if (p.mask) v = (p.mask[i] ? v : 0.0f) / fmaxf(p.scale[0], 1e-12f);
+          }
+          p.gx[i] = v;
+        }
       }
     }
     if (!has_next) break;
@@ -315,24 +330,48 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
   }
 }
 
+// The image gradient of a 1x1 stride-1 conv with no output channels: the
+// epilogue's operations on a zero sum.
+__global__ void img_empty_kernel(int N, int K, int L, const float* __restrict__ pos,
+                                 const uint8_t* __restrict__ mask,
+                                 const float* __restrict__ scale, float* __restrict__ img) {
+  const long long total = (long long)N * K * L;
+  const float s = mask ? fmaxf(scale[0], 1e-12f) : 1.0f;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    float v = 0.0f + 0.0f;
+    if (pos) {
+      const long long n = i / ((long long)K * L), l = i % L;
+      v += 0.0f + pos[n * L + l];
+    }
+    if (mask) v = (mask[i] ? v : 0.0f) / s;
+    img[i] = v;
+  }
+}
+
 }  // namespace ohx
 }  // namespace atx
 
 using namespace atx;
 
-extern "C" {
-
-int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
-                              const float* dy, const float* dy_scale, const float* tabT,
-                              int wbase, int N, int K, int L, int O, float* grad_x,
-                              hipStream_t stream) {
+static int custom_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                            const float* dy, const float* dy_scale, const float* tabT, int wbase,
+                            int N, int K, int L, int O, const float* pos, const uint8_t* mask,
+                            const float* scale, int img, float* grad_x, hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_custom_grad_dx_narrow: negative size");
   ATX_REQUIRE(wbase >= 0 && wbase <= 240, "atx_custom_grad_dx_narrow: wbase must be in [0, 240]");
+  ATX_REQUIRE(!mask || scale, "atx_custom_grad_dx_narrow_img: mask without scale");
   const long long R = (long long)N * L;
   const long long numel = R * K;
   if (numel == 0) return ATX_OK;
-  if (O == 0)   // an empty sum: zeros
+  if (O == 0 && !img)   // an empty sum: zeros
     return atx_custom_grad_dx(xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, grad_x, stream);
+  if (O == 0) {         // an empty sum with the position term and the STE
+    ATX_REQUIRE(grad_x, "atx_custom_grad_dx_narrow_img: null output");
+    hipLaunchKernelGGL(ohx::img_empty_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0, stream,
+                       N, K, L, pos, mask, scale, grad_x);
+    return check_launch("img_empty_kernel");
+  }
   ATX_REQUIRE(xt && wt && dy && tabT && grad_x, "atx_custom_grad_dx_narrow: null pointer");
   ATX_REQUIRE(Rpad >= R && Rpad % ATX_ROW_TILE == 0,
               "atx_custom_grad_dx_narrow: Rpad must be a multiple of %d and >= N*L",
@@ -343,9 +382,10 @@ int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, i
   ATX_REQUIRE(R * O * 4 < 0x7fffffffLL && (long long)K * Opad < 0x7fffffffLL &&
                   (long long)operand_rows(K) * Rpad * 2 < 0x7fffffffLL,
               "atx_custom_grad_dx_narrow: operand too large for 32-bit buffer offsets");
-  ohx::Params p;
+  ohx::Params p{};
   p.xt = xt; p.Rpad = Rpad; p.wt = wt; p.Opad = Opad; p.tab = tabT; p.dy = dy; p.gx = grad_x;
   p.dys = dy_scale;
+  p.pos = pos; p.mask = mask; p.scale = scale;
   p.K = K; p.R = (int)R; p.L = L; p.O = O; p.wbase = wbase;
   p.tiles_k = (int)cdiv(K, ohx::KT);
   const long long tiles = cdiv(R, ohx::ROWS) * p.tiles_k;
@@ -357,8 +397,30 @@ int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, i
   // one workgroup per CU (512 threads at up to 256 registers), a multiple of
   // the 8 XCDs
   const int blocks = (int)std::min<long long>(256, ((tiles + 7) / 8) * 8);
-  hipLaunchKernelGGL(ohx::onehot_dx_kernel, dim3(blocks), dim3(ohx::NT), 0, stream, p);
+  if (img)
+    hipLaunchKernelGGL(ohx::onehot_dx_kernel<true>, dim3(blocks), dim3(ohx::NT), 0, stream, p);
+  else
+    hipLaunchKernelGGL(ohx::onehot_dx_kernel<false>, dim3(blocks), dim3(ohx::NT), 0, stream, p);
   return check_launch("onehot_dx_kernel");
+}
+
+extern "C" {
+
+int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                              const float* dy, const float* dy_scale, const float* tabT,
+                              int wbase, int N, int K, int L, int O, float* grad_x,
+                              hipStream_t stream) {
+  return custom_dx_narrow(xt, Rpad, wt, Opad, dy, dy_scale, tabT, wbase, N, K, L, O, nullptr,
+                          nullptr, nullptr, 0, grad_x, stream);
+}
+
+int atx_custom_grad_dx_narrow_img(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                                  const float* dy, const float* dy_scale, const float* tabT,
+                                  int wbase, int N, int K, int L, int O, const float* pos,
+                                  const uint8_t* mask, const float* scale, float* grad_img,
+                                  hipStream_t stream) {
+  return custom_dx_narrow(xt, Rpad, wt, Opad, dy, dy_scale, tabT, wbase, N, K, L, O, pos, mask,
+                          scale, 1, grad_img, stream);
 }
 
 }  // extern "C"

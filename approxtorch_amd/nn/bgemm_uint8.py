@@ -288,10 +288,18 @@ class _conv2d_uint8_fused(Function):
         gxs = ops.zero_point_pos(go, sx, sw, zw) if need_x else None
         gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
         if ctx.kind == 'custom':
-            grad_col, gw_q = ops.custom_grads((xt, ctx.rpad), wq, go, tx if need_x else None,
-                                              tw if need_w else None, g.N, K, Lc,
-                                              wbase=ctx.wbase, dy_scale=c)
-            if need_x:   # fold, zero-point term and the STE in one pass
+            # a 1x1 stride-1 unpadded conv's column gradient is its image
+            # gradient: the matrix-core grad_x applies the zero-point term and
+            # the STE in its epilogue (the fold's operations for that geometry)
+            pointwise = (ctx.wbase is not None and need_x and g.KH == 1 and g.KW == 1 and
+                         g.SH == 1 and g.SW == 1 and g.PH == 0 and g.PW == 0)
+            grad_col, gw_q = ops.custom_grads(
+                (xt, ctx.rpad), wq, go, tx if need_x else None, tw if need_w else None, g.N,
+                K, Lc, wbase=ctx.wbase, dy_scale=c,
+                img_ste=(gxs, mask_x, sx) if pointwise else None)
+            if pointwise:
+                gx = grad_col.view(mask_x.shape)
+            elif need_x:   # fold, zero-point term and the STE in one pass
                 gx = ops.col2im(grad_col, g, pos=gxs, mask=mask_x, scale=sx)
         else:
             gp = go * c.view(1, -1, 1)

@@ -596,6 +596,21 @@ int atx_custom_grad_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, i
                               int wbase, int N, int K, int L, int O, float* grad_x,
                               hipStream_t stream);
 
+/* atx_custom_grad_dx_narrow for a 1x1, stride-1, unpadded conv, whose
+ * column gradient [N][K][L] is the image gradient [N][C][H*W]: the epilogue
+ * also adds pos[n][l] (nullable) and applies the fake-quant STE (mask
+ * [N][C][H][W] nullable, scale [1] with it), the operations and order of
+ * atx_col2im_pos for that geometry, so the result equals
+ * atx_custom_grad_dx_narrow followed by atx_col2im_pos bit for bit, without
+ * the column buffer or the fold pass.  Replaces the same reference calls
+ * for the uint8 layer's 1x1 convs (nn/bgemm_uint8.py:89-114 with the fold and
+ * fake-quant backward of nn/Conv2d_uint8.py:308-325). */
+int atx_custom_grad_dx_narrow_img(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                                  const float* dy, const float* dy_scale, const float* tabT,
+                                  int wbase, int N, int K, int L, int O, const float* pos,
+                                  const uint8_t* mask, const float* scale, float* grad_img,
+                                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

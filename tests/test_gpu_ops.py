@@ -874,6 +874,33 @@ def test_custom_grad_dx_narrow_matches_general():
     close(a.cpu().numpy(), b.cpu().numpy(), 2 * ax)
 
 
+@pytest.mark.parametrize("case", [(2, 40, (14, 14), 70, True, True), (1, 33, (25, 40), 16, False, True),
+                                  (3, 16, (8, 8), 20, True, False), (2, 8, (6, 6), 0, True, True)])
+def test_custom_grad_dx_narrow_img_is_the_fold(case):
+    """For a 1x1 stride-1 unpadded conv the matrix-core grad_x with the
+    zero-point position term and the fake-quant STE in its epilogue
+    (atx_custom_grad_dx_narrow_img) equals grad_x followed by the fold with
+    them (atx_col2im_pos) bit for bit; O = 0 gives the fold of zeros."""
+    N, C, (H, W), Oc, with_pos, with_mask = case
+    Lc = H * W
+    r = gen(zlib.crc32(repr(("img", case)).encode()))
+    xi = r.integers(0, 256, (N, C, Lc), dtype=np.uint8)
+    wi = r.integers(0, 16, (Oc, C), dtype=np.uint8)
+    dxl = t(r.standard_normal(65536).astype(np.float32))
+    go = t(r.standard_normal((N, Oc, Lc)).astype(np.float32))
+    c = t((r.random(Oc) * 3e-3 + 1e-4).astype(np.float32))
+    pos = t(r.standard_normal((N, Lc)).astype(np.float32)) if with_pos else None
+    mask = t(r.random((N, C, H, W)) < 0.8) if with_mask else None
+    sc = t(np.array([0.037], np.float32))
+    g = ops.conv_geom((N, C, H, W), 1, 1, 0, 1)
+    op = ops.pack_rows_u8(t(xi))
+    a, _ = ops.custom_grads(op, t(wi), go, dxl, None, N, C, Lc, wbase=0, dy_scale=c,
+                            img_ste=(pos, mask, sc))
+    col, _ = ops.custom_grads(op, t(wi), go, dxl, None, N, C, Lc, wbase=0, dy_scale=c)
+    b = ops.col2im(col, g, pos=pos, mask=mask, scale=sc)
+    assert torch.equal(a.view_as(b), b)
+
+
 def test_custom_grads_deterministic():
     """The grad_w partial slices are summed in a fixed order: two runs agree bitwise."""
     N, K, Lc, Oc = 4, 288, 3136, 64
