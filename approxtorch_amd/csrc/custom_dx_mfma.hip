@@ -67,6 +67,7 @@ struct Params {
   int K, R, L, O, wbase;
   int tiles_k, tiles;
   unsigned dy_bytes, wt_bytes, xt_bytes;
+  unsigned pos_bytes, mask_bytes;            // 0 for a null pos / mask
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
@@ -142,6 +143,15 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
   const unsigned brep = (unsigned)p.wbase * 0x01010101u;
   const int chan_bytes = p.L * 4;
   const int ptail = p.O - (nsteps - 1) * OC;           // channels of the last step
+  // The image epilogue's operands: range-checked loads (a null operand has
+  // no bytes, its loads return 0) and, for a null one, a value that leaves the
+  // sum as it is: -0 for the position term, 1 for every mask byte, 1 for the
+  // STE divisor (read once: the epilogue's stores may alias p.scale).
+  const __amdgpu_buffer_rsrc_t posr = rsrc(p.pos ? (const void*)p.pos : p.gx, p.pos_bytes);
+  const __amdgpu_buffer_rsrc_t mkr = rsrc(p.mask ? (const void*)p.mask : p.gx, p.mask_bytes);
+  const unsigned pos_fill = p.pos ? 0u : 0x80000000u;
+  const unsigned mk_fill = p.mask ? 0u : 1u;
+  const float sdiv = (IMG && p.mask) ? fmaxf(p.scale[0], 1e-12f) : 1.0f;
 
   // Persistent over the tiles (each XCD walks a contiguous range), one
   // pipeline across tile boundaries: the last channel step of a tile
@@ -281,6 +291,30 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
     *(uint4*)&xsh[wave][lane >> 2][8 * (lane & 3)] = xq;
     __builtin_amdgcn_wave_barrier();          // the wave's own rows: no workgroup barrier
     asm volatile("" ::: "memory");
+    // the image epilogue's position terms and STE mask bytes of this lane's
+    // rows and taps, loaded before its first store so that no load waits on
+    // a store (registers are free here; in the product steps they are not)
+    float posv[RB];
+    unsigned mk[RB][KT / 4];
+    if constexpr (IMG) {
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int r = cur.rt * ROWS + wave * (RB * 16) + b * 16 + j;
+        const int n = r / p.L, l = r - n * p.L;
+        const bool rvalid = r < p.R;
+        const float pv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                       posr, rvalid ? (unsigned)r * 4u : OOB, 0, 0));
+        posv[b] = __uint_as_float(__float_as_uint(0.0f + pv) | pos_fill);
+        const unsigned mbase = (unsigned)n * (unsigned)p.K * (unsigned)p.L + (unsigned)l;
+#pragma unroll
+        for (int tq = 0; tq < KT / 4; ++tq) {
+          const int k = cur.k0 + 4 * tq + g;
+          mk[b][tq] = __builtin_amdgcn_raw_buffer_load_b8(
+                          mkr, rvalid && k < p.K ? mbase + (unsigned)k * (unsigned)p.L : OOB, 0, 0) |
+                      mk_fill;
+        }
+      }
+    }
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = cur.rt * ROWS + wave * (RB * 16) + b * 16 + j;
@@ -316,9 +350,8 @@ __global__ void __launch_bounds__(NT, 1) onehot_dx_kernel(const Params p) {
           const long long i = gbase + (long long)k * p.L;
           float v = tot;
           if constexpr (IMG) {    // the col2im sum of one tap, in its order
-            v = 0.0f + tot;
-            if (p.pos) v += 0.0f + p.pos[(long long)n * p.L + l];
-            if (p.mask) v = (p.mask[i] ? v : 0.0f) / fmaxf(p.scale[0], 1e-12f);
+            v = 0.0f + tot + posv[b];
+            v = (mk[b][tq] ? v : 0.0f) / sdiv;
           }
           p.gx[i] = v;
         }
@@ -394,6 +427,10 @@ static int custom_dx_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int
   p.dy_bytes = (unsigned)(R * O * 4);
   p.wt_bytes = (unsigned)((long long)K * Opad);
   p.xt_bytes = (unsigned)((long long)operand_rows(K) * Rpad * 2);
+  ATX_REQUIRE(!img || numel < 0x7fffffffLL,
+              "atx_custom_grad_dx_narrow_img: image too large for 32-bit buffer offsets");
+  p.pos_bytes = pos ? (unsigned)(R * 4) : 0u;
+  p.mask_bytes = mask ? (unsigned)numel : 0u;
   // one workgroup per CU (512 threads at up to 256 registers), a multiple of
   // the 8 XCDs
   const int blocks = (int)std::min<long long>(256, ((tiles + 7) / 8) * 8);

@@ -875,7 +875,8 @@ def test_custom_grad_dx_narrow_matches_general():
 
 
 @pytest.mark.parametrize("case", [(2, 40, (14, 14), 70, True, True), (1, 33, (25, 40), 16, False, True),
-                                  (3, 16, (8, 8), 20, True, False), (2, 8, (6, 6), 0, True, True)])
+                                  (3, 16, (8, 8), 20, True, False), (2, 24, (10, 10), 32, False, False),
+                                  (2, 8, (6, 6), 0, True, True)])
 def test_custom_grad_dx_narrow_img_is_the_fold(case):
     """For a 1x1 stride-1 unpadded conv the matrix-core grad_x with the
     zero-point position term and the fake-quant STE in its epilogue
