@@ -190,8 +190,8 @@ __global__ void lut_map_pad_kernel(const T* __restrict__ in, int N, int C, int H
 // loaded in batches of CT with no branches (a tap that does not hit the
 // element loads element 0 and is skipped in the sum), so a thread has CT
 // loads in flight; the sum keeps ascending (kh, kw) order (CT = 1 for a
-// one-tap kernel).  ST = the stride when both strides equal 1 or 2
-// (divisions become shifts), 0 for the general case.
+// one-tap kernel).  ST = 1 when both strides are 1 (no divisions), 0 for
+// the general case; both strides 2 take col2im_s2_kernel.
 template <typename I, int ST, int CT>
 __global__ void __launch_bounds__(TB)
 col2im_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __restrict__ pos,
@@ -222,9 +222,6 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __res
         if constexpr (ST == 1) {
           oh = y; ow = x;
           hit = true;
-        } else if constexpr (ST == 2) {
-          oh = y >> 1; ow = x >> 1;
-          hit = ((y | x) & 1) == 0;
         } else {
           oh = y >= 0 ? y / g.SH : 0; ow = x >= 0 ? x / g.SW : 0;
           hit = oh * g.SH == y && ow * g.SW == x;
@@ -247,6 +244,91 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __res
     if (pn) a += b;
     if (mask) a = (mask[i] ? a : 0.0f) / s;
     img[i] = a;
+  }
+}
+
+// col2im with both strides 2, one thread per 2 x 2 block of pixels (rows
+// 2a, 2a + 1, columns 2b, 2b + 1).  Pixel row h = 2a + e is reached by tap
+// row kh when h + PH - kh * DH is even, i.e. for e = (PH - kh * DH) & 1
+// whatever a: every tap feeds exactly one pixel of the block, and the lanes
+// (consecutive b) read consecutive col elements for it.  Each pixel sums its
+// taps in the same ascending (kh, kw) order as col2im_kernel: a tap that
+// misses it adds +0, which leaves a sum started at +0 unchanged (such a sum
+// is never -0).  A pixel that no tap reaches is +0 with or without its mask
+// (0 / s), so its mask byte is not read.  VEC: W is even and img 8-byte
+// aligned, so a block row is one 8-byte store.
+template <typename I, int CT, bool VEC>
+__global__ void __launch_bounds__(TB)
+col2im_s2_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __restrict__ pos,
+                 const uint8_t* __restrict__ mask, const float* __restrict__ scale,
+                 float* __restrict__ img) {
+  const int L = g.OH * g.OW;
+  const int KK = g.KH * g.KW;
+  const int H2 = (g.H + 1) >> 1, W2 = (g.W + 1) >> 1;
+  const I B2 = (I)H2 * W2;
+  const I HW = (I)g.H * g.W;
+  const I total = (I)g.N * g.C * B2;
+  const float s = mask ? fmaxf(scale[0], 1e-12f) : 1.0f;
+  for (I i = (I)blockIdx.x * TB + threadIdx.x; i < total; i += (I)gridDim.x * TB) {
+    const I plane = i / B2;                   // n * C + c
+    const int q = (int)(i - plane * B2);
+    const int a = q / W2, b = q - a * W2;
+    const float* cn = col + (long long)plane * KK * L;
+    const float* pn = pos ? pos + (long long)(plane / g.C) * L : nullptr;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    unsigned any = 0;                         // pixels of the block some tap reaches
+    int kh = 0, kw = 0;
+    for (int t0 = 0; t0 < KK; t0 += CT) {
+      float v[CT], u[CT];
+      int e[CT];
+      bool ok[CT];
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        const int yb = g.PH - kh * g.DH, xb = g.PW - kw * g.DW;
+        const int eh = yb & 1, ew = xb & 1;   // the block row and column the tap reaches
+        const int y = 2 * a + eh + yb, x = 2 * b + ew + xb;   // both even
+        const int oh = y >> 1, ow = x >> 1;
+        ok[j] = t0 + j < KK && y >= 0 && x >= 0 && oh < g.OH && ow < g.OW &&
+                2 * a + eh < g.H && 2 * b + ew < g.W;
+        const int at = ok[j] ? oh * g.OW + ow : 0;
+        v[j] = cn[ok[j] ? (long long)(t0 + j) * L + at : 0];
+        u[j] = pn ? pn[at] : 0.0f;
+        e[j] = 2 * eh + ew;
+        if (++kw == g.KW) { kw = 0; ++kh; }
+      }
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += ok[j] && e[j] == c ? v[j] : 0.0f;
+        any |= (ok[j] ? 1u : 0u) << e[j];
+      }
+      if (pn) {
+#pragma unroll
+        for (int j = 0; j < CT; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) pb[c] += ok[j] && e[j] == c ? u[j] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (pn) acc[c] += pb[c];
+      if (mask && ((any >> c) & 1u)) {
+        const I idx = plane * HW + (I)(2 * a + (c >> 1)) * g.W + 2 * b + (c & 1);
+        acc[c] = (mask[idx] ? acc[c] : 0.0f) / s;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int h = 2 * a + r;
+      if (h >= g.H) break;
+      const I idx = plane * HW + (I)h * g.W + 2 * b;
+      if constexpr (VEC) {
+        *(float2*)(img + idx) = make_float2(acc[2 * r], acc[2 * r + 1]);
+      } else {
+        img[idx] = acc[2 * r];
+        if (2 * b + 1 < g.W) img[idx + 1] = acc[2 * r + 1];
+      }
+    }
   }
 }
 
@@ -567,7 +649,16 @@ int atx_col2im_pos(const float* col, atx_conv_geom g, const float* pos, const ui
                      mask, scale, img)
   if (!small) ATX_COL2IM(long long, 0, 9);
   else if (st == 1) { if (one) ATX_COL2IM(int, 1, 1); else ATX_COL2IM(int, 1, 9); }
-  else if (st == 2) { if (one) ATX_COL2IM(int, 2, 1); else ATX_COL2IM(int, 2, 9); }
+  else if (st == 2) {
+    const dim3 grid2(elem_grid((long long)g.N * g.C * ((g.H + 1) / 2) * ((g.W + 1) / 2), TB));
+    const bool vec = g.W % 2 == 0 && ((uintptr_t)img & 7) == 0;
+#define ATX_COL2IM_S2(C, V)                                                                 \
+  hipLaunchKernelGGL((col2im_s2_kernel<int, C, V>), grid2, dim3(TB), 0, stream, col, g, pos, \
+                     mask, scale, img)
+    if (one) { if (vec) ATX_COL2IM_S2(1, true); else ATX_COL2IM_S2(1, false); }
+    else { if (vec) ATX_COL2IM_S2(9, true); else ATX_COL2IM_S2(9, false); }
+#undef ATX_COL2IM_S2
+  }
   else { if (one) ATX_COL2IM(int, 0, 1); else ATX_COL2IM(int, 0, 9); }
 #undef ATX_COL2IM
   return check_launch("col2im_kernel");

@@ -713,7 +713,26 @@ def test_custom_grad_kernels(signed):
 
 TAP_GEOMS = [((2, 5, 9, 7), (3, 3), (1, 1), (1, 1), (1, 1)), ((3, 130, 6, 5), (3, 3), (2, 2), (1, 1), (1, 1)),
              ((2, 64, 7, 7), (1, 1), (1, 1), (0, 0), (1, 1)), ((1, 200, 11, 13), (3, 3), (1, 2), (2, 2), (2, 1)),
-             ((4, 3, 16, 16), (7, 7), (2, 2), (3, 3), (1, 1))]
+             ((4, 3, 16, 16), (7, 7), (2, 2), (3, 3), (1, 1)), ((2, 6, 9, 7), (1, 1), (2, 2), (0, 0), (1, 1)),
+             ((2, 4, 8, 10), (3, 3), (2, 2), (1, 1), (1, 1)), ((1, 3, 11, 9), (3, 3), (2, 2), (2, 2), (2, 2)),
+             ((2, 5, 10, 9), (3, 2), (2, 2), (0, 1), (1, 3))]
+
+
+def fold_f32(col, shape, k, s, p, d):
+    """F.fold in fp32 with every pixel's taps added in ascending (kh, kw)
+    order from +0: the order the col2im kernels document, so their output is
+    this bit for bit."""
+    N, C, H, W = shape
+    OH, OW = O.out_size(H, W, k, s, p, d)
+    padded = np.zeros((N, C, H + 2 * p[0] + s[0] + d[0] * k[0], W + 2 * p[1] + s[1] + d[1] * k[1]),
+                      dtype=np.float32)
+    c6 = np.asarray(col, dtype=np.float32).reshape(N, C, k[0], k[1], OH, OW)
+    for i in range(k[0]):
+        for j in range(k[1]):
+            hs, ws = i * d[0], j * d[1]
+            padded[:, :, hs:hs + s[0] * (OH - 1) + 1:s[0],
+                   ws:ws + s[1] * (OW - 1) + 1:s[1]] += c6[:, :, i, j]
+    return padded[:, :, p[0]:p[0] + H, p[1]:p[1] + W]
 
 
 @pytest.mark.parametrize("shape", [(2, 37, 100), (3, 1, 64), (5, 200, 49), (1, 3, 7), (4, 2048, 9)])
@@ -812,6 +831,14 @@ def test_col2im_pos_ste(case):
     close(got.cpu().numpy(), want, absref)
     plain = ops.col2im(t(col), g)
     close(plain.cpu().numpy(), fcol, O.fold(np.abs(col), shape, k, s_, p, d))
+    # bit for bit: the fp32 sums in ascending tap order, the position sum
+    # added once, then the STE's select and division in fp32
+    f32col = fold_f32(col, shape, k, s_, p, d)
+    f32pos = fold_f32(np.broadcast_to(pos[:, None, :], col.shape), shape, k, s_, p, d)
+    exact = np.where(mask, f32col + f32pos, np.float32(0)) / np.maximum(scale, np.float32(1e-12))
+    assert exact.dtype == np.float32
+    assert np.array_equal(got.cpu().numpy(), exact)
+    assert np.array_equal(plain.cpu().numpy(), f32col)
 
 
 NARROW_SHAPES = CUSTOM_SHAPES +[(2, 64, 3136, 256), (3, 4608, 49, 40), (2, 20, 196, 2048)]
