@@ -73,6 +73,9 @@ _SIGS = {
     "atx_tap_sum_workspace_bytes": (c_ll, [ConvGeom]),
     "atx_tap_sum": (c_int, [c_vp, c_int, ConvGeom, c_vp, c_vp, c_vp, c_vp]),
     "atx_zero_point_pos": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "atx_zero_point_terms_workspace_bytes": (c_ll, [c_int, c_int, c_int]),
+    "atx_zero_point_terms": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                     c_vp, c_vp]),
     "atx_tap_sum_bwd": (c_int, [c_vp, ConvGeom, c_vp, c_vp]),
     "atx_uint8_dequant": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                   c_vp, c_int, c_vp]),

@@ -587,6 +587,30 @@ def zero_point_pos(go: Tensor, scale_x: Tensor, scale_w: Tensor, zero_w: Tensor)
     return pos
 
 
+# channel sums of go in atx_zero_point_terms: at most this many channels
+ZERO_POINT_SUM_MAX_O = 8192
+
+
+def zero_point_terms(go: Tensor, scale_x: Tensor, scale_w: Tensor, zero_w: Tensor,
+                     want_pos: bool = True):
+    """(pos [N, L] or None, gsum [O]) from one pass over go [N, O, L]: pos as
+    zero_point_pos (when want_pos) and gsum[o] = sum_{n,l} go[n, o, l], the
+    gradient of the uint8 layer's -z_x * sum_k q_w[o, k] term and of its
+    bias, summed in a fixed order."""
+    goc = go.contiguous()
+    N, O, Lc = goc.shape
+    if O > ZERO_POINT_SUM_MAX_O:
+        raise RuntimeError(f"zero_point_terms: at most {ZERO_POINT_SUM_MAX_O} channels")
+    pos = torch.empty((N, Lc), dtype=torch.float32, device=goc.device) if want_pos else None
+    gsum = torch.empty(O, dtype=torch.float32, device=goc.device)
+    wsb = L.query("atx_zero_point_terms_workspace_bytes", N, O, Lc)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=goc.device)
+    L.call("atx_zero_point_terms", L.ptr(goc), N, O, Lc, L.ptr(scale_x.contiguous()),
+           L.ptr(scale_w.contiguous()), L.ptr(zero_w.contiguous()), L.ptr(pos), L.ptr(gsum),
+           L.ptr(ws), L.stream_of(goc))
+    return pos, gsum
+
+
 def tap_sum_backward(go: Tensor, g) -> Tensor:
     goc = go.contiguous()
     img = torch.empty((g.N, g.C, g.H, g.W), dtype=torch.float32, device=goc.device)

@@ -424,6 +424,136 @@ channel_dot_kernel(const float* __restrict__ go, int O, int L, const float* __re
   }
 }
 
+// v + the value of the lane that DPP control CTRL picks (0 in the rows that
+// ROW_MASK leaves out).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(
+                 __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum of v over a group of P lanes in a fixed order: pairs (quad_perm
+// [1,0,3,2]), quads ([2,3,0,1]), half rows (row_half_mirror), rows of 16
+// (row_mirror) -- every lane of a row then holds the row's sum -- and for
+// P = 64 rows 0+1 and 2+3 (row_bcast15 into rows 1 and 3), then all four
+// (row_bcast31 into row 3): the wave's sum is in lane 63.
+template <int P>
+__device__ __forceinline__ float group_sum(float v) {
+  v = dpp_add<0xB1, 0xf>(v);
+  v = dpp_add<0x4E, 0xf>(v);
+  v = dpp_add<0x141, 0xf>(v);
+  v = dpp_add<0x140, 0xf>(v);
+  if constexpr (P == 64) {
+    v = dpp_add<0x142, 0xa>(v);
+    v = dpp_add<0x143, 0xc>(v);
+  }
+  return v;
+}
+
+// Both zero-point reductions of go in one pass: pos[n,l] as
+// channel_dot_kernel (the same products and order, so the same bits) when
+// POS, and per-channel sums of go when SUM.  Persistent blocks walk the
+// (image, P-position chunk) pairs blockIdx.x, + gridDim.x, ...; a chunk's
+// value of channel o is summed over its P positions by group_sum and added
+// by one lane to the block's total chs[o] in LDS (channel o belongs to group
+// o % G only, so no two lanes update one total).  At the end each block
+// writes its totals to part[blockIdx.x][O]; chan_total_kernel sums them.
+// Loads: U channels per group in flight per thread.
+template <int P, bool POS, bool SUM>
+__global__ void __launch_bounds__(256)
+zero_point_terms_kernel(const float* __restrict__ go, int N, int O, int L,
+                        const float* __restrict__ sx, const float* __restrict__ sw,
+                        const float* __restrict__ zw, float* __restrict__ pos,
+                        float* __restrict__ part) {
+  constexpr int G = 256 / P;
+  constexpr int U = 8;
+  constexpr int LAST = P == 64 ? 63 : 0;        // the lane that holds a group's sum
+  __shared__ float pp[G][P];
+  extern __shared__ float chs[];                // [O]
+  const int p = threadIdx.x % P, gi = threadIdx.x / P;
+  const int nlb = (L + P - 1) / P;
+  const long long total = (long long)N * nlb;
+  const float s = POS ? sx[0] : 0.0f;
+  if constexpr (SUM)
+    for (int o = threadIdx.x; o < O; o += 256) chs[o] = 0.0f;
+  __syncthreads();
+  for (long long c = blockIdx.x; c < total; c += gridDim.x) {
+    const long long n = c / nlb;
+    const int l = (int)(c - n * nlb) * P + p;
+    const bool in = l < L;
+    const float* src = go + n * O * L + (in ? l : 0);
+    float acc = 0.0f;
+    for (int o0 = gi; o0 < O; o0 += G * U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int o = o0 + G * u;
+        v[u] = in && o < O ? src[(long long)o * L] : 0.0f;
+      }
+      if constexpr (POS) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int o = o0 + G * u;
+          if (o < O) acc += -((s * sw[o]) * zw[o]) * v[u];
+        }
+      }
+      if constexpr (SUM) {
+        float t[U], prev[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) t[u] = group_sum<P>(v[u]);
+        if (p == LAST) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) prev[u] = o0 + G * u < O ? chs[o0 + G * u] : 0.0f;
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            if (o0 + G * u < O) chs[o0 + G * u] = prev[u] + t[u];
+        }
+      }
+    }
+    if constexpr (POS) {
+      pp[gi][p] = acc;
+      __syncthreads();
+      if (gi == 0 && in) {
+        float t = pp[0][p];
+#pragma unroll
+        for (int j = 1; j < G; ++j) t += pp[j][p];
+        pos[n * L + l] = t;
+      }
+      __syncthreads();                          // pp is rewritten by the next chunk
+    }
+  }
+  if constexpr (SUM) {
+    __syncthreads();
+    for (int o = threadIdx.x; o < O; o += 256) part[(long long)blockIdx.x * O + o] = chs[o];
+  }
+}
+
+__global__ void zp_zero_kernel(float* __restrict__ out, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = 0.0f;
+}
+
+// gsum[o] = sum over b < nb of part[b][o]: 16 slices (b = s, s + 16, ...)
+// per channel, combined in slice order (deterministic).
+__global__ void __launch_bounds__(256)
+chan_total_kernel(const float* __restrict__ part, int nb, int O, float* __restrict__ gsum) {
+  __shared__ float sl[16][16];
+  const int c = threadIdx.x % 16, sidx = threadIdx.x / 16;
+  const int o = blockIdx.x * 16 + c;
+  float a = 0.0f;
+  if (o < O) {
+#pragma unroll 8
+    for (int b = sidx; b < nb; b += 16) a += part[(long long)b * O + o];
+  }
+  sl[sidx][c] = a;
+  __syncthreads();
+  if (sidx == 0 && o < O) {
+    float t = sl[0][c];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) t += sl[j][c];
+    gsum[o] = t;
+  }
+}
+
 // Backward of tap_sum: img_grad[n,c,h,w] = sum of go[n,l] over the taps
 // (kh, kw) that read (h, w) (independent of c).
 __global__ void tap_sum_bwd_kernel(const float* __restrict__ go, atx_conv_geom g,
@@ -626,6 +756,51 @@ int atx_zero_point_pos(const float* go, int N, int O, int L, const float* scale_
     hipLaunchKernelGGL(channel_dot_kernel<16>, dim3((unsigned)cdiv(L, 16), (unsigned)N),
                        dim3(256), 0, stream, go, O, L, scale_x, scale_w, zero_w, pos);
   return check_launch("channel_dot_kernel");
+}
+
+// Blocks of zero_point_terms_kernel: enough resident waves to stream go,
+// few enough partial rows for chan_total_kernel.
+constexpr int ZP_BLOCKS = 1024;
+constexpr int ZP_MAX_O = 8192;          // the per-block channel totals in LDS (32 KiB)
+
+static long long zp_blocks(int N, int L) {
+  const int P = L >= 64 ? 64 : 16;
+  return std::max<long long>(1, std::min<long long>(ZP_BLOCKS, (long long)N * cdiv(L, P)));
+}
+
+long long atx_zero_point_terms_workspace_bytes(int N, int O, int L) {
+  if (N <= 0 || O <= 0 || L <= 0) return 0;
+  return zp_blocks(N, L) * O * (long long)sizeof(float);
+}
+
+int atx_zero_point_terms(const float* go, int N, int O, int L, const float* scale_x,
+                         const float* scale_w, const float* zero_w, float* pos, float* gsum,
+                         float* workspace, hipStream_t stream) {
+  ATX_REQUIRE(N >= 0 && O >= 0 && L >= 0, "atx_zero_point_terms: negative size");
+  ATX_REQUIRE(O <= ZP_MAX_O || !gsum, "atx_zero_point_terms: channel sums support at most %d channels",
+              ZP_MAX_O);
+  if (!gsum) return atx_zero_point_pos(go, N, O, L, scale_x, scale_w, zero_w, pos, stream);
+  if (O == 0) return ATX_OK;
+  const long long NL = (long long)N * L;
+  if (NL == 0) {                          // empty sums; no positions to write
+    hipLaunchKernelGGL(zp_zero_kernel, dim3(1), dim3(256), 0, stream, gsum, O);
+    return check_launch("zp_zero_kernel");
+  }
+  ATX_REQUIRE(go && workspace && (!pos || (scale_x && scale_w && zero_w)),
+              "atx_zero_point_terms: null pointer");
+  const int nb = (int)zp_blocks(N, L);
+  const size_t lds = (size_t)O * sizeof(float);
+#define ATX_ZPT(P, POS)                                                                        \
+  hipLaunchKernelGGL((zero_point_terms_kernel<P, POS, true>), dim3(nb), dim3(256), lds, stream, \
+                     go, N, O, L, scale_x, scale_w, zero_w, pos, workspace)
+  if (L >= 64) { if (pos) ATX_ZPT(64, true); else ATX_ZPT(64, false); }
+  else { if (pos) ATX_ZPT(16, true); else ATX_ZPT(16, false); }
+#undef ATX_ZPT
+  int rc = check_launch("zero_point_terms_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(chan_total_kernel, dim3((unsigned)cdiv(O, 16)), dim3(256), 0, stream,
+                     workspace, nb, O, gsum);
+  return check_launch("chan_total_kernel");
 }
 
 int atx_col2im(const float* col, atx_conv_geom g, const uint8_t* mask, const float* scale,

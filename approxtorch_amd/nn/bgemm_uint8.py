@@ -285,8 +285,12 @@ class _conv2d_uint8_fused(Function):
         gx = gw = gb = None
         # zero-point terms: -sum_o g' z_w[o] per position (a channel reduction
         # per image) and -z_x sum_{n,l} g' per channel
-        gxs = ops.zero_point_pos(go, sx, sw, zw) if need_x else None
-        gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
+        gxs = gsum = None
+        if (need_w or need_b) and O <= ops.ZERO_POINT_SUM_MAX_O:
+            gxs, gsum = ops.zero_point_terms(go, sx, sw, zw, want_pos=need_x)
+        else:
+            gxs = ops.zero_point_pos(go, sx, sw, zw) if need_x else None
+            gsum = go.sum(dim=(0, 2)) if (need_w or need_b) else None
         if ctx.kind == 'custom':
             # a 1x1 stride-1 unpadded conv's column gradient is its image
             # gradient: the matrix-core grad_x applies the zero-point term and

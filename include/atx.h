@@ -375,6 +375,21 @@ int atx_zero_point_pos(const float* go, int N, int O, int L, const float* scale_
                        const float* scale_w, const float* zero_w, float* pos,
                        hipStream_t stream);
 
+/* Both reductions of go [N,O,L] that the uint8 layer's backward needs, in
+ * one pass over go: pos as atx_zero_point_pos (nullable: then only the
+ * sums), and gsum[o] = sum_{n,l} go[n,o,l] (O <= 8192), the gradient that
+ * reaches the -z_x * sum_k q_w[o,k] term and the bias.  Each block of
+ * positions is summed in a fixed lane order, each persistent workgroup's
+ * blocks in order, and the workgroups' totals in a fixed order
+ * (deterministic).  gsum == NULL: atx_zero_point_pos.  workspace:
+ * atx_zero_point_terms_workspace_bytes(N, O, L) bytes.  Replaces go.sum over
+ * (n, l) in the reference's autograd through nn/Conv2d_uint8.py:312-315
+ * (the zero_x * wsum term) and :320-321 (the bias). */
+long long atx_zero_point_terms_workspace_bytes(int N, int O, int L);
+int atx_zero_point_terms(const float* go, int N, int O, int L, const float* scale_x,
+                         const float* scale_w, const float* zero_w, float* pos, float* gsum,
+                         float* workspace, hipStream_t stream);
+
 /* --------------------------------------------------------------- EMA stats
  * absmax EMA (nn/Conv2d_int8.py:137-146):
  *   stat = max|x|; scale <- m*(stat/denom) + (1-m)*scale, in fp32 with

@@ -754,6 +754,35 @@ def test_zero_point_pos(shape):
     close(a.cpu().numpy(), want, bound)
 
 
+@pytest.mark.parametrize("shape", [(2, 37, 100), (3, 1, 64), (5, 200, 49), (1, 3, 7), (4, 2048, 9),
+                                   (3, 130, 30), (64, 20, 3136), (2, 5000, 20), (2, 4, 0)])
+@pytest.mark.parametrize("want_pos", [True, False])
+def test_zero_point_terms(shape, want_pos):
+    """atx_zero_point_terms: pos equal bit for bit to atx_zero_point_pos and
+    gsum[o] = sum_{n,l} go[n,o,l] against fp64 (rel 1e-5 of the sum of
+    |terms| + abs 1e-4), both identical run to run.  Shapes: 64- and
+    16-position blocks (L >= 64 / < 64), channel counts that are not a
+    multiple of a group's eight loads, more position blocks than workgroups
+    (each walks several), more than 4096 channels, and L = 0 (zero sums)."""
+    N, Oc, Lc = shape
+    r = gen(zlib.crc32(repr(("zpt", shape)).encode()))
+    go = r.standard_normal(shape).astype(np.float32)
+    sx = np.float32(0.037)
+    sw = (r.random(Oc) * 0.1 + 0.01).astype(np.float32)
+    zw = r.integers(0, 16, Oc).astype(np.float32)
+    args = (t(go), t(np.array(sx)), t(sw), t(zw))
+    pos, gsum = ops.zero_point_terms(*args, want_pos=want_pos)
+    pos2, gsum2 = ops.zero_point_terms(*args, want_pos=want_pos)
+    assert torch.equal(gsum, gsum2)
+    want = go.astype(np.float64).sum(axis=(0, 2))
+    close(gsum.cpu().numpy(), want, np.abs(go).astype(np.float64).sum(axis=(0, 2)))
+    if want_pos:
+        assert torch.equal(pos, pos2)
+        assert torch.equal(pos, ops.zero_point_pos(*args))
+    else:
+        assert pos is None
+
+
 @pytest.mark.parametrize("case", TAP_GEOMS)
 @pytest.mark.parametrize("dtype", ["uint8", "float32"])
 def test_tap_sum_exact(case, dtype):
