@@ -456,7 +456,8 @@ __device__ __forceinline__ float group_sum(float v) {
 // (image, P-position chunk) pairs blockIdx.x, + gridDim.x, ...; a chunk's
 // value of channel o is summed over its P positions by group_sum and added
 // by one lane to the block's total chs[o] in LDS (channel o belongs to group
-// o % G only, so no two lanes update one total).  At the end each block
+// o % G only: each total has one writer lane, whose LDS adds take effect in
+// program order, so the sums are the same run to run).  At the end each block
 // writes its totals to part[blockIdx.x][O]; chan_total_kernel sums them.
 // Loads: U channels per group in flight per thread.
 template <int P, bool POS, bool SUM>
@@ -498,15 +499,13 @@ zero_point_terms_kernel(const float* __restrict__ go, int N, int O, int L,
         }
       }
       if constexpr (SUM) {
-        float t[U], prev[U];
+        float t[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) t[u] = group_sum<P>(v[u]);
-        if (p == LAST) {
-#pragma unroll
-          for (int u = 0; u < U; ++u) prev[u] = o0 + G * u < O ? chs[o0 + G * u] : 0.0f;
+        if (p == LAST) {      // LDS adds without a return value: nothing waits on them
 #pragma unroll
           for (int u = 0; u < U; ++u)
-            if (o0 + G * u < O) chs[o0 + G * u] = prev[u] + t[u];
+            if (o0 + G * u < O) atomicAdd(&chs[o0 + G * u], t[u]);
         }
       }
     }
@@ -760,7 +759,7 @@ int atx_zero_point_pos(const float* go, int N, int O, int L, const float* scale_
 
 // Blocks of zero_point_terms_kernel: enough resident waves to stream go,
 // few enough partial rows for chan_total_kernel.
-constexpr int ZP_BLOCKS = 1024;
+constexpr int ZP_BLOCKS = 2048;
 constexpr int ZP_MAX_O = 8192;          // the per-block channel totals in LDS (32 KiB)
 
 static long long zp_blocks(int N, int L) {
