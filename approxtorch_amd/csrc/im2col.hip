@@ -359,6 +359,48 @@ __global__ void tap_chan_sum_kernel(const T* __restrict__ img, int C, int HW, in
   }
 }
 
+// The same chunk sums for a byte image whose planes are 4-byte aligned
+// (H * W % 4 == 0): a thread owns four consecutive pixels and reads them
+// with one 4-byte load per channel, 16 channels' loads in flight.  The
+// bytes are summed two to a register in 16-bit fields (even bytes, odd
+// bytes; at most 64 * 255 = 16320 per field, so no carry crosses a field):
+// the integer sums, converted once, are the values tap_chan_sum_kernel's
+// fp32 sums of integers below 2^24 give.
+__global__ void __launch_bounds__(256)
+tap_chan_sum_u8x4_kernel(const uint8_t* __restrict__ img, int C, int HW, int chunks,
+                         long long total4, float* __restrict__ partial) {
+  constexpr int U = 16;
+  const int HW4 = HW >> 2;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total4; i += stride) {
+    const int p4 = (int)(i % HW4);
+    const long long t = i / HW4;
+    const int ch = (int)(t % chunks);
+    const long long n = t / chunks;
+    const int c0 = ch * TS_CHUNK, nc = min(C - c0, TS_CHUNK);
+    const unsigned* src = (const unsigned*)(img + (n * C + c0) * HW) + p4;
+    unsigned ev = 0, od = 0;                  // bytes 0 and 2 / 1 and 3, 16 bits each
+    int c = 0;
+    for (; c + U <= nc; c += U) {
+      unsigned v[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) v[j] = src[(long long)(c + j) * HW4];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        ev += v[j] & 0x00ff00ffu;
+        od += (v[j] >> 8) & 0x00ff00ffu;
+      }
+    }
+    for (; c < nc; ++c) {
+      const unsigned v = src[(long long)c * HW4];
+      ev += v & 0x00ff00ffu;
+      od += (v >> 8) & 0x00ff00ffu;
+    }
+    *(float4*)(partial + 4 * i) = make_float4((float)(ev & 0xffffu), (float)(od & 0xffffu),
+                                              (float)(ev >> 16), (float)(od >> 16));
+  }
+}
+
 __global__ void tap_window_sum_kernel(const float* __restrict__ partial, atx_conv_geom g,
                                       int chunks, const float* __restrict__ pad_dev,
                                       float* __restrict__ out) {
@@ -715,9 +757,13 @@ int atx_tap_sum(const void* img, int dtype, atx_conv_geom g, const float* pad_de
   const long long ptotal = (long long)g.N * chunks * g.H * g.W;
   if (ptotal > 0) {
     ATX_REQUIRE(img && workspace, "atx_tap_sum: null image / workspace");
-    if (dtype == 1)
+    const int HW = g.H * g.W;
+    if (dtype == 1 && HW % 4 == 0 && ((uintptr_t)img & 3) == 0 && ((uintptr_t)workspace & 15) == 0)
+      hipLaunchKernelGGL(tap_chan_sum_u8x4_kernel, dim3(elem_grid(ptotal / 4, TB)), dim3(TB), 0,
+                         stream, (const uint8_t*)img, g.C, HW, chunks, ptotal / 4, workspace);
+    else if (dtype == 1)
       hipLaunchKernelGGL(tap_chan_sum_kernel<uint8_t>, dim3(elem_grid(ptotal, TB)), dim3(TB), 0,
-                         stream, (const uint8_t*)img, g.C, g.H * g.W, chunks, ptotal, workspace);
+                         stream, (const uint8_t*)img, g.C, HW, chunks, ptotal, workspace);
     else
       hipLaunchKernelGGL(tap_chan_sum_kernel<float>, dim3(elem_grid(ptotal, TB)), dim3(TB), 0,
                          stream, (const float*)img, g.C, g.H * g.W, chunks, ptotal, workspace);

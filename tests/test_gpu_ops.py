@@ -715,7 +715,8 @@ TAP_GEOMS = [((2, 5, 9, 7), (3, 3), (1, 1), (1, 1), (1, 1)), ((3, 130, 6, 5), (3
              ((2, 64, 7, 7), (1, 1), (1, 1), (0, 0), (1, 1)), ((1, 200, 11, 13), (3, 3), (1, 2), (2, 2), (2, 1)),
              ((4, 3, 16, 16), (7, 7), (2, 2), (3, 3), (1, 1)), ((2, 6, 9, 7), (1, 1), (2, 2), (0, 0), (1, 1)),
              ((2, 4, 8, 10), (3, 3), (2, 2), (1, 1), (1, 1)), ((1, 3, 11, 9), (3, 3), (2, 2), (2, 2), (2, 2)),
-             ((2, 5, 10, 9), (3, 2), (2, 2), (0, 1), (1, 3))]
+             ((2, 5, 10, 9), (3, 2), (2, 2), (0, 1), (1, 3)), ((2, 150, 12, 8), (3, 3), (1, 1), (1, 1), (1, 1)),
+             ((3, 80, 14, 14), (1, 1), (1, 1), (0, 0), (1, 1))]
 
 
 def fold_f32(col, shape, k, s, p, d):
@@ -796,6 +797,18 @@ def test_tap_sum_exact(case, dtype):
     src = t(img) if dtype == "uint8" else t(img.astype(np.float32))
     got = ops.tap_sum(src, g, pad_dev=t(np.array([z], np.float32)))
     want = O.im2col_index(img, k, s_, p, d, int(z)).astype(np.int64).sum(axis=1)
+    assert np.array_equal(got.cpu().numpy(), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("shape", [(2, 130, 8, 12), (1, 64, 4, 4)])
+def test_tap_sum_saturated(shape):
+    """Byte images of 255 everywhere (H * W % 4 == 0: the 4-pixel kernel, whose
+    16-bit fields then hold their largest sums, 64 * 255): exact."""
+    img = np.full(shape, 255, dtype=np.uint8)
+    z = np.float32(3.0)
+    g = ops.conv_geom(shape, (3, 3), (1, 1), (1, 1), (1, 1))
+    got = ops.tap_sum(t(img), g, pad_dev=t(np.array([z], np.float32)))
+    want = O.im2col_index(img, (3, 3), (1, 1), (1, 1), (1, 1), int(z)).astype(np.int64).sum(axis=1)
     assert np.array_equal(got.cpu().numpy(), want.astype(np.float32))
 
 
