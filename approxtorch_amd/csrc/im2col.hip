@@ -31,9 +31,12 @@ template <> __device__ __forceinline__ unsigned elem_index<float>(float v, int o
 // of the block's slots (channel, kh, kw) are decomposed once into an LDS
 // table; slot s of quad q holds tap (s & ~3) | ((q + s) & 3).  The run is
 // `slots` long (a multiple of 4, at most IM_SLOTS): shorter runs give small
-// images (few row quads) more blocks.
+// images (few row quads) more blocks.  PW4 (byte images of a 1x1, stride-1,
+// unpadded conv with L % 4 == 0 and a 4-byte aligned image): a row quad is
+// four consecutive bytes of each channel plane, read with one 4-byte load
+// per tap (the int8 index v + 128 of byte b is b ^ 0x80).
 constexpr int IM_SLOTS = 32;
-template <typename T>
+template <typename T, bool PW4 = false>
 __global__ void __launch_bounds__(TB)
 im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int pad_index,
                    const float* __restrict__ pad_dev, uint16_t* __restrict__ xt, int Rpad,
@@ -78,6 +81,28 @@ im2col_rows_kernel(const T* __restrict__ img, atx_conv_geom g, int offset, int p
   }
   const int nslots = min(slots, operand_rows(K) - k0);   // a multiple of 4
   uint16_t* dst = xt + (long long)k0 * Rpad + r0;
+  if constexpr (PW4) {
+    const unsigned flip = offset == 128 ? 0x80808080u : 0u;
+    for (int s4 = 0; s4 < nslots; s4 += 4) {
+      unsigned w4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int kl = s4 | ((q + u) & 3);
+        const bool b = k0 + kl < K && valid;   // L % 4 == 0: a quad is all rows or none
+        w4[u] = b ? *(const unsigned*)(img + base[0] + toff[kl]) ^ flip : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool b = k0 + (s4 | ((q + u) & 3)) < K && valid;
+        unsigned off[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) off[e] = b ? row_offset((w4[u] >> (8 * e)) & 255u) : 0u;
+        *(uint2*)(dst + (long long)(s4 + u) * Rpad) =
+            make_uint2(off[0] | (off[1] << 16), off[2] | (off[3] << 16));
+      }
+    }
+    return;
+  }
   for (int s4 = 0; s4 < nslots; s4 += 4) {
     // one quad of taps per iteration: its 16 loads are in flight together
     T raw[4][4];
@@ -666,7 +691,15 @@ int atx_im2col_rows(const void* img, int dtype, atx_conv_geom g, int pad_index,
   while (slots > 4 && xblocks * cdiv(operand_rows(K), slots) < 2048) slots >>= 1;
   ATX_REQUIRE(cdiv(operand_rows(K), slots) <= 65535, "atx_im2col_rows: K too large");
   dim3 grid((unsigned)xblocks, (unsigned)cdiv(operand_rows(K), slots));
-  if (dtype == 0)
+  const bool pw4 = g.KH == 1 && g.KW == 1 && g.SH == 1 && g.SW == 1 && g.PH == 0 && g.PW == 0 &&
+                   (g.H * g.W) % 4 == 0 && ((uintptr_t)img & 3) == 0;
+  if (pw4 && dtype == 0)
+    hipLaunchKernelGGL((im2col_rows_kernel<int8_t, true>), grid, dim3(TB), 0, stream,
+                       (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad, slots);
+  else if (pw4 && dtype == 1)
+    hipLaunchKernelGGL((im2col_rows_kernel<uint8_t, true>), grid, dim3(TB), 0, stream,
+                       (const uint8_t*)img, g, 0, pad_index, pad_dev, xt, Rpad, slots);
+  else if (dtype == 0)
     hipLaunchKernelGGL(im2col_rows_kernel<int8_t>, grid, dim3(TB), 0, stream,
                        (const int8_t*)img, g, 128, pad_index, pad_dev, xt, Rpad, slots);
   else if (dtype == 1)

@@ -511,7 +511,9 @@ def test_im2col_rows_slot_runs_sampled(case):
 
 # (N, C, H, W): L = 49 and K = 6 take the element-wise path, L = 64 / 784
 # the 16-byte one; K = 40 and 64 span two slot runs; the last is a 1x1 pixel.
-FQ_ROWS_CASES = [(2, 6, 7, 7), (3, 40, 8, 8), (2, 64, 28, 28), (5, 3, 1, 1)]
+# With L % 4 == 0 the byte image's im2col reads 4-byte row quads; (3, 6, 4, 4)
+# has K % 4 != 0 and padding rows past N*L.
+FQ_ROWS_CASES = [(2, 6, 7, 7), (3, 40, 8, 8), (2, 64, 28, 28), (5, 3, 1, 1), (3, 6, 4, 4)]
 
 
 @pytest.mark.parametrize("shape", FQ_ROWS_CASES)
