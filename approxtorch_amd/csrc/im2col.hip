@@ -376,10 +376,18 @@ __global__ void tap_chan_sum_kernel(const T* __restrict__ img, int C, int HW, in
     const long long t = i / HW;
     const int ch = (int)(t % chunks);
     const int n = (int)(t / chunks);
-    const int c0 = ch * TS_CHUNK, c1 = min(C, c0 + TS_CHUNK);
-    const T* src = img + ((long long)n * C + c0) * HW + p;
+    const int nc = min(C - ch * TS_CHUNK, TS_CHUNK);
+    const T* src = img + ((long long)n * C + ch * TS_CHUNK) * HW + p;
     float a = 0.0f;
-    for (int c = c0; c < c1; ++c, src += HW) a += (float)*src;
+    int c = 0;
+    for (; c + 16 <= nc; c += 16) {           // 16 channels' loads in flight, added in order
+      T v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = src[(long long)(c + j) * HW];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a += (float)v[j];
+    }
+    for (; c < nc; ++c) a += (float)src[(long long)c * HW];
     partial[i] = a;
   }
 }
