@@ -272,6 +272,71 @@ col2im_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __res
   }
 }
 
+// col2im with at most 9 taps and stride 1, one thread per pixel position
+// (n, h, w) and run of CC channels (blockIdx.y): the taps that reach the
+// position, their col offsets and the position-term sum (the same for every
+// channel, in the same ascending tap order) are worked out once and reused
+// for each channel, whose tap loads, mask byte and store are then coalesced
+// across the threads (consecutive w).  The same values as col2im_kernel.
+// Taken when a position term is given: c5-shape 3 x 3 layers at batch 128
+// take 225 / 124 / 55 / 27 us against 424 / 200 / 87 / 43 us for
+// col2im_kernel, which re-reads the position term per channel; without one
+// the two kernels are within 5% of each other and col2im_kernel stays.
+constexpr int C2_CC = 16;
+template <typename I>
+__global__ void __launch_bounds__(TB)
+col2im_cc_kernel(const float* __restrict__ col, atx_conv_geom g, const float* __restrict__ pos,
+                 const uint8_t* __restrict__ mask, const float* __restrict__ scale,
+                 float* __restrict__ img) {
+  const int L = g.OH * g.OW;
+  const int KK = g.KH * g.KW;
+  const int HW = g.H * g.W;
+  const I total = (I)g.N * HW;
+  const float s = mask ? fmaxf(scale[0], 1e-12f) : 1.0f;
+  const int c0 = blockIdx.y * C2_CC, nc = min(g.C - c0, C2_CC);
+  for (I i = (I)blockIdx.x * TB + threadIdx.x; i < total; i += (I)gridDim.x * TB) {
+    const I n = i / HW;
+    const int p = (int)(i - n * HW);
+    const int h = p / g.W, w = p - h * g.W;
+    int at[9];
+    unsigned ok = 0;
+    int kh = 0, kw = 0;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const int oh = h + g.PH - kh * g.DH, ow = w + g.PW - kw * g.DW;
+      const bool hit = j < KK && oh >= 0 && ow >= 0 && oh < g.OH && ow < g.OW;
+      at[j] = hit ? j * L + oh * g.OW + ow : 0;
+      ok |= (hit ? 1u : 0u) << j;
+      if (++kw == g.KW) { kw = 0; ++kh; }
+    }
+    float b = 0.0f;
+    if (pos) {
+      const float* pn = pos + (long long)n * L;
+      float u[9];
+#pragma unroll
+      for (int j = 0; j < 9; ++j) u[j] = pn[(ok >> j) & 1u ? at[j] - j * L : 0];
+#pragma unroll
+      for (int j = 0; j < 9; ++j)
+        if ((ok >> j) & 1u) b += u[j];
+    }
+    for (int cc = 0; cc < nc; ++cc) {
+      const I plane = n * g.C + c0 + cc;
+      const float* cn = col + (long long)plane * KK * L;
+      float v[9];
+#pragma unroll
+      for (int j = 0; j < 9; ++j) v[j] = cn[at[j]];
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 9; ++j)
+        if ((ok >> j) & 1u) a += v[j];
+      if (pos) a += b;
+      const I idx = plane * HW + p;
+      if (mask) a = (mask[idx] ? a : 0.0f) / s;
+      img[idx] = a;
+    }
+  }
+}
+
 // col2im with both strides 2, one thread per 2 x 2 block of pixels (rows
 // 2a, 2a + 1, columns 2b, 2b + 1).  Pixel row h = 2a + e is reached by tap
 // row kh when h + PH - kh * DH is even, i.e. for e = (PH - kh * DH) & 1
@@ -909,6 +974,11 @@ int atx_col2im_pos(const float* col, atx_conv_geom g, const float* pos, const ui
   hipLaunchKernelGGL((col2im_kernel<I, S, C>), grid, dim3(TB), 0, stream, col, g, pos,    \
                      mask, scale, img)
   if (!small) ATX_COL2IM(long long, 0, 9);
+  else if (st == 1 && !one && g.KH * g.KW <= 9 && pos) {
+    const dim3 grid_cc(elem_grid((long long)g.N * g.H * g.W, TB), (unsigned)cdiv(g.C, C2_CC));
+    hipLaunchKernelGGL(col2im_cc_kernel<int>, grid_cc, dim3(TB), 0, stream, col, g, pos, mask,
+                       scale, img);
+  }
   else if (st == 1) { if (one) ATX_COL2IM(int, 1, 1); else ATX_COL2IM(int, 1, 9); }
   else if (st == 2) {
     const dim3 grid2(elem_grid((long long)g.N * g.C * ((g.H + 1) / 2) * ((g.W + 1) / 2), TB));
