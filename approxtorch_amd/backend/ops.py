@@ -1088,9 +1088,9 @@ def fakequant_per_tensor_backward(grad_output: Tensor, mask: Tensor, scale: Tens
 
 
 def fakequant_per_channel(w: Tensor, scale: Tensor, qmin: int, qmax: int, zero_point=None,
-                          offset=None, want_wt=False):
-    """Per-channel (axis 0) fake-quant of a weight: (q, mask, wq index image,
-    wt GEMM operand or None, Opad)."""
+                          offset=None, want_wt=False, want_q=True):
+    """Per-channel (axis 0) fake-quant of a weight: (q or None, mask, wq index
+    image, wt GEMM operand or None, Opad)."""
     require_cuda_f32(w, "w")
     if w.dim() < 1:
         raise RuntimeError("w must have a channel dimension")
@@ -1101,7 +1101,7 @@ def fakequant_per_channel(w: Tensor, scale: Tensor, qmin: int, qmax: int, zero_p
         raise RuntimeError(f"qmin must be < qmax, got [{qmin}, {qmax}]")
     wc = w.contiguous()
     inner = wc.numel() // max(O, 1)
-    q = torch.empty_like(wc)
+    q = torch.empty_like(wc) if want_q else None
     mask = torch.empty(wc.shape, dtype=torch.bool, device=wc.device)
     wq = torch.empty((O, inner), dtype=torch.uint8, device=wc.device) if offset is not None \
         else None

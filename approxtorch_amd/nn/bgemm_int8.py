@@ -261,11 +261,7 @@ class _conv2d_int8_fused(Function):
         else:
             _, mask_x, xq8 = ops.fakequant_per_tensor(x, scale_x, qmin, qmax, want_q=False,
                                                       q8_dtype=torch.int8, nonneg=fq_flag)
-        # per-channel scales promote an fp16 / bf16 weight's x / s to fp32
-        # (nn/quantization.py:100-105): the fp32 kernels on its exact values
-        _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight.detach().float(), scale_w,
-                                                            -qmax_w, qmax_w, offset=128,
-                                                            want_wt=not depthwise)
+        mask_w, wq, wt, Opad = weight_pack(weight, scale_w, qmax_w, not depthwise)
         # addcmul(bias, y, s) promotes a low-precision bias to fp32 as well
         b = None if bias is None else bias.detach().float().contiguous()
         if pointwise:
@@ -333,6 +329,18 @@ class _conv2d_int8_fused(Function):
         if ctx.has_bias and ctx.needs_input_grad[2]:
             gb = go.sum(dim=(0, 2, 3))
         return gx, gw, gb, None, None, None, None, None, None, None, None, None, None, None
+
+
+def weight_pack(weight, scale_w, qmax_w, want_wt=True):
+    """The fused layer's weight operand: per-channel fake-quant of W to
+    indices w + 128 in [-qmax_w, qmax_w] + 128 (mask, wq [O, K], the transposed
+    GEMM operand wt or None, Opad), no fp32 fake-quantized copy.  Per-channel
+    scales promote an fp16 / bf16 weight's x / s to fp32
+    (nn/quantization.py:100-105): the fp32 kernels run on its exact values."""
+    _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight.detach().float(), scale_w,
+                                                        -qmax_w, qmax_w, offset=128,
+                                                        want_wt=want_wt, want_q=False)
+    return mask_w, wq, wt, Opad
 
 
 def conv2d_int8_fused(x, weight, bias, scale_x, scale_w, lut, tx, tw, geom, qmin, qmax,

@@ -254,7 +254,7 @@ class _conv2d_uint8_fused(Function):
                                                   want_q=False, q8_dtype=torch.uint8)
         _, mask_w, wq, wt, Opad = ops.fakequant_per_channel(weight, scale_w, 0, qmax_w,
                                                             zero_point=zero_w, offset=0,
-                                                            want_wt=True)
+                                                            want_wt=True, want_q=False)
         # at most 16 weight indices (weight_bits <= 4): matrix-core LUT GEMM and grad_x
         wbase = 0 if qmax_w <= 15 else None
         y, _, (xt, Rpad) = ops.conv_forward(q8, wq, lut, g, 0, 0, pad_dev=zero_x,
