@@ -61,6 +61,9 @@ _SIGS = {
     "atx_lut_gemm_narrow_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
     "atx_lut_gemm_narrow": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp,
                                     c_int, c_int, GemmEpilogue, c_vp, c_vp, c_vp]),
+    "atx_lut_gemm_narrow_uint8": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int,
+                                          c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                          c_vp, c_vp, c_vp]),
     "atx_fakequant_fwd": (c_int, [c_vp, c_ll, c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                   c_vp, c_vp]),
     "atx_fakequant_rows": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp, c_int, c_int, c_int,

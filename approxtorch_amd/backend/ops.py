@@ -151,13 +151,30 @@ def date_tables(lut: Tensor, half_ws: int = 32):
 
 # -------------------------------------------------------------- LUT GEMM
 def _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx=None, sw=None, bias=None,
-          transposed=False, wbase=None, x_upper=None):
+          transposed=False, wbase=None, x_upper=None, u8=None):
     """wbase: the caller guarantees every weight index lies in [wbase, wbase + 16)
     (weight_bits <= 4); integer LUTs then run on the matrix cores.  x_upper: a
     device int32 flag that, when nonzero, guarantees every activation index of
-    the rows is >= 128 (atx_gemm_epilogue.x_upper; upper-half tables)."""
+    the rows is >= 128 (atx_gemm_epilogue.x_upper; upper-half tables).
+    u8 = (xsum, wsum, zero_x, zero_w): the uint8 layer's zero-point correction
+    and dequant by sx * sw (+ bias) into the fp32 y, in the matrix-core GEMM's
+    epilogue when it runs (wbase 0, integer LUT), else as atx_uint8_dequant
+    after the fp32 sums; the same values either way."""
     img16, imgf, cls = lut_image(lut, transposed)
     dev = y.device
+    if u8 is not None:
+        xsum, wsum, zx, zw = u8
+        if wbase == 0 and cls != L.ATX_LUT_F32 and K > 0:
+            wsb = L.query("atx_lut_gemm_narrow_workspace_bytes", N, K, Lc, O)
+            ws = torch.empty(max(wsb // 4, 1), dtype=torch.int32, device=dev) if wsb else None
+            L.call("atx_lut_gemm_narrow_uint8", L.ptr(xt), Rpad, L.ptr(wt), Opad, N, K, Lc, O,
+                   L.ptr(img16), cls, L.ptr(sx), L.ptr(sw), L.ptr(bias), L.ptr(xsum),
+                   L.ptr(wsum), L.ptr(zx), L.ptr(zw), L.ptr(y), L.ptr(ws), L.stream_of(y))
+            return y
+        _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, L.ATX_OUT_F32, y, transposed=transposed,
+              wbase=wbase, x_upper=x_upper)
+        uint8_dequant(y, xsum, wsum, zx, zw, sx, sw, bias, K)
+        return y
     ep = L.GemmEpilogue(out_kind, L.ptr(sx), L.ptr(sw), L.ptr(bias), L.ptr(x_upper))
     if wbase is not None and cls != L.ATX_LUT_F32:
         wsb = L.query("atx_lut_gemm_narrow_workspace_bytes", N, K, Lc, O)
@@ -393,7 +410,7 @@ def conv_geom(x_shape, kernel_size, stride, padding, dilation):
 def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
                  pad_index: int, out_kind=L.ATX_OUT_F32, sx=None, sw=None, bias=None,
                  pad_dev=None, packed_w=None, return_operand=False, wbase=None,
-                 x_upper=None):
+                 x_upper=None, u8=None):
     """LUT conv via implicit im2col: y [N, O, OH*OW] = sum_k lut[xi][wi].
 
     img: quantized image [N,C,H,W] (int8 values, uint8 values or fp32 values;
@@ -405,7 +422,8 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     row-offset operand for conv_backward_weight_rows.  wbase: every weight
     index lies in [wbase, wbase + 16) (weight_bits <= 4; matrix-core GEMM).
     x_upper: device flag as in _gemm (the image's indices and pad_index are
-    all >= 128 when it is set)."""
+    all >= 128 when it is set).  u8: the uint8 correction and dequant terms as
+    in _gemm (y is then the layer's fp32 output)."""
     imgc = img.contiguous()
     N, K = g.N, g.C * g.KH * g.KW
     Lc = g.OH * g.OW
@@ -424,7 +442,7 @@ def conv_forward(img: Tensor, w_idx_or_val: Tensor, lut: Tensor, g, offset: int,
     ydt = torch.int32 if out_kind == L.ATX_OUT_I32 else torch.float32
     y = torch.empty((N, O, Lc), dtype=ydt, device=dev)
     _gemm(xt, Rpad, wt, Opad, N, K, Lc, O, lut, out_kind, y, sx, sw, bias, wbase=wbase,
-          x_upper=x_upper)
+          x_upper=x_upper, u8=u8)
     if return_operand:
         return y, wq, (xt, Rpad)
     return y, wq

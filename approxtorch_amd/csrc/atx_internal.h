@@ -40,10 +40,32 @@ int lut_gemm_f32_tiled(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        const float* sx, const float* sw, const float* bias, float* y,
                        hipStream_t stream);
 
+// The uint8 layer's zero-point correction and dequant as an epilogue
+// (atx_lut_gemm_narrow_uint8): for the sum v = (float) y[n,o,l],
+//   t = v - zw[o] * xs[n*L + l];  t = t - zx * ws[o];  t = t + (K * zx) * zw[o];
+//   out = bias ? bias[o] + t * (sx * sw[o]) : t * (sx * sw[o])
+// with each operation in fp32 in that order, the same roundings as
+// atx_uint8_dequant applied to the fp32 sums.
+constexpr int OUT_DEQUANT_U8 = 3;
+struct U8Terms {
+  const float* xs; const float* ws; const float* zx; const float* zw;
+  float K;
+};
+__device__ __forceinline__ float u8_dequant(float v, float x, float zo, float wo, float ko,
+                                            float so, const float* bias, float bo) {
+  float t = v - zo * x;
+  t = t - wo;
+  t = t + ko;
+  t = t * so;
+  return bias ? bo + t : t;
+}
+
 // Sum of S int32 partial slices of an [N][O][L] LUT GEMM output (ws[s *
-// numel + i], exact in int64) followed by the epilogue ep into y.
+// numel + i], exact in int64) followed by the epilogue ep into y
+// (ep.out_kind may be OUT_DEQUANT_U8, with its terms in u8).
 int launch_split_reduce(const int* ws, int S, long long numel, int O, int L,
-                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream);
+                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream,
+                        const U8Terms& u8 = U8Terms{});
 
 // Grid size for grid-stride elementwise kernels.
 inline int elem_grid(long long n, int threads, int cap = 8192) {

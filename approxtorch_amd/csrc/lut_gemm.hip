@@ -824,7 +824,7 @@ sk_finish_kernel(const GemmParams p) {
 __global__ void split_reduce1_kernel(const int* __restrict__ ws, int S,
                                      long long numel, int O, int L, int out_kind,
                                      void* __restrict__ y, const float* sx,
-                                     const float* sw, const float* bias) {
+                                     const float* sw, const float* bias, U8Terms u8) {
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < numel;
        i += (long long)gridDim.x * blockDim.x) {
     long long a = 0;
@@ -833,6 +833,13 @@ __global__ void split_reduce1_kernel(const int* __restrict__ ws, int S,
       ((int*)y)[i] = (int)a;
     } else if (out_kind == ATX_OUT_F32) {
       ((float*)y)[i] = (float)a;
+    } else if (out_kind == OUT_DEQUANT_U8) {
+      const long long nl = i / L;              // n * O + o
+      const int o = (int)(nl % O), l = (int)(i - nl * L);
+      const long long n = nl / O;
+      const float z = u8.zx[0], zo = u8.zw[o];
+      ((float*)y)[i] = u8_dequant((float)a, u8.xs[n * L + l], zo, z * u8.ws[o],
+                                  (u8.K * z) * zo, sx[0] * sw[o], bias, bias ? bias[o] : 0.f);
     } else {
       const int o = (int)((i / L) % O);
       const float sc = sx[0] * sw[o];
@@ -846,7 +853,7 @@ __global__ void split_reduce1_kernel(const int* __restrict__ ws, int S,
 __global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
                                     long long numel, int O, int L, int out_kind,
                                     void* __restrict__ y, const float* sx,
-                                    const float* sw, const float* bias) {
+                                    const float* sw, const float* bias, U8Terms u8) {
   for (long long q = blockIdx.x * (long long)blockDim.x + threadIdx.x; q < (numel >> 2);
        q += (long long)gridDim.x * blockDim.x) {
     const long long i = q << 2;
@@ -860,6 +867,20 @@ __global__ void split_reduce_kernel(const int* __restrict__ ws, int S,
     } else if (out_kind == ATX_OUT_F32) {
       *(float4*)((float*)y + i) =
           make_float4((float)a[0], (float)a[1], (float)a[2], (float)a[3]);
+    } else if (out_kind == OUT_DEQUANT_U8) {
+      long long nl = i / L;                    // n * O + o
+      int l = (int)(i - nl * L), o = (int)(nl % O);
+      long long n = nl / O;
+      const float z = u8.zx[0], kz = u8.K * z, s0 = sx[0];
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float zo = u8.zw[o];
+        f[e] = u8_dequant((float)a[e], u8.xs[n * L + l], zo, z * u8.ws[o], kz * zo,
+                          s0 * sw[o], bias, bias ? bias[o] : 0.f);
+        if (++l == L) { l = 0; if (++o == O) { o = 0; ++n; } }
+      }
+      *(float4*)((float*)y + i) = make_float4(f[0], f[1], f[2], f[3]);
     } else {
       long long nl = i / L;                    // n * O + o
       int l = (int)(i - nl * L), o = (int)(nl % O);
@@ -1287,15 +1308,16 @@ static int lut_gemm_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
 }
 
 int launch_split_reduce(const int* ws, int S, long long numel, int O, int L,
-                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream) {
+                        const atx_gemm_epilogue& ep, void* y, hipStream_t stream,
+                        const U8Terms& u8) {
   if (numel % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)ws & 15) == 0)
     hipLaunchKernelGGL(split_reduce_kernel, dim3(elem_grid(numel / 4, 256)), dim3(256), 0,
                        stream, ws, S, numel, O, L, ep.out_kind, y, ep.scale_x, ep.scale_w,
-                       ep.bias);
+                       ep.bias, u8);
   else
     hipLaunchKernelGGL(split_reduce1_kernel, dim3(elem_grid(numel, 256)), dim3(256), 0,
                        stream, ws, S, numel, O, L, ep.out_kind, y, ep.scale_x, ep.scale_w,
-                       ep.bias);
+                       ep.bias, u8);
   return check_launch("split_reduce_kernel");
 }
 

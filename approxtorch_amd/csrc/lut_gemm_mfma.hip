@@ -53,6 +53,7 @@ struct Params {
   int out_kind;                              // ATX_OUT_* (int32 partials when split)
   void* y;
   const float* sx; const float* sw; const float* bias;
+  U8Terms u8;                                // out_kind OUT_DEQUANT_U8
   long long split_stride;                    // elements per partial slice (splits > 1)
   int tiles_r, tiles_c, splits, kq;          // kq = tap quads per split
   int tiles;
@@ -204,15 +205,29 @@ __global__ void __launch_bounds__(NT, 1) onehot_gemm_kernel(const Params p) {
     const bool split = p.splits > 1;
     const int okind = split ? ATX_OUT_I32 : p.out_kind;
     const long long sbase = split ? (long long)sp * p.split_stride : 0;
-    const float sx = okind == ATX_OUT_DEQUANT ? p.sx[0] : 0.f;
+    const bool u8 = okind == OUT_DEQUANT_U8;
+    const float sx = okind == ATX_OUT_DEQUANT || u8 ? p.sx[0] : 0.f;
+    // uint8 correction: the rows' tap sums, read once for all channels
+    const float z = u8 ? p.u8.zx[0] : 0.f, kz = p.u8.K * z;
+    float xr[RB][4];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xr[b][e] = u8 ? p.u8.xs[std::min(r0 + 16 * b + 4 * g + e, p.R - 1)] : 0.f;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
       const int o = c0 + 16 * c + m;
       if (o >= p.O) continue;
-      float sc = 0.f, bo = 0.f;
-      if (okind == ATX_OUT_DEQUANT) {
+      float sc = 0.f, bo = 0.f, zo = 0.f, wo = 0.f, ko = 0.f;
+      if (okind == ATX_OUT_DEQUANT || u8) {
         sc = sx * p.sw[o];
         bo = p.bias ? p.bias[o] : 0.f;
+      }
+      if (u8) {
+        zo = p.u8.zw[o];
+        wo = z * p.u8.ws[o];
+        ko = kz * zo;
       }
 #pragma unroll
       for (int b = 0; b < RB; ++b) {
@@ -226,7 +241,9 @@ __global__ void __launch_bounds__(NT, 1) onehot_gemm_kernel(const Params p) {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (okind == ATX_OUT_DEQUANT) {
+          if (u8) {
+            f[e] = u8_dequant((float)v[e], xr[b][e], zo, wo, ko, sc, p.bias, bo);
+          } else if (okind == ATX_OUT_DEQUANT) {
             const float tv = (float)v[e] * sc;
             f[e] = p.bias ? bo + tv : tv;
           } else {
@@ -300,16 +317,46 @@ long long atx_lut_gemm_narrow_workspace_bytes(int N, int K, int L, int O) {
   return pl.splits > 1 ? (long long)pl.splits * N * O * L * 4 : 0;
 }
 
+static int narrow_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N, int K,
+                      int L, int O, const uint16_t* lut16t, int lut_class, int wbase,
+                      atx_gemm_epilogue ep, const U8Terms& u8, void* y, void* workspace,
+                      hipStream_t stream);
+
 int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N, int K,
                         int L, int O, const uint16_t* lut16t, int lut_class, int wbase,
                         atx_gemm_epilogue ep, void* y, void* workspace, hipStream_t stream) {
   ATX_REQUIRE_EPILOGUE(ep, "atx_lut_gemm_narrow");
+  ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,
+              "atx_lut_gemm_narrow: bad out_kind");
+  return narrow_run(xt, Rpad, wt, Opad, N, K, L, O, lut16t, lut_class, wbase, ep, U8Terms{}, y,
+                    workspace, stream);
+}
+
+int atx_lut_gemm_narrow_uint8(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N,
+                              int K, int L, int O, const uint16_t* lut16t, int lut_class,
+                              const float* scale_x, const float* scale_w, const float* bias,
+                              const float* xsum, const float* wsum, const float* zero_x,
+                              const float* zero_w, float* y, void* workspace,
+                              hipStream_t stream) {
+  ATX_REQUIRE(K > 0, "atx_lut_gemm_narrow_uint8: needs K > 0");
+  ATX_REQUIRE((long long)N * L * O == 0 ||
+                  (scale_x && scale_w && xsum && wsum && zero_x && zero_w),
+              "atx_lut_gemm_narrow_uint8: null pointer");
+  const atx_gemm_epilogue ep =
+      atx_gemm_epilogue_make(OUT_DEQUANT_U8, scale_x, scale_w, bias, nullptr);
+  const U8Terms u8{xsum, wsum, zero_x, zero_w, (float)K};
+  return narrow_run(xt, Rpad, wt, Opad, N, K, L, O, lut16t, lut_class, 0, ep, u8, y, workspace,
+                    stream);
+}
+
+static int narrow_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad, int N, int K,
+                      int L, int O, const uint16_t* lut16t, int lut_class, int wbase,
+                      atx_gemm_epilogue ep, const U8Terms& u8, void* y, void* workspace,
+                      hipStream_t stream) {
   ATX_REQUIRE(N >= 0 && K >= 0 && L >= 0 && O >= 0, "atx_lut_gemm_narrow: negative size");
   ATX_REQUIRE(lut_class == ATX_LUT_I16 || lut_class == ATX_LUT_U16,
               "atx_lut_gemm_narrow: needs an integer LUT class (int16 or uint16)");
   ATX_REQUIRE(wbase >= 0 && wbase <= 240, "atx_lut_gemm_narrow: wbase must be in [0, 240]");
-  ATX_REQUIRE(ep.out_kind >= ATX_OUT_F32 && ep.out_kind <= ATX_OUT_DEQUANT,
-              "atx_lut_gemm_narrow: bad out_kind");
   ATX_REQUIRE(ep.out_kind != ATX_OUT_DEQUANT || (ep.scale_x && ep.scale_w),
               "atx_lut_gemm_narrow: dequant epilogue needs scale_x and scale_w");
   const long long R = (long long)N * L;
@@ -329,7 +376,7 @@ int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
   p.K = K; p.R = (int)R; p.L = L; p.O = O; p.wbase = wbase;
   p.is_signed = lut_class == ATX_LUT_I16;
   p.out_kind = ep.out_kind; p.y = y;
-  p.sx = ep.scale_x; p.sw = ep.scale_w; p.bias = ep.bias;
+  p.sx = ep.scale_x; p.sw = ep.scale_w; p.bias = ep.bias; p.u8 = u8;
   p.tiles_r = pl.tiles_r; p.tiles_c = pl.tiles_c; p.splits = pl.splits; p.kq = pl.kq;
   const long long tiles = (long long)pl.tiles_r * pl.tiles_c * pl.splits;
   ATX_REQUIRE(tiles < 0x7fffffffLL, "atx_lut_gemm_narrow: grid too large");
@@ -353,7 +400,7 @@ int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
   rc = check_launch("onehot_gemm_kernel");
   if (rc == ATX_OK) rc = timing_mark(true, stream);
   if (rc != ATX_OK || pl.splits == 1) return rc;
-  return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream);
+  return launch_split_reduce((const int*)workspace, pl.splits, numel, O, L, ep, y, stream, u8);
 }
 
 }  // extern "C"

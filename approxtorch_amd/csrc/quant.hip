@@ -558,13 +558,7 @@ __global__ void uint8_dequant_kernel(float* __restrict__ y, long long rows, int 
       v[0] = yp[0]; x[0] = xp[0];
     }
 #pragma unroll
-    for (int e = 0; e < W; ++e) {
-      float t = v[e] - zo * x[e];
-      t = t - wo;
-      t = t + ko;
-      t = t * so;
-      v[e] = bias ? b + t : t;
-    }
+    for (int e = 0; e < W; ++e) v[e] = u8_dequant(v[e], x[e], zo, wo, ko, so, bias, b);
     if constexpr (VEC) *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
     else yp[0] = v[0];
   }

@@ -257,14 +257,15 @@ class _conv2d_uint8_fused(Function):
                                                             want_wt=True, want_q=False)
         # at most 16 weight indices (weight_bits <= 4): matrix-core LUT GEMM and grad_x
         wbase = 0 if qmax_w <= 15 else None
-        y, _, (xt, Rpad) = ops.conv_forward(q8, wq, lut, g, 0, 0, pad_dev=zero_x,
-                                            packed_w=(wq, wt, Opad), return_operand=True,
-                                            wbase=wbase)
         xsum = ops.tap_sum(q8, g, pad_dev=zero_x)
         wsum = wq.sum(dim=1, dtype=torch.float32)
         b = None if bias is None else bias.detach().contiguous()
-        ops.uint8_dequant(y, xsum, wsum, zero_x.contiguous(), zero_w.contiguous(),
-                          scale_x.contiguous(), scale_w.contiguous(), b, K)
+        # correction and dequant in the GEMM's epilogue (matrix-core path) or
+        # as one in-place pass after it
+        y, _, (xt, Rpad) = ops.conv_forward(
+            q8, wq, lut, g, 0, 0, sx=scale_x.contiguous(), sw=scale_w.contiguous(), bias=b,
+            pad_dev=zero_x, packed_w=(wq, wt, Opad), return_operand=True, wbase=wbase,
+            u8=(xsum, wsum, zero_x.contiguous(), zero_w.contiguous()))
         ctx.save_for_backward(xt, mask_x, wq, mask_w.view(O, K), scale_x, zero_x, scale_w,
                               zero_w, tx, tw)
         ctx.g, ctx.rpad, ctx.kind = g, Rpad, kind

@@ -238,6 +238,23 @@ int atx_lut_gemm_narrow(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opa
                         int wbase, atx_gemm_epilogue ep, void* y, void* workspace,
                         hipStream_t stream);
 
+/* atx_lut_gemm_narrow (wbase 0: uint8 weight indices in [0, 16)) with the
+ * uint8 layer's zero-point correction and dequant as its epilogue, the
+ * in-place pass of atx_uint8_dequant folded into the GEMM's stores:
+ *   y[n,o,l] = ((S - zero_w[o]*xsum[n,l] - zero_x*wsum[o] + K*zero_x*zero_w[o])
+ *               * (scale_x * scale_w[o])) (+ bias[o], nullable)
+ * for the exact sum S, each fp32 operation in atx_uint8_dequant's order, so
+ * y is bit for bit the F32 GEMM followed by atx_uint8_dequant.  xsum
+ * [N*L] = atx_tap_sum of the uint8 image, wsum[o] = sum_k q_w[o,k].  K > 0;
+ * same workspace as atx_lut_gemm_narrow.  Replaces the LUT conv and the
+ * correction / dequant tail of nn/Conv2d_uint8.py:257-325. */
+int atx_lut_gemm_narrow_uint8(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                              int N, int K, int L, int O, const uint16_t* lut16t,
+                              int lut_class, const float* scale_x, const float* scale_w,
+                              const float* bias, const float* xsum, const float* wsum,
+                              const float* zero_x, const float* zero_w, float* y,
+                              void* workspace, hipStream_t stream);
+
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory -- code under HIP graph capture, serving loops, harnesses that
  * forbid hipMalloc.  atx_lut_gemm with the same arguments and results, minus

@@ -118,6 +118,53 @@ def test_lut_gemm_narrow_beyond_int32_pass():
     assert np.array_equal(y.cpu().numpy(), want.astype(np.float32))
 
 
+@pytest.mark.parametrize("shape", NARROW_GEMM_SHAPES + [(2, 40000, 8, 20)])
+@pytest.mark.parametrize("lut_name", ["u16_c5", "perturbed"])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_lut_gemm_narrow_uint8_epilogue(shape, lut_name, with_bias):
+    """atx_lut_gemm_narrow_uint8: the uint8 layer's zero-point correction and
+    dequant in the matrix-core GEMM's epilogue (and in the split-K reduce:
+    the (1, 2304, 196, 256) and K > 32768 shapes split) equal the fp32 GEMM
+    followed by atx_uint8_dequant bit for bit, and the oracle's int64 sums
+    corrected in fp64 within 1e-6 of the terms' magnitude (five fp32
+    roundings)."""
+    N, K, L, Oc = shape
+    r = gen(zlib.crc32(repr(("narrow_u8", shape, lut_name, with_bias)).encode()))
+    xi = r.integers(0, 256, (N, K, L), dtype=np.uint8)
+    wi = r.integers(0, 16, (Oc, K), dtype=np.uint8)
+    lut_np = luts(9)[lut_name]
+    lut = t(lut_np, torch.float32)
+    xt, Rpad = ops.pack_rows_u8(t(xi))
+    _, wt, Opad = ops._pack_w(t(wi), 0)
+    xsum = xi.astype(np.float64).sum(axis=1).astype(np.float32)          # [N, L], exact
+    wsum = wi.astype(np.float64).sum(axis=1).astype(np.float32)          # [O], exact
+    zx = np.array([r.integers(0, 256)], np.float32)
+    zw = r.integers(0, 16, Oc).astype(np.float32)
+    sx = np.array([0.0371], np.float32)
+    sw = (r.random(Oc) * 0.02 + 0.001).astype(np.float32)
+    bias = r.standard_normal(Oc).astype(np.float32) if with_bias else None
+    dev = [t(a) for a in (xsum, wsum, zx, zw, sx, sw)]
+    tb = None if bias is None else t(bias)
+    a = torch.empty((N, Oc, L), dtype=torch.float32, device=DEV)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, lut, ops.L.ATX_OUT_F32, a, dev[4], dev[5], tb,
+              wbase=0, u8=tuple(dev[:4]))
+    b = torch.empty_like(a)
+    ops._gemm(xt, Rpad, wt, Opad, N, K, L, Oc, lut, ops.L.ATX_OUT_F32, b, wbase=0)
+    ops.uint8_dequant(b, *dev[:4], dev[4], dev[5], tb, K)
+    assert torch.equal(a, b)
+    S = O.lut_gemm_i64(xi, wi, lut_np).astype(np.float64)
+    zo, so = zw.astype(np.float64)[None, :, None], (sx.astype(np.float64) * sw)[None, :, None]
+    xs, z = xsum.astype(np.float64)[:, None, :], float(zx[0])
+    ws = wsum.astype(np.float64)[None, :, None]
+    want = (S - zo * xs - z * ws + K * z * zo) * so
+    mag = (np.abs(S) + zo * xs + z * ws + K * z * zo) * so
+    if bias is not None:
+        want = want + bias.astype(np.float64)[None, :, None]
+        mag = mag + np.abs(bias.astype(np.float64))[None, :, None]
+    err = np.abs(a.cpu().numpy().astype(np.float64) - want)
+    assert (err <= 1e-6 * mag + 1e-30).all(), err.max()
+
+
 # Stream-K schedule of the LUT GEMM: full rounds of whole tiles, then the
 # (tile, 4-table quad) iterations of the remaining tiles dealt out evenly over
 # 256 workgroups; a tile cut by a workgroup boundary sums its int32 parts
