@@ -974,7 +974,7 @@ int atx_col2im_pos(const float* col, atx_conv_geom g, const float* pos, const ui
   hipLaunchKernelGGL((col2im_kernel<I, S, C>), grid, dim3(TB), 0, stream, col, g, pos,    \
                      mask, scale, img)
   if (!small) ATX_COL2IM(long long, 0, 9);
-  else if (st == 1 && !one && g.KH * g.KW <= 9 && pos) {
+  else if (st == 1 && !one && g.KH * g.KW <= 9 && pos && cdiv(g.C, C2_CC) <= 65535) {
     const dim3 grid_cc(elem_grid((long long)g.N * g.H * g.W, TB), (unsigned)cdiv(g.C, C2_CC));
     hipLaunchKernelGGL(col2im_cc_kernel<int>, grid_cc, dim3(TB), 0, stream, col, g, pos, mask,
                        scale, img);
