@@ -548,6 +548,29 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def graph_replay_time(torch, args, step):
+    """Wall time of args.steps replays of `step` captured once in a HIP graph
+    (torch.cuda.CUDAGraph; warmed up on a side stream first, as capture
+    requires), after args.warmup untimed replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(max(args.warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
 def timed_gemm_pass(torch, timer, steps, step):
     """The timed steps again with the GemmTimer's per-call HIP events (the
     roofline's kernel durations), after the timed region that gives `value`:
@@ -689,6 +712,7 @@ def main_c1(torch, args):
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         dt_kern = timed_gemm_pass(torch, timer, args.steps, lambda: layer(xg))
+        dt_graph = graph_replay_time(torch, args, lambda: layer(xg))
     macs = 8 * 32 * 32 * 64 * 576
     result = {
         "metric": "LUT-MAC/s (G), config 1 (one approximate 3x3 conv 64->64 forward, [8,64,32,32])",
@@ -707,6 +731,11 @@ def main_c1(torch, args):
                                "M=8192 N=64 K=576 + dequant", "lut_macs_per_step": macs,
                    "parallelism": "single GPU"},
         "roofline": roofline(timer, dt_kern, "c1"),
+        # the same forward captured once in a HIP graph and replayed: the
+        # launch-bound forward without its host issue (a serving loop's form)
+        "graph_replay": {"value": round(macs * args.steps / dt_graph / 1e9, 1),
+                         "unit": "GLUT-MAC/s",
+                         "ms_per_step": round(dt_graph * 1e3 / args.steps, 4)},
     }
     if not args.no_cpu_baseline:
         from oracle import torch_cpu

@@ -1,0 +1,81 @@
+"""HIP graph capture of the layers' eval-mode forward (torch.cuda.CUDAGraph).
+
+The library launches on the capturing stream, takes its temporaries from
+torch's allocator and issues no memset, copy or synchronisation of its own,
+so a serving loop can capture a forward once and replay it.  Each case
+replays the graph several times with the program's own eager work and
+synchronisations in between (new input copied into the static input, an
+eager forward of another input), and every replay equals the eager forward
+of the same input bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import approxtorch_amd as at
+from approxtorch_amd import workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _int8_layer(k, s, p, O, wbits, grad):
+    lut = torch.from_numpy(workloads.lut_perturbed(0)).to(DEV)
+    kw = {}
+    if grad == "lre":
+        ga, gb = workloads.lre_tables(lut.cpu().numpy())
+        kw = dict(dx=torch.as_tensor(ga).to(DEV), dw=torch.as_tensor(gb).to(DEV))
+    return at.nn.Conv2d_int8(16, O, k, lut, grad=grad, bias=True, stride=s, padding=p,
+                             weight_bits=wbits, **kw)
+
+
+def _uint8_layer(k, s, p, O, wbits, grad):
+    v = np.arange(256)
+    lut = torch.from_numpy(((v[:, None] * v[None, :]) & ~63).astype(np.float32).reshape(-1))
+    return at.nn.Conv2d_uint8(16, O, k, lut.to(DEV), grad=grad, bias=True, stride=s, padding=p,
+                              weight_bits=wbits)
+
+
+CASES = [
+    ("int8 3x3 gather", _int8_layer, 3, 1, 1, 40, 8, "ste"),
+    ("int8 1x1 rows", _int8_layer, 1, 1, 0, 72, 8, "ste"),
+    ("int8 3x3 s2 lre", _int8_layer, 3, 2, 1, 24, 8, "lre"),
+    ("int8 3x3 w4 matrix cores", _int8_layer, 3, 1, 1, 40, 4, "ste"),
+    ("uint8 3x3 w4 matrix cores", _uint8_layer, 3, 1, 1, 40, 4, "ste"),
+    ("uint8 3x3 w8", _uint8_layer, 3, 1, 1, 40, 8, "ste"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_eval_forward_graph_replays(case):
+    _, make, k, s, p, O, wbits, grad = case
+    torch.manual_seed(3)
+    layer = make(k, s, p, O, wbits, grad).to(DEV)
+    x0 = torch.randn(4, 16, 20, 20, device=DEV) + 0.3
+    layer.train()
+    with torch.no_grad():
+        layer(x0)                                  # one EMA step sets the scales
+    layer.eval()
+    inputs = [torch.randn(4, 16, 20, 20, device=DEV) * (1 + i) + 0.2 * i for i in range(3)]
+    with torch.no_grad():
+        want = [layer(x).clone() for x in inputs]
+        static_x = inputs[0].clone()
+        layer(static_x)                            # warm-up on the capture's input
+        torch.cuda.synchronize()
+        s_cap = torch.cuda.Stream()
+        s_cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s_cap):
+            layer(static_x)                        # warm-up on the side stream as well
+        torch.cuda.current_stream().wait_stream(s_cap)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_y = layer(static_x)
+        for rep in range(2):
+            for i, x in enumerate(inputs):
+                static_x.copy_(x)
+                graph.replay()
+                got = static_y.clone()
+                other = layer(inputs[(i + 1) % len(inputs)])     # eager work in between
+                torch.cuda.synchronize()
+                assert torch.equal(got, want[i]), (rep, i)
+                assert torch.equal(other, want[(i + 1) % len(inputs)])
