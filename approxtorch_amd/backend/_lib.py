@@ -143,6 +143,9 @@ _SIGS = {
     "atx_custom_grad_dw_workspace_bytes": (c_ll, [c_int, c_int, c_int, c_int]),
     "atx_custom_grad_dw": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int,
                                    c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "atx_custom_grad_dw_uint8": (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
+                                         c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                         c_vp, c_vp, c_vp]),
 }
 
 _lib = None

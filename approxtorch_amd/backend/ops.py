@@ -813,7 +813,8 @@ def bgemm_lre_backward_claude_im2col(grad_output: Tensor, x: Tensor, w: Tensor, 
 
 # --------------------------------------------------------- custom backward
 def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int, Lc: int,
-                 mask_w=None, scale_w=None, wbase=None, dy_scale=None, img_ste=None):
+                 mask_w=None, scale_w=None, wbase=None, dy_scale=None, img_ste=None,
+                 w_zero_point=None):
     """(grad_x [N,K,L] or None, grad_w [O,K] or None) of the pair-table
     estimator from the LUT GEMM's row-offset operand (xt, Rpad) and the uint8
     weight index image wq [O,K]; dx_lut / dw_lut are fp32 [65536] tables
@@ -826,7 +827,10 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
     img_ste (with wbase; a 1x1 stride-1 unpadded conv, whose column gradient
     is the image gradient): (pos [N, L] or None, mask [N, K, L] or None,
     scale [1]) -- grad_x comes back as col2im(grad_x, pos, mask, scale) of
-    that geometry, computed in the grad_x kernel's epilogue."""
+    that geometry, computed in the grad_x kernel's epilogue.
+    w_zero_point = (go_sum [O], scale_x [1], zero_x [1]), with scale_w: the
+    uint8 layer's weight zero-point term, grad_w -= (go_sum * (scale_x *
+    scale_w)) * zero_x before the STE (atx_custom_grad_dw_uint8)."""
     xt, Rpad = operand
     O = wq.size(0)
     dyc = dy.contiguous()
@@ -871,9 +875,20 @@ def custom_grads(operand, wq: Tensor, dy: Tensor, dx_lut, dw_lut, N: int, K: int
         gw = torch.empty((O, K), dtype=torch.float32, device=dev)
         wsb = L.query("atx_custom_grad_dw_workspace_bytes", N, K, Lc, O)
         ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
-        L.call("atx_custom_grad_dw", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
-               L.ptr(dy_scale), L.ptr(tab), N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w),
-               L.ptr(gw), L.ptr(ws), s)
+        if w_zero_point is None:
+            L.call("atx_custom_grad_dw", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+                   L.ptr(dy_scale), L.ptr(tab), N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w),
+                   L.ptr(gw), L.ptr(ws), s)
+        else:
+            zsum, zsx, zzx = (t.contiguous() for t in w_zero_point)
+            for name, t, n in (("go_sum", zsum, O), ("scale_x", zsx, 1), ("zero_x", zzx, 1)):
+                if t.dtype != torch.float32 or t.numel() != n or t.device != dev:
+                    raise RuntimeError(f"{name} must be float32 [{n}] on {dev}")
+            if scale_w is None:
+                raise RuntimeError("w_zero_point needs scale_w")
+            L.call("atx_custom_grad_dw_uint8", L.ptr(xt), Rpad, L.ptr(wt), Opad, L.ptr(dyc),
+                   L.ptr(dy_scale), L.ptr(tab), N, K, Lc, O, L.ptr(mask_w), L.ptr(scale_w),
+                   L.ptr(zsum), L.ptr(zsx), L.ptr(zzx), L.ptr(gw), L.ptr(ws), s)
     return gx, gw
 
 

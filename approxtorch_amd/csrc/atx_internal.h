@@ -28,9 +28,13 @@ int check_geom(const atx_conv_geom& g);
 
 // out[i] = sum_s ws[s*numel + i] in a fixed order (deterministic), with the
 // optional per-channel fake-quant STE out = (mask ? sum : 0) / max(scale[i/K],
-// 1e-12); S = 0 writes zeros.
+// 1e-12); S = 0 writes zeros.  zsum (nullable, with zsx, zzx and scale):
+// before the STE, out -= (zsum[o] * (zsx[0] * scale[o])) * zzx[0], each
+// operation rounded on its own (the uint8 layer's weight zero-point term).
 int launch_split_sum(const float* ws, int S, long long numel, int K, const uint8_t* mask,
-                     const float* scale, float* out, hipStream_t stream);
+                     const float* scale, float* out, hipStream_t stream,
+                     const float* zsum = nullptr, const float* zsx = nullptr,
+                     const float* zzx = nullptr);
 
 // fp32-class LUT GEMM (ascending-k fp32 sums, tiled over LDS tables built
 // from the transposed fp32 LUT image); out_kind ATX_OUT_F32 or

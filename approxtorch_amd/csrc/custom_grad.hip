@@ -1050,10 +1050,36 @@ long long atx_custom_grad_dw_workspace_bytes(int N, int K, int L, int O) {
   return cdiv((long long)N * L, cg::RT) * O * K * 4;
 }
 
+static int custom_dw_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                         const float* dy, const float* dy_scale, const float* tabT, int N,
+                         int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
+                         const float* zsum, const float* zsx, const float* zzx, float* grad_w,
+                         float* workspace, hipStream_t stream);
+
 int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
                        const float* dy, const float* dy_scale, const float* tabT, int N, int K,
                        int L, int O, const uint8_t* mask_w, const float* scale_w,
                        float* grad_w, float* workspace, hipStream_t stream) {
+  return custom_dw_run(xt, Rpad, wt, Opad, dy, dy_scale, tabT, N, K, L, O, mask_w, scale_w,
+                       nullptr, nullptr, nullptr, grad_w, workspace, stream);
+}
+
+int atx_custom_grad_dw_uint8(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                             const float* dy, const float* dy_scale, const float* tabT, int N,
+                             int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
+                             const float* go_sum, const float* scale_x, const float* zero_x,
+                             float* grad_w, float* workspace, hipStream_t stream) {
+  ATX_REQUIRE((long long)O * K == 0 || (go_sum && scale_x && zero_x && scale_w),
+              "atx_custom_grad_dw_uint8: null zero-point operand");
+  return custom_dw_run(xt, Rpad, wt, Opad, dy, dy_scale, tabT, N, K, L, O, mask_w, scale_w,
+                       go_sum, scale_x, zero_x, grad_w, workspace, stream);
+}
+
+static int custom_dw_run(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                         const float* dy, const float* dy_scale, const float* tabT, int N,
+                         int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
+                         const float* zsum, const float* zsx, const float* zzx, float* grad_w,
+                         float* workspace, hipStream_t stream) {
   cg::Params p;
   int rc = custom_params(p, xt, Rpad, wt, Opad, dy, tabT, N, K, L, O, workspace,
                          "atx_custom_grad_dw");
@@ -1063,7 +1089,8 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
   if (numel == 0) return ATX_OK;
   ATX_REQUIRE(grad_w && !(mask_w && !scale_w), "atx_custom_grad_dw: null output / scale");
   if (p.R == 0)
-    return launch_split_sum(nullptr, 0, numel, K, mask_w, scale_w, grad_w, stream);
+    return launch_split_sum(nullptr, 0, numel, K, mask_w, scale_w, grad_w, stream, zsum, zsx,
+                            zzx);
   ATX_REQUIRE(xt && wt && dy && tabT && workspace, "atx_custom_grad_dw: null operand");
   if (L % 4 != 0 || (long long)Rpad * 16 > 0x7fffffffLL) {
     // Fewer (row, channel) tiles than CUs: split the tap quads over enough
@@ -1081,7 +1108,8 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        0, stream, p);
     rc = check_launch("custom_dw_tile_kernel");
     if (rc != ATX_OK) return rc;
-    return launch_split_sum(workspace, p.tiles_r, numel, K, mask_w, scale_w, grad_w, stream);
+    return launch_split_sum(workspace, p.tiles_r, numel, K, mask_w, scale_w, grad_w, stream,
+                            zsum, zsx, zzx);
   }
   // Workgroups of (channel tile, chunk of NB tap quads, chunk of row steps),
   // one per CU (128 KiB of tables), NW waves of 256 rows each.  Row chunks:
@@ -1122,7 +1150,8 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        stream, p);
   rc = check_launch("custom_dw_kernel");
   if (rc != ATX_OK) return rc;
-  return launch_split_sum(workspace, slices, numel, K, mask_w, scale_w, grad_w, stream);
+  return launch_split_sum(workspace, slices, numel, K, mask_w, scale_w, grad_w, stream, zsum,
+                          zsx, zzx);
 }
 
 }  // extern "C"

@@ -1217,15 +1217,19 @@ weight_gemm_kernel(WeightA<BM, VA> la, LB lb, WeightOut ep, const float* __restr
                  n0 + wn * (BN / 2) + j * 16 + (lane & 15), acc[i][j][r], s);
 }
 
-// gw[i] = sum_s ws[s][i]; optional fused per-channel fake-quant backward:
-// gw = mask ? sum / max(scale[o], 1e-12) : 0 with o = i / K.  A block sums
-// 256 / G consecutive elements over G groups of slices (group g takes slices
-// g, g + G, ...), then adds the G partials in group order: deterministic.
+// gw[i] = sum_s ws[s][i]; optional per-channel term (the uint8 layer's weight
+// zero point): gw -= (zsum[o] * (zsx * scale[o])) * zzx, each product and the
+// difference rounded on its own; optional fused per-channel fake-quant
+// backward: gw = mask ? gw / max(scale[o], 1e-12) : 0 with o = i / K.  A block
+// sums 256 / G consecutive elements over G groups of slices (group g takes
+// slices g, g + G, ...), then adds the G partials in group order:
+// deterministic.
 template <bool VEC>
 __global__ void __launch_bounds__(256)
 split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, int G,
                  const uint8_t* __restrict__ mask, const float* __restrict__ scale,
-                 float* __restrict__ out) {
+                 float* __restrict__ out, const float* __restrict__ zsum,
+                 const float* __restrict__ zsx, const float* __restrict__ zzx) {
   // VEC: each item is four consecutive elements (16-byte loads and stores;
   // numel % 4 == 0); every element keeps the same summation order.
   constexpr int W = VEC ? 4 : 1;
@@ -1242,11 +1246,17 @@ split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, in
   __syncthreads();
   if (grp == 0 && i < numel) {
     for (int g = 1; g < G; ++g) a += part[g * epb + e];
-    if (mask) {
+    if (mask || zsum) {
       long long o = i / K, r = i - o * K;
 #pragma unroll
       for (int j = 0; j < W; ++j) {
-        a[j] = (mask[i + j] ? a[j] : 0.0f) / fmaxf(scale[o], 1e-12f);
+        float v = a[j];
+        if (zsum) {
+#pragma clang fp contract(off)
+          v = v - (zsum[o] * (zsx[0] * scale[o])) * zzx[0];
+        }
+        if (mask) v = (mask[i + j] ? v : 0.0f) / fmaxf(scale[o], 1e-12f);
+        a[j] = v;
         if (++r == K) { r = 0; ++o; }
       }
     }
@@ -1257,7 +1267,8 @@ split_sum_kernel(const float* __restrict__ ws, int S, long long numel, int K, in
 // Launch of split_sum_kernel: enough groups that the grid has >= 1024 blocks.
 int launch_split_sum(const float* ws, int S, long long numel, int K,
                             const uint8_t* mask, const float* scale, float* out,
-                            hipStream_t stream) {
+                            hipStream_t stream, const float* zsum, const float* zsx,
+                            const float* zzx) {
   const bool vec = numel % 4 == 0 && ((uintptr_t)ws & 15) == 0 && ((uintptr_t)out & 15) == 0;
   const long long items = vec ? numel / 4 : numel;
   int G = 1;
@@ -1266,10 +1277,10 @@ int launch_split_sum(const float* ws, int S, long long numel, int K,
   ATX_REQUIRE(blocks <= 0x7fffffffLL, "split_sum: too many elements");
   if (vec)
     hipLaunchKernelGGL(split_sum_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       ws, S, numel, K, G, mask, scale, out);
+                       ws, S, numel, K, G, mask, scale, out, zsum, zsx, zzx);
   else
     hipLaunchKernelGGL(split_sum_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       ws, S, numel, K, G, mask, scale, out);
+                       ws, S, numel, K, G, mask, scale, out, zsum, zsx, zzx);
   return check_launch("split_sum_kernel");
 }
 

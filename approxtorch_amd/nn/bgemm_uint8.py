@@ -298,10 +298,17 @@ class _conv2d_uint8_fused(Function):
             # the STE in its epilogue (the fold's operations for that geometry)
             pointwise = (ctx.wbase is not None and need_x and g.KH == 1 and g.KW == 1 and
                          g.SH == 1 and g.SW == 1 and g.PH == 0 and g.PW == 0)
+            # the weight zero-point term and the weight STE in grad_w's slice sum
+            fuse_w = need_w and gsum is not None
             grad_col, gw_q = ops.custom_grads(
                 (xt, ctx.rpad), wq, go, tx if need_x else None, tw if need_w else None, g.N,
                 K, Lc, wbase=ctx.wbase, dy_scale=c,
-                img_ste=(gxs, mask_x, sx) if pointwise else None)
+                img_ste=(gxs, mask_x, sx) if pointwise else None,
+                mask_w=mask_w if fuse_w else None, scale_w=sw if fuse_w else None,
+                w_zero_point=(gsum, sx, zx) if fuse_w else None)
+            if fuse_w:
+                gw = gw_q.view(ctx.wshape)
+                need_w = False
             if pointwise:
                 gx = grad_col.view(mask_x.shape)
             elif need_x:   # fold, zero-point term and the STE in one pass

@@ -611,6 +611,17 @@ int atx_custom_grad_dw(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad
                        const float* dy, const float* dy_scale, const float* tabT, int N,
                        int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
                        float* grad_w, float* workspace, hipStream_t stream);
+/* atx_custom_grad_dw with the uint8 layer's weight zero-point term applied
+ * before the STE: grad_w[o,k] = sum - (go_sum[o] * (scale_x * scale_w[o])) *
+ * zero_x, each operation rounded on its own as the reference's elementwise
+ * tensor ops round it, then the STE of mask_w / scale_w when mask_w is given.
+ * go_sum[o] = sum_{n,l} go[n,o,l] (atx_zero_point_terms).  Replaces the
+ * weight side of nn/Conv2d_uint8.py:308-325 after the custom gradient. */
+int atx_custom_grad_dw_uint8(const uint16_t* xt, int Rpad, const uint8_t* wt, int Opad,
+                             const float* dy, const float* dy_scale, const float* tabT, int N,
+                             int K, int L, int O, const uint8_t* mask_w, const float* scale_w,
+                             const float* go_sum, const float* scale_x, const float* zero_x,
+                             float* grad_w, float* workspace, hipStream_t stream);
 
 /* atx_custom_grad_dx for weights with at most 16 distinct indices: every
  * wt entry of the O channels lies in [wbase, wbase + 16) (weight_bits <= 4:

@@ -932,6 +932,35 @@ def test_col2im_pos_ste(case):
     assert np.array_equal(plain.cpu().numpy(), f32col)
 
 
+@pytest.mark.parametrize("shape", CUSTOM_SHAPES[:4] + [(2, 72, 3136, 64), (3, 40, 49, 70)])
+def test_custom_grad_dw_uint8_zero_point(shape):
+    """atx_custom_grad_dw_uint8: the uint8 layer's weight zero-point term
+    (go_sum[o] * (scale_x * scale_w[o])) * zero_x subtracted in grad_w's slice
+    sum, then the weight STE, equals the custom grad_w followed by the same
+    torch expressions the layer used before (gw -= (gsum * (sx * sw)) * zx;
+    (mask ? gw : 0) / max(sw, 1e-12)) bit for bit (resident-table and
+    per-row-tile forms)."""
+    N, K, Lc, Oc = shape
+    r = gen(zlib.crc32(repr(("custom_u8zp", shape)).encode()))
+    xi = r.integers(0, 256, (N, K, Lc), dtype=np.uint8)
+    wi = r.integers(0, 256, (Oc, K), dtype=np.uint8)
+    dwl = r.standard_normal(65536).astype(np.float32)
+    go = t(r.standard_normal((N, Oc, Lc)).astype(np.float32))
+    mask = t(r.random((Oc, K)) < 0.8)
+    sw = t((r.random(Oc) * 0.05 + 0.01).astype(np.float32))
+    sx = t(np.array([0.043], np.float32))
+    zx = t(np.array([37.0], np.float32))
+    gsum = go.sum(dim=(0, 2))
+    c = (sx * sw).contiguous()
+    op = ops.pack_rows_u8(t(xi))
+    _, a = ops.custom_grads(op, t(wi), go, None, t(dwl), N, K, Lc, dy_scale=c, mask_w=mask,
+                            scale_w=sw, w_zero_point=(gsum, sx, zx))
+    _, b = ops.custom_grads(op, t(wi), go, None, t(dwl), N, K, Lc, dy_scale=c)
+    b -= (gsum * c).mul_(zx).view(-1, 1)
+    b = ops.fakequant_per_tensor_backward(b, mask, sw, channels=Oc, inner=K)
+    assert torch.equal(a, b)
+
+
 NARROW_SHAPES = CUSTOM_SHAPES +[(2, 64, 3136, 256), (3, 4608, 49, 40), (2, 20, 196, 2048)]
 
 
