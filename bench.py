@@ -93,6 +93,8 @@ def parse():
     ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c4", "c5", "c3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the step captured once in a HIP graph and replayed")
     ap.add_argument("--cpu-sample-batch", type=int, default=None,
                     help="batch of the CPU baseline's training steps (default: c2 4, c4 2, c5 1)")
     ap.add_argument("--probe-lds", action="store_true",
@@ -542,22 +544,43 @@ def main():
         result["layer_memory_MB"] = layer_memory(torch)
     if args.probe_lds:
         result["lds_probe_GBs"] = lds_probe(torch)
+    if args.graph:
+        # the same training step captured once in a HIP graph and replayed
+        dt_graph = graph_replay_time(torch, args, lambda: graph_step(model, opt, x, y),
+                                     lambda: opt.zero_grad(set_to_none=True))
+        result["graph_replay"] = {"value": round(cfg["batch"] * args.steps / dt_graph, 2),
+                                  "unit": "img/s",
+                                  "ms_per_step": round(dt_graph * 1e3 / args.steps, 3)}
     if not args.no_cpu_baseline:
         batch = args.cpu_sample_batch or {"c2": 4, "c4": 2, "c5": 1}[name]
         result["cpu_baseline"] = cpu_baseline(model, cfg, batch)
     print(json.dumps(result), flush=True)
 
 
-def graph_replay_time(torch, args, step):
+def graph_step(model, opt, x, y):
+    """The training step in the form a HIP graph captures: the gradients
+    are released before the capture, so the captured backward writes them
+    into the graph's own memory on every replay instead of accumulating."""
+    import torch.nn.functional as F
+    loss = F.cross_entropy(model(x), y)
+    loss.backward()
+    opt.step()
+    return loss
+
+
+def graph_replay_time(torch, args, step, before_capture=None):
     """Wall time of args.steps replays of `step` captured once in a HIP graph
     (torch.cuda.CUDAGraph; warmed up on a side stream first, as capture
-    requires), after args.warmup untimed replays."""
+    requires; before_capture() runs right before the capture), after
+    args.warmup untimed replays."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         step()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
+    if before_capture is not None:
+        before_capture()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()

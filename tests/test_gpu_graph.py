@@ -79,3 +79,54 @@ def test_eval_forward_graph_replays(case):
                 torch.cuda.synchronize()
                 assert torch.equal(got, want[i]), (rep, i)
                 assert torch.equal(other, want[(i + 1) % len(inputs)])
+
+
+TRAIN_CASES = [
+    ("int8 3x3 lre", _int8_layer, 3, 1, 1, 40, 8, "lre"),
+    ("int8 1x1 ste", _int8_layer, 1, 1, 0, 72, 8, "ste"),
+    ("uint8 3x3 w8 ste", _uint8_layer, 3, 1, 1, 40, 8, "ste"),
+]
+
+
+@pytest.mark.parametrize("case", TRAIN_CASES, ids=[c[0] for c in TRAIN_CASES])
+def test_train_step_graphed(case):
+    """A training-mode layer under torch.cuda.make_graphed_callables (forward
+    and backward each captured once, the EMA statistics included): over three
+    steps with an SGD update of the weights in between, the outputs, the
+    input, weight and bias gradients and the scale buffers equal an eager
+    copy's bit for bit."""
+    import copy
+    _, make, k, s, p, O, wbits, grad = case
+    torch.manual_seed(4)
+    layer = make(k, s, p, O, wbits, grad).to(DEV).train()
+    shape = (4, 16, 20, 20)
+    with torch.no_grad():
+        layer(torch.randn(shape, device=DEV) + 0.3)            # non-trivial scales
+    state = {n: v.clone() for n, v in layer.state_dict().items()}
+    eager = copy.deepcopy(layer)
+    sample = torch.randn(shape, device=DEV, requires_grad=True)
+    graphed = torch.cuda.make_graphed_callables(layer, (sample,))
+    with torch.no_grad():                                       # undo the warm-up's EMA steps
+        for n, v in layer.state_dict().items():
+            v.copy_(state[n])
+    layer.zero_grad(set_to_none=True)
+    for step in range(3):
+        x = torch.randn(shape, device=DEV) * (1 + step) + 0.1 * step
+        xa, xb = x.clone().requires_grad_(), x.clone().requires_grad_()
+        ya, yb = eager(xa), graphed(xb)
+        g = torch.randn_like(ya)
+        ya.backward(g)
+        yb.backward(g)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb), step
+        assert torch.equal(xa.grad, xb.grad), step
+        for (n, a), (_, b) in zip(eager.named_parameters(), layer.named_parameters()):
+            assert torch.equal(a.grad, b.grad), (step, n)
+        for (n, a), (_, b) in zip(eager.state_dict().items(), layer.state_dict().items()):
+            assert torch.equal(a, b), (step, n)
+        with torch.no_grad():
+            for a, b in zip(eager.parameters(), layer.parameters()):
+                a -= 0.05 * a.grad
+                b -= 0.05 * b.grad
+        eager.zero_grad(set_to_none=True)
+        layer.zero_grad(set_to_none=True)
