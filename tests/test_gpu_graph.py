@@ -88,6 +88,10 @@ TRAIN_CASES = [
 ]
 
 
+# make_graphed_callables warms the layer up on a side stream, where the
+# parameters' gradient-accumulation nodes are created; torch then notes that
+# the eager steps on the default stream feed them from another stream
+@pytest.mark.filterwarnings("ignore:The AccumulateGrad node's stream")
 @pytest.mark.parametrize("case", TRAIN_CASES, ids=[c[0] for c in TRAIN_CASES])
 def test_train_step_graphed(case):
     """A training-mode layer under torch.cuda.make_graphed_callables (forward
